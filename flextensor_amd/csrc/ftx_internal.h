@@ -1,0 +1,59 @@
+// Internal declarations shared by the runtime (C ABI) and the kernel file.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ftx.h"
+
+namespace ftx {
+
+// Thread-local error message behind ftx_last_error().
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int hip_fail(hipError_t err, const char *what);
+
+#define FTX_HIP(expr)                                   \
+  do {                                                  \
+    hipError_t ftx_err_ = (expr);                       \
+    if (ftx_err_ != hipSuccess) return ::ftx::hip_fail(ftx_err_, #expr); \
+  } while (0)
+
+// Default bytes per wave tile of the scatter kernel.
+constexpr size_t kScatterTileBytes = 64 * 1024;
+// Wave tiles handled by one workgroup (one tile per wavefront).
+constexpr int kScatterWavesPerGroup = 4;
+// Checksum block: 64 lanes x 8 bytes x 8 steps.
+constexpr size_t kChecksumBlockBytes = 4096;
+
+// Device-resident scatter plan.
+struct ScatterPlanDev {
+  const ftx_desc *descs;        // n_desc descriptors
+  const uint64_t *tile_start;   // n_desc + 1 exclusive prefix of tiles per descriptor
+  const uint32_t *group_desc0;  // n_groups: descriptor of each workgroup's first tile
+  int n_desc;
+  int64_t n_tiles;
+  int64_t n_groups;
+  uint64_t tile_bytes;
+};
+
+// Kernel launchers (ftx_kernels.hip). Each returns hipSuccess or the launch error.
+hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid,
+                            hipStream_t stream);
+hipError_t launch_scatter(const ScatterPlanDev &plan, const void *chunk, hipStream_t stream);
+hipError_t launch_checksum(const void *dev, size_t nbytes, uint64_t *partials, int n_waves,
+                           hipStream_t stream);
+hipError_t launch_fill_u8(void *dev, uint8_t value, size_t nbytes, hipStream_t stream);
+
+// Host-side helpers shared with the oracle's definition of the checksum.
+inline uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  uint64_t z = x;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+}  // namespace ftx

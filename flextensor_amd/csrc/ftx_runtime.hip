@@ -1,0 +1,693 @@
+// C ABI of the MI355X weight-streaming engine: host arenas, copy engines,
+// streams/events, scatter plans and checksums. Declarations and the reference
+// constructs each entry point replaces are in include/ftx.h.
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "ftx_internal.h"
+
+namespace ftx {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+constexpr int kMaxDevices = 64;
+constexpr int kMaxCopyStreams = 8;
+
+struct CopyPolicy {
+  size_t kernel_max_bytes = 1u << 20;  // AUTO: chunks up to 1 MiB go to the zero-copy kernel
+  size_t split_min_bytes = ~size_t(0); // SDMA splitting disabled until measured
+  int n_copy_streams = 1;
+  int kernel_grid = 0;                 // 0: 4 workgroups per CU
+};
+
+struct DeviceState {
+  bool ready = false;
+  int cu_count = 0;
+  int xcd_count = 1;
+  size_t total_mem = 0;
+  hipStream_t copy_streams[kMaxCopyStreams] = {};
+  hipEvent_t fork_event = nullptr;
+  hipEvent_t join_events[kMaxCopyStreams] = {};
+};
+
+struct ArenaRecord {
+  size_t nbytes;
+  void *dev;
+  bool registered;  // true: page-locked in place (hipHostRegister); false: hipHostMalloc
+};
+
+std::mutex g_mutex;      // guards g_policy and g_arenas
+std::mutex g_dev_mutex;  // guards first-use setup of g_devices
+CopyPolicy g_policy;
+DeviceState g_devices[kMaxDevices];
+std::map<uintptr_t, ArenaRecord> g_arenas;
+
+int current_device(int *dev) {
+  FTX_HIP(hipGetDevice(dev));
+  if (*dev < 0 || *dev >= kMaxDevices) return fail(FTX_ERR_UNSUPPORTED, "device index out of range");
+  return FTX_OK;
+}
+
+// Per-device copy streams and fork/join events, created on first use with the
+// device current. Streams are non-blocking and at default priority.
+int device_state(DeviceState **out) {
+  int dev = 0;
+  int rc = current_device(&dev);
+  if (rc != FTX_OK) return rc;
+  DeviceState &st = g_devices[dev];
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  if (!st.ready) {
+    int cus = 0;
+    FTX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    int xccs = 0;
+    if (hipDeviceGetAttribute(&xccs, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || xccs <= 0) {
+      (void)hipGetLastError();
+      hipDeviceProp_t prop;
+      xccs = 1;
+      if (hipGetDeviceProperties(&prop, dev) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+        xccs = 8;
+      (void)hipGetLastError();
+    }
+    size_t free_b = 0, total_b = 0;
+    FTX_HIP(hipMemGetInfo(&free_b, &total_b));
+    for (int i = 0; i < kMaxCopyStreams; ++i) {
+      FTX_HIP(hipStreamCreateWithFlags(&st.copy_streams[i], hipStreamNonBlocking));
+      FTX_HIP(hipEventCreateWithFlags(&st.join_events[i], hipEventDisableTiming));
+    }
+    FTX_HIP(hipEventCreateWithFlags(&st.fork_event, hipEventDisableTiming));
+    st.cu_count = cus;
+    st.xcd_count = xccs;
+    st.total_mem = total_b;
+    st.ready = true;
+  }
+  *out = &st;
+  return FTX_OK;
+}
+
+// Device-visible address of the pinned host range [host, host+nbytes):
+// arenas created here are looked up in the registry; other pinned memory
+// (e.g. torch pin_memory) is resolved through hipPointerGetAttributes and
+// hipMemGetAddressRange. The whole range must lie in one pinned allocation.
+int mapped_source(const void *host, size_t nbytes, const void **dev) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(host);
+  {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    auto it = g_arenas.upper_bound(a);
+    if (it != g_arenas.begin()) {
+      --it;
+      if (a < it->first + it->second.nbytes) {
+        if (a + nbytes > it->first + it->second.nbytes)
+          return fail(FTX_ERR_INVALID, "host range exceeds its pinned arena");
+        *dev = static_cast<const uint8_t *>(it->second.dev) + (a - it->first);
+        return FTX_OK;
+      }
+    }
+  }
+  hipPointerAttribute_t attr;
+  hipError_t err = hipPointerGetAttributes(&attr, host);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(FTX_ERR_UNSUPPORTED, "zero-copy source is not pinned host memory");
+  }
+  if (attr.type != hipMemoryTypeHost || attr.devicePointer == nullptr)
+    return fail(FTX_ERR_UNSUPPORTED, "zero-copy source is not device-mapped pinned host memory");
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  err = hipMemGetAddressRange(&base, &size, const_cast<void *>(host));
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(FTX_ERR_UNSUPPORTED, "extent of the pinned source is unknown");
+  }
+  if (a + nbytes > reinterpret_cast<uintptr_t>(base) + size)
+    return fail(FTX_ERR_INVALID, "host range exceeds its pinned allocation");
+  *dev = attr.devicePointer;
+  return FTX_OK;
+}
+
+// [p, p+nbytes) must lie inside one device allocation; anything else (host
+// memory, unmapped addresses, overruns past the allocation) is rejected on
+// the host before a kernel or copy can touch it.
+int check_device_range(const void *p, size_t nbytes, const char *what) {
+  hipPointerAttribute_t attr;
+  hipError_t err = hipPointerGetAttributes(&attr, p);
+  if (err != hipSuccess || attr.type != hipMemoryTypeDevice) {
+    (void)hipGetLastError();
+    return fail(FTX_ERR_INVALID, std::string(what) + " is not device memory");
+  }
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  err = hipMemGetAddressRange(&base, &size, const_cast<void *>(p));
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(FTX_ERR_INVALID, std::string(what) + ": device allocation extent unknown");
+  }
+  if (reinterpret_cast<uintptr_t>(p) + nbytes > reinterpret_cast<uintptr_t>(base) + size)
+    return fail(FTX_ERR_INVALID, std::string(what) + " range exceeds its device allocation");
+  return FTX_OK;
+}
+
+int copy_sdma(void *dst, const void *src, size_t nbytes, hipStream_t stream, const CopyPolicy &pol) {
+  int vrc = check_device_range(dst, nbytes, "copy destination");
+  if (vrc != FTX_OK) return vrc;
+  if (pol.n_copy_streams <= 1 || nbytes < pol.split_min_bytes) {
+    FTX_HIP(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, stream));
+    return FTX_OK;
+  }
+  DeviceState *st = nullptr;
+  int rc = device_state(&st);
+  if (rc != FTX_OK) return rc;
+  const int k = std::min(pol.n_copy_streams, kMaxCopyStreams);
+  const size_t align = size_t(1) << 16;
+  size_t piece = (nbytes + k - 1) / k;
+  piece = (piece + align - 1) / align * align;
+  FTX_HIP(hipEventRecord(st->fork_event, stream));
+  size_t off = 0;
+  for (int i = 0; i < k && off < nbytes; ++i) {
+    const size_t n = std::min(piece, nbytes - off);
+    FTX_HIP(hipStreamWaitEvent(st->copy_streams[i], st->fork_event, 0));
+    FTX_HIP(hipMemcpyAsync(static_cast<uint8_t *>(dst) + off, static_cast<const uint8_t *>(src) + off, n,
+                           hipMemcpyHostToDevice, st->copy_streams[i]));
+    FTX_HIP(hipEventRecord(st->join_events[i], st->copy_streams[i]));
+    FTX_HIP(hipStreamWaitEvent(stream, st->join_events[i], 0));
+    off += n;
+  }
+  return FTX_OK;
+}
+
+int copy_kernel(void *dst, const void *src, size_t nbytes, hipStream_t stream, const CopyPolicy &pol,
+                bool allow_fallback) {
+  int rc = check_device_range(dst, nbytes, "copy destination");
+  if (rc != FTX_OK) return rc;
+  const void *src_dev = nullptr;
+  rc = mapped_source(src, nbytes, &src_dev);
+  const bool congruent =
+      rc == FTX_OK && ((reinterpret_cast<uintptr_t>(src_dev) ^ reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+  if (!congruent) {
+    if (allow_fallback) return copy_sdma(dst, src, nbytes, stream, pol);
+    if (rc != FTX_OK) return rc;
+    return fail(FTX_ERR_UNSUPPORTED, "zero-copy kernel needs src and dst congruent modulo 16");
+  }
+  DeviceState *st = nullptr;
+  rc = device_state(&st);
+  if (rc != FTX_OK) return rc;
+  const int grid = pol.kernel_grid > 0 ? pol.kernel_grid : std::max(1, st->cu_count * 4);
+  FTX_HIP(launch_zero_copy(dst, src_dev, nbytes, grid, stream));
+  return FTX_OK;
+}
+
+}  // namespace
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+int fail(int code, const std::string &msg) {
+  set_error(msg);
+  return code;
+}
+
+int hip_fail(hipError_t err, const char *what) {
+  std::string msg = std::string(what) + ": " + hipGetErrorName(err) + " (" + hipGetErrorString(err) + ")";
+  (void)hipGetLastError();  // do not leave the error for the next caller of the runtime
+  set_error(msg);
+  return err == hipErrorOutOfMemory || err == hipErrorMemoryAllocation ? FTX_ERR_OOM : FTX_ERR_HIP;
+}
+
+}  // namespace ftx
+
+struct ftx_scatter_plan {
+  ftx::ScatterPlanDev dev;
+  void *storage;  // one device allocation holding the three tables
+  int n_desc_in;
+  uint64_t total_bytes;
+  uint64_t max_src_end;
+};
+
+namespace {
+
+// Host-side tables of a scatter plan, laid out as one contiguous buffer:
+// [descs | tile_start | group_desc0], each section 256-byte aligned.
+struct PlanTables {
+  std::vector<uint8_t> buf;
+  size_t off_tile_start = 0, off_group = 0;
+  int n_desc = 0;
+  int64_t n_tiles = 0, n_groups = 0;
+  uint64_t total_bytes = 0;
+  uint64_t max_src_end = 0;  // chunk bytes the descriptors read
+};
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+int build_plan_tables(const ftx_desc *descs, int n_desc, size_t tile_bytes, PlanTables *t) {
+  if (n_desc < 0) return ftx::fail(FTX_ERR_INVALID, "n_desc must be >= 0");
+  if (n_desc > 0 && descs == nullptr) return ftx::fail(FTX_ERR_INVALID, "descs is null");
+  if (tile_bytes == 0) tile_bytes = ftx::kScatterTileBytes;
+  if (tile_bytes % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "tile_bytes must be a multiple of 16");
+  std::vector<ftx_desc> kept;
+  kept.reserve(static_cast<size_t>(n_desc));
+  uint64_t max_src_end = 0;
+  for (int i = 0; i < n_desc; ++i) {
+    if (descs[i].nbytes == 0) continue;
+    if (descs[i].dst == 0) return ftx::fail(FTX_ERR_INVALID, "descriptor with null destination");
+    if (descs[i].src_off + descs[i].nbytes < descs[i].src_off)
+      return ftx::fail(FTX_ERR_INVALID, "descriptor source range overflows");
+    int vrc = ftx::check_device_range(reinterpret_cast<const void *>(descs[i].dst), descs[i].nbytes,
+                                      "scatter destination");
+    if (vrc != FTX_OK) return vrc;
+    max_src_end = std::max<uint64_t>(max_src_end, descs[i].src_off + descs[i].nbytes);
+    kept.push_back(descs[i]);
+  }
+  t->max_src_end = max_src_end;
+  const size_t nd = kept.size();
+  std::vector<uint64_t> tile_start(nd + 1, 0);
+  uint64_t total = 0;
+  for (size_t i = 0; i < nd; ++i) {
+    tile_start[i + 1] = tile_start[i] + (kept[i].nbytes + tile_bytes - 1) / tile_bytes;
+    total += kept[i].nbytes;
+  }
+  const int64_t n_tiles = static_cast<int64_t>(tile_start[nd]);
+  const int64_t n_groups = (n_tiles + ftx::kScatterWavesPerGroup - 1) / ftx::kScatterWavesPerGroup;
+  if (n_groups > 0x7fffffff) return ftx::fail(FTX_ERR_INVALID, "scatter plan too large for one launch");
+  std::vector<uint32_t> group_desc0(static_cast<size_t>(n_groups));
+  size_t d = 0;
+  for (int64_t g = 0; g < n_groups; ++g) {
+    const uint64_t tile = static_cast<uint64_t>(g) * ftx::kScatterWavesPerGroup;
+    while (tile_start[d + 1] <= tile) ++d;
+    group_desc0[static_cast<size_t>(g)] = static_cast<uint32_t>(d);
+  }
+  t->off_tile_start = align256(nd * sizeof(ftx_desc));
+  t->off_group = t->off_tile_start + align256((nd + 1) * sizeof(uint64_t));
+  const size_t total_sz = t->off_group + align256(std::max<size_t>(1, group_desc0.size()) * sizeof(uint32_t));
+  t->buf.assign(total_sz, 0);
+  if (nd) std::memcpy(t->buf.data(), kept.data(), nd * sizeof(ftx_desc));
+  std::memcpy(t->buf.data() + t->off_tile_start, tile_start.data(), (nd + 1) * sizeof(uint64_t));
+  if (!group_desc0.empty())
+    std::memcpy(t->buf.data() + t->off_group, group_desc0.data(), group_desc0.size() * sizeof(uint32_t));
+  t->n_desc = static_cast<int>(nd);
+  t->n_tiles = n_tiles;
+  t->n_groups = n_groups;
+  t->total_bytes = total;
+  return FTX_OK;
+}
+
+ftx::ScatterPlanDev plan_view(const PlanTables &t, void *storage, size_t tile_bytes) {
+  ftx::ScatterPlanDev p;
+  uint8_t *base = static_cast<uint8_t *>(storage);
+  p.descs = reinterpret_cast<const ftx_desc *>(base);
+  p.tile_start = reinterpret_cast<const uint64_t *>(base + t.off_tile_start);
+  p.group_desc0 = reinterpret_cast<const uint32_t *>(base + t.off_group);
+  p.n_desc = t.n_desc;
+  p.n_tiles = t.n_tiles;
+  p.n_groups = t.n_groups;
+  p.tile_bytes = tile_bytes ? tile_bytes : ftx::kScatterTileBytes;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ftx_last_error(void) { return ftx::g_last_error.c_str(); }
+
+int ftx_version(void) { return 1; }
+
+int ftx_device_count(int *count) {
+  if (!count) return ftx::fail(FTX_ERR_INVALID, "count is null");
+  FTX_HIP(hipGetDeviceCount(count));
+  return FTX_OK;
+}
+
+int ftx_set_device(int device) {
+  FTX_HIP(hipSetDevice(device));
+  return FTX_OK;
+}
+
+int ftx_get_device(int *device) {
+  if (!device) return ftx::fail(FTX_ERR_INVALID, "device is null");
+  FTX_HIP(hipGetDevice(device));
+  return FTX_OK;
+}
+
+int ftx_device_synchronize(void) {
+  FTX_HIP(hipDeviceSynchronize());
+  return FTX_OK;
+}
+
+int ftx_device_info(int *cu_count, int *xcd_count, size_t *total_mem) {
+  ftx::DeviceState *st = nullptr;
+  int rc = ftx::device_state(&st);
+  if (rc != FTX_OK) return rc;
+  if (cu_count) *cu_count = st->cu_count;
+  if (xcd_count) *xcd_count = st->xcd_count;
+  if (total_mem) *total_mem = st->total_mem;
+  return FTX_OK;
+}
+
+int ftx_arena_alloc(size_t nbytes, unsigned flags, void **host) {
+  if (!host) return ftx::fail(FTX_ERR_INVALID, "host is null");
+  if (nbytes == 0) return ftx::fail(FTX_ERR_INVALID, "arena size must be > 0");
+  if ((flags & FTX_ARENA_COHERENT) && (flags & FTX_ARENA_NONCOHERENT))
+    return ftx::fail(FTX_ERR_INVALID, "arena cannot be both coherent and non-coherent");
+  unsigned hflags = hipHostMallocPortable | hipHostMallocMapped;
+  if (flags & FTX_ARENA_COHERENT) hflags |= hipHostMallocCoherent;
+  if (flags & FTX_ARENA_NONCOHERENT) hflags |= hipHostMallocNonCoherent;
+  if (flags & FTX_ARENA_WRITECOMBINED) hflags |= hipHostMallocWriteCombined;
+  void *p = nullptr;
+  FTX_HIP(hipHostMalloc(&p, nbytes, hflags));
+  void *dev = nullptr;
+  hipError_t err = hipHostGetDevicePointer(&dev, p, 0);
+  if (err != hipSuccess) {
+    (void)hipHostFree(p);
+    return ftx::hip_fail(err, "hipHostGetDevicePointer");
+  }
+  {
+    std::lock_guard<std::mutex> lock(ftx::g_mutex);
+    ftx::g_arenas[reinterpret_cast<uintptr_t>(p)] = ftx::ArenaRecord{nbytes, dev, false};
+  }
+  *host = p;
+  return FTX_OK;
+}
+
+int ftx_arena_free(void *host) {
+  if (!host) return FTX_OK;
+  {
+    std::lock_guard<std::mutex> lock(ftx::g_mutex);
+    auto it = ftx::g_arenas.find(reinterpret_cast<uintptr_t>(host));
+    if (it == ftx::g_arenas.end() || it->second.registered)
+      return ftx::fail(FTX_ERR_INVALID, "pointer is not an arena from ftx_arena_alloc");
+    ftx::g_arenas.erase(it);
+  }
+  FTX_HIP(hipHostFree(host));
+  return FTX_OK;
+}
+
+int ftx_arena_register(void *host, size_t nbytes, unsigned flags) {
+  (void)flags;
+  if (!host || nbytes == 0) return ftx::fail(FTX_ERR_INVALID, "host is null or size is 0");
+  {
+    std::lock_guard<std::mutex> lock(ftx::g_mutex);
+    if (ftx::g_arenas.count(reinterpret_cast<uintptr_t>(host)))
+      return ftx::fail(FTX_ERR_INVALID, "memory is already pinned by this library");
+  }
+  FTX_HIP(hipHostRegister(host, nbytes, hipHostRegisterPortable | hipHostRegisterMapped));
+  void *dev = nullptr;
+  hipError_t err = hipHostGetDevicePointer(&dev, host, 0);
+  if (err != hipSuccess) {
+    (void)hipHostUnregister(host);
+    return ftx::hip_fail(err, "hipHostGetDevicePointer");
+  }
+  std::lock_guard<std::mutex> lock(ftx::g_mutex);
+  ftx::g_arenas[reinterpret_cast<uintptr_t>(host)] = ftx::ArenaRecord{nbytes, dev, true};
+  return FTX_OK;
+}
+
+int ftx_arena_unregister(void *host) {
+  {
+    std::lock_guard<std::mutex> lock(ftx::g_mutex);
+    auto it = ftx::g_arenas.find(reinterpret_cast<uintptr_t>(host));
+    if (it == ftx::g_arenas.end() || !it->second.registered)
+      return ftx::fail(FTX_ERR_INVALID, "pointer was not registered with ftx_arena_register");
+    ftx::g_arenas.erase(it);
+  }
+  FTX_HIP(hipHostUnregister(host));
+  return FTX_OK;
+}
+
+int ftx_host_device_ptr(void *host, void **dev) {
+  if (!host || !dev) return ftx::fail(FTX_ERR_INVALID, "null argument");
+  const void *d = nullptr;
+  int rc = ftx::mapped_source(host, 1, &d);
+  if (rc != FTX_OK) return rc;
+  *dev = const_cast<void *>(d);
+  return FTX_OK;
+}
+
+int ftx_device_alloc(size_t nbytes, void **dev) {
+  if (!dev || nbytes == 0) return ftx::fail(FTX_ERR_INVALID, "dev is null or size is 0");
+  FTX_HIP(hipMalloc(dev, nbytes));
+  return FTX_OK;
+}
+
+int ftx_device_free(void *dev) {
+  if (!dev) return FTX_OK;
+  FTX_HIP(hipFree(dev));
+  return FTX_OK;
+}
+
+int ftx_memset_async(void *dev, int value, size_t nbytes, void *stream) {
+  if (nbytes == 0) return FTX_OK;
+  if (!dev) return ftx::fail(FTX_ERR_INVALID, "dev is null");
+  int rc = ftx::check_device_range(dev, nbytes, "memset destination");
+  if (rc != FTX_OK) return rc;
+  FTX_HIP(ftx::launch_fill_u8(dev, static_cast<uint8_t>(value), nbytes, static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_copy_d2h(void *dst_host, const void *src_dev, size_t nbytes, void *stream) {
+  if ((!dst_host || !src_dev) && nbytes) return ftx::fail(FTX_ERR_INVALID, "null argument");
+  if (nbytes == 0) return FTX_OK;
+  int rc = ftx::check_device_range(src_dev, nbytes, "copy source");
+  if (rc != FTX_OK) return rc;
+  FTX_HIP(hipMemcpyAsync(dst_host, src_dev, nbytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_stream_create(void **stream) {
+  if (!stream) return ftx::fail(FTX_ERR_INVALID, "stream is null");
+  hipStream_t s = nullptr;
+  FTX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return FTX_OK;
+}
+
+int ftx_stream_destroy(void *stream) {
+  if (!stream) return FTX_OK;
+  FTX_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_stream_synchronize(void *stream) {
+  FTX_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_stream_query(void *stream, int *done) {
+  if (!done) return ftx::fail(FTX_ERR_INVALID, "done is null");
+  hipError_t err = hipStreamQuery(static_cast<hipStream_t>(stream));
+  if (err == hipErrorNotReady) {
+    (void)hipGetLastError();
+    *done = 0;
+    return FTX_OK;
+  }
+  FTX_HIP(err);
+  *done = 1;
+  return FTX_OK;
+}
+
+int ftx_event_create(unsigned flags, void **event) {
+  if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
+  hipEvent_t e = nullptr;
+  FTX_HIP(hipEventCreateWithFlags(&e, (flags & FTX_EVENT_TIMING) ? hipEventDefault : hipEventDisableTiming));
+  *event = e;
+  return FTX_OK;
+}
+
+int ftx_event_destroy(void *event) {
+  if (!event) return FTX_OK;
+  FTX_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return FTX_OK;
+}
+
+int ftx_event_record(void *event, void *stream) {
+  if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
+  FTX_HIP(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_stream_wait_event(void *stream, void *event) {
+  if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
+  FTX_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0));
+  return FTX_OK;
+}
+
+int ftx_event_query(void *event, int *done) {
+  if (!event || !done) return ftx::fail(FTX_ERR_INVALID, "null argument");
+  hipError_t err = hipEventQuery(static_cast<hipEvent_t>(event));
+  if (err == hipErrorNotReady) {
+    (void)hipGetLastError();
+    *done = 0;
+    return FTX_OK;
+  }
+  FTX_HIP(err);
+  *done = 1;
+  return FTX_OK;
+}
+
+int ftx_event_synchronize(void *event) {
+  if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
+  FTX_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+  return FTX_OK;
+}
+
+int ftx_event_elapsed_ms(void *start, void *end, float *ms) {
+  if (!start || !end || !ms) return ftx::fail(FTX_ERR_INVALID, "null argument");
+  FTX_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)));
+  return FTX_OK;
+}
+
+int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stream) {
+  if (nbytes == 0) return FTX_OK;
+  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  ftx::CopyPolicy pol;
+  {
+    std::lock_guard<std::mutex> lock(ftx::g_mutex);
+    pol = ftx::g_policy;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (mode) {
+    case FTX_COPY_SDMA:
+      return ftx::copy_sdma(dst, src, nbytes, s, pol);
+    case FTX_COPY_KERNEL:
+      return ftx::copy_kernel(dst, src, nbytes, s, pol, false);
+    case FTX_COPY_AUTO:
+      if (nbytes <= pol.kernel_max_bytes) return ftx::copy_kernel(dst, src, nbytes, s, pol, true);
+      return ftx::copy_sdma(dst, src, nbytes, s, pol);
+    default:
+      return ftx::fail(FTX_ERR_INVALID, "unknown copy mode");
+  }
+}
+
+int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams, int kernel_grid) {
+  if (n_copy_streams < 1 || n_copy_streams > ftx::kMaxCopyStreams)
+    return ftx::fail(FTX_ERR_INVALID, "n_copy_streams must be in [1, 8]");
+  if (kernel_grid < 0 || kernel_grid > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "kernel_grid out of range");
+  std::lock_guard<std::mutex> lock(ftx::g_mutex);
+  ftx::g_policy.kernel_max_bytes = kernel_max_bytes;
+  ftx::g_policy.split_min_bytes = split_min_bytes;
+  ftx::g_policy.n_copy_streams = n_copy_streams;
+  ftx::g_policy.kernel_grid = kernel_grid;
+  return FTX_OK;
+}
+
+int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams, int *kernel_grid) {
+  std::lock_guard<std::mutex> lock(ftx::g_mutex);
+  if (kernel_max_bytes) *kernel_max_bytes = ftx::g_policy.kernel_max_bytes;
+  if (split_min_bytes) *split_min_bytes = ftx::g_policy.split_min_bytes;
+  if (n_copy_streams) *n_copy_streams = ftx::g_policy.n_copy_streams;
+  if (kernel_grid) *kernel_grid = ftx::g_policy.kernel_grid;
+  return FTX_OK;
+}
+
+int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes, ftx_scatter_plan **plan) {
+  if (!plan) return ftx::fail(FTX_ERR_INVALID, "plan is null");
+  PlanTables t;
+  int rc = build_plan_tables(descs, n_desc, tile_bytes, &t);
+  if (rc != FTX_OK) return rc;
+  void *storage = nullptr;
+  FTX_HIP(hipMalloc(&storage, t.buf.size()));
+  hipError_t err = hipMemcpy(storage, t.buf.data(), t.buf.size(), hipMemcpyHostToDevice);
+  if (err != hipSuccess) {
+    (void)hipFree(storage);
+    return ftx::hip_fail(err, "hipMemcpy(scatter plan)");
+  }
+  auto *p = new ftx_scatter_plan;
+  p->dev = plan_view(t, storage, tile_bytes);
+  p->storage = storage;
+  p->n_desc_in = n_desc;
+  p->total_bytes = t.total_bytes;
+  p->max_src_end = t.max_src_end;
+  *plan = p;
+  return FTX_OK;
+}
+
+int ftx_scatter_plan_destroy(ftx_scatter_plan *plan) {
+  if (!plan) return FTX_OK;
+  hipError_t err = hipFree(plan->storage);
+  delete plan;
+  FTX_HIP(err);
+  return FTX_OK;
+}
+
+int ftx_scatter_plan_info(const ftx_scatter_plan *plan, int *n_desc, int64_t *n_tiles, uint64_t *total_bytes) {
+  if (!plan) return ftx::fail(FTX_ERR_INVALID, "plan is null");
+  if (n_desc) *n_desc = plan->n_desc_in;
+  if (n_tiles) *n_tiles = plan->dev.n_tiles;
+  if (total_bytes) *total_bytes = plan->total_bytes;
+  return FTX_OK;
+}
+
+int ftx_scatter_run(const ftx_scatter_plan *plan, const void *chunk, void *stream) {
+  if (!plan) return ftx::fail(FTX_ERR_INVALID, "plan is null");
+  if (plan->dev.n_tiles == 0) return FTX_OK;
+  if (!chunk) return ftx::fail(FTX_ERR_INVALID, "chunk is null");
+  int rc = ftx::check_device_range(chunk, plan->max_src_end, "scatter chunk");
+  if (rc != FTX_OK) return rc;
+  FTX_HIP(ftx::launch_scatter(plan->dev, chunk, static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stream) {
+  PlanTables t;
+  int rc = build_plan_tables(descs, n_desc, 0, &t);
+  if (rc != FTX_OK) return rc;
+  if (t.n_tiles == 0) return FTX_OK;
+  if (!chunk) return ftx::fail(FTX_ERR_INVALID, "chunk is null");
+  rc = ftx::check_device_range(chunk, t.max_src_end, "scatter chunk");
+  if (rc != FTX_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void *storage = nullptr;
+  FTX_HIP(hipMallocAsync(&storage, t.buf.size(), s));
+  hipError_t err = hipMemcpyAsync(storage, t.buf.data(), t.buf.size(), hipMemcpyHostToDevice, s);
+  if (err == hipSuccess) err = ftx::launch_scatter(plan_view(t, storage, 0), chunk, s);
+  if (err == hipSuccess) {
+    // The pageable source table must stay valid until the upload has been
+    // staged; synchronizing keeps the one-shot form simple and safe.
+    err = hipStreamSynchronize(s);
+  }
+  hipError_t ferr = hipFreeAsync(storage, s);
+  FTX_HIP(err);
+  FTX_HIP(ferr);
+  return FTX_OK;
+}
+
+int ftx_checksum64(const void *dev, size_t nbytes, void *stream, uint64_t *out) {
+  if (!out) return ftx::fail(FTX_ERR_INVALID, "out is null");
+  if (nbytes == 0) {
+    *out = ftx::splitmix64(0);
+    return FTX_OK;
+  }
+  if (!dev) return ftx::fail(FTX_ERR_INVALID, "dev is null");
+  if (reinterpret_cast<uintptr_t>(dev) % 8 != 0) return ftx::fail(FTX_ERR_INVALID, "checksum needs 8-byte alignment");
+  {
+    int vrc = ftx::check_device_range(dev, nbytes, "checksum input");
+    if (vrc != FTX_OK) return vrc;
+  }
+  int cus = 256;
+  {
+    ftx::DeviceState *st = nullptr;
+    if (ftx::device_state(&st) == FTX_OK) cus = st->cu_count;
+  }
+  const uint64_t n_blocks = (nbytes + ftx::kChecksumBlockBytes - 1) / ftx::kChecksumBlockBytes;
+  uint64_t waves = std::min<uint64_t>(n_blocks, static_cast<uint64_t>(cus) * 32);
+  waves = (waves + 3) / 4 * 4;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint64_t *partials = nullptr;
+  FTX_HIP(hipMalloc(&partials, waves * sizeof(uint64_t)));
+  std::vector<uint64_t> host(waves, 0);
+  hipError_t err = ftx::launch_checksum(dev, nbytes, partials, static_cast<int>(waves), s);
+  if (err == hipSuccess) err = hipMemcpyAsync(host.data(), partials, waves * sizeof(uint64_t), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  hipError_t ferr = hipFree(partials);
+  FTX_HIP(err);
+  FTX_HIP(ferr);
+  uint64_t sum = 0;
+  for (uint64_t v : host) sum += v;
+  *out = ftx::splitmix64(sum + static_cast<uint64_t>(nbytes));
+  return FTX_OK;
+}
+
+}  // extern "C"

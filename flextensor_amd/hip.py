@@ -1,0 +1,154 @@
+"""Streams, events and host arenas over the C ABI.
+
+:class:`HipStream` wraps a ``hipStream_t`` (normally the handle of a
+``torch.cuda.Stream``) and offers the ``record_event / wait_event /
+wait_stream / synchronize`` surface the transfer runtime uses, in the
+shape the reference uses PyTorch's stream objects (core/transfer.py:49-146).
+:class:`HostArena` is one page-locked, device-mapped host allocation exposed
+as a CPU ``uint8`` tensor without copying.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Iterator
+from contextlib import contextmanager
+from typing import Any
+
+import torch
+
+from . import _native as nat
+
+
+class HipEvent:
+    """One ``hipEvent_t``; destroyed with the Python object."""
+
+    __slots__ = ("handle", "timing", "__weakref__")
+
+    def __init__(self, timing: bool = False) -> None:
+        self.timing = timing
+        self.handle = nat.event_create(nat.EVENT_TIMING if timing else nat.EVENT_DEFAULT)
+
+    def record(self, stream: "HipStream | None" = None) -> "HipEvent":
+        s = stream if stream is not None else current_stream()
+        nat.call("ftx_event_record", self.handle, s.handle)
+        return self
+
+    def query(self) -> bool:
+        return nat.event_query(self.handle)
+
+    def synchronize(self) -> None:
+        nat.call("ftx_event_synchronize", self.handle)
+
+    def elapsed_time(self, end: "HipEvent") -> float:
+        return nat.event_elapsed_ms(self.handle, end.handle)
+
+    def __del__(self) -> None:
+        h = getattr(self, "handle", None)
+        if h and nat.live():
+            nat.lib().ftx_event_destroy(h)
+            self.handle = None
+
+
+class HipStream:
+    """A HIP stream. ``torch_stream`` keeps the owning torch object alive."""
+
+    __slots__ = ("handle", "torch_stream", "name", "__weakref__")
+
+    def __init__(self, torch_stream: Any = None, handle: int | None = None, name: str = "") -> None:
+        self.torch_stream = torch_stream
+        self.handle = int(handle if handle is not None else torch_stream.cuda_stream)
+        self.name = name
+
+    def record_event(self, event: HipEvent | None = None) -> HipEvent:
+        ev = event if event is not None else HipEvent()
+        nat.call("ftx_event_record", ev.handle, self.handle)
+        return ev
+
+    def wait_event(self, event: HipEvent) -> None:
+        nat.call("ftx_stream_wait_event", self.handle, event.handle)
+
+    def wait_stream(self, other: "HipStream") -> None:
+        self.wait_event(other.record_event())
+
+    def synchronize(self) -> None:
+        nat.call("ftx_stream_synchronize", self.handle)
+
+    def query(self) -> bool:
+        done = ctypes.c_int(0)
+        nat.call("ftx_stream_query", self.handle, ctypes.byref(done))
+        return bool(done.value)
+
+    def __eq__(self, other: object) -> bool:
+        return isinstance(other, HipStream) and other.handle == self.handle
+
+    def __hash__(self) -> int:
+        return hash(self.handle)
+
+    def __repr__(self) -> str:
+        return f"HipStream({self.name or hex(self.handle)})"
+
+
+def current_stream(device: torch.device | int | None = None) -> HipStream:
+    """torch's current stream on ``device`` as a :class:`HipStream`."""
+    return HipStream(torch.cuda.current_stream(device), name="compute")
+
+
+def new_stream(device: torch.device | int | None = None, name: str = "transfer") -> HipStream:
+    """A new stream at default priority, owned by torch's stream pool."""
+    return HipStream(torch.cuda.Stream(device=device), name=name)
+
+
+@contextmanager
+def use_stream(stream: HipStream) -> Iterator[None]:
+    """Make ``stream`` torch's current stream inside the block."""
+    if stream.torch_stream is None:
+        raise ValueError("use_stream needs a stream created through torch")
+    with torch.cuda.stream(stream.torch_stream):
+        yield
+
+
+class HostArena:
+    """Page-locked, device-mapped host bytes from ``ftx_arena_alloc``.
+
+    ``tensor`` is a CPU ``uint8`` tensor over the arena. The tensor keeps the
+    arena alive, so views of it stay valid after the arena object goes out of
+    scope; the memory is returned when the last view is gone.
+    """
+
+    def __init__(self, nbytes: int, flags: int = nat.ARENA_DEFAULT) -> None:
+        if nbytes <= 0:
+            raise ValueError(f"arena size must be positive, got {nbytes}")
+        self.nbytes = int(nbytes)
+        self.flags = flags
+        self.ptr = nat.arena_alloc(self.nbytes, flags)
+        self.device_ptr = nat.host_device_ptr(self.ptr)
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(self.ptr)
+        buf._ftx_arena = self  # the buffer (held by every view) keeps the arena alive
+        self.tensor = torch.frombuffer(buf, dtype=torch.uint8)
+
+    def __del__(self) -> None:
+        ptr = getattr(self, "ptr", None)
+        if ptr and nat.live():
+            nat.lib().ftx_arena_free(ptr)
+            self.ptr = None
+
+
+def copy_h2d(dst: torch.Tensor, src: torch.Tensor, mode: int, stream: HipStream | None = None,
+             nbytes: int | None = None) -> None:
+    """Stream-ordered copy of ``nbytes`` (default: all of ``src``) host -> device."""
+    n = src.numel() * src.element_size() if nbytes is None else int(nbytes)
+    if n > dst.numel() * dst.element_size():
+        raise ValueError(f"copy of {n} bytes does not fit destination of {dst.numel() * dst.element_size()} bytes")
+    if src.device.type != "cpu" or dst.device.type != "cuda":
+        raise ValueError("copy_h2d needs a CPU source and a device destination")
+    s = stream if stream is not None else current_stream(dst.device)
+    nat.copy_h2d(dst.data_ptr(), src.data_ptr(), n, mode, s.handle)
+
+
+def checksum(t: torch.Tensor, stream: HipStream | None = None) -> int:
+    """Device checksum of the bytes of a contiguous device tensor."""
+    if t.device.type != "cuda" or not t.is_contiguous():
+        raise ValueError("checksum needs a contiguous device tensor")
+    s = stream if stream is not None else current_stream(t.device)
+    return nat.checksum64(t.data_ptr(), t.numel() * t.element_size(), s.handle)

@@ -1,0 +1,204 @@
+"""Host-link model: live H2D measurements and a size <-> duration interpolator.
+
+* :class:`MemoryTransferInterpolator` keeps the reference's contract
+  (memory_transfer_interpolator.py:10-183): linear interpolation in log-log
+  space, linear extrapolation with the slope of the two end points, and a
+  constant answer when only one point is known.
+* :func:`benchmark_memory_transfers` plays the role of the reference's live
+  curve (memory_transfer_benchmark.py:59-129): the largest label size halved
+  ``max_depth`` times, timed from pinned memory.
+* :func:`measure_copy_curve` / :func:`choose_copy_policy` measure each copy
+  engine of this build (SDMA, SDMA split over copy streams, zero-copy
+  kernel) and derive the per-chunk-size choice the library applies under
+  ``FTX_COPY_AUTO``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _native as nat
+
+
+class MemoryTransferInterpolator:
+    """Bidirectional size (bytes) <-> duration (ms) model of the host link."""
+
+    def __init__(self, memory_transfers: dict[int, float]) -> None:
+        if not memory_transfers:
+            raise ValueError("memory_transfers dictionary cannot be empty")
+        pairs = sorted(memory_transfers.items())
+        self.bytes_array = np.array([p[0] for p in pairs], dtype=np.float64)
+        self.duration_array = np.array([p[1] for p in pairs], dtype=np.float64)
+        if (self.bytes_array <= 0).any():
+            raise ValueError("All byte values must be positive")
+        if (self.duration_array <= 0).any():
+            raise ValueError("All duration values must be positive")
+        self.min_bytes = self.bytes_array[0]
+        self.max_bytes = self.bytes_array[-1]
+        self.min_duration = self.duration_array[0]
+        self.max_duration = self.duration_array[-1]
+        self._lx = np.log(self.bytes_array)
+        self._ly = np.log(self.duration_array)
+        # keep the reference's attribute names for callers that read them
+        self.log_bytes = self._lx
+        self.log_duration = self._ly
+
+    @staticmethod
+    def _loglog(x: float, xs: np.ndarray, ys: np.ndarray, flat_if_no_slope: bool) -> float:
+        if x < xs[0]:
+            i0, i1, anchor = 0, 1, 0
+        elif x > xs[-1]:
+            i0, i1, anchor = -2, -1, -1
+        else:
+            return float(np.interp(x, xs, ys))
+        dx = xs[i1] - xs[i0]
+        if dx == 0:
+            if flat_if_no_slope:
+                return float(ys[anchor])
+            raise ZeroDivisionError("two points with the same abscissa")
+        return float(ys[anchor] + (ys[i1] - ys[i0]) / dx * (x - xs[anchor]))
+
+    def bytes_to_duration(self, size_bytes: int | float) -> float:
+        if size_bytes <= 0:
+            raise ValueError(f"size_bytes must be positive, got {size_bytes}")
+        if len(self._lx) == 1:
+            return float(self.duration_array[0])
+        return math.exp(self._loglog(math.log(float(size_bytes)), self._lx, self._ly, False))
+
+    def duration_to_bytes(self, duration_ms: float) -> float:
+        if duration_ms <= 0:
+            raise ValueError(f"duration_ms must be positive, got {duration_ms}")
+        if len(self._ly) == 1:
+            return float(self.bytes_array[0])
+        # durations need not be sorted when measured noise is large; the
+        # reference interpolates over the duration axis in byte order too.
+        return math.exp(self._loglog(math.log(float(duration_ms)), self._ly, self._lx, True))
+
+    def get_bandwidth_mbps(self) -> float:
+        """MB/s (MiB-based) of the largest measured transfer."""
+        return float(self.bytes_array[-1] / (1024 * 1024) / (self.duration_array[-1] / 1000.0))
+
+    def __repr__(self) -> str:
+        return (
+            f"MemoryTransferInterpolator(bytes_range=[{self.min_bytes:.0f}, {self.max_bytes:.0f}], "
+            f"duration_range=[{self.min_duration:.2f}, {self.max_duration:.2f}] ms, "
+            f"bandwidth≈{self.get_bandwidth_mbps():.2f} MB/s)"
+        )
+
+
+def create_interpolator_from_benchmarks(memory_transfers: dict[int, float]) -> MemoryTransferInterpolator:
+    return MemoryTransferInterpolator(memory_transfers)
+
+
+@dataclass
+class CopyCurve:
+    """Best-of-N milliseconds per size for one copy engine."""
+
+    engine: str
+    best_ms: dict[int, float] = field(default_factory=dict)
+
+    def gbps(self) -> dict[int, float]:
+        return {n: n / (ms * 1e-3) / 1e9 for n, ms in self.best_ms.items()}
+
+    def peak_gbps(self) -> float:
+        return max(self.gbps().values()) if self.best_ms else 0.0
+
+
+def time_h2d(nbytes: int, engine: str, repeats: int = 10, warmup: int = 2, device=None) -> list[float]:
+    """Time ``repeats`` copies of ``nbytes`` pinned host -> device with one engine.
+
+    Engines: ``sdma`` (one hipMemcpyAsync), ``sdma_split<k>`` (split over k
+    copy streams), ``kernel`` / ``kernel_g<grid>`` (zero-copy kernel).
+    Returns milliseconds per copy (device events around each copy).
+    """
+    import torch
+
+    from .hip import HipEvent, HostArena, new_stream
+
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if device.type != "cuda":
+        raise ValueError(f"time_h2d needs a device destination, got {device}")
+    arena = HostArena(nbytes)
+    arena.tensor[: min(nbytes, 1 << 20)].fill_(1)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    stream = new_stream(device, name="link-probe")
+    old = nat.get_copy_policy()
+    mode = nat.COPY_SDMA
+    try:
+        if engine.startswith("sdma_split"):
+            k = int(engine[len("sdma_split"):])
+            nat.set_copy_policy(old[0], 1, k, old[3])
+        elif engine.startswith("kernel"):
+            mode = nat.COPY_KERNEL
+            grid = int(engine[len("kernel_g"):]) if engine.startswith("kernel_g") else 0
+            nat.set_copy_policy(old[0], old[1], old[2], grid)
+        elif engine != "sdma":
+            raise ValueError(f"unknown engine {engine!r}")
+        times = []
+        for i in range(warmup + repeats):
+            e0, e1 = HipEvent(timing=True), HipEvent(timing=True)
+            stream.record_event(e0)
+            nat.copy_h2d(dst.data_ptr(), arena.ptr, nbytes, mode, stream.handle)
+            stream.record_event(e1)
+            e1.synchronize()
+            if i >= warmup:
+                times.append(e0.elapsed_time(e1))
+        return times
+    finally:
+        nat.set_copy_policy(*old)
+        stream.synchronize()
+        del dst
+
+
+def measure_copy_curve(engine: str, sizes: list[int], repeats: int = 10, device=None) -> CopyCurve:
+    curve = CopyCurve(engine)
+    for n in sizes:
+        curve.best_ms[n] = min(time_h2d(n, engine, repeats=repeats, device=device))
+    return curve
+
+
+def choose_copy_policy(sdma: CopyCurve, kernel: CopyCurve, split: CopyCurve | None = None,
+                       n_split: int = 1) -> tuple[int, int, int]:
+    """Per-chunk choice from measured curves.
+
+    Returns ``(kernel_max_bytes, split_min_bytes, n_copy_streams)``: chunks up
+    to ``kernel_max_bytes`` are faster on the zero-copy kernel, SDMA copies
+    from ``split_min_bytes`` up are faster split over ``n_copy_streams``.
+    """
+    kernel_max = 0
+    for n in sorted(sdma.best_ms):
+        if n in kernel.best_ms and kernel.best_ms[n] < sdma.best_ms[n]:
+            kernel_max = n
+        else:
+            break
+    split_min = 2**63 - 1
+    if split is not None and n_split > 1:
+        for n in sorted(sdma.best_ms, reverse=True):
+            if n in split.best_ms and split.best_ms[n] < sdma.best_ms[n]:
+                split_min = n
+            else:
+                break
+    return kernel_max, split_min, (n_split if split_min < 2**63 - 1 else 1)
+
+
+def benchmark_memory_transfers(max_label_bytes: int, device=None, max_depth: int = 4,
+                               max_size_bytes: int = 4 * 1024**3, engine: str = "sdma") -> dict[int, float]:
+    """Median ms per size for sizes ``base / 2**d``, d < max_depth (pinned source).
+
+    ``base`` is the largest label size capped at ``max_size_bytes`` and, as in
+    the reference (memory_transfer_benchmark.py:92-102), sizes are multiples of
+    4 bytes (the reference times fp32 tensors).
+    """
+    base = min(max_label_bytes, (max_size_bytes // 4) * 4)
+    base = (base // 4) * 4
+    out: dict[int, float] = {}
+    for d in range(max_depth):
+        n = (int(base / (2**d)) // 4) * 4
+        if n <= 0:
+            continue
+        times = sorted(time_h2d(n, engine, repeats=10, warmup=5, device=device))
+        out[n] = times[len(times) // 2]
+    return out

@@ -1,0 +1,231 @@
+"""Per-trap transfer / compute / wait timing and the hidden-transfer fraction.
+
+Same records and hooks as the reference's offload timing
+(offload_timing.py:31-217, 355-720):
+
+* ``transfer_ms`` - events around the transfer submission on the transfer
+  stream;
+* ``compute_ms``  - compute-stream events from ``enter`` to ``exit``;
+* ``wait_ms``     - compute-stream events around the readiness wait; zero
+  means the transfer was fully hidden.
+
+A pass is finalized when the next pass starts (or on ``flush``). Device
+timing uses HIP events with timing enabled. :func:`hidden_fraction` is
+``1 - sum(wait) / sum(transfer)``.
+"""
+
+from __future__ import annotations
+
+import statistics
+from collections.abc import Callable, Sequence
+from dataclasses import dataclass
+from typing import Any
+
+
+@dataclass(frozen=True, slots=True)
+class TrapTimingRecord:
+    label: str
+    transfer_ms: float = 0.0
+    compute_ms: float = 0.0
+    wait_ms: float = 0.0
+
+
+@dataclass(frozen=True, slots=True)
+class OffloadTimingSnapshot:
+    per_trap: Sequence[TrapTimingRecord] = ()
+
+    def __post_init__(self) -> None:
+        object.__setattr__(self, "per_trap", tuple(self.per_trap))
+
+    @property
+    def total_wait_ms(self) -> float:
+        return sum(r.wait_ms for r in self.per_trap)
+
+    @property
+    def total_transfer_ms(self) -> float:
+        return sum(r.transfer_ms for r in self.per_trap)
+
+    @property
+    def total_compute_ms(self) -> float:
+        return sum(r.compute_ms for r in self.per_trap)
+
+
+def hidden_fraction(wait_ms: float, transfer_ms: float) -> float:
+    """Fraction of transfer time hidden under compute: 1 - wait / transfer."""
+    if transfer_ms <= 0:
+        return 1.0
+    return max(0.0, min(1.0, 1.0 - wait_ms / transfer_ms))
+
+
+@dataclass(frozen=True, slots=True)
+class TrapTimingStats:
+    label: str
+    compute_avg: float
+    compute_median: float
+    transfer_avg: float
+    transfer_median: float
+    wait_avg: float
+    wait_median: float
+
+
+@dataclass
+class OffloadTimingReport:
+    snapshots: list[OffloadTimingSnapshot]
+
+    @property
+    def num_passes(self) -> int:
+        return len(self.snapshots)
+
+    @property
+    def total_wait_sum(self) -> float:
+        return sum(s.total_wait_ms for s in self.snapshots)
+
+    @property
+    def total_transfer_sum(self) -> float:
+        return sum(s.total_transfer_ms for s in self.snapshots)
+
+    @property
+    def total_compute_sum(self) -> float:
+        return sum(s.total_compute_ms for s in self.snapshots)
+
+    @property
+    def hidden_fraction(self) -> float:
+        return hidden_fraction(self.total_wait_sum, self.total_transfer_sum)
+
+    def per_trap_stats(self) -> list[TrapTimingStats]:
+        by_label: dict[str, list[TrapTimingRecord]] = {}
+        for snap in self.snapshots:
+            for r in snap.per_trap:
+                by_label.setdefault(r.label, []).append(r)
+        out = []
+        for label, recs in by_label.items():
+            c = [r.compute_ms for r in recs]
+            t = [r.transfer_ms for r in recs]
+            w = [r.wait_ms for r in recs]
+            out.append(TrapTimingStats(label, statistics.fmean(c), statistics.median(c), statistics.fmean(t),
+                                       statistics.median(t), statistics.fmean(w), statistics.median(w)))
+        return out
+
+    def table(self) -> str:
+        lines = [f"{'trap':<24}{'compute ms':>12}{'transfer ms':>13}{'wait ms':>10}"]
+        for s in self.per_trap_stats():
+            lines.append(f"{s.label:<24}{s.compute_median:>12.3f}{s.transfer_median:>13.3f}{s.wait_median:>10.3f}")
+        lines.append(f"passes={self.num_passes} hidden={self.hidden_fraction:.3f}")
+        return "\n".join(lines)
+
+
+class OffloadTimingCollector:
+    """Records per-trap events during a pass; a no-op when ``enabled`` is False.
+
+    ``event_factory()`` returns an object with ``record(stream)`` and
+    ``elapsed_time(end)``; ``current_stream()`` returns the compute stream;
+    ``synchronize()`` waits for the device before events are read.
+    """
+
+    def __init__(
+        self,
+        trap_labels: Sequence[str] | None = None,
+        *,
+        enabled: bool = True,
+        event_factory: Callable[[], Any] | None = None,
+        current_stream: Callable[[], Any] | None = None,
+        synchronize: Callable[[], None] | None = None,
+        on_pass: Callable[[OffloadTimingSnapshot], None] | None = None,
+        max_passes: int = 1024,
+    ) -> None:
+        self.enabled = enabled
+        self._labels = list(trap_labels or [])
+        self._label_set = set(self._labels) if enabled else set()
+        self._on_pass = on_pass
+        self._max_passes = max_passes
+        self.snapshots: list[OffloadTimingSnapshot] = []
+        self._pass_active = False
+        self._events: dict[str, dict[str, Any]] = {}
+        self._done: dict[str, set[str]] = {"transfer": set(), "compute": set(), "wait": set()}
+        if not enabled:
+            return
+        if event_factory is None or current_stream is None or synchronize is None:
+            from . import hip
+
+            event_factory = event_factory or (lambda: hip.HipEvent(timing=True))
+            current_stream = current_stream or hip.current_stream
+            synchronize = synchronize or (lambda: hip.nat.call("ftx_device_synchronize"))
+        self._current_stream = current_stream
+        self._synchronize = synchronize
+        for label in self._labels:
+            self._events[label] = {k: event_factory() for k in ("ts", "te", "cs", "ce", "ws", "we")}
+
+    def _rec(self, label: str, key: str, stream: Any = None) -> None:
+        self._events[label][key].record(stream if stream is not None else self._current_stream())
+
+    def record_transfer_start(self, label: str, stream: Any) -> None:
+        if label in self._label_set:
+            self._rec(label, "ts", stream)
+            self._done["transfer"].discard(label)
+
+    def record_transfer_end(self, label: str, stream: Any) -> None:
+        if label in self._label_set:
+            self._rec(label, "te", stream)
+            self._done["transfer"].add(label)
+
+    def record_compute_start(self, label: str) -> None:
+        if label in self._label_set:
+            self._rec(label, "cs")
+            self._done["compute"].discard(label)
+
+    def record_compute_end(self, label: str) -> None:
+        if label in self._label_set:
+            self._rec(label, "ce")
+            self._done["compute"].add(label)
+
+    def record_wait_start(self, label: str) -> None:
+        if label in self._label_set:
+            self._rec(label, "ws")
+            self._done["wait"].discard(label)
+
+    def record_wait_end(self, label: str) -> None:
+        if label in self._label_set:
+            self._rec(label, "we")
+            self._done["wait"].add(label)
+
+    def on_pass_start(self) -> None:
+        if not self.enabled:
+            return
+        if self._pass_active:
+            self._finalize()
+        self._pass_active = True
+
+    def flush(self) -> bool:
+        """Publish a pending pass (the newest pass is otherwise only finalized by the next one)."""
+        if not self.enabled or not self._pass_active:
+            return False
+        self._finalize()
+        return True
+
+    def _finalize(self) -> None:
+        self._synchronize()
+        recs = []
+        for label in self._labels:
+            ev = self._events[label]
+            t = ev["ts"].elapsed_time(ev["te"]) if label in self._done["transfer"] else 0.0
+            c = ev["cs"].elapsed_time(ev["ce"]) if label in self._done["compute"] else 0.0
+            w = ev["ws"].elapsed_time(ev["we"]) if label in self._done["wait"] else 0.0
+            recs.append(TrapTimingRecord(label, t, c, w))
+        for s in self._done.values():
+            s.clear()
+        self._pass_active = False
+        snap = OffloadTimingSnapshot(recs)
+        self.snapshots.append(snap)
+        del self.snapshots[: max(0, len(self.snapshots) - self._max_passes)]
+        if self._on_pass is not None:
+            self._on_pass(snap)
+
+    def report(self) -> OffloadTimingReport:
+        self.flush()
+        return OffloadTimingReport(list(self.snapshots))
+
+    def reset(self) -> None:
+        self.snapshots.clear()
+        for s in self._done.values():
+            s.clear()
+        self._pass_active = False

@@ -1,0 +1,148 @@
+/*
+ * ftx.h - C ABI of the MI355X weight-streaming engine (libftx_hip.so).
+ *
+ * Plain pointers, sizes and opaque handles only; no C++ or torch types cross
+ * this boundary. Every entry point returns an int status (FTX_OK on success);
+ * ftx_last_error() returns the calling thread's message for the last failure.
+ * Streams are hipStream_t values passed as void* (on the Python side they come
+ * from torch.cuda.Stream.cuda_stream). All calls for one engine instance must
+ * come from one host thread, as in the reference (core/transfer.py:42-46).
+ *
+ * Each declaration names the reference construct it replaces. The reference is
+ * pure Python over PyTorch, so "replaces" means the PyTorch call the reference
+ * makes on this path.
+ */
+#ifndef FTX_H_
+#define FTX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define FTX_OK 0
+#define FTX_ERR_INVALID 1     /* bad argument (null, misaligned, out of range) */
+#define FTX_ERR_HIP 2         /* the HIP runtime returned an error           */
+#define FTX_ERR_OOM 3         /* host or device allocation failed            */
+#define FTX_ERR_UNSUPPORTED 4 /* request not possible for this memory/device */
+
+/* ---- copy engines ------------------------------------------------------ */
+#define FTX_COPY_SDMA 0   /* hipMemcpyAsync (SDMA engines), optionally split over copy streams */
+#define FTX_COPY_KERNEL 1 /* zero-copy kernel: CUs read mapped pinned host memory             */
+#define FTX_COPY_AUTO 2   /* pick per chunk from the policy set by ftx_set_copy_policy         */
+
+/* ---- host arena flags -------------------------------------------------- */
+#define FTX_ARENA_DEFAULT 0u
+#define FTX_ARENA_COHERENT 1u      /* hipHostMallocCoherent (fine-grained)     */
+#define FTX_ARENA_NONCOHERENT 2u   /* hipHostMallocNonCoherent (coarse-grained) */
+#define FTX_ARENA_WRITECOMBINED 4u /* hipHostMallocWriteCombined              */
+
+/* ---- events ------------------------------------------------------------ */
+#define FTX_EVENT_DEFAULT 0u /* no timing: cheapest record/wait */
+#define FTX_EVENT_TIMING 1u  /* timing enabled (ftx_event_elapsed_ms) */
+
+/* One scatter descriptor: dst[0:nbytes) = chunk[src_off : src_off+nbytes).
+ * Replaces the per-tensor copies the reference makes when it places tensors
+ * (allocation_block.py:179-186 pack; tensor_processors.py:685-742 move of
+ * unmapped tensors; loaders.py:592-617 per-tensor .to()). */
+typedef struct ftx_desc {
+  uint64_t src_off; /* byte offset inside the streamed chunk */
+  uint64_t dst;     /* device address of the destination     */
+  uint64_t nbytes;  /* bytes to copy                         */
+} ftx_desc;
+
+/* Opaque scatter plan: descriptor table + per-tile work table resident in HBM. */
+typedef struct ftx_scatter_plan ftx_scatter_plan;
+
+/* ---- library / device -------------------------------------------------- */
+const char *ftx_last_error(void);
+int ftx_version(void);                 /* returns the ABI version number (not a status) */
+int ftx_device_count(int *count);
+int ftx_set_device(int device);
+int ftx_get_device(int *device);
+int ftx_device_synchronize(void);
+/* CU count and L2-domain (XCD) count of the current device, for launch shaping. */
+int ftx_device_info(int *cu_count, int *xcd_count, size_t *total_mem);
+
+/* ---- host arenas ---------------------------------------------------------
+ * Replace HostPinner.pin in "torch" mode (host_pinning.py:374-400: a fresh
+ * pinned copy via Tensor.pin_memory) with one page-locked, device-mapped arena
+ * per packed block. */
+int ftx_arena_alloc(size_t nbytes, unsigned flags, void **host);
+int ftx_arena_free(void *host);
+/* Replace HostPinRegistry.pin_in_place (host_pinning.py:206-265, the
+ * cudaHostRegister(ptr, n, Portable) call at :257) and SHM pinning
+ * (shm/flexible_shm.py:832-848): page-lock existing memory in place. */
+int ftx_arena_register(void *host, size_t nbytes, unsigned flags);
+int ftx_arena_unregister(void *host);
+/* Device-visible address of pinned host memory (zero-copy kernel source). */
+int ftx_host_device_ptr(void *host, void **dev);
+
+/* ---- device memory (ring slots when no torch allocator is in use) -------
+ * Replace AllocationManager.create_max_block (allocation_block.py:260-280). */
+int ftx_device_alloc(size_t nbytes, void **dev);
+int ftx_device_free(void *dev);
+int ftx_memset_async(void *dev, int value, size_t nbytes, void *stream);
+int ftx_copy_d2h(void *dst_host, const void *src_dev, size_t nbytes, void *stream);
+
+/* ---- streams and events --------------------------------------------------
+ * Replace torch.cuda.Stream / Stream.record_event / Stream.wait_event /
+ * Stream.synchronize as used by CudaTransferRuntime (core/transfer.py:49,
+ * 69-70, 92, 97, 109, 116, 124-125, 20). Streams are created at default
+ * priority. */
+int ftx_stream_create(void **stream);
+int ftx_stream_destroy(void *stream);
+int ftx_stream_synchronize(void *stream);
+int ftx_stream_query(void *stream, int *done);
+int ftx_event_create(unsigned flags, void **event);
+int ftx_event_destroy(void *event);
+int ftx_event_record(void *event, void *stream);
+int ftx_stream_wait_event(void *stream, void *event);
+int ftx_event_query(void *event, int *done);
+int ftx_event_synchronize(void *event);
+int ftx_event_elapsed_ms(void *start, void *end, float *ms);
+
+/* ---- host-to-device copy engines ------------------------------------------
+ * Replace AllocationBlock.copy_to (allocation_block.py:104-106) and
+ * RawBlockController.schedule_transfer (loaders.py:1064-1067), i.e.
+ * gpu_view.copy_(pinned_block, non_blocking=True) on the transfer stream.
+ * Stream-ordered on `stream`: work split over internal copy streams is forked
+ * from and joined back into `stream`. `src` must be pinned host memory. */
+int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stream);
+/* Policy used by FTX_COPY_AUTO and by FTX_COPY_SDMA splitting:
+ *   kernel_max_bytes  chunks <= this go to the zero-copy kernel under AUTO;
+ *   split_min_bytes   SDMA copies >= this are split over n_copy_streams;
+ *   n_copy_streams    1..8 dedicated copy streams;
+ *   kernel_grid       zero-copy kernel workgroups (0 = derive from CU count). */
+int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams,
+                        int kernel_grid);
+int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams,
+                        int *kernel_grid);
+
+/* ---- batched scatter / unpack --------------------------------------------
+ * No reference counterpart; it places a streamed chunk into many tensors in
+ * one launch where the reference copies tensor by tensor (see ftx_desc).
+ * A plan uploads descriptors once (device memory) and can be run any number
+ * of times on any stream; tile_bytes 0 selects the default (64 KiB). */
+int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes,
+                            ftx_scatter_plan **plan);
+int ftx_scatter_plan_destroy(ftx_scatter_plan *plan);
+int ftx_scatter_plan_info(const ftx_scatter_plan *plan, int *n_desc, int64_t *n_tiles,
+                          uint64_t *total_bytes);
+int ftx_scatter_run(const ftx_scatter_plan *plan, const void *chunk, void *stream);
+/* One-shot form: stream-ordered upload of the table, launch, stream-ordered free. */
+int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stream);
+
+/* ---- checksums (size-independent parity checks on device data) ----------- */
+/* Order-sensitive 64-bit checksum of nbytes at dev (FNV-1a over 8-byte lanes,
+ * folded per 4 KiB block); result written to *out after stream sync. */
+int ftx_checksum64(const void *dev, size_t nbytes, void *stream, uint64_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FTX_H_ */
