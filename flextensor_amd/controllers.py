@@ -1,0 +1,287 @@
+"""Block controllers: own the pinned label blocks and the GPU ring slots.
+
+:class:`AllocationBlockController` follows the reference controller of the
+same name (loaders.py:1104-1416): one 128-byte aligned pinned block per
+label, one GPU slot per slot group sized to the group's largest block, typed
+GPU views at the same byte offsets (the model's parameters alias them), and
+``schedule_transfer(label)`` = one host-to-device copy of the label's block
+into its slot on the current (transfer) stream.
+
+:class:`RawBlockController` follows ``RawBlockController`` (loaders.py:903-1101):
+back-to-back packing without alignment; dense tensors are copied as raw
+storage bytes, tensors with gaps as C-contiguous copies.
+
+Failures during construction restore every source tensor that had already
+been packed and released (the reference's construction rollback,
+loaders.py:1194-1207) before the error propagates.
+"""
+
+from __future__ import annotations
+
+import logging
+from collections.abc import Mapping, Sequence
+from typing import Any
+
+import torch
+
+from . import _native as nat
+from .allocation_block import AllocationBlock, AllocationManager, HostPinner
+from .layout import contiguous_strides, is_dense_layout, raw_storage_bytes, view_from_block
+from .planner import TensorStatistics
+
+LOGGER = logging.getLogger(__name__)
+
+
+class _Rollback:
+    """Remembers packed-and-released sources so a failed build can restore them."""
+
+    def __init__(self) -> None:
+        self._entries: list[tuple[torch.Tensor, torch.Tensor]] = []  # (source, host view holding its bytes)
+
+    def record(self, source: torch.Tensor, view: torch.Tensor) -> None:
+        self._entries.append((source, view))
+
+    def restore(self) -> None:
+        for source, view in reversed(self._entries):
+            if source.numel() == 0 and view.numel() != 0:
+                source.data = view.detach().clone()
+        self._entries.clear()
+
+    def commit(self) -> None:
+        self._entries.clear()
+
+
+def _unique_tensors(strategy: Sequence[TensorStatistics], tensors_map: Mapping[int, torch.Tensor]):
+    seen: set[int] = set()
+    ids, tensors = [], []
+    for info in strategy:
+        if info.tensor_id in seen:
+            continue
+        seen.add(info.tensor_id)
+        ids.append(info.tensor_id)
+        tensors.append(tensors_map[info.tensor_id])
+    return ids, tensors
+
+
+class AllocationBlockController:
+    def __init__(
+        self,
+        allocation_ordered: Mapping[int, Sequence[str]],
+        device_gpu: torch.device,
+        tensors_map: Mapping[int, torch.Tensor],
+        strategy_map: Mapping[str, Sequence[TensorStatistics]],
+        label_to_block_id: Mapping[str, int],
+        *,
+        host_pinner: HostPinner,
+        release_tensor_memory: bool = True,
+        copy_mode: int = nat.COPY_AUTO,
+        memory_alignment: int = 128,
+    ) -> None:
+        self.device_gpu = torch.device(device_gpu)
+        self.host_pinner = host_pinner
+        self.release_tensor_memory = release_tensor_memory
+        self.copy_mode = copy_mode
+        self.block_map_cpu: dict[str, AllocationBlock] = {}
+        self.label_to_cpu_tensor_id_map: dict[str, list[int]] = {}
+        self.label_to_gpu_block: dict[str, AllocationBlock] = {}
+        self.block_map_gpu: dict[int, torch.Tensor] = {}
+        self.gpu_block_view_map: dict[str, torch.Tensor] = {}
+        self.label_to_tensor_views_map: dict[str, list[torch.Tensor]] = {}
+        self.tensor_id_to_view_map: dict[int, torch.Tensor] = {}
+        self._gpu_slots: list[AllocationBlock] = []
+        self._rollback = _Rollback()
+        try:
+            for _slot_id, labels in allocation_ordered.items():
+                manager = AllocationManager(host_pinner=host_pinner, memory_alignment=memory_alignment,
+                                            release_tensor_memory=False)
+                for label in labels:
+                    strategy = strategy_map.get(label, ())
+                    if not strategy:
+                        continue
+                    ids, tensors = _unique_tensors(strategy, tensors_map)
+                    block = manager.block()
+                    for t in tensors:
+                        block.add(t)
+                    views = block.allocate()
+                    if release_tensor_memory:
+                        for t, v in zip(tensors, views):
+                            self._rollback.record(t, v)
+                            t.data = torch.empty(0, dtype=t.dtype)
+                    self.block_map_cpu[label] = block
+                    self.label_to_cpu_tensor_id_map[label] = ids
+                slot = manager.create_max_block(self.device_gpu)
+                self._gpu_slots.append(slot)
+                for label in labels:
+                    self.label_to_gpu_block[label] = slot
+            for label, block in self.block_map_cpu.items():
+                views, prefix = block.project_views(self.label_to_gpu_block[label])
+                self.label_to_tensor_views_map[label] = views
+                self.block_map_gpu[label_to_block_id[label]] = prefix
+                self.gpu_block_view_map[label] = prefix
+            self.prepare_tensor_id_to_view_mapping()
+        except BaseException:
+            self._rollback.restore()
+            self._clear()
+            raise
+
+    def prepare_tensor_id_to_view_mapping(self) -> None:
+        self.tensor_id_to_view_map = {}
+        for label, views in self.label_to_tensor_views_map.items():
+            for tid, view in zip(self.label_to_cpu_tensor_id_map[label], views):
+                self.tensor_id_to_view_map[tid] = view
+
+    def get_tensor_id_to_view_mapping(self) -> dict[int, torch.Tensor]:
+        return self.tensor_id_to_view_map
+
+    def cpu_views(self, label: str) -> list[torch.Tensor]:
+        return self.block_map_cpu[label].views
+
+    def schedule_transfer(self, label: str, non_blocking: bool = True) -> None:
+        """One host-to-device copy of ``label``'s block into its slot, on the current stream."""
+        self.block_map_cpu[label].copy_to(self.gpu_block_view_map[label], non_blocking=non_blocking,
+                                          mode=self.copy_mode)
+
+    def transfer_bytes(self, label: str) -> int:
+        return self.block_map_cpu[label].nbytes
+
+    def commit_construction(self) -> None:
+        self._rollback.commit()
+
+    def abort_construction(self, primary_error: BaseException | None = None) -> None:
+        self.shutdown()
+
+    def _clear(self) -> None:
+        for d in (self.block_map_cpu, self.label_to_cpu_tensor_id_map, self.label_to_gpu_block, self.block_map_gpu,
+                  self.gpu_block_view_map, self.label_to_tensor_views_map, self.tensor_id_to_view_map):
+            d.clear()
+        self._gpu_slots = []
+
+    def shutdown(self) -> None:
+        self._rollback.restore()
+        self._clear()
+
+    def release_gpu_blocks(self) -> None:
+        self.label_to_gpu_block = {}
+        self.block_map_gpu = {}
+        self.gpu_block_view_map = {}
+        self.label_to_tensor_views_map = {}
+        self.tensor_id_to_view_map = {}
+        self._gpu_slots = []
+
+    def get_gpu_memory_bytes(self) -> int:
+        return sum(s.nbytes for s in self._gpu_slots)
+
+
+class RawBlockController:
+    def __init__(
+        self,
+        label_to_size_map: Mapping[str, int],
+        block_sizes: Mapping[int, int],
+        device_gpu: torch.device,
+        tensors_map: Mapping[int, torch.Tensor],
+        strategy_map: Mapping[str, Sequence[TensorStatistics]],
+        label_to_block_id: Mapping[str, int],
+        *,
+        host_pinner: HostPinner,
+        release_tensor_memory: bool = True,
+        copy_mode: int = nat.COPY_AUTO,
+    ) -> None:
+        self.device_gpu = torch.device(device_gpu)
+        self.host_pinner = host_pinner
+        self.release_tensor_memory = release_tensor_memory
+        self.copy_mode = copy_mode
+        self.label_to_block_id = dict(label_to_block_id)
+        self.block_map_cpu: dict[str, torch.Tensor] = {}
+        self.block_meta_map: dict[str, list] = {}
+        self.label_to_cpu_tensor_id_map: dict[str, list[int]] = {}
+        for label, strategy in strategy_map.items():
+            if not strategy:
+                continue
+            ids, tensors = _unique_tensors(strategy, tensors_map)
+            block = host_pinner.new_block(label_to_size_map[label])
+            block.zero_()
+            self.block_map_cpu[label] = block
+            self.block_meta_map[label] = self.combine_tensors(tensors, block)
+            self.label_to_cpu_tensor_id_map[label] = ids
+        self.block_map_gpu = {
+            b: torch.zeros(max(n, 1), dtype=torch.uint8, device=self.device_gpu) for b, n in block_sizes.items()
+        }
+        self.gpu_block_view_map = {
+            label: self.block_map_gpu[b][: self.block_map_cpu[label].numel()]
+            for label, b in self.label_to_block_id.items()
+            if label in self.block_map_cpu
+        }
+        self.prepare_tensor_id_to_view_mapping()
+
+    def combine_tensors(self, tensors: Sequence[torch.Tensor], combined: torch.Tensor) -> list:
+        """Pack back to back; metadata per tensor is (start, end, shape, dtype, stride)."""
+        meta = []
+        cursor = 0
+        for t in tensors:
+            n = t.numel() * t.element_size()
+            if is_dense_layout(t):
+                stride = tuple(t.stride())
+                src = raw_storage_bytes(t.detach()) if t.numel() else torch.empty(0, dtype=torch.uint8)
+            else:
+                c = t.detach().contiguous()
+                stride = contiguous_strides(c.shape)
+                src = c.view(-1).view(torch.uint8)
+            combined[cursor: cursor + n] = src
+            meta.append((cursor, cursor + n, tuple(t.shape), t.dtype, stride))
+            cursor += n
+            if self.release_tensor_memory:
+                t.data = torch.empty(0, dtype=t.dtype)
+        return meta
+
+    @staticmethod
+    def reconstruct_original_shapes(combined: torch.Tensor, metadata: Sequence) -> list[torch.Tensor]:
+        return [view_from_block(combined, dtype, shape, start, stride) for start, _end, shape, dtype, stride in metadata]
+
+    def prepare_tensor_id_to_view_mapping(self) -> None:
+        self.label_to_tensor_views_map = {
+            label: self.reconstruct_original_shapes(self.block_map_gpu[self.label_to_block_id[label]], meta)
+            for label, meta in self.block_meta_map.items()
+        }
+        self.tensor_id_to_view_map = {}
+        for label, views in self.label_to_tensor_views_map.items():
+            for tid, v in zip(self.label_to_cpu_tensor_id_map[label], views):
+                self.tensor_id_to_view_map[tid] = v
+
+    def get_tensor_id_to_view_mapping(self) -> dict[int, torch.Tensor]:
+        return self.tensor_id_to_view_map
+
+    def schedule_transfer(self, label: str, non_blocking: bool = True) -> None:
+        from .hip import copy_h2d, current_stream
+
+        dst = self.gpu_block_view_map[label]
+        copy_h2d(dst, self.block_map_cpu[label], self.copy_mode)
+        if not non_blocking:
+            current_stream(dst.device).synchronize()
+
+    def transfer_bytes(self, label: str) -> int:
+        return self.block_map_cpu[label].numel()
+
+    def commit_construction(self) -> None:
+        return None
+
+    def abort_construction(self, primary_error: BaseException | None = None) -> None:
+        self.shutdown()
+
+    def shutdown(self) -> None:
+        for d in (self.block_map_cpu, self.block_meta_map, self.label_to_cpu_tensor_id_map, self.block_map_gpu,
+                  self.gpu_block_view_map, self.label_to_tensor_views_map, self.tensor_id_to_view_map):
+            d.clear()
+
+    def release_gpu_blocks(self) -> None:
+        self.block_map_gpu = {}
+        self.gpu_block_view_map = {}
+        self.label_to_tensor_views_map = {}
+        self.tensor_id_to_view_map = {}
+
+    def get_gpu_memory_bytes(self) -> int:
+        return sum(b.numel() for b in self.block_map_gpu.values())
+
+
+def describe(controller: Any) -> str:
+    labels = list(getattr(controller, "block_map_cpu", {}))
+    return f"{type(controller).__name__}(labels={len(labels)}, gpu_bytes={controller.get_gpu_memory_bytes()})"

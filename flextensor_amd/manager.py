@@ -1,0 +1,512 @@
+"""``offload(model, config)``: the reference's entry point and phase contract.
+
+Phases advance after each forward of the root module, as in the reference
+(offload_manager.py:297-303, 1747-1820): ``DISCOVERY`` (execution order of
+the offload units), ``PROFILING`` (per-unit compute time), then
+``INFERENCE``, when the plan is computed and the streaming loader is built
+(offload_manager.py:1714-1728; tensor_manager.py:1661-1800):
+
+1. unit tensors are packed per transfer label into pinned blocks and the
+   streamed parameters alias typed views of GPU ring slots
+   (tensor_processors.py:802-833);
+2. units kept resident and every tensor outside the units are placed on the
+   GPU by stream-and-scatter (the role of tensor_processors.py:685-742);
+3. each unit's forward is wrapped in a trap that calls ``loader.enter`` /
+   ``loader.exit`` (trap_tensor_mode.py:376-397).
+
+During discovery and profiling a unit's tensors are loaded synchronously on
+``enter`` and dropped on ``exit`` (the role of the warm-up and profile
+loaders). The plan keeps every unit resident when the budget allows, and
+otherwise streams the fewest units that fit the budget, spread evenly over
+the pass; slots are added while the slot-reuse check of the reference
+(strategy_operations.py:525-620) reports a hazard.
+"""
+
+from __future__ import annotations
+
+import fnmatch
+import logging
+import re
+import threading
+import time
+from collections.abc import Sequence
+from dataclasses import dataclass, field
+from enum import Enum
+from typing import Any
+
+import torch
+from torch import nn
+
+from . import _native as nat
+from .allocation_block import HostPinner
+from .config import OffloadConfig
+from .controllers import AllocationBlockController, RawBlockController
+from .loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
+from .planner import (
+    BlockStrategyData,
+    LayerStatistics,
+    TensorStatistics,
+    check_overlap_constraint,
+    create_allocation_ordered,
+    prepare_block_strategy,
+    rearrange_transfers,
+    remap_strategy,
+)
+from .prefetch_policy import PiecewisePrefetchPolicy
+from .scatter import upload_tensors
+from .timing import OffloadTimingCollector, OffloadTimingReport
+
+LOGGER = logging.getLogger(__name__)
+DEFAULT_MANAGER_NAME = "default"
+
+
+class OffloadPhase(Enum):
+    NOT_INITIALIZED = "not_initialized"
+    DISCOVERY = "discovery"
+    PROFILING = "profiling"
+    INFERENCE = "inference"
+
+
+@dataclass(frozen=True)
+class GPUMemoryUsage:
+    """GPU bytes held by ring slots and by tensors placed permanently (types.py:13-59)."""
+
+    blocks_bytes: int = 0
+    unmapped_tensors_bytes: int = 0
+
+    @property
+    def total_bytes(self) -> int:
+        return self.blocks_bytes + self.unmapped_tensors_bytes
+
+
+@dataclass
+class StreamPlan:
+    """What the planner decided: streamed and resident units plus the slot plan."""
+
+    streamed: list[str]
+    resident: list[str]
+    block_data: BlockStrategyData | None
+    strategy_map: dict[str, list[TensorStatistics]]
+    reordered: bool
+    budget_bytes: int | None
+    planned_gpu_bytes: int
+
+
+def _glob_regex(pattern: str) -> re.Pattern[str]:
+    """``*`` and ``?`` stay within one path component; ``**`` crosses dots."""
+    out, i = [], 0
+    while i < len(pattern):
+        if pattern.startswith("**", i):
+            out.append(".*")
+            i += 2
+            continue
+        c = pattern[i]
+        out.append("[^.]*" if c == "*" else "[^.]" if c == "?" else re.escape(c))
+        i += 1
+    return re.compile("".join(out))
+
+
+def _match(path: str, pattern: str) -> bool:
+    return _glob_regex(pattern).fullmatch(path) is not None
+
+
+def _matches(path: str, module: nn.Module, patterns: Sequence[str]) -> bool:
+    for p in patterns:
+        if p.startswith("class:"):
+            body = p[len("class:"):]
+            cls = type(module)
+            if fnmatch.fnmatchcase(cls.__name__, body) or fnmatch.fnmatchcase(f"{cls.__module__}.{cls.__qualname__}", body):
+                return True
+        elif _match(path, p[len("name:"):] if p.startswith("name:") else p):
+            return True
+    return False
+
+
+def select_offload_units(model: nn.Module, include: Sequence[str], exclude: Sequence[str]) -> list[str]:
+    """Outermost modules matching ``include`` and not ``exclude``, in module order.
+
+    A matched container without its own forward (``ModuleList`` /
+    ``ModuleDict``) stands for its children.
+    """
+    chosen: list[str] = []
+    for path, mod in model.named_modules():
+        if not path or any(path.startswith(c + ".") for c in chosen):
+            continue
+        if not _matches(path, mod, include):
+            continue
+        if isinstance(mod, (nn.ModuleList, nn.ModuleDict)):
+            for child, _ in mod.named_children():
+                chosen.append(f"{path}.{child}")
+            continue
+        chosen.append(path)
+    return [p for p in chosen if not _matches(p, model.get_submodule(p), exclude)]
+
+
+@dataclass
+class _Unit:
+    label: str
+    module: nn.Module
+    params: list[nn.Parameter] = field(default_factory=list)
+
+    @property
+    def nbytes(self) -> int:
+        return sum(p.numel() * p.element_size() for p in self.params)
+
+
+def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | None, base_bytes: int,
+                   num_blocks: int) -> StreamPlan:
+    """Choose streamed units and the slot plan under a GPU byte budget."""
+    by_label = {u.label: u for u in units}
+    labels = list(order)
+    sizes = [by_label[x].nbytes for x in labels]
+    total = base_bytes + sum(sizes)
+    if budget is not None and total <= budget:
+        return StreamPlan([], labels, None, {}, False, budget, total)
+    n = len(labels)
+    stats = [LayerStatistics(x, [TensorStatistics(id(p), x, p.numel() * p.element_size()) for p in by_label[x].params])
+             for x in labels]
+    for k in range(1, n + 1):
+        pick = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
+        if len(pick) < k:
+            continue
+        streamed = [labels[i] for i in pick]
+        if budget is None and k < n:
+            continue
+        blocks = num_blocks
+        while True:
+            strategy = {}
+            for i in pick:
+                consumer = labels[i]
+                producer = labels[i - 1]  # i == 0 wraps to the last label: a cyclic preload
+                strategy[producer] = list(stats[i].tensors)
+            bd = prepare_block_strategy(strategy, stats, blocks)
+            if check_overlap_constraint(bd.transfer_to_compute_map, stats, bd.label_to_block_id):
+                break
+            blocks += 1
+            if blocks > n + 2:
+                raise RuntimeError("no hazard-free slot plan found")
+        resident = [x for x in labels if x not in streamed]
+        gpu = base_bytes + sum(by_label[x].nbytes for x in resident) + sum(bd.block_sizes.values())
+        if budget is not None and gpu > budget:
+            continue
+        reordered = bool(resident)
+        if reordered:
+            t2c, l2b, remapped = rearrange_transfers(bd.transfer_to_compute_map, bd.label_to_block_id, stats)
+            strategy = remap_strategy(strategy, remapped)
+            bd = BlockStrategyData(
+                label_to_size_map={remapped.get(k, k): v for k, v in bd.label_to_size_map.items()},
+                allocation_ordered=create_allocation_ordered(l2b, stats),
+                block_sizes=bd.block_sizes,
+                label_to_block_id=l2b,
+                transfer_to_compute_map=t2c,
+            )
+        return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
+    raise ValueError(f"GPU budget of {budget} bytes cannot hold the ring slots plus {base_bytes} resident bytes")
+
+
+class OffloadManager:
+    """One named offload session: phases, plan, loader and the patched model."""
+
+    def __init__(self, name: str = DEFAULT_MANAGER_NAME) -> None:
+        self.name = name
+        self.phase = OffloadPhase.NOT_INITIALIZED
+        self.config = OffloadConfig()
+        self.model: nn.Module | None = None
+        self.device = torch.device("cpu")
+        self.units: list[_Unit] = []
+        self.order: list[str] = []
+        self.durations: dict[str, list[float]] = {}
+        self.loader: Any = None
+        self.controller: Any = None
+        self.plan: StreamPlan | None = None
+        self.timing: OffloadTimingCollector | None = None
+        self._owner = threading.get_ident()
+        self._forwards = 0
+        self._hooks: list[Any] = []
+        self._patched: list[tuple[nn.Module, Any]] = []
+        self._resident_bytes = 0
+        self._cpu_data: dict[int, torch.Tensor] = {}
+        self._seen_this_pass: list[str] = []
+        self._events: dict[str, tuple[Any, Any]] = {}
+        self.build_seconds = 0.0
+
+    # -- public ---------------------------------------------------------------
+
+    def offload(self, model: nn.Module, config: OffloadConfig | None = None) -> nn.Module:
+        self._check_thread()
+        if self.model is not None:
+            raise RuntimeError(f"offload manager {self.name!r} already manages a model; release() it first")
+        self.config = config or OffloadConfig()
+        if not self.config.enabled:
+            return model
+        nat.load()
+        self.device = torch.device("cuda", self.config.gpu_device)
+        torch.cuda.set_device(self.device)
+        self.model = model
+        labels = select_offload_units(model, self.config.include_patterns, self.config.exclude_patterns)
+        unit_params: set[int] = set()
+        for label in labels:
+            mod = model.get_submodule(label)
+            params = [p for p in mod.parameters() if id(p) not in unit_params]
+            unit_params.update(id(p) for p in params)
+            self.units.append(_Unit(label, mod, params))
+        self._place_outside_units(unit_params)
+        for u in self.units:
+            self._patch(u)
+        self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
+        self.phase = OffloadPhase.DISCOVERY if self.config.discovery_iters > 0 else OffloadPhase.PROFILING
+        if self.config.discovery_iters == 0 and self.config.profiling_iters == 0:
+            self.order = [u.label for u in self.units]
+            self._to_inference()
+        return model
+
+    def iters_before_inference(self) -> int:
+        if self.phase == OffloadPhase.INFERENCE:
+            return 0
+        return max(0, self.config.discovery_iters + self.config.profiling_iters - self._forwards)
+
+    def get_gpu_memory_usage(self) -> GPUMemoryUsage:
+        blocks = self.loader.get_gpu_memory_bytes() if self.loader is not None else 0
+        return GPUMemoryUsage(blocks, self._resident_bytes)
+
+    def collect_offload_timing(self) -> OffloadTimingReport | None:
+        return self.timing.report() if self.timing is not None and self.timing.enabled else None
+
+    def reset_offload_timing(self) -> None:
+        if self.timing is not None:
+            self.timing.reset()
+
+    def release(self, preserve_model: bool = True) -> None:
+        """Stop streaming and hand the model back (tensors on the CPU when preserved)."""
+        self._check_thread()
+        if self.model is None:
+            return
+        torch.cuda.synchronize(self.device)
+        for h in self._hooks:
+            h.remove()
+        for mod, orig in self._patched:
+            if "forward" in mod.__dict__:
+                del mod.forward
+        restore = {}
+        if self.controller is not None and preserve_model:
+            for label in self.controller.block_map_cpu:
+                ids = self.controller.label_to_cpu_tensor_id_map[label]
+                for tid, view in zip(ids, self._cpu_views(label)):
+                    restore[tid] = view
+        params = {id(p): p for u in self.units for p in u.params}
+        params.update({id(p): p for p in self.model.parameters()})
+        if self.loader is not None:
+            self.loader.shutdown()
+        for tid, p in params.items():
+            if not preserve_model:
+                p.data = torch.empty(0, dtype=p.dtype)
+            elif tid in restore:
+                p.data = restore[tid].clone()
+            elif p.device.type != "cpu":
+                p.data = p.data.cpu()
+        if preserve_model:
+            for b in self.model.buffers():
+                b.data = b.data.cpu()
+        self.loader = self.controller = self.plan = None
+        self.model = None
+        self.units, self._patched, self._hooks = [], [], []
+        self.phase = OffloadPhase.NOT_INITIALIZED
+
+    # -- internals ------------------------------------------------------------
+
+    def _check_thread(self) -> None:
+        if threading.get_ident() != self._owner:
+            raise RuntimeError(f"offload manager {self.name!r} is owned by another thread")
+
+    def _cpu_views(self, label: str) -> list[torch.Tensor]:
+        block = self.controller.block_map_cpu[label]
+        if isinstance(self.controller, RawBlockController):
+            from .controllers import RawBlockController as R
+
+            return R.reconstruct_original_shapes(block, self.controller.block_meta_map[label])
+        return block.views
+
+    def _place_outside_units(self, unit_params: set[int]) -> None:
+        """Tensors outside the offload units go to the GPU once (stream-and-scatter)."""
+        assert self.model is not None
+        rest = [p for p in self.model.parameters() if id(p) not in unit_params and p.device.type == "cpu"]
+        bufs = [b for b in self.model.buffers() if b.device.type == "cpu"]
+        self._resident_bytes += self._upload_into(rest + bufs)
+
+    def _upload_into(self, tensors: Sequence[torch.Tensor]) -> int:
+        cpu = [t for t in tensors if t.device.type == "cpu" and t.numel()]
+        if not cpu:
+            return 0
+        dests = upload_tensors([t.data for t in cpu], self.device)
+        for t, d in zip(cpu, dests):
+            t.data = d
+        return sum(t.numel() * t.element_size() for t in cpu)
+
+    def _patch(self, unit: _Unit) -> None:
+        orig = unit.module.forward
+        mgr, label = self, unit.label
+
+        def forward(*args: Any, **kwargs: Any) -> Any:
+            mgr._enter(label)
+            out = orig(*args, **kwargs)
+            mgr._exit(label)
+            return out
+
+        unit.module.forward = forward
+        self._patched.append((unit.module, orig))
+
+    def _unit(self, label: str) -> _Unit:
+        for u in self.units:
+            if u.label == label:
+                return u
+        raise KeyError(label)
+
+    def _enter(self, label: str) -> None:
+        if self.phase == OffloadPhase.INFERENCE:
+            self.loader.enter(label)
+            return
+        if label in self._seen_this_pass:
+            raise NotImplementedError(f"offload unit {label!r} ran twice in one forward")
+        self._seen_this_pass.append(label)
+        u = self._unit(label)
+        for p in u.params:
+            self._cpu_data[id(p)] = p.data
+            p.data = p.data.to(self.device, non_blocking=False)
+        if self.phase == OffloadPhase.PROFILING:
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            self._events[label] = (start, end)
+
+    def _exit(self, label: str) -> None:
+        if self.phase == OffloadPhase.INFERENCE:
+            self.loader.exit(label)
+            return
+        if self.phase == OffloadPhase.PROFILING:
+            self._events[label][1].record()
+        u = self._unit(label)
+        for p in u.params:
+            p.data = self._cpu_data.pop(id(p))
+
+    def _after_forward(self) -> None:
+        if self.phase == OffloadPhase.INFERENCE:
+            return
+        self._forwards += 1
+        if self.phase == OffloadPhase.DISCOVERY:
+            if not self.order:
+                self.order = list(self._seen_this_pass)
+            if self._forwards >= self.config.discovery_iters:
+                self.phase = OffloadPhase.PROFILING
+        elif self.phase == OffloadPhase.PROFILING:
+            if not self.order:
+                self.order = list(self._seen_this_pass)
+            torch.cuda.synchronize(self.device)
+            for label, (s, e) in self._events.items():
+                self.durations.setdefault(label, []).append(s.elapsed_time(e))
+            self._events.clear()
+        self._seen_this_pass = []
+        if self.phase == OffloadPhase.PROFILING and self._forwards >= self.config.discovery_iters + self.config.profiling_iters:
+            self._to_inference()
+
+    def _budget(self) -> int | None:
+        if self.config.max_gpu_mem_bytes is not None:
+            return self.config.max_gpu_mem_bytes
+        if self.config.max_gpu_mem_fraction is not None:
+            total = torch.cuda.get_device_properties(self.device).total_memory
+            return int(total * self.config.max_gpu_mem_fraction)
+        return None
+
+    def _to_inference(self) -> None:
+        t0 = time.perf_counter()
+        cfg = self.config
+        units_in_order = [self._unit(x) for x in self.order] if self.order else list(self.units)
+        order = [u.label for u in units_in_order]
+        blocks = max(cfg.num_blocks, 2)
+        self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks)
+        plan = self.plan
+        resident_params = [p for x in plan.resident for p in self._unit(x).params]
+        self._resident_bytes += self._upload_into(resident_params)
+        layer_stats = [
+            LayerStatistics(x, [TensorStatistics(id(p), x, p.numel() * p.element_size()) for p in self._unit(x).params],
+                            float(sum(self.durations.get(x, [0.0])) / max(1, len(self.durations.get(x, [])))))
+            for x in order
+        ]
+        if plan.block_data is None:
+            self.loader = _ResidentLoader()
+        else:
+            bd = plan.block_data
+            tensors_map = {id(p): p for x in plan.streamed for p in self._unit(x).params}
+            pinner = HostPinner(cfg.pinned_memory_mode, enabled=cfg.pinned_memory)
+            mode = nat.COPY_MODES[cfg.copy_engine]
+            if cfg.transfer_mode == "raw_block_transfer":
+                self.controller = RawBlockController(bd.label_to_size_map, bd.block_sizes, self.device, tensors_map,
+                                                     plan.strategy_map, bd.label_to_block_id, host_pinner=pinner,
+                                                     copy_mode=mode)
+            else:
+                self.controller = AllocationBlockController(bd.allocation_ordered, self.device, tensors_map,
+                                                            plan.strategy_map, bd.label_to_block_id,
+                                                            host_pinner=pinner, copy_mode=mode)
+            for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
+                tensors_map[tid].data = view
+            reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"
+            cls = PreallocatedBatchTransferTensorLoaderReordered if reordered else PreallocatedBatchTransferTensorLoader
+            self.timing = OffloadTimingCollector(order, enabled=cfg.offload_timing == "eager")
+            policy = PiecewisePrefetchPolicy(enabled=cfg.piecewise_prefetch != "off",
+                                             strict=cfg.piecewise_prefetch == "error")
+            self.loader = cls(layer_stats, self.device, bd.label_to_block_id, bd.transfer_to_compute_map,
+                              self.controller, self.timing, policy)
+            self.controller.commit_construction()
+        self.phase = OffloadPhase.INFERENCE
+        self.build_seconds = time.perf_counter() - t0
+        LOGGER.info("offload %r: %d streamed / %d resident units, %.1f s to build", self.name, len(plan.streamed),
+                    len(plan.resident), self.build_seconds)
+
+
+class _ResidentLoader:
+    """Everything fits the budget: traps do nothing."""
+
+    def enter(self, label: str) -> None:
+        return None
+
+    def exit(self, label: str) -> None:
+        return None
+
+    def shutdown(self) -> None:
+        return None
+
+    def get_gpu_memory_bytes(self) -> int:
+        return 0
+
+
+_MANAGERS: dict[str, OffloadManager] = {}
+
+
+def get_offload_manager(name: str = DEFAULT_MANAGER_NAME) -> OffloadManager:
+    mgr = _MANAGERS.get(name)
+    if mgr is None:
+        mgr = _MANAGERS[name] = OffloadManager(name)
+    mgr._check_thread()
+    return mgr
+
+
+def offload(model: nn.Module, config: OffloadConfig | None = None, name: str = DEFAULT_MANAGER_NAME) -> nn.Module:
+    """Patch ``model`` so its offload units stream from pinned host memory."""
+    return get_offload_manager(name).offload(model, config)
+
+
+def release(name: str = DEFAULT_MANAGER_NAME, preserve_model: bool = True) -> None:
+    mgr = _MANAGERS.pop(name, None)
+    if mgr is not None:
+        mgr.release(preserve_model)
+
+
+def get_gpu_memory_usage(name: str = DEFAULT_MANAGER_NAME) -> GPUMemoryUsage:
+    return get_offload_manager(name).get_gpu_memory_usage()
+
+
+def collect_offload_timing(name: str = DEFAULT_MANAGER_NAME) -> OffloadTimingReport | None:
+    return get_offload_manager(name).collect_offload_timing()
+
+
+def reset_offload_timing(name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).reset_offload_timing()

@@ -1,0 +1,260 @@
+"""Synthetic, seeded workloads that exercise the streaming path.
+
+* :func:`build_mlp_stack` - n x [Linear(h -> i, bias) -> SiLU -> Linear(i -> h, bias)]
+  (8 layers at 4096 -> 11008 -> 4096 for the MLP-stack workload).
+* :class:`LlamaModel` - Llama-style decoder: RMSNorm, rotary attention with a
+  KV cache, SwiGLU MLP (32 layers, hidden 4096, 32 x 128 heads, 11008
+  intermediate, vocab 32000 for the 7B shape).
+* :func:`scatter_tensor_set` - the tensor set of the scatter microbenchmark:
+  byte sizes log-uniform in [4 KiB, 64 MiB], bf16, 1-D or 2-D shapes.
+
+Weights are drawn N(0, 0.02) in float32 from one ``torch.Generator`` seeded
+with ``seed``, parameter by parameter in module registration order, then
+cast to bfloat16. ``init_device="cuda"`` draws on the device generator (fast
+for multi-GB models) and copies the result into CPU tensors; the two devices
+give different (each deterministic) weights.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+
+def init_normal_(model: nn.Module, seed: int, std: float = 0.02, init_device: str = "cpu") -> nn.Module:
+    """Overwrite every parameter with N(0, std) draws (float32, then cast)."""
+    gen = torch.Generator(device=init_device).manual_seed(seed)
+    with torch.no_grad():
+        for p in model.parameters():
+            w = torch.empty(p.shape, dtype=torch.float32, device=init_device)
+            w.normal_(0.0, std, generator=gen)
+            p.copy_(w.to(p.dtype))
+    return model
+
+
+class MLPBlock(nn.Module):
+    def __init__(self, hidden: int, inter: int, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.fc1 = nn.Linear(hidden, inter, bias=True, dtype=dtype)
+        self.fc2 = nn.Linear(inter, hidden, bias=True, dtype=dtype)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.fc2(F.silu(self.fc1(x)))
+
+
+class MLPStack(nn.Module):
+    def __init__(self, n_layers: int, hidden: int, inter: int, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.layers = nn.ModuleList(MLPBlock(hidden, inter, dtype) for _ in range(n_layers))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        for layer in self.layers:
+            x = layer(x)
+        return x
+
+
+def build_mlp_stack(n_layers: int = 8, hidden: int = 4096, inter: int = 11008, seed: int = 0,
+                    init_device: str = "cpu") -> MLPStack:
+    with torch.device("meta"):
+        model = MLPStack(n_layers, hidden, inter)
+    model = model.to_empty(device="cpu")
+    return init_normal_(model, seed, 0.02, init_device)
+
+
+def mlp_input(batch: int = 16, hidden: int = 4096, seed: int = 0) -> torch.Tensor:
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randn(batch, hidden, generator=gen, dtype=torch.float32).to(torch.bfloat16)
+
+
+# ---- Llama-style decoder -----------------------------------------------------
+
+
+@dataclass(frozen=True)
+class LlamaShape:
+    n_layers: int = 32
+    hidden: int = 4096
+    n_heads: int = 32
+    n_kv_heads: int = 32
+    head_dim: int = 128
+    inter: int = 11008
+    vocab: int = 32000
+    max_seq: int = 2048
+    eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    def layer_bytes(self, itemsize: int = 2) -> int:
+        h, d = self.hidden, self.head_dim
+        attn = h * self.n_heads * d + 2 * h * self.n_kv_heads * d + self.n_heads * d * h
+        return itemsize * (attn + 3 * h * self.inter + 2 * h)
+
+
+LLAMA_7B = LlamaShape()
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float, dtype: torch.dtype) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim, dtype=dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotary embedding with full-width cos/sin tables (halves rotate against each other)."""
+    half = x.shape[-1] // 2
+    rotated = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    return x * cos + rotated * sin
+
+
+class Attention(nn.Module):
+    def __init__(self, s: LlamaShape, dtype: torch.dtype) -> None:
+        super().__init__()
+        self.s = s
+        self.wq = nn.Linear(s.hidden, s.n_heads * s.head_dim, bias=False, dtype=dtype)
+        self.wk = nn.Linear(s.hidden, s.n_kv_heads * s.head_dim, bias=False, dtype=dtype)
+        self.wv = nn.Linear(s.hidden, s.n_kv_heads * s.head_dim, bias=False, dtype=dtype)
+        self.wo = nn.Linear(s.n_heads * s.head_dim, s.hidden, bias=False, dtype=dtype)
+
+    def forward(self, x: torch.Tensor, pos: int, cos: torch.Tensor, sin: torch.Tensor,
+                cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
+        s = self.s
+        b, t, _ = x.shape
+        q = self.wq(x).view(b, t, s.n_heads, s.head_dim)
+        k = self.wk(x).view(b, t, s.n_kv_heads, s.head_dim)
+        v = self.wv(x).view(b, t, s.n_kv_heads, s.head_dim)
+        c = cos[pos: pos + t].view(1, t, 1, -1).to(q.dtype)
+        sn = sin[pos: pos + t].view(1, t, 1, -1).to(q.dtype)
+        q, k = _rotate(q, c, sn), _rotate(k, c, sn)
+        cache_k[:b, pos: pos + t] = k
+        cache_v[:b, pos: pos + t] = v
+        keys = cache_k[:b, : pos + t]
+        vals = cache_v[:b, : pos + t]
+        rep = s.n_heads // s.n_kv_heads
+        if rep > 1:
+            keys = keys.repeat_interleave(rep, dim=2)
+            vals = vals.repeat_interleave(rep, dim=2)
+        qh = q.transpose(1, 2).contiguous()                    # [b, h, t, d]
+        kt = keys.permute(0, 2, 3, 1).contiguous()             # [b, h, d, S]  (contiguous right operand)
+        vh = vals.transpose(1, 2).contiguous()                 # [b, h, S, d]
+        scores = torch.matmul(qh, kt).float() * (1.0 / math.sqrt(s.head_dim))
+        if t > 1:
+            n = pos + t
+            mask = torch.ones(t, n, dtype=torch.bool, device=x.device).triu(diagonal=pos + 1)
+            scores = scores.masked_fill(mask, float("-inf"))
+        p = torch.softmax(scores, dim=-1).to(vh.dtype)
+        o = torch.matmul(p, vh).transpose(1, 2).reshape(b, t, s.n_heads * s.head_dim)
+        return self.wo(o)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, s: LlamaShape, dtype: torch.dtype) -> None:
+        super().__init__()
+        self.attn_norm = RMSNorm(s.hidden, s.eps, dtype)
+        self.attn = Attention(s, dtype)
+        self.mlp_norm = RMSNorm(s.hidden, s.eps, dtype)
+        self.gate = nn.Linear(s.hidden, s.inter, bias=False, dtype=dtype)
+        self.up = nn.Linear(s.hidden, s.inter, bias=False, dtype=dtype)
+        self.down = nn.Linear(s.inter, s.hidden, bias=False, dtype=dtype)
+
+    def forward(self, x: torch.Tensor, pos: int, cos: torch.Tensor, sin: torch.Tensor,
+                cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
+        x = x + self.attn(self.attn_norm(x), pos, cos, sin, cache_k, cache_v)
+        h = self.mlp_norm(x)
+        return x + self.down(F.silu(self.gate(h)) * self.up(h))
+
+
+class LlamaModel(nn.Module):
+    def __init__(self, s: LlamaShape = LLAMA_7B, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.shape = s
+        self.embed = nn.Embedding(s.vocab, s.hidden, dtype=dtype)
+        self.layers = nn.ModuleList(DecoderLayer(s, dtype) for _ in range(s.n_layers))
+        self.norm = RMSNorm(s.hidden, s.eps, dtype)
+        self.lm_head = nn.Linear(s.hidden, s.vocab, bias=False, dtype=dtype)
+        inv = 1.0 / (s.rope_theta ** (torch.arange(0, s.head_dim, 2, dtype=torch.float32) / s.head_dim))
+        ang = torch.outer(torch.arange(s.max_seq, dtype=torch.float32), inv)
+        self.register_buffer("rope_cos", torch.cat([ang.cos(), ang.cos()], -1), persistent=False)
+        self.register_buffer("rope_sin", torch.cat([ang.sin(), ang.sin()], -1), persistent=False)
+        self.cache_k: list[torch.Tensor] = []
+        self.cache_v: list[torch.Tensor] = []
+
+    def init_cache(self, batch: int, max_len: int, device: torch.device) -> None:
+        s = self.shape
+        shape = (batch, max_len, s.n_kv_heads, s.head_dim)
+        dt = self.embed.weight.dtype
+        self.cache_k = [torch.zeros(shape, dtype=dt, device=device) for _ in range(s.n_layers)]
+        self.cache_v = [torch.zeros(shape, dtype=dt, device=device) for _ in range(s.n_layers)]
+
+    def forward(self, tokens: torch.Tensor, pos: int = 0) -> torch.Tensor:
+        """Logits of the last position, float32."""
+        x = self.embed(tokens)
+        for i, layer in enumerate(self.layers):
+            x = layer(x, pos, self.rope_cos, self.rope_sin, self.cache_k[i], self.cache_v[i])
+        return self.lm_head(self.norm(x[:, -1:])).float()
+
+
+def build_llama(shape: LlamaShape = LLAMA_7B, seed: int = 0, init_device: str = "cpu") -> LlamaModel:
+    with torch.device("meta"):
+        model = LlamaModel(shape)
+    model = model.to_empty(device="cpu")
+    s = shape
+    inv = 1.0 / (s.rope_theta ** (torch.arange(0, s.head_dim, 2, dtype=torch.float32) / s.head_dim))
+    ang = torch.outer(torch.arange(s.max_seq, dtype=torch.float32), inv)
+    model.rope_cos.copy_(torch.cat([ang.cos(), ang.cos()], -1))
+    model.rope_sin.copy_(torch.cat([ang.sin(), ang.sin()], -1))
+    return init_normal_(model, seed, 0.02, init_device)
+
+
+@torch.no_grad()
+def generate(model: LlamaModel, prompt: torch.Tensor, steps: int) -> tuple[torch.Tensor, list[torch.Tensor]]:
+    """Greedy decoding with no host synchronisation between steps.
+
+    Returns the generated tokens ``[batch, steps]`` and the logits of every step.
+    """
+    logits = model(prompt, 0)
+    out, all_logits = [], [logits]
+    tok = logits.argmax(-1)
+    pos = prompt.shape[1]
+    for _ in range(steps - 1):
+        out.append(tok)
+        logits = model(tok, pos)
+        all_logits.append(logits)
+        tok = logits.argmax(-1)
+        pos += 1
+    out.append(tok)
+    return torch.cat(out, dim=1), all_logits
+
+
+def prompt_tokens(batch: int, length: int, vocab: int, seed: int = 0) -> torch.Tensor:
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (batch, length), generator=gen)
+
+
+# ---- scatter microbenchmark tensor set ------------------------------------------
+
+
+def scatter_sizes(n: int = 2000, lo: int = 4096, hi: int = 64 << 20, seed: int = 1) -> list[int]:
+    """Byte sizes log-uniform in [lo, hi], rounded down to whole bf16 elements."""
+    rng = np.random.default_rng(seed)
+    u = rng.uniform(math.log(lo), math.log(hi), size=n)
+    return [int(math.exp(x)) // 2 * 2 for x in u]
+
+
+def scatter_shape(nbytes: int, index: int) -> tuple[int, ...]:
+    """1-D for even indices, 2-D [rows, cols] (cols = largest power of two <= 1024 dividing numel) for odd."""
+    numel = nbytes // 2
+    if index % 2 == 0 or numel == 0:
+        return (numel,)
+    cols = 1
+    while cols < 1024 and numel % (cols * 2) == 0:
+        cols *= 2
+    return (numel // cols, cols)

@@ -1,0 +1,174 @@
+"""End-to-end streaming on the GPU.
+
+Parity bar (the reference's own oracle, L0_cuda_graphs/test_cuda_graphs.py:208-233
+and L0_offload_validation/offload_validation.py:629-645): the streamed forward
+is bitwise equal to the same model run fully resident with the same kernels;
+streamed slot bytes equal the packed host bytes; and the bf16 output is within
+1e-2 relative error of a float32 CPU forward.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from flextensor_amd import workloads as W
+from flextensor_amd.config import OffloadConfig
+from flextensor_amd.manager import OffloadManager, OffloadPhase
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2  # bf16 outputs vs the float32 forward
+
+
+def _rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _resident(model, device):
+    m = copy.deepcopy(model).to(device)
+    return m
+
+
+def _small_mlp(n_layers=6, hidden=256, inter=704, seed=0):
+    return W.build_mlp_stack(n_layers, hidden, inter, seed=seed)
+
+
+def _stream(model, device, **cfg):
+    # no budget: every unit streams
+    base = dict(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1, profiling_iters=1)
+    base.update(cfg)
+    mgr = OffloadManager(name=f"t{id(model)}")
+    mgr.offload(model, OffloadConfig(**base))
+    return mgr
+
+
+@pytest.mark.parametrize("copy_engine", ["auto", "sdma", "kernel"])
+@pytest.mark.parametrize("transfer_mode", ["allocation_block_transfer", "raw_block_transfer"])
+def test_mlp_streamed_equals_resident(gpu, copy_engine, transfer_mode):
+    torch.manual_seed(0)
+    model = _small_mlp()
+    x = W.mlp_input(16, 256, seed=0)
+    ref_model = _resident(model, gpu)
+    with torch.no_grad():
+        want = ref_model(x.to(gpu))
+        want32 = copy.deepcopy(model).float()(x.float())
+    mgr = _stream(model, gpu, copy_engine=copy_engine, transfer_mode=transfer_mode)
+    outs = []
+    with torch.no_grad():
+        for _ in range(5):  # discovery, profiling, then three streamed passes
+            outs.append(model(x.to(gpu)))
+    torch.cuda.synchronize()
+    assert mgr.phase == OffloadPhase.INFERENCE
+    assert mgr.plan is not None and len(mgr.plan.streamed) == 6
+    for out in outs:
+        assert torch.equal(out, want)
+    assert _rel_err(outs[-1], want32) < REL_TOL
+    # every parameter now aliases a ring slot on the device
+    assert all(p.device.type == "cuda" for p in model.parameters())
+    assert mgr.get_gpu_memory_usage().blocks_bytes > 0
+    mgr.release()
+    for p, q in zip(model.parameters(), ref_model.parameters()):
+        assert p.device.type == "cpu" and torch.equal(p, q.cpu())
+
+
+def test_slot_bytes_equal_host_bytes(gpu):
+    model = _small_mlp(4, 128, 320)
+    mgr = _stream(model, gpu)
+    x = W.mlp_input(4, 128, seed=1).to(gpu)
+    with torch.no_grad():
+        for _ in range(2):
+            model(x)
+    ctrl = mgr.controller
+    rt = mgr.loader._transfer_runtime
+    s = mgr.loader.backend.current_stream()
+    for label in ctrl.block_map_cpu:
+        rt.begin()
+        t = rt.submit(mgr.loader.label_to_block_id[label], lambda label=label: ctrl.schedule_transfer(label))
+        rt.wait_ready(t)
+        rt.join()
+        s.synchronize()
+        host = ctrl.block_map_cpu[label].block
+        dev = ctrl.gpu_block_view_map[label]
+        assert torch.equal(dev.cpu(), host)
+    mgr.release()
+
+
+def test_partial_budget_uses_reordered_loader(gpu):
+    model = _small_mlp(8, 256, 704, seed=3)
+    x = W.mlp_input(16, 256, seed=3)
+    want = _resident(model, gpu)(x.to(gpu)).detach()
+    layer = sum(p.numel() * 2 for p in model.layers[0].parameters())
+    mgr = _stream(model, gpu, max_gpu_mem_bytes=5 * layer, num_blocks=2)
+    with torch.no_grad():
+        outs = [model(x.to(gpu)) for _ in range(4)]
+    plan = mgr.plan
+    assert plan.resident and plan.streamed and plan.reordered
+    assert plan.planned_gpu_bytes <= 5 * layer
+    for out in outs:
+        assert torch.equal(out, want)
+    mgr.release()
+
+
+def test_offload_timing_reports_hidden_fraction(gpu):
+    model = _small_mlp(6, 512, 1408, seed=4)
+    x = W.mlp_input(64, 512, seed=4).to(gpu)
+    mgr = _stream(model, gpu, offload_timing="eager")
+    with torch.no_grad():
+        for _ in range(6):
+            model(x)
+    rep = mgr.collect_offload_timing()
+    assert rep is not None and rep.num_passes >= 3
+    assert rep.total_transfer_sum > 0 and 0.0 <= rep.hidden_fraction <= 1.0
+    mgr.release()
+
+
+def test_llama_small_generate_matches_resident(gpu):
+    shape = W.LlamaShape(n_layers=4, hidden=256, n_heads=4, n_kv_heads=4, head_dim=64, inter=688, vocab=1000,
+                         max_seq=128)
+    model = W.build_llama(shape, seed=2)
+    prompt = W.prompt_tokens(1, 24, shape.vocab, seed=2).to(gpu)
+    ref = _resident(model, gpu)
+    ref.init_cache(1, 64, gpu)
+    want_tokens, want_logits = W.generate(ref, prompt, 8)
+    mgr = _stream(model, gpu, discovery_iters=1, profiling_iters=1)
+    model.init_cache(1, 64, gpu)
+    got_tokens, got_logits = W.generate(model, prompt, 8)  # discovery + profiling happen inside
+    model.init_cache(1, 64, gpu)
+    got2_tokens, got2_logits = W.generate(model, prompt, 8)  # fully streamed
+    assert mgr.phase == OffloadPhase.INFERENCE
+    for a, b in zip(got2_logits, want_logits):
+        assert torch.equal(a, b)
+    assert torch.equal(got_tokens, want_tokens) and torch.equal(got2_tokens, want_tokens)
+    mgr.release()
+
+
+@pytest.mark.parametrize("chunk_mib", [1, 4])
+def test_chunked_upload_bit_exact(gpu, chunk_mib):
+    from flextensor_amd.hip import checksum
+    from flextensor_amd.scatter import upload_tensors
+    from oracle import native as onat
+
+    sizes = W.scatter_sizes(300, 4096, 3 << 20, seed=1)
+    gen = torch.Generator().manual_seed(1)
+    tensors = []
+    for i, n in enumerate(sizes):
+        t = torch.randint(-32768, 32767, (n // 2,), generator=gen, dtype=torch.int16).view(torch.bfloat16)
+        tensors.append(t.view(W.scatter_shape(n, i)))
+    tensors.append(torch.arange(12, dtype=torch.float32).reshape(3, 4).t())  # Fortran layout
+    tensors.append(torch.arange(20, dtype=torch.float32).reshape(4, 5)[:, ::2])  # gaps -> C-contiguous
+    out = upload_tensors(tensors, gpu, chunk_bytes=chunk_mib << 20)
+    for src, dst in zip(tensors, out):
+        assert dst.shape == src.shape and dst.dtype == src.dtype
+        # compare bit patterns: random bf16 words include NaNs
+        same_width = torch.int16 if src.element_size() == 2 else torch.int32
+        assert torch.equal(dst.cpu().view(same_width), src.view(same_width))
+    for src, dst in zip(tensors[:-2], out[:-2]):
+        assert dst.stride() == src.stride()
+        assert checksum(dst.view(-1).view(torch.uint8)) == onat.checksum64(src.contiguous().view(-1).view(torch.uint8))
+    assert out[-2].stride() == (1, 4)
+    assert out[-1].is_contiguous()

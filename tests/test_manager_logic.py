@@ -1,0 +1,83 @@
+"""CPU tests of the offload manager's host logic: unit selection, config, planning."""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+from torch import nn
+
+from flextensor_amd.config import OffloadConfig, load_config_from_env
+from flextensor_amd.manager import _Unit, plan_streaming, select_offload_units
+from flextensor_amd.planner import LayerStatistics, check_overlap_constraint, check_transfer_constraint
+from flextensor_amd.workloads import LlamaModel, LlamaShape, MLPStack
+
+
+def test_select_units_llama():
+    m = LlamaModel(LlamaShape(n_layers=3, hidden=16, n_heads=2, n_kv_heads=2, head_dim=8, inter=32, vocab=50,
+                              max_seq=8))
+    assert select_offload_units(m, ["layers.*"], []) == ["layers.0", "layers.1", "layers.2"]
+    assert select_offload_units(m, ["*"], []) == ["embed", "layers.0", "layers.1", "layers.2", "norm", "lm_head"]
+    assert select_offload_units(m, ["layers.*"], ["layers.1"]) == ["layers.0", "layers.2"]
+    assert select_offload_units(m, ["class:DecoderLayer"], []) == ["layers.0", "layers.1", "layers.2"]
+    assert select_offload_units(m, ["layers.**"], []) == ["layers.0", "layers.1", "layers.2"]
+    assert select_offload_units(m, ["layers.*.attn"], []) == ["layers.0.attn", "layers.1.attn", "layers.2.attn"]
+
+
+def test_config_defaults_and_env(monkeypatch):
+    c = OffloadConfig()
+    assert (c.num_blocks, c.min_blocks, c.pinned_memory_mode, c.transfer_mode) == (
+        4, 4, "torch", "allocation_block_transfer")
+    assert c.include_patterns == ["*"] and c.profiling_iters == 10 and c.discovery_iters == 1
+    with pytest.raises(ValueError):
+        OffloadConfig(num_blocks=1)
+    with pytest.raises(ValueError):
+        OffloadConfig(transfer_mode="nope")
+    monkeypatch.setenv("FT_NUM_BLOCKS", "6")
+    monkeypatch.setenv("FT_INCLUDE_PATTERNS", '["layers.*"]')
+    c = load_config_from_env()
+    assert c.num_blocks == 6 and c.include_patterns == ["layers.*"]
+
+
+def _mk(sizes):
+    return [_Unit(f"l{i}", nn.Identity(), [nn.Parameter(torch.empty(n // 2, dtype=torch.bfloat16))])
+            for i, n in enumerate(sizes)]
+
+
+@pytest.mark.parametrize("n", [2, 3, 5, 8])
+@pytest.mark.parametrize("blocks", [2, 3, 4])
+def test_plan_all_streamed_is_hazard_free(n, blocks):
+    units = _mk([1000] * n)
+    order = [u.label for u in units]
+    plan = plan_streaming(units, order, None, 0, blocks)
+    assert plan.streamed == order and not plan.resident
+    bd = plan.block_data
+    stats = [LayerStatistics(x) for x in order]
+    assert check_overlap_constraint(bd.transfer_to_compute_map, stats, bd.label_to_block_id)
+    assert check_transfer_constraint(bd.transfer_to_compute_map, bd.label_to_block_id, stats)
+    assert sorted(bd.transfer_to_compute_map.values()) == sorted(order)  # every unit fed once
+
+
+def test_plan_fits_budget_and_spreads_streamed_units():
+    units = _mk([1000] * 10)
+    order = [u.label for u in units]
+    plan = plan_streaming(units, order, budget=7000, base_bytes=500, num_blocks=2)
+    assert plan.planned_gpu_bytes <= 7000
+    assert plan.resident and plan.streamed and plan.reordered
+    k = len(plan.streamed)
+    assert 500 + (10 - k) * 1000 + sum(plan.block_data.block_sizes.values()) <= 7000
+    # no fewer streamed units would fit
+    assert 500 + (10 - (k - 1)) * 1000 + 2 * 1000 > 7000
+
+
+def test_plan_everything_resident_when_it_fits():
+    units = _mk([100] * 4)
+    plan = plan_streaming(units, [u.label for u in units], budget=10_000, base_bytes=0, num_blocks=2)
+    assert plan.block_data is None and plan.streamed == []
+
+
+def test_plan_rejects_impossible_budget():
+    units = _mk([1000] * 4)
+    with pytest.raises(ValueError, match="budget"):
+        plan_streaming(units, [u.label for u in units], budget=1500, base_bytes=0, num_blocks=2)

@@ -1,0 +1,332 @@
+"""Transfer runtime and pipelined loaders on recording fake streams (no GPU).
+
+The runtime tests restate the reference's runtime contract
+(tests/unit/core/test_transfer.py); the loader tests pin the frozen trace
+(tests/unit/test_loader_synchronization.py:288-363) and compare full
+operation traces with the oracle across gap patterns, cyclic preloads,
+several passes and abort recovery.
+"""
+
+from __future__ import annotations
+
+import json
+import logging
+import random
+from pathlib import Path
+
+import pytest
+
+from flextensor_amd.loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
+from flextensor_amd.planner import LayerStatistics, TensorStatistics
+from flextensor_amd.timing import OffloadTimingCollector
+from flextensor_amd.transfer import HipTransferRuntime, TransferStreamSynchronizationError
+from oracle import schedule as osch
+from tests.fakes import FakeBackend, FakeController, Recorder
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "reference_cases.json").read_text())
+LOADERS = {"default": PreallocatedBatchTransferTensorLoader, "reordered": PreallocatedBatchTransferTensorLoaderReordered}
+
+
+@pytest.fixture
+def rt():
+    rec = Recorder()
+    backend = FakeBackend(rec)
+    return HipTransferRuntime(None, backend=backend), rec, backend
+
+
+# ---- runtime ---------------------------------------------------------------
+
+
+def test_same_slot_reuse_waits_for_last_use(rt):
+    runtime, rec, backend = rt
+    runtime.begin()
+    first = runtime.submit("slot-0", lambda: rec.log.append(_e("copy", "first")))
+    runtime.wait_ready(first)
+    runtime.finish_use("slot-0")
+    last_use = next(e.target for e in reversed(rec.log) if (e.op, e.stream) == ("record_event", "compute"))
+    runtime.submit("slot-0", lambda: rec.log.append(_e("copy", "second")))
+    wait = next(i for i, e in enumerate(rec.log) if (e.op, e.stream, e.target) == ("wait_event", "transfer", last_use))
+    copy = next(i for i, e in enumerate(rec.log) if e.target == "second")
+    assert wait < copy
+
+
+def _e(op, target):
+    from tests.fakes import Entry
+
+    return Entry(op, "transfer", target)
+
+
+def test_no_cross_slot_wait(rt):
+    runtime, rec, _ = rt
+    runtime.begin()
+    runtime.submit("slot-0", lambda: None)
+    runtime.submit("slot-1", lambda: None)
+    assert len(rec.find("wait_event", stream="transfer")) == 1  # only the fork
+
+
+def test_transfer_runs_on_transfer_stream(rt):
+    runtime, rec, backend = rt
+    seen = []
+    runtime.begin()
+    runtime.submit(0, lambda: seen.append(backend.current_stream().name))
+    assert seen == ["transfer"] and backend.current_stream().name == "compute"
+
+
+def test_ticket_repr(rt):
+    runtime, _, _ = rt
+    runtime.begin()
+    t = runtime.submit("slot", lambda: None, trace_label="schedule=embed consume=L0")
+    assert repr(t) == "TransferTicket(slot='slot', trace_label='schedule=embed consume=L0')"
+
+
+def test_busy_slot_rejected(rt):
+    runtime, _, _ = rt
+    runtime.begin()
+    active = runtime.submit("slot", lambda: None, trace_label="x")
+    with pytest.raises(RuntimeError, match="still in use") as caught:
+        runtime.submit("slot", lambda: None)
+    assert repr(active) in str(caught.value)
+
+
+def test_foreign_and_stale_tickets(rt):
+    runtime, rec, backend = rt
+    other = HipTransferRuntime(None, backend=backend)
+    runtime.begin()
+    other.begin()
+    t = runtime.submit("slot", lambda: None)
+    with pytest.raises(ValueError, match="different"):
+        other.wait_ready(t)
+    runtime.wait_ready(t)
+    runtime.finish_use("slot")
+    cur = runtime.submit("slot", lambda: None)
+    runtime.wait_ready(cur)
+    with pytest.raises(ValueError, match="stale") as caught:
+        runtime.wait_ready(t)
+    assert repr(t) in str(caught.value)
+    runtime.join()
+    with pytest.raises(ValueError, match="stale"):
+        runtime.wait_ready(cur)
+
+
+def test_lifecycle_errors(rt):
+    runtime, rec, _ = rt
+    with pytest.raises(RuntimeError, match="begin"):
+        runtime.submit(0, lambda: None)
+    with pytest.raises(RuntimeError, match="begin"):
+        runtime.finish_use(0)
+    assert not runtime.is_active
+    runtime.begin()
+    assert runtime.is_active
+    with pytest.raises(RuntimeError, match="already active"):
+        runtime.begin()
+    runtime.join()
+    assert not runtime.is_active
+    runtime.close()
+    runtime.close()
+    assert [(e.op, e.stream) for e in rec.log].count(("synchronize", "transfer")) == 1
+    with pytest.raises(RuntimeError, match="closed"):
+        runtime.begin()
+
+
+def test_callback_error_propagates(rt):
+    runtime, _, _ = rt
+    runtime.begin()
+
+    def fail():
+        raise LookupError("copy failed")
+
+    with pytest.raises(LookupError, match="copy failed"):
+        runtime.submit("slot", fail)
+
+
+@pytest.mark.parametrize("which", ["record_event", "wait_event"])
+def test_join_wraps_stream_errors(rt, which):
+    runtime, _, backend = rt
+    runtime.begin()
+    (backend.transfer if which == "record_event" else backend.compute).fail_on.add(which)
+    with pytest.raises(TransferStreamSynchronizationError, match=which) as caught:
+        runtime.join()
+    assert isinstance(caught.value.__cause__, RuntimeError)
+
+
+def test_close_wraps_sync_error(rt):
+    runtime, _, backend = rt
+    backend.transfer.fail_on.add("synchronize")
+    with pytest.raises(TransferStreamSynchronizationError, match="synchronize failed"):
+        runtime.close()
+
+
+# ---- loaders -----------------------------------------------------------------
+
+
+def _stats(labels, gaps=()):
+    t = TensorStatistics(tensor_id=1, name="t", size_bytes=1024, load_time_ms=0.1)
+    return [LayerStatistics(x, [] if x in gaps else [t], 1.0) for x in labels]
+
+
+def _make(kind, labels, t2c, l2b, slow=False, gaps=(), collector=None):
+    rec = Recorder()
+    backend = FakeBackend(rec, slow_transfer=slow)
+    ctrl = FakeController(rec, backend)
+    loader = LOADERS[kind](_stats(labels, gaps), None, l2b, t2c, ctrl, collector, None, backend=backend)
+    rec.log.clear()
+    rec.counter = 0
+    return loader, rec, ctrl
+
+
+def _run(loader, rec, labels, passes=1):
+    for _ in range(passes):
+        for x in labels:
+            loader.enter(x)
+            rec.forward(x)
+            loader.exit(x)
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_frozen_trace(kind):
+    c = GOLD["frozen_trace"]
+    loader, rec, ctrl = _make(kind, c["labels"], c["transfer_to_compute_map"], c["label_to_block_id"])
+    _run(loader, rec, c["labels"])
+    assert [list(x) for x in rec.ops()] == c["expected"][kind]
+    assert set(ctrl.streams_seen) == {"transfer"}
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_ticket_trace_label(kind):
+    c = GOLD["ticket_trace_label"]
+    loader, rec, _ = _make(kind, c["labels"], c["transfer_to_compute_map"], c["label_to_block_id"])
+    loader.enter("embed")
+    scheduled = next(iter(loader.scheduled_transfers.values()))
+    ticket = scheduled[0] if isinstance(scheduled, list) else scheduled
+    assert ticket.trace_label == c["expected"]
+
+
+def _pipeline(labels, gaps, blocks, cyclic):
+    off = [x for x in labels if x not in gaps]
+    t2c = {off[i]: off[i + 1] for i in range(len(off) - 1)}
+    if cyclic and len(off) > 2:
+        t2c[off[-1]] = off[0]
+    l2b = {t: i % blocks for i, t in enumerate(t2c)}
+    return t2c, l2b
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+@pytest.mark.parametrize("seed", range(30))
+def test_traces_match_oracle(kind, seed):
+    rng = random.Random(seed)
+    n = rng.randrange(2, 11)
+    labels = ["embed"] + [f"L{i}" for i in range(n - 1)]
+    gaps = set(rng.sample(labels[1:], rng.randrange(0, max(1, n // 3))))
+    blocks = rng.choice([2, 3])
+    cyclic = kind == "reordered" and rng.random() < 0.5
+    t2c, l2b = _pipeline(labels, gaps, blocks, cyclic)
+    passes = rng.choice([1, 2, 3])
+    loader, rec, _ = _make(kind, labels, t2c, l2b, gaps=gaps)
+    _run(loader, rec, labels, passes)
+    want = osch.trace(kind, labels, t2c, l2b, osch.passes(labels, passes))
+    assert rec.triples() == want
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_abort_recovery_joins_then_clears(kind, caplog):
+    labels = ["embed", "L0", "L1"]
+    t2c, l2b = {"embed": "L0", "L0": "L1"}, {"embed": 0, "L0": 1}
+    loader, rec, _ = _make(kind, labels, t2c, l2b)
+    loader.enter("embed")
+    stale = next(iter(loader.scheduled_transfers.values()))
+    rec.log.clear()
+    with caplog.at_level(logging.DEBUG, logger="flextensor_amd.loaders"):
+        loader.enter("embed")  # previous pass never exited
+    assert stale not in loader.scheduled_transfers.values()
+    assert any("abort recovery" in r.getMessage() for r in caplog.records)
+    assert rec.find("record_event", stream="transfer") and rec.find("wait_event", stream="compute")
+    calls = [("enter", "embed"), ("enter", "embed")]
+    assert osch.trace(kind, labels, t2c, l2b, calls)[-len(rec.log):] == rec.triples()
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_slow_transfer_stalls_before_read(kind):
+    labels = ["embed", "L0", "L1", "L2"]
+    c = GOLD["frozen_trace"]
+    loader, rec, _ = _make(kind, labels, c["transfer_to_compute_map"], c["label_to_block_id"], slow=True)
+    _run(loader, rec, labels)
+    for x in ("L0", "L1", "L2"):
+        fwd = rec.find("forward", target=x)[0]
+        assert any(e.op == "wait_event" and e.stream == "compute" and e.stalled for e in rec.log[:fwd]), rec.dump()
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_maps_cleared_after_last_layer(kind):
+    labels = ["embed", "L0", "L1"]
+    loader, rec, _ = _make(kind, labels, {"embed": "L0", "L0": "L1"}, {"embed": 0, "L0": 1})
+    _run(loader, rec, labels)
+    assert loader._transfer_runtime._last_use_by_slot == {} and loader.scheduled_transfers == {}
+    assert not loader._transfer_runtime.is_active
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_piece_join_allows_second_fork(kind):
+    labels = ["embed", "L0", "L1"]
+    loader, rec, _ = _make(kind, labels, {"embed": "L0", "L0": "L1"}, {"embed": 0, "L0": 1})
+    loader.enter("embed")
+    loader.exit("embed")
+    loader.join_after_forward()
+
+    def forks():
+        return sum(1 for a, b in zip(rec.log, rec.log[1:])
+                   if (a.op, a.stream, b.op, b.stream) == ("record_event", "compute", "wait_event", "transfer"))
+
+    assert forks() == 1
+    loader.enter("L0")
+    assert forks() == 2
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_sync_prev_onload(kind):
+    labels = ["embed", "L0"]
+    loader, rec, _ = _make(kind, labels, {"embed": "L0"}, {"embed": 0})
+    loader.sync_prev_onload()
+    assert [(e.op, e.stream) for e in rec.log] == [("wait_stream", "compute")]
+
+
+def test_reordered_preload_adds_no_compute_wait():
+    labels = ["embed", "L0", "L1"]
+    loader, rec, _ = _make("reordered", labels, {"embed": "L0", "L0": "L1", "L1": "embed"},
+                           {"embed": 0, "L0": 1, "L1": 2})
+    loader.sync_prev_onload()
+    rec.log.clear()
+    loader.enter("embed")
+    assert rec.find("wait_event", stream="compute") == []
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_one_compute_label_releases_every_consumed_slot(kind):
+    labels = ["A", "B", "C", "tail"]
+    loader, rec, _ = _make(kind, labels, {"A": "C", "B": "C"}, {"A": 0, "B": 1})
+    for x in ("A", "B", "C"):
+        loader.enter(x)
+        loader.exit(x)
+    loader._transfer_runtime.submit(0, lambda: None)
+    loader._transfer_runtime.submit(1, lambda: None)
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_timing_hooks_pair_up(kind):
+    calls = []
+
+    class Spy(OffloadTimingCollector):
+        def __init__(self):
+            super().__init__(enabled=False)
+
+    spy = Spy()
+    for name in ("on_pass_start", "record_transfer_start", "record_transfer_end", "record_compute_start",
+                 "record_compute_end", "record_wait_start", "record_wait_end"):
+        setattr(spy, name, (lambda n: lambda *a, **k: calls.append(n))(name))
+    labels = ["embed", "L0", "L1"]
+    loader, rec, _ = _make(kind, labels, {"embed": "L0", "L0": "L1"}, {"embed": 0, "L0": 1}, collector=spy)
+    _run(loader, rec, labels)
+    assert calls[0] == "on_pass_start"
+    for col in ("transfer", "compute", "wait"):
+        starts = [i for i, c in enumerate(calls) if c == f"record_{col}_start"]
+        ends = [i for i, c in enumerate(calls) if c == f"record_{col}_end"]
+        assert len(starts) == len(ends) > 0 and all(s < e for s, e in zip(starts, ends))
