@@ -44,7 +44,8 @@ def measure_link_peak(repeats: int = 20) -> dict:
     return out
 
 
-def bench_scatter(steps: int, warmup: int, chunk_mib: int, n_tensors: int, copy_engine: str) -> dict:
+def bench_scatter(steps: int, warmup: int, chunk_mib: int, n_tensors: int, copy_engine: str,
+                  verify: bool = True) -> dict:
     import torch
 
     from flextensor_amd import _native as nat
@@ -78,7 +79,7 @@ def bench_scatter(steps: int, warmup: int, chunk_mib: int, n_tensors: int, copy_
     scat_payload = [sum(p.nbytes for p in ch.pieces) for ch in chunks] * steps
     # verification through torch's own copy path, independent of the engine under test
     bad = 0
-    for ch in chunks:
+    for ch in chunks if verify else []:
         ref = ch.host.to(dev)
         for p in ch.pieces:
             if p.nbytes:
@@ -198,6 +199,10 @@ def main() -> int:
     ap.add_argument("--budget-gb", type=float, default=8.0)
     ap.add_argument("--decode", type=int, default=128)
     ap.add_argument("--prefill", type=int, default=512)
+    ap.add_argument("--skip-peak", action="store_true", help="do not measure the 512 MiB link peak")
+    ap.add_argument("--skip-verify", action="store_true", help="skip the independent byte check")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="run one device-to-device copy of this size first (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build streams weights into a single MI355X "
@@ -213,16 +218,24 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     nat.load()
-    peak = measure_link_peak()
+    if args.calibration_copy_mib:
+        src = torch.ones(args.calibration_copy_mib * MiB, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        _log(f"calibration copy: {args.calibration_copy_mib} MiB device to device")
+        del src, dst
+    peak = {"sdma": float("nan"), "kernel": float("nan")} if args.skip_peak else measure_link_peak()
     _log(f"measured H2D peak (512 MiB, best of 20): sdma {peak['sdma']:.2f} GB/s, kernel {peak['kernel']:.2f} GB/s")
-    res = bench_scatter(args.steps, args.warmup, args.chunk_mib, args.tensors, args.copy_engine)
+    res = bench_scatter(args.steps, args.warmup, args.chunk_mib, args.tensors, args.copy_engine,
+                        verify=not args.skip_verify)
     _log(f"scatter workload: {res['effective_GBps']:.2f} GB/s effective, link {res['link_GBps']:.2f} GB/s, "
          f"scatter kernel {res['scatter_hbm_GBps']:.0f} GB/s HBM, mismatches {res['mismatched_tensors']}")
     if res["mismatched_tensors"]:
         print(f"bench: {res['mismatched_tensors']} destination tensors differ from the streamed bytes", file=sys.stderr)
         return 1
     cpu = None if args.skip_cpu_baseline else cpu_baseline_scatter(res["chunks"])
-    measured_peak = max(peak["sdma"], peak["kernel"])
+    measured_peak = max(peak["sdma"], peak["kernel"]) if not args.skip_peak else float("nan")
     line = {
         "metric": "effective streamed-weight GB/s (% of link peak); tok/s at 7B shape, 8 GB budget",
         "value": round(res["effective_GBps"], 3),

@@ -30,9 +30,13 @@ extern "C" {
 #define FTX_ERR_UNSUPPORTED 4 /* request not possible for this memory/device */
 
 /* ---- copy engines ------------------------------------------------------ */
-#define FTX_COPY_SDMA 0   /* hipMemcpyAsync (SDMA engines), optionally split over copy streams */
-#define FTX_COPY_KERNEL 1 /* zero-copy kernel: CUs read mapped pinned host memory             */
-#define FTX_COPY_AUTO 2   /* pick per chunk from the policy set by ftx_set_copy_policy         */
+/* FTX_COPY_SDMA is hipMemcpyAsync: the HIP runtime picks its engine (an SDMA
+ * queue or its own blit kernel; the ROCm 7 runtime used with PyTorch runs
+ * pinned host-to-device copies as a blit kernel). Copies may be split over
+ * dedicated copy streams. FTX_COPY_KERNEL is this library's zero-copy kernel. */
+#define FTX_COPY_SDMA 0   /* hipMemcpyAsync, optionally split over copy streams   */
+#define FTX_COPY_KERNEL 1 /* zero-copy kernel: CUs read mapped pinned host memory */
+#define FTX_COPY_AUTO 2   /* pick per chunk from the policy set by ftx_set_copy_policy */
 
 /* ---- host arena flags -------------------------------------------------- */
 #define FTX_ARENA_DEFAULT 0u
