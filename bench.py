@@ -186,6 +186,161 @@ def bench_llama7b(budget_gb: float, prefill: int, decode: int, copy_engine: str)
     return out
 
 
+def cpu_llama_decode_baseline(layers: int = 2, tokens: int = 4, context: int = 512) -> dict:
+    """Batch-1 decode of ``layers`` 7B-shape decoder layers in PyTorch on the host cores, scaled to 32 layers."""
+    import torch
+
+    from flextensor_amd import workloads as W
+
+    s = W.LlamaShape(n_layers=layers, vocab=256)
+    model = W.build_llama(s, seed=0)
+    model.init_cache(1, context + tokens + 2, torch.device("cpu"))
+    x = torch.randn(1, 1, s.hidden, dtype=torch.bfloat16)
+    with torch.no_grad():
+        for i in range(2):
+            for layer_i, layer in enumerate(model.layers):
+                layer(x, context + i, model.rope_cos, model.rope_sin, model.cache_k[layer_i], model.cache_v[layer_i])
+        t0 = time.perf_counter()
+        for i in range(tokens):
+            for layer_i, layer in enumerate(model.layers):
+                layer(x, context + 2 + i, model.rope_cos, model.rope_sin, model.cache_k[layer_i],
+                      model.cache_v[layer_i])
+        per_layer = (time.perf_counter() - t0) / (tokens * layers)
+    per_token = per_layer * W.LLAMA_7B.n_layers
+    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "pytorch_cpu_forward",
+            "sample": f"PyTorch bf16 decode of {layers} 7B-shape layers x {tokens} tokens at context {context}, "
+                      "scaled linearly to 32 layers"}
+
+
+def bench_dit(budget_gb: float, tokens: int, text: int, steps: int) -> dict:
+    import gc
+
+    import torch
+
+    from flextensor_amd import workloads as W
+    from flextensor_amd.config import OffloadConfig
+    from flextensor_amd.manager import OffloadManager
+
+    dev = torch.device("cuda", 0)
+    S = W.WAN_DIT
+    model = W.build_dit(S, seed=0, init_device="cuda")
+    x, e, ctx = W.dit_inputs(S, tokens, text, seed=0, device="cuda")
+    blk = model.blocks[0].to(dev)  # resident reference time of one block
+    with torch.no_grad():
+        times = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            blk(x, e, ctx)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+    blk.to("cpu")
+    gc.collect()
+    torch.cuda.empty_cache()
+    resident_block_s = min(times[1:])
+    mgr = OffloadManager("bench-dit")
+    mgr.offload(model, OffloadConfig(include_patterns=["blocks.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                                     profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9),
+                                     offload_timing="eager"))
+    with torch.no_grad():
+        xs = x[:, :2048].contiguous()
+        model(xs, e, ctx)
+        model(xs, e, ctx)
+        model(x, e, ctx)  # warm-up step
+        mgr.reset_offload_timing()
+        step_times = []
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            model(x, e, ctx)
+            torch.cuda.synchronize()
+            step_times.append(time.perf_counter() - t0)
+    rep = mgr.collect_offload_timing()
+    plan = mgr.plan
+    streamed = sum(mgr._unit(b).nbytes for b in plan.streamed)
+    step = sum(step_times) / len(step_times)
+    out = {
+        "tokens": tokens, "text_tokens": text, "blocks": S.n_blocks,
+        "streamed_blocks": len(plan.streamed), "resident_blocks": len(plan.resident),
+        "step_s": step, "resident_estimate_step_s": resident_block_s * S.n_blocks,
+        "overhead_vs_resident": step / (resident_block_s * S.n_blocks) - 1.0,
+        "hidden_fraction": rep.hidden_fraction,
+        "transfer_ms_per_step": rep.total_transfer_sum / rep.num_passes,
+        "wait_ms_per_step": rep.total_wait_sum / rep.num_passes,
+        "link_GBps_during_transfer": streamed / (rep.total_transfer_sum / rep.num_passes * 1e-3) / 1e9,
+        "streamed_bytes_per_step": streamed,
+        "tflops_per_step": S.block_flops(tokens, text) * S.n_blocks / 1e12,
+        "achieved_tflops": S.block_flops(tokens, text) * S.n_blocks / step / 1e12,
+        "gpu_weight_bytes": mgr.get_gpu_memory_usage().total_bytes, "budget_bytes": int(budget_gb * 1e9),
+    }
+    mgr.release(preserve_model=False)
+    return out
+
+
+def measure_traffic(args) -> dict | None:
+    """HBM bytes per scatter launch from two ``rocprofv3 --pmc`` child runs.
+
+    Each child runs this script in ``--traffic-probe`` mode: one 1 GiB
+    device-to-device copy (the runtime's copy kernel, whose traffic is known:
+    1 GiB read, 1 GiB written), then one step of the scatter workload. The
+    counter reading of the calibration copy gives the scale of each counter;
+    traffic = scaled FETCH_SIZE + scaled WRITE_SIZE, averaged over the scatter
+    launches. Returns None when rocprofv3 is not available or a pass fails.
+    """
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    calib = 1024 * MiB
+    out: dict = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix=f"ftx_pmc_{ctr.lower()}_", dir="/tmp")
+        cmd = [exe, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
+               os.path.abspath(__file__), "--traffic-probe", "--chunk-mib", str(args.chunk_mib),
+               "--tensors", str(args.tensors), "--copy-engine", args.copy_engine]
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), capture_output=True, text=True,
+                               timeout=300)
+        except subprocess.TimeoutExpired:
+            _log(f"traffic: rocprofv3 {ctr} pass timed out")
+            return None
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if r.returncode != 0 or not files:
+            _log(f"traffic: rocprofv3 {ctr} pass failed (rc {r.returncode}): {r.stderr[-400:]}")
+            return None
+        with open(files[0]) as fh:
+            rows = sorted(csv.DictReader(fh), key=lambda row: int(row["Dispatch_Id"]))
+        copies = [row for row in rows if row["Kernel_Name"] == "__amd_rocclr_copyBuffer"]
+        scat = [row for row in rows if "scatter_kernel" in row["Kernel_Name"]]
+        if not copies or not scat:
+            return None
+        scale = calib / (float(copies[0]["Counter_Value"]) * 1024)
+        out[ctr] = {"scale": round(scale, 4),
+                    "bytes_per_launch": sum(float(row["Counter_Value"]) for row in scat) * 1024 * scale / len(scat)}
+        shutil.rmtree(d, ignore_errors=True)
+    return {"traffic": out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"],
+            "fetch_bytes_per_launch": out["FETCH_SIZE"]["bytes_per_launch"],
+            "write_bytes_per_launch": out["WRITE_SIZE"]["bytes_per_launch"],
+            "fetch_scale": out["FETCH_SIZE"]["scale"], "write_scale": out["WRITE_SIZE"]["scale"]}
+
+
+def traffic_probe(args) -> int:
+    import torch
+
+    src = torch.ones(1024 * MiB, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    bench_scatter(1, 0, args.chunk_mib, args.tensors, args.copy_engine, verify=False)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -203,6 +358,11 @@ def main() -> int:
     ap.add_argument("--skip-verify", action="store_true", help="skip the independent byte check")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (HBM counter calibration)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--skip-dit", action="store_true")
+    ap.add_argument("--dit-tokens", type=int, default=32760)
+    ap.add_argument("--dit-steps", type=int, default=2)
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build streams weights into a single MI355X "
@@ -218,6 +378,8 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     nat.load()
+    if args.traffic_probe:
+        return traffic_probe(args)
     if args.calibration_copy_mib:
         src = torch.ones(args.calibration_copy_mib * MiB, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -264,13 +426,31 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     del res
-    if not args.skip_llama:
-        import gc
+    import gc
 
+    gc.collect()
+    torch.cuda.empty_cache()
+    if not args.no_traffic:
+        tr = measure_traffic(args)
+        if tr is not None:
+            line["roofline"]["traffic"] = int(tr["traffic"])
+            line["roofline"]["traffic_detail"] = {k: (int(v) if "bytes" in k else v) for k, v in tr.items()
+                                                  if k != "traffic"}
+            _log(f"traffic per scatter launch: {tr['traffic'] / 1e9:.3f} GB "
+                 f"(algorithmic {line['roofline']['algorithmic_bytes_per_launch'] / 1e9:.3f} GB)")
+    if not args.skip_llama:
         gc.collect()
         torch.cuda.empty_cache()
         line["llama7b"] = bench_llama7b(args.budget_gb, args.prefill, args.decode, args.copy_engine)
         _log(f"llama7b: {line['llama7b']}")
+        if not args.skip_cpu_baseline:
+            line["llama7b"]["cpu_baseline"] = cpu_llama_decode_baseline()
+            _log(f"llama7b cpu baseline: {line['llama7b']['cpu_baseline']}")
+    if not args.skip_dit:
+        gc.collect()
+        torch.cuda.empty_cache()
+        line["dit"] = bench_dit(12.0, args.dit_tokens, 512, args.dit_steps)
+        _log(f"dit: {line['dit']}")
     print(json.dumps(line), flush=True)
     return 0
 

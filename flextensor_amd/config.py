@@ -8,8 +8,9 @@ Kept from config.py:55-402: ``enabled``, ``gpu_device``, ``pinned_memory``,
 override fields (config.py:1012).
 
 Added for this build: ``max_gpu_mem_bytes`` (a budget in bytes instead of a
-fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel``) and
-``loader_order`` (``auto`` / ``default`` / ``reordered``).
+fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel``),
+``loader_order`` (``auto`` / ``default`` / ``reordered``) and
+``max_inflight_passes`` (bounded host run-ahead).
 """
 
 from __future__ import annotations
@@ -44,6 +45,11 @@ class OffloadConfig(BaseModel):
     profile_storage_dir: str | None = None
     copy_engine: Literal["auto", "sdma", "kernel"] = "auto"
     loader_order: Literal["auto", "default", "reordered"] = "auto"
+    # Before the host enqueues a streamed forward it waits until the forward
+    # this many passes back has finished on the device (0: never waits). A host
+    # that runs further ahead fills the device command queue and then issues
+    # each next transfer late, which idles the host link.
+    max_inflight_passes: int = Field(default=1, ge=0)
 
     @model_validator(mode="after")
     def _check(self) -> "OffloadConfig":

@@ -20,14 +20,26 @@ import torch
 from . import _native as nat
 
 
+_FREE_EVENTS: dict[bool, list[int]] = {False: [], True: []}
+_MAX_FREE_EVENTS = 4096
+
+
 class HipEvent:
-    """One ``hipEvent_t``; destroyed with the Python object."""
+    """One ``hipEvent_t``.
+
+    Handles are recycled through a free list instead of being destroyed: the
+    streaming loop creates and drops several events per label, and an event
+    dropped by Python may still be pending on a stream. Re-recording a
+    recycled handle is safe because a wait always refers to the record that
+    preceded it.
+    """
 
     __slots__ = ("handle", "timing", "__weakref__")
 
     def __init__(self, timing: bool = False) -> None:
         self.timing = timing
-        self.handle = nat.event_create(nat.EVENT_TIMING if timing else nat.EVENT_DEFAULT)
+        free = _FREE_EVENTS[timing]
+        self.handle = free.pop() if free else nat.event_create(nat.EVENT_TIMING if timing else nat.EVENT_DEFAULT)
 
     def record(self, stream: "HipStream | None" = None) -> "HipEvent":
         s = stream if stream is not None else current_stream()
@@ -46,7 +58,11 @@ class HipEvent:
     def __del__(self) -> None:
         h = getattr(self, "handle", None)
         if h and nat.live():
-            nat.lib().ftx_event_destroy(h)
+            free = _FREE_EVENTS[self.timing]
+            if len(free) < _MAX_FREE_EVENTS:
+                free.append(h)
+            else:
+                nat.lib().ftx_event_destroy(h)
             self.handle = None
 
 

@@ -228,6 +228,7 @@ class OffloadManager:
         self._cpu_data: dict[int, torch.Tensor] = {}
         self._seen_this_pass: list[str] = []
         self._events: dict[str, tuple[Any, Any]] = {}
+        self._pass_done: list[Any] = []  # completion events of the latest streamed passes
         self.build_seconds = 0.0
 
     # -- public ---------------------------------------------------------------
@@ -253,6 +254,7 @@ class OffloadManager:
         self._place_outside_units(unit_params)
         for u in self.units:
             self._patch(u)
+        self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
         self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
         self.phase = OffloadPhase.DISCOVERY if self.config.discovery_iters > 0 else OffloadPhase.PROFILING
         if self.config.discovery_iters == 0 and self.config.profiling_iters == 0:
@@ -308,6 +310,7 @@ class OffloadManager:
             for b in self.model.buffers():
                 b.data = b.data.cpu()
         self.loader = self.controller = self.plan = None
+        self._pass_done = []
         self.model = None
         self.units, self._patched, self._hooks = [], [], []
         self.phase = OffloadPhase.NOT_INITIALIZED
@@ -388,8 +391,19 @@ class OffloadManager:
         for p in u.params:
             p.data = self._cpu_data.pop(id(p))
 
+    def _before_forward(self) -> None:
+        """Bound the host's run-ahead: wait for the pass ``max_inflight_passes`` back."""
+        k = self.config.max_inflight_passes
+        if self.phase == OffloadPhase.INFERENCE and k > 0 and len(self._pass_done) >= k:
+            self._pass_done[-k].synchronize()
+
     def _after_forward(self) -> None:
         if self.phase == OffloadPhase.INFERENCE:
+            if self.config.max_inflight_passes > 0:
+                from .hip import HipEvent, current_stream
+
+                self._pass_done.append(HipEvent().record(current_stream(self.device)))
+                del self._pass_done[: -self.config.max_inflight_passes]
             return
         self._forwards += 1
         if self.phase == OffloadPhase.DISCOVERY:

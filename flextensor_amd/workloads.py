@@ -239,6 +239,127 @@ def prompt_tokens(batch: int, length: int, vocab: int, seed: int = 0) -> torch.T
     return torch.randint(0, vocab, (batch, length), generator=gen)
 
 
+# ---- Wan-style diffusion transformer -------------------------------------------
+
+
+@dataclass(frozen=True)
+class DiTShape:
+    n_blocks: int = 40
+    dim: int = 5120
+    n_heads: int = 40
+    ffn: int = 13824
+    eps: float = 1e-6
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.n_heads
+
+    def block_params(self) -> int:
+        d, f = self.dim, self.ffn
+        attn = 4 * (d * d + d) + 2 * d  # q, k, v, o with bias + q/k RMSNorm weights
+        return 2 * attn + 2 * d + (d * f + f + f * d + d) + 6 * d  # + cross-attn norm, ffn, modulation
+
+    def block_flops(self, tokens: int, text: int) -> float:
+        d, f = self.dim, self.ffn
+        lin = 2 * tokens * d * d * 4 + 2 * tokens * d * d * 2 + 2 * text * d * d * 2 + 2 * tokens * d * f * 2
+        attn = 4 * tokens * tokens * d + 4 * tokens * text * d
+        return float(lin + attn)
+
+
+WAN_DIT = DiTShape()
+
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Attention over [batch, heads, seq, head_dim].
+
+    On the GPU only the fused flash / memory-efficient kernels are allowed (a
+    32760-token score matrix does not belong in HBM, and the unfused path runs
+    batched products on transposed views); without a fused kernel this raises.
+    """
+    if q.device.type == "cuda":
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v)
+    return F.scaled_dot_product_attention(q, k, v)
+
+
+class _DiTAttention(nn.Module):
+    def __init__(self, s: DiTShape, dtype: torch.dtype) -> None:
+        super().__init__()
+        self.s = s
+        self.q = nn.Linear(s.dim, s.dim, dtype=dtype)
+        self.k = nn.Linear(s.dim, s.dim, dtype=dtype)
+        self.v = nn.Linear(s.dim, s.dim, dtype=dtype)
+        self.o = nn.Linear(s.dim, s.dim, dtype=dtype)
+        self.norm_q = RMSNorm(s.dim, s.eps, dtype)
+        self.norm_k = RMSNorm(s.dim, s.eps, dtype)
+
+    def forward(self, x: torch.Tensor, ctx: torch.Tensor, attn=None) -> torch.Tensor:
+        b, n, _ = x.shape
+        h, d = self.s.n_heads, self.s.head_dim
+        q = self.norm_q(self.q(x)).view(b, n, h, d).transpose(1, 2)
+        k = self.norm_k(self.k(ctx)).view(b, ctx.shape[1], h, d).transpose(1, 2)
+        v = self.v(ctx).view(b, ctx.shape[1], h, d).transpose(1, 2)
+        o = (attn or sdpa)(q, k, v)
+        return self.o(o.transpose(1, 2).reshape(b, n, h * d))
+
+
+class DiTBlock(nn.Module):
+    """AdaLN-modulated block: self-attention, cross-attention to text, GELU FFN."""
+
+    def __init__(self, s: DiTShape = WAN_DIT, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.s = s
+        self.self_attn = _DiTAttention(s, dtype)
+        self.cross_attn = _DiTAttention(s, dtype)
+        self.norm3 = nn.LayerNorm(s.dim, eps=s.eps, dtype=dtype)
+        self.fc1 = nn.Linear(s.dim, s.ffn, dtype=dtype)
+        self.fc2 = nn.Linear(s.ffn, s.dim, dtype=dtype)
+        self.modulation = nn.Parameter(torch.zeros(1, 6, s.dim, dtype=dtype))
+
+    def _norm(self, x: torch.Tensor) -> torch.Tensor:
+        return F.layer_norm(x.float(), (self.s.dim,), eps=self.s.eps).to(x.dtype)
+
+    def forward(self, x: torch.Tensor, e: torch.Tensor, ctx: torch.Tensor, attn=None) -> torch.Tensor:
+        m = (self.modulation.float() + e.float()).chunk(6, dim=1)
+        h = (self._norm(x).float() * (1 + m[1]) + m[0]).to(x.dtype)
+        x = (x.float() + self.self_attn(h, h, attn).float() * m[2]).to(x.dtype)
+        x = x + self.cross_attn(self.norm3(x), ctx, attn)
+        h = (self._norm(x).float() * (1 + m[4]) + m[3]).to(x.dtype)
+        y = self.fc2(F.gelu(self.fc1(h), approximate="tanh"))
+        return (x.float() + y.float() * m[5]).to(x.dtype)
+
+
+class DiTModel(nn.Module):
+    def __init__(self, s: DiTShape = WAN_DIT, dtype: torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        self.shape = s
+        self.blocks = nn.ModuleList(DiTBlock(s, dtype) for _ in range(s.n_blocks))
+        self.attn = None  # attention override (callable on [b, h, s, d] tensors)
+
+    def forward(self, x: torch.Tensor, e: torch.Tensor, ctx: torch.Tensor) -> torch.Tensor:
+        for blk in self.blocks:
+            x = blk(x, e, ctx, self.attn)
+        return x
+
+
+def build_dit(shape: DiTShape = WAN_DIT, seed: int = 0, init_device: str = "cpu") -> DiTModel:
+    with torch.device("meta"):
+        model = DiTModel(shape)
+    model = model.to_empty(device="cpu")
+    return init_normal_(model, seed, 0.02, init_device)
+
+
+def dit_inputs(shape: DiTShape, tokens: int, text: int, seed: int = 0, device: str = "cpu"):
+    """Latent tokens, timestep modulation and text context, all ~N(0, 1) in bf16."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(1, tokens, shape.dim, generator=gen, device=device).to(torch.bfloat16)
+    e = torch.randn(1, 6, shape.dim, generator=gen, device=device).to(torch.bfloat16)
+    ctx = torch.randn(1, text, shape.dim, generator=gen, device=device).to(torch.bfloat16)
+    return x, e, ctx
+
+
 # ---- scatter microbenchmark tensor set ------------------------------------------
 
 

@@ -84,3 +84,57 @@ def test_scatter_set_shapes():
         shape = W.scatter_shape(n, i)
         assert math.prod(shape) * 2 == n and len(shape) == (1 if i % 2 == 0 else 2)
     assert 12e9 < sum(sizes) < 15e9
+
+
+def _ref_dit_block(blk: W.DiTBlock, x, e, ctx):
+    """Float32 restatement of one AdaLN DiT block (explicit softmax attention)."""
+    s = blk.s
+    f = {k: v.float() for k, v in blk.state_dict().items()}
+    x, e, ctx = x.float(), e.float(), ctx.float()
+    m = [(f["modulation"] + e)[:, i: i + 1] for i in range(6)]
+
+    def ln(v, w=None, b=None):
+        mu = v.mean(-1, keepdim=True)
+        var = ((v - mu) ** 2).mean(-1, keepdim=True)
+        y = (v - mu) / torch.sqrt(var + s.eps)
+        return y * w + b if w is not None else y
+
+    def rms(v, w):
+        return v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + s.eps) * w
+
+    def attn(p, xq, xkv):
+        q = rms(xq @ f[p + "q.weight"].T + f[p + "q.bias"], f[p + "norm_q.weight"])
+        k = rms(xkv @ f[p + "k.weight"].T + f[p + "k.bias"], f[p + "norm_k.weight"])
+        v = xkv @ f[p + "v.weight"].T + f[p + "v.bias"]
+        hd = s.head_dim
+        q = q.view(1, -1, s.n_heads, hd).transpose(1, 2)
+        k = k.view(1, -1, s.n_heads, hd).transpose(1, 2)
+        v = v.view(1, -1, s.n_heads, hd).transpose(1, 2)
+        a = torch.softmax(q @ k.transpose(-1, -2) / math.sqrt(hd), -1)
+        o = (a @ v).transpose(1, 2).reshape(1, -1, s.dim)
+        return o @ f[p + "o.weight"].T + f[p + "o.bias"]
+
+    h = ln(x) * (1 + m[1]) + m[0]
+    x = x + attn("self_attn.", h, h) * m[2]
+    x = x + attn("cross_attn.", ln(x, f["norm3.weight"], f["norm3.bias"]), ctx)
+    h = ln(x) * (1 + m[4]) + m[3]
+    y = torch.nn.functional.gelu(h @ f["fc1.weight"].T + f["fc1.bias"], approximate="tanh") @ f["fc2.weight"].T
+    return x + (y + f["fc2.bias"]) * m[5]
+
+
+def test_dit_block_matches_float32_restatement():
+    shape = W.DiTShape(n_blocks=2, dim=64, n_heads=4, ffn=160)
+    model = W.build_dit(shape, seed=7)
+    with torch.no_grad():
+        for p in model.parameters():  # norm weights around 1 so the test exercises them
+            if p.dim() == 1 and p.numel() == 64 and p.abs().max() < 0.2:
+                p.add_(1.0)
+    x, e, ctx = W.dit_inputs(shape, 24, 8, seed=7)
+    got = model(x, e, ctx)
+    want = x
+    for blk in model.blocks:
+        want = _ref_dit_block(blk, want, e, ctx)
+    rel = (got.float() - want).norm() / want.norm()
+    assert rel < 2e-2, float(rel)
+    assert sum(p.numel() for p in model.blocks[0].parameters()) == shape.block_params()
+    assert W.WAN_DIT.block_params() * 2 == 702_788_608
