@@ -359,6 +359,8 @@ def main() -> int:
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (HBM counter calibration)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--link-sweep", action="store_true",
+                    help="only print the host-to-device GB/s of each copy engine over chunk sizes 64 KiB-512 MiB")
     ap.add_argument("--skip-dit", action="store_true")
     ap.add_argument("--dit-tokens", type=int, default=32760)
     ap.add_argument("--dit-steps", type=int, default=2)
@@ -380,6 +382,17 @@ def main() -> int:
     nat.load()
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.link_sweep:
+        from flextensor_amd.link_model import choose_copy_policy, measure_copy_curve
+
+        sizes = [64 << 10, 256 << 10, 1 << 20, 2 << 20, 4 << 20, 16 << 20, 64 << 20, 180 << 20, 512 << 20]
+        curves = {e: measure_copy_curve(e, sizes, repeats=10) for e in ("sdma", "kernel", "sdma_split2")}
+        table = {e: {str(n): round(g, 2) for n, g in c.gbps().items()} for e, c in curves.items()}
+        policy = choose_copy_policy(curves["sdma"], curves["kernel"], curves["sdma_split2"], 2)
+        print(json.dumps({"link_sweep_GBps": table, "auto_policy": {"kernel_max_bytes": policy[0],
+                                                                     "split_min_bytes": policy[1],
+                                                                     "n_copy_streams": policy[2]}}), flush=True)
+        return 0
     if args.calibration_copy_mib:
         src = torch.ones(args.calibration_copy_mib * MiB, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)

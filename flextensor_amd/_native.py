@@ -34,6 +34,7 @@ ARENA_DEFAULT = 0
 ARENA_COHERENT = 1
 ARENA_NONCOHERENT = 2
 ARENA_WRITECOMBINED = 4
+ARENA_NUMA_USER = 8
 
 EVENT_DEFAULT = 0
 EVENT_TIMING = 1

@@ -356,6 +356,7 @@ int ftx_arena_alloc(size_t nbytes, unsigned flags, void **host) {
   if (flags & FTX_ARENA_COHERENT) hflags |= hipHostMallocCoherent;
   if (flags & FTX_ARENA_NONCOHERENT) hflags |= hipHostMallocNonCoherent;
   if (flags & FTX_ARENA_WRITECOMBINED) hflags |= hipHostMallocWriteCombined;
+  if (flags & FTX_ARENA_NUMA_USER) hflags |= hipHostMallocNumaUser;
   void *p = nullptr;
   FTX_HIP(hipHostMalloc(&p, nbytes, hflags));
   void *dev = nullptr;

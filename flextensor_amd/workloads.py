@@ -26,14 +26,30 @@ import torch.nn.functional as F
 from torch import nn
 
 
+FP8_E4M3_MAX = 448.0
+
+
 def init_normal_(model: nn.Module, seed: int, std: float = 0.02, init_device: str = "cpu") -> nn.Module:
-    """Overwrite every parameter with N(0, std) draws (float32, then cast)."""
+    """Overwrite every parameter with N(0, std) draws (float32, then cast).
+
+    An ``Fp8Linear`` draws its weight the same way, then stores it as
+    float8_e4m3fn with a per-output-channel scale ``absmax / 448`` (bf16); the
+    quantised weight is ``round_e4m3(w / scale)``.
+    """
     gen = torch.Generator(device=init_device).manual_seed(seed)
     with torch.no_grad():
-        for p in model.parameters():
-            w = torch.empty(p.shape, dtype=torch.float32, device=init_device)
-            w.normal_(0.0, std, generator=gen)
-            p.copy_(w.to(p.dtype))
+        for mod in model.modules():
+            if isinstance(mod, Fp8Linear):
+                w = torch.empty(mod.weight.shape, dtype=torch.float32, device=init_device)
+                w.normal_(0.0, std, generator=gen)
+                scale = (w.abs().amax(dim=1) / FP8_E4M3_MAX).clamp_min(1e-12).to(torch.bfloat16)
+                mod.weight.copy_((w / scale.float()[:, None]).to(torch.float8_e4m3fn))
+                mod.scale.copy_(scale)
+                continue
+            for p in mod.parameters(recurse=False):
+                w = torch.empty(p.shape, dtype=torch.float32, device=init_device)
+                w.normal_(0.0, std, generator=gen)
+                p.copy_(w.to(p.dtype))
     return model
 
 
@@ -86,14 +102,43 @@ class LlamaShape:
     max_seq: int = 2048
     eps: float = 1e-5
     rope_theta: float = 10000.0
+    fp8: bool = False  # projection weights in float8_e4m3fn with per-output-channel bf16 scales
 
     def layer_bytes(self, itemsize: int = 2) -> int:
         h, d = self.hidden, self.head_dim
-        attn = h * self.n_heads * d + 2 * h * self.n_kv_heads * d + self.n_heads * d * h
-        return itemsize * (attn + 3 * h * self.inter + 2 * h)
+        mats = h * self.n_heads * d + 2 * h * self.n_kv_heads * d + self.n_heads * d * h + 3 * h * self.inter
+        if self.fp8:
+            outs = self.n_heads * d + 2 * self.n_kv_heads * d + h + 2 * self.inter + h
+            return mats + 2 * outs + 2 * 2 * h
+        return itemsize * (mats + 2 * h)
 
 
 LLAMA_7B = LlamaShape()
+LLAMA_70B_FP8 = LlamaShape(n_layers=80, hidden=8192, n_heads=64, n_kv_heads=8, head_dim=128, inter=28672,
+                           vocab=32000, max_seq=4096, fp8=True)
+
+
+class Fp8Linear(nn.Module):
+    """y = x @ (W_fp8 * scale[:, None])^T with W in float8_e4m3fn and a bf16 scale per output channel.
+
+    Every e4m3 value is exactly representable in bf16, so dequantising and
+    running a bf16 GEMM computes the same products as the reference's
+    dequantise-then-linear forward.
+    """
+
+    def __init__(self, in_features: int, out_features: int) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, dtype=torch.float8_e4m3fn),
+                                   requires_grad=False)
+        self.scale = nn.Parameter(torch.ones(out_features, dtype=torch.bfloat16), requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        w = self.weight.to(torch.bfloat16)
+        return F.linear(x, w) * self.scale
+
+
+def _proj(s: LlamaShape, n_in: int, n_out: int, dtype: torch.dtype) -> nn.Module:
+    return Fp8Linear(n_in, n_out) if s.fp8 else nn.Linear(n_in, n_out, bias=False, dtype=dtype)
 
 
 class RMSNorm(nn.Module):
@@ -119,10 +164,10 @@ class Attention(nn.Module):
     def __init__(self, s: LlamaShape, dtype: torch.dtype) -> None:
         super().__init__()
         self.s = s
-        self.wq = nn.Linear(s.hidden, s.n_heads * s.head_dim, bias=False, dtype=dtype)
-        self.wk = nn.Linear(s.hidden, s.n_kv_heads * s.head_dim, bias=False, dtype=dtype)
-        self.wv = nn.Linear(s.hidden, s.n_kv_heads * s.head_dim, bias=False, dtype=dtype)
-        self.wo = nn.Linear(s.n_heads * s.head_dim, s.hidden, bias=False, dtype=dtype)
+        self.wq = _proj(s, s.hidden, s.n_heads * s.head_dim, dtype)
+        self.wk = _proj(s, s.hidden, s.n_kv_heads * s.head_dim, dtype)
+        self.wv = _proj(s, s.hidden, s.n_kv_heads * s.head_dim, dtype)
+        self.wo = _proj(s, s.n_heads * s.head_dim, s.hidden, dtype)
 
     def forward(self, x: torch.Tensor, pos: int, cos: torch.Tensor, sin: torch.Tensor,
                 cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
@@ -161,9 +206,9 @@ class DecoderLayer(nn.Module):
         self.attn_norm = RMSNorm(s.hidden, s.eps, dtype)
         self.attn = Attention(s, dtype)
         self.mlp_norm = RMSNorm(s.hidden, s.eps, dtype)
-        self.gate = nn.Linear(s.hidden, s.inter, bias=False, dtype=dtype)
-        self.up = nn.Linear(s.hidden, s.inter, bias=False, dtype=dtype)
-        self.down = nn.Linear(s.inter, s.hidden, bias=False, dtype=dtype)
+        self.gate = _proj(s, s.hidden, s.inter, dtype)
+        self.up = _proj(s, s.hidden, s.inter, dtype)
+        self.down = _proj(s, s.inter, s.hidden, dtype)
 
     def forward(self, x: torch.Tensor, pos: int, cos: torch.Tensor, sin: torch.Tensor,
                 cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:

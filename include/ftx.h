@@ -43,6 +43,7 @@ extern "C" {
 #define FTX_ARENA_COHERENT 1u      /* hipHostMallocCoherent (fine-grained)     */
 #define FTX_ARENA_NONCOHERENT 2u   /* hipHostMallocNonCoherent (coarse-grained) */
 #define FTX_ARENA_WRITECOMBINED 4u /* hipHostMallocWriteCombined              */
+#define FTX_ARENA_NUMA_USER 8u     /* hipHostMallocNumaUser: pages follow the calling thread's NUMA policy */
 
 /* ---- events ------------------------------------------------------------ */
 #define FTX_EVENT_DEFAULT 0u /* no timing: cheapest record/wait */

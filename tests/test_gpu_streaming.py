@@ -147,6 +147,29 @@ def test_llama_small_generate_matches_resident(gpu):
     mgr.release()
 
 
+def test_fp8_llama_batch8_decode_matches_resident(gpu):
+    shape = W.LlamaShape(n_layers=4, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=704, vocab=1000,
+                         max_seq=128, fp8=True)
+    model = W.build_llama(shape, seed=3)
+    prompt = W.prompt_tokens(8, 16, shape.vocab, seed=3).to(gpu)
+    ref = _resident(model, gpu)
+    ref.init_cache(8, 40, gpu)
+    want_tokens, want_logits = W.generate(ref, prompt, 6)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    other = sum(p.numel() * p.element_size() for n, p in model.named_parameters() if not n.startswith("layers."))
+    other += sum(b.numel() * b.element_size() for b in model.buffers())
+    mgr = _stream(model, gpu, max_gpu_mem_bytes=other + int(3.5 * layer))  # 3 streamed + 1 resident
+    model.init_cache(8, 40, gpu)
+    W.generate(model, prompt, 6)  # discovery + profiling
+    model.init_cache(8, 40, gpu)
+    got_tokens, got_logits = W.generate(model, prompt, 6)
+    assert mgr.plan.streamed and mgr.plan.resident
+    assert torch.equal(got_tokens, want_tokens)
+    for a, b in zip(got_logits, want_logits):
+        assert torch.equal(a, b)
+    mgr.release()
+
+
 @pytest.mark.parametrize("chunk_mib", [1, 4])
 def test_chunked_upload_bit_exact(gpu, chunk_mib):
     from flextensor_amd.hip import checksum

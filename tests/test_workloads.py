@@ -138,3 +138,39 @@ def test_dit_block_matches_float32_restatement():
     assert rel < 2e-2, float(rel)
     assert sum(p.numel() for p in model.blocks[0].parameters()) == shape.block_params()
     assert W.WAN_DIT.block_params() * 2 == 702_788_608
+
+
+def _dequantized_twin(model: W.LlamaModel) -> W.LlamaModel:
+    """Float32 copy of an fp8 model with every projection replaced by W_fp8 * scale."""
+    s = model.shape
+    twin = W.build_llama(W.LlamaShape(**{**s.__dict__, "fp8": False}), seed=0).float()
+    mods = dict(model.named_modules())
+    sd = {}
+    for name, p in model.named_parameters():
+        owner = name.rsplit(".", 1)[0]
+        if isinstance(mods.get(owner), W.Fp8Linear):
+            if name.endswith(".weight"):
+                sd[name] = mods[owner].weight.float() * mods[owner].scale.float()[:, None]
+        else:
+            sd[name] = p.detach().float()
+    twin.load_state_dict(sd, strict=False)
+    return twin
+
+
+def test_fp8_llama_matches_dequantized_float32():
+    shape = W.LlamaShape(n_layers=2, hidden=64, n_heads=4, n_kv_heads=2, head_dim=16, inter=96, vocab=100,
+                         max_seq=32, fp8=True)
+    model = W.build_llama(shape, seed=3)
+    fp8_linears = [m for m in model.modules() if isinstance(m, W.Fp8Linear)]
+    assert len(fp8_linears) == 14 and all(m.weight.dtype == torch.float8_e4m3fn for m in fp8_linears)
+    # per-channel scales put every row's absmax at the top of the e4m3 range
+    w = fp8_linears[0].weight.float()
+    assert torch.allclose(w.abs().amax(1), torch.full((w.shape[0],), 448.0), rtol=0.07)
+    tokens = W.prompt_tokens(2, 6, shape.vocab, seed=3)
+    model.init_cache(2, 32, torch.device("cpu"))
+    got = model(tokens, 0)
+    twin = _dequantized_twin(model)
+    twin.init_cache(2, 32, torch.device("cpu"))
+    want = twin(tokens, 0)
+    assert float((got - want).norm() / want.norm()) < 1e-2
+    assert W.LLAMA_70B_FP8.layer_bytes() == 855_838_720
