@@ -76,11 +76,8 @@ int device_state(DeviceState **out) {
     }
     size_t free_b = 0, total_b = 0;
     FTX_HIP(hipMemGetInfo(&free_b, &total_b));
-    for (int i = 0; i < kMaxCopyStreams; ++i) {
-      FTX_HIP(hipStreamCreateWithFlags(&st.copy_streams[i], hipStreamNonBlocking));
-      FTX_HIP(hipEventCreateWithFlags(&st.join_events[i], hipEventDisableTiming));
-    }
-    FTX_HIP(hipEventCreateWithFlags(&st.fork_event, hipEventDisableTiming));
+    // Copy streams are created on the first split copy (copy_streams_ready):
+    // every extra stream changes how streams share the device's hardware queues.
     st.cu_count = cus;
     st.xcd_count = xccs;
     st.total_mem = total_b;
@@ -163,6 +160,14 @@ int copy_sdma(void *dst, const void *src, size_t nbytes, hipStream_t stream, con
   int rc = device_state(&st);
   if (rc != FTX_OK) return rc;
   const int k = std::min(pol.n_copy_streams, kMaxCopyStreams);
+  {
+    std::lock_guard<std::mutex> lock(g_dev_mutex);
+    if (!st->fork_event) FTX_HIP(hipEventCreateWithFlags(&st->fork_event, hipEventDisableTiming));
+    for (int i = 0; i < k; ++i) {
+      if (!st->copy_streams[i]) FTX_HIP(hipStreamCreateWithFlags(&st->copy_streams[i], hipStreamNonBlocking));
+      if (!st->join_events[i]) FTX_HIP(hipEventCreateWithFlags(&st->join_events[i], hipEventDisableTiming));
+    }
+  }
   const size_t align = size_t(1) << 16;
   size_t piece = (nbytes + k - 1) / k;
   piece = (piece + align - 1) / align * align;

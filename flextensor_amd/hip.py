@@ -115,6 +115,72 @@ def new_stream(device: torch.device | int | None = None, name: str = "transfer")
     return HipStream(torch.cuda.Stream(device=device), name=name)
 
 
+_TRANSFER_STREAMS: dict[int, HipStream] = {}
+_REJECTED_STREAMS: list[Any] = []  # kept alive so later streams are not handed the same queue again
+
+
+def _runs_concurrently(candidate: HipStream, compute: HipStream, device: torch.device) -> bool:
+    """Whether work on ``candidate`` proceeds while ``compute`` is busy.
+
+    Streams share the device's hardware queues; a stream on the compute
+    stream's queue waits behind every compute packet. The check queues about
+    two milliseconds of matrix products on ``compute`` (enqueued in a tenth of
+    that) and a one-kilobyte fill on ``candidate``, and compares when each
+    finishes.
+    """
+    a = torch.ones(4096, 4096, dtype=torch.bfloat16, device=device)
+    small = torch.empty(1024, dtype=torch.uint8, device=device)
+    torch.cuda.synchronize(device)
+    c_end, s_end, start = HipEvent(timing=True), HipEvent(timing=True), HipEvent(timing=True)
+    compute.record_event(start)
+    with torch.cuda.stream(compute.torch_stream) if compute.torch_stream is not None else _nullctx():
+        for _ in range(16):
+            torch.matmul(a, a)
+    compute.record_event(c_end)
+    with torch.cuda.stream(candidate.torch_stream):
+        small.fill_(1)
+    candidate.record_event(s_end)
+    torch.cuda.synchronize(device)
+    busy = start.elapsed_time(c_end)
+    return start.elapsed_time(s_end) < 0.5 * busy
+
+
+@contextmanager
+def _nullctx() -> Iterator[None]:
+    yield
+
+
+def transfer_stream(device: torch.device | int | None = None, attempts: int = 8) -> HipStream:
+    """The per-device stream used for host-to-device transfers.
+
+    Chosen once per device among new default-priority streams: the first one
+    whose work runs concurrently with torch's current stream (see
+    :func:`_runs_concurrently`). If none of ``attempts`` candidates does, the
+    last one is used and a warning is logged.
+    """
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    cached = _TRANSFER_STREAMS.get(dev.index)
+    if cached is not None:
+        return cached
+    compute = current_stream(dev)
+    chosen = None
+    for _ in range(attempts):
+        cand = new_stream(dev, name="transfer")
+        if _runs_concurrently(cand, compute, dev):
+            chosen = cand
+            break
+        _REJECTED_STREAMS.append(cand)
+    if chosen is None:
+        import logging
+
+        logging.getLogger(__name__).warning("no transfer stream found that runs beside the compute stream")
+        chosen = _REJECTED_STREAMS.pop()
+    _TRANSFER_STREAMS[dev.index] = chosen
+    return chosen
+
+
 @contextmanager
 def use_stream(stream: HipStream) -> Iterator[None]:
     """Make ``stream`` torch's current stream inside the block."""

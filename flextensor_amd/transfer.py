@@ -59,9 +59,10 @@ class HipBackend:
         return current_stream(self.device)
 
     def new_stream(self, device: Any) -> Any:
-        from .hip import new_stream
+        """The device's transfer stream: shared by all runtimes, chosen to run beside compute."""
+        from .hip import transfer_stream
 
-        return new_stream(device if device is not None else self.device)
+        return transfer_stream(device if device is not None else self.device)
 
     def use_stream(self, stream: Any) -> AbstractContextManager:
         from .hip import use_stream

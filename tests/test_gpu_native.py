@@ -168,3 +168,26 @@ def test_kernel_copy_rejects_source_past_arena(gpu):
     with pytest.raises(nat.FtxError) as err:
         nat.copy_h2d(dst.data_ptr(), arena.ptr, 8192, nat.COPY_KERNEL, current_stream(gpu).handle)
     assert err.value.code == nat.FTX_ERR_INVALID
+
+
+def test_transfer_stream_runs_beside_compute(gpu):
+    """The transfer stream does not share a hardware queue with torch's compute stream."""
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import HipEvent, HostArena, current_stream, transfer_stream
+
+    s = transfer_stream(gpu)
+    comp = current_stream(gpu)
+    a = torch.randn(8192, 8192, device=gpu, dtype=torch.bfloat16)
+    arena = HostArena(64 << 20)
+    dst = torch.empty(64 << 20, dtype=torch.uint8, device=gpu)
+    torch.cuda.synchronize()
+    start, gemm_end, copy_end = HipEvent(True), HipEvent(True), HipEvent(True)
+    comp.record_event(start)
+    for _ in range(10):
+        torch.matmul(a, a)
+    comp.record_event(gemm_end)
+    nat.copy_h2d(dst.data_ptr(), arena.ptr, 64 << 20, nat.COPY_SDMA, s.handle)
+    s.record_event(copy_end)
+    torch.cuda.synchronize()
+    assert start.elapsed_time(copy_end) < 0.5 * start.elapsed_time(gemm_end)
+    assert transfer_stream(gpu) is s  # one per device
