@@ -277,6 +277,73 @@ def bench_dit(budget_gb: float, tokens: int, text: int, steps: int) -> dict:
     return out
 
 
+def _mem_available_bytes() -> int:
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return 0
+
+
+def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: int, layers: int) -> dict:
+    """Batch decode of the 70B-shape decoder with fp8 weights (per-channel bf16 scales) under a GPU budget."""
+    import torch
+
+    from flextensor_amd import workloads as W
+    from flextensor_amd.config import OffloadConfig
+    from flextensor_amd.manager import OffloadManager
+
+    s = W.LlamaShape(**{**W.LLAMA_70B_FP8.__dict__, "n_layers": layers})
+    need = s.layer_bytes() * s.n_layers * 2 + (8 << 30)
+    avail = _mem_available_bytes()
+    if avail < need:
+        return {"skipped": f"needs ~{need / 2**30:.0f} GiB of host memory, {avail / 2**30:.0f} GiB available"}
+    dev = torch.device("cuda", 0)
+    t0 = time.perf_counter()
+    model = W.build_llama(s, seed=3, init_device="cuda")
+    t_build = time.perf_counter() - t0
+    mgr = OffloadManager("bench-70b")
+    t0 = time.perf_counter()
+    # module order is the execution order of this decoder: plan at offload() time
+    mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=0,
+                                     profiling_iters=0, max_gpu_mem_bytes=int(budget_gb * 1e9)))
+    t_setup = time.perf_counter() - t0
+    _log(f"70b: built {t_build:.1f} s, streaming set up {t_setup:.1f} s; "
+         f"{len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers")
+    prompt = W.prompt_tokens(batch, prompt_len, s.vocab, seed=3).to(dev)
+    model.init_cache(batch, prompt_len + decode + 2, dev)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = model(prompt, 0)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        tok = logits.argmax(-1)
+        pos = prompt_len
+        model(tok, pos)  # warm-up step
+        pos += 1
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode):
+            tok = model(tok, pos).argmax(-1)
+            pos += 1
+        torch.cuda.synchronize()
+        t_step = (time.perf_counter() - t0) / decode
+    streamed = sum(mgr._unit(x).nbytes for x in mgr.plan.streamed)
+    out = {
+        "layers": s.n_layers, "batch": batch, "prompt_tokens": prompt_len, "decode_steps": decode,
+        "streamed_layers": len(mgr.plan.streamed), "resident_layers": len(mgr.plan.resident),
+        "layer_bytes": s.layer_bytes(), "streamed_bytes_per_step": streamed,
+        "step_s": t_step, "decode_tok_s": batch / t_step, "decode_effective_GBps": streamed / t_step / 1e9,
+        "prefill_s": t_prefill, "gpu_weight_bytes": mgr.get_gpu_memory_usage().total_bytes,
+        "budget_bytes": int(budget_gb * 1e9), "setup_s": t_setup,
+    }
+    mgr.release(preserve_model=False)
+    return out
+
+
 def measure_traffic(args) -> dict | None:
     """HBM bytes per scatter launch from two ``rocprofv3 --pmc`` child runs.
 
@@ -362,6 +429,8 @@ def main() -> int:
     ap.add_argument("--link-sweep", action="store_true",
                     help="only print the host-to-device GB/s of each copy engine over chunk sizes 64 KiB-512 MiB")
     ap.add_argument("--skip-dit", action="store_true")
+    ap.add_argument("--with-70b", action="store_true", help="also run the 80-layer fp8 70B-shape batch-8 decode")
+    ap.add_argument("--layers-70b", type=int, default=80)
     ap.add_argument("--dit-tokens", type=int, default=32760)
     ap.add_argument("--dit-steps", type=int, default=2)
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
@@ -464,6 +533,11 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["dit"] = bench_dit(12.0, args.dit_tokens, 512, args.dit_steps)
         _log(f"dit: {line['dit']}")
+    if args.with_70b:
+        gc.collect()
+        torch.cuda.empty_cache()
+        line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b)
+        _log(f"70b: {line['llama70b_fp8']}")
     print(json.dumps(line), flush=True)
     return 0
 

@@ -190,12 +190,27 @@ def use_stream(stream: HipStream) -> Iterator[None]:
         yield
 
 
+class _ArenaOwner:
+    """Frees one arena when the last reference to it goes away."""
+
+    __slots__ = ("ptr",)
+
+    def __init__(self, ptr: int) -> None:
+        self.ptr = ptr
+
+    def __del__(self) -> None:
+        if self.ptr and nat.live():
+            nat.lib().ftx_arena_free(self.ptr)
+            self.ptr = 0
+
+
 class HostArena:
     """Page-locked, device-mapped host bytes from ``ftx_arena_alloc``.
 
-    ``tensor`` is a CPU ``uint8`` tensor over the arena. The tensor keeps the
-    arena alive, so views of it stay valid after the arena object goes out of
-    scope; the memory is returned when the last view is gone.
+    ``tensor`` is a CPU ``uint8`` tensor over the arena. Ownership runs one
+    way - tensor -> buffer -> owner - so the memory is returned by reference
+    counting as soon as this object and every view of the tensor are gone
+    (no cycle waits for the garbage collector while pinned memory is held).
     """
 
     def __init__(self, nbytes: int, flags: int = nat.ARENA_DEFAULT) -> None:
@@ -204,16 +219,11 @@ class HostArena:
         self.nbytes = int(nbytes)
         self.flags = flags
         self.ptr = nat.arena_alloc(self.nbytes, flags)
+        owner = _ArenaOwner(self.ptr)
         self.device_ptr = nat.host_device_ptr(self.ptr)
         buf = (ctypes.c_uint8 * self.nbytes).from_address(self.ptr)
-        buf._ftx_arena = self  # the buffer (held by every view) keeps the arena alive
+        buf._ftx_owner = owner  # every view holds the buffer, the buffer holds the owner
         self.tensor = torch.frombuffer(buf, dtype=torch.uint8)
-
-    def __del__(self) -> None:
-        ptr = getattr(self, "ptr", None)
-        if ptr and nat.live():
-            nat.lib().ftx_arena_free(ptr)
-            self.ptr = None
 
 
 def copy_h2d(dst: torch.Tensor, src: torch.Tensor, mode: int, stream: HipStream | None = None,

@@ -53,6 +53,7 @@ from .planner import (
     remap_strategy,
 )
 from .prefetch_policy import PiecewisePrefetchPolicy
+from .profile import TensorManagerState, load_state, save_state
 from .scatter import upload_tensors
 from .timing import OffloadTimingCollector, OffloadTimingReport
 
@@ -147,10 +148,16 @@ class _Unit:
     label: str
     module: nn.Module
     params: list[nn.Parameter] = field(default_factory=list)
+    names: list[str] = field(default_factory=list)  # qualified parameter names, parallel to params
 
     @property
     def nbytes(self) -> int:
         return sum(p.numel() * p.element_size() for p in self.params)
+
+    def stats(self, duration: float = 0.0) -> LayerStatistics:
+        names = self.names or [f"{self.label}.{i}" for i in range(len(self.params))]
+        return LayerStatistics(self.label, [TensorStatistics(id(p), n, p.numel() * p.element_size())
+                                            for p, n in zip(self.params, names)], duration)
 
 
 def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | None, base_bytes: int,
@@ -163,8 +170,7 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
     if budget is not None and total <= budget:
         return StreamPlan([], labels, None, {}, False, budget, total)
     n = len(labels)
-    stats = [LayerStatistics(x, [TensorStatistics(id(p), x, p.numel() * p.element_size()) for p in by_label[x].params])
-             for x in labels]
+    stats = [by_label[x].stats() for x in labels]
     for k in range(1, n + 1):
         pick = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
         if len(pick) < k:
@@ -204,6 +210,74 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
     raise ValueError(f"GPU budget of {budget} bytes cannot hold the ring slots plus {base_bytes} resident bytes")
 
 
+def state_from_plan(model: nn.Module, units: Sequence[_Unit], plan: StreamPlan, durations: dict[str, float],
+                    loader_type: str) -> TensorManagerState:
+    """A plan as a saved state (state_handler.py:501-633): ids are this process's, names tie them to the model.
+
+    ``units`` are the offload units in execution order; ``durations`` their
+    profiled seconds.
+    """
+    id_to_name = {id(p): n for n, p in model.named_parameters()}
+    params = {id(p): p for p in model.parameters()}
+    bd = plan.block_data
+    streamed = [t for ts in plan.strategy_map.values() for t in ts]
+    return TensorManagerState(
+        loader_type=loader_type,
+        tensor_id_to_name_map=id_to_name,
+        allocation_ordered={b: list(v) for b, v in bd.allocation_ordered.items()} if bd else {},
+        label_to_size_map=dict(bd.label_to_size_map) if bd else {},
+        block_sizes=dict(bd.block_sizes) if bd else {},
+        load_strategy={k: list(v) for k, v in plan.strategy_map.items()},
+        release_strategy={},
+        label_to_block_id=dict(bd.label_to_block_id) if bd else {},
+        stats=[u.stats(durations.get(u.label, 0.0)) for u in units],
+        transfer_to_compute_map=dict(bd.transfer_to_compute_map) if bd else {},
+        view_tensors_ids=[t.tensor_id for t in streamed],
+        view_tensors_names=[t.name for t in streamed],
+        gpu_tensors_names=sorted(set(id_to_name.values()) - {t.name for t in streamed}),
+        managed_tensor_dtypes={t.name: str(params[t.tensor_id].dtype).removeprefix("torch.") for t in streamed},
+        managed_tensor_layouts={t.name: {"shape": list(params[t.tensor_id].shape),
+                                         "stride": list(params[t.tensor_id].stride())} for t in streamed},
+    )
+
+
+def plan_from_state(state: TensorManagerState, units: Sequence[_Unit], base_bytes: int,
+                    budget: int | None) -> StreamPlan:
+    """The saved plan re-keyed to the live tensors by name (the role of state_handler.py:673-745, 1072-1420).
+
+    ``units`` are the live offload units in the saved execution order. A
+    streamed tensor that is missing, or whose size, dtype or layout differs
+    from the saved metadata, raises ``ValueError``.
+    """
+    by_name = {n: p for u in units for n, p in zip(u.names, u.params)}
+    strategy: dict[str, list[TensorStatistics]] = {}
+    for label, ts in state.load_strategy.items():
+        cur = []
+        for t in ts:
+            p = by_name.get(t.name)
+            if p is None or p.numel() * p.element_size() != t.size_bytes:
+                raise ValueError(f"profile tensor {t.name!r} is missing or has a different size in this model")
+            dt = state.managed_tensor_dtypes.get(t.name)
+            if dt is not None and str(p.dtype).removeprefix("torch.") != dt:
+                raise ValueError(f"profile tensor {t.name!r} was {dt}, the model holds {p.dtype}")
+            lay = state.managed_tensor_layouts.get(t.name)
+            if lay is not None and (list(p.shape) != lay["shape"] or list(p.stride()) != lay["stride"]):
+                raise ValueError(f"profile tensor {t.name!r} has shape/stride {lay['shape']}/{lay['stride']}, "
+                                 f"the model holds {list(p.shape)}/{list(p.stride())}")
+            cur.append(TensorStatistics(id(p), t.name, t.size_bytes, t.load_time_ms))
+        strategy[label] = cur
+    bd = state.block_data() if state.load_strategy else None
+    order = [u.label for u in units]
+    consumers = set(state.transfer_to_compute_map.values())
+    streamed = [x for x in order if x in consumers]
+    resident = [x for x in order if x not in consumers]
+    nxt = {a: order[(i + 1) % len(order)] for i, a in enumerate(order)}
+    reordered = any(nxt.get(t) != c for t, c in state.transfer_to_compute_map.items())
+    by_label = {u.label: u for u in units}
+    gpu = base_bytes + sum(by_label[x].nbytes for x in resident) + (sum(bd.block_sizes.values()) if bd else 0)
+    return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
+
+
 class OffloadManager:
     """One named offload session: phases, plan, loader and the patched model."""
 
@@ -233,7 +307,9 @@ class OffloadManager:
 
     # -- public ---------------------------------------------------------------
 
-    def offload(self, model: nn.Module, config: OffloadConfig | None = None) -> nn.Module:
+    def offload(self, model: nn.Module, config: OffloadConfig | None = None,
+                state: TensorManagerState | None = None) -> nn.Module:
+        """Patch ``model``; with a saved ``state`` the plan is restored and streaming starts at once."""
         self._check_thread()
         if self.model is not None:
             raise RuntimeError(f"offload manager {self.name!r} already manages a model; release() it first")
@@ -241,26 +317,110 @@ class OffloadManager:
         if not self.config.enabled:
             return model
         nat.load()
-        self.device = torch.device("cuda", self.config.gpu_device)
-        torch.cuda.set_device(self.device)
-        self.model = model
-        labels = select_offload_units(model, self.config.include_patterns, self.config.exclude_patterns)
+        name_of = {id(p): n for n, p in model.named_parameters()}
+        if state is not None:
+            labels = [s.label for s in state.stats]
+            self._check_state(state, name_of)
+        else:
+            labels = select_offload_units(model, self.config.include_patterns, self.config.exclude_patterns)
+        units: list[_Unit] = []
         unit_params: set[int] = set()
         for label in labels:
             mod = model.get_submodule(label)
             params = [p for p in mod.parameters() if id(p) not in unit_params]
             unit_params.update(id(p) for p in params)
-            self.units.append(_Unit(label, mod, params))
+            units.append(_Unit(label, mod, params, [name_of[id(p)] for p in params]))
+        if state is not None:
+            plan_from_state(state, units, 0, None)  # every mismatch surfaces before the model is touched
+        self.device = torch.device("cuda", self.config.gpu_device)
+        torch.cuda.set_device(self.device)
+        self.model = model
+        self.units = units
         self._place_outside_units(unit_params)
         for u in self.units:
             self._patch(u)
         self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
         self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
         self.phase = OffloadPhase.DISCOVERY if self.config.discovery_iters > 0 else OffloadPhase.PROFILING
-        if self.config.discovery_iters == 0 and self.config.profiling_iters == 0:
+        if state is not None:
+            self.order = labels
+            self._to_inference(state)
+        elif self.config.discovery_iters == 0 and self.config.profiling_iters == 0:
             self.order = [u.label for u in self.units]
             self._to_inference()
         return model
+
+    def _check_state(self, state: TensorManagerState, name_of: dict[int, str]) -> None:
+        if state.loader_type != self.config.transfer_mode:
+            raise ValueError(f"profile was made with transfer_mode={state.loader_type!r}, "
+                             f"config selects {self.config.transfer_mode!r}")
+        self._check_inventory(state, name_of)
+
+    def _check_inventory(self, state: TensorManagerState, name_of: dict[int, str]) -> None:
+        saved = set(state.tensor_id_to_name_map.values())
+        current = set(name_of.values())
+        if saved != current:
+            raise ValueError(f"profile does not match the model: missing={sorted(saved - current)[:8]}, "
+                             f"unexpected={sorted(current - saved)[:8]}")
+
+    def _resolve_profile_directory(self, profile_directory: str | None) -> str:
+        """The explicit directory, else ``config.profile_storage_dir`` (offload_manager.py:750-768)."""
+        resolved = profile_directory or (self.config.profile_storage_dir if self.config is not None else None)
+        if resolved is None:
+            raise ValueError("No profile directory specified. Provide profile_directory argument "
+                             "or set profile_storage_dir in OffloadConfig.")
+        return resolved
+
+    def save_profile(self, profile_directory: str | None = None) -> str:
+        """Write the current plan as ``<dir>/profile.json`` (schema 3); returns the file path.
+
+        Mirrors offload_manager.py:770-792: a manager with no model raises
+        ``RuntimeError``; a missing directory raises ``ValueError``.
+        """
+        if self.model is None:
+            raise RuntimeError("Tensor manager not initialized. Call offload() first.")
+        directory = self._resolve_profile_directory(profile_directory)
+        if self.phase != OffloadPhase.INFERENCE or self.plan is None:
+            raise RuntimeError("No profile data yet: the model has not reached the INFERENCE phase.")
+        return str(save_state(self.state(), directory))
+
+    def load_profile(self, profile_directory: str | None = None, model: nn.Module | None = None) -> None:
+        """Adopt ``<dir>/profile.json`` (offload_manager.py:794-816).
+
+        With no model under management, ``model`` is offloaded with the saved
+        plan. A model still in discovery or profiling switches to streaming
+        with the saved plan at once.
+        """
+        self._check_thread()
+        target = model if model is not None else self.model
+        if target is None:
+            raise RuntimeError("No model provided and no model has been offloaded yet.")
+        state = load_state(self._resolve_profile_directory(profile_directory))
+        if self.model is None:
+            self.offload(target, self.config, state=state)
+            return
+        if target is not self.model:
+            raise RuntimeError("this manager manages another model; release() it first")
+        if self.phase == OffloadPhase.INFERENCE:
+            raise RuntimeError("the model is already streaming; release() it before loading a profile")
+        self._check_state(state, {id(p): n for n, p in self.model.named_parameters()})
+        saved = [s.label for s in state.stats]
+        if set(saved) != {u.label for u in self.units}:
+            diff = sorted(set(saved) ^ {u.label for u in self.units})
+            raise ValueError(f"profile offload units differ from this model's: {diff[:8]}")
+        plan_from_state(state, [self._unit(x) for x in saved], 0, None)  # mismatches raise before any change
+        self.order = saved
+        self._to_inference(state)
+
+    def state(self) -> TensorManagerState:
+        """The plan as a :class:`TensorManagerState` keyed by this process's tensor ids."""
+        assert self.model is not None and self.plan is not None
+        return state_from_plan(self.model, [self._unit(x) for x in self.order], self.plan,
+                               {x: self._duration(x) for x in self.order}, self.config.transfer_mode)
+
+    def _duration(self, label: str) -> float:
+        d = self.durations.get(label, [])
+        return float(sum(d) / len(d)) if d else 0.0
 
     def iters_before_inference(self) -> int:
         if self.phase == OffloadPhase.INFERENCE:
@@ -430,21 +590,26 @@ class OffloadManager:
             return int(total * self.config.max_gpu_mem_fraction)
         return None
 
-    def _to_inference(self) -> None:
+    def _plan_from_state(self, state: TensorManagerState) -> StreamPlan:
+        for st in state.stats:
+            if st.duration:
+                self.durations.setdefault(st.label, []).append(st.duration)
+        return plan_from_state(state, [self._unit(x) for x in self.order], self._resident_bytes, self._budget())
+
+    def _to_inference(self, state: TensorManagerState | None = None) -> None:
         t0 = time.perf_counter()
         cfg = self.config
         units_in_order = [self._unit(x) for x in self.order] if self.order else list(self.units)
         order = [u.label for u in units_in_order]
         blocks = max(cfg.num_blocks, 2)
-        self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks)
+        if state is not None:
+            self.plan = self._plan_from_state(state)
+        else:
+            self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks)
         plan = self.plan
         resident_params = [p for x in plan.resident for p in self._unit(x).params]
         self._resident_bytes += self._upload_into(resident_params)
-        layer_stats = [
-            LayerStatistics(x, [TensorStatistics(id(p), x, p.numel() * p.element_size()) for p in self._unit(x).params],
-                            float(sum(self.durations.get(x, [0.0])) / max(1, len(self.durations.get(x, [])))))
-            for x in order
-        ]
+        layer_stats = [self._unit(x).stats(self._duration(x)) for x in order]
         if plan.block_data is None:
             self.loader = _ResidentLoader()
         else:
@@ -524,3 +689,32 @@ def collect_offload_timing(name: str = DEFAULT_MANAGER_NAME) -> OffloadTimingRep
 
 def reset_offload_timing(name: str = DEFAULT_MANAGER_NAME) -> None:
     get_offload_manager(name).reset_offload_timing()
+
+
+def save_profile(profile_directory: str | None = None, name: str = DEFAULT_MANAGER_NAME) -> str:
+    """Save the named manager's plan as ``<dir>/profile.json`` (offload_manager.py:2898-2907)."""
+    return get_offload_manager(name).save_profile(profile_directory)
+
+
+def load_profile(profile_directory: str | None = None, model: nn.Module | None = None,
+                 name: str = DEFAULT_MANAGER_NAME) -> None:
+    """Adopt a saved profile in the named manager (offload_manager.py:2910-2922)."""
+    get_offload_manager(name).load_profile(profile_directory, model)
+
+
+def offload_from_profile(model: nn.Module, config: OffloadConfig | None = None, profile_directory: str | None = None,
+                         name: str = DEFAULT_MANAGER_NAME) -> nn.Module:
+    """Offload ``model`` straight into streaming with a saved plan: no discovery or profiling passes."""
+    cfg = config or OffloadConfig()
+    directory = profile_directory or cfg.profile_storage_dir
+    if directory is None:
+        raise ValueError("No profile directory specified. Provide profile_directory argument "
+                         "or set profile_storage_dir in OffloadConfig.")
+    return get_offload_manager(name).offload(model, cfg, state=load_state(directory))
+
+
+def offload_from_state(model: nn.Module, state: TensorManagerState, config: OffloadConfig | None = None,
+                       name: str = DEFAULT_MANAGER_NAME) -> nn.Module:
+    """Adopt an in-memory saved plan (offload_manager.py:2925-2958); ``state`` must use ``config``'s transfer mode."""
+    mgr = get_offload_manager(name)
+    return mgr.offload(model, config or mgr.config or OffloadConfig(), state=state)
