@@ -26,7 +26,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
 constexpr int kZeroCopyUnroll = 8;
-constexpr int kScatterUnroll = 8;
 
 __device__ __forceinline__ uint64_t d_splitmix64(uint64_t x) {
   x += 0x9e3779b97f4a7c15ull;
@@ -80,6 +79,9 @@ __global__ __launch_bounds__(kThreads) void zero_copy_kernel(uint8_t *__restrict
 // One wavefront copies `len` bytes. The widest access that both pointers
 // allow is used: 16 bytes when src and dst are congruent modulo 16, 4 bytes
 // when congruent modulo 4, single bytes otherwise.
+// UNROLL 16-byte loads are issued per lane before the matching stores, so a
+// 16 KiB tile with UNROLL 16 is a single round of loads then stores.
+template <int UNROLL>
 __device__ __forceinline__ void wave_copy(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src,
                                           uint64_t len, int lane) {
   const uint64_t sa = reinterpret_cast<uint64_t>(src);
@@ -90,15 +92,15 @@ __device__ __forceinline__ void wave_copy(uint8_t *__restrict__ dst, const uint8
     const uint64_t n16 = (len - head) / 16;
     const u32x4 *s = reinterpret_cast<const u32x4 *>(src + head);
     u32x4 *d = reinterpret_cast<u32x4 *>(dst + head);
-    for (uint64_t base = lane; base < n16; base += static_cast<uint64_t>(kWave) * kScatterUnroll) {
-      u32x4 v[kScatterUnroll];
+    for (uint64_t base = lane; base < n16; base += static_cast<uint64_t>(kWave) * UNROLL) {
+      u32x4 v[UNROLL];
 #pragma unroll
-      for (int k = 0; k < kScatterUnroll; ++k) {
+      for (int k = 0; k < UNROLL; ++k) {
         const uint64_t i = base + static_cast<uint64_t>(k) * kWave;
         if (i < n16) v[k] = __builtin_nontemporal_load(s + i);
       }
 #pragma unroll
-      for (int k = 0; k < kScatterUnroll; ++k) {
+      for (int k = 0; k < UNROLL; ++k) {
         const uint64_t i = base + static_cast<uint64_t>(k) * kWave;
         if (i < n16) d[i] = v[k];
       }
@@ -125,6 +127,7 @@ __device__ __forceinline__ void wave_copy(uint8_t *__restrict__ dst, const uint8
 // built, so every descriptor owns at least one tile and the
 // kScatterWavesPerGroup consecutive tiles of a workgroup touch at most
 // kScatterWavesPerGroup consecutive descriptors starting at group_desc0.
+template <int UNROLL>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(const ftx_desc *__restrict__ descs,
                                                            const uint64_t *__restrict__ tile_start,
                                                            const uint32_t *__restrict__ group_desc0,
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const ftx_desc *__res
   const ftx_desc dsc = s_desc[j];
   const uint64_t off = (static_cast<uint64_t>(tile) - s_tile_start[j]) * tile_bytes;
   const uint64_t len = min<uint64_t>(tile_bytes, dsc.nbytes - off);
-  wave_copy(reinterpret_cast<uint8_t *>(dsc.dst) + off, chunk + dsc.src_off + off, len, lane);
+  wave_copy<UNROLL>(reinterpret_cast<uint8_t *>(dsc.dst) + off, chunk + dsc.src_off + off, len, lane);
 }
 
 // Checksum: word w (8 bytes, little endian, zero padded past nbytes) belongs
@@ -224,9 +227,15 @@ hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int g
 
 hipError_t launch_scatter(const ScatterPlanDev &plan, const void *chunk, hipStream_t stream) {
   if (plan.n_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(scatter_kernel, dim3(static_cast<unsigned>(plan.n_groups)), dim3(kThreads), 0,
-                     stream, plan.descs, plan.tile_start, plan.group_desc0, plan.n_desc,
-                     plan.n_tiles, plan.tile_bytes, static_cast<const uint8_t *>(chunk));
+  // 16 KiB and larger tiles: 16 loads in flight per lane; smaller tiles: 8.
+  if (plan.tile_bytes >= 16 * 1024)
+    hipLaunchKernelGGL(scatter_kernel<16>, dim3(static_cast<unsigned>(plan.n_groups)), dim3(kThreads), 0,
+                       stream, plan.descs, plan.tile_start, plan.group_desc0, plan.n_desc,
+                       plan.n_tiles, plan.tile_bytes, static_cast<const uint8_t *>(chunk));
+  else
+    hipLaunchKernelGGL(scatter_kernel<8>, dim3(static_cast<unsigned>(plan.n_groups)), dim3(kThreads), 0,
+                       stream, plan.descs, plan.tile_start, plan.group_desc0, plan.n_desc,
+                       plan.n_tiles, plan.tile_bytes, static_cast<const uint8_t *>(chunk));
   return hipGetLastError();
 }
 

@@ -23,7 +23,7 @@ struct CopyPolicy {
   size_t kernel_max_bytes = 1u << 20;  // AUTO: chunks up to 1 MiB go to the zero-copy kernel
   size_t split_min_bytes = ~size_t(0); // SDMA splitting disabled until measured
   int n_copy_streams = 1;
-  int kernel_grid = 0;                 // 0: 4 workgroups per CU
+  int kernel_grid = 0;                 // 0: kZeroCopyDefaultGrid
 };
 
 struct DeviceState {
@@ -201,7 +201,7 @@ int copy_kernel(void *dst, const void *src, size_t nbytes, hipStream_t stream, c
   DeviceState *st = nullptr;
   rc = device_state(&st);
   if (rc != FTX_OK) return rc;
-  const int grid = pol.kernel_grid > 0 ? pol.kernel_grid : std::max(1, st->cu_count * 4);
+  const int grid = pol.kernel_grid > 0 ? pol.kernel_grid : kZeroCopyDefaultGrid;
   FTX_HIP(launch_zero_copy(dst, src_dev, nbytes, grid, stream));
   return FTX_OK;
 }

@@ -57,13 +57,19 @@ class HipEvent:
 
     def __del__(self) -> None:
         h = getattr(self, "handle", None)
-        if h and nat.live():
+        if not h:
+            return
+        self.handle = None
+        try:
+            if not nat.live():
+                return
             free = _FREE_EVENTS[self.timing]
             if len(free) < _MAX_FREE_EVENTS:
                 free.append(h)
             else:
                 nat.lib().ftx_event_destroy(h)
-            self.handle = None
+        except (TypeError, AttributeError):
+            pass  # interpreter shutdown: module globals are already gone; the process frees the handle
 
 
 class HipStream:

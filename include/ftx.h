@@ -121,7 +121,7 @@ int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stre
  *   kernel_max_bytes  chunks <= this go to the zero-copy kernel under AUTO;
  *   split_min_bytes   SDMA copies >= this are split over n_copy_streams;
  *   n_copy_streams    1..8 dedicated copy streams;
- *   kernel_grid       zero-copy kernel workgroups (0 = derive from CU count). */
+ *   kernel_grid       zero-copy kernel workgroups (0 = 64, enough to hold the link at its peak). */
 int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams,
                         int kernel_grid);
 int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams,
@@ -131,7 +131,7 @@ int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *
  * No reference counterpart; it places a streamed chunk into many tensors in
  * one launch where the reference copies tensor by tensor (see ftx_desc).
  * A plan uploads descriptors once (device memory) and can be run any number
- * of times on any stream; tile_bytes 0 selects the default (64 KiB). */
+ * of times on any stream; tile_bytes 0 selects the default (16 KiB). */
 int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes,
                             ftx_scatter_plan **plan);
 int ftx_scatter_plan_destroy(ftx_scatter_plan *plan);

@@ -92,8 +92,8 @@ def _scatter_case(seed: int, n_desc: int, max_bytes: int, align_dst: bool):
 
 
 @pytest.mark.parametrize("seed,n_desc,max_bytes", [(1, 1, 4096), (2, 37, 70000), (3, 500, 1 << 20), (4, 2000, 200000)])
-@pytest.mark.parametrize("planned", [True, False])
-def test_scatter_matches_oracle(gpu, seed, n_desc, max_bytes, planned):
+@pytest.mark.parametrize("tile", [None, 0, 1040, 4096, 65536])  # None: one-shot ftx_scatter; 0: default tile
+def test_scatter_matches_oracle(gpu, seed, n_desc, max_bytes, tile):
     from flextensor_amd import _native as nat
     from flextensor_amd.hip import current_stream
 
@@ -106,11 +106,11 @@ def test_scatter_matches_oracle(gpu, seed, n_desc, max_bytes, planned):
     descs = [(off, d.data_ptr() + int(sh), int(n)) for off, d, sh, n in zip(offsets, dsts, shifts, sizes)]
     arr = nat.make_desc_array(descs)
     s = current_stream(gpu)
-    if planned:
+    if tile is not None:
         import ctypes
 
         plan = ctypes.c_void_p()
-        nat.call("ftx_scatter_plan_create", arr, len(descs), 0, ctypes.byref(plan))
+        nat.call("ftx_scatter_plan_create", arr, len(descs), tile, ctypes.byref(plan))
         try:
             nat.call("ftx_scatter_run", plan, chunk_dev.data_ptr(), s.handle)
             torch.cuda.synchronize()
