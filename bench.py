@@ -408,6 +408,85 @@ def traffic_probe(args) -> int:
     return 0
 
 
+def engine_contention() -> dict:
+    """How each copy engine shares the GPU with an HBM-bound kernel.
+
+    Three tables, medians of repeated runs on one GPU:
+
+    * host-to-device GB/s of the zero-copy kernel by workgroup count (512 MiB);
+    * scatter-kernel time alone, by wave-tile size, for the 512 MiB chunk of
+      the 2000-tensor set that holds the most tensors;
+    * the same scatter (default tile) launched on the compute stream while a
+      512 MiB host-to-device copy runs on the transfer stream, per engine.
+    """
+    import torch
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import workloads as W
+    from flextensor_amd.hip import HipEvent, HostArena, current_stream, transfer_stream
+    from flextensor_amd.scatter import ScatterPlan, _dst_base, plan_chunks
+
+    dev = torch.device("cuda", 0)
+    comp, xs = current_stream(dev), transfer_stream(dev)
+    n = 512 * MiB
+    arena = HostArena(n)
+    arena.tensor.random_(0, 256)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    saved = nat.get_copy_policy()
+
+    def median_ms(fn, stream, reps):
+        ts = []
+        for _ in range(reps):
+            a, b = HipEvent(True), HipEvent(True)
+            stream.record_event(a)
+            fn()
+            stream.record_event(b)
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sorted(ts)[len(ts) // 2]
+
+    out: dict = {"kernel_grid_GBps": {}, "scatter_alone_us": {}, "scatter_beside_copy_us": {}}
+    try:
+        for grid in (4, 8, 16, 32, 64, 128, 1024):
+            nat.set_copy_policy(saved[0], saved[1], saved[2], grid)
+            ms = median_ms(lambda: nat.copy_h2d(dst.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, comp.handle), comp, 5)
+            out["kernel_grid_GBps"][grid] = round(n / ms / 1e6, 2)
+        sizes = W.scatter_sizes()
+        chunk = max(plan_chunks(sizes, 512 * MiB)[:6], key=lambda c: len(c.pieces))
+        dests = {p.index: torch.empty(sizes[p.index], dtype=torch.uint8, device=dev) for p in chunk.pieces}
+        descs = [(p.chunk_off, _dst_base(dests[p.index]) + p.tensor_off, p.nbytes) for p in chunk.pieces if p.nbytes]
+        if any(off + k > chunk.nbytes for off, _, k in descs) or chunk.nbytes > n:
+            raise RuntimeError("scatter probe descriptors exceed the chunk")
+        payload = sum(k for _, _, k in descs)
+        src = torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev)
+        for tile in (8 << 10, 16 << 10, 32 << 10, 64 << 10):
+            plan = ScatterPlan(descs, tile)
+            out["scatter_alone_us"][tile] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
+            plan.close()
+        plan = ScatterPlan(descs)
+        for label, mode, grid in (("hipMemcpyAsync", nat.COPY_SDMA, 0), ("kernel_grid_1024", nat.COPY_KERNEL, 1024),
+                                  ("kernel_grid_64", nat.COPY_KERNEL, 64), ("kernel_grid_16", nat.COPY_KERNEL, 16),
+                                  ("kernel_grid_4", nat.COPY_KERNEL, 4)):
+            nat.set_copy_policy(saved[0], saved[1], saved[2], grid)
+            ts = []
+            for _ in range(8):
+                torch.cuda.synchronize()
+                nat.copy_h2d(dst.data_ptr(), arena.ptr, n, mode, xs.handle)
+                a, b = HipEvent(True), HipEvent(True)
+                comp.record_event(a)
+                plan.run(src, comp)
+                comp.record_event(b)
+                torch.cuda.synchronize()
+                ts.append(a.elapsed_time(b))
+            out["scatter_beside_copy_us"][label] = round(1e3 * sorted(ts)[len(ts) // 2], 1)
+        plan.close()
+        out["scatter_payload_bytes"] = payload
+        out["scatter_pieces"] = len(descs)
+    finally:
+        nat.set_copy_policy(*saved)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -428,6 +507,8 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
     ap.add_argument("--link-sweep", action="store_true",
                     help="only print the host-to-device GB/s of each copy engine over chunk sizes 64 KiB-512 MiB")
+    ap.add_argument("--engine-contention", action="store_true",
+                    help="only print how each copy engine shares the GPU with the scatter kernel")
     ap.add_argument("--skip-dit", action="store_true")
     ap.add_argument("--with-70b", action="store_true", help="also run the 80-layer fp8 70B-shape batch-8 decode")
     ap.add_argument("--layers-70b", type=int, default=80)
@@ -451,6 +532,9 @@ def main() -> int:
     nat.load()
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.engine_contention:
+        print(json.dumps(engine_contention()), flush=True)
+        return 0
     if args.link_sweep:
         from flextensor_amd.link_model import choose_copy_policy, measure_copy_curve
 

@@ -79,47 +79,62 @@ __global__ __launch_bounds__(kThreads) void zero_copy_kernel(uint8_t *__restrict
 // One wavefront copies `len` bytes. The widest access that both pointers
 // allow is used: 16 bytes when src and dst are congruent modulo 16, 4 bytes
 // when congruent modulo 4, single bytes otherwise.
-// UNROLL 16-byte loads are issued per lane before the matching stores, so a
-// 16 KiB tile with UNROLL 16 is a single round of loads then stores.
+// Pointers in the global address space. Destinations come from descriptor
+// tables, so without the cast the compiler cannot tell they are global and
+// emits flat stores (which also count against the LDS counter and add waits).
+typedef __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) uint32_t g_u32;
+typedef __attribute__((address_space(1))) uint8_t g_u8;
+
+template <typename T>
+__device__ __forceinline__ T *as_global(const void *p) {
+  return (T *)(p);  // generic -> global address-space cast
+}
+
+// One wavefront copies `len` bytes. The widest access that both pointers
+// allow is used: 16 bytes when src and dst are congruent modulo 16, 4 bytes
+// when congruent modulo 4, single bytes otherwise. In the 16-byte path each
+// lane issues UNROLL loads before the matching stores; whole rounds of
+// 64 x UNROLL words run without bounds checks, and what is left of a partial
+// round is copied one word per lane at a time. A 16 KiB tile with UNROLL 16
+// is exactly one round.
 template <int UNROLL>
-__device__ __forceinline__ void wave_copy(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src,
+__device__ __forceinline__ void wave_copy(uint8_t *__restrict__ dst_, const uint8_t *__restrict__ src_,
                                           uint64_t len, int lane) {
-  const uint64_t sa = reinterpret_cast<uint64_t>(src);
-  const uint64_t da = reinterpret_cast<uint64_t>(dst);
+  g_u8 *dst = as_global<g_u8>(dst_);
+  const g_u8 *src = as_global<const g_u8>(src_);
+  const uint64_t sa = reinterpret_cast<uint64_t>(src_);
+  const uint64_t da = reinterpret_cast<uint64_t>(dst_);
+  const uint64_t ln = static_cast<uint64_t>(lane);
   if (((sa ^ da) & 15) == 0) {
     const uint64_t head = min<uint64_t>((16 - (sa & 15)) & 15, len);
-    if (static_cast<uint64_t>(lane) < head) dst[lane] = src[lane];
+    if (ln < head) dst[ln] = src[ln];
     const uint64_t n16 = (len - head) / 16;
-    const u32x4 *s = reinterpret_cast<const u32x4 *>(src + head);
-    u32x4 *d = reinterpret_cast<u32x4 *>(dst + head);
-    for (uint64_t base = lane; base < n16; base += static_cast<uint64_t>(kWave) * UNROLL) {
+    const g_u32x4 *s = as_global<const g_u32x4>(src_ + head);
+    g_u32x4 *d = as_global<g_u32x4>(dst_ + head);
+    constexpr uint64_t kRound = static_cast<uint64_t>(kWave) * UNROLL;
+    const uint64_t full = n16 / kRound * kRound;
+    for (uint64_t base = ln; base < full; base += kRound) {
       u32x4 v[UNROLL];
 #pragma unroll
-      for (int k = 0; k < UNROLL; ++k) {
-        const uint64_t i = base + static_cast<uint64_t>(k) * kWave;
-        if (i < n16) v[k] = __builtin_nontemporal_load(s + i);
-      }
+      for (int k = 0; k < UNROLL; ++k) v[k] = __builtin_nontemporal_load(s + base + k * kWave);
 #pragma unroll
-      for (int k = 0; k < UNROLL; ++k) {
-        const uint64_t i = base + static_cast<uint64_t>(k) * kWave;
-        if (i < n16) d[i] = v[k];
-      }
+      for (int k = 0; k < UNROLL; ++k) d[base + k * kWave] = v[k];
     }
+    for (uint64_t i = full + ln; i < n16; i += kWave) d[i] = __builtin_nontemporal_load(s + i);
     const uint64_t done = head + n16 * 16;
-    const uint64_t tail = len - done;
-    if (static_cast<uint64_t>(lane) < tail) dst[done + lane] = src[done + lane];
+    if (ln < len - done) dst[done + ln] = src[done + ln];
   } else if (((sa ^ da) & 3) == 0) {
     const uint64_t head = min<uint64_t>((4 - (sa & 3)) & 3, len);
-    if (static_cast<uint64_t>(lane) < head) dst[lane] = src[lane];
+    if (ln < head) dst[ln] = src[ln];
     const uint64_t n4 = (len - head) / 4;
-    const uint32_t *s = reinterpret_cast<const uint32_t *>(src + head);
-    uint32_t *d = reinterpret_cast<uint32_t *>(dst + head);
-    for (uint64_t i = lane; i < n4; i += kWave) d[i] = s[i];
+    const g_u32 *s = as_global<const g_u32>(src_ + head);
+    g_u32 *d = as_global<g_u32>(dst_ + head);
+    for (uint64_t i = ln; i < n4; i += kWave) d[i] = s[i];
     const uint64_t done = head + n4 * 4;
-    const uint64_t tail = len - done;
-    if (static_cast<uint64_t>(lane) < tail) dst[done + lane] = src[done + lane];
+    if (ln < len - done) dst[done + ln] = src[done + ln];
   } else {
-    for (uint64_t i = lane; i < len; i += kWave) dst[i] = src[i];
+    for (uint64_t i = ln; i < len; i += kWave) dst[i] = src[i];
   }
 }
 
@@ -128,7 +143,7 @@ __device__ __forceinline__ void wave_copy(uint8_t *__restrict__ dst, const uint8
 // kScatterWavesPerGroup consecutive tiles of a workgroup touch at most
 // kScatterWavesPerGroup consecutive descriptors starting at group_desc0.
 template <int UNROLL>
-__global__ __launch_bounds__(kThreads) void scatter_kernel(const ftx_desc *__restrict__ descs,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(6))) void scatter_kernel(const ftx_desc *__restrict__ descs,
                                                            const uint64_t *__restrict__ tile_start,
                                                            const uint32_t *__restrict__ group_desc0,
                                                            int n_desc, int64_t n_tiles,

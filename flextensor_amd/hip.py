@@ -205,9 +205,14 @@ class _ArenaOwner:
         self.ptr = ptr
 
     def __del__(self) -> None:
-        if self.ptr and nat.live():
-            nat.lib().ftx_arena_free(self.ptr)
-            self.ptr = 0
+        ptr, self.ptr = self.ptr, 0
+        if not ptr:
+            return
+        try:
+            if nat.live():
+                nat.lib().ftx_arena_free(ptr)
+        except (TypeError, AttributeError):
+            pass  # interpreter shutdown: module globals are already gone; the process frees the arena
 
 
 class HostArena:

@@ -161,16 +161,21 @@ def measure_copy_curve(engine: str, sizes: list[int], repeats: int = 10, device=
 
 
 def choose_copy_policy(sdma: CopyCurve, kernel: CopyCurve, split: CopyCurve | None = None,
-                       n_split: int = 1) -> tuple[int, int, int]:
+                       n_split: int = 1, min_kernel_gain: float = 1.10) -> tuple[int, int, int]:
     """Per-chunk choice from measured curves.
 
     Returns ``(kernel_max_bytes, split_min_bytes, n_copy_streams)``: chunks up
-    to ``kernel_max_bytes`` are faster on the zero-copy kernel, SDMA copies
-    from ``split_min_bytes`` up are faster split over ``n_copy_streams``.
+    to ``kernel_max_bytes`` go to the zero-copy kernel, SDMA copies from
+    ``split_min_bytes`` up are split over ``n_copy_streams``.
+
+    The kernel is chosen only where it is at least ``min_kernel_gain`` times
+    faster than SDMA: while it runs, its host reads hold up the memory
+    accesses of kernels sharing its CUs, a cost SDMA does not have, so a few
+    percent of link speed does not pay for it.
     """
     kernel_max = 0
     for n in sorted(sdma.best_ms):
-        if n in kernel.best_ms and kernel.best_ms[n] < sdma.best_ms[n]:
+        if n in kernel.best_ms and kernel.best_ms[n] * min_kernel_gain <= sdma.best_ms[n]:
             kernel_max = n
         else:
             break

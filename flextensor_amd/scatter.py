@@ -1,7 +1,7 @@
 """Stream packed host chunks through a device ring and scatter them into tensors.
 
-This is the build's batched unpack (row a14) and its use for placing tensors
-that stay resident on the GPU (row a10). The reference moves such tensors to
+This is the batched unpack of the streaming engine and its use for placing
+tensors that stay resident on the GPU. The reference moves such tensors to
 the device one ``.to()`` / ``copy_`` at a time (tensor_processors.py:685-742;
 loaders.py:592-617, 792-797); here they are packed into large pinned chunks,
 each chunk crosses the host link in one copy, and one scatter launch per chunk
@@ -11,6 +11,13 @@ Ordering uses :class:`~flextensor_amd.transfer.HipTransferRuntime`: chunk *i*
 is copied on the transfer stream into ring slot ``i % n_slots`` once the
 scatter of chunk ``i - n_slots`` released that slot, and its scatter runs on
 the caller's stream after the copy's ready event.
+
+Chunks are either packed up front into pinned memory of their own (the
+steady state of streaming, :func:`fill_chunks`) or staged: packed on the fly
+into a small ring of pinned staging buffers, buffer ``i % n_host`` being
+refilled once the copy of chunk ``i - n_host`` out of it has finished, so the
+host packing of one chunk overlaps the link transfer of the previous one and
+pinned memory stays at ``n_host`` chunks whatever the total.
 """
 
 from __future__ import annotations
@@ -56,9 +63,14 @@ class ScatterPlan:
 
     def __del__(self) -> None:
         h = getattr(self, "_handle", None)
-        if h is not None and h.value and nat.live():
-            nat.lib().ftx_scatter_plan_destroy(h)
+        if h is None or not h.value:
+            return
+        try:
+            if nat.live():
+                nat.lib().ftx_scatter_plan_destroy(h)
             self._handle = ctypes.c_void_p()
+        except (TypeError, AttributeError):
+            pass  # interpreter shutdown: module globals are already gone; the process frees the plan
 
 
 @dataclass
@@ -117,14 +129,21 @@ def _source_bytes(t: torch.Tensor) -> torch.Tensor:
     return t.detach().contiguous().view(-1).view(torch.uint8)
 
 
+def pack_chunk(host: torch.Tensor, ch: Chunk, tensors: Sequence[torch.Tensor]) -> None:
+    """Copy every piece of ``ch`` from ``tensors`` into the host bytes ``host``."""
+    if host.numel() < ch.nbytes:
+        raise ValueError(f"staging buffer of {host.numel()} bytes cannot hold a {ch.nbytes}-byte chunk")
+    for p in ch.pieces:
+        if p.nbytes:
+            src = _source_bytes(tensors[p.index])
+            host[p.chunk_off: p.chunk_off + p.nbytes].copy_(src[p.tensor_off: p.tensor_off + p.nbytes])
+
+
 def fill_chunks(chunks: Sequence[Chunk], tensors: Sequence[torch.Tensor]) -> None:
     """Allocate one pinned arena per chunk and copy every piece into it."""
     for ch in chunks:
         ch.host = HostArena(max(ch.nbytes, 1)).tensor
-        for p in ch.pieces:
-            if p.nbytes:
-                src = _source_bytes(tensors[p.index])
-                ch.host[p.chunk_off: p.chunk_off + p.nbytes].copy_(src[p.tensor_off: p.tensor_off + p.nbytes])
+        pack_chunk(ch.host, ch, tensors)
 
 
 def destination_like(t: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -142,12 +161,21 @@ class ChunkedUploader:
     """Uploads packed chunks into destination tensors through an ``n_slots`` ring."""
 
     def __init__(self, chunks: Sequence[Chunk], destinations: Sequence[torch.Tensor], device: torch.device,
-                 n_slots: int = 2, copy_mode: int = nat.COPY_AUTO, runtime: HipTransferRuntime | None = None) -> None:
-        if n_slots < 1:
-            raise ValueError("n_slots must be >= 1")
+                 n_slots: int = 2, copy_mode: int = nat.COPY_AUTO, runtime: HipTransferRuntime | None = None,
+                 sources: Sequence[torch.Tensor] | None = None, n_host: int = 2) -> None:
+        """``sources`` given: chunks without host bytes are staged through ``n_host`` pinned buffers."""
+        if n_slots < 1 or n_host < 1:
+            raise ValueError("n_slots and n_host must be >= 1")
         self.device = torch.device(device)
         self.chunks = list(chunks)
         self.copy_mode = copy_mode
+        self.sources = sources
+        staged = [c for c in self.chunks if c.host is None]
+        if staged and sources is None:
+            raise ValueError("chunks without host bytes need the source tensors to stage from")
+        stage_bytes = max((c.nbytes for c in staged), default=0)
+        self.staging = [HostArena(max(stage_bytes, 1)).tensor for _ in range(min(n_host, len(staged)))]
+        self._staging_free: list = [None] * len(self.staging)  # copy-done event of each staging buffer
         slot_bytes = max((c.nbytes for c in self.chunks), default=1)
         self.n_slots = min(n_slots, max(1, len(self.chunks)))
         self.slots = [torch.empty(max(slot_bytes, 1), dtype=torch.uint8, device=self.device)
@@ -177,18 +205,29 @@ class ChunkedUploader:
 
         rt = self.runtime
         rt.begin()
+        n_staged = 0
         for i, ch in enumerate(self.chunks):
             slot = i % self.n_slots
             dst = self.slots[slot]
             ev = [HipEvent(timing=True) for _ in range(4)] if timing is not None else None
+            host, stage = ch.host, None
+            if host is None:
+                stage = n_staged % len(self.staging)
+                n_staged += 1
+                if self._staging_free[stage] is not None:
+                    self._staging_free[stage].synchronize()  # the copy out of this buffer has finished
+                host = self.staging[stage]
+                pack_chunk(host, ch, self.sources)
 
-            def copy(ch: Chunk = ch, dst: torch.Tensor = dst, ev=ev) -> None:
+            def copy(ch: Chunk = ch, dst: torch.Tensor = dst, ev=ev, host: torch.Tensor = host, stage=stage) -> None:
                 s = rt.backend.current_stream()
                 if ev:
                     s.record_event(ev[0])
-                nat.copy_h2d(dst.data_ptr(), ch.host.data_ptr(), ch.nbytes, self.copy_mode, s.handle)
+                nat.copy_h2d(dst.data_ptr(), host.data_ptr(), ch.nbytes, self.copy_mode, s.handle)
                 if ev:
                     s.record_event(ev[1])
+                if stage is not None:
+                    self._staging_free[stage] = s.record_event(HipEvent())
 
             ticket = rt.submit(slot, copy, trace_label=f"chunk={i}")
             rt.wait_ready(ticket)
@@ -207,16 +246,23 @@ class ChunkedUploader:
         self.plans = []
         self.slots = []
         self.runtime.close()
+        self.staging, self._staging_free, self.sources = [], [], None
 
 
 def upload_tensors(tensors: Sequence[torch.Tensor], device: torch.device, chunk_bytes: int = DEFAULT_CHUNK_BYTES,
-                   n_slots: int = 2) -> list[torch.Tensor]:
-    """Device copies of host ``tensors`` placed by stream-and-scatter (layouts preserved)."""
+                   n_slots: int = 2, staged: bool = True, n_host: int = 2) -> list[torch.Tensor]:
+    """Device copies of host ``tensors`` placed by stream-and-scatter (layouts preserved).
+
+    ``staged`` packs chunk by chunk through ``n_host`` pinned staging buffers
+    (pinned memory bounded by ``n_host * chunk_bytes``); otherwise every chunk
+    is packed into pinned memory of its own before the first copy.
+    """
     device = torch.device(device)
     dests = [destination_like(t, device) for t in tensors]
     chunks = plan_chunks([t.numel() * t.element_size() for t in tensors], chunk_bytes)
-    fill_chunks(chunks, tensors)
-    up = ChunkedUploader(chunks, dests, device, n_slots=n_slots)
+    if not staged:
+        fill_chunks(chunks, tensors)
+    up = ChunkedUploader(chunks, dests, device, n_slots=n_slots, sources=tensors, n_host=n_host)
     try:
         up.upload()
         current_stream(device).synchronize()

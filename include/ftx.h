@@ -30,10 +30,14 @@ extern "C" {
 #define FTX_ERR_UNSUPPORTED 4 /* request not possible for this memory/device */
 
 /* ---- copy engines ------------------------------------------------------ */
-/* FTX_COPY_SDMA is hipMemcpyAsync: the HIP runtime picks its engine (an SDMA
- * queue or its own blit kernel; the ROCm 7 runtime used with PyTorch runs
- * pinned host-to-device copies as a blit kernel). Copies may be split over
- * dedicated copy streams. FTX_COPY_KERNEL is this library's zero-copy kernel. */
+/* FTX_COPY_SDMA is hipMemcpyAsync. From page-locked host memory the runtime
+ * hands the copy to an SDMA engine (traced as MEMORY_COPY_HOST_TO_DEVICE, no
+ * kernel dispatch), so it uses no CUs and does not slow kernels running
+ * beside it. Copies may be split over dedicated copy streams.
+ * FTX_COPY_KERNEL is this library's zero-copy kernel: CUs load from mapped
+ * host memory. It starts faster on small copies, but while it runs its
+ * outstanding host reads delay the memory accesses of other kernels on the
+ * same CUs, so FTX_COPY_AUTO keeps it to small chunks. */
 #define FTX_COPY_SDMA 0   /* hipMemcpyAsync, optionally split over copy streams   */
 #define FTX_COPY_KERNEL 1 /* zero-copy kernel: CUs read mapped pinned host memory */
 #define FTX_COPY_AUTO 2   /* pick per chunk from the policy set by ftx_set_copy_policy */

@@ -170,8 +170,9 @@ def test_fp8_llama_batch8_decode_matches_resident(gpu):
     mgr.release()
 
 
-@pytest.mark.parametrize("chunk_mib", [1, 4])
-def test_chunked_upload_bit_exact(gpu, chunk_mib):
+@pytest.mark.parametrize("chunk_mib,staged,n_host", [(1, False, 2), (4, False, 2), (1, True, 2), (1, True, 1),
+                                                     (4, True, 3)])
+def test_chunked_upload_bit_exact(gpu, chunk_mib, staged, n_host):
     from flextensor_amd.hip import checksum
     from flextensor_amd.scatter import upload_tensors
     from oracle import native as onat
@@ -184,7 +185,7 @@ def test_chunked_upload_bit_exact(gpu, chunk_mib):
         tensors.append(t.view(W.scatter_shape(n, i)))
     tensors.append(torch.arange(12, dtype=torch.float32).reshape(3, 4).t())  # Fortran layout
     tensors.append(torch.arange(20, dtype=torch.float32).reshape(4, 5)[:, ::2])  # gaps -> C-contiguous
-    out = upload_tensors(tensors, gpu, chunk_bytes=chunk_mib << 20)
+    out = upload_tensors(tensors, gpu, chunk_bytes=chunk_mib << 20, staged=staged, n_host=n_host)
     for src, dst in zip(tensors, out):
         assert dst.shape == src.shape and dst.dtype == src.dtype
         # compare bit patterns: random bf16 words include NaNs

@@ -81,3 +81,22 @@ def test_plan_rejects_impossible_budget():
     units = _mk([1000] * 4)
     with pytest.raises(ValueError, match="budget"):
         plan_streaming(units, [u.label for u in units], budget=1500, base_bytes=0, num_blocks=2)
+
+
+def test_copy_policy_from_measured_curves():
+    """The link sweep measured on the MI355X picks the kernel only for chunks up to 1 MiB."""
+    from flextensor_amd.link_model import CopyCurve, choose_copy_policy
+
+    gbps = {  # bench.py --link-sweep on the MI355X (GB/s per size)
+        "sdma": {65536: 5.06, 262144: 14.66, 1048576: 33.74, 2097152: 42.56, 4194304: 48.57, 16777216: 54.88,
+                 67108864: 56.67, 188743680: 57.09, 536870912: 57.24},
+        "kernel": {65536: 10.12, 262144: 25.8, 1048576: 43.62, 2097152: 43.33, 4194304: 49.96, 16777216: 55.24,
+                   67108864: 56.69, 188743680: 57.04, 536870912: 57.14},
+        "sdma_split2": {65536: 1.77, 262144: 4.35, 1048576: 19.76, 2097152: 28.45, 4194304: 38.51,
+                        16777216: 50.05, 67108864: 55.2, 188743680: 56.57, 536870912: 56.92},
+    }
+    curves = {e: CopyCurve(e, {n: n / (g * 1e9) * 1e3 for n, g in t.items()}) for e, t in gbps.items()}
+    kmax, split_min, n_streams = choose_copy_policy(curves["sdma"], curves["kernel"], curves["sdma_split2"], 2)
+    assert kmax == 1 << 20  # 2 MiB is only 2% faster on the kernel: not worth its cost to kernels beside it
+    assert split_min == 2**63 - 1 and n_streams == 1  # splitting never helps
+    assert choose_copy_policy(curves["sdma"], curves["kernel"], min_kernel_gain=1.0)[0] == 64 << 20
