@@ -416,6 +416,8 @@ def engine_contention() -> dict:
     * host-to-device GB/s of the zero-copy kernel by workgroup count (512 MiB);
     * scatter-kernel time alone, by wave-tile size, for the 512 MiB chunk of
       the 2000-tensor set that holds the most tensors;
+    * the same chunk as one descriptor into one buffer, and torch's device
+      copy of the same bytes (the plain-copy rate of this HBM);
     * the same scatter (default tile) launched on the compute stream while a
       512 MiB host-to-device copy runs on the transfer stream, per engine.
     """
@@ -463,6 +465,13 @@ def engine_contention() -> dict:
             plan = ScatterPlan(descs, tile)
             out["scatter_alone_us"][tile] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
             plan.close()
+        # the same bytes as one descriptor into one buffer, and torch's own device copy: the plain-copy rate
+        whole = torch.empty(n, dtype=torch.uint8, device=dev)
+        plan = ScatterPlan([(0, whole.data_ptr(), chunk.nbytes)])
+        out["scatter_one_descriptor_us"] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
+        plan.close()
+        out["torch_copy_us"] = round(1e3 * median_ms(lambda: whole[:chunk.nbytes].copy_(src[:chunk.nbytes]), comp, 10), 1)
+        del whole
         plan = ScatterPlan(descs)
         for label, mode, grid in (("hipMemcpyAsync", nat.COPY_SDMA, 0), ("kernel_grid_1024", nat.COPY_KERNEL, 1024),
                                   ("kernel_grid_64", nat.COPY_KERNEL, 64), ("kernel_grid_16", nat.COPY_KERNEL, 16),
