@@ -186,6 +186,83 @@ def bench_llama7b(budget_gb: float, prefill: int, decode: int, copy_engine: str)
     return out
 
 
+def bench_mlp(steps: int, copy_engine: str) -> dict:
+    """The 8-layer 4096->11008->4096 MLP stack, every layer streamed through a 2-slot ring.
+
+    Times ``steps`` eager streamed forwards, then the same forward captured in
+    a HIP graph and replayed ``steps`` times; both outputs are checked bitwise
+    against the all-resident forward. The CPU baseline is the same forward in
+    PyTorch on the host cores.
+    """
+    import torch
+
+    from flextensor_amd import workloads as W
+    from flextensor_amd.config import OffloadConfig
+    from flextensor_amd.manager import OffloadManager
+
+    dev = torch.device("cuda", 0)
+    model = W.build_mlp_stack(8, 4096, 11008, seed=0)
+    x = W.mlp_input(16, 4096, seed=0).to(dev)
+    resident = W.build_mlp_stack(8, 4096, 11008, seed=0).to(dev)
+    with torch.no_grad():
+        want = resident(x)
+    del resident
+    streamed_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    mgr = OffloadManager("bench-mlp")
+    mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                                     profiling_iters=1, copy_engine=copy_engine))
+    with torch.no_grad():
+        for _ in range(4):  # discovery, profiling, two streamed warm-up passes
+            out = model(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = model(x)
+        torch.cuda.synchronize()
+        t_eager = (time.perf_counter() - t0) / steps
+    eager_ok = bool(torch.equal(out, want))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.no_grad():
+        model(x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s), torch.no_grad():
+        static_out = model(x)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    t_graph = (time.perf_counter() - t0) / steps
+    graph_ok = bool(torch.equal(static_out, want))
+    del g, static_out
+    mgr.release(preserve_model=True)
+    # CPU baseline: the same forward in PyTorch on the host cores
+    xc = x.cpu()
+    with torch.no_grad():
+        for _ in range(2):
+            model(xc)
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            model(xc)
+            ts.append(time.perf_counter() - t0)
+    t_cpu = sorted(ts)[len(ts) // 2]
+    return {
+        "streamed_bytes_per_forward": streamed_bytes,
+        "eager_ms_per_forward": 1e3 * t_eager,
+        "eager_effective_GBps": streamed_bytes / t_eager / 1e9,
+        "graph_ms_per_forward": 1e3 * t_graph,
+        "graph_effective_GBps": streamed_bytes / t_graph / 1e9,
+        "bitwise_equal_to_resident": eager_ok and graph_ok,
+        "cpu_baseline": {"value": 1e3 * t_cpu, "unit": "ms per forward", "cores": torch.get_num_threads(),
+                         "kind": "pytorch_cpu_forward",
+                         "sample": "the full 8-layer bf16 forward on the host cores, median of 5"},
+    }
+
+
 def cpu_llama_decode_baseline(layers: int = 2, tokens: int = 4, context: int = 512) -> dict:
     """Batch-1 decode of ``layers`` 7B-shape decoder layers in PyTorch on the host cores, scaled to 32 layers."""
     import torch
@@ -519,6 +596,7 @@ def main() -> int:
     ap.add_argument("--engine-contention", action="store_true",
                     help="only print how each copy engine shares the GPU with the scatter kernel")
     ap.add_argument("--skip-dit", action="store_true")
+    ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--with-70b", action="store_true", help="also run the 80-layer fp8 70B-shape batch-8 decode")
     ap.add_argument("--layers-70b", type=int, default=80)
     ap.add_argument("--dit-tokens", type=int, default=32760)
@@ -613,6 +691,14 @@ def main() -> int:
                                                   if k != "traffic"}
             _log(f"traffic per scatter launch: {tr['traffic'] / 1e9:.3f} GB "
                  f"(algorithmic {line['roofline']['algorithmic_bytes_per_launch'] / 1e9:.3f} GB)")
+    if not args.skip_mlp:
+        gc.collect()
+        torch.cuda.empty_cache()
+        line["mlp8"] = bench_mlp(args.steps * 4, args.copy_engine)
+        _log(f"mlp8: {line['mlp8']}")
+        if not line["mlp8"]["bitwise_equal_to_resident"]:
+            print("bench: the streamed MLP forward differs from the resident forward", file=sys.stderr)
+            return 1
     if not args.skip_llama:
         gc.collect()
         torch.cuda.empty_cache()

@@ -528,6 +528,9 @@ class OffloadManager:
         if self.phase == OffloadPhase.INFERENCE:
             self.loader.enter(label)
             return
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"offload manager {self.name!r} is in {self.phase.value}: run the discovery and "
+                               "profiling passes eagerly before capturing a graph")
         if label in self._seen_this_pass:
             raise NotImplementedError(f"offload unit {label!r} ran twice in one forward")
         self._seen_this_pass.append(label)
@@ -552,13 +555,25 @@ class OffloadManager:
             p.data = self._cpu_data.pop(id(p))
 
     def _before_forward(self) -> None:
-        """Bound the host's run-ahead: wait for the pass ``max_inflight_passes`` back."""
+        """Bound the host's run-ahead: wait for the pass ``max_inflight_passes`` back.
+
+        Under graph capture nothing is waited for: a captured pass is one
+        fork/join region of the capturing stream, and replays are ordered by
+        the stream they are launched on.
+        """
+        if torch.cuda.is_current_stream_capturing():
+            if self.phase == OffloadPhase.INFERENCE and self.timing is not None and self.timing.enabled:
+                raise RuntimeError("offload_timing='eager' records host-read events and cannot be captured; "
+                                   "capture with offload_timing='off'")
+            return
         k = self.config.max_inflight_passes
         if self.phase == OffloadPhase.INFERENCE and k > 0 and len(self._pass_done) >= k:
             self._pass_done[-k].synchronize()
 
     def _after_forward(self) -> None:
         if self.phase == OffloadPhase.INFERENCE:
+            if torch.cuda.is_current_stream_capturing():
+                return
             if self.config.max_inflight_passes > 0:
                 from .hip import HipEvent, current_stream
 

@@ -1,0 +1,104 @@
+"""Streamed forwards captured in a HIP graph and replayed.
+
+Mirrors the reference's CUDA-graph suite (tests/integration/L0_cuda_graphs/
+test_cuda_graphs.py:1-30, 208-233): capture during INFERENCE after eager
+discovery and profiling; every replay bitwise equal to the eager resident
+forward; replays with new static inputs; eager streamed passes between
+replays keep working. Each replay is checked, with eager work and
+synchronizations in between.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from flextensor_amd import workloads as W
+from flextensor_amd.config import OffloadConfig
+from flextensor_amd.manager import OffloadManager, OffloadPhase
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(gpu, n_layers, budget_layers, seed, transfer_mode="allocation_block_transfer"):
+    model = W.build_mlp_stack(n_layers, 256, 704, seed=seed)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, transfer_mode=transfer_mode,
+                        max_gpu_mem_bytes=None if budget_layers is None else budget_layers * layer)
+    mgr = OffloadManager(name=f"graph-{seed}-{budget_layers}-{transfer_mode}")
+    mgr.offload(model, cfg)
+    return model, resident, mgr
+
+
+def _capture(model, static_x, feedback=2, warmup=3):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.no_grad():
+        for _ in range(warmup):
+            out = static_x
+            for _ in range(feedback):
+                out = model(out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s), torch.no_grad():
+        out = static_x
+        for _ in range(feedback):
+            out = model(out)
+    return g, out
+
+
+def _resident_feedback(resident, x, feedback=2):
+    with torch.no_grad():
+        out = x
+        for _ in range(feedback):
+            out = resident(out)
+    return out
+
+
+@pytest.mark.parametrize("budget_layers,transfer_mode", [(None, "allocation_block_transfer"),
+                                                         (None, "raw_block_transfer"),
+                                                         (5, "allocation_block_transfer")])
+def test_graph_replays_match_resident(gpu, budget_layers, transfer_mode):
+    model, resident, mgr = _setup(gpu, 8, budget_layers, seed=21, transfer_mode=transfer_mode)
+    x = W.mlp_input(16, 256, seed=21).to(gpu)
+    with torch.no_grad():
+        for _ in range(3):  # discovery, profiling, first streamed pass (eager)
+            model(x)
+    assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.streamed
+    if budget_layers is not None:
+        assert mgr.plan.resident and mgr.plan.reordered
+
+    static_x = x.clone()
+    g, static_out = _capture(model, static_x)
+    want = _resident_feedback(resident, static_x)
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, want), f"replay {i}"
+        with torch.no_grad():  # eager streamed work between replays
+            assert torch.equal(_resident_feedback(model, x), _resident_feedback(resident, x))
+        torch.cuda.synchronize()
+
+    static_x.copy_(W.mlp_input(16, 256, seed=22).to(gpu))  # new input, same graph
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static_out, _resident_feedback(resident, static_x))
+    del g
+    mgr.release()
+
+
+def test_capture_before_inference_is_refused(gpu, monkeypatch):
+    """The guard fires before any device work, so it is tested without driving a real capture into an error."""
+    model, _, mgr = _setup(gpu, 4, None, seed=23)
+    x = W.mlp_input(4, 256, seed=23).to(gpu)
+    assert mgr.phase == OffloadPhase.DISCOVERY
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="discovery"):
+        with torch.no_grad():
+            model(x)
+    monkeypatch.undo()
+    mgr.release()
