@@ -90,6 +90,8 @@ _SIGNATURES: dict[str, list] = {
     "ftx_event_create": [_uint, ctypes.POINTER(_vp)],
     "ftx_event_destroy": [_vp],
     "ftx_event_record": [_vp, _vp],
+    "ftx_timestamp": [_vp, _vp],
+    "ftx_wall_clock_khz": [ctypes.POINTER(ctypes.c_int)],
     "ftx_stream_wait_event": [_vp, _vp],
     "ftx_event_query": [_vp, ctypes.POINTER(_int)],
     "ftx_event_synchronize": [_vp],

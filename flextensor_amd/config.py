@@ -38,7 +38,7 @@ class OffloadConfig(BaseModel):
     min_blocks: int = Field(default=4, ge=2)
     max_gpu_mem_fraction: float | None = Field(default=None, gt=0.0, le=1.0)
     max_gpu_mem_bytes: int | None = Field(default=None, gt=0)
-    offload_timing: Literal["off", "eager"] = "off"
+    offload_timing: Literal["off", "eager", "cuda_graph"] = "off"
     piecewise_prefetch: Literal["off", "warn", "error"] = "warn"
     include_patterns: list[str] = Field(default_factory=lambda: ["*"])
     exclude_patterns: list[str] = Field(default_factory=list)

@@ -13,6 +13,8 @@
 //                        streamed bytes at full size without a host copy.
 //  * fill_kernel       - byte fill (memset replacement that is safe to
 //                        capture in a graph).
+//  * timestamp_kernel  - writes the wall clock to device memory; the timing
+//                        points of captured graphs.
 //
 // None of these kernels has data reuse, so blockIdx is mapped linearly: the
 // round-robin dispatch over the 8 XCDs only spreads independent tiles.
@@ -85,6 +87,7 @@ __global__ __launch_bounds__(kThreads) void zero_copy_kernel(uint8_t *__restrict
 typedef __attribute__((address_space(1))) u32x4 g_u32x4;
 typedef __attribute__((address_space(1))) uint32_t g_u32;
 typedef __attribute__((address_space(1))) uint8_t g_u8;
+typedef __attribute__((address_space(1))) uint64_t g_u64;
 
 template <typename T>
 __device__ __forceinline__ T *as_global(const void *p) {
@@ -222,7 +225,17 @@ __global__ __launch_bounds__(kThreads) void fill_kernel(uint8_t *__restrict__ p,
   for (uint64_t i = tid; i < n16; i += stride) d[i] = vv;
 }
 
+// One lane writes the constant-rate wall clock (a vector store).
+__global__ __launch_bounds__(kWave) void timestamp_kernel(uint64_t *__restrict__ slot) {
+  if (threadIdx.x == 0) *as_global<g_u64>(slot) = static_cast<uint64_t>(wall_clock64());
+}
+
 }  // namespace
+
+hipError_t launch_timestamp(uint64_t *slot, hipStream_t stream) {
+  hipLaunchKernelGGL(timestamp_kernel, dim3(1), dim3(kWave), 0, stream, slot);
+  return hipGetLastError();
+}
 
 hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid,
                             hipStream_t stream) {

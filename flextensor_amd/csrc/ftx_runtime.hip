@@ -514,6 +514,23 @@ int ftx_event_record(void *event, void *stream) {
   return FTX_OK;
 }
 
+int ftx_timestamp(void *dev_slot, void *stream) {
+  if (!dev_slot) return ftx::fail(FTX_ERR_INVALID, "timestamp slot is null");
+  if (reinterpret_cast<uintptr_t>(dev_slot) % 8) return ftx::fail(FTX_ERR_INVALID, "timestamp slot is not 8-byte aligned");
+  int rc = ftx::check_device_range(dev_slot, 8, "timestamp slot");
+  if (rc != FTX_OK) return rc;
+  FTX_HIP(ftx::launch_timestamp(static_cast<uint64_t *>(dev_slot), static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
+int ftx_wall_clock_khz(int *khz) {
+  if (!khz) return ftx::fail(FTX_ERR_INVALID, "khz is null");
+  int dev = 0;
+  FTX_HIP(hipGetDevice(&dev));
+  FTX_HIP(hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev));
+  return FTX_OK;
+}
+
 int ftx_stream_wait_event(void *stream, void *event) {
   if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
   FTX_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0));

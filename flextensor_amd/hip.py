@@ -72,6 +72,53 @@ class HipEvent:
             pass  # interpreter shutdown: module globals are already gone; the process frees the handle
 
 
+class DeviceClock:
+    """A device array of wall-clock timestamps written by ``ftx_timestamp``.
+
+    Its events are kernel launches, so a graph that captures them writes new
+    times on every replay. :meth:`refresh` copies the array to the host once
+    the device is idle; elapsed times are then read from that copy.
+    """
+
+    def __init__(self, n: int, device: torch.device | int | None = None) -> None:
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        self.buf = torch.zeros(max(1, n), dtype=torch.int64, device=dev)
+        self.host: list[int] = [0] * max(1, n)
+        khz = ctypes.c_int(0)
+        nat.call("ftx_wall_clock_khz", ctypes.byref(khz))
+        if khz.value <= 0:
+            raise RuntimeError("the device reports no wall-clock rate")
+        self.ticks_per_ms = float(khz.value)
+        self._next = 0
+
+    def event(self) -> "ClockEvent":
+        if self._next >= self.buf.numel():
+            raise RuntimeError(f"device clock has only {self.buf.numel()} slots")
+        self._next += 1
+        return ClockEvent(self, self._next - 1)
+
+    def refresh(self) -> None:
+        self.host = self.buf.cpu().tolist()
+
+
+class ClockEvent:
+    """One timestamp slot of a :class:`DeviceClock`, with the ``record`` / ``elapsed_time`` of an event."""
+
+    __slots__ = ("clock", "index")
+
+    def __init__(self, clock: DeviceClock, index: int) -> None:
+        self.clock, self.index = clock, index
+
+    def record(self, stream: "HipStream | None" = None) -> "ClockEvent":
+        s = stream if stream is not None else current_stream()
+        nat.call("ftx_timestamp", self.clock.buf.data_ptr() + 8 * self.index, s.handle)
+        return self
+
+    def elapsed_time(self, end: "ClockEvent") -> float:
+        h = self.clock.host
+        return (h[end.index] - h[self.index]) / self.clock.ticks_per_ms
+
+
 class HipStream:
     """A HIP stream. ``torch_stream`` keeps the owning torch object alive."""
 
@@ -83,9 +130,7 @@ class HipStream:
         self.name = name
 
     def record_event(self, event: HipEvent | None = None) -> HipEvent:
-        ev = event if event is not None else HipEvent()
-        nat.call("ftx_event_record", ev.handle, self.handle)
-        return ev
+        return (event if event is not None else HipEvent()).record(self)
 
     def wait_event(self, event: HipEvent) -> None:
         nat.call("ftx_stream_wait_event", self.handle, event.handle)
@@ -109,6 +154,11 @@ class HipStream:
 
     def __repr__(self) -> str:
         return f"HipStream({self.name or hex(self.handle)})"
+
+
+def is_capturing() -> bool:
+    """Whether torch's current stream is capturing a graph (False without a GPU)."""
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
 
 
 def current_stream(device: torch.device | int | None = None) -> HipStream:

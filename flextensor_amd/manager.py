@@ -38,6 +38,7 @@ import torch
 from torch import nn
 
 from . import _native as nat
+from . import custom_ops, hip
 from .allocation_block import HostPinner
 from .config import OffloadConfig
 from .controllers import AllocationBlockController, RawBlockController
@@ -337,6 +338,7 @@ class OffloadManager:
         self.model = model
         self.units = units
         self._place_outside_units(unit_params)
+        custom_ops.register_manager(id(self), self)
         for u in self.units:
             self._patch(u)
         self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
@@ -444,6 +446,7 @@ class OffloadManager:
         if self.model is None:
             return
         torch.cuda.synchronize(self.device)
+        custom_ops.unregister_manager(id(self))
         for h in self._hooks:
             h.remove()
         for mod, orig in self._patched:
@@ -506,10 +509,29 @@ class OffloadManager:
         return sum(t.numel() * t.element_size() for t in cpu)
 
     def _patch(self, unit: _Unit) -> None:
+        """Wrap the unit's forward in enter/exit (offload_manager.py:1136-1162).
+
+        Eagerly the manager is called directly. Under ``torch.compile`` the
+        calls go through the ``flextensor::pre_compute`` / ``post_compute``
+        custom ops, which the compiler keeps in place around the unit's
+        compute (custom_ops.py:267-328).
+        """
         orig = unit.module.forward
-        mgr, label = self, unit.label
+        mgr, label, mid = self, unit.label, id(self)
 
         def forward(*args: Any, **kwargs: Any) -> Any:
+            if torch.compiler.is_compiling():
+                if mgr.phase != OffloadPhase.INFERENCE:
+                    raise RuntimeError(f"offload manager {mgr.name!r} is in {mgr.phase.value}: run the discovery and "
+                                       "profiling passes eagerly, then compile")
+                carrier = custom_ops.first_tensor((args, kwargs))
+                if carrier is None:
+                    raise RuntimeError(f"offload unit {label!r} has no tensor input to order its transfers against")
+                torch.ops.flextensor.pre_compute(carrier, label, mid)
+                out = orig(*args, **kwargs)
+                produced = custom_ops.first_tensor(out)
+                torch.ops.flextensor.post_compute(produced if produced is not None else carrier, label, mid)
+                return out
             mgr._enter(label)
             out = orig(*args, **kwargs)
             mgr._exit(label)
@@ -528,7 +550,7 @@ class OffloadManager:
         if self.phase == OffloadPhase.INFERENCE:
             self.loader.enter(label)
             return
-        if torch.cuda.is_current_stream_capturing():
+        if hip.is_capturing():
             raise RuntimeError(f"offload manager {self.name!r} is in {self.phase.value}: run the discovery and "
                                "profiling passes eagerly before capturing a graph")
         if label in self._seen_this_pass:
@@ -559,20 +581,30 @@ class OffloadManager:
 
         Under graph capture nothing is waited for: a captured pass is one
         fork/join region of the capturing stream, and replays are ordered by
-        the stream they are launched on.
+        the stream they are launched on. A compiled forward skips this host
+        bookkeeping (it must not enter the traced graph); its units' traps
+        run as custom ops.
         """
-        if torch.cuda.is_current_stream_capturing():
-            if self.phase == OffloadPhase.INFERENCE and self.timing is not None and self.timing.enabled:
-                raise RuntimeError("offload_timing='eager' records host-read events and cannot be captured; "
-                                   "capture with offload_timing='off'")
+        if torch.compiler.is_compiling():
+            return
+        if hip.is_capturing():
+            if self.phase == OffloadPhase.INFERENCE and self.timing is not None and self.timing.enabled \
+                    and not self.timing.graph_replay:
+                raise RuntimeError("offload_timing='eager' cannot time a captured graph; "
+                                   "capture with offload_timing='cuda_graph' or 'off'")
             return
         k = self.config.max_inflight_passes
         if self.phase == OffloadPhase.INFERENCE and k > 0 and len(self._pass_done) >= k:
             self._pass_done[-k].synchronize()
 
     def _after_forward(self) -> None:
+        if torch.compiler.is_compiling():
+            if self.phase != OffloadPhase.INFERENCE:
+                raise RuntimeError(f"offload manager {self.name!r} is in {self.phase.value}: run the discovery and "
+                                   "profiling passes eagerly, then compile")
+            return
         if self.phase == OffloadPhase.INFERENCE:
-            if torch.cuda.is_current_stream_capturing():
+            if hip.is_capturing():
                 return
             if self.config.max_inflight_passes > 0:
                 from .hip import HipEvent, current_stream
@@ -644,7 +676,8 @@ class OffloadManager:
                 tensors_map[tid].data = view
             reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"
             cls = PreallocatedBatchTransferTensorLoaderReordered if reordered else PreallocatedBatchTransferTensorLoader
-            self.timing = OffloadTimingCollector(order, enabled=cfg.offload_timing == "eager")
+            self.timing = OffloadTimingCollector(order, enabled=cfg.offload_timing != "off",
+                                                 graph_replay=cfg.offload_timing == "cuda_graph")
             policy = PiecewisePrefetchPolicy(enabled=cfg.piecewise_prefetch != "off",
                                              strict=cfg.piecewise_prefetch == "error")
             self.loader = cls(layer_stats, self.device, bd.label_to_block_id, bd.transfer_to_compute_map,

@@ -132,8 +132,18 @@ class OffloadTimingCollector:
         synchronize: Callable[[], None] | None = None,
         on_pass: Callable[[OffloadTimingSnapshot], None] | None = None,
         max_passes: int = 1024,
+        graph_replay: bool = False,
+        is_capturing: Callable[[], bool] | None = None,
     ) -> None:
+        """``graph_replay``: timing points are device timestamps written by
+        kernels, so a captured pass is re-timed by every replay and
+        :meth:`report` after a replay reads that replay (the role of the
+        reference's external events, offload_timing.py:319-352). Read only
+        after a replay: before the first one the slots hold no captured times."""
         self.enabled = enabled
+        self.graph_replay = graph_replay
+        self._in_capture = False
+        self._capture_done: dict[str, set[str]] | None = None
         self._labels = list(trap_labels or [])
         self._label_set = set(self._labels) if enabled else set()
         self._on_pass = on_pass
@@ -144,14 +154,21 @@ class OffloadTimingCollector:
         self._done: dict[str, set[str]] = {"transfer": set(), "compute": set(), "wait": set()}
         if not enabled:
             return
-        if event_factory is None or current_stream is None or synchronize is None:
+        self._clock = None
+        if event_factory is None or current_stream is None or synchronize is None or is_capturing is None:
             from . import hip
 
+            if event_factory is None and graph_replay:
+                # timestamps written by kernels: a captured pass is re-timed by every replay
+                self._clock = hip.DeviceClock(6 * len(self._labels))
+                event_factory = self._clock.event
             event_factory = event_factory or (lambda: hip.HipEvent(timing=True))
             current_stream = current_stream or hip.current_stream
             synchronize = synchronize or (lambda: hip.nat.call("ftx_device_synchronize"))
+            is_capturing = is_capturing or hip.is_capturing
         self._current_stream = current_stream
         self._synchronize = synchronize
+        self._is_capturing = is_capturing
         for label in self._labels:
             self._events[label] = {k: event_factory() for k in ("ts", "te", "cs", "ce", "ws", "we")}
 
@@ -191,25 +208,57 @@ class OffloadTimingCollector:
     def on_pass_start(self) -> None:
         if not self.enabled:
             return
+        if self._is_capturing():
+            if not self.graph_replay:
+                raise RuntimeError("offload_timing='eager' cannot time a captured graph; use 'cuda_graph'")
+            # events are only read after a replay; a pending eager pass is dropped
+            for s in self._done.values():
+                s.clear()
+            self._pass_active = True
+            self._in_capture = True
+            return
+        self._end_capture()
         if self._pass_active:
             self._finalize()
         self._pass_active = True
 
-    def flush(self) -> bool:
-        """Publish a pending pass (the newest pass is otherwise only finalized by the next one)."""
-        if not self.enabled or not self._pass_active:
-            return False
-        self._finalize()
-        return True
+    def _end_capture(self) -> None:
+        """After a capture: keep which events the captured pass records, for reading replays."""
+        if self._in_capture and not self._is_capturing():
+            self._capture_done = {k: set(v) for k, v in self._done.items()}
+            for s in self._done.values():
+                s.clear()
+            self._in_capture = False
+            self._pass_active = False
 
-    def _finalize(self) -> None:
+    def flush(self) -> bool:
+        """Publish a pending pass (the newest pass is otherwise only finalized by the next one).
+
+        With no eager pass pending after a graph was captured, the events of
+        the latest replay are read instead.
+        """
+        if not self.enabled or self._is_capturing():
+            return False
+        self._end_capture()
+        if self._pass_active:
+            self._finalize()
+            return True
+        if self._capture_done is not None:
+            self._finalize(self._capture_done)
+            return True
+        return False
+
+    def _finalize(self, done: dict[str, set[str]] | None = None) -> None:
         self._synchronize()
+        if self._clock is not None:
+            self._clock.refresh()
+        done = self._done if done is None else done
         recs = []
         for label in self._labels:
             ev = self._events[label]
-            t = ev["ts"].elapsed_time(ev["te"]) if label in self._done["transfer"] else 0.0
-            c = ev["cs"].elapsed_time(ev["ce"]) if label in self._done["compute"] else 0.0
-            w = ev["ws"].elapsed_time(ev["we"]) if label in self._done["wait"] else 0.0
+            t = ev["ts"].elapsed_time(ev["te"]) if label in done["transfer"] else 0.0
+            c = ev["cs"].elapsed_time(ev["ce"]) if label in done["compute"] else 0.0
+            w = ev["ws"].elapsed_time(ev["we"]) if label in done["wait"] else 0.0
             recs.append(TrapTimingRecord(label, t, c, w))
         for s in self._done.values():
             s.clear()
@@ -225,7 +274,10 @@ class OffloadTimingCollector:
         return OffloadTimingReport(list(self.snapshots))
 
     def reset(self) -> None:
+        """Drop published passes and a pending eager pass; a captured pass stays readable after replays."""
         self.snapshots.clear()
+        if self._in_capture:
+            return  # _done holds what the captured pass records
         for s in self._done.values():
             s.clear()
         self._pass_active = False

@@ -109,6 +109,14 @@ int ftx_stream_query(void *stream, int *done);
 int ftx_event_create(unsigned flags, void **event);
 int ftx_event_destroy(void *event);
 int ftx_event_record(void *event, void *stream);
+/* Device timestamps for timing captured graphs: writes the GPU's constant-rate
+ * wall clock into dev_slot (8 bytes of device memory) when the stream reaches
+ * it. Captured in a graph it is a kernel node, so every replay writes a new
+ * time. Replaces torch.cuda.Event(external=True).record() of the graph-replay
+ * timing mode (offload_timing.py:319-352); ticks per millisecond come from
+ * ftx_wall_clock_khz. */
+int ftx_timestamp(void *dev_slot, void *stream);
+int ftx_wall_clock_khz(int *khz);
 int ftx_stream_wait_event(void *stream, void *event);
 int ftx_event_query(void *event, int *done);
 int ftx_event_synchronize(void *event);

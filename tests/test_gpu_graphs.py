@@ -102,3 +102,49 @@ def test_capture_before_inference_is_refused(gpu, monkeypatch):
             model(x)
     monkeypatch.undo()
     mgr.release()
+
+
+@pytest.mark.parametrize("budget_layers", [None, 5])
+def test_compiled_streamed_forward_matches_resident(gpu, budget_layers):
+    """torch.compile (aot_eager: no code generation) keeps the streaming traps as custom ops."""
+    torch._dynamo.reset()
+    model, resident, mgr = _setup(gpu, 8, budget_layers, seed=31)
+    x = W.mlp_input(16, 256, seed=31).to(gpu)
+    with torch.no_grad():
+        for _ in range(3):
+            model(x)
+    assert mgr.phase == OffloadPhase.INFERENCE
+    compiled = torch.compile(model, backend="aot_eager", fullgraph=True)
+    want = _resident_feedback(resident, x)
+    with torch.no_grad():
+        for _ in range(3):
+            assert torch.equal(_resident_feedback(compiled, x), want)
+    torch.cuda.synchronize()
+    torch._dynamo.reset()
+    mgr.release()
+
+
+def test_graph_replay_timing(gpu):
+    """offload_timing='cuda_graph': every replay re-times the captured pass (external event nodes)."""
+    model = W.build_mlp_stack(6, 512, 1408, seed=41)
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, offload_timing="cuda_graph")
+    mgr = OffloadManager(name="graph-timing")
+    mgr.offload(model, cfg)
+    x = W.mlp_input(64, 512, seed=41).to(gpu)
+    with torch.no_grad():
+        for _ in range(3):
+            model(x)
+    mgr.reset_offload_timing()
+    g, out = _capture(model, x.clone(), feedback=1, warmup=1)
+    mgr.reset_offload_timing()  # drops the eager passes; the captured pass is not a timed pass itself
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        rep = mgr.collect_offload_timing()  # reads the replay that just ran
+        assert rep.num_passes == i + 1
+        snap = rep.snapshots[-1]
+        assert snap.total_transfer_ms > 0 and snap.total_compute_ms > 0
+        assert 0.0 <= rep.hidden_fraction <= 1.0
+    del g
+    mgr.release()

@@ -216,3 +216,36 @@ def test_arena_freed_by_refcount_when_last_view_dies(gpu):
             nat.host_device_ptr(ptr)
     finally:
         gc.enable()
+
+
+def test_device_clock_agrees_with_hip_events(gpu):
+    """ftx_timestamp: kernel-written wall-clock stamps time the same span as hipEvents."""
+    from flextensor_amd.hip import DeviceClock, HipEvent, current_stream
+
+    clock = DeviceClock(2, gpu)
+    a, b = clock.event(), clock.event()
+    e0, e1 = HipEvent(True), HipEvent(True)
+    s = current_stream(gpu)
+    x = torch.randn(4096, 4096, device=gpu, dtype=torch.bfloat16)
+    torch.matmul(x, x)
+    torch.cuda.synchronize()
+    a.record(s)
+    e0.record(s)
+    for _ in range(20):
+        torch.matmul(x, x)
+    e1.record(s)
+    b.record(s)
+    torch.cuda.synchronize()
+    clock.refresh()
+    ms_clock, ms_event = a.elapsed_time(b), e0.elapsed_time(e1)
+    assert ms_event > 0.5
+    assert abs(ms_clock - ms_event) <= 0.05 * ms_event + 0.05
+
+
+def test_timestamp_rejects_host_slot(gpu):
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import current_stream
+
+    host = torch.zeros(2, dtype=torch.int64)
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_timestamp", host.data_ptr(), current_stream(gpu).handle)

@@ -330,3 +330,72 @@ def test_timing_hooks_pair_up(kind):
         starts = [i for i, c in enumerate(calls) if c == f"record_{col}_start"]
         ends = [i for i, c in enumerate(calls) if c == f"record_{col}_end"]
         assert len(starts) == len(ends) > 0 and all(s < e for s, e in zip(starts, ends))
+
+
+class _ClockEvent:
+    """Fake timing event: ``record`` stamps the fake clock; a replay re-stamps through ``clock``."""
+
+    def __init__(self, clock):
+        self.clock, self.t = clock, None
+
+    def record(self, stream=None):
+        self.t = self.clock["now"]
+        self.clock["now"] += self.clock["step"]
+        self.clock["recorded"].append(self)
+        return self
+
+    def elapsed_time(self, end):
+        return end.t - self.t
+
+
+def _graph_collector(capturing):
+    clock = {"now": 0.0, "step": 1.0, "recorded": []}
+    col = OffloadTimingCollector(["L0", "L1"], event_factory=lambda: _ClockEvent(clock), current_stream=lambda: None,
+                                 synchronize=lambda: None, graph_replay=True, is_capturing=lambda: capturing["on"])
+    return col, clock
+
+
+def _timed_pass(col):
+    col.on_pass_start()
+    for label in ("L0", "L1"):
+        col.record_transfer_start(label, None)
+        col.record_transfer_end(label, None)
+        col.record_compute_start(label)
+        col.record_compute_end(label)
+        col.record_wait_start(label)
+        col.record_wait_end(label)
+
+
+def test_graph_replay_timing_reads_each_replay():
+    """offload_timing.py:319-352: a captured pass is timed by every replay, read after it."""
+    capturing = {"on": False}
+    col, clock = _graph_collector(capturing)
+    _timed_pass(col)  # eager pass
+    capturing["on"] = True
+    _timed_pass(col)  # the captured pass: recorded once, read never
+    assert col.flush() is False and col.snapshots == []
+    capturing["on"] = False
+    captured = list(clock["recorded"][-12:])
+    for step in (2.0, 5.0):  # two replays: each re-records the captured events with new times
+        clock["step"] = step
+        for ev in captured:
+            ev.record()
+        assert col.flush() is True
+        snap = col.snapshots[-1]
+        assert [r.transfer_ms for r in snap.per_trap] == [step, step]
+        assert [r.wait_ms for r in snap.per_trap] == [step, step]
+    assert len(col.snapshots) == 2  # the eager pass before the capture was dropped, not mixed in
+    clock["step"] = 3.0
+    _timed_pass(col)  # eager work after the replays is timed as usual
+    clock["step"] = 1.0
+    _timed_pass(col)  # its start publishes the previous eager pass
+    assert len(col.snapshots) == 3 and col.snapshots[-1].per_trap[0].compute_ms == 3.0
+
+
+def test_eager_timing_refuses_capture():
+    capturing = {"on": True}
+    clock = {"now": 0.0, "step": 1.0, "recorded": []}
+    col = OffloadTimingCollector(["L0"], event_factory=lambda: _ClockEvent(clock), current_stream=lambda: None,
+                                 synchronize=lambda: None, is_capturing=lambda: capturing["on"])
+    with pytest.raises(RuntimeError, match="cuda_graph"):
+        col.on_pass_start()
