@@ -421,6 +421,34 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
     return out
 
 
+def cpu_llama70b_decode_baseline(batch: int = 8, context: int = 64, steps: int = 2) -> dict:
+    """Batch decode of one 70B-shape layer in PyTorch on the host cores, scaled to 80 layers.
+
+    torch has no fp8 GEMM on the CPU, so the layer holds bf16 weights, which
+    is what dequantizing the fp8 weights on the host gives.
+    """
+    import torch
+
+    from flextensor_amd import workloads as W
+
+    s = W.LlamaShape(**{**W.LLAMA_70B_FP8.__dict__, "n_layers": 1, "vocab": 256, "fp8": False,
+                        "max_seq": context + steps + 4})
+    model = W.build_llama(s, seed=3)
+    model.init_cache(batch, context + steps + 4, torch.device("cpu"))
+    layer = model.layers[0]
+    x = torch.randn(batch, 1, s.hidden, dtype=torch.bfloat16)
+    with torch.no_grad():
+        layer(x, context, model.rope_cos, model.rope_sin, model.cache_k[0], model.cache_v[0])  # warm-up
+        t0 = time.perf_counter()
+        for i in range(steps):
+            layer(x, context + 1 + i, model.rope_cos, model.rope_sin, model.cache_k[0], model.cache_v[0])
+        per_layer = (time.perf_counter() - t0) / steps
+    per_step = per_layer * W.LLAMA_70B_FP8.n_layers
+    return {"value": batch / per_step, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "pytorch_cpu_forward",
+            "sample": f"PyTorch bf16 (fp8 dequantized) batch-{batch} decode of one 70B-shape layer x {steps} steps "
+                      f"at context {context}, scaled linearly to 80 layers"}
+
+
 def measure_traffic(args) -> dict | None:
     """HBM bytes per scatter launch from two ``rocprofv3 --pmc`` child runs.
 
@@ -597,7 +625,7 @@ def main() -> int:
                     help="only print how each copy engine shares the GPU with the scatter kernel")
     ap.add_argument("--skip-dit", action="store_true")
     ap.add_argument("--skip-mlp", action="store_true")
-    ap.add_argument("--with-70b", action="store_true", help="also run the 80-layer fp8 70B-shape batch-8 decode")
+    ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
     ap.add_argument("--layers-70b", type=int, default=80)
     ap.add_argument("--dit-tokens", type=int, default=32760)
     ap.add_argument("--dit-steps", type=int, default=2)
@@ -712,10 +740,12 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["dit"] = bench_dit(12.0, args.dit_tokens, 512, args.dit_steps)
         _log(f"dit: {line['dit']}")
-    if args.with_70b:
+    if not args.skip_70b:
         gc.collect()
         torch.cuda.empty_cache()
         line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b)
+        if not args.skip_cpu_baseline and "skipped" not in line["llama70b_fp8"]:
+            line["llama70b_fp8"]["cpu_baseline"] = cpu_llama70b_decode_baseline()
         _log(f"70b: {line['llama70b_fp8']}")
     print(json.dumps(line), flush=True)
     return 0
