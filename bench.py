@@ -421,6 +421,94 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
     return out
 
 
+def bench_fp8_linear(batch: int = 8, reps: int = 40) -> dict:
+    """HBM roofline of the fp8-weight MFMA linear on the 70B-shape decode projections.
+
+    One call per projection of a decoder layer (q, k, v, o, gate, up, down) at
+    ``batch`` activation rows. Algorithmic bytes per call = fp8 weights (n*k) +
+    bf16 activations (m*k*2) + bf16 outputs (m*n*2) + bf16 scales (n*2). The
+    time is GPU time per call: ``reps`` calls are captured in one HIP graph
+    and one replay is timed with HIP events on the replay stream, so host
+    overhead is excluded; a call is the main kernel plus, when K is split, the
+    reduce kernel. The dequantize-then-bf16-GEMM forward it replaces is timed
+    beside it (eager, same events).
+    """
+    import torch
+    import torch.nn.functional as F
+
+    from flextensor_amd import hip
+    from flextensor_amd import workloads as W
+
+    s = W.LLAMA_70B_FP8
+    h, q, kv, it = s.hidden, s.n_heads * s.head_dim, s.n_kv_heads * s.head_dim, s.inter
+    projections = [("wq", q, h), ("wk", kv, h), ("wv", kv, h), ("wo", h, q), ("gate", it, h), ("up", it, h),
+                   ("down", h, it)]
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(3)
+
+    def timed_eager(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    def timed_graph(fn, n):
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(n):
+                    fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    rows, cache = [], {}
+    total_bytes = total_ms = total_dq_ms = 0.0
+    for name, n, k in projections:
+        if (n, k) not in cache:
+            x = torch.randn(batch, k, device=dev, generator=gen).to(torch.bfloat16)
+            w = (torch.randn(n, k, device=dev, generator=gen) * 64).clamp(-448, 448).to(torch.float8_e4m3fn)
+            sc = (torch.rand(n, device=dev, generator=gen) / 448).to(torch.bfloat16)
+            ms = timed_graph(lambda: hip.fp8_linear(x, w, sc), reps)
+            eager_ms = timed_eager(lambda: hip.fp8_linear(x, w, sc), reps)
+            dq_ms = timed_eager(lambda: F.linear(x, w.to(torch.bfloat16)) * sc, max(5, reps // 5))
+            want = (x.float() @ w.float().t()) * sc.float()
+            err = float((hip.fp8_linear(x, w, sc).float() - want).norm() / want.norm())
+            splits = hip.fp8_linear_workspace_bytes(batch, n, k) // (4 * batch * n) or 1
+            cache[(n, k)] = (ms, eager_ms, dq_ms, err, splits)
+            del x, w, sc, want
+        ms, eager_ms, dq_ms, err, splits = cache[(n, k)]
+        nbytes = n * k + batch * k * 2 + batch * n * 2 + n * 2
+        total_bytes += nbytes
+        total_ms += ms
+        total_dq_ms += dq_ms
+        rows.append({"proj": name, "n": n, "k": k, "k_slices": splits, "us": round(ms * 1e3, 2),
+                     "GBps": round(nbytes / ms / 1e6, 1), "eager_call_us": round(eager_ms * 1e3, 2),
+                     "dequant_gemm_us": round(dq_ms * 1e3, 2), "rel_err_vs_fp32": round(err, 5)})
+    achieved = total_bytes / total_ms / 1e6
+    return {"batch": batch, "projections": rows, "layer_us": round(total_ms * 1e3, 2),
+            "layer_dequant_gemm_us": round(total_dq_ms * 1e3, 2), "timing": "HIP graph of calls, one replay",
+            "roofline": {"kernel": "fp8_linear_kernel + fp8_linear_reduce_kernel", "bound": "hbm",
+                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_layer": int(total_bytes)}}
+
+
 def cpu_llama70b_decode_baseline(batch: int = 8, context: int = 64, steps: int = 2) -> dict:
     """Batch decode of one 70B-shape layer in PyTorch on the host cores, scaled to 80 layers.
 
@@ -626,6 +714,8 @@ def main() -> int:
     ap.add_argument("--skip-dit", action="store_true")
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
+    ap.add_argument("--fp8-linear-only", action="store_true",
+                    help="only print the fp8 linear roofline on the 70B-shape decode projections")
     ap.add_argument("--layers-70b", type=int, default=80)
     ap.add_argument("--dit-tokens", type=int, default=32760)
     ap.add_argument("--dit-steps", type=int, default=2)
@@ -649,6 +739,9 @@ def main() -> int:
         return traffic_probe(args)
     if args.engine_contention:
         print(json.dumps(engine_contention()), flush=True)
+        return 0
+    if args.fp8_linear_only:
+        print(json.dumps({"fp8_linear": bench_fp8_linear()}), flush=True)
         return 0
     if args.link_sweep:
         from flextensor_amd.link_model import choose_copy_policy, measure_copy_curve
@@ -743,6 +836,8 @@ def main() -> int:
     if not args.skip_70b:
         gc.collect()
         torch.cuda.empty_cache()
+        line["fp8_linear"] = bench_fp8_linear()
+        _log(f"fp8 linear: {line['fp8_linear']}")
         line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b)
         if not args.skip_cpu_baseline and "skipped" not in line["llama70b_fp8"]:
             line["llama70b_fp8"]["cpu_baseline"] = cpu_llama70b_decode_baseline()

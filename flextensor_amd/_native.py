@@ -105,6 +105,9 @@ _SIGNATURES: dict[str, list] = {
     "ftx_scatter_run": [_vp, _vp, _vp],
     "ftx_scatter": [_vp, ctypes.POINTER(FtxDesc), _int, _vp],
     "ftx_checksum64": [_vp, _sz, _vp, ctypes.POINTER(ctypes.c_uint64)],
+    "ftx_fp8_linear_workspace": [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(_sz)],
+    "ftx_fp8_linear": [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp, _sz, _vp],
+    "ftx_set_fp8_linear_config": [_int, _int],
 }
 
 _lib: ctypes.CDLL | None = None

@@ -1,0 +1,313 @@
+// fp8-weight linear layer for decode-sized batches, written for gfx950.
+//
+//   y[m, n] = bf16( scale[n] * sum_k x[m, k] * w[n, k] )
+//
+// x is bf16 [M, K], w is float8 e4m3fn [N, K] (row-major, K contiguous),
+// scale is one bf16 per output channel, y is bf16 [M, N]; M <= 64.
+//
+// Decode multiplies a few activation rows by a large weight matrix, so the
+// kernel is bound by reading the fp8 weights from HBM once (1 byte per
+// weight). Each lane loads 16 weight bytes of one row, converts them to bf16
+// in registers with v_cvt_scalef32_pk_bf16_fp8 (scale 1.0; every e4m3 value is
+// exact in bf16) and feeds v_mfma_f32_16x16x32_bf16 with the weights as the A
+// operand (16 output channels) and the activations as the B operand (16 batch
+// columns). The activations stay bf16, so the products are exactly those of
+// dequantizing the weights and running a bf16 GEMM; only the fp32
+// accumulation order differs.
+//
+// Work split: a workgroup owns 16*RT output channels; its S wavefronts split
+// K by 64*U-byte steps (wave w takes steps w, w+S, ...), so every wave streams
+// whole 16-byte pieces of RT*16 rows. The S partial tiles are summed in LDS in
+// wave order, so results do not depend on timing.
+//
+// MFMA 16x16x32 operand layout (gfx950): lane l supplies row/column l%16 and
+// the eight k values 8*(l/16)..8*(l/16)+7 of the 32-wide k block; lane l
+// receives D rows 4*(l/16)..4*(l/16)+3 of column l%16. Any permutation of k
+// that A and B share gives the same sum, so here lane group g = l/16 holds the
+// k values g*16..g*16+15 of a 64-byte piece: the first eight go to one MFMA,
+// the last eight to a second one.
+#include <algorithm>
+
+#include "ftx_internal.h"
+
+namespace ftx {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kPieceBytes = 16;              // fp8 bytes one lane loads per row and step
+constexpr int kStepBytes = 4 * kPieceBytes;  // K bytes one step covers per row (4 lane groups)
+
+__device__ __forceinline__ bf16x8 join8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) {
+  const bf16x4 lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+  const bf16x4 hi = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// 16 e4m3fn bytes -> bf16 of bytes 0-7 (lo) and bytes 8-15 (hi), in byte order.
+__device__ __forceinline__ void fp8x16_to_bf16(u32x4 w, bf16x8 &lo, bf16x8 &hi) {
+  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.0f, false);
+  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.0f, true);
+  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.0f, false);
+  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.0f, true);
+  const bf16x2 p4 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2], 1.0f, false);
+  const bf16x2 p5 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2], 1.0f, true);
+  const bf16x2 p6 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[3], 1.0f, false);
+  const bf16x2 p7 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[3], 1.0f, true);
+  lo = join8(p0, p1, p2, p3);
+  hi = join8(p4, p5, p6, p7);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Bytes of one weight row loaded per iteration: 16 lanes x 16 bytes, so one
+// load instruction covers 4 rows x 256 contiguous bytes. Fewer, longer runs
+// per instruction keep HBM near its streaming rate; the MFMA layout (16 rows
+// per 16 lanes, 64 bytes each) is reached through a per-wave LDS tile.
+constexpr int kIterK = 256;
+constexpr int kRowsPerLoad = kWave * kPieceBytes / kIterK;   // 4
+constexpr int kLoads = 16 / kRowsPerLoad;                     // 4 per 16 rows
+constexpr int kSteps = kIterK / kStepBytes;                   // 4 MFMA steps per iteration
+constexpr int kTileRow = kIterK + 16;                         // LDS bytes per staged row (+16: bank spread)
+constexpr int kTileBytes = 16 * kTileRow;                     // per wave
+
+// MB: 16-column batch blocks (M <= 16*MB). Workgroup b owns rows
+// [rg*16*S, rg*16*S + 16*S) (S waves, 16 rows each), rg = b / splits, and
+// the K slice [sp*Kc, min(K, (sp+1)*Kc)), sp = b % splits.
+template <int MB>
+__global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restrict__ x,
+                                                         const uint8_t *__restrict__ w,
+                                                         const uint16_t *__restrict__ scale,
+                                                         uint16_t *__restrict__ y, float *__restrict__ part,
+                                                         int M, int N, int K, int Kc, int splits) {
+  extern __shared__ __align__(16) uint8_t lds[];  // [M][row_bytes] activations, then S weight tiles
+  const int S = blockDim.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int rg = blockIdx.x / splits;
+  const int sp = blockIdx.x % splits;
+  const int kb = sp * Kc;
+  const int klen = min(K - kb, Kc);  // multiple of 16
+  const int kpad = (klen + kIterK - 1) / kIterK * kIterK;
+  const int row_bytes = kpad * 2 + 16;  // +16 spreads the 16 rows one MFMA operand load touches over all banks
+  uint8_t *xs = lds;
+  uint8_t *tile = lds + M * row_bytes + wave * kTileBytes;
+  const int n0 = (rg * S + wave) * 16;
+
+  // Load mapping: instruction j reads rows n0 + 4j + lane/16, bytes (lane%16)*16
+  // of the iteration's 256-byte window. Rows past N read the last row.
+  const int lrow = lane >> 4;
+  const int lcol = (lane & 15) * kPieceBytes;
+  const uint8_t *wr[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j)
+    wr[j] = w + static_cast<size_t>(min(n0 + j * kRowsPerLoad + lrow, N - 1)) * K + kb + lcol;
+
+  // Two register stages: iterations it+1 and it+2 are in flight while it is
+  // multiplied. A piece that starts at or past the slice end reads as zero
+  // (the slice length is a multiple of 16).
+  u32x4 va[kLoads], vb[kLoads];
+  auto load = [&](u32x4(&v)[kLoads], int it) {
+    const bool ok = it * kIterK + lcol < klen;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j)
+      v[j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wr[j] + it * kIterK))
+                : u32x4{0u, 0u, 0u, 0u};
+  };
+  const int n_iter = kpad / kIterK;
+  load(va, 0);
+  if (n_iter > 1) load(vb, 1);
+
+  // Stage x[0:M, kb:kb+kpad) in LDS (zero past the slice end) while the first
+  // weight loads are in flight.
+  const int vec_per_row = kpad / 8;
+  for (int v = threadIdx.x; v < M * vec_per_row; v += blockDim.x) {
+    const int m = v / vec_per_row;
+    const int kk = (v - m * vec_per_row) * 8;
+    u32x4 val = u32x4{0u, 0u, 0u, 0u};
+    if (kk < klen) val = *reinterpret_cast<const u32x4 *>(x + (static_cast<size_t>(m) * K + kb + kk) * 2);
+    *reinterpret_cast<u32x4 *>(xs + m * row_bytes + kk * 2) = val;
+  }
+  __syncthreads();
+
+  const uint8_t *brow[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) brow[b] = xs + min(b * 16 + r, M - 1) * row_bytes;
+  f32x4 acc[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One iteration: registers -> wave tile (row-contiguous), then MFMA
+  // operands read back in the MFMA layout: lane (r, g) takes row r, bytes
+  // s*64 + g*16 .. +15 of the window for step s.
+  auto multiply = [&](const u32x4(&v)[kLoads], int it) {
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j)
+      *reinterpret_cast<u32x4 *>(tile + (j * kRowsPerLoad + lrow) * kTileRow + lcol) = v[j];
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      const u32x4 a = *reinterpret_cast<const u32x4 *>(tile + r * kTileRow + st * kStepBytes + g * kPieceBytes);
+      bf16x8 a_lo, a_hi;
+      fp8x16_to_bf16(a, a_lo, a_hi);
+      const int kk = it * kIterK + st * kStepBytes + g * kPieceBytes;
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        const u32x4 *bp = reinterpret_cast<const u32x4 *>(brow[b] + kk * 2);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, as_bf16x8(bp[0]), acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, as_bf16x8(bp[1]), acc[b], 0, 0, 0);
+      }
+    }
+  };
+  for (int it = 0; it < n_iter; it += 2) {
+    multiply(va, it);
+    if (it + 2 < n_iter) load(va, it + 2);
+    if (it + 1 < n_iter) {
+      multiply(vb, it + 1);
+      if (it + 3 < n_iter) load(vb, it + 3);
+    }
+  }
+
+  // Lane l holds rows n0 + 4*(l/16) + i, column b*16 + l%16.
+  const int nb = n0 + 4 * g;
+  if (splits == 1) {
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const int m = b * 16 + r;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (nb + i < N) {
+          const float sc = __uint_as_float(static_cast<uint32_t>(scale[nb + i]) << 16);
+          y[static_cast<size_t>(m) * N + nb + i] = f32_to_bf16_bits(acc[b][i] * sc);
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const int m = b * 16 + r;
+    if (m >= M) continue;
+    float *dst = part + (static_cast<size_t>(sp) * M + m) * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (nb + i < N) dst[nb + i] = acc[b][i];
+  }
+}
+
+// y[i] = bf16(scale[i % N] * sum over splits of part[s][i]), summed in split
+// order. Each thread owns kReduceVec consecutive outputs and keeps up to
+// kReduceBatch independent loads in flight.
+constexpr int kReduceVec = 4;
+constexpr int kReduceBatch = 8;
+__global__ __launch_bounds__(256) void fp8_linear_reduce_kernel(const float *__restrict__ part,
+                                                                const uint16_t *__restrict__ scale,
+                                                                uint16_t *__restrict__ y, int64_t MN, int N,
+                                                                int splits) {
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * kReduceVec;
+  if (i0 >= MN) return;
+  float acc[kReduceVec] = {0.f, 0.f, 0.f, 0.f};
+  if (MN % kReduceVec == 0) {
+    for (int p0 = 0; p0 < splits; p0 += kReduceBatch) {
+      f32x4 v[kReduceBatch];
+#pragma unroll
+      for (int j = 0; j < kReduceBatch; ++j)
+        v[j] = p0 + j < splits ? *reinterpret_cast<const f32x4 *>(part + (p0 + j) * MN + i0)
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kReduceBatch; ++j)
+#pragma unroll
+        for (int e = 0; e < kReduceVec; ++e) acc[e] += v[j][e];
+    }
+  } else {
+    for (int p = 0; p < splits; ++p)
+      for (int e = 0; e < kReduceVec; ++e)
+        if (i0 + e < MN) acc[e] += part[p * MN + i0 + e];
+  }
+#pragma unroll
+  for (int e = 0; e < kReduceVec; ++e) {
+    const int64_t i = i0 + e;
+    if (i < MN) {
+      const float sc = __uint_as_float(static_cast<uint32_t>(scale[i % N]) << 16);
+      y[i] = f32_to_bf16_bits(acc[e] * sc);
+    }
+  }
+}
+
+template <int MB>
+hipError_t launch_mb(const Fp8LinearLaunch &p, hipStream_t stream) {
+  hipLaunchKernelGGL((fp8_linear_kernel<MB>), dim3(static_cast<unsigned>(p.grid)), dim3(p.waves * kWave),
+                     p.lds_bytes, stream, static_cast<const uint8_t *>(p.x), static_cast<const uint8_t *>(p.w),
+                     static_cast<const uint16_t *>(p.scale), static_cast<uint16_t *>(p.y),
+                     static_cast<float *>(p.workspace), static_cast<int>(p.m), static_cast<int>(p.n),
+                     static_cast<int>(p.k), static_cast<int>(p.kc), p.splits);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || p.splits == 1) return err;
+  const int64_t mn = p.m * p.n;
+  const int64_t threads = (mn + kReduceVec - 1) / kReduceVec;
+  hipLaunchKernelGGL(fp8_linear_reduce_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                     stream, static_cast<const float *>(p.workspace), static_cast<const uint16_t *>(p.scale),
+                     static_cast<uint16_t *>(p.y), mn, static_cast<int>(p.n), p.splits);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+Fp8LinearLaunch plan_fp8_linear(int64_t m, int64_t n, int64_t k, int cus, int waves, int kc_override) {
+  Fp8LinearLaunch p{};
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.batch_blocks = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  // LDS: m activation rows of (2*Kc + 16) bytes plus one weight tile per
+  // wave, within kFp8LinearMaxLds (less a margin for the kernel's own flag).
+  const int64_t budget = static_cast<int64_t>(kFp8LinearMaxLds) - 256;
+  p.waves = waves ? waves : 8;
+  while (p.waves > 1 && m * (2 * kIterK + 16) + static_cast<int64_t>(p.waves) * kTileBytes > budget) --p.waves;
+  const int64_t rows = 16 * static_cast<int64_t>(p.waves);
+  const int64_t row_groups = (n + rows - 1) / rows;
+  const int64_t kblocks = std::max<int64_t>(1, (k + kIterK - 1) / kIterK);
+  const int64_t tiles = static_cast<int64_t>(p.waves) * kTileBytes;
+  const int64_t x_budget = budget - tiles;
+  const int64_t lds_blocks = std::max<int64_t>(1, ((x_budget / m - 16) / 2) / kIterK);
+  int64_t kc_blocks;
+  if (kc_override) {
+    kc_blocks = std::max<int64_t>(1, kc_override / kIterK);
+  } else {
+    // Aim for at least 4 workgroups per CU, with slices of at least 4 iterations.
+    const int64_t want_splits = std::max<int64_t>(1, (4 * static_cast<int64_t>(cus) + row_groups - 1) / row_groups);
+    kc_blocks = std::max<int64_t>(std::min<int64_t>(4, kblocks), (kblocks + want_splits - 1) / want_splits);
+  }
+  kc_blocks = std::min(std::min(kc_blocks, kblocks), lds_blocks);
+  p.splits = static_cast<int>((kblocks + kc_blocks - 1) / kc_blocks);
+  p.kc = kc_blocks * kIterK;
+  p.grid = row_groups * p.splits;
+  p.row_groups = row_groups;
+  p.lds_bytes = static_cast<size_t>(m) * (2 * p.kc + 16) + static_cast<size_t>(tiles);
+  p.workspace_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * m * n * sizeof(float) : 0;
+  return p;
+}
+
+hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream) {
+  switch (p.batch_blocks) {
+    case 1: return launch_mb<1>(p, stream);
+    case 2: return launch_mb<2>(p, stream);
+    default: return launch_mb<4>(p, stream);
+  }
+}
+
+}  // namespace ftx

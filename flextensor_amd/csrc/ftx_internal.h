@@ -44,6 +44,29 @@ struct ScatterPlanDev {
   uint64_t tile_bytes;
 };
 
+// One launch of the fp8-weight linear kernel (ftx_gemm.hip), as planned by
+// plan_fp8_linear from the shape, the CU count and optional overrides.
+struct Fp8LinearLaunch {
+  const void *x;      // bf16 [m, k]
+  const void *w;      // e4m3fn [n, k]
+  const void *scale;  // bf16 [n]
+  void *y;            // bf16 [m, n]
+  void *workspace;    // fp32 [splits, m, n] partial sums when splits > 1
+  int64_t m, n, k;
+  int batch_blocks;   // 16-column batch blocks: 1, 2 or 4 (m <= 16 * batch_blocks)
+  int waves;          // wavefronts per workgroup, 16 output rows each
+  int splits;         // K slices, one workgroup each per row group
+  int64_t kc;         // K values per slice (multiple of 256)
+  int64_t row_groups; // groups of 16 * waves output rows
+  int64_t grid;       // workgroups = row_groups * splits
+  size_t lds_bytes;   // activation slice + one weight tile per wave
+  size_t workspace_bytes;
+};
+constexpr int kFp8LinearMaxRows = 64;
+constexpr size_t kFp8LinearMaxLds = 64 * 1024;
+Fp8LinearLaunch plan_fp8_linear(int64_t m, int64_t n, int64_t k, int cus, int waves, int kc);
+hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream);
+
 // Kernel launchers (ftx_kernels.hip). Each returns hipSuccess or the launch error.
 hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid,
                             hipStream_t stream);

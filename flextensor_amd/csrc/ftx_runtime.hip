@@ -45,6 +45,9 @@ struct ArenaRecord {
 std::mutex g_mutex;      // guards g_policy and g_arenas
 std::mutex g_dev_mutex;  // guards first-use setup of g_devices
 CopyPolicy g_policy;
+// fp8 linear launch shape; 0 = chosen per call from the shape and the CU count.
+int g_fp8_waves = 0;
+int g_fp8_slice_k = 0;
 DeviceState g_devices[kMaxDevices];
 std::map<uintptr_t, ArenaRecord> g_arenas;
 
@@ -602,6 +605,94 @@ int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *
   if (split_min_bytes) *split_min_bytes = ftx::g_policy.split_min_bytes;
   if (n_copy_streams) *n_copy_streams = ftx::g_policy.n_copy_streams;
   if (kernel_grid) *kernel_grid = ftx::g_policy.kernel_grid;
+  return FTX_OK;
+}
+
+int ftx_set_fp8_linear_config(int waves, int slice_k) {
+  if (waves < 0 || waves > 8) return ftx::fail(FTX_ERR_INVALID, "waves must be 0 (automatic) or in [1, 8]");
+  if (slice_k < 0 || slice_k % 256 != 0)
+    return ftx::fail(FTX_ERR_INVALID, "slice_k must be 0 (automatic) or a positive multiple of 256");
+  std::lock_guard<std::mutex> lock(ftx::g_mutex);
+  ftx::g_fp8_waves = waves;
+  ftx::g_fp8_slice_k = slice_k;
+  return FTX_OK;
+}
+
+namespace {
+
+int plan_fp8(int64_t m, int64_t n, int64_t k, ftx::Fp8LinearLaunch *p) {
+  if (m < 0 || n < 0 || k < 0) return ftx::fail(FTX_ERR_INVALID, "negative dimension");
+  if (m > ftx::kFp8LinearMaxRows)
+    return ftx::fail(FTX_ERR_UNSUPPORTED, "fp8 linear takes at most 64 activation rows");
+  if (k % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "k must be a multiple of 16");
+  if (n > (int64_t(1) << 30) || k > (int64_t(1) << 30) || m * n > (int64_t(1) << 31))
+    return ftx::fail(FTX_ERR_INVALID, "fp8 linear dimensions too large");
+  if (m == 0 || n == 0) {
+    *p = ftx::Fp8LinearLaunch{};
+    return FTX_OK;
+  }
+  int waves, slice_k;
+  {
+    std::lock_guard<std::mutex> lock(ftx::g_mutex);
+    waves = ftx::g_fp8_waves;
+    slice_k = ftx::g_fp8_slice_k;
+  }
+  int cus = 256;
+  {
+    ftx::DeviceState *st = nullptr;
+    if (ftx::device_state(&st) == FTX_OK) cus = st->cu_count;
+  }
+  *p = ftx::plan_fp8_linear(m, n, k, cus, waves, slice_k);
+  if (p->grid > (int64_t(1) << 31) - 1) return ftx::fail(FTX_ERR_INVALID, "fp8 linear grid too large");
+  return FTX_OK;
+}
+
+}  // namespace
+
+int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes) {
+  if (!bytes) return ftx::fail(FTX_ERR_INVALID, "bytes is null");
+  ftx::Fp8LinearLaunch p;
+  int rc = plan_fp8(m, n, k, &p);
+  if (rc != FTX_OK) return rc;
+  *bytes = p.workspace_bytes;
+  return FTX_OK;
+}
+
+int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  ftx::Fp8LinearLaunch p;
+  int rc = plan_fp8(m, n, k, &p);
+  if (rc != FTX_OK) return rc;
+  if (m == 0 || n == 0) return FTX_OK;
+  if (!y || !scale) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  if (reinterpret_cast<uintptr_t>(y) % 2 != 0 || reinterpret_cast<uintptr_t>(scale) % 2 != 0)
+    return ftx::fail(FTX_ERR_INVALID, "y and scale need 2-byte alignment");
+  rc = ftx::check_device_range(y, static_cast<size_t>(m * n * 2), "fp8 linear output");
+  if (rc == FTX_OK) rc = ftx::check_device_range(scale, static_cast<size_t>(n * 2), "fp8 linear scale");
+  if (rc != FTX_OK) return rc;
+  if (k > 0) {
+    if (!x || !w) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
+      return ftx::fail(FTX_ERR_INVALID, "x and w need 16-byte alignment");
+    rc = ftx::check_device_range(x, static_cast<size_t>(m * k * 2), "fp8 linear input");
+    if (rc == FTX_OK) rc = ftx::check_device_range(w, static_cast<size_t>(n * k), "fp8 linear weight");
+    if (rc != FTX_OK) return rc;
+  }
+  if (p.workspace_bytes > 0) {
+    if (!workspace || workspace_bytes < p.workspace_bytes)
+      return ftx::fail(FTX_ERR_INVALID, "fp8 linear needs a workspace of " + std::to_string(p.workspace_bytes) +
+                                            " bytes (ftx_fp8_linear_workspace)");
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+      return ftx::fail(FTX_ERR_INVALID, "workspace needs 16-byte alignment");
+    rc = ftx::check_device_range(workspace, p.workspace_bytes, "fp8 linear workspace");
+    if (rc != FTX_OK) return rc;
+  }
+  p.x = x;
+  p.w = w;
+  p.scale = scale;
+  p.y = y;
+  p.workspace = workspace;
+  FTX_HIP(ftx::launch_fp8_linear(p, static_cast<hipStream_t>(stream)));
   return FTX_OK;
 }
 

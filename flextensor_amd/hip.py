@@ -305,3 +305,59 @@ def checksum(t: torch.Tensor, stream: HipStream | None = None) -> int:
         raise ValueError("checksum needs a contiguous device tensor")
     s = stream if stream is not None else current_stream(t.device)
     return nat.checksum64(t.data_ptr(), t.numel() * t.element_size(), s.handle)
+
+
+FP8_LINEAR_MAX_ROWS = 64
+_FP8_WORKSPACE: dict[tuple[int, int, int], int] = {}
+
+
+def fp8_linear_workspace_bytes(m: int, n: int, k: int) -> int:
+    """Bytes of device workspace one ``fp8_linear`` call of this shape needs (cached per shape)."""
+    key = (m, n, k)
+    got = _FP8_WORKSPACE.get(key)
+    if got is None:
+        b = ctypes.c_size_t(0)
+        nat.call("ftx_fp8_linear_workspace", m, n, k, ctypes.byref(b))
+        got = _FP8_WORKSPACE[key] = int(b.value)
+    return got
+
+
+def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``bf16(scale * (x @ weight.T))`` by the library's fp8-weight MFMA kernel.
+
+    ``x``: bf16 ``[m, k]`` with ``m <= 64``; ``weight``: float8 e4m3fn ``[n, k]``;
+    ``scale``: bf16 ``[n]``; all on one device. The weights are widened to
+    bf16 in registers, so the products are those of dequantizing and running
+    a bf16 GEMM. Runs on torch's current stream; the split-K workspace comes
+    from torch's allocator on that stream.
+    """
+    if x.dim() != 2 or weight.dim() != 2 or scale.dim() != 1:
+        raise ValueError("fp8_linear needs x [m, k], weight [n, k] and scale [n]")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.float8_e4m3fn or scale.dtype != torch.bfloat16:
+        raise TypeError(f"fp8_linear needs bf16 x, float8_e4m3fn weight and bf16 scale; got "
+                        f"{x.dtype}, {weight.dtype}, {scale.dtype}")
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or scale.shape[0] != n:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, weight {tuple(weight.shape)}, scale {tuple(scale.shape)}")
+    if not (x.is_cuda and weight.device == x.device and scale.device == x.device):
+        raise ValueError("fp8_linear needs x, weight and scale on one GPU")
+    if not weight.is_contiguous() or weight.data_ptr() % 16:
+        raise ValueError("fp8_linear needs a contiguous, 16-byte aligned weight")
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        x = x.clone(memory_format=torch.contiguous_format)
+    if not scale.is_contiguous():
+        scale = scale.contiguous()
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    ws_bytes = fp8_linear_workspace_bytes(m, n, k)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    nat.call("ftx_fp8_linear", x.data_ptr(), weight.data_ptr(), scale.data_ptr(), y.data_ptr(), m, n, k,
+             ws.data_ptr() if ws is not None else None, ws_bytes, torch.cuda.current_stream(x.device).cuda_stream)
+    return y
+
+
+def set_fp8_linear_config(waves: int = 0, slice_k: int = 0) -> None:
+    """Fix the fp8 linear launch shape: wavefronts per workgroup and K values
+    per workgroup (0 = chosen per call from the shape)."""
+    nat.call("ftx_set_fp8_linear_config", waves, slice_k)
+    _FP8_WORKSPACE.clear()

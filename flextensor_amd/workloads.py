@@ -25,6 +25,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import hip
+
 
 FP8_E4M3_MAX = 448.0
 
@@ -121,9 +123,12 @@ LLAMA_70B_FP8 = LlamaShape(n_layers=80, hidden=8192, n_heads=64, n_kv_heads=8, h
 class Fp8Linear(nn.Module):
     """y = x @ (W_fp8 * scale[:, None])^T with W in float8_e4m3fn and a bf16 scale per output channel.
 
-    Every e4m3 value is exactly representable in bf16, so dequantising and
-    running a bf16 GEMM computes the same products as the reference's
-    dequantise-then-linear forward.
+    On the GPU, decode-sized inputs (at most 64 rows, K a multiple of 16) run
+    the library's fp8-weight MFMA kernel, which reads each fp8 weight once and
+    widens it to bf16 in registers. Larger inputs (prefill) and CPU inputs
+    dequantise to bf16 and run a bf16 GEMM. Every e4m3 value is exactly
+    representable in bf16, so both compute the same products; they differ in
+    accumulation order and in rounding the product before the scale.
     """
 
     def __init__(self, in_features: int, out_features: int) -> None:
@@ -133,6 +138,12 @@ class Fp8Linear(nn.Module):
         self.scale = nn.Parameter(torch.ones(out_features, dtype=torch.bfloat16), requires_grad=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        k = x.shape[-1]
+        m = x.numel() // k if k else 0
+        if (x.is_cuda and x.dtype == torch.bfloat16 and 0 < m <= hip.FP8_LINEAR_MAX_ROWS and k % 16 == 0
+                and self.weight.is_contiguous()):
+            y = hip.fp8_linear(x.reshape(m, k), self.weight, self.scale)
+            return y.view(*x.shape[:-1], y.shape[-1])
         w = self.weight.to(torch.bfloat16)
         return F.linear(x, w) * self.scale
 

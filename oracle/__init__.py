@@ -14,6 +14,8 @@ a pure-Python library) and cites the file:line it follows:
                    both pipelined loaders, replayed on a recording fake stream
 * ``interpolator`` log-log size <-> duration link model
 * ``timing``       per-trap transfer/compute/wait records and hidden fraction
+* ``fp8``          float8 e4m3fn decoding (OCP format definition) and the
+                   fp8-weight linear layer in float64
 * ``native``       ctypes access to ``liboracle.so`` (plain C: layout, pack,
                    scatter, checksum)
 """

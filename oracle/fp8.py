@@ -1,0 +1,43 @@
+"""Oracle: float8 e4m3fn decoding and the fp8-weight linear layer, in float64.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+The reference streams whatever weights the user's model holds and has no fp8
+code of its own; the fp8 workload's layer is ``F.linear(x, w.to(bf16)) *
+scale``. This module restates the OCP 8-bit floating-point format (OFP8,
+E4M3 variant: 1 sign, 4 exponent bits with bias 7, 3 mantissa bits,
+subnormals, no infinities, NaN = S.1111.111, largest finite 448) and the layer
+``y[i, j] = scale[j] * sum_k x[i, k] * w[j, k]`` in exact float64 arithmetic.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def e4m3fn_value(byte: int) -> float:
+    """Value of one e4m3fn byte from the format definition."""
+    if not 0 <= byte <= 255:
+        raise ValueError(f"not a byte: {byte}")
+    sign = -1.0 if byte & 0x80 else 1.0
+    exp = (byte >> 3) & 0xF
+    man = byte & 0x7
+    if exp == 0xF and man == 0x7:
+        return float("nan")
+    if exp == 0:
+        return sign * (man / 8.0) * 2.0 ** (1 - 7)
+    return sign * (1.0 + man / 8.0) * 2.0 ** (exp - 7)
+
+
+E4M3FN_TABLE = np.array([e4m3fn_value(b) for b in range(256)], dtype=np.float64)
+
+
+def decode_e4m3fn(raw: np.ndarray) -> np.ndarray:
+    """float64 values of an array of e4m3fn bytes (uint8)."""
+    return E4M3FN_TABLE[np.asarray(raw, dtype=np.uint8)]
+
+
+def fp8_linear(x: np.ndarray, w_raw: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """float64 ``scale[j] * sum_k x[i, k] * w[j, k]``; x and scale as float64-convertible arrays."""
+    w = decode_e4m3fn(w_raw)
+    return (np.asarray(x, dtype=np.float64) @ w.T) * np.asarray(scale, dtype=np.float64)[None, :]

@@ -1,0 +1,302 @@
+"""GPU parity of the fp8-weight MFMA linear kernel (``ftx_fp8_linear``).
+
+The oracle is ``oracle.fp8`` (e4m3fn decoded from the format definition, the
+layer in float64). Where every product and partial sum is exact in float32
+(small integers times powers of two) the kernel must match the oracle bit for
+bit after round-to-nearest-even to bf16; on random data the tolerance is 1e-2
+relative error (norm-wise), with a tighter per-element bound.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2  # bf16 outputs vs the float64 oracle, norm-wise
+ELEM_TOL = 2.0 ** -7  # per element, relative to max(|ref|, rms(ref))
+
+# e4m3fn codes of 0, +-1, +-2, +-3, +-4
+_SMALL_INT_CODES = np.array([0x00, 0x38, 0xB8, 0x40, 0xC0, 0x44, 0xC4, 0x48, 0xC8], dtype=np.uint8)
+_SHAPES = [(1, 16, 16), (8, 1024, 8192), (5, 100, 48), (16, 37, 1040), (17, 300, 528), (33, 96, 160),
+           (64, 512, 256), (8, 8192, 4096), (3, 8200, 64)]
+
+
+@pytest.fixture
+def default_config(gpu):
+    from flextensor_amd import hip
+
+    hip.set_fp8_linear_config(0, 0)
+    yield
+    hip.set_fp8_linear_config(0, 0)
+
+
+def _exact_case(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    w_raw = rng.choice(_SMALL_INT_CODES, size=(n, k))
+    x = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    scale = rng.choice(np.array([0.25, 0.5, 1.0, 2.0], dtype=np.float32), size=n)
+    return x, w_raw, scale
+
+
+def _to_device(x, w_raw, scale, dev):
+    xt = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16).to(dev)
+    wt = torch.from_numpy(np.ascontiguousarray(w_raw)).view(torch.float8_e4m3fn).to(dev)
+    st = torch.from_numpy(np.ascontiguousarray(scale, dtype=np.float32)).to(torch.bfloat16).to(dev)
+    return xt, wt, st
+
+
+def _same_values(got: torch.Tensor, want: torch.Tensor) -> bool:
+    """Equal bf16 values (an exact zero may carry either sign)."""
+    return torch.equal(got.cpu().float(), want.float())
+
+
+@pytest.mark.parametrize("m,n,k", _SHAPES)
+def test_exact_products_bit_exact(gpu, default_config, m, n, k):
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _exact_case(m, n, k, seed=m * 7 + n + k)
+    want = torch.from_numpy(ofp8.fp8_linear(x, w_raw, scale)).to(torch.bfloat16)
+    got = hip.fp8_linear(*_to_device(x, w_raw, scale, gpu))
+    torch.cuda.synchronize()
+    assert got.shape == (m, n)
+    assert _same_values(got, want)
+
+
+@pytest.mark.parametrize("waves", [1, 4, 8])
+@pytest.mark.parametrize("slice_k", [256, 768, 0])
+@pytest.mark.parametrize("m,n,k", [(8, 96, 1040), (40, 64, 4096), (20, 48, 208), (64, 200, 1536), (1, 300, 2560)])
+def test_every_launch_shape_bit_exact(gpu, default_config, waves, slice_k, m, n, k):
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _exact_case(m, n, k, seed=waves + slice_k + k)
+    want = torch.from_numpy(ofp8.fp8_linear(x, w_raw, scale)).to(torch.bfloat16)
+    hip.set_fp8_linear_config(waves, slice_k)
+    got = hip.fp8_linear(*_to_device(x, w_raw, scale, gpu))
+    torch.cuda.synchronize()
+    assert _same_values(got, want)
+
+
+def test_workspace_size_follows_the_split(gpu, default_config):
+    from flextensor_amd import hip
+
+    hip.set_fp8_linear_config(0, 1024)
+    assert hip.fp8_linear_workspace_bytes(8, 1000, 4096) == 4 * 8 * 1000 * 4
+    hip.set_fp8_linear_config(0, 0)
+    assert hip.fp8_linear_workspace_bytes(8, 1000, 1024) == 0  # one slice of four iterations
+    hip.set_fp8_linear_config(0, 256)
+    assert hip.fp8_linear_workspace_bytes(8, 1000, 512) == 2 * 8 * 1000 * 4
+    # the activation slice and eight 16-row weight tiles share 64 KiB of LDS:
+    # 8 rows x 4096 bf16 do not fit, so a 4096-wide slice is cut to 1792
+    hip.set_fp8_linear_config(0, 4096)
+    assert hip.fp8_linear_workspace_bytes(8, 1000, 4096) == 3 * 8 * 1000 * 4
+
+
+def test_split_calls_in_a_row_stay_exact(gpu, default_config):
+    """Split-K calls of different shapes in a row, then the first again: every result stays exact."""
+    from flextensor_amd import hip
+
+    hip.set_fp8_linear_config(4, 256)
+    cases = [(8, 640, 2048), (3, 70, 1024), (8, 640, 2048), (16, 1024, 512)]
+    for m, n, k in cases:
+        x, w_raw, scale = _exact_case(m, n, k, seed=n + k)
+        want = torch.from_numpy(ofp8.fp8_linear(x, w_raw, scale)).to(torch.bfloat16)
+        for _ in range(3):
+            got = hip.fp8_linear(*_to_device(x, w_raw, scale, gpu))
+            assert _same_values(got, want)
+
+
+def test_graph_replays_match_eager(gpu, default_config):
+    """Captured split-K calls (main kernel + reduce) replay exactly, with eager calls between replays."""
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _random_case(8, 4096, 8192, seed=11)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    assert hip.fp8_linear_workspace_bytes(8, 4096, 8192) > 0
+    eager = hip.fp8_linear(xt, wt, st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        hip.fp8_linear(xt, wt, st)  # warm-up on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            out = hip.fp8_linear(xt, wt, st)
+    torch.cuda.current_stream().wait_stream(stream)
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        other = hip.fp8_linear(xt, wt, st)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(other, eager)
+
+
+@pytest.mark.parametrize("scale_value", [1.0, 0.5])
+def test_every_e4m3_code_decodes_exactly(gpu, default_config, scale_value):
+    """x = identity rows pick single weights: y[i, j] = w[j, i] * scale for all 256 codes."""
+    from flextensor_amd import hip
+
+    codes = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    codes[(codes & 0x7F) == 0x7F] = 0x00  # NaN codes would poison the zero products of their row
+    w_raw = np.zeros((16, 64), dtype=np.uint8)
+    w_raw[:, :16] = codes
+    x = np.zeros((16, 64), dtype=np.float32)
+    x[np.arange(16), np.arange(16)] = 1.0
+    scale = np.full(16, scale_value, dtype=np.float32)
+    got = hip.fp8_linear(*_to_device(x, w_raw, scale, gpu)).cpu()
+    want = torch.from_numpy(ofp8.decode_e4m3fn(codes).T * scale_value).to(torch.bfloat16)
+    assert _same_values(got, want)
+
+
+def _random_case(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32) * 64.0
+    w_raw = torch.from_numpy(np.clip(w, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    scale = (rng.random(n).astype(np.float32) + 0.5) / 448.0
+    return x, w_raw, scale
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 8192, 8192), (8, 1024, 8192), (8, 28672, 8192), (8, 8192, 28672),
+                                   (1, 4096, 11008), (64, 256, 4096), (27, 1000, 2000)])
+def test_random_matches_float64_oracle(gpu, default_config, m, n, k):
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _random_case(m, n, k, seed=m + n + k)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    got = hip.fp8_linear(xt, wt, st).double().cpu()
+    # the oracle sees the bf16-rounded activations and scales the kernel sees
+    want = torch.from_numpy(ofp8.fp8_linear(xt.float().cpu().numpy(), w_raw, st.float().cpu().numpy()))
+    assert float((got - want).norm() / want.norm()) < REL_TOL
+    bound = ELEM_TOL * torch.maximum(want.abs(), want.pow(2).mean().sqrt())
+    assert bool(((got - want).abs() <= bound).all())
+
+
+def test_deterministic_and_matches_dequantized_gemm(gpu, default_config):
+    from flextensor_amd import workloads as W
+
+    lin = W.Fp8Linear(4096, 2048)
+    x, w_raw, scale = _random_case(8, 2048, 4096, seed=5)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    lin.weight.data = wt
+    lin.scale.data = st
+    with torch.no_grad():
+        a = lin(xt.view(8, 1, 4096))
+        b = lin(xt.view(8, 1, 4096))
+        dequant = torch.nn.functional.linear(xt, wt.to(torch.bfloat16)) * st
+    assert a.shape == (8, 1, 2048)
+    assert torch.equal(a, b)
+    assert float((a.view(8, 2048).double() - dequant.double()).norm() / dequant.double().norm()) < REL_TOL
+
+
+def test_writes_only_its_output(gpu, default_config):
+    """Sentinels around the output stay intact (rows m..15 of the MFMA tile are never stored)."""
+    from flextensor_amd import _native as nat
+
+    m, n, k = 5, 40, 64
+    x, w_raw, scale = _exact_case(m, n, k, seed=3)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    buf = torch.full((m * n + 256,), 0x5A5A, dtype=torch.int16, device=gpu)
+    y = buf[128 : 128 + m * n]
+    nat.call("ftx_fp8_linear", xt.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), m, n, k, None, 0,
+             torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = buf.cpu()
+    assert (out[:128] == 0x5A5A).all() and (out[128 + m * n :] == 0x5A5A).all()
+    want = torch.from_numpy(ofp8.fp8_linear(x, w_raw, scale)).to(torch.bfloat16).reshape(-1)
+    assert _same_values(out[128 : 128 + m * n].view(torch.bfloat16), want)
+
+
+def test_rejects_bad_arguments(gpu, default_config):
+    from flextensor_amd import _native as nat
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _exact_case(8, 32, 64, seed=1)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    y = torch.empty(65 * 32, dtype=torch.bfloat16, device=gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    with pytest.raises(nat.FtxError) as err:  # more rows than the kernel takes
+        nat.call("ftx_fp8_linear", xt.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), 65, 32, 64, None, 0, s)
+    assert err.value.code == nat.FTX_ERR_UNSUPPORTED
+    with pytest.raises(nat.FtxError) as err:  # k not a multiple of 16
+        nat.call("ftx_fp8_linear", xt.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), 8, 32, 24, None, 0, s)
+    assert err.value.code == nat.FTX_ERR_INVALID
+    # weight range past its allocation: a 2 MiB hipMalloc asked to hold 512 x 8192 bytes
+    import ctypes
+
+    wbuf = ctypes.c_void_p()
+    nat.call("ftx_device_alloc", 1 << 21, ctypes.byref(wbuf))
+    try:
+        big_x = torch.zeros(8, 8192, dtype=torch.bfloat16, device=gpu)
+        big_s = torch.ones(512, dtype=torch.bfloat16, device=gpu)
+        big_y = torch.empty(8, 512, dtype=torch.bfloat16, device=gpu)
+        with pytest.raises(nat.FtxError) as err:
+            nat.call("ftx_fp8_linear", big_x.data_ptr(), wbuf.value, big_s.data_ptr(), big_y.data_ptr(), 8, 512,
+                     8192, None, 0, s)
+        assert err.value.code == nat.FTX_ERR_INVALID
+        assert "weight" in str(err.value)
+    finally:
+        torch.cuda.synchronize()
+        nat.call("ftx_device_free", wbuf.value)
+    host_x = torch.zeros(8, 64, dtype=torch.bfloat16)
+    with pytest.raises(nat.FtxError) as err:  # host memory as the input
+        nat.call("ftx_fp8_linear", host_x.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), 8, 32, 64, None, 0,
+                 s)
+    assert err.value.code == nat.FTX_ERR_INVALID
+    hip.set_fp8_linear_config(0, 256)  # two K slices need a workspace
+    x2, w2, s2 = _to_device(*_exact_case(8, 32, 512, seed=2), gpu)
+    with pytest.raises(nat.FtxError) as err:
+        nat.call("ftx_fp8_linear", x2.data_ptr(), w2.data_ptr(), s2.data_ptr(), y.data_ptr(), 8, 32, 512, None, 0, s)
+    assert err.value.code == nat.FTX_ERR_INVALID and "workspace" in str(err.value)
+    small = torch.empty(2 * 8 * 32 * 4 - 16, dtype=torch.uint8, device=gpu)
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_fp8_linear", x2.data_ptr(), w2.data_ptr(), s2.data_ptr(), y.data_ptr(), 8, 32, 512,
+                 small.data_ptr(), small.numel(), s)
+    hip.set_fp8_linear_config(0, 0)
+    with pytest.raises(nat.FtxError):
+        hip.set_fp8_linear_config(9, 0)
+    with pytest.raises(nat.FtxError):
+        hip.set_fp8_linear_config(0, 100)
+    with pytest.raises(TypeError):
+        hip.fp8_linear(xt.float(), wt, st)
+
+
+def test_fp8_decoder_on_gpu_matches_dequantized_float32(gpu, default_config):
+    """A small fp8 decoder: decode steps (8 rows) run the kernel, the prompt (64 rows x 2) the bf16 GEMM."""
+    from flextensor_amd import workloads as W
+
+    shape = W.LlamaShape(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=512, vocab=300,
+                         max_seq=64, fp8=True)
+    model = W.build_llama(shape, seed=3)
+    twin = W.build_llama(W.LlamaShape(**{**shape.__dict__, "fp8": False}), seed=0).float()
+    mods = dict(model.named_modules())
+    sd = {}
+    for name, p in model.named_parameters():
+        owner = name.rsplit(".", 1)[0]
+        if isinstance(mods.get(owner), W.Fp8Linear):
+            if name.endswith(".weight"):
+                sd[name] = mods[owner].weight.float() * mods[owner].scale.float()[:, None]
+        else:
+            sd[name] = p.detach().float()
+    twin.load_state_dict(sd, strict=False)
+    model = model.to(gpu)
+    prompt = W.prompt_tokens(8, 16, shape.vocab, seed=3)
+    model.init_cache(8, 40, gpu)
+    twin.init_cache(8, 40, torch.device("cpu"))
+    with torch.no_grad():
+        got = [model(prompt.to(gpu), 0).float().cpu()]
+        want = [twin(prompt, 0)]
+        tok = want[0].argmax(-1)
+        for pos in range(16, 20):
+            got.append(model(tok.to(gpu), pos).float().cpu())
+            want.append(twin(tok, pos))
+            tok = want[-1].argmax(-1)
+    for g, w in zip(got, want):
+        assert float((g - w).norm() / w.norm()) < REL_TOL
