@@ -21,10 +21,10 @@ int hip_fail(hipError_t err, const char *what);
     if (ftx_err_ != hipSuccess) return ::ftx::hip_fail(ftx_err_, #expr); \
   } while (0)
 
-// Default bytes per wave tile of the scatter kernel: one round of 16 loads
-// and 16 stores of 16 bytes per lane (fastest of 16/32/64/128 KiB on a
-// 512 MiB chunk of 96 tensors).
-constexpr size_t kScatterTileBytes = 16 * 1024;
+// Default bytes per wave tile of the scatter kernel: one round of 8 loads and
+// 8 non-temporal stores of 16 bytes per lane (fastest of 8/16/32 KiB on the
+// 2000-tensor set's 512 MiB chunks: 5.94 TB/s against 5.78 and 5.77).
+constexpr size_t kScatterTileBytes = 8 * 1024;
 // Default zero-copy grid: 64 workgroups keep the link at its peak (more
 // workgroups only add outstanding PCIe reads).
 constexpr int kZeroCopyDefaultGrid = 64;

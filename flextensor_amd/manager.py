@@ -26,10 +26,11 @@ from __future__ import annotations
 
 import fnmatch
 import logging
+import os
 import re
 import threading
 import time
-from collections.abc import Sequence
+from collections.abc import Callable, Sequence
 from dataclasses import dataclass, field
 from enum import Enum
 from typing import Any
@@ -144,12 +145,38 @@ def select_offload_units(model: nn.Module, include: Sequence[str], exclude: Sequ
     return [p for p in chosen if not _matches(p, model.get_submodule(p), exclude)]
 
 
+class _CompiledCall(threading.local):
+    active = False
+
+
+_COMPILED_CALL = _CompiledCall()
+
+
+def raise_dynamo_limits(n_units: int) -> None:
+    """Raise the compiler's recompile limits so each of ``n_units`` units keeps its own graph.
+
+    Each unit's forward closes over its own label, so the compiler specializes
+    once per unit; with more units than the default limit (8) the rest would
+    silently run uncompiled. Limits are only raised (compiled_offload.py:24-46).
+    """
+    if n_units <= 0:
+        return
+    import torch._dynamo as dynamo
+
+    needed = 2 * n_units + 16
+    for attr in ("recompile_limit", "cache_size_limit", "accumulated_recompile_limit",
+                 "accumulated_cache_size_limit"):
+        if hasattr(dynamo.config, attr) and (getattr(dynamo.config, attr) or 0) < needed:
+            setattr(dynamo.config, attr, needed)
+
+
 @dataclass
 class _Unit:
     label: str
     module: nn.Module
     params: list[nn.Parameter] = field(default_factory=list)
     names: list[str] = field(default_factory=list)  # qualified parameter names, parallel to params
+    compiled: Callable[..., Any] | None = None  # compile_fn(module), installed at INFERENCE
 
     @property
     def nbytes(self) -> int:
@@ -305,15 +332,26 @@ class OffloadManager:
         self._events: dict[str, tuple[Any, Any]] = {}
         self._pass_done: list[Any] = []  # completion events of the latest streamed passes
         self.build_seconds = 0.0
+        self.compile_fn: Callable[[nn.Module], Any] | None = None
 
     # -- public ---------------------------------------------------------------
 
     def offload(self, model: nn.Module, config: OffloadConfig | None = None,
-                state: TensorManagerState | None = None) -> nn.Module:
-        """Patch ``model``; with a saved ``state`` the plan is restored and streaming starts at once."""
+                state: TensorManagerState | None = None,
+                compile_fn: Callable[[nn.Module], Any] | None = None) -> nn.Module:
+        """Patch ``model``; with a saved ``state`` the plan is restored and streaming starts at once.
+
+        ``compile_fn`` is the reference's per-unit compiler (offload_manager.py:2858-2884): at the
+        INFERENCE transition it is applied to each offload unit, so every unit compiles as its own
+        graph with the unit's ``pre_compute`` / ``post_compute`` ops inside. Discovery and
+        profiling stay eager.
+        """
         self._check_thread()
         if self.model is not None:
             raise RuntimeError(f"offload manager {self.name!r} already manages a model; release() it first")
+        if compile_fn is not None and not callable(compile_fn):
+            raise TypeError("compile_fn must be callable: module -> compiled module")
+        self.compile_fn = compile_fn
         self.config = config or OffloadConfig()
         if not self.config.enabled:
             return model
@@ -452,6 +490,9 @@ class OffloadManager:
         for mod, orig in self._patched:
             if "forward" in mod.__dict__:
                 del mod.forward
+        for u in self.units:
+            u.compiled = None
+        self.compile_fn = None
         restore = {}
         if self.controller is not None and preserve_model:
             for label in self.controller.block_map_cpu:
@@ -520,6 +561,16 @@ class OffloadManager:
         mgr, label, mid = self, unit.label, id(self)
 
         def forward(*args: Any, **kwargs: Any) -> Any:
+            if (unit.compiled is not None and not torch.compiler.is_compiling() and not _COMPILED_CALL.active
+                    and mgr.phase == OffloadPhase.INFERENCE):
+                # Per-unit compiled graph: it re-enters this forward while tracing (the branch below).
+                # Should the compiler run this frame eagerly instead, the flag sends the call down
+                # the eager path rather than back into the compiled unit.
+                _COMPILED_CALL.active = True
+                try:
+                    return unit.compiled(*args, **kwargs)
+                finally:
+                    _COMPILED_CALL.active = False
             if torch.compiler.is_compiling():
                 if mgr.phase != OffloadPhase.INFERENCE:
                     raise RuntimeError(f"offload manager {mgr.name!r} is in {mgr.phase.value}: run the discovery and "
@@ -684,6 +735,10 @@ class OffloadManager:
                               self.controller, self.timing, policy)
             self.controller.commit_construction()
         self.phase = OffloadPhase.INFERENCE
+        if self.compile_fn is not None:
+            raise_dynamo_limits(len(self.units))
+            for u in self.units:
+                u.compiled = self.compile_fn(u.module)
         self.build_seconds = time.perf_counter() - t0
         LOGGER.info("offload %r: %d streamed / %d resident units, %.1f s to build", self.name, len(plan.streamed),
                     len(plan.resident), self.build_seconds)
@@ -716,9 +771,14 @@ def get_offload_manager(name: str = DEFAULT_MANAGER_NAME) -> OffloadManager:
     return mgr
 
 
-def offload(model: nn.Module, config: OffloadConfig | None = None, name: str = DEFAULT_MANAGER_NAME) -> nn.Module:
-    """Patch ``model`` so its offload units stream from pinned host memory."""
-    return get_offload_manager(name).offload(model, config)
+def offload(model: nn.Module, config: OffloadConfig | None = None, name: str = DEFAULT_MANAGER_NAME,
+            compile_fn: Callable[[nn.Module], Any] | None = None) -> nn.Module:
+    """Patch ``model`` so its offload units stream from pinned host memory.
+
+    ``compile_fn`` compiles each offload unit separately once streaming starts
+    (offload_manager.py:2858-2884).
+    """
+    return get_offload_manager(name).offload(model, config, compile_fn=compile_fn)
 
 
 def release(name: str = DEFAULT_MANAGER_NAME, preserve_model: bool = True) -> None:
@@ -750,15 +810,24 @@ def load_profile(profile_directory: str | None = None, model: nn.Module | None =
     get_offload_manager(name).load_profile(profile_directory, model)
 
 
-def offload_from_profile(model: nn.Module, config: OffloadConfig | None = None, profile_directory: str | None = None,
-                         name: str = DEFAULT_MANAGER_NAME) -> nn.Module:
-    """Offload ``model`` straight into streaming with a saved plan: no discovery or profiling passes."""
+def offload_from_profile(model: nn.Module, profile_directory: str | os.PathLike[str] | None,
+                         config: OffloadConfig | None = None, name: str = DEFAULT_MANAGER_NAME,
+                         compile_fn: Callable[[nn.Module], Any] | None = None) -> nn.Module:
+    """Offload ``model`` straight into streaming with a saved plan: no discovery or profiling passes.
+
+    Same signature as the reference (offload_manager.py:2961-2986); ``profile_directory`` None
+    falls back to ``config.profile_storage_dir``.
+    """
+    if isinstance(profile_directory, OffloadConfig):
+        raise TypeError("offload_from_profile(model, profile_directory, config=...): the second argument is the "
+                        "profile directory")
     cfg = config or OffloadConfig()
     directory = profile_directory or cfg.profile_storage_dir
     if directory is None:
         raise ValueError("No profile directory specified. Provide profile_directory argument "
                          "or set profile_storage_dir in OffloadConfig.")
-    return get_offload_manager(name).offload(model, cfg, state=load_state(directory))
+    return get_offload_manager(name).offload(model, cfg, state=load_state(os.fspath(directory)),
+                                             compile_fn=compile_fn)
 
 
 def offload_from_state(model: nn.Module, state: TensorManagerState, config: OffloadConfig | None = None,

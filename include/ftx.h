@@ -143,7 +143,7 @@ int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *
  * No reference counterpart; it places a streamed chunk into many tensors in
  * one launch where the reference copies tensor by tensor (see ftx_desc).
  * A plan uploads descriptors once (device memory) and can be run any number
- * of times on any stream; tile_bytes 0 selects the default (16 KiB). */
+ * of times on any stream; tile_bytes 0 selects the default (8 KiB). */
 int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes,
                             ftx_scatter_plan **plan);
 int ftx_scatter_plan_destroy(ftx_scatter_plan *plan);

@@ -124,6 +124,41 @@ def test_compiled_streamed_forward_matches_resident(gpu, budget_layers):
     mgr.release()
 
 
+@pytest.mark.parametrize("budget_layers", [None, 5])
+def test_per_unit_compile_fn_matches_resident(gpu, budget_layers):
+    """offload(..., compile_fn=...) compiles each unit on its own at INFERENCE (offload_manager.py:2858-2884)."""
+    torch._dynamo.reset()
+    model = W.build_mlp_stack(8, 256, 704, seed=33)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, max_gpu_mem_bytes=None if budget_layers is None else budget_layers * layer)
+    compiled_units = []
+
+    def compile_fn(module):
+        compiled_units.append(module)
+        return torch.compile(module, backend="aot_eager", fullgraph=True)
+
+    mgr = OffloadManager(name=f"compile-fn-{budget_layers}")
+    mgr.offload(model, cfg, compile_fn=compile_fn)
+    x = W.mlp_input(16, 256, seed=33).to(gpu)
+    want = _resident_feedback(resident, x)
+    with torch.no_grad():
+        model(x)  # discovery runs eagerly: nothing compiled yet
+        assert mgr.phase == OffloadPhase.PROFILING and not compiled_units
+        model(x)  # profiling, then the switch to streaming compiles the units
+        assert mgr.phase == OffloadPhase.INFERENCE
+        for _ in range(3):
+            assert torch.equal(_resident_feedback(model, x), want)
+    units = list(mgr.units)
+    assert compiled_units == [u.module for u in units]  # one compiled graph per unit
+    assert budget_layers is None or mgr.plan.streamed
+    torch.cuda.synchronize()
+    mgr.release()
+    assert all(u.compiled is None for u in units)
+    torch._dynamo.reset()
+
+
 def test_graph_replay_timing(gpu):
     """offload_timing='cuda_graph': every replay re-times the captured pass (external event nodes)."""
     model = W.build_mlp_stack(6, 512, 1408, seed=41)

@@ -49,7 +49,7 @@ def test_saved_profile_streams_a_fresh_model(gpu, tmp_path):
     assert str(tmp_path) in path and st.loader_type == cfg.transfer_mode
 
     twin = W.build_mlp_stack(8, 256, 704, seed=5)
-    offload_from_profile(twin, cfg, name="profile-dst")
+    offload_from_profile(twin, None, cfg, name="profile-dst")
     from flextensor_amd.manager import get_offload_manager
 
     dst = get_offload_manager("profile-dst")
