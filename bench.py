@@ -509,6 +509,66 @@ def bench_fp8_linear(batch: int = 8, reps: int = 40) -> dict:
                          "frac": round(achieved / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_layer": int(total_bytes)}}
 
 
+def staged_sweep(repeats: int = 5) -> dict:
+    """Host-to-device GB/s from pageable memory: the staged engine by threads and piece size.
+
+    Sources: an ordinary pageable allocation and a POSIX shared-memory mapping
+    (the blocks a shared-offload follower streams from). Beside them:
+    ``hipMemcpyAsync`` straight from the pageable source (the runtime's own
+    staging) and from pinned memory (the link's peak). Each figure is the best
+    of ``repeats`` copies of 512 MiB, timed on the host around the call plus a
+    stream synchronize (the staged copy works on the host while the link runs).
+    """
+    import uuid
+
+    import torch
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import HostArena, current_stream
+    from flextensor_amd.shm import SharedSegment
+
+    dev = torch.device("cuda", 0)
+    n = 512 * MiB
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    s = current_stream(dev)
+    pageable = torch.randint(0, 256, (n,), dtype=torch.uint8)
+    seg = SharedSegment(f"ftbench_{uuid.uuid4().hex[:8]}", n, create=True)
+    shm = torch.frombuffer(seg.buf, dtype=torch.uint8)
+    shm.copy_(pageable)
+    pinned = HostArena(n)
+    pinned.tensor.copy_(pageable)
+
+    def best(src: torch.Tensor, mode: int) -> float:
+        times = []
+        for _ in range(repeats + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            nat.copy_h2d(dst.data_ptr(), src.data_ptr(), n, mode, s.handle)
+            s.synchronize()
+            times.append(time.perf_counter() - t0)
+        return n / min(times[1:]) / 1e9
+
+    piece0, threads0 = nat.get_staging_policy()
+    out: dict = {"bytes": n, "pinned_sdma_GBps": round(best(pinned.tensor, nat.COPY_SDMA), 2),
+                 "pageable_hipMemcpyAsync_GBps": round(best(pageable, nat.COPY_SDMA), 2), "staged": []}
+    try:
+        for piece_mib in (8, 32, 64):
+            for threads in (1, 2, 4, 8, 16):
+                nat.set_staging_policy(piece_mib * MiB, threads)
+                out["staged"].append({"piece_MiB": piece_mib, "threads": threads,
+                                      "pageable_GBps": round(best(pageable, nat.COPY_STAGED), 2),
+                                      "shm_GBps": round(best(shm, nat.COPY_STAGED), 2)})
+                _log(f"staged {piece_mib} MiB x {threads} threads: {out['staged'][-1]}")
+    finally:
+        nat.set_staging_policy(piece0, 0)
+        ok = torch.equal(dst.cpu(), pageable)
+        del shm
+        seg.unlink()
+    out["last_copy_bit_exact"] = bool(ok)
+    out["default_policy"] = {"piece_MiB": piece0 // MiB, "threads": threads0}
+    return out
+
+
 def cpu_llama70b_decode_baseline(batch: int = 8, context: int = 64, steps: int = 2) -> dict:
     """Batch decode of one 70B-shape layer in PyTorch on the host cores, scaled to 80 layers.
 
@@ -714,6 +774,8 @@ def main() -> int:
     ap.add_argument("--skip-dit", action="store_true")
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
+    ap.add_argument("--staged-sweep", action="store_true",
+                    help="only print host-to-device GB/s of the staged engine from pageable and shared memory")
     ap.add_argument("--fp8-linear-only", action="store_true",
                     help="only print the fp8 linear roofline on the 70B-shape decode projections")
     ap.add_argument("--layers-70b", type=int, default=80)
@@ -742,6 +804,9 @@ def main() -> int:
         return 0
     if args.fp8_linear_only:
         print(json.dumps({"fp8_linear": bench_fp8_linear()}), flush=True)
+        return 0
+    if args.staged_sweep:
+        print(json.dumps({"staged_sweep": staged_sweep()}), flush=True)
         return 0
     if args.link_sweep:
         from flextensor_amd.link_model import choose_copy_policy, measure_copy_curve

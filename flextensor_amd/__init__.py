@@ -27,6 +27,7 @@ from .manager import (  # noqa: E402
     save_profile,
 )
 from .profile import TensorManagerState, load_state, save_state  # noqa: E402
+from .shared_offload import SharedOffloadSession  # noqa: E402
 
 __all__ = [
     "DEFAULT_MANAGER_NAME",
@@ -34,6 +35,7 @@ __all__ = [
     "OffloadConfig",
     "OffloadManager",
     "OffloadPhase",
+    "SharedOffloadSession",
     "TensorManagerState",
     "collect_offload_timing",
     "get_gpu_memory_usage",

@@ -28,7 +28,8 @@ FTX_ERR_UNSUPPORTED = 4
 COPY_SDMA = 0
 COPY_KERNEL = 1
 COPY_AUTO = 2
-COPY_MODES = {"sdma": COPY_SDMA, "kernel": COPY_KERNEL, "auto": COPY_AUTO}
+COPY_STAGED = 3
+COPY_MODES = {"sdma": COPY_SDMA, "kernel": COPY_KERNEL, "auto": COPY_AUTO, "staged": COPY_STAGED}
 
 ARENA_DEFAULT = 0
 ARENA_COHERENT = 1
@@ -105,6 +106,9 @@ _SIGNATURES: dict[str, list] = {
     "ftx_scatter_run": [_vp, _vp, _vp],
     "ftx_scatter": [_vp, ctypes.POINTER(FtxDesc), _int, _vp],
     "ftx_checksum64": [_vp, _sz, _vp, ctypes.POINTER(ctypes.c_uint64)],
+    "ftx_set_staging_policy": [_sz, _int],
+    "ftx_get_staging_policy": [ctypes.POINTER(_sz), ctypes.POINTER(_int)],
+    "ftx_host_memcpy": [_vp, _vp, _sz],
     "ftx_fp8_linear_workspace": [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(_sz)],
     "ftx_fp8_linear": [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp, _sz, _vp],
     "ftx_set_fp8_linear_config": [_int, _int],
@@ -274,3 +278,18 @@ def checksum64(dev_ptr: int, nbytes: int, stream: int) -> int:
 def exported_symbols() -> list[str]:
     """Names of the C entry points this binding declares."""
     return ["ftx_last_error", "ftx_version", *_SIGNATURES.keys()]
+
+
+def set_staging_policy(piece_bytes: int, n_threads: int = 0) -> None:
+    call("ftx_set_staging_policy", piece_bytes, n_threads)
+
+
+def get_staging_policy() -> tuple[int, int]:
+    piece, threads = _sz(0), _int(0)
+    call("ftx_get_staging_policy", ctypes.byref(piece), ctypes.byref(threads))
+    return int(piece.value), int(threads.value)
+
+
+def host_memcpy(dst: int, src: int, nbytes: int) -> None:
+    """Parallel host copy of ``nbytes`` (the staged engine's thread pool)."""
+    call("ftx_host_memcpy", dst, src, nbytes)

@@ -101,7 +101,16 @@ class HostPinner:
 
 
 class AllocationBlock:
-    """One label's packed host block (``device="cpu"``) or a GPU ring slot."""
+    """One label's packed host block (``device="cpu"``) or a GPU ring slot.
+
+    With ``shm_block_name`` the host block is a named POSIX shared-memory
+    segment (allocation_block.py:133-158): the creator packs the tensors into
+    a new segment and publishes it; with ``load_from_shm`` a follower maps the
+    published segment and only builds views (its tensors supply shapes,
+    dtypes and strides, not bytes). Such a block is page-locked in place only
+    in ``host_register`` pinning mode; otherwise it stays pageable and its
+    copies go through the staged copy engine.
+    """
 
     def __init__(
         self,
@@ -113,11 +122,19 @@ class AllocationBlock:
         pinned_memory: bool = True,
         memory_alignment: int = DEFAULT_ALIGNMENT,
         release_tensor_memory: bool = False,
+        shm_block_name: str | None = None,
+        load_from_shm: bool = False,
     ) -> None:
+        if load_from_shm and shm_block_name is None:
+            raise ValueError("load_from_shm needs shm_block_name")
         self.manager = manager
         self.device = torch.device(device)
         self.host_pinner = host_pinner
         self.pinned_memory = pinned_memory
+        self.shm_block_name = shm_block_name if self.device.type == "cpu" else None
+        self.load_from_shm = load_from_shm
+        self.shm_segment: Any = None
+        self._shm_pinned_ptr = 0
         self.memory_alignment = _check_alignment(memory_alignment)
         self.release_tensor_memory = release_tensor_memory
         self.tensors: list[torch.Tensor] = []
@@ -148,11 +165,43 @@ class AllocationBlock:
     def add(self, tensor: torch.Tensor) -> None:
         self.tensors.append(tensor)
 
+    @property
+    def is_memory_creator(self) -> bool:
+        return self.shm_block_name is not None and not self.load_from_shm
+
+    def _shm_block(self, total: int) -> torch.Tensor:
+        from .shm import SharedSegment
+
+        size = max(int(total), 1)
+        if self.load_from_shm:
+            seg = SharedSegment(self.shm_block_name)
+            if seg.size < size:
+                have = seg.size
+                seg.close()
+                raise ValueError(f"shared block {self.shm_block_name!r} holds {have} bytes, its tensors need {size}")
+        else:
+            slots, tensors = self.slots, self.tensors
+
+            def fill(buf: memoryview) -> None:
+                pack_into(torch.frombuffer(buf, dtype=torch.uint8), slots, tensors)
+
+            seg = SharedSegment(self.shm_block_name, size, create=True, initializer=fill)
+        self.shm_segment = seg
+        block = torch.frombuffer(seg.buf, dtype=torch.uint8, count=size)
+        if self.pinned_memory and self.host_pinner.enabled and self.host_pinner.mode == "host_register":
+            self.host_pinner.pin_in_place(block)
+            self._shm_pinned_ptr = block.data_ptr()
+        return block
+
     def allocate(self) -> list[torch.Tensor]:
         """Pack the added tensors; returns host views that alias the block."""
         self.slots, total = plan_block(self.tensors, self.memory_alignment)
-        self.block = self._new_block(total)
-        self.views = pack_into(self.block, self.slots, self.tensors)
+        if self.shm_block_name is not None:
+            self.block = self._shm_block(total)
+            self.views = [s.view(self.block) for s in self.slots]
+        else:
+            self.block = self._new_block(total)
+            self.views = pack_into(self.block, self.slots, self.tensors)
         if self.release_tensor_memory:
             for t in self.tensors:
                 t.data = torch.empty(0, dtype=t.dtype)
@@ -185,6 +234,16 @@ class AllocationBlock:
         self.views = []
         self.slots = []
         self.tensors = []
+        seg, self.shm_segment = self.shm_segment, None
+        if seg is not None:
+            if self._shm_pinned_ptr:
+                # a registered mapping must be unregistered before it can be unmapped
+                self.host_pinner.release(self._shm_pinned_ptr)
+                self._shm_pinned_ptr = 0
+            # The creator removes the name; other processes' mappings stay valid. The
+            # mapping itself is not closed here: tensors (restored parameters, user
+            # references) may still view it, and it is unmapped with the last of them.
+            seg.unlink()
 
 
 def _current(device: torch.device):
@@ -210,7 +269,8 @@ class AllocationManager:
         self.memory_alignment = memory_alignment
         self.release_tensor_memory = release_tensor_memory
 
-    def block(self, device: str | torch.device = "cpu") -> AllocationBlock:
+    def block(self, device: str | torch.device = "cpu", *, shm_block_name: str | None = None,
+              load_from_shm: bool = False) -> AllocationBlock:
         b = AllocationBlock(
             self,
             device=device,
@@ -218,6 +278,8 @@ class AllocationManager:
             pinned_memory=self.pinned_memory,
             memory_alignment=self.memory_alignment,
             release_tensor_memory=self.release_tensor_memory,
+            shm_block_name=shm_block_name,
+            load_from_shm=load_from_shm,
         )
         self.blocks.append(b)
         return b

@@ -7,8 +7,11 @@ Kept from config.py:55-402: ``enabled``, ``gpu_device``, ``pinned_memory``,
 ``exclude_patterns``, ``profile_storage_dir``. ``FT_*`` environment variables
 override fields (config.py:1012).
 
+Also kept: ``shm_enabled``, ``shm_namespace``, ``shm_wait_timeout``
+(config.py:97-125).
+
 Added for this build: ``max_gpu_mem_bytes`` (a budget in bytes instead of a
-fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel``),
+fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel`` / ``staged``),
 ``loader_order`` (``auto`` / ``default`` / ``reordered``) and
 ``max_inflight_passes`` (bounded host run-ahead).
 """
@@ -43,18 +46,25 @@ class OffloadConfig(BaseModel):
     include_patterns: list[str] = Field(default_factory=lambda: ["*"])
     exclude_patterns: list[str] = Field(default_factory=list)
     profile_storage_dir: str | None = None
-    copy_engine: Literal["auto", "sdma", "kernel"] = "auto"
+    copy_engine: Literal["auto", "sdma", "kernel", "staged"] = "auto"
     loader_order: Literal["auto", "default", "reordered"] = "auto"
     # Before the host enqueues a streamed forward it waits until the forward
     # this many passes back has finished on the device (0: never waits). A host
     # that runs further ahead fills the device command queue and then issues
     # each next transfer late, which idles the host link.
     max_inflight_passes: int = Field(default=1, ge=0)
+    # Cross-process sharing of the streamed blocks through POSIX shared memory
+    # (config.py:97-125): blocks live in named segments under ``shm_namespace``.
+    shm_enabled: bool = False
+    shm_namespace: str | None = None
+    shm_wait_timeout: float = Field(default=0.0, ge=0.0)
 
     @model_validator(mode="after")
     def _check(self) -> "OffloadConfig":
         if self.transfer_mode not in TRANSFER_MODES:
             raise ValueError(f"transfer_mode must be one of {TRANSFER_MODES}, got {self.transfer_mode!r}")
+        if self.shm_enabled and (self.shm_namespace is None or not self.shm_namespace.strip()):
+            raise ValueError("shm_namespace must be non-empty when shm_enabled=True")
         return self
 
 

@@ -76,11 +76,20 @@ class AllocationBlockController:
         release_tensor_memory: bool = True,
         copy_mode: int = nat.COPY_AUTO,
         memory_alignment: int = 128,
+        shm_block_name_map: Mapping[str, str] | None = None,
+        load_from_shm: bool = False,
     ) -> None:
+        """``shm_block_name_map`` puts each label's host block in a named shared-memory
+        segment (loaders.py:1150-1175); with ``load_from_shm`` the segments already exist
+        and are mapped instead of packed, and the tensors only supply their layouts."""
+        if load_from_shm and not shm_block_name_map:
+            raise ValueError("load_from_shm needs shm_block_name_map")
         self.device_gpu = torch.device(device_gpu)
         self.host_pinner = host_pinner
         self.release_tensor_memory = release_tensor_memory
         self.copy_mode = copy_mode
+        self.shm_block_name_map = dict(shm_block_name_map or {})
+        self.load_from_shm = load_from_shm
         self.block_map_cpu: dict[str, AllocationBlock] = {}
         self.label_to_cpu_tensor_id_map: dict[str, list[int]] = {}
         self.label_to_gpu_block: dict[str, AllocationBlock] = {}
@@ -99,7 +108,10 @@ class AllocationBlockController:
                     if not strategy:
                         continue
                     ids, tensors = _unique_tensors(strategy, tensors_map)
-                    block = manager.block()
+                    shm_name = self.shm_block_name_map.get(label)
+                    if self.shm_block_name_map and shm_name is None:
+                        raise ValueError(f"no shared-memory block name for label {label!r}")
+                    block = manager.block(shm_block_name=shm_name, load_from_shm=load_from_shm)
                     for t in tensors:
                         block.add(t)
                     views = block.allocate()
@@ -158,6 +170,9 @@ class AllocationBlockController:
 
     def shutdown(self) -> None:
         self._rollback.restore()
+        for block in self.block_map_cpu.values():
+            if block.shm_segment is not None:
+                block.release()  # unmaps; the creator also removes the segment's name
         self._clear()
 
     def release_gpu_blocks(self) -> None:

@@ -67,6 +67,13 @@ constexpr size_t kFp8LinearMaxLds = 64 * 1024;
 Fp8LinearLaunch plan_fp8_linear(int64_t m, int64_t n, int64_t k, int cus, int waves, int kc);
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream);
 
+// Staged copies from pageable host memory and the parallel host memcpy
+// (ftx_staged.hip).
+int staged_copy_h2d(void *dst, const void *src, size_t nbytes, hipStream_t stream);
+int host_memcpy(void *dst, const void *src, size_t nbytes);
+int set_staging_policy(size_t piece_bytes, int threads);
+void get_staging_policy(size_t *piece_bytes, int *threads);
+
 // Kernel launchers (ftx_kernels.hip). Each returns hipSuccess or the launch error.
 hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid,
                             hipStream_t stream);

@@ -579,12 +579,39 @@ int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stre
       return ftx::copy_sdma(dst, src, nbytes, s, pol);
     case FTX_COPY_KERNEL:
       return ftx::copy_kernel(dst, src, nbytes, s, pol, false);
-    case FTX_COPY_AUTO:
+    case FTX_COPY_STAGED: {
+      int rc = ftx::check_device_range(dst, nbytes, "copy destination");
+      if (rc != FTX_OK) return rc;
+      return ftx::staged_copy_h2d(dst, src, nbytes, s);
+    }
+    case FTX_COPY_AUTO: {
+      const void *mapped = nullptr;
+      if (ftx::mapped_source(src, nbytes, &mapped) != FTX_OK) {  // pageable: stage it
+        int rc = ftx::check_device_range(dst, nbytes, "copy destination");
+        if (rc != FTX_OK) return rc;
+        return ftx::staged_copy_h2d(dst, src, nbytes, s);
+      }
       if (nbytes <= pol.kernel_max_bytes) return ftx::copy_kernel(dst, src, nbytes, s, pol, true);
       return ftx::copy_sdma(dst, src, nbytes, s, pol);
+    }
     default:
       return ftx::fail(FTX_ERR_INVALID, "unknown copy mode");
   }
+}
+
+int ftx_set_staging_policy(size_t piece_bytes, int n_threads) { return ftx::set_staging_policy(piece_bytes, n_threads); }
+
+int ftx_get_staging_policy(size_t *piece_bytes, int *n_threads) {
+  ftx::get_staging_policy(piece_bytes, n_threads);
+  return FTX_OK;
+}
+
+int ftx_host_memcpy(void *dst, const void *src, size_t nbytes) {
+  if (nbytes == 0) return FTX_OK;
+  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  const uintptr_t d = reinterpret_cast<uintptr_t>(dst), sp = reinterpret_cast<uintptr_t>(src);
+  if (d < sp + nbytes && sp < d + nbytes) return ftx::fail(FTX_ERR_INVALID, "host copy ranges overlap");
+  return ftx::host_memcpy(dst, src, nbytes);
 }
 
 int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams, int kernel_grid) {

@@ -333,12 +333,14 @@ class OffloadManager:
         self._pass_done: list[Any] = []  # completion events of the latest streamed passes
         self.build_seconds = 0.0
         self.compile_fn: Callable[[nn.Module], Any] | None = None
+        self._load_from_shm = False
 
     # -- public ---------------------------------------------------------------
 
     def offload(self, model: nn.Module, config: OffloadConfig | None = None,
                 state: TensorManagerState | None = None,
-                compile_fn: Callable[[nn.Module], Any] | None = None) -> nn.Module:
+                compile_fn: Callable[[nn.Module], Any] | None = None, *,
+                load_from_shm: bool = False) -> nn.Module:
         """Patch ``model``; with a saved ``state`` the plan is restored and streaming starts at once.
 
         ``compile_fn`` is the reference's per-unit compiler (offload_manager.py:2858-2884): at the
@@ -351,8 +353,11 @@ class OffloadManager:
             raise RuntimeError(f"offload manager {self.name!r} already manages a model; release() it first")
         if compile_fn is not None and not callable(compile_fn):
             raise TypeError("compile_fn must be callable: module -> compiled module")
-        self.compile_fn = compile_fn
         self.config = config or OffloadConfig()
+        if load_from_shm and (state is None or not self.config.shm_enabled or not state.shm_block_name_map):
+            raise ValueError("load_from_shm needs shm_enabled and a saved state that names its shared blocks")
+        self.compile_fn = compile_fn
+        self._load_from_shm = load_from_shm
         if not self.config.enabled:
             return model
         nat.load()
@@ -455,8 +460,12 @@ class OffloadManager:
     def state(self) -> TensorManagerState:
         """The plan as a :class:`TensorManagerState` keyed by this process's tensor ids."""
         assert self.model is not None and self.plan is not None
-        return state_from_plan(self.model, [self._unit(x) for x in self.order], self.plan,
-                               {x: self._duration(x) for x in self.order}, self.config.transfer_mode)
+        state = state_from_plan(self.model, [self._unit(x) for x in self.order], self.plan,
+                                {x: self._duration(x) for x in self.order}, self.config.transfer_mode)
+        names = getattr(self.controller, "shm_block_name_map", None)
+        if names:
+            state.shm_block_name_map = dict(names)
+        return state
 
     def _duration(self, label: str) -> float:
         d = self.durations.get(label, [])
@@ -493,6 +502,7 @@ class OffloadManager:
         for u in self.units:
             u.compiled = None
         self.compile_fn = None
+        self._load_from_shm = False
         restore = {}
         if self.controller is not None and preserve_model:
             for label in self.controller.block_map_cpu:
@@ -720,9 +730,20 @@ class OffloadManager:
                                                      plan.strategy_map, bd.label_to_block_id, host_pinner=pinner,
                                                      copy_mode=mode)
             else:
+                shm_names: dict[str, str] | None = None
+                if cfg.shm_enabled:
+                    if self._load_from_shm:
+                        assert state is not None and state.shm_block_name_map
+                        shm_names = dict(state.shm_block_name_map)
+                    else:
+                        labels = [x for group in bd.allocation_ordered.values() for x in group
+                                  if plan.strategy_map.get(x)]
+                        shm_names = {x: f"{cfg.shm_namespace}_b{i}" for i, x in enumerate(labels)}
                 self.controller = AllocationBlockController(bd.allocation_ordered, self.device, tensors_map,
                                                             plan.strategy_map, bd.label_to_block_id,
-                                                            host_pinner=pinner, copy_mode=mode)
+                                                            host_pinner=pinner, copy_mode=mode,
+                                                            shm_block_name_map=shm_names,
+                                                            load_from_shm=self._load_from_shm)
             for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
                 tensors_map[tid].data = view
             reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"

@@ -137,19 +137,31 @@ class SharedSegment:
             self._buf.release()
             self._buf = None
         if self._mmap is not None:
-            self._mmap.close()  # BufferError while a tensor still views the mapping
+            self._mmap.close()  # unmaps: callers make sure no tensor views the mapping any more
             self._mmap = None
 
-    def close(self) -> None:
-        """Unmap; the creator also removes the name. Idempotent."""
-        if self._mmap is None:
-            return
-        self._unmap()
+    def unlink(self) -> None:
+        """The creator removes the name (other processes' mappings stay valid). Idempotent."""
         if self.creator:
+            self.creator = False
             try:
                 os.unlink(self.path)
             except FileNotFoundError:
                 pass
+
+    def close(self) -> None:
+        """The creator removes the name, then the mapping is closed. Idempotent.
+
+        Only for segments no tensor views any more: ``torch.frombuffer`` keeps
+        the buffer object alive but not its export, so closing would unmap
+        memory that live tensors still point at. Owners of tensor views call
+        :meth:`unlink` and drop the segment instead; the mapping then goes
+        away with the last tensor that references it.
+        """
+        if self._mmap is None:
+            return
+        self.unlink()
+        self._unmap()
 
 
 # ---- store format ---------------------------------------------------------------

@@ -40,7 +40,8 @@ extern "C" {
  * same CUs, so FTX_COPY_AUTO keeps it to small chunks. */
 #define FTX_COPY_SDMA 0   /* hipMemcpyAsync, optionally split over copy streams   */
 #define FTX_COPY_KERNEL 1 /* zero-copy kernel: CUs read mapped pinned host memory */
-#define FTX_COPY_AUTO 2   /* pick per chunk from the policy set by ftx_set_copy_policy */
+#define FTX_COPY_AUTO 2   /* pageable source: FTX_COPY_STAGED; pinned: per chunk from ftx_set_copy_policy */
+#define FTX_COPY_STAGED 3 /* pageable source staged through pinned buffers by a host thread pool */
 
 /* ---- host arena flags -------------------------------------------------- */
 #define FTX_ARENA_DEFAULT 0u
@@ -138,6 +139,21 @@ int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_c
                         int kernel_grid);
 int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams,
                         int *kernel_grid);
+
+/* ---- staged copies from pageable host memory ------------------------------
+ * Replace the reference's copy from pageable or shared-memory blocks that are
+ * not page-locked (pinned_memory=False blocks, allocation_block.py:104-106 with
+ * an unpinned source; FlexibleSharedMemory blocks without in-place
+ * registration, shm/flexible_shm.py:832-848): FTX_COPY_STAGED copies the
+ * source in pieces of `piece_bytes` into two page-locked staging buffers per
+ * device with `n_threads` host threads, each piece then crossing the link by
+ * SDMA while the next one is copied. The call returns once the last piece is
+ * enqueued; the source may be reused then. Staged copies are refused on a
+ * capturing stream. ftx_host_memcpy is the same thread pool's parallel host
+ * copy (no overlap allowed). n_threads 0 = half the host's cores, at most 8. */
+int ftx_set_staging_policy(size_t piece_bytes, int n_threads);
+int ftx_get_staging_policy(size_t *piece_bytes, int *n_threads);
+int ftx_host_memcpy(void *dst, const void *src, size_t nbytes);
 
 /* ---- batched scatter / unpack --------------------------------------------
  * No reference counterpart; it places a streamed chunk into many tensors in
