@@ -9,25 +9,47 @@ hipEvent gating.
 
 __version__ = "0.1.0"
 
-from .config import OffloadConfig, load_config_from_env  # noqa: E402
+from .config import (  # noqa: E402
+    OffloadConfig,
+    PinnedMemoryMode,
+    load_config,
+    load_config_from_env,
+    load_config_from_file,
+)
 from .manager import (  # noqa: E402
     DEFAULT_MANAGER_NAME,
     GPUMemoryUsage,
     OffloadManager,
     OffloadPhase,
+    clear_profiling_durations,
     collect_offload_timing,
     get_gpu_memory_usage,
     get_offload_manager,
+    init,
     load_profile,
     offload,
     offload_from_profile,
     offload_from_state,
+    offload_units,
+    pause_profiling,
     release,
     reset_offload_timing,
+    resident_units,
+    resume_profiling,
     save_profile,
+    set_config,
+    suspend_profiling,
+    update_offload_timing,
+    update_state,
 )
 from .profile import TensorManagerState, load_state, save_state  # noqa: E402
-from .shared_offload import SharedOffloadSession  # noqa: E402
+from .shared_offload import (  # noqa: E402
+    SharedOffloadSession,
+    ShmCoordinatorError,
+    ShmCreatorDiedError,
+    ShmCreatorFailedError,
+)
+from .timing import OffloadTimingReport, OffloadTimingSnapshot, format_offload_timing_table  # noqa: E402
 
 __all__ = [
     "DEFAULT_MANAGER_NAME",
@@ -35,19 +57,38 @@ __all__ = [
     "OffloadConfig",
     "OffloadManager",
     "OffloadPhase",
+    "OffloadTimingReport",
+    "OffloadTimingSnapshot",
+    "PinnedMemoryMode",
     "SharedOffloadSession",
+    "ShmCoordinatorError",
+    "ShmCreatorDiedError",
+    "ShmCreatorFailedError",
     "TensorManagerState",
+    "clear_profiling_durations",
     "collect_offload_timing",
+    "format_offload_timing_table",
     "get_gpu_memory_usage",
     "get_offload_manager",
+    "init",
+    "load_config",
     "load_config_from_env",
+    "load_config_from_file",
     "load_profile",
     "load_state",
     "offload",
     "offload_from_profile",
     "offload_from_state",
+    "offload_units",
+    "pause_profiling",
     "release",
     "reset_offload_timing",
+    "resident_units",
+    "resume_profiling",
     "save_profile",
     "save_state",
+    "set_config",
+    "suspend_profiling",
+    "update_offload_timing",
+    "update_state",
 ]

@@ -4,8 +4,10 @@ Kept from config.py:55-402: ``enabled``, ``gpu_device``, ``pinned_memory``,
 ``pinned_memory_mode``, ``discovery_iters``, ``profiling_iters``,
 ``transfer_mode``, ``num_blocks``, ``min_blocks``, ``max_gpu_mem_fraction``,
 ``offload_timing``, ``piecewise_prefetch``, ``include_patterns``,
-``exclude_patterns``, ``profile_storage_dir``. ``FT_*`` environment variables
-override fields (config.py:1012).
+``exclude_patterns``, ``profile_storage_dir``. :func:`load_config`,
+:func:`load_config_from_file` and :func:`load_config_from_env` read INI, JSON
+or YAML files and ``FT_*`` environment variables with the reference's
+precedence and text conversions (config.py:560-1060).
 
 Also kept: ``shm_enabled``, ``shm_namespace``, ``shm_wait_timeout``
 (config.py:97-125).
@@ -18,9 +20,16 @@ fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel`` / ``staged``),
 
 from __future__ import annotations
 
+import configparser
+import difflib
 import json
 import os
+import types
+import typing
+from pathlib import Path
 from typing import Any, Literal
+
+import yaml
 
 from pydantic import BaseModel, ConfigDict, Field, model_validator
 
@@ -68,18 +77,161 @@ class OffloadConfig(BaseModel):
         return self
 
 
-def _coerce(value: str) -> Any:
-    try:
-        return json.loads(value)
-    except json.JSONDecodeError:
-        return value
+PinnedMemoryMode = Literal["torch", "host_register"]
 
 
-def load_config_from_env(prefix: str = "FT_", base: OffloadConfig | None = None) -> OffloadConfig:
-    """``base`` (or defaults) with fields overridden by ``<prefix><FIELD>`` variables."""
-    data = base.model_dump() if base is not None else {}
-    for name in OffloadConfig.model_fields:
-        raw = os.environ.get(prefix + name.upper())
-        if raw is not None:
-            data[name] = _coerce(raw)
+# ---- loading from files and the environment (config.py:560-1060) ------------------
+
+
+def _field_kind(annotation: Any) -> type:
+    """The conversion type of a field: bool/int/float/str, list, or object (not loadable from text)."""
+    if annotation is None:
+        return str
+    origin = typing.get_origin(annotation)
+    if origin in (typing.Union, types.UnionType):
+        kinds = [_field_kind(a) for a in typing.get_args(annotation) if a is not type(None)]
+        return kinds[0] if kinds else str
+    if origin is list:
+        return list
+    if origin is Literal:
+        first = typing.get_args(annotation)[0] if typing.get_args(annotation) else ""
+        return type(first) if type(first) in (bool, int, float, str) else str
+    if annotation in (bool, int, float, str):
+        return annotation
+    return object
+
+
+def _field_kinds() -> dict[str, type]:
+    return {name: _field_kind(f.annotation) for name, f in OffloadConfig.model_fields.items()}
+
+
+def _parse_bool(value: str) -> bool:
+    low = value.lower()
+    if low in ("true", "1", "yes", "y", "on"):
+        return True
+    if low in ("false", "0", "no", "n", "off"):
+        return False
+    raise ValueError(f"Cannot parse '{value}' as boolean")
+
+
+def _convert(value: str, kind: type) -> Any:
+    """Text -> field value: ``none``/``null``/empty is None, then by the field's type."""
+    if value == "" or value.lower() in ("none", "null"):
+        return None
+    if kind is bool:
+        return _parse_bool(value)
+    if kind is int:
+        return int(value)
+    if kind is float:
+        return float(value)
+    return value
+
+
+def _split_list(value: str) -> list[str]:
+    return [p.strip() for p in value.split(",") if p.strip()]
+
+
+def _from_mapping(data: dict[str, Any], kinds: dict[str, type]) -> dict[str, Any]:
+    out: dict[str, Any] = {}
+    for name, value in data.items():
+        kind = kinds.get(name)
+        if kind is None or kind is object:
+            continue
+        if kind is not list and kind is not str and isinstance(value, str):
+            out[name] = _convert(value, kind)
+        else:
+            out[name] = value
+    return out
+
+
+def _load_file(path: Path, kinds: dict[str, type]) -> dict[str, Any]:
+    suffix = path.suffix.lower()
+    if suffix in (".conf", ".ini"):
+        parser = configparser.ConfigParser()
+        parser.read(path)
+        if "flextensor" not in parser:
+            raise ValueError("INI file must contain [flextensor] section")
+        sec = parser["flextensor"]
+        out: dict[str, Any] = {}
+        for name, kind in kinds.items():
+            if name in sec and kind is not object:
+                out[name] = _split_list(sec[name]) if kind is list else _convert(sec[name], kind)
+        return out
+    if suffix == ".json":
+        with path.open() as fh:
+            data = json.load(fh)
+    elif suffix in (".yaml", ".yml"):
+        with path.open() as fh:
+            data = yaml.safe_load(fh) or {}
+    else:
+        raise ValueError(f"Unsupported config file format: {suffix}. Use .conf, .ini, .json, .yaml, or .yml")
+    if not isinstance(data, dict):
+        raise ValueError(f"config file {path} must hold a mapping")
+    return _from_mapping(data, kinds)
+
+
+def _load_env(prefix: str, kinds: dict[str, type], config_file_env_var: str) -> dict[str, Any]:
+    if prefix:
+        known = {f"{prefix}{n.upper()}" for n in kinds} | {f"{prefix}CONFIG_FILE"}
+        if config_file_env_var:
+            known.add(config_file_env_var)
+        errors = []
+        for var in sorted(v for v in os.environ if v.startswith(prefix) and v not in known):
+            msg = f"Unrecognized environment variable with {prefix} prefix: {var}"
+            close = difflib.get_close_matches(var, sorted(known), n=1, cutoff=0.75)
+            errors.append(msg + (f". Did you mean: {close[0]}?" if close else ""))
+        if errors:
+            raise ValueError("\n".join(errors))
+    out: dict[str, Any] = {}
+    for name, kind in kinds.items():
+        if kind is object:
+            continue
+        var = f"{prefix}{name.upper()}"
+        raw = os.environ.get(var)
+        if raw is None:
+            continue
+        try:
+            out[name] = _split_list(raw) if kind is list else _convert(raw, kind)
+        except (ValueError, TypeError) as exc:
+            raise ValueError(f"Failed to convert {var}={raw}: {exc}") from exc
+    return out
+
+
+def load_config(config_path: str | os.PathLike | None = None, env_prefix: str = "FT_", use_env: bool = True,
+                config_file_env_var: str = "FT_CONFIG_FILE", **kwargs: Any) -> OffloadConfig:
+    """``OffloadConfig`` from a file, then ``FT_*`` variables, then ``kwargs`` (config.py:900-969).
+
+    Files: INI (``.conf``/``.ini``, section ``[flextensor]``), JSON or YAML.
+    With no file, ``enabled`` defaults to False: offloading from the
+    environment alone needs ``FT_ENABLED=1``. List fields take
+    comma-separated text; ``none``/``null`` is None; booleans accept
+    true/false, 1/0, yes/no, y/n, on/off.
+    """
+    kinds = _field_kinds()
+    data: dict[str, Any] = {}
+    path = config_path if config_path is not None else (os.environ.get(config_file_env_var)
+                                                         if config_file_env_var else None)
+    if path is not None:
+        p = Path(path)
+        if not p.exists():
+            raise FileNotFoundError(f"Config file not found: {p}")
+        data = _load_file(p, kinds)
+    elif use_env:
+        data["enabled"] = False
+    if use_env:
+        data.update(_load_env(env_prefix, kinds, config_file_env_var))
+    data.update(kwargs)
     return OffloadConfig(**data)
+
+
+def load_config_from_file(config_path: str | os.PathLike | None = None, env_var: str = "FT_CONFIG_FILE",
+                          **kwargs: Any) -> OffloadConfig:
+    """File values, then ``kwargs``; no environment overrides (config.py:972-1009)."""
+    if config_path is None and os.environ.get(env_var) is None:
+        raise FileNotFoundError(f"No config file specified. Provide config_path or set {env_var} environment variable.")
+    return load_config(config_path=config_path, use_env=False, config_file_env_var=env_var, **kwargs)
+
+
+def load_config_from_env(prefix: str = "FT_", **kwargs: Any) -> OffloadConfig:
+    """``<prefix><FIELD>`` variables, then ``kwargs``; ``enabled`` defaults to False (config.py:1012-1059)."""
+    return load_config(config_path=None, env_prefix=prefix, use_env=True, config_file_env_var="", **kwargs)

@@ -24,13 +24,14 @@ the pass; slots are added while the slot-reuse check of the reference
 
 from __future__ import annotations
 
+import contextlib
 import fnmatch
 import logging
 import os
 import re
 import threading
 import time
-from collections.abc import Callable, Sequence
+from collections.abc import Callable, Iterator, Sequence
 from dataclasses import dataclass, field
 from enum import Enum
 from typing import Any
@@ -334,6 +335,7 @@ class OffloadManager:
         self.build_seconds = 0.0
         self.compile_fn: Callable[[nn.Module], Any] | None = None
         self._load_from_shm = False
+        self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
 
     # -- public ---------------------------------------------------------------
 
@@ -486,6 +488,67 @@ class OffloadManager:
     def reset_offload_timing(self) -> None:
         if self.timing is not None:
             self.timing.reset()
+
+    def init(self, config: OffloadConfig | None = None) -> None:
+        """Set the configuration before ``offload`` (offload_manager.py:2853-2856)."""
+        self.set_config(config or OffloadConfig())
+
+    def set_config(self, config: OffloadConfig) -> None:
+        """Replace the configuration; refused once a model is managed (offload_manager.py:2887-2895)."""
+        self._check_thread()
+        if self.model is not None:
+            raise RuntimeError(f"offload manager {self.name!r} already manages a model; release() it before "
+                               "changing its configuration")
+        self.config = config
+
+    def offload_units(self) -> tuple[tuple[str, nn.Module], ...]:
+        """Streamed offload units as ``(qualified_name, module)`` (offload_manager.py:3075-3080)."""
+        names = set(self.plan.streamed) if self.plan is not None else {u.label for u in self.units}
+        return tuple((u.label, u.module) for u in self.units if u.label in names)
+
+    def resident_units(self) -> tuple[tuple[str, nn.Module], ...]:
+        """Offload units that stayed on the GPU as ``(qualified_name, module)`` (offload_manager.py:3083-3088)."""
+        names = set(self.plan.resident) if self.plan is not None else set()
+        return tuple((u.label, u.module) for u in self.units if u.label in names)
+
+    def clear_profiling_durations(self) -> None:
+        """Drop every profiled duration; the unit order found by discovery stays (offload_manager.py:3131-3141)."""
+        self.durations.clear()
+
+    def suspend_profiling(self) -> None:
+        """Stop recording profiling passes until the matching :meth:`resume_profiling`.
+
+        Suspensions nest. A suspended profiling pass records no durations and
+        does not count against ``profiling_iters`` (offload_manager.py:3144-3184).
+        """
+        self._suspend_count += 1
+
+    def resume_profiling(self) -> None:
+        if self._suspend_count == 0:
+            raise RuntimeError("resume_profiling() without a matching suspend_profiling()")
+        self._suspend_count -= 1
+
+    @contextlib.contextmanager
+    def pause_profiling(self) -> Iterator[None]:
+        """Context-manager form of suspend/resume (offload_manager.py:3199-3220)."""
+        self.suspend_profiling()
+        try:
+            yield
+        finally:
+            self.resume_profiling()
+
+    def update_state(self) -> None:
+        """Advance the phase machine by one pass, as the post-forward hook does (offload_manager.py:3110-3123).
+
+        For passes the hook does not see, such as graph replays.
+        """
+        self._after_forward()
+
+    def update_offload_timing(self) -> bool:
+        """Store the current timing pass (offload_manager.py:3061-3072); True when stored or timing is off."""
+        if self.timing is not None and self.timing.enabled:
+            self.timing.flush()
+        return True
 
     def release(self, preserve_model: bool = True) -> None:
         """Stop streaming and hand the model back (tensors on the CPU when preserved)."""
@@ -673,6 +736,11 @@ class OffloadManager:
                 self._pass_done.append(HipEvent().record(current_stream(self.device)))
                 del self._pass_done[: -self.config.max_inflight_passes]
             return
+        if self.phase == OffloadPhase.PROFILING and self._suspend_count:
+            # a suspended profiling pass records no durations and does not use up profiling_iters
+            self._events.clear()
+            self._seen_this_pass = []
+            return
         self._forwards += 1
         if self.phase == OffloadPhase.DISCOVERY:
             if not self.order:
@@ -800,6 +868,48 @@ def offload(model: nn.Module, config: OffloadConfig | None = None, name: str = D
     (offload_manager.py:2858-2884).
     """
     return get_offload_manager(name).offload(model, config, compile_fn=compile_fn)
+
+
+def init(config: OffloadConfig | None = None, name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).init(config)
+
+
+def set_config(config: OffloadConfig, name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).set_config(config)
+
+
+def offload_units(name: str = DEFAULT_MANAGER_NAME) -> tuple[tuple[str, nn.Module], ...]:
+    return get_offload_manager(name).offload_units()
+
+
+def resident_units(name: str = DEFAULT_MANAGER_NAME) -> tuple[tuple[str, nn.Module], ...]:
+    return get_offload_manager(name).resident_units()
+
+
+def clear_profiling_durations(name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).clear_profiling_durations()
+
+
+def suspend_profiling(name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).suspend_profiling()
+
+
+def resume_profiling(name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).resume_profiling()
+
+
+@contextlib.contextmanager
+def pause_profiling(name: str = DEFAULT_MANAGER_NAME) -> Iterator[None]:
+    with get_offload_manager(name).pause_profiling():
+        yield
+
+
+def update_state(name: str = DEFAULT_MANAGER_NAME) -> None:
+    get_offload_manager(name).update_state()
+
+
+def update_offload_timing(name: str = DEFAULT_MANAGER_NAME) -> bool:
+    return get_offload_manager(name).update_offload_timing()
 
 
 def release(name: str = DEFAULT_MANAGER_NAME, preserve_model: bool = True) -> None:

@@ -114,6 +114,50 @@ class OffloadTimingReport:
         return "\n".join(lines)
 
 
+def format_offload_timing_table(data: OffloadTimingSnapshot | OffloadTimingReport) -> str:
+    """A text table of one pass or of a report (offload_timing.py:220-300).
+
+    One row per trap: compute, transfer and wait milliseconds (averages and
+    medians for a report). A row whose wait exceeds 0.01 ms is flagged: its
+    transfer was not hidden.
+    """
+    if isinstance(data, OffloadTimingReport):
+        stats = data.per_trap_stats()
+        if not stats:
+            return "No offload timing data."
+        w = max(max(len(st.label) for st in stats), 5) + 2
+        rule = "=" * (w + 74)
+        lines = [f"Offload Timing ({data.num_passes} passes)", rule,
+                 f"{'Trap':<{w}} {'Compute avg':>12} {'med':>8}  {'Transfer avg':>13} {'med':>8}  "
+                 f"{'Wait avg':>9} {'med':>8}", "-" * (w + 74)]
+        for st in stats:
+            flag = "  <-" if st.wait_avg > 0.01 else ""
+            lines.append(f"{st.label:<{w}} {st.compute_avg:>12.3f} {st.compute_median:>8.3f}  "
+                         f"{st.transfer_avg:>13.3f} {st.transfer_median:>8.3f}  "
+                         f"{st.wait_avg:>9.3f} {st.wait_median:>8.3f}{flag}")
+        n = max(data.num_passes, 1)
+        lines += ["-" * (w + 74),
+                  f"{'Avg/pass':<{w}} {data.total_compute_sum / n:>12.3f} {'':>8}  "
+                  f"{data.total_transfer_sum / n:>13.3f} {'':>8}  {data.total_wait_sum / n:>9.3f}",
+                  f"{'Sum (all)':<{w}} {data.total_compute_sum:>12.1f} {'':>8}  "
+                  f"{data.total_transfer_sum:>13.1f} {'':>8}  {data.total_wait_sum:>9.1f}",
+                  f"hidden fraction {data.hidden_fraction:.4f}", rule]
+        return "\n".join(lines)
+    if not data.per_trap:
+        return "No offload timing data."
+    w = max(max(len(r.label) for r in data.per_trap), 5) + 2
+    rule = "=" * (w + 46)
+    lines = ["Offload Timing (single pass)", rule,
+             f"{'Trap':<{w}} {'Compute (ms)':>13} {'Transfer (ms)':>14} {'Wait (ms)':>10}", "-" * (w + 46)]
+    for r in data.per_trap:
+        flag = "  <-" if r.wait_ms > 0.01 else ""
+        lines.append(f"{r.label:<{w}} {r.compute_ms:>13.3f} {r.transfer_ms:>14.3f} {r.wait_ms:>10.3f}{flag}")
+    lines += ["-" * (w + 46),
+              f"{'Total':<{w}} {data.total_compute_ms:>13.3f} {data.total_transfer_ms:>14.3f} "
+              f"{data.total_wait_ms:>10.3f}", rule]
+    return "\n".join(lines)
+
+
 class OffloadTimingCollector:
     """Records per-trap events during a pass; a no-op when ``enabled`` is False.
 

@@ -1,0 +1,54 @@
+"""The reference's convenience API on a streamed model (GPU).
+
+``offload_units`` / ``resident_units`` report the plan, ``pause_profiling``
+keeps warm-up passes out of the profile and the phase count
+(offload_manager.py:3075-3220), and the configuration is fixed once a model
+is managed.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+import flextensor_amd as ft
+from flextensor_amd import workloads as W
+from flextensor_amd.config import OffloadConfig
+from flextensor_amd.manager import OffloadPhase
+
+pytestmark = pytest.mark.gpu
+
+
+def test_units_profiling_pause_and_fixed_config(gpu):
+    model = W.build_mlp_stack(8, 256, 704, seed=91)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=2, max_gpu_mem_bytes=5 * layer)
+    name = "api-test"
+    ft.offload(model, cfg, name=name)
+    mgr = ft.get_offload_manager(name)
+    x = W.mlp_input(16, 256, seed=91).to(gpu)
+    with torch.no_grad():
+        model(x)  # discovery
+        assert mgr.phase == OffloadPhase.PROFILING
+        with ft.pause_profiling(name):
+            for _ in range(4):  # warm-up passes: not recorded, not counted
+                model(x)
+        assert mgr.phase == OffloadPhase.PROFILING and not mgr.durations
+        model(x)
+        assert mgr.phase == OffloadPhase.PROFILING and all(len(v) == 1 for v in mgr.durations.values())
+        model(x)  # second recorded profiling pass: streaming starts
+        assert mgr.phase == OffloadPhase.INFERENCE
+        assert torch.equal(model(x), resident(x))
+    streamed = [label for label, _ in ft.offload_units(name)]
+    kept = [label for label, _ in ft.resident_units(name)]
+    assert streamed == mgr.plan.streamed and kept == mgr.plan.resident
+    assert streamed and kept and sorted(streamed + kept) == sorted(f"layers.{i}" for i in range(8))
+    assert all(mod is model.get_submodule(label) for label, mod in ft.offload_units(name))
+    with pytest.raises(RuntimeError, match="release"):
+        ft.set_config(OffloadConfig(), name=name)
+    assert ft.update_offload_timing(name) is True  # timing is off: nothing to store
+    ft.release(name)

@@ -35,9 +35,10 @@ def test_config_defaults_and_env(monkeypatch):
     with pytest.raises(ValueError):
         OffloadConfig(transfer_mode="nope")
     monkeypatch.setenv("FT_NUM_BLOCKS", "6")
-    monkeypatch.setenv("FT_INCLUDE_PATTERNS", '["layers.*"]')
+    monkeypatch.setenv("FT_INCLUDE_PATTERNS", "layers.*")
     c = load_config_from_env()
     assert c.num_blocks == 6 and c.include_patterns == ["layers.*"]
+    assert c.enabled is False  # from the environment alone offloading needs FT_ENABLED=1
 
 
 def _mk(sizes):
