@@ -300,3 +300,17 @@ def test_fp8_decoder_on_gpu_matches_dequantized_float32(gpu, default_config):
             tok = want[-1].argmax(-1)
     for g, w in zip(got, want):
         assert float((g - w).norm() / w.norm()) < REL_TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(0, 32, 64), (4, 0, 64), (4, 32, 0)])
+def test_empty_shapes(gpu, default_config, m, n, k):
+    """Empty batches and outputs launch nothing; an empty reduction gives zeros (0 * scale)."""
+    from flextensor_amd import hip
+
+    x = torch.zeros(m, k, dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros(n, k, dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.ones(n, dtype=torch.bfloat16, device=gpu)
+    y = hip.fp8_linear(x, w, s)
+    torch.cuda.synchronize()
+    assert y.shape == (m, n)
+    assert bool((y == 0).all())
