@@ -59,59 +59,103 @@ def hidden_fraction(wait_ms: float, transfer_ms: float) -> float:
 
 @dataclass(frozen=True, slots=True)
 class TrapTimingStats:
+    """One trap's statistics over a report's passes (offload_timing.py:76-117)."""
+
     label: str
-    compute_avg: float
-    compute_median: float
-    transfer_avg: float
-    transfer_median: float
-    wait_avg: float
-    wait_median: float
+    compute_min: float = 0.0
+    compute_max: float = 0.0
+    compute_avg: float = 0.0
+    compute_median: float = 0.0
+    compute_std: float = 0.0
+    transfer_min: float = 0.0
+    transfer_max: float = 0.0
+    transfer_avg: float = 0.0
+    transfer_median: float = 0.0
+    transfer_std: float = 0.0
+    wait_min: float = 0.0
+    wait_max: float = 0.0
+    wait_avg: float = 0.0
+    wait_median: float = 0.0
+    wait_std: float = 0.0
+
+    def compute_budget_ms(self, *, conservative: bool = False) -> float:
+        """The first positive of median, mean, min (``conservative``: min, median, mean), else 0."""
+        order = ((self.compute_min, self.compute_median, self.compute_avg) if conservative
+                 else (self.compute_median, self.compute_avg, self.compute_min))
+        return next((float(v) for v in order if v and v > 0), 0.0)
+
+
+def _column_stats(values: Sequence[float]) -> tuple[float, float, float, float, float]:
+    """min, max, mean, median and sample standard deviation (0 below two samples)."""
+    return (min(values), max(values), sum(values) / len(values), statistics.median(values),
+            statistics.stdev(values) if len(values) >= 2 else 0.0)
+
+
+def build_report(passes: Sequence[OffloadTimingSnapshot]) -> "OffloadTimingReport":
+    """Per-trap statistics over ``passes`` (offload_timing.py:802-855).
+
+    Traps are matched by position; their labels come from the first pass.
+    """
+    passes = tuple(passes)
+    if not passes:
+        return OffloadTimingReport()
+    labels = [r.label for r in passes[0].per_trap]
+    per_trap = []
+    for i, label in enumerate(labels):
+        rows = [p.per_trap[i] for p in passes if i < len(p.per_trap)]
+        c = _column_stats([r.compute_ms for r in rows])
+        t = _column_stats([r.transfer_ms for r in rows])
+        w = _column_stats([r.wait_ms for r in rows])
+        per_trap.append(TrapTimingStats(label, *c, *t, *w))
+    return OffloadTimingReport(per_trap=per_trap, passes=passes)
 
 
 @dataclass
 class OffloadTimingReport:
-    snapshots: list[OffloadTimingSnapshot]
+    """Passes of a collection window and their per-trap statistics (offload_timing.py:120-217)."""
+
+    per_trap: Sequence[TrapTimingStats] = ()
+    passes: Sequence[OffloadTimingSnapshot] = ()
+
+    def __post_init__(self) -> None:
+        self.per_trap = tuple(self.per_trap)
+        self.passes = tuple(self.passes)
 
     @property
     def num_passes(self) -> int:
-        return len(self.snapshots)
+        return len(self.passes)
 
     @property
     def total_wait_sum(self) -> float:
-        return sum(s.total_wait_ms for s in self.snapshots)
+        return sum(s.total_wait_ms for s in self.passes)
 
     @property
     def total_transfer_sum(self) -> float:
-        return sum(s.total_transfer_ms for s in self.snapshots)
+        return sum(s.total_transfer_ms for s in self.passes)
 
     @property
     def total_compute_sum(self) -> float:
-        return sum(s.total_compute_ms for s in self.snapshots)
+        return sum(s.total_compute_ms for s in self.passes)
+
+    @property
+    def total_wait_avg(self) -> float:
+        return self.total_wait_sum / self.num_passes if self.passes else 0.0
+
+    @property
+    def total_transfer_avg(self) -> float:
+        return self.total_transfer_sum / self.num_passes if self.passes else 0.0
+
+    @property
+    def total_compute_avg(self) -> float:
+        return self.total_compute_sum / self.num_passes if self.passes else 0.0
 
     @property
     def hidden_fraction(self) -> float:
+        """Share of transfer time hidden under compute over all passes: 1 - wait / transfer."""
         return hidden_fraction(self.total_wait_sum, self.total_transfer_sum)
 
-    def per_trap_stats(self) -> list[TrapTimingStats]:
-        by_label: dict[str, list[TrapTimingRecord]] = {}
-        for snap in self.snapshots:
-            for r in snap.per_trap:
-                by_label.setdefault(r.label, []).append(r)
-        out = []
-        for label, recs in by_label.items():
-            c = [r.compute_ms for r in recs]
-            t = [r.transfer_ms for r in recs]
-            w = [r.wait_ms for r in recs]
-            out.append(TrapTimingStats(label, statistics.fmean(c), statistics.median(c), statistics.fmean(t),
-                                       statistics.median(t), statistics.fmean(w), statistics.median(w)))
-        return out
-
     def table(self) -> str:
-        lines = [f"{'trap':<24}{'compute ms':>12}{'transfer ms':>13}{'wait ms':>10}"]
-        for s in self.per_trap_stats():
-            lines.append(f"{s.label:<24}{s.compute_median:>12.3f}{s.transfer_median:>13.3f}{s.wait_median:>10.3f}")
-        lines.append(f"passes={self.num_passes} hidden={self.hidden_fraction:.3f}")
-        return "\n".join(lines)
+        return format_offload_timing_table(self)
 
 
 def format_offload_timing_table(data: OffloadTimingSnapshot | OffloadTimingReport) -> str:
@@ -122,7 +166,7 @@ def format_offload_timing_table(data: OffloadTimingSnapshot | OffloadTimingRepor
     transfer was not hidden.
     """
     if isinstance(data, OffloadTimingReport):
-        stats = data.per_trap_stats()
+        stats = data.per_trap
         if not stats:
             return "No offload timing data."
         w = max(max(len(st.label) for st in stats), 5) + 2
@@ -135,10 +179,9 @@ def format_offload_timing_table(data: OffloadTimingSnapshot | OffloadTimingRepor
             lines.append(f"{st.label:<{w}} {st.compute_avg:>12.3f} {st.compute_median:>8.3f}  "
                          f"{st.transfer_avg:>13.3f} {st.transfer_median:>8.3f}  "
                          f"{st.wait_avg:>9.3f} {st.wait_median:>8.3f}{flag}")
-        n = max(data.num_passes, 1)
         lines += ["-" * (w + 74),
-                  f"{'Avg/pass':<{w}} {data.total_compute_sum / n:>12.3f} {'':>8}  "
-                  f"{data.total_transfer_sum / n:>13.3f} {'':>8}  {data.total_wait_sum / n:>9.3f}",
+                  f"{'Avg/pass':<{w}} {data.total_compute_avg:>12.3f} {'':>8}  "
+                  f"{data.total_transfer_avg:>13.3f} {'':>8}  {data.total_wait_avg:>9.3f}",
                   f"{'Sum (all)':<{w}} {data.total_compute_sum:>12.1f} {'':>8}  "
                   f"{data.total_transfer_sum:>13.1f} {'':>8}  {data.total_wait_sum:>9.1f}",
                   f"hidden fraction {data.hidden_fraction:.4f}", rule]
@@ -315,7 +358,7 @@ class OffloadTimingCollector:
 
     def report(self) -> OffloadTimingReport:
         self.flush()
-        return OffloadTimingReport(list(self.snapshots))
+        return build_report(self.snapshots)
 
     def reset(self) -> None:
         """Drop published passes and a pending eager pass; a captured pass stays readable after replays."""

@@ -13,7 +13,8 @@ a pure-Python library) and cites the file:line it follows:
 * ``schedule``     stream/event operation traces of the transfer runtime and
                    both pipelined loaders, replayed on a recording fake stream
 * ``interpolator`` log-log size <-> duration link model
-* ``timing``       per-trap transfer/compute/wait records and hidden fraction
+* ``timing``       per-pass totals, per-trap report statistics and the hidden
+                   fraction of the offload timing
 * ``fp8``          float8 e4m3fn decoding (OCP format definition) and the
                    fp8-weight linear layer in float64
 * ``native``       ctypes access to ``liboracle.so`` (plain C: layout, pack,

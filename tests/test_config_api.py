@@ -15,7 +15,7 @@ import pytest
 
 import flextensor_amd as ft
 from flextensor_amd.config import OffloadConfig, load_config, load_config_from_env, load_config_from_file
-from flextensor_amd.timing import OffloadTimingReport, OffloadTimingSnapshot, TrapTimingRecord
+from flextensor_amd.timing import OffloadTimingSnapshot, TrapTimingRecord, build_report
 
 
 @pytest.fixture(autouse=True)
@@ -121,7 +121,7 @@ def test_timing_tables():
     assert lines[0] == "Offload Timing (single pass)"
     assert any(ln.startswith("layers.1") and ln.endswith("<-") for ln in lines)  # a wait that was not hidden
     assert any(ln.startswith("Total") and "10.000" in ln and "4.000" in ln and "0.500" in ln for ln in lines)
-    rep = OffloadTimingReport([snap, snap])
+    rep = build_report([snap, snap])
     text = ft.format_offload_timing_table(rep)
     assert text.splitlines()[0] == "Offload Timing (2 passes)"
     assert "hidden fraction 0.8750" in text  # 1 - 1.0 / 8.0

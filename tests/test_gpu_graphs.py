@@ -178,7 +178,7 @@ def test_graph_replay_timing(gpu):
         torch.cuda.synchronize()
         rep = mgr.collect_offload_timing()  # reads the replay that just ran
         assert rep.num_passes == i + 1
-        snap = rep.snapshots[-1]
+        snap = rep.passes[-1]
         assert snap.total_transfer_ms > 0 and snap.total_compute_ms > 0
         assert 0.0 <= rep.hidden_fraction <= 1.0
     del g
