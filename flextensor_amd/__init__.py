@@ -4,7 +4,9 @@ Host logic (planning, scheduling, the offload phases) is Python over PyTorch;
 device work goes through the HIP C-ABI library ``libftx_hip.so``
 (``include/ftx.h``): pinned host arenas, host-to-device copy engines
 (hipMemcpyAsync and a zero-copy kernel), a batched scatter kernel and
-hipEvent gating.
+hipEvent gating, an fp8-weight MFMA GEMM, and a staged copy engine for
+pageable and shared-memory sources. Models can be built straight from a
+saved profile and a safetensors checkpoint (``load_model_from_profile``).
 """
 
 __version__ = "0.1.0"
@@ -16,9 +18,11 @@ from .config import (  # noqa: E402
     load_config_from_env,
     load_config_from_file,
 )
+from .lazy_model_init import load_model_from_profile  # noqa: E402
 from .manager import (  # noqa: E402
     DEFAULT_MANAGER_NAME,
     GPUMemoryUsage,
+    OffloadBlock,
     OffloadManager,
     OffloadPhase,
     clear_profiling_durations,
@@ -28,6 +32,7 @@ from .manager import (  # noqa: E402
     init,
     load_profile,
     offload,
+    offload_block,
     offload_from_profile,
     offload_from_state,
     offload_units,
@@ -54,6 +59,7 @@ from .timing import OffloadTimingReport, OffloadTimingSnapshot, format_offload_t
 __all__ = [
     "DEFAULT_MANAGER_NAME",
     "GPUMemoryUsage",
+    "OffloadBlock",
     "OffloadConfig",
     "OffloadManager",
     "OffloadPhase",
@@ -74,9 +80,11 @@ __all__ = [
     "load_config",
     "load_config_from_env",
     "load_config_from_file",
+    "load_model_from_profile",
     "load_profile",
     "load_state",
     "offload",
+    "offload_block",
     "offload_from_profile",
     "offload_from_state",
     "offload_units",

@@ -16,7 +16,17 @@ the offload units), ``PROFILING`` (per-unit compute time), then
 
 During discovery and profiling a unit's tensors are loaded synchronously on
 ``enter`` and dropped on ``exit`` (the role of the warm-up and profile
-loaders). The plan keeps every unit resident when the budget allows, and
+loaders).
+
+Units are modules chosen by ``include_patterns`` (their forwards are
+patched) or, when no module is chosen, manual ``offload_block(label)``
+regions of the caller's code (offload_manager.py:2251-2298). A manual
+block's tensors are found during discovery by watching which parameters the
+code inside the block hands to torch functions (the role of the reference's
+trap tensor mode, trap_tensor_mode.py): the model's parameters stay on the
+host until first used; one used inside a single block belongs to it and is
+uploaded for the block's duration, one used outside blocks or by two blocks
+is placed on the GPU for good. The plan keeps every unit resident when the budget allows, and
 otherwise streams the fewest units that fit the budget, spread evenly over
 the pass; slots are added while the slot-reuse check of the reference
 (strategy_operations.py:525-620) reports a hazard.
@@ -38,6 +48,8 @@ from typing import Any
 
 import torch
 from torch import nn
+from torch.overrides import TorchFunctionMode
+from torch.utils._pytree import tree_leaves
 
 from . import _native as nat
 from . import custom_ops, hip
@@ -174,7 +186,7 @@ def raise_dynamo_limits(n_units: int) -> None:
 @dataclass
 class _Unit:
     label: str
-    module: nn.Module
+    module: nn.Module | None  # None for a manual ``offload_block`` region
     params: list[nn.Parameter] = field(default_factory=list)
     names: list[str] = field(default_factory=list)  # qualified parameter names, parallel to params
     compiled: Callable[..., Any] | None = None  # compile_fn(module), installed at INFERENCE
@@ -307,6 +319,15 @@ def plan_from_state(state: TensorManagerState, units: Sequence[_Unit], base_byte
     return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
 
 
+def _submodule(model: nn.Module, label: str) -> nn.Module | None:
+    if not label:
+        return None
+    try:
+        return model.get_submodule(label)
+    except AttributeError:
+        return None
+
+
 class OffloadManager:
     """One named offload session: phases, plan, loader and the patched model."""
 
@@ -336,6 +357,19 @@ class OffloadManager:
         self.compile_fn: Callable[[nn.Module], Any] | None = None
         self._load_from_shm = False
         self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
+        self._reset_manual()
+
+    def _reset_manual(self) -> None:
+        self._manual = False  # no module units: manual offload blocks, parameters placed on first use
+        self._pending: dict[int, nn.Parameter] = {}  # parameters still on the host, not yet placed for good
+        self._block_owner: dict[int, str] = {}
+        self._block_params: dict[str, list[nn.Parameter]] = {}
+        self._empty_blocks: set[str] = set()
+        self._block: str | None = None  # the manual block being run
+        self._block_tmp: list[nn.Parameter] = []
+        self._mode_depth = 0
+        self._mode: _DiscoveryMode | None = None
+        self._quiet = False  # set while the manager itself moves parameters under the discovery mode
 
     # -- public ---------------------------------------------------------------
 
@@ -371,21 +405,37 @@ class OffloadManager:
             labels = select_offload_units(model, self.config.include_patterns, self.config.exclude_patterns)
         units: list[_Unit] = []
         unit_params: set[int] = set()
+        by_name = dict(model.named_parameters())
+        saved = {st.label: [t.name for t in st.tensors] for st in state.stats} if state is not None else {}
         for label in labels:
-            mod = model.get_submodule(label)
-            params = [p for p in mod.parameters() if id(p) not in unit_params]
+            mod = _submodule(model, label)
+            params = [p for p in mod.parameters() if id(p) not in unit_params] if mod is not None else []
+            names = [name_of[id(p)] for p in params]
+            if state is not None and (mod is None or names != saved[label]):
+                # a manual offload block of the saved plan: its tensors by name
+                mod = None
+                names = [n for n in saved[label] if n in by_name and id(by_name[n]) not in unit_params]
+                params = [by_name[n] for n in names]
             unit_params.update(id(p) for p in params)
-            units.append(_Unit(label, mod, params, [name_of[id(p)] for p in params]))
+            units.append(_Unit(label, mod, params, names))
         if state is not None:
             plan_from_state(state, units, 0, None)  # every mismatch surfaces before the model is touched
         self.device = torch.device("cuda", self.config.gpu_device)
         torch.cuda.set_device(self.device)
         self.model = model
         self.units = units
-        self._place_outside_units(unit_params)
+        self._manual = state is None and not units and self.config.discovery_iters > 0
+        if self._manual:
+            # manual offload blocks: parameters wait on the host until discovery sees where they are used
+            self._pending = {id(p): p for p in model.parameters() if p.device.type == "cpu"}
+            self._resident_bytes += self._upload_into([b for b in model.buffers() if b.device.type == "cpu"])
+            self._patch_root(model)
+        else:
+            self._place_outside_units(unit_params)
         custom_ops.register_manager(id(self), self)
         for u in self.units:
-            self._patch(u)
+            if u.module is not None:
+                self._patch(u)
         self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
         self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
         self.phase = OffloadPhase.DISCOVERY if self.config.discovery_iters > 0 else OffloadPhase.PROFILING
@@ -586,6 +636,10 @@ class OffloadManager:
         if preserve_model:
             for b in self.model.buffers():
                 b.data = b.data.cpu()
+        if self._mode is not None:
+            self._mode_depth = 1
+            self._pop_mode()
+        self._reset_manual()
         self.loader = self.controller = self.plan = None
         self._pass_done = []
         self.model = None
@@ -621,6 +675,149 @@ class OffloadManager:
         for t, d in zip(cpu, dests):
             t.data = d
         return sum(t.numel() * t.element_size() for t in cpu)
+
+    # -- manual offload blocks -----------------------------------------------------
+
+    def offload_block(self, name: str) -> OffloadBlock:
+        """A context manager that makes the code inside it the offload unit ``name``
+        (offload_manager.py:2251-2298).
+
+        For models offloaded with no module units (``include_patterns=[]``).
+        Discovery passes record which parameters the block uses; later passes
+        load them on entry (profiling) or stream them (inference). A block
+        around a module unit that the manager already patches does nothing.
+        Blocks run eagerly and do not nest.
+
+        Example::
+
+            with om.offload_block("encoder"):
+                out = encoder(hidden)
+        """
+        self._check_thread()
+        if self.model is None:
+            raise RuntimeError("Tensor manager not initialized. Call offload() on a model first to initialize the "
+                               "manager.")
+        return OffloadBlock(self, name)
+
+    def _block_enter(self, label: str) -> str | None:
+        """Start block ``label``; returns what its exit must undo (None: nothing)."""
+        self._check_thread()
+        if self.model is None:
+            raise RuntimeError(f"offload manager {self.name!r} manages no model (released?)")
+        if torch.compiler.is_compiling():
+            raise RuntimeError("offload_block runs eagerly: compile the code inside the block instead")
+        if self._block is not None:
+            raise RuntimeError(f"offload block {label!r} opened inside block {self._block!r}: blocks do not nest")
+        unit = next((u for u in self.units if u.label == label), None)
+        if unit is not None and unit.module is not None:
+            return None  # a patched module unit traps itself
+        if self.phase == OffloadPhase.DISCOVERY:
+            if not self._manual:
+                raise RuntimeError("manual offload blocks need a model offloaded with no module units "
+                                   f"(include_patterns=[]); this model has {len(self.units)} patched unit(s)")
+            if label in self._seen_this_pass:
+                raise NotImplementedError(f"offload unit {label!r} ran twice in one forward")
+            self._seen_this_pass.append(label)
+            self._block, self._block_tmp = label, []
+            self._push_mode()
+            return "discovery"
+        if label in self._empty_blocks:
+            return None
+        if unit is None:
+            raise RuntimeError(f"offload block {label!r} was not seen during discovery; every manual block must run "
+                               "in the discovery passes (discovery_iters > 0)")
+        self._enter(label)
+        self._block = label
+        return "unit"
+
+    def _block_exit(self, label: str, kind: str) -> None:
+        self._block = None
+        if kind == "unit":
+            self._exit(label)
+            return
+        self._quiet = True  # the mode must not take these moves for uses of the parameters
+        try:
+            for p in self._block_tmp:  # uploaded for this block only: back to the host
+                if id(p) in self._cpu_data and self._block_owner.get(id(p)) == label:
+                    p.data = self._cpu_data.pop(id(p))
+        finally:
+            self._quiet = False
+        self._block_tmp = []
+        self._pop_mode()
+
+    def _push_mode(self) -> None:
+        if self._mode_depth == 0:
+            self._mode = _DiscoveryMode(self)
+            self._mode.__enter__()
+        self._mode_depth += 1
+
+    def _pop_mode(self) -> None:
+        self._mode_depth -= 1
+        if self._mode_depth == 0 and self._mode is not None:
+            mode, self._mode = self._mode, None
+            mode.__exit__(None, None, None)
+
+    def _touch(self, p: nn.Parameter) -> None:
+        """Discovery saw ``p`` used: place it for the current block, or on the GPU for good."""
+        pid, label = id(p), self._block
+        owner = self._block_owner.get(pid)
+        if label is not None and owner in (None, label):
+            if owner is None:
+                self._block_owner[pid] = label
+                self._block_params.setdefault(label, []).append(p)
+            if pid not in self._cpu_data:
+                self._cpu_data[pid] = p.data
+                p.data = p.data.to(self.device)
+                self._block_tmp.append(p)
+            return
+        # used outside every block, or by a second block: it stays on the GPU
+        if owner is not None:
+            del self._block_owner[pid]
+            self._block_params[owner] = [q for q in self._block_params[owner] if q is not p]
+        del self._pending[pid]
+        if self._cpu_data.pop(pid, None) is None:
+            p.data = p.data.to(self.device)
+        self._resident_bytes += p.numel() * p.element_size()
+
+    def _patch_root(self, model: nn.Module) -> None:
+        """Watch the whole forward during manual discovery, so parameters used outside blocks are placed too."""
+        orig = model.forward
+        mgr = self
+
+        def forward(*args: Any, **kwargs: Any) -> Any:
+            if mgr.phase == OffloadPhase.DISCOVERY and mgr._pending and not torch.compiler.is_compiling():
+                mgr._push_mode()
+                try:
+                    return orig(*args, **kwargs)
+                finally:
+                    mgr._pop_mode()
+            return orig(*args, **kwargs)
+
+        model.forward = forward
+        self._patched.append((model, orig))
+
+    def _finish_manual_discovery(self) -> None:
+        """The blocks seen become units; parameters no block owns go to the GPU for good."""
+        if not self._manual or self.model is None:
+            return
+        order = list(self.order) + [x for x in self._block_params if x not in self.order]
+        name_of = {id(p): n for n, p in self.model.named_parameters()}
+        units = []
+        for label in order:
+            params = self._block_params.get(label, [])
+            if params:
+                units.append(_Unit(label, None, list(params), [name_of[id(p)] for p in params]))
+            else:
+                self._empty_blocks.add(label)
+        owned = {id(p) for u in units for p in u.params}
+        self._quiet = True
+        try:
+            self._resident_bytes += self._upload_into([p for pid, p in self._pending.items() if pid not in owned])
+        finally:
+            self._quiet = False
+        self._pending = {}
+        self.units = units
+        self.order = [u.label for u in units]
 
     def _patch(self, unit: _Unit) -> None:
         """Wrap the unit's forward in enter/exit (offload_manager.py:1136-1162).
@@ -746,6 +943,7 @@ class OffloadManager:
             if not self.order:
                 self.order = list(self._seen_this_pass)
             if self._forwards >= self.config.discovery_iters:
+                self._finish_manual_discovery()
                 self.phase = OffloadPhase.PROFILING
         elif self.phase == OffloadPhase.PROFILING:
             if not self.order:
@@ -827,7 +1025,8 @@ class OffloadManager:
         if self.compile_fn is not None:
             raise_dynamo_limits(len(self.units))
             for u in self.units:
-                u.compiled = self.compile_fn(u.module)
+                if u.module is not None:  # manual blocks stay eager
+                    u.compiled = self.compile_fn(u.module)
         self.build_seconds = time.perf_counter() - t0
         LOGGER.info("offload %r: %d streamed / %d resident units, %.1f s to build", self.name, len(plan.streamed),
                     len(plan.resident), self.build_seconds)
@@ -847,6 +1046,41 @@ class _ResidentLoader:
 
     def get_gpu_memory_bytes(self) -> int:
         return 0
+
+
+class _DiscoveryMode(TorchFunctionMode):
+    """Sees every torch call while manual blocks are discovered; places the parameters it is handed."""
+
+    def __init__(self, mgr: OffloadManager) -> None:
+        super().__init__()
+        self.mgr = mgr
+
+    def __torch_function__(self, func: Any, types: Any, args: Any = (), kwargs: Any = None) -> Any:
+        kwargs = kwargs or {}
+        pending = self.mgr._pending
+        if pending and not self.mgr._quiet:
+            for t in tree_leaves((args, kwargs)):
+                if isinstance(t, torch.Tensor) and id(t) in pending and pending[id(t)] is t:
+                    self.mgr._touch(t)
+        return func(*args, **kwargs)
+
+
+class OffloadBlock:
+    """``with manager.offload_block(label):`` (the trap the reference returns, trap_tensor_mode.py:376-397)."""
+
+    def __init__(self, mgr: OffloadManager, label: str) -> None:
+        self.manager = mgr
+        self.label = label
+        self._kind: str | None = None
+
+    def __enter__(self) -> OffloadBlock:
+        self._kind = self.manager._block_enter(self.label)
+        return self
+
+    def __exit__(self, *exc: Any) -> None:
+        kind, self._kind = self._kind, None
+        if kind is not None:
+            self.manager._block_exit(self.label, kind)
 
 
 _MANAGERS: dict[str, OffloadManager] = {}
@@ -910,6 +1144,11 @@ def update_state(name: str = DEFAULT_MANAGER_NAME) -> None:
 
 def update_offload_timing(name: str = DEFAULT_MANAGER_NAME) -> bool:
     return get_offload_manager(name).update_offload_timing()
+
+
+def offload_block(block_name: str, name: str = DEFAULT_MANAGER_NAME) -> OffloadBlock:
+    """Manual offload block of the named manager (offload_manager.py:2990-2998)."""
+    return get_offload_manager(name).offload_block(block_name)
 
 
 def release(name: str = DEFAULT_MANAGER_NAME, preserve_model: bool = True) -> None:
