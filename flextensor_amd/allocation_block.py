@@ -151,6 +151,8 @@ class AllocationBlock:
         return 0 if self.block is None else self.block.numel()
 
     def _new_block(self, nbytes: int) -> torch.Tensor:
+        if int(nbytes) <= 0:  # nothing to hold (create_max_block over uncommitted blocks): no pin, no allocation
+            return torch.empty(0, dtype=torch.uint8, device=self.device)
         if self.device.type == "cpu":
             if self.pinned_memory:
                 return self.host_pinner.new_block(nbytes)

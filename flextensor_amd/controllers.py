@@ -133,6 +133,7 @@ class AllocationBlockController:
             self.prepare_tensor_id_to_view_mapping()
         except BaseException:
             self._rollback.restore()
+            self._release_shm_blocks()  # segments this build created must not outlive it
             self._clear()
             raise
 
@@ -168,11 +169,14 @@ class AllocationBlockController:
             d.clear()
         self._gpu_slots = []
 
-    def shutdown(self) -> None:
-        self._rollback.restore()
+    def _release_shm_blocks(self) -> None:
         for block in self.block_map_cpu.values():
             if block.shm_segment is not None:
-                block.release()  # unmaps; the creator also removes the segment's name
+                block.release()  # the creator removes the segment's name; the mapping goes with its last view
+
+    def shutdown(self) -> None:
+        self._rollback.restore()
+        self._release_shm_blocks()
         self._clear()
 
     def release_gpu_blocks(self) -> None:

@@ -83,16 +83,32 @@ class OffloadPhase(Enum):
     INFERENCE = "inference"
 
 
-@dataclass(frozen=True)
+@dataclass
 class GPUMemoryUsage:
-    """GPU bytes held by ring slots and by tensors placed permanently (types.py:13-59)."""
+    """GPU bytes held by ring slots and by tensors placed permanently (types.py:13-59).
+
+    ``total_bytes`` defaults to the sum of the two parts.
+    """
 
     blocks_bytes: int = 0
     unmapped_tensors_bytes: int = 0
+    total_bytes: int | None = None
+
+    def __post_init__(self) -> None:
+        if self.total_bytes is None:
+            self.total_bytes = self.blocks_bytes + self.unmapped_tensors_bytes
 
     @property
-    def total_bytes(self) -> int:
-        return self.blocks_bytes + self.unmapped_tensors_bytes
+    def blocks_mb(self) -> float:
+        return self.blocks_bytes / (1024 * 1024)
+
+    @property
+    def unmapped_tensors_mb(self) -> float:
+        return self.unmapped_tensors_bytes / (1024 * 1024)
+
+    @property
+    def total_mb(self) -> float:
+        return self.total_bytes / (1024 * 1024)
 
 
 @dataclass
@@ -529,6 +545,10 @@ class OffloadManager:
         return max(0, self.config.discovery_iters + self.config.profiling_iters - self._forwards)
 
     def get_gpu_memory_usage(self) -> GPUMemoryUsage:
+        """Ring-slot and permanently placed bytes; only in INFERENCE (offload_manager.py:866-905)."""
+        if self.phase != OffloadPhase.INFERENCE:
+            raise RuntimeError(f"Cannot get GPU memory usage in phase {self.phase.value}. "
+                               "This method is only available after transitioning to inference mode.")
         blocks = self.loader.get_gpu_memory_bytes() if self.loader is not None else 0
         return GPUMemoryUsage(blocks, self._resident_bytes)
 
@@ -649,8 +669,10 @@ class OffloadManager:
     # -- internals ------------------------------------------------------------
 
     def _check_thread(self) -> None:
-        if threading.get_ident() != self._owner:
-            raise RuntimeError(f"offload manager {self.name!r} is owned by another thread")
+        here = threading.get_ident()
+        if here != self._owner:
+            raise RuntimeError(f"offload manager {self.name!r} belongs to thread {self._owner} but was used from "
+                               f"thread {here}; each named manager is used from the thread that created it")
 
     def _cpu_views(self, label: str) -> list[torch.Tensor]:
         block = self.controller.block_map_cpu[label]
@@ -1084,12 +1106,16 @@ class OffloadBlock:
 
 
 _MANAGERS: dict[str, OffloadManager] = {}
+_MANAGERS_LOCK = threading.Lock()
 
 
 def get_offload_manager(name: str = DEFAULT_MANAGER_NAME) -> OffloadManager:
-    mgr = _MANAGERS.get(name)
-    if mgr is None:
-        mgr = _MANAGERS[name] = OffloadManager(name)
+    """The manager registered under ``name``, created on first use by the calling thread
+    (offload_manager.py:2815-2850); another thread's manager raises ``RuntimeError``."""
+    with _MANAGERS_LOCK:
+        mgr = _MANAGERS.get(name)
+        if mgr is None:
+            mgr = _MANAGERS[name] = OffloadManager(name)
     mgr._check_thread()
     return mgr
 

@@ -32,28 +32,28 @@ class PiecewisePrefetchPolicy:
     def __init__(self, *, enabled: bool = False, strict: bool = False) -> None:
         self.enabled = enabled
         self.strict = strict
-        self._pending: dict[str, str] = {}  # compute label -> schedule label
+        self._outstanding: dict[str, str] = {}  # compute label -> schedule label
         self._reported: set[tuple[str, str]] = set()
         self._waited: set[str] = set()
 
     def reset(self) -> None:
-        self._pending.clear()
+        self._outstanding.clear()
         self._waited.clear()
 
     def on_schedule(self, schedule_label: str, compute_label: str) -> None:
         if self.enabled:
-            self._pending[compute_label] = schedule_label
+            self._outstanding[compute_label] = schedule_label
 
     def on_wait(self, compute_label: str) -> None:
         if self.enabled:
-            self._pending.pop(compute_label, None)
+            self._outstanding.pop(compute_label, None)
             self._waited.add(compute_label)
 
     def on_piece_join(self, *, at_last_layer: bool = False) -> list[OutstandingPrefetch]:
         if not self.enabled:
             return []
-        pending = [OutstandingPrefetch(s, c) for c, s in self._pending.items()]
-        self._pending.clear()
+        pending = [OutstandingPrefetch(s, c) for c, s in self._outstanding.items()]
+        self._outstanding.clear()
         broken = [p for p in pending if not (at_last_layer and p.compute_label in self._waited)]
         if not broken:
             return []
@@ -65,9 +65,9 @@ class PiecewisePrefetchPolicy:
             repr(p.schedule_label) if p.schedule_label == p.compute_label else f"{p.schedule_label!r}→{p.compute_label!r}"
             for p in (fresh or broken)
         )
-        where = "end-of-forward join" if at_last_layer else "graph piece join"
+        where = "end-of-forward join" if at_last_layer else "PIECEWISE piece join"
         msg = (
-            f"piecewise prefetch policy: {where} with outstanding prefetch(es) [{pairs}]; "
+            f"piecewise prefetch policy: {where} with outstanding H2D prefetch(es) [{pairs}]; "
             "the join forced these transfers to finish before their waits, so their overlap is lost"
         )
         if self.strict:

@@ -1,0 +1,180 @@
+"""Allocation blocks, slot sizing, pin lifetime and controller release semantics on the CPU.
+
+The cases are those of the reference's tests/unit/test_allocation_block.py:14-372,
+test_allocation_manager.py:9-294, test_allocation_block_controller_release.py:42-93
+and test_raw_block_controller_release.py:35-74, restated against this
+package's API. A CPU device stands in for the GPU slots, as in those tests;
+pinning is disabled, or its native register calls are recorded.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from flextensor_amd import _native as nat
+from flextensor_amd.allocation_block import AllocationBlock, AllocationManager, HostPinner
+from flextensor_amd.controllers import AllocationBlockController, RawBlockController
+from flextensor_amd.planner import TensorStatistics
+
+NO_PIN = HostPinner("torch", enabled=False)
+
+
+def _sources() -> list[torch.Tensor]:
+    return [torch.ones(12, dtype=torch.float32), torch.ones(15, dtype=torch.float32) * 2,
+            torch.ones(13, dtype=torch.int32) * 3, torch.arange(20, dtype=torch.bfloat16).reshape(4, 5).t()]
+
+
+@pytest.mark.parametrize("alignment", [0, -1, 1.5, True, "128"])
+def test_rejects_invalid_memory_alignment(alignment):
+    with pytest.raises(ValueError, match="memory_alignment must be a positive integer"):
+        AllocationBlock(device="cpu", host_pinner=NO_PIN, memory_alignment=alignment)
+
+
+def test_allocate_packs_views_at_aligned_offsets():
+    src = _sources()
+    block = AllocationBlock(device="cpu", host_pinner=NO_PIN, pinned_memory=False)
+    for t in src:
+        block.add(t)
+    views = block.allocate()
+    assert [o % 128 for o in block.tensor_offsets] == [0] * len(src)
+    for t, v, off in zip(src, views, block.tensor_offsets):
+        assert v.dtype == t.dtype and v.shape == t.shape and v.stride() == t.stride()  # Fortran stays Fortran
+        assert torch.equal(v, t)
+        assert v.storage_offset() * v.element_size() == off and v.untyped_storage().data_ptr() == block.block.data_ptr()
+    block.block.zero_()
+    assert not views[0].any()  # the views alias the block
+
+
+def test_copy_to_a_cpu_slot_and_projected_views():
+    src = [torch.randn(10), torch.randint(0, 9, (3, 7), dtype=torch.int16)]
+    mgr = AllocationManager(host_pinner=NO_PIN, pinned_memory=False)
+    block = mgr.block()
+    for t in src:
+        block.add(t)
+    block.allocate()
+    slot = mgr.create_max_block(device="cpu")
+    views, prefix = block.project_views(slot)
+    block.copy_to(prefix)
+    for t, v in zip(src, views):
+        assert torch.equal(v, t) and v.untyped_storage().data_ptr() == slot.block.data_ptr()
+    small = AllocationBlock(device="cpu", block_size=8, host_pinner=NO_PIN, pinned_memory=False)
+    with pytest.raises(ValueError, match="does not fit"):
+        block.project_views(small)
+
+
+def test_max_block_sizes_to_the_largest_committed_block():
+    mgr = AllocationManager(host_pinner=NO_PIN, pinned_memory=False)
+    for t in (torch.ones(10), torch.ones(20), torch.ones(5, dtype=torch.int32), torch.ones(40)):
+        b = mgr.block()
+        b.add(t)
+        b.allocate()
+    # the packed total rounds up to the alignment after each tensor (utils.py:114-127): 80 bytes take 128
+    assert [b.nbytes for b in mgr.blocks] == [128, 128, 128, 256]
+    assert mgr.create_max_block(device="cpu").nbytes == 256
+    empty = AllocationManager(host_pinner=NO_PIN, pinned_memory=False)
+    empty.block().add(torch.ones(10))  # never allocated
+    assert empty.create_max_block(device="cpu").block.numel() == 0
+
+
+@pytest.fixture
+def recorded_pins(monkeypatch):
+    calls = {"register": [], "unregister": []}
+    monkeypatch.setattr(nat, "arena_register", lambda ptr, n: calls["register"].append((ptr, n)))
+    monkeypatch.setattr(nat, "arena_unregister", lambda ptr: calls["unregister"].append(ptr))
+    return calls
+
+
+def test_block_release_keeps_pins(recorded_pins):
+    pinner = HostPinner("host_register")
+    block = AllocationBlock(device="cpu", block_size=128, host_pinner=pinner)
+    assert len(recorded_pins["register"]) == 1 and pinner.pinned_bytes == 128
+    block.release()
+    assert recorded_pins["unregister"] == [] and pinner.pinned_bytes == 128  # only release_all unpins
+    pinner.release_all()
+    assert len(recorded_pins["unregister"]) == 1 and pinner.pinned_bytes == 0
+
+
+def test_manager_release_keeps_pins(recorded_pins):
+    pinner = HostPinner("host_register")
+    mgr = AllocationManager(host_pinner=pinner)
+    for n in (64, 96, 128):
+        b = mgr.block()
+        b.add(torch.ones(n, dtype=torch.uint8))
+        b.allocate()
+    assert len(recorded_pins["register"]) == 3
+    mgr.release()
+    assert recorded_pins["unregister"] == [] and pinner.pinned_bytes == 3 * 128
+    pinner.release_all()
+    assert len(recorded_pins["unregister"]) == 3
+
+
+def _stats(tid: int, n: int) -> list[TensorStatistics]:
+    return [TensorStatistics(tid, f"t{tid}", n, 0.0)]
+
+
+def _alloc_controller(release, **kw):
+    label = "model.layers.0"
+    tensors = {1: torch.arange(64, dtype=torch.uint8)}
+    args = {} if release is None else {"release_tensor_memory": release}
+    c = AllocationBlockController({0: [label]}, torch.device("cpu"), tensors, {label: _stats(1, 64)}, {label: 0},
+                                  host_pinner=NO_PIN, **args, **kw)
+    return c, tensors
+
+
+def _raw_controller(release):
+    label = "model.layers.0"
+    tensors = {1: torch.arange(64, dtype=torch.uint8)}
+    args = {} if release is None else {"release_tensor_memory": release}
+    c = RawBlockController({label: 64}, {0: 64}, torch.device("cpu"), tensors, {label: _stats(1, 64)}, {label: 0},
+                           host_pinner=NO_PIN, **args)
+    return c, tensors
+
+
+@pytest.mark.parametrize("build", [_alloc_controller, _raw_controller], ids=["allocation", "raw"])
+def test_source_release_semantics(build):
+    _, kept = build(False)
+    assert torch.equal(kept[1], torch.arange(64, dtype=torch.uint8))
+    _, released = build(True)
+    assert released[1].numel() == 0
+    _, default = build(None)
+    assert default[1].numel() == 0  # the inference default frees the sources
+
+
+@pytest.mark.parametrize("build", [_alloc_controller, _raw_controller], ids=["allocation", "raw"])
+def test_release_gpu_blocks_drops_every_slot_reference(build):
+    c, _ = build(False)
+    assert c.block_map_gpu and c.gpu_block_view_map and c.label_to_tensor_views_map and c.tensor_id_to_view_map
+    c.release_gpu_blocks()
+    assert c.block_map_gpu == {} and c.gpu_block_view_map == {}
+    assert c.label_to_tensor_views_map == {} and c.tensor_id_to_view_map == {}
+    assert c.get_gpu_memory_bytes() == 0
+
+
+def test_schedule_transfer_fills_the_slot_views():
+    labels = ["a", "b", "c"]
+    tensors = {i: torch.randn(16 + 8 * i) for i in range(3)}
+    want = {i: t.clone() for i, t in tensors.items()}
+    strategy = {x: _stats(i, tensors[i].numel() * 4) for i, x in enumerate(labels)}
+    c = AllocationBlockController({0: ["a", "c"], 1: ["b"]}, torch.device("cpu"), tensors, strategy,
+                                  {"a": 0, "b": 1, "c": 0}, host_pinner=NO_PIN)
+    views = c.get_tensor_id_to_view_mapping()
+    assert c.get_gpu_memory_bytes() == c.block_map_cpu["c"].nbytes + c.block_map_cpu["b"].nbytes
+    for i, x in enumerate(labels):
+        c.schedule_transfer(x)
+        assert torch.equal(views[i], want[i])
+    # a and c share slot 0: loading c overwrote a's bytes, as the ring intends
+    assert views[0].untyped_storage().data_ptr() == views[2].untyped_storage().data_ptr()
+
+
+def test_failed_construction_restores_released_sources():
+    tensors = {1: torch.arange(64, dtype=torch.uint8), 2: torch.arange(32, dtype=torch.uint8)}
+    strategy = {"a": _stats(1, 64), "b": _stats(2, 32)}
+    with pytest.raises(ValueError, match="no shared-memory block name"):
+        AllocationBlockController({0: ["a", "b"]}, torch.device("cpu"), tensors, strategy, {"a": 0, "b": 0},
+                                  host_pinner=NO_PIN, shm_block_name_map={"a": "ftx_unused_name_a"})
+    assert torch.equal(tensors[1], torch.arange(64, dtype=torch.uint8))  # packed, released, then restored
+    assert torch.equal(tensors[2], torch.arange(32, dtype=torch.uint8))
+    assert not os.path.exists("/dev/shm/ftx_unused_name_a")  # the segment made for "a" went with the build

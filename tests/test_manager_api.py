@@ -1,0 +1,110 @@
+"""Named-manager registry, thread ownership and the GPU memory report, on the CPU.
+
+Cases of the reference's tests/unit/test_offload_manager_thread_guard.py:17-113
+(one thread owns each named manager; a race to create one name has one
+winner; the error names both threads) and tests/unit/test_gpu_memory_usage.py
+(the report's fields and MB properties; it is only available in INFERENCE).
+"""
+
+from __future__ import annotations
+
+import threading
+
+import pytest
+
+import flextensor_amd.manager as M
+
+
+@pytest.fixture
+def names():
+    made: list[str] = []
+    yield made
+    for n in made:
+        M._MANAGERS.pop(n, None)
+
+
+def test_same_thread_gets_the_same_manager(names):
+    names.append("tg-same")
+    assert M.get_offload_manager("tg-same") is M.get_offload_manager("tg-same")
+
+
+def test_other_thread_is_refused_with_both_thread_ids(names):
+    names.append("tg-cross")
+    M.get_offload_manager("tg-cross")
+    owner = threading.get_ident()
+    seen: dict[str, object] = {}
+
+    def use() -> None:
+        seen["thread"] = threading.get_ident()
+        try:
+            M.get_offload_manager("tg-cross")
+        except RuntimeError as exc:
+            seen["error"] = str(exc)
+
+    t = threading.Thread(target=use)
+    t.start()
+    t.join()
+    msg = seen["error"]
+    assert "tg-cross" in msg and "thread" in msg and str(owner) in msg and str(seen["thread"]) in msg
+
+
+def test_different_names_on_different_threads(names):
+    names += ["tg-main", "tg-other"]
+    M.get_offload_manager("tg-main")
+    out: dict[str, object] = {}
+    t = threading.Thread(target=lambda: out.setdefault("mgr", M.get_offload_manager("tg-other")))
+    t.start()
+    t.join()
+    assert isinstance(out["mgr"], M.OffloadManager)
+
+
+def test_racing_creation_has_one_winner(names):
+    names.append("tg-race")
+    barrier = threading.Barrier(2)
+    wins, losses = [], []
+
+    def race() -> None:
+        barrier.wait()
+        try:
+            M.get_offload_manager("tg-race")
+            wins.append(1)
+        except RuntimeError:
+            losses.append(1)
+
+    threads = [threading.Thread(target=race) for _ in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(wins) == 1 and len(losses) == 1
+
+
+def test_memory_usage_fields_and_megabytes():
+    u = M.GPUMemoryUsage(blocks_bytes=100 * 2**20, unmapped_tensors_bytes=50 * 2**20, total_bytes=150 * 2**20)
+    assert (u.blocks_mb, u.unmapped_tensors_mb, u.total_mb) == (100.0, 50.0, 150.0)
+    half = M.GPUMemoryUsage(int(1.5 * 2**20), 2**19)
+    assert half.total_bytes == 2 * 2**20 and (half.blocks_mb, half.unmapped_tensors_mb, half.total_mb) == (1.5, 0.5, 2.0)
+    zero = M.GPUMemoryUsage(0, 0, 0)
+    assert (zero.total_bytes, zero.total_mb) == (0, 0.0)
+
+
+def test_memory_usage_only_in_inference(names):
+    names.append("mem-phase")
+    mgr = M.get_offload_manager("mem-phase")
+    with pytest.raises(RuntimeError, match="Cannot get GPU memory usage in phase not_initialized"):
+        mgr.get_gpu_memory_usage()
+    for phase in (M.OffloadPhase.DISCOVERY, M.OffloadPhase.PROFILING):
+        mgr.phase = phase
+        with pytest.raises(RuntimeError, match=f"Cannot get GPU memory usage in phase {phase.value}"):
+            M.get_gpu_memory_usage("mem-phase")
+    mgr.phase = M.OffloadPhase.INFERENCE
+    mgr._resident_bytes = 4096
+    usage = mgr.get_gpu_memory_usage()
+    assert (usage.blocks_bytes, usage.unmapped_tensors_bytes, usage.total_bytes) == (0, 4096, 4096)
+    mgr.phase = M.OffloadPhase.NOT_INITIALIZED
+
+
+def test_offload_block_needs_an_offloaded_model(names):
+    names.append("blk-none")
+    with pytest.raises(RuntimeError, match="Call offload"):
+        M.offload_block("x", name="blk-none")
