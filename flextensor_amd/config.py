@@ -10,7 +10,22 @@ or YAML files and ``FT_*`` environment variables with the reference's
 precedence and text conversions (config.py:560-1060).
 
 Also kept: ``shm_enabled``, ``shm_namespace``, ``shm_wait_timeout``
-(config.py:97-125).
+(config.py:97-125), ``skip_discovery`` (:133-160), ``profile_read_only``
+(:240-241) and ``enable_diagnostics`` (:377-380).
+
+Accepted for compatibility, acting differently or not at all here:
+
+* ``external_compile`` (:172-191): the ``flextensor::pre_compute`` /
+  ``post_compute`` ops are always in place, so a caller may compile each unit
+  after INFERENCE without it.
+* ``profile_mode`` (:382-402): profiling here always loads a unit's tensors
+  on entry. ``"view"`` and ``"getter"`` both select that;
+  ``"torch_function"`` needs the per-tensor strategy loader and is refused.
+* ``load_strategy`` (:243-244), ``transfer_budget_scale`` (:193-200),
+  ``enable_instrumentation`` and ``instrumentation_output_dir``
+  (:246-250): they steer the strategy search and the instrumentation
+  subsystem, which are not part of this build. A value other than the
+  default logs a warning at ``offload()``.
 
 Added for this build: ``max_gpu_mem_bytes`` (a budget in bytes instead of a
 fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel`` / ``staged``),
@@ -67,6 +82,15 @@ class OffloadConfig(BaseModel):
     shm_enabled: bool = False
     shm_namespace: str | None = None
     shm_wait_timeout: float = Field(default=0.0, ge=0.0)
+    skip_discovery: bool = False
+    profile_read_only: bool = False
+    enable_diagnostics: bool = False
+    external_compile: bool = False
+    profile_mode: Literal["view", "getter", "torch_function"] = "view"
+    load_strategy: Any = None
+    transfer_budget_scale: float = Field(default=1.0, gt=0.0)
+    enable_instrumentation: bool = False
+    instrumentation_output_dir: str = ".flextensor/instrumentation"
 
     @model_validator(mode="after")
     def _check(self) -> "OffloadConfig":
@@ -74,7 +98,21 @@ class OffloadConfig(BaseModel):
             raise ValueError(f"transfer_mode must be one of {TRANSFER_MODES}, got {self.transfer_mode!r}")
         if self.shm_enabled and (self.shm_namespace is None or not self.shm_namespace.strip()):
             raise ValueError("shm_namespace must be non-empty when shm_enabled=True")
+        if self.profile_mode == "torch_function":
+            raise ValueError("profile_mode='torch_function' is only valid with transfer_mode='strategy', which this "
+                             f"build does not provide; use 'view' or 'getter' with {self.transfer_mode!r}")
         return self
+
+    def inert_settings(self) -> list[str]:
+        """Settings given a non-default value that this build does not act on."""
+        inert = []
+        if self.load_strategy is not None:
+            inert.append("load_strategy")
+        if self.transfer_budget_scale != 1.0:
+            inert.append("transfer_budget_scale")
+        if self.enable_instrumentation:
+            inert.append("enable_instrumentation")
+        return inert
 
 
 PinnedMemoryMode = Literal["torch", "host_register"]

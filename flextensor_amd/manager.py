@@ -373,6 +373,9 @@ class OffloadManager:
         self.compile_fn: Callable[[nn.Module], Any] | None = None
         self._load_from_shm = False
         self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
+        self._from_state = False
+        self.skip_discovery_honored: bool | None = None  # None until offload() decides
+        self._discovery_passes = 0
         self._reset_manual()
 
     def _reset_manual(self) -> None:
@@ -436,11 +439,22 @@ class OffloadManager:
             units.append(_Unit(label, mod, params, names))
         if state is not None:
             plan_from_state(state, units, 0, None)  # every mismatch surfaces before the model is touched
+        for setting in self.config.inert_settings():
+            LOGGER.warning("offload %r: %s has no effect in this build (it steers the reference's strategy search "
+                           "or instrumentation)", self.name, setting)
+        self._from_state = state is not None
+        self.skip_discovery_honored = None
+        if state is None and self.config.skip_discovery:
+            self.skip_discovery_honored = bool(units)
+            if not units:
+                LOGGER.warning("offload %r: skip_discovery=True but include_patterns select no module; running the "
+                               "discovery passes instead", self.name)
+        self._discovery_passes = 0 if self.skip_discovery_honored else self.config.discovery_iters
         self.device = torch.device("cuda", self.config.gpu_device)
         torch.cuda.set_device(self.device)
         self.model = model
         self.units = units
-        self._manual = state is None and not units and self.config.discovery_iters > 0
+        self._manual = state is None and not units and self._discovery_passes > 0
         if self._manual:
             # manual offload blocks: parameters wait on the host until discovery sees where they are used
             self._pending = {id(p): p for p in model.parameters() if p.device.type == "cpu"}
@@ -454,7 +468,7 @@ class OffloadManager:
                 self._patch(u)
         self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
         self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
-        self.phase = OffloadPhase.DISCOVERY if self.config.discovery_iters > 0 else OffloadPhase.PROFILING
+        self.phase = OffloadPhase.DISCOVERY if self._discovery_passes > 0 else OffloadPhase.PROFILING
         if state is not None:
             self.order = labels
             self._to_inference(state)
@@ -490,6 +504,9 @@ class OffloadManager:
         Mirrors offload_manager.py:770-792: a manager with no model raises
         ``RuntimeError``; a missing directory raises ``ValueError``.
         """
+        if self.config.profile_read_only:
+            raise ValueError("Cannot save profile: config.profile_read_only is True. "
+                             "Set profile_read_only=False in OffloadConfig to enable saving.")
         if self.model is None:
             raise RuntimeError("Tensor manager not initialized. Call offload() first.")
         directory = self._resolve_profile_directory(profile_directory)
@@ -539,10 +556,23 @@ class OffloadManager:
         d = self.durations.get(label, [])
         return float(sum(d) / len(d)) if d else 0.0
 
+    @property
     def iters_before_inference(self) -> int:
-        if self.phase == OffloadPhase.INFERENCE:
+        """Forwards that take the offloaded model to INFERENCE (offload_manager.py:1827-1863).
+
+        Discovery passes count unless they are skipped (``skip_discovery``
+        honoured, or ``discovery_iters=0``). A skipped discovery still takes one
+        profiling forward, which records the execution order. A model offloaded
+        with a saved plan streams at once (0).
+        """
+        if self.model is None or self._from_state:
             return 0
-        return max(0, self.config.discovery_iters + self.config.profiling_iters - self._forwards)
+        d, p = self.config.discovery_iters, self.config.profiling_iters
+        if d == 0 and p == 0:
+            return 0
+        if self.skip_discovery_honored:
+            return max(1, p)
+        return d + p
 
     def get_gpu_memory_usage(self) -> GPUMemoryUsage:
         """Ring-slot and permanently placed bytes; only in INFERENCE (offload_manager.py:866-905)."""
@@ -660,6 +690,8 @@ class OffloadManager:
             self._mode_depth = 1
             self._pop_mode()
         self._reset_manual()
+        self._from_state = False
+        self.skip_discovery_honored = None
         self.loader = self.controller = self.plan = None
         self._pass_done = []
         self.model = None
@@ -719,6 +751,9 @@ class OffloadManager:
         if self.model is None:
             raise RuntimeError("Tensor manager not initialized. Call offload() on a model first to initialize the "
                                "manager.")
+        if self.skip_discovery_honored:
+            raise RuntimeError("offload_block() is not supported when OffloadConfig.skip_discovery is True: manual "
+                               "offload blocks are found in the discovery passes. Set skip_discovery=False.")
         return OffloadBlock(self, name)
 
     def _block_enter(self, label: str) -> str | None:
@@ -964,7 +999,7 @@ class OffloadManager:
         if self.phase == OffloadPhase.DISCOVERY:
             if not self.order:
                 self.order = list(self._seen_this_pass)
-            if self._forwards >= self.config.discovery_iters:
+            if self._forwards >= self._discovery_passes:
                 self._finish_manual_discovery()
                 self.phase = OffloadPhase.PROFILING
         elif self.phase == OffloadPhase.PROFILING:
@@ -975,7 +1010,7 @@ class OffloadManager:
                 self.durations.setdefault(label, []).append(s.elapsed_time(e))
             self._events.clear()
         self._seen_this_pass = []
-        if self.phase == OffloadPhase.PROFILING and self._forwards >= self.config.discovery_iters + self.config.profiling_iters:
+        if self.phase == OffloadPhase.PROFILING and self._forwards >= self._discovery_passes + self.config.profiling_iters:
             self._to_inference()
 
     def _budget(self) -> int | None:
@@ -1052,6 +1087,26 @@ class OffloadManager:
         self.build_seconds = time.perf_counter() - t0
         LOGGER.info("offload %r: %d streamed / %d resident units, %.1f s to build", self.name, len(plan.streamed),
                     len(plan.resident), self.build_seconds)
+        if cfg.enable_diagnostics:
+            LOGGER.info("offload %r plan:\n%s", self.name, self.plan_table())
+
+    def plan_table(self) -> str:
+        """Per unit: bytes, profiled ms, and where it lives (its slot and transfer label when streamed)."""
+        plan = self.plan
+        if plan is None:
+            return "(no plan yet)"
+        bd = plan.block_data
+        producer = {c: t for t, c in bd.transfer_to_compute_map.items()} if bd else {}
+        rows = [f"{'unit':<32} {'MB':>10} {'ms':>9}  placement"]
+        for label in self.order:
+            u = self._unit(label)
+            if label in plan.streamed and bd is not None:
+                src = producer.get(label, "?")
+                where = f"slot {bd.label_to_block_id.get(src, '?')}, loaded during {src!r}"
+            else:
+                where = "resident"
+            rows.append(f"{label:<32} {u.nbytes / 2**20:>10.2f} {self._duration(label):>9.3f}  {where}")
+        return "\n".join(rows)
 
 
 class _ResidentLoader:

@@ -52,3 +52,28 @@ def test_units_profiling_pause_and_fixed_config(gpu):
         ft.set_config(OffloadConfig(), name=name)
     assert ft.update_offload_timing(name) is True  # timing is off: nothing to store
     ft.release(name)
+
+
+def test_skip_discovery_streams_after_iters_before_inference(gpu, caplog):
+    model = W.build_mlp_stack(8, 256, 704, seed=92)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, skip_discovery=True,
+                        profiling_iters=2, max_gpu_mem_bytes=5 * layer, enable_diagnostics=True)
+    name = "skip-discovery"
+    ft.offload(model, cfg, name=name)
+    mgr = ft.get_offload_manager(name)
+    assert mgr.skip_discovery_honored and mgr.phase == OffloadPhase.PROFILING
+    x = W.mlp_input(16, 256, seed=92).to(gpu)
+    with torch.no_grad():
+        want = resident(x)
+        with caplog.at_level("INFO", logger="flextensor_amd.manager"):
+            for _ in range(mgr.iters_before_inference):
+                assert torch.equal(model(x), want)
+        assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.streamed
+        assert mgr.order == [f"layers.{i}" for i in range(8)]  # the first profiling pass recorded the order
+        for _ in range(2):
+            assert torch.equal(model(x), want)
+    assert "plan:" in caplog.text and all(f"layers.{i}" in caplog.text for i in range(8))
+    assert "loaded during" in caplog.text and "resident" in caplog.text
+    ft.release(name)

@@ -9,10 +9,13 @@ winner; the error names both threads) and tests/unit/test_gpu_memory_usage.py
 from __future__ import annotations
 
 import threading
+from unittest import mock
 
 import pytest
+import torch
 
 import flextensor_amd.manager as M
+from flextensor_amd.config import OffloadConfig
 
 
 @pytest.fixture
@@ -108,3 +111,67 @@ def test_offload_block_needs_an_offloaded_model(names):
     names.append("blk-none")
     with pytest.raises(RuntimeError, match="Call offload"):
         M.offload_block("x", name="blk-none")
+
+
+# ---- skip_discovery, profile_read_only, inert settings (config.py:133-160, 240-250, 377-402) ------------
+
+
+class _Stack(torch.nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.layers = torch.nn.ModuleList(torch.nn.Linear(4, 4) for _ in range(3))
+
+
+@pytest.fixture
+def host_offload(names):
+    """``offload()`` on the host: no library, no device placement."""
+    with mock.patch.object(M.nat, "load", lambda: None), \
+            mock.patch.object(M.torch.cuda, "set_device", lambda d: None), \
+            mock.patch.object(M.custom_ops, "register_manager", lambda *a: None), \
+            mock.patch.object(M.OffloadManager, "_upload_into", lambda self, ts: 0):
+        def run(name, **cfg):
+            names.append(name)
+            mgr = M.get_offload_manager(name)
+            mgr.offload(_Stack(), OffloadConfig(**cfg))
+            return mgr
+        yield run
+
+
+def test_skip_discovery_honoured_with_module_units(host_offload):
+    mgr = host_offload("skip-yes", include_patterns=["layers.*"], skip_discovery=True, profiling_iters=3)
+    assert mgr.skip_discovery_honored is True and mgr.phase == M.OffloadPhase.PROFILING
+    assert mgr.iters_before_inference == 3
+    with pytest.raises(RuntimeError, match="skip_discovery is True"):
+        mgr.offload_block("blk")
+
+
+def test_skip_discovery_falls_back_without_module_units(host_offload, caplog):
+    with caplog.at_level("WARNING"):
+        mgr = host_offload("skip-no", include_patterns=[], skip_discovery=True, discovery_iters=2, profiling_iters=3)
+    assert mgr.skip_discovery_honored is False and mgr.phase == M.OffloadPhase.DISCOVERY and mgr._manual
+    assert "running the discovery passes instead" in caplog.text
+    assert mgr.iters_before_inference == 5
+
+
+@pytest.mark.parametrize("d, p, want", [(1, 10, 11), (2, 0, 2), (0, 4, 4)])
+def test_iters_before_inference_counts_the_passes(host_offload, d, p, want):
+    mgr = host_offload(f"iters-{d}-{p}", include_patterns=["layers.*"], discovery_iters=d, profiling_iters=p)
+    assert mgr.iters_before_inference == want
+
+
+def test_read_only_profile_refuses_to_save(host_offload, tmp_path):
+    mgr = host_offload("ro", include_patterns=["layers.*"], profile_read_only=True)
+    with pytest.raises(ValueError, match="profile_read_only is True"):
+        mgr.save_profile(str(tmp_path))
+
+
+def test_inert_settings_warn(host_offload, caplog):
+    with caplog.at_level("WARNING"):
+        host_offload("inert", include_patterns=["layers.*"], transfer_budget_scale=0.9, enable_instrumentation=True)
+    assert "transfer_budget_scale has no effect" in caplog.text and "enable_instrumentation has no effect" in caplog.text
+
+
+def test_profile_mode_torch_function_refused():
+    with pytest.raises(ValueError, match="torch_function"):
+        OffloadConfig(profile_mode="torch_function")
+    assert OffloadConfig(profile_mode="getter").profile_mode == "getter"
