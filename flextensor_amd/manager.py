@@ -374,6 +374,7 @@ class OffloadManager:
         self._load_from_shm = False
         self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
         self._from_state = False
+        self.memory_transfer_stats: dict[int, float] = {}
         self.skip_discovery_honored: bool | None = None  # None until offload() decides
         self._discovery_passes = 0
         self._reset_manual()
@@ -588,6 +589,89 @@ class OffloadManager:
     def reset_offload_timing(self) -> None:
         if self.timing is not None:
             self.timing.reset()
+
+    def reset_offload_timing_sampling(self) -> None:
+        """Drop the stored timing passes and close the sample window (offload_manager.py:1439-1444).
+
+        From then on only passes between :meth:`begin_offload_timing_sample`
+        and :meth:`finish_offload_timing_sample` are stored.
+        """
+        self.reset_offload_timing()
+        if self.timing is not None:
+            self.timing.set_measure_window(False)
+
+    def begin_offload_timing_sample(self) -> None:
+        """Open the sample window for the next pass (offload_manager.py:1446-1450)."""
+        if self.timing is not None:
+            self.timing.set_measure_window(True)
+
+    def finish_offload_timing_sample(self, *, replay_generation: int | None) -> bool:
+        """Store the sampled pass, then close the window; True if one was stored (offload_manager.py:1452-1463).
+
+        ``replay_generation`` is None for an eager pass. For a graph replay
+        the latest replay is read: the timestamps here are rewritten by every
+        replay, so no generation needs matching.
+        """
+        if self.timing is None or not self.timing.enabled:
+            return False
+        try:
+            return self.timing.flush()
+        finally:
+            self.timing.set_measure_window(False)
+
+    def cancel_offload_timing_sample(self) -> None:
+        """Close the sample window without storing (offload_manager.py:1465-1469)."""
+        if self.timing is not None:
+            self.timing.set_measure_window(False)
+
+    def sync_prev_onload(self) -> None:
+        """Make the current stream wait for the transfers issued so far (offload_manager.py:858-860)."""
+        fn = getattr(self.loader, "sync_prev_onload", None)
+        if fn is not None:
+            fn()
+
+    def join_after_forward(self) -> None:
+        """Join the transfer stream back into the current one after a forward (offload_manager.py:862-864)."""
+        fn = getattr(self.loader, "join_after_forward", None)
+        if fn is not None:
+            fn()
+
+    def get_layer_label_by_idx(self) -> list[str]:
+        """Labels of the patched module units, in patch order (offload_manager.py:1203-1214)."""
+        return [u.label for u in self.units if u.module is not None]
+
+    @property
+    def eager_profiling_iters(self) -> int:
+        """Profiling forwards before INFERENCE, at least 1 (offload_manager.py:731-740)."""
+        return max(1, self.config.profiling_iters)
+
+    def benchmark_transfers(self) -> dict[int, float]:
+        """Measure host-to-device copy times at the largest unit's size and below
+        (memory_transfer_benchmark.py:59-129); returns and keeps ``{bytes: ms}``.
+
+        The reference's method of this name is an empty placeholder
+        (offload_manager.py:844-848).
+        """
+        if self.model is None:
+            return {}
+        largest = max((u.nbytes for u in self.units), default=0)
+        if largest == 0:
+            return {}
+        from .link_model import benchmark_memory_transfers
+
+        self.memory_transfer_stats = benchmark_memory_transfers(largest, self.device)
+        return self.memory_transfer_stats
+
+    def offload_from_state(self, model: nn.Module, state: TensorManagerState, config: OffloadConfig | None = None,
+                           *, allow_strategy_replan: bool = True) -> nn.Module:
+        """Adopt a saved plan (offload_manager.py:1924-1960): streaming starts at the first forward.
+
+        ``allow_strategy_replan`` is accepted for the reference's signature;
+        there is no strategy replan here.
+        """
+        if self.phase != OffloadPhase.NOT_INITIALIZED or self.model is not None:
+            raise RuntimeError("OffloadManager is already active; call release() before adopting another state.")
+        return self.offload(model, config if config is not None else self.config, state=state)
 
     def init(self, config: OffloadConfig | None = None) -> None:
         """Set the configuration before ``offload`` (offload_manager.py:2853-2856)."""
@@ -1285,4 +1369,4 @@ def offload_from_state(model: nn.Module, state: TensorManagerState, config: Offl
                        name: str = DEFAULT_MANAGER_NAME) -> nn.Module:
     """Adopt an in-memory saved plan (offload_manager.py:2925-2958); ``state`` must use ``config``'s transfer mode."""
     mgr = get_offload_manager(name)
-    return mgr.offload(model, config or mgr.config or OffloadConfig(), state=state)
+    return mgr.offload_from_state(model, state, config or mgr.config or OffloadConfig())

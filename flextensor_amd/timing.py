@@ -236,6 +236,7 @@ class OffloadTimingCollector:
         self._on_pass = on_pass
         self._max_passes = max_passes
         self.snapshots: list[OffloadTimingSnapshot] = []
+        self._measure_window = True  # passes are published while open (offload_timing.py:445-449)
         self._pass_active = False
         self._events: dict[str, dict[str, Any]] = {}
         self._done: dict[str, set[str]] = {"transfer": set(), "compute": set(), "wait": set()}
@@ -258,6 +259,18 @@ class OffloadTimingCollector:
         self._is_capturing = is_capturing
         for label in self._labels:
             self._events[label] = {k: event_factory() for k in ("ts", "te", "cs", "ce", "ws", "we")}
+
+    def set_measure_window(self, enabled: bool) -> None:
+        """Publish finished passes only while the window is open (it is open from the start).
+
+        Opening it drops an eager pass already under way, which began
+        outside the window (offload_timing.py:445-449).
+        """
+        if enabled and not self._measure_window and self._pass_active and not self._in_capture:
+            for s in self._done.values():
+                s.clear()
+            self._pass_active = False
+        self._measure_window = enabled
 
     def _rec(self, label: str, key: str, stream: Any = None) -> None:
         self._events[label][key].record(stream if stream is not None else self._current_stream())
@@ -322,20 +335,19 @@ class OffloadTimingCollector:
         """Publish a pending pass (the newest pass is otherwise only finalized by the next one).
 
         With no eager pass pending after a graph was captured, the events of
-        the latest replay are read instead.
+        the latest replay are read instead. Returns whether a pass was
+        published (a closed measure window publishes nothing).
         """
         if not self.enabled or self._is_capturing():
             return False
         self._end_capture()
         if self._pass_active:
-            self._finalize()
-            return True
+            return self._finalize()
         if self._capture_done is not None:
-            self._finalize(self._capture_done)
-            return True
+            return self._finalize(self._capture_done)
         return False
 
-    def _finalize(self, done: dict[str, set[str]] | None = None) -> None:
+    def _finalize(self, done: dict[str, set[str]] | None = None) -> bool:
         self._synchronize()
         if self._clock is not None:
             self._clock.refresh()
@@ -350,11 +362,14 @@ class OffloadTimingCollector:
         for s in self._done.values():
             s.clear()
         self._pass_active = False
+        if not self._measure_window:
+            return False
         snap = OffloadTimingSnapshot(recs)
         self.snapshots.append(snap)
         del self.snapshots[: max(0, len(self.snapshots) - self._max_passes)]
         if self._on_pass is not None:
             self._on_pass(snap)
+        return True
 
     def report(self) -> OffloadTimingReport:
         self.flush()

@@ -77,3 +77,41 @@ def test_skip_discovery_streams_after_iters_before_inference(gpu, caplog):
     assert "plan:" in caplog.text and all(f"layers.{i}" in caplog.text for i in range(8))
     assert "loaded during" in caplog.text and "resident" in caplog.text
     ft.release(name)
+
+
+def test_manager_seam_and_transfer_benchmark(gpu, tmp_path):
+    """The calls a serving loop makes around a streamed forward (offload_manager.py:858-864;
+    contrib/vllm/v2/offloader.py:393-401), and the state adoption method (:1924-1960)."""
+    model = W.build_mlp_stack(6, 256, 704, seed=93)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, max_gpu_mem_bytes=4 * layer)
+    src = ft.get_offload_manager("seam-src")
+    src.offload(model, cfg)
+    x = W.mlp_input(8, 256, seed=93).to(gpu)
+    with torch.no_grad():
+        want = resident(x)
+        for _ in range(2):
+            model(x)
+        assert src.phase == OffloadPhase.INFERENCE and src.plan.streamed
+        for _ in range(3):
+            src.sync_prev_onload()
+            out = model(x)
+            src.join_after_forward()
+            assert torch.equal(out, want)
+    stats = src.benchmark_transfers()
+    assert sorted(stats) == sorted(src.memory_transfer_stats) and max(stats) <= layer and all(v > 0 for v in stats.values())
+    assert src.get_layer_label_by_idx() == [f"layers.{i}" for i in range(6)] and src.eager_profiling_iters == 1
+    state = src.state()
+    ft.release("seam-src")
+
+    twin = W.build_mlp_stack(6, 256, 704, seed=93)
+    dst = ft.get_offload_manager("seam-dst")
+    dst.offload_from_state(twin, state, cfg)
+    assert dst.phase == OffloadPhase.INFERENCE and dst.iters_before_inference == 0
+    with pytest.raises(RuntimeError, match="already active"):
+        dst.offload_from_state(twin, state, cfg)
+    with torch.no_grad():
+        assert torch.equal(twin(x), want)
+    ft.release("seam-dst")

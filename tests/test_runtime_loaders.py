@@ -399,3 +399,32 @@ def test_eager_timing_refuses_capture():
                                  synchronize=lambda: None, is_capturing=lambda: capturing["on"])
     with pytest.raises(RuntimeError, match="cuda_graph"):
         col.on_pass_start()
+
+
+def test_measure_window_stores_only_sampled_passes():
+    """offload_timing.py:445-449 and offload_manager.py:1439-1469: only passes inside a sample window are stored."""
+    from flextensor_amd.manager import OffloadManager
+
+    clock = {"now": 0.0, "step": 1.0, "recorded": []}
+    col = OffloadTimingCollector(["L0", "L1"], event_factory=lambda: _ClockEvent(clock), current_stream=lambda: None,
+                                 synchronize=lambda: None, is_capturing=lambda: False)
+    mgr = OffloadManager(name="sampling")
+    mgr.timing = col
+    _timed_pass(col)
+    _timed_pass(col)  # an open window (the default) stores the previous pass
+    assert len(col.snapshots) == 1
+    mgr.reset_offload_timing_sampling()  # drops what was stored and closes the window
+    assert col.snapshots == []
+    _timed_pass(col)  # not sampled
+    clock["step"] = 2.0
+    mgr.begin_offload_timing_sample()  # drops the unsampled pass under way
+    _timed_pass(col)
+    assert mgr.finish_offload_timing_sample(replay_generation=None) is True
+    assert len(col.snapshots) == 1 and col.snapshots[0].per_trap[0].transfer_ms == 2.0
+    clock["step"] = 4.0
+    _timed_pass(col)  # the window closed with the sample
+    assert col.flush() is False and len(col.snapshots) == 1
+    mgr.begin_offload_timing_sample()
+    _timed_pass(col)
+    mgr.cancel_offload_timing_sample()
+    assert mgr.finish_offload_timing_sample(replay_generation=None) is False and len(col.snapshots) == 1
