@@ -35,10 +35,8 @@ the pass; slots are added while the slot-reuse check of the reference
 from __future__ import annotations
 
 import contextlib
-import fnmatch
 import logging
 import os
-import re
 import threading
 import time
 from collections.abc import Callable, Iterator, Sequence
@@ -70,6 +68,7 @@ from .planner import (
 from .prefetch_policy import PiecewisePrefetchPolicy
 from .profile import TensorManagerState, load_state, save_state
 from .scatter import upload_tensors
+from .selection import select_offload_units
 from .timing import OffloadTimingCollector, OffloadTimingReport
 
 LOGGER = logging.getLogger(__name__)
@@ -122,56 +121,6 @@ class StreamPlan:
     reordered: bool
     budget_bytes: int | None
     planned_gpu_bytes: int
-
-
-def _glob_regex(pattern: str) -> re.Pattern[str]:
-    """``*`` and ``?`` stay within one path component; ``**`` crosses dots."""
-    out, i = [], 0
-    while i < len(pattern):
-        if pattern.startswith("**", i):
-            out.append(".*")
-            i += 2
-            continue
-        c = pattern[i]
-        out.append("[^.]*" if c == "*" else "[^.]" if c == "?" else re.escape(c))
-        i += 1
-    return re.compile("".join(out))
-
-
-def _match(path: str, pattern: str) -> bool:
-    return _glob_regex(pattern).fullmatch(path) is not None
-
-
-def _matches(path: str, module: nn.Module, patterns: Sequence[str]) -> bool:
-    for p in patterns:
-        if p.startswith("class:"):
-            body = p[len("class:"):]
-            cls = type(module)
-            if fnmatch.fnmatchcase(cls.__name__, body) or fnmatch.fnmatchcase(f"{cls.__module__}.{cls.__qualname__}", body):
-                return True
-        elif _match(path, p[len("name:"):] if p.startswith("name:") else p):
-            return True
-    return False
-
-
-def select_offload_units(model: nn.Module, include: Sequence[str], exclude: Sequence[str]) -> list[str]:
-    """Outermost modules matching ``include`` and not ``exclude``, in module order.
-
-    A matched container without its own forward (``ModuleList`` /
-    ``ModuleDict``) stands for its children.
-    """
-    chosen: list[str] = []
-    for path, mod in model.named_modules():
-        if not path or any(path.startswith(c + ".") for c in chosen):
-            continue
-        if not _matches(path, mod, include):
-            continue
-        if isinstance(mod, (nn.ModuleList, nn.ModuleDict)):
-            for child, _ in mod.named_children():
-                chosen.append(f"{path}.{child}")
-            continue
-        chosen.append(path)
-    return [p for p in chosen if not _matches(p, model.get_submodule(p), exclude)]
 
 
 class _CompiledCall(threading.local):

@@ -1,0 +1,193 @@
+"""Offload-unit selection by include/exclude patterns, on the CPU.
+
+Cases of the reference's tests/unit/test_forward_patching.py:723-1560
+(ancestor guard, parameter-level include patterns and their derivation,
+unmatched-pattern warnings and aggregate errors, label uniqueness, the
+DeepSeek-style ``*.scale`` alias) on models of the same shapes.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch import nn
+
+from flextensor_amd.selection import module_patterns, partition, path_matches, select_offload_units
+
+
+class SimpleLayer(nn.Module):
+    def __init__(self, dim: int = 10) -> None:
+        super().__init__()
+        self.linear = nn.Linear(dim, dim)
+
+
+class ModelWithLayers(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.layer1, self.layer2, self.layer3 = SimpleLayer(), SimpleLayer(), SimpleLayer()
+
+
+class AttentionBlock(nn.Module):
+    def __init__(self, dim: int = 10) -> None:
+        super().__init__()
+        self.q_proj = nn.Linear(dim, dim)
+        self.k_proj = nn.Linear(dim, dim)
+
+
+class TransformerLayer(nn.Module):
+    def __init__(self, dim: int = 10) -> None:
+        super().__init__()
+        self.attn = AttentionBlock(dim)
+        self.norm = nn.LayerNorm(dim)
+
+
+class NestedModel(nn.Module):
+    def __init__(self, n: int = 2, dim: int = 10) -> None:
+        super().__init__()
+        self.layers = nn.ModuleList(TransformerLayer(dim) for _ in range(n))
+        self.head = nn.Linear(dim, dim)
+
+
+class WrappedNestedModel(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.model = NestedModel()
+
+
+class LayerWithDirectParam(nn.Module):
+    def __init__(self, dim: int = 10) -> None:
+        super().__init__()
+        self.x = nn.Parameter(torch.randn(dim))
+        self.linear = nn.Linear(dim, dim)
+
+
+class ModelWithDirectParams(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.layers = nn.ModuleList(LayerWithDirectParam() for _ in range(2))
+
+
+class LinearWithScale(nn.Module):
+    def __init__(self, dim: int = 10) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.randn(dim, dim))
+        self.weight.scale = self.scale = nn.Parameter(torch.randn(dim))
+
+
+class ModelWithInnerFieldLayers(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.layers = nn.ModuleList(LinearWithScale() for _ in range(2))
+
+
+def _paths(model: nn.Module) -> list[str]:
+    return [p for p, _ in model.named_modules() if p]
+
+
+@pytest.mark.parametrize("path, pattern, recursive, want", [
+    ("layers.0", "layers.*", False, True),
+    ("layers.0.attn", "layers.*", False, False),
+    ("layers.0.attn", "layers.*", True, True),
+    ("layers.0.attn", "*.attn", True, True),
+    ("layers.0.attn", "*.attn", False, False),
+    ("layers.10", "layers.1?", False, True),
+    ("layers.1", "layers.1?", False, False),
+    ("model.layers.3.mlp", "model.*.mlp", True, True),
+    ("q_proj", "*proj", False, True),
+])
+def test_segment_glob(path, pattern, recursive, want):
+    assert path_matches(path, pattern, recursive_star=recursive) is want
+
+
+def test_partition_and_empty_bodies():
+    assert partition(["layers.*", "name:embed", "class:MoELayer"]) == (["layers.*", "embed"], ["MoELayer"])
+    for bad in ("class:", "name:  "):
+        with pytest.raises(ValueError, match="empty body"):
+            partition([bad])
+
+
+def test_module_patterns_from_parameter_patterns():
+    nested = NestedModel()
+    assert "layers.*" in module_patterns(["layers.*"], _paths(nested), nested)
+    assert "layers.*" in module_patterns(["layers.*.weight"], _paths(nested), nested)
+    assert module_patterns(["layers.*.weight", "layers.*.bias"], _paths(nested), nested).count("layers.*") == 1
+    flat = ModelWithLayers()
+    assert set(module_patterns(["layer1.linear.weight"], _paths(flat), flat)) == {"layer1.linear"}
+    assert set(module_patterns(["*.weight"], _paths(flat), flat)) == {"layer1.linear", "layer2.linear",
+                                                                         "layer3.linear"}
+    assert module_patterns(["*"], _paths(flat), flat) == ["*"]
+
+
+def test_star_weight_on_a_wrapper_names_the_owners():
+    m = WrappedNestedModel()
+    got = set(module_patterns(["*.weight"], _paths(m), m))
+    assert got == {"model.layers.0.attn.q_proj", "model.layers.0.attn.k_proj", "model.layers.0.norm",
+                   "model.layers.1.attn.q_proj", "model.layers.1.attn.k_proj", "model.layers.1.norm", "model.head"}
+    assert module_patterns(["*.weight"], _paths(m), None) == []  # no model: no per-parameter fallback
+    mixed = set(module_patterns(["model.layers.*", "*.bias"], _paths(m), m))
+    assert "model.layers.*" in mixed and "model.head" in mixed and "*" not in mixed
+
+
+def test_unmatched_sibling_does_not_widen_to_the_ancestor():
+    m = WrappedNestedModel()
+    m.model.norm_f = nn.LayerNorm(10)
+    got = set(module_patterns(["model.layers.*", "model.norm", "model.norm_f", "model.head"], _paths(m), m))
+    assert {"model.layers.*", "model.norm_f", "model.head"} <= got and "model" not in got
+    units = select_offload_units(m, ["model.layers.*", "model.norm", "model.head"], [])
+    assert units == ["model.layers.0", "model.layers.1", "model.head"]
+
+
+def test_parameter_patterns_select_owning_modules():
+    assert select_offload_units(NestedModel(), ["layers.*.weight"], []) == ["layers.0", "layers.1"]
+    assert select_offload_units(ModelWithLayers(), ["*"], []) == ["layer1", "layer2", "layer3"]
+    units = select_offload_units(WrappedNestedModel(), ["*.weight"], [])
+    assert len(units) > 1 and "model" not in units
+    assert select_offload_units(ModelWithLayers(), ["*.weight"], []) == ["layer1.linear", "layer2.linear",
+                                                                        "layer3.linear"]
+
+
+def test_ancestor_guard_keeps_the_outermost_unit():
+    m = NestedModel()
+    assert select_offload_units(m, ["layers.*", "layers.*.attn"], []) == ["layers.0", "layers.1"]
+    assert select_offload_units(m, ["layers.*", "*.weight"], []) == ["layers.0", "layers.1", "head"]
+    assert select_offload_units(ModelWithDirectParams(), ["*.x", "*.weight"], []) == ["layers.0", "layers.1"]
+    assert select_offload_units(ModelWithInnerFieldLayers(), ["*.scale"], []) == ["layers.0", "layers.1"]
+
+
+def test_excludes_span_segments_and_classes():
+    m = NestedModel(n=3)
+    assert select_offload_units(m, ["layers.*"], ["layers.1"]) == ["layers.0", "layers.2"]
+    assert select_offload_units(m, ["layers.*", "head"], ["*.2"]) == ["layers.0", "layers.1", "head"]
+    assert select_offload_units(m, ["layers.*", "head"], ["class:Linear"]) == ["layers.0", "layers.1", "layers.2"]
+    assert select_offload_units(m, ["class:torch.nn.modules.linear.*"], []) == ["layers.0.attn.q_proj",
+                                                                               "layers.0.attn.k_proj",
+                                                                               "layers.1.attn.q_proj",
+                                                                               "layers.1.attn.k_proj",
+                                                                               "layers.2.attn.q_proj",
+                                                                               "layers.2.attn.k_proj", "head"]
+
+
+def test_unmatched_patterns_warn_and_empty_selections_log_errors(caplog):
+    m = NestedModel()
+    with caplog.at_level("WARNING", logger="flextensor_amd.selection"):
+        assert select_offload_units(m, ["layers.*", "bogus"], ["nothing.here"]) == ["layers.0", "layers.1"]
+    assert "Include pattern 'bogus' did not match" in caplog.text
+    assert "Exclude pattern 'nothing.here' did not match" in caplog.text
+    assert "Include pattern 'layers.*'" not in caplog.text
+    caplog.clear()
+    with caplog.at_level("WARNING", logger="flextensor_amd.selection"):
+        assert select_offload_units(m, ["bogus", "also_bogus"], []) == []
+    assert "No modules matched any include pattern" in caplog.text
+    caplog.clear()
+    with caplog.at_level("WARNING", logger="flextensor_amd.selection"):
+        assert select_offload_units(m, ["layers.*"], ["layers.*"]) == []
+    assert "All 2 included modules were removed" in caplog.text
+    caplog.clear()
+    with caplog.at_level("WARNING", logger="flextensor_amd.selection"):
+        assert select_offload_units(m, ["layers.*.weight", "*.bias"], ["*.norm.weight"]) == ["layers.0", "layers.1",
+                                                                                             "head"]
+    assert "did not match" not in caplog.text  # parameter patterns count as matched
+    caplog.clear()
+    with caplog.at_level("WARNING", logger="flextensor_amd.selection"):
+        assert select_offload_units(m, [], []) == []
+    assert "empty list" in caplog.text and "No modules matched" not in caplog.text
