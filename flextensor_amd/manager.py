@@ -635,14 +635,68 @@ class OffloadManager:
         self.config = config
 
     def offload_units(self) -> tuple[tuple[str, nn.Module], ...]:
-        """Streamed offload units as ``(qualified_name, module)`` (offload_manager.py:3075-3080)."""
-        names = set(self.plan.streamed) if self.plan is not None else {u.label for u in self.units}
-        return tuple((u.label, u.module) for u in self.units if u.label in names)
+        """The patched offload units as ``(qualified_name, live module)`` pairs, in selection order
+        (offload_manager.py:1216-1238).
+
+        The module is the one at that path now, so a unit the caller replaced
+        (a compiled wrapper) is returned as the replacement. Paths that no
+        longer resolve are skipped; a module reachable by two units is listed
+        once. Manual ``offload_block`` regions have no module and are not
+        listed. Which of them stream is ``plan.streamed``.
+        """
+        if self.model is None:
+            return ()
+        seen: set[int] = set()
+        out: list[tuple[str, nn.Module]] = []
+        for u in self.units:
+            if u.module is None:
+                continue
+            try:
+                live = self.model.get_submodule(u.label)
+            except (AttributeError, KeyError):
+                continue
+            if id(live) not in seen:
+                seen.add(id(live))
+                out.append((u.label, live))
+        return tuple(out)
 
     def resident_units(self) -> tuple[tuple[str, nn.Module], ...]:
-        """Offload units that stayed on the GPU as ``(qualified_name, module)`` (offload_manager.py:3083-3088)."""
-        names = set(self.plan.resident) if self.plan is not None else set()
-        return tuple((u.label, u.module) for u in self.units if u.label in names)
+        """The outermost modules that are not offload units and contain none (offload_manager.py:1240-1265;
+        compile/module_swap.py:105-160): the parts of the model that stay on the GPU.
+
+        The root is never listed. A module holding an offload unit, or a
+        container without a forward of its own (``ModuleList``,
+        ``ModuleDict``), is descended into; children of offload units are
+        omitted; a shared module is listed once, at its first path.
+        """
+        if self.model is None:
+            return ()
+        offload_ids = {id(m) for _, m in self.offload_units()}
+        holds: dict[int, bool] = {}
+
+        def holds_unit(mod: nn.Module) -> bool:
+            key = id(mod)
+            if key not in holds:
+                holds[key] = False  # a module tree with a cycle stops here
+                holds[key] = key in offload_ids or any(holds_unit(c) for c in mod.children())
+            return holds[key]
+
+        out: list[tuple[str, nn.Module]] = []
+        seen: set[int] = set()
+
+        def visit(path: str, mod: nn.Module, root: bool) -> None:
+            if not root and id(mod) in offload_ids:
+                return
+            if root or holds_unit(mod) or type(mod).forward is nn.Module.forward:
+                for name, child in mod.named_children():
+                    visit(f"{path}.{name}" if path else name, child, False)
+                return
+            if id(mod) not in seen:
+                seen.add(id(mod))
+                out.append((path, mod))
+
+        visit("", self.model, True)
+        return tuple(out)
 
     def clear_profiling_durations(self) -> None:
         """Drop every profiled duration; the unit order found by discovery stays (offload_manager.py:3131-3141)."""

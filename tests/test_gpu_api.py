@@ -1,6 +1,6 @@
 """The reference's convenience API on a streamed model (GPU).
 
-``offload_units`` / ``resident_units`` report the plan, ``pause_profiling``
+``offload_units`` / ``resident_units`` list the units and the rest, ``pause_profiling``
 keeps warm-up passes out of the profile and the phase count
 (offload_manager.py:3075-3220), and the configuration is fixed once a model
 is managed.
@@ -43,11 +43,11 @@ def test_units_profiling_pause_and_fixed_config(gpu):
         model(x)  # second recorded profiling pass: streaming starts
         assert mgr.phase == OffloadPhase.INFERENCE
         assert torch.equal(model(x), resident(x))
-    streamed = [label for label, _ in ft.offload_units(name)]
-    kept = [label for label, _ in ft.resident_units(name)]
-    assert streamed == mgr.plan.streamed and kept == mgr.plan.resident
-    assert streamed and kept and sorted(streamed + kept) == sorted(f"layers.{i}" for i in range(8))
+    units = [label for label, _ in ft.offload_units(name)]
+    assert units == [f"layers.{i}" for i in range(8)]  # every offload unit, streamed or kept resident
+    assert mgr.plan.streamed and mgr.plan.resident and sorted(mgr.plan.streamed + mgr.plan.resident) == sorted(units)
     assert all(mod is model.get_submodule(label) for label, mod in ft.offload_units(name))
+    assert ft.resident_units(name) == ()  # the stack has nothing outside its layers
     with pytest.raises(RuntimeError, match="release"):
         ft.set_config(OffloadConfig(), name=name)
     assert ft.update_offload_timing(name) is True  # timing is off: nothing to store
