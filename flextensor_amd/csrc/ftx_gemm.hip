@@ -15,10 +15,14 @@
 // dequantizing the weights and running a bf16 GEMM; only the fp32
 // accumulation order differs.
 //
-// Work split: a workgroup owns 16*RT output channels; its S wavefronts split
-// K by 64*U-byte steps (wave w takes steps w, w+S, ...), so every wave streams
-// whole 16-byte pieces of RT*16 rows. The S partial tiles are summed in LDS in
-// wave order, so results do not depend on timing.
+// Work split: a workgroup of S wavefronts owns 16*S output channels (16 per
+// wave) and one K slice; the grid is row groups x K slices. Each workgroup
+// stages its slice of x in LDS once, so L2 serves activations about 2M/(16 S)
+// times the weight bytes. With one slice the kernel writes y directly;
+// otherwise it writes fp32 partials [slice][M][N] and fp8_linear_reduce_kernel
+// sums them in slice order, so results do not depend on timing. The split is
+// a separate kernel because an in-kernel last-arriver reduction needs
+// agent-scope release/acquire, which costs a whole-L2 writeback per workgroup.
 //
 // MFMA 16x16x32 operand layout (gfx950): lane l supplies row/column l%16 and
 // the eight k values 8*(l/16)..8*(l/16)+7 of the 32-wide k block; lane l
