@@ -213,24 +213,35 @@ class RawBlockController:
         self.block_map_cpu: dict[str, torch.Tensor] = {}
         self.block_meta_map: dict[str, list] = {}
         self.label_to_cpu_tensor_id_map: dict[str, list[int]] = {}
-        for label, strategy in strategy_map.items():
-            if not strategy:
-                continue
-            ids, tensors = _unique_tensors(strategy, tensors_map)
-            block = host_pinner.new_block(label_to_size_map[label])
-            block.zero_()
-            self.block_map_cpu[label] = block
-            self.block_meta_map[label] = self.combine_tensors(tensors, block)
-            self.label_to_cpu_tensor_id_map[label] = ids
-        self.block_map_gpu = {
-            b: torch.zeros(max(n, 1), dtype=torch.uint8, device=self.device_gpu) for b, n in block_sizes.items()
-        }
-        self.gpu_block_view_map = {
-            label: self.block_map_gpu[b][: self.block_map_cpu[label].numel()]
-            for label, b in self.label_to_block_id.items()
-            if label in self.block_map_cpu
-        }
-        self.prepare_tensor_id_to_view_mapping()
+        self.block_map_gpu: dict[int, torch.Tensor] = {}
+        self.gpu_block_view_map: dict[str, torch.Tensor] = {}
+        self.label_to_tensor_views_map: dict[str, list[torch.Tensor]] = {}
+        self.tensor_id_to_view_map: dict[int, torch.Tensor] = {}
+        self._rollback = _Rollback()
+        try:
+            # device slots first: a failed allocation then leaves every source untouched
+            self.block_map_gpu = {
+                b: torch.zeros(max(n, 1), dtype=torch.uint8, device=self.device_gpu) for b, n in block_sizes.items()
+            }
+            for label, strategy in strategy_map.items():
+                if not strategy:
+                    continue
+                ids, tensors = _unique_tensors(strategy, tensors_map)
+                block = host_pinner.new_block(label_to_size_map[label])
+                block.zero_()
+                self.block_map_cpu[label] = block
+                self.block_meta_map[label] = self.combine_tensors(tensors, block)
+                self.label_to_cpu_tensor_id_map[label] = ids
+            self.gpu_block_view_map = {
+                label: self.block_map_gpu[b][: self.block_map_cpu[label].numel()]
+                for label, b in self.label_to_block_id.items()
+                if label in self.block_map_cpu
+            }
+            self.prepare_tensor_id_to_view_mapping()
+        except BaseException:
+            self._rollback.restore()
+            self.shutdown()
+            raise
 
     def combine_tensors(self, tensors: Sequence[torch.Tensor], combined: torch.Tensor) -> list:
         """Pack back to back; metadata per tensor is (start, end, shape, dtype, stride)."""
@@ -247,9 +258,12 @@ class RawBlockController:
                 src = c.view(-1).view(torch.uint8)
             combined[cursor: cursor + n] = src
             meta.append((cursor, cursor + n, tuple(t.shape), t.dtype, stride))
-            cursor += n
             if self.release_tensor_memory:
+                rollback = getattr(self, "_rollback", None)
+                if rollback is not None:
+                    rollback.record(t, view_from_block(combined, t.dtype, tuple(t.shape), cursor, stride))
                 t.data = torch.empty(0, dtype=t.dtype)
+            cursor += n
         return meta
 
     @staticmethod
@@ -281,12 +295,13 @@ class RawBlockController:
         return self.block_map_cpu[label].numel()
 
     def commit_construction(self) -> None:
-        return None
+        self._rollback.commit()
 
     def abort_construction(self, primary_error: BaseException | None = None) -> None:
         self.shutdown()
 
     def shutdown(self) -> None:
+        self._rollback.restore()
         for d in (self.block_map_cpu, self.block_meta_map, self.label_to_cpu_tensor_id_map, self.block_map_gpu,
                   self.gpu_block_view_map, self.label_to_tensor_views_map, self.tensor_id_to_view_map):
             d.clear()

@@ -284,6 +284,17 @@ def plan_from_state(state: TensorManagerState, units: Sequence[_Unit], base_byte
     return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
 
 
+@contextlib.contextmanager
+def _oom_context(tensors: Sequence[torch.Tensor], what: str, advice: str) -> Iterator[None]:
+    """Re-raise a device allocation failure naming what was being placed (tensor_manager.py:755-775)."""
+    try:
+        yield
+    except (torch.cuda.OutOfMemoryError, nat.FtxOutOfMemoryError) as exc:
+        nbytes = sum(t.numel() * t.element_size() for t in tensors)
+        raise torch.cuda.OutOfMemoryError(f"GPU out of memory while moving {len(tensors)} {what} "
+                                          f"({nbytes / 2**30:.2f} GiB) to the GPU. {advice}") from exc
+
+
 def _submodule(model: nn.Module, label: str) -> nn.Module | None:
     if not label:
         return None
@@ -404,28 +415,64 @@ class OffloadManager:
         torch.cuda.set_device(self.device)
         self.model = model
         self.units = units
-        self._manual = state is None and not units and self._discovery_passes > 0
-        if self._manual:
-            # manual offload blocks: parameters wait on the host until discovery sees where they are used
-            self._pending = {id(p): p for p in model.parameters() if p.device.type == "cpu"}
-            self._resident_bytes += self._upload_into([b for b in model.buffers() if b.device.type == "cpu"])
-            self._patch_root(model)
-        else:
-            self._place_outside_units(unit_params)
-        custom_ops.register_manager(id(self), self)
-        for u in self.units:
-            if u.module is not None:
-                self._patch(u)
-        self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
-        self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
-        self.phase = OffloadPhase.DISCOVERY if self._discovery_passes > 0 else OffloadPhase.PROFILING
-        if state is not None:
-            self.order = labels
-            self._to_inference(state)
-        elif self.config.discovery_iters == 0 and self.config.profiling_iters == 0:
-            self.order = [u.label for u in self.units]
-            self._to_inference()
+        try:
+            self._manual = state is None and not units and self._discovery_passes > 0
+            if self._manual:
+                # manual offload blocks: parameters wait on the host until discovery sees where they are used
+                self._pending = {id(p): p for p in model.parameters() if p.device.type == "cpu"}
+                self._resident_bytes += self._upload_into([b for b in model.buffers() if b.device.type == "cpu"])
+                self._patch_root(model)
+            else:
+                self._place_outside_units(unit_params)
+            custom_ops.register_manager(id(self), self)
+            for u in self.units:
+                if u.module is not None:
+                    self._patch(u)
+            self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
+            self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
+            self.phase = OffloadPhase.DISCOVERY if self._discovery_passes > 0 else OffloadPhase.PROFILING
+            if state is not None:
+                self.order = labels
+                self._to_inference(state)
+            elif self.config.discovery_iters == 0 and self.config.profiling_iters == 0:
+                self.order = [u.label for u in self.units]
+                self._to_inference()
+        except BaseException:
+            self._abandon()
+            raise
         return model
+
+    def _abandon(self) -> None:
+        """Undo the manager's own changes after a failed ``offload()`` so it can be used again
+        (offload_manager.py:1932-1937): hooks, patched forwards and the loader go; tensors
+        already placed on the GPU stay there, so the model should be discarded."""
+        for h in self._hooks:
+            h.remove()
+        for mod, _orig in self._patched:
+            if "forward" in mod.__dict__:
+                del mod.forward
+        if self._mode is not None:
+            self._mode_depth = 1
+            self._pop_mode()
+        custom_ops.unregister_manager(id(self))
+        if self.loader is not None:
+            try:
+                self.loader.shutdown()
+            except Exception:  # noqa: BLE001 - the primary error is the one to report
+                LOGGER.exception("offload %r: loader shutdown after a failed offload() failed", self.name)
+        self._reset_manual()
+        self.loader = self.controller = self.plan = self.timing = None
+        self.model = None
+        self.units, self._patched, self._hooks, self.order = [], [], [], []
+        self._seen_this_pass, self._pass_done, self._events = [], [], {}
+        self._cpu_data = {}
+        self._forwards = 0
+        self._resident_bytes = 0
+        self._from_state = False
+        self.skip_discovery_honored = None
+        self.compile_fn = None
+        self._load_from_shm = False
+        self.phase = OffloadPhase.NOT_INITIALIZED
 
     def _check_state(self, state: TensorManagerState, name_of: dict[int, str]) -> None:
         if state.loader_type != self.config.transfer_mode:
@@ -806,7 +853,10 @@ class OffloadManager:
         assert self.model is not None
         rest = [p for p in self.model.parameters() if id(p) not in unit_params and p.device.type == "cpu"]
         bufs = [b for b in self.model.buffers() if b.device.type == "cpu"]
-        self._resident_bytes += self._upload_into(rest + bufs)
+        with _oom_context(rest + bufs, "tensors outside the offload units", "Tensors outside the offload units "
+                          "(not matching include_patterns, or matching exclude_patterns) stay on the GPU for good. "
+                          "Broaden include_patterns or narrow exclude_patterns."):
+            self._resident_bytes += self._upload_into(rest + bufs)
 
     def _upload_into(self, tensors: Sequence[torch.Tensor]) -> int:
         cpu = [t for t in tensors if t.device.type == "cpu" and t.numel()]
@@ -1126,7 +1176,9 @@ class OffloadManager:
             self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks)
         plan = self.plan
         resident_params = [p for x in plan.resident for p in self._unit(x).params]
-        self._resident_bytes += self._upload_into(resident_params)
+        with _oom_context(resident_params, f"the {len(plan.resident)} offload units kept resident",
+                          "Lower the budget (max_gpu_mem_fraction / max_gpu_mem_bytes) so that more units stream."):
+            self._resident_bytes += self._upload_into(resident_params)
         layer_stats = [self._unit(x).stats(self._duration(x)) for x in order]
         if plan.block_data is None:
             self.loader = _ResidentLoader()
@@ -1135,25 +1187,16 @@ class OffloadManager:
             tensors_map = {id(p): p for x in plan.streamed for p in self._unit(x).params}
             pinner = HostPinner(cfg.pinned_memory_mode, enabled=cfg.pinned_memory)
             mode = nat.COPY_MODES[cfg.copy_engine]
-            if cfg.transfer_mode == "raw_block_transfer":
-                self.controller = RawBlockController(bd.label_to_size_map, bd.block_sizes, self.device, tensors_map,
-                                                     plan.strategy_map, bd.label_to_block_id, host_pinner=pinner,
-                                                     copy_mode=mode)
-            else:
-                shm_names: dict[str, str] | None = None
-                if cfg.shm_enabled:
-                    if self._load_from_shm:
-                        assert state is not None and state.shm_block_name_map
-                        shm_names = dict(state.shm_block_name_map)
-                    else:
-                        labels = [x for group in bd.allocation_ordered.values() for x in group
-                                  if plan.strategy_map.get(x)]
-                        shm_names = {x: f"{cfg.shm_namespace}_b{i}" for i, x in enumerate(labels)}
-                self.controller = AllocationBlockController(bd.allocation_ordered, self.device, tensors_map,
-                                                            plan.strategy_map, bd.label_to_block_id,
-                                                            host_pinner=pinner, copy_mode=mode,
-                                                            shm_block_name_map=shm_names,
-                                                            load_from_shm=self._load_from_shm)
+            try:
+                self._build_controller(cfg, plan, bd, tensors_map, pinner, mode, state)
+            except (torch.cuda.OutOfMemoryError, nat.FtxOutOfMemoryError) as exc:
+                host = sum(bd.label_to_size_map.values())
+                slots = sum(bd.block_sizes.values())
+                raise torch.cuda.OutOfMemoryError(
+                    f"out of memory while building the streaming blocks: {len(bd.label_to_size_map)} page-locked "
+                    f"host blocks ({host / 2**30:.2f} GiB) and {len(bd.block_sizes)} GPU ring slots "
+                    f"({slots / 2**30:.2f} GiB). The slots take GPU memory within the budget; the blocks take "
+                    "page-locked host memory.") from exc
             for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
                 tensors_map[tid].data = view
             reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"
@@ -1176,6 +1219,29 @@ class OffloadManager:
                     len(plan.resident), self.build_seconds)
         if cfg.enable_diagnostics:
             LOGGER.info("offload %r plan:\n%s", self.name, self.plan_table())
+
+    def _build_controller(self, cfg: OffloadConfig, plan: StreamPlan, bd: Any, tensors_map: dict[int, torch.Tensor],
+                          pinner: HostPinner, mode: int, state: TensorManagerState | None) -> None:
+        """The block controller of the plan: packed host blocks and GPU ring slots."""
+        if cfg.transfer_mode == "raw_block_transfer":
+            self.controller = RawBlockController(bd.label_to_size_map, bd.block_sizes, self.device, tensors_map,
+                                                 plan.strategy_map, bd.label_to_block_id, host_pinner=pinner,
+                                                 copy_mode=mode)
+        else:
+            shm_names: dict[str, str] | None = None
+            if cfg.shm_enabled:
+                if self._load_from_shm:
+                    assert state is not None and state.shm_block_name_map
+                    shm_names = dict(state.shm_block_name_map)
+                else:
+                    labels = [x for group in bd.allocation_ordered.values() for x in group
+                              if plan.strategy_map.get(x)]
+                    shm_names = {x: f"{cfg.shm_namespace}_b{i}" for i, x in enumerate(labels)}
+            self.controller = AllocationBlockController(bd.allocation_ordered, self.device, tensors_map,
+                                                        plan.strategy_map, bd.label_to_block_id,
+                                                        host_pinner=pinner, copy_mode=mode,
+                                                        shm_block_name_map=shm_names,
+                                                        load_from_shm=self._load_from_shm)
 
     def plan_table(self) -> str:
         """Per unit: bytes, profiled ms, and where it lives (its slot and transfer label when streamed)."""

@@ -178,3 +178,28 @@ def test_failed_construction_restores_released_sources():
     assert torch.equal(tensors[1], torch.arange(64, dtype=torch.uint8))  # packed, released, then restored
     assert torch.equal(tensors[2], torch.arange(32, dtype=torch.uint8))
     assert not os.path.exists("/dev/shm/ftx_unused_name_a")  # the segment made for "a" went with the build
+
+
+class _FailingPinner(HostPinner):
+    """Hands out unpinned blocks and fails the n-th request, as an exhausted pinned pool would."""
+
+    def __init__(self, fail_at: int) -> None:
+        super().__init__("torch", enabled=False)
+        self.calls, self.fail_at = 0, fail_at
+
+    def new_block(self, nbytes: int) -> torch.Tensor:
+        self.calls += 1
+        if self.calls == self.fail_at:
+            raise nat.FtxOutOfMemoryError(nat.FTX_ERR_OOM, "hipHostMalloc failed")
+        return super().new_block(nbytes)
+
+
+def test_raw_controller_failure_restores_released_sources():
+    tensors = {1: torch.arange(64, dtype=torch.uint8), 2: torch.arange(16, dtype=torch.float32).reshape(4, 4).t()}
+    want = {k: v.clone() for k, v in tensors.items()}
+    strategy = {"a": _stats(1, 64), "b": _stats(2, 64)}
+    with pytest.raises(nat.FtxOutOfMemoryError):
+        RawBlockController({"a": 64, "b": 64}, {0: 64}, torch.device("cpu"), tensors, strategy, {"a": 0, "b": 0},
+                           host_pinner=_FailingPinner(fail_at=2))
+    for k in tensors:  # "a" was packed and released before "b" failed
+        assert torch.equal(tensors[k], want[k])

@@ -175,3 +175,20 @@ def test_profile_mode_torch_function_refused():
     with pytest.raises(ValueError, match="torch_function"):
         OffloadConfig(profile_mode="torch_function")
     assert OffloadConfig(profile_mode="getter").profile_mode == "getter"
+
+
+def test_out_of_memory_names_what_was_being_placed(names):
+    names.append("oom")
+
+    def no_room(self, tensors):
+        raise torch.cuda.OutOfMemoryError("HIP out of memory")
+
+    with mock.patch.object(M.nat, "load", lambda: None), \
+            mock.patch.object(M.torch.cuda, "set_device", lambda d: None), \
+            mock.patch.object(M.custom_ops, "register_manager", lambda *a: None), \
+            mock.patch.object(M.OffloadManager, "_upload_into", no_room):
+        with pytest.raises(torch.cuda.OutOfMemoryError, match="tensors outside the offload units") as info:
+            M.get_offload_manager("oom").offload(_Stack(), OffloadConfig(include_patterns=["layers.0"]))
+    assert "include_patterns" in str(info.value) and isinstance(info.value.__cause__, torch.cuda.OutOfMemoryError)
+    mgr = M.get_offload_manager("oom")  # the failed offload() left the manager reusable
+    assert mgr.model is None and mgr.phase == M.OffloadPhase.NOT_INITIALIZED and not mgr._hooks
