@@ -16,10 +16,13 @@ timing uses HIP events with timing enabled. :func:`hidden_fraction` is
 
 from __future__ import annotations
 
+import logging
 import statistics
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 from typing import Any
+
+LOGGER = logging.getLogger(__name__)
 
 
 @dataclass(frozen=True, slots=True)
@@ -201,6 +204,10 @@ def format_offload_timing_table(data: OffloadTimingSnapshot | OffloadTimingRepor
     return "\n".join(lines)
 
 
+OFFLOAD_TIMING_LOG_EVERY = 10  # passes per periodic timing table (offload_timing.py:26)
+OFFLOAD_TIMING_MEASURE_MAX_PASSES = 1024  # stored passes kept for collect_offload_timing (offload_timing.py:27)
+
+
 class OffloadTimingCollector:
     """Records per-trap events during a pass; a no-op when ``enabled`` is False.
 
@@ -218,9 +225,10 @@ class OffloadTimingCollector:
         current_stream: Callable[[], Any] | None = None,
         synchronize: Callable[[], None] | None = None,
         on_pass: Callable[[OffloadTimingSnapshot], None] | None = None,
-        max_passes: int = 1024,
+        max_passes: int = OFFLOAD_TIMING_MEASURE_MAX_PASSES,
         graph_replay: bool = False,
         is_capturing: Callable[[], bool] | None = None,
+        log_every: int = OFFLOAD_TIMING_LOG_EVERY,
     ) -> None:
         """``graph_replay``: timing points are device timestamps written by
         kernels, so a captured pass is re-timed by every replay and
@@ -237,6 +245,8 @@ class OffloadTimingCollector:
         self._max_passes = max_passes
         self.snapshots: list[OffloadTimingSnapshot] = []
         self._measure_window = True  # passes are published while open (offload_timing.py:445-449)
+        self._log_every = log_every
+        self._log_window: list[OffloadTimingSnapshot] = []  # every finished pass, for the periodic table
         self._pass_active = False
         self._events: dict[str, dict[str, Any]] = {}
         self._done: dict[str, set[str]] = {"transfer": set(), "compute": set(), "wait": set()}
@@ -362,14 +372,27 @@ class OffloadTimingCollector:
         for s in self._done.values():
             s.clear()
         self._pass_active = False
+        snap = OffloadTimingSnapshot(recs)
+        self._maybe_log(snap)
         if not self._measure_window:
             return False
-        snap = OffloadTimingSnapshot(recs)
         self.snapshots.append(snap)
         del self.snapshots[: max(0, len(self.snapshots) - self._max_passes)]
         if self._on_pass is not None:
             self._on_pass(snap)
         return True
+
+    def _maybe_log(self, snap: OffloadTimingSnapshot) -> None:
+        """Every ``log_every`` finished passes, log their table at INFO (offload_timing.py:721-736)."""
+        if self._log_every <= 0:
+            return
+        self._log_window.append(snap)
+        if len(self._log_window) < self._log_every:
+            return
+        rep = build_report(self._log_window)
+        LOGGER.info("offload timing (last %d passes, average stall per pass %.2f ms)\n%s", rep.num_passes,
+                    rep.total_wait_avg, format_offload_timing_table(rep))
+        self._log_window = []
 
     def report(self) -> OffloadTimingReport:
         self.flush()

@@ -428,3 +428,18 @@ def test_measure_window_stores_only_sampled_passes():
     _timed_pass(col)
     mgr.cancel_offload_timing_sample()
     assert mgr.finish_offload_timing_sample(replay_generation=None) is False and len(col.snapshots) == 1
+
+
+def test_periodic_table_every_ten_passes_even_outside_the_sample_window(caplog):
+    """offload_timing.py:683-736: every finished pass goes to the rolling log table, sampled or not."""
+    clock = {"now": 0.0, "step": 1.0, "recorded": []}
+    col = OffloadTimingCollector(["L0", "L1"], event_factory=lambda: _ClockEvent(clock), current_stream=lambda: None,
+                                 synchronize=lambda: None, is_capturing=lambda: False)
+    col.set_measure_window(False)
+    with caplog.at_level("INFO", logger="flextensor_amd.timing"):
+        for _ in range(10):
+            _timed_pass(col)
+        assert "offload timing" not in caplog.text  # nine finished so far
+        _timed_pass(col)  # finishes the tenth
+    assert caplog.text.count("offload timing (last 10 passes") == 1 and "L0" in caplog.text
+    assert col.snapshots == []  # the closed window stored none of them
