@@ -122,6 +122,10 @@ class _PipelinedLoader(PreallocatedLoader):
                          type(self).__name__, len(self.scheduled_transfers))
             self._transfer_runtime.join()
             self.scheduled_transfers.clear()
+            # The aborted pass never reached the labels that load the next pass's first slots:
+            # load them again, as at construction. (The reference, loaders.py:1729-1740, only
+            # joins and clears, so its first labels would then read stale slots.)
+            self.preload()
         self.offload_timing_collector.on_pass_start()
         self.piecewise_prefetch_policy.reset()
 

@@ -1048,9 +1048,10 @@ class OffloadManager:
                 torch.ops.flextensor.post_compute(produced if produced is not None else carrier, label, mid)
                 return out
             mgr._enter(label)
-            out = orig(*args, **kwargs)
-            mgr._exit(label)
-            return out
+            try:
+                return orig(*args, **kwargs)
+            finally:
+                mgr._exit(label)  # also when the unit raises, as the reference's trap exit does
 
         unit.module.forward = forward
         self._patched.append((unit.module, orig))
@@ -1108,6 +1109,10 @@ class OffloadManager:
                 raise RuntimeError("offload_timing='eager' cannot time a captured graph; "
                                    "capture with offload_timing='cuda_graph' or 'off'")
             return
+        if self.phase in (OffloadPhase.DISCOVERY, OffloadPhase.PROFILING):
+            # a pass that raised never reached the post-forward hook: drop what it left behind
+            self._seen_this_pass = []
+            self._events.clear()
         k = self.config.max_inflight_passes
         if self.phase == OffloadPhase.INFERENCE and k > 0 and len(self._pass_done) >= k:
             self._pass_done[-k].synchronize()

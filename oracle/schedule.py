@@ -97,11 +97,18 @@ def _preload_set(t2c, layers):
     return {t: c for t, c in t2c.items() if t in where and c in where and where[c] < where[t]}
 
 
-def trace(kind, layers, t2c, l2b, calls):
+def trace(kind, layers, t2c, l2b, calls, *, reload_after_abort=False):
     """Operations issued for ``calls`` (a list of ('enter'|'forward'|'exit'|'join', label)).
 
     ``kind`` is ``"default"`` or ``"reordered"``. Construction (with its
     preload) is not part of the returned trace.
+
+    ``reload_after_abort`` models one deliberate difference of the product
+    from the reference: after the abort recovery at the first label (a pass
+    that never reached its last label), the cyclic preload transfers are
+    issued again, because the aborted pass never issued the transfers that
+    fill the next pass's first slots. The reference (loaders.py:1729-1740)
+    only joins and clears; its default is kept here.
     """
     sim = _Sim()
     rt = _Runtime(sim)
@@ -146,6 +153,11 @@ def trace(kind, layers, t2c, l2b, calls):
             if label == first and rt.active:
                 rt.join()
                 scheduled.clear()
+                if reload_after_abort and pre:
+                    rt.begin()
+                    for t in pre:
+                        rt.submit(l2b[t], t)
+                    rt.join()
             if not rt.active:
                 rt.begin()
             if kind == "reordered":

@@ -115,3 +115,49 @@ def test_manager_seam_and_transfer_benchmark(gpu, tmp_path):
     with torch.no_grad():
         assert torch.equal(twin(x), want)
     ft.release("seam-dst")
+
+
+class _Flaky(torch.nn.Module):
+    """A unit that raises after its compute when told to."""
+
+    def __init__(self, inner: torch.nn.Module) -> None:
+        super().__init__()
+        self.inner = inner
+        self.fail = False
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = self.inner(x)
+        if self.fail:
+            raise RuntimeError("unit failed")
+        return y
+
+
+def test_a_failing_unit_leaves_every_phase_usable(gpu):
+    """A unit that raises still exits its trap (trap_tensor_mode.py:376-397): its tensors go back in
+    discovery and profiling, its slot is released in streaming, and the next forward is exact."""
+    model = W.build_mlp_stack(6, 256, 704, seed=94)
+    resident = copy.deepcopy(model).to(gpu)
+    model.layers = torch.nn.ModuleList(_Flaky(layer) for layer in model.layers)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, max_gpu_mem_bytes=4 * layer)
+    name = "flaky"
+    ft.offload(model, cfg, name=name)
+    mgr = ft.get_offload_manager(name)
+    x = W.mlp_input(8, 256, seed=94).to(gpu)
+    with torch.no_grad():
+        want = resident(x)
+        for phase in (OffloadPhase.DISCOVERY, OffloadPhase.PROFILING, OffloadPhase.INFERENCE):
+            assert mgr.phase == phase
+            model.layers[3].fail = True
+            with pytest.raises(RuntimeError, match="unit failed"):
+                model(x)
+            model.layers[3].fail = False
+            if phase != OffloadPhase.INFERENCE:
+                assert all(p.device.type == "cpu" for p in model.layers[3].parameters())  # handed back
+                assert mgr.phase == phase  # the failed pass counted for nothing
+            assert torch.equal(model(x), want)
+        assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.streamed
+        for _ in range(2):
+            assert torch.equal(model(x), want)
+    ft.release(name)

@@ -241,7 +241,29 @@ def test_abort_recovery_joins_then_clears(kind, caplog):
     assert any("abort recovery" in r.getMessage() for r in caplog.records)
     assert rec.find("record_event", stream="transfer") and rec.find("wait_event", stream="compute")
     calls = [("enter", "embed"), ("enter", "embed")]
-    assert osch.trace(kind, labels, t2c, l2b, calls)[-len(rec.log):] == rec.triples()
+    assert osch.trace(kind, labels, t2c, l2b, calls, reload_after_abort=True)[-len(rec.log):] == rec.triples()
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_abort_recovery_reloads_the_first_slots(kind):
+    """A pass that stopped early never issued the cyclic transfers for the next pass's first labels;
+    recovery issues them again before the first label reads its slot."""
+    labels = ["L0", "L1", "L2", "L3"]
+    t2c = {"L0": "L1", "L1": "L2", "L2": "L3", "L3": "L0"}
+    l2b = {"L0": 0, "L1": 1, "L2": 0, "L3": 1}
+    loader, rec, ctrl = _make(kind, labels, t2c, l2b)
+    calls = [("enter", "L0"), ("forward", "L0"), ("exit", "L0"), ("enter", "L1")]  # the pass stops in L1
+    for op, x in calls:
+        getattr(loader, op)(x) if op != "forward" else rec.forward(x)
+    rec.log.clear()
+    loader.enter("L0")  # next pass
+    reload = [e for e in rec.log if e.op == "schedule_transfer" and e.target == "L3"]
+    assert reload, rec.dump()  # L3 carries L0's weights: issued again
+    full = calls + [("enter", "L0")]
+    product = osch.trace(kind, labels, t2c, l2b, full, reload_after_abort=True)
+    assert product[-len(rec.log):] == rec.triples()
+    reference = osch.trace(kind, labels, t2c, l2b, full)
+    assert len(reference) < len(product)  # the reference's recovery issues no transfer
 
 
 @pytest.mark.parametrize("kind", ["default", "reordered"])
