@@ -334,6 +334,7 @@ class OffloadManager:
         self._load_from_shm = False
         self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
         self._from_state = False
+        self._pinner: HostPinner | None = None
         self.memory_transfer_stats: dict[int, float] = {}
         self.skip_discovery_honored: bool | None = None  # None until offload() decides
         self._discovery_passes = 0
@@ -442,6 +443,16 @@ class OffloadManager:
             raise
         return model
 
+    def _release_pins(self) -> None:
+        """End the in-place page locks of ``host_register`` mode (host_pinning.py:314-344).
+
+        The reference releases pins at manager shutdown, not with the blocks.
+        The memory stays valid, now pageable, for the views that still hold it.
+        """
+        pinner, self._pinner = self._pinner, None
+        if pinner is not None:
+            pinner.release_all()
+
     def _abandon(self) -> None:
         """Undo the manager's own changes after a failed ``offload()`` so it can be used again
         (offload_manager.py:1932-1937): hooks, patched forwards and the loader go; tensors
@@ -461,6 +472,7 @@ class OffloadManager:
             except Exception:  # noqa: BLE001 - the primary error is the one to report
                 LOGGER.exception("offload %r: loader shutdown after a failed offload() failed", self.name)
         self._reset_manual()
+        self._release_pins()
         self.loader = self.controller = self.plan = self.timing = None
         self.model = None
         self.units, self._patched, self._hooks, self.order = [], [], [], []
@@ -800,12 +812,15 @@ class OffloadManager:
             u.compiled = None
         self.compile_fn = None
         self._load_from_shm = False
-        restore = {}
+        restore: dict[int, torch.Tensor] = {}
+        shared: set[int] = set()
         if self.controller is not None and preserve_model:
-            for label in self.controller.block_map_cpu:
+            for label, block in self.controller.block_map_cpu.items():
                 ids = self.controller.label_to_cpu_tensor_id_map[label]
                 for tid, view in zip(ids, self._cpu_views(label)):
                     restore[tid] = view
+                    if getattr(block, "shm_segment", None) is not None:
+                        shared.add(tid)
         params = {id(p): p for u in self.units for p in u.params}
         params.update({id(p): p for p in self.model.parameters()})
         if self.loader is not None:
@@ -814,7 +829,9 @@ class OffloadManager:
             if not preserve_model:
                 p.data = torch.empty(0, dtype=p.dtype)
             elif tid in restore:
-                p.data = restore[tid].clone()
+                # the host block's own view (tensor_manager.py:2320-2354): no second copy of the model;
+                # a shared-memory block is copied out so the parameter does not keep other processes' segment
+                p.data = restore[tid].clone() if tid in shared else restore[tid]
             elif p.device.type != "cpu":
                 p.data = p.data.cpu()
         if preserve_model:
@@ -824,6 +841,7 @@ class OffloadManager:
             self._mode_depth = 1
             self._pop_mode()
         self._reset_manual()
+        self._release_pins()
         self._from_state = False
         self.skip_discovery_honored = None
         self.loader = self.controller = self.plan = None
@@ -1190,7 +1208,7 @@ class OffloadManager:
         else:
             bd = plan.block_data
             tensors_map = {id(p): p for x in plan.streamed for p in self._unit(x).params}
-            pinner = HostPinner(cfg.pinned_memory_mode, enabled=cfg.pinned_memory)
+            pinner = self._pinner = HostPinner(cfg.pinned_memory_mode, enabled=cfg.pinned_memory)
             mode = nat.COPY_MODES[cfg.copy_engine]
             try:
                 self._build_controller(cfg, plan, bd, tensors_map, pinner, mode, state)

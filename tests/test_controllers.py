@@ -203,3 +203,34 @@ def test_raw_controller_failure_restores_released_sources():
                            host_pinner=_FailingPinner(fail_at=2))
     for k in tensors:  # "a" was packed and released before "b" failed
         assert torch.equal(tensors[k], want[k])
+
+
+def test_release_hands_back_block_views_and_ends_the_pins(recorded_pins):
+    """tensor_manager.py:2320-2354 and host_pinning.py:314-344: released parameters view their host block
+    (no second copy of the model) and the in-place page locks end with the manager."""
+    from unittest import mock
+
+    import flextensor_amd.manager as M
+
+    model = torch.nn.Sequential(torch.nn.Linear(4, 4), torch.nn.Linear(4, 4))
+    params = list(model[0].parameters())
+    want = [p.detach().clone() for p in params]
+    tensors = {id(p): p for p in params}
+    strategy = {"0": [TensorStatistics(id(p), f"t{i}", p.numel() * p.element_size(), 0.0)
+                      for i, p in enumerate(params)]}
+    pinner = HostPinner("host_register")
+    ctrl = AllocationBlockController({0: ["0"]}, torch.device("cpu"), tensors, strategy, {"0": 0}, host_pinner=pinner)
+    ctrl.commit_construction()
+    for tid, view in ctrl.get_tensor_id_to_view_mapping().items():
+        tensors[tid].data = view  # the parameters alias their slot, as when streaming
+    ctrl.schedule_transfer("0")
+    host_block = ctrl.block_map_cpu["0"].block
+    mgr = M.OffloadManager("release-views")
+    mgr.model, mgr.controller, mgr._pinner, mgr.device = model, ctrl, pinner, torch.device("cpu")
+    mgr.units = [M._Unit("0", model[0], params, ["0.weight", "0.bias"])]
+    assert len(recorded_pins["register"]) == 1 and recorded_pins["unregister"] == []
+    with mock.patch.object(M.torch.cuda, "synchronize", lambda *a: None):
+        mgr.release()
+    for p, w in zip(params, want):
+        assert torch.equal(p, w) and p.untyped_storage().data_ptr() == host_block.data_ptr()
+    assert len(recorded_pins["unregister"]) == 1 and pinner.pinned_bytes == 0
