@@ -39,6 +39,7 @@ import logging
 import os
 import threading
 import time
+import types
 from collections.abc import Callable, Iterator, Sequence
 from dataclasses import dataclass, field
 from enum import Enum
@@ -459,9 +460,7 @@ class OffloadManager:
         already placed on the GPU stay there, so the model should be discarded."""
         for h in self._hooks:
             h.remove()
-        for mod, _orig in self._patched:
-            if "forward" in mod.__dict__:
-                del mod.forward
+        self._unpatch(self._patched)
         if self._mode is not None:
             self._mode_depth = 1
             self._pop_mode()
@@ -805,9 +804,7 @@ class OffloadManager:
         custom_ops.unregister_manager(id(self))
         for h in self._hooks:
             h.remove()
-        for mod, orig in self._patched:
-            if "forward" in mod.__dict__:
-                del mod.forward
+        self._unpatch(self._patched)
         for u in self.units:
             u.compiled = None
         self.compile_fn = None
@@ -993,20 +990,24 @@ class OffloadManager:
 
     def _patch_root(self, model: nn.Module) -> None:
         """Watch the whole forward during manual discovery, so parameters used outside blocks are placed too."""
-        orig = model.forward
+        own = model.__dict__.get("forward")
         mgr = self
 
-        def forward(*args: Any, **kwargs: Any) -> Any:
+        def forward(self_module: nn.Module, *args: Any, **kwargs: Any) -> Any:
+            def orig() -> Any:
+                return own(*args, **kwargs) if own is not None else type(self_module).forward(self_module, *args,
+                                                                                              **kwargs)
+
             if mgr.phase == OffloadPhase.DISCOVERY and mgr._pending and not torch.compiler.is_compiling():
                 mgr._push_mode()
                 try:
-                    return orig(*args, **kwargs)
+                    return orig()
                 finally:
                     mgr._pop_mode()
-            return orig(*args, **kwargs)
+            return orig()
 
-        model.forward = forward
-        self._patched.append((model, orig))
+        model.forward = types.MethodType(forward, model)
+        self._patched.append((model, own))
 
     def _finish_manual_discovery(self) -> None:
         """The blocks seen become units; parameters no block owns go to the GPU for good."""
@@ -1032,17 +1033,27 @@ class OffloadManager:
         self.order = [u.label for u in units]
 
     def _patch(self, unit: _Unit) -> None:
-        """Wrap the unit's forward in enter/exit (offload_manager.py:1136-1162).
+        """Wrap the unit's forward in enter/exit (offload_manager.py:1114-1162).
 
         Eagerly the manager is called directly. Under ``torch.compile`` the
         calls go through the ``flextensor::pre_compute`` / ``post_compute``
         custom ops, which the compiler keeps in place around the unit's
         compute (custom_ops.py:267-328).
+
+        The wrapper is bound to the module and runs the class's ``forward``
+        on the module it is called on, so a copy of the model runs its own
+        forward (the reason the reference patches with the unbound class
+        function). A ``forward`` the caller had set on the instance is kept
+        and put back by :meth:`release`.
         """
-        orig = unit.module.forward
+        module = unit.module
+        own = module.__dict__.get("forward")
         mgr, label, mid = self, unit.label, id(self)
 
-        def forward(*args: Any, **kwargs: Any) -> Any:
+        def forward(self_module: nn.Module, *args: Any, **kwargs: Any) -> Any:
+            def orig(*a: Any, **k: Any) -> Any:
+                return own(*a, **k) if own is not None else type(self_module).forward(self_module, *a, **k)
+
             if (unit.compiled is not None and not torch.compiler.is_compiling() and not _COMPILED_CALL.active
                     and mgr.phase == OffloadPhase.INFERENCE):
                 # Per-unit compiled graph: it re-enters this forward while tracing (the branch below).
@@ -1071,8 +1082,17 @@ class OffloadManager:
             finally:
                 mgr._exit(label)  # also when the unit raises, as the reference's trap exit does
 
-        unit.module.forward = forward
-        self._patched.append((unit.module, orig))
+        module.forward = types.MethodType(forward, module)
+        self._patched.append((module, own))
+
+    @staticmethod
+    def _unpatch(patched: Sequence[tuple[nn.Module, Any]]) -> None:
+        """Put back each module's own forward: the class's, or the one the caller had set on the instance."""
+        for mod, own in patched:
+            if own is not None:
+                mod.forward = own
+            elif "forward" in mod.__dict__:
+                del mod.forward
 
     def _unit(self, label: str) -> _Unit:
         for u in self.units:

@@ -192,3 +192,57 @@ def test_out_of_memory_names_what_was_being_placed(names):
     assert "include_patterns" in str(info.value) and isinstance(info.value.__cause__, torch.cuda.OutOfMemoryError)
     mgr = M.get_offload_manager("oom")  # the failed offload() left the manager reusable
     assert mgr.model is None and mgr.phase == M.OffloadPhase.NOT_INITIALIZED and not mgr._hooks
+
+
+class _Ident(torch.nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.lin = torch.nn.Linear(2, 2)
+
+    def forward(self, x):
+        return id(self)
+
+
+class _Holder(torch.nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.layers = torch.nn.ModuleList(_Ident() for _ in range(2))
+
+
+class _Loader:
+    def __init__(self) -> None:
+        self.calls: list[tuple[str, str]] = []
+
+    def enter(self, label):
+        self.calls.append(("enter", label))
+
+    def exit(self, label):
+        self.calls.append(("exit", label))
+
+    def shutdown(self):
+        return None
+
+
+def test_patched_forward_runs_on_a_copy_of_the_module(names):
+    """offload_manager.py:1114-1135: a copied model's patched forward must run the copy, not the original."""
+    import copy
+
+    names.append("rebind")
+    with mock.patch.object(M.nat, "load", lambda: None), \
+            mock.patch.object(M.torch.cuda, "set_device", lambda d: None), \
+            mock.patch.object(M.custom_ops, "register_manager", lambda *a: None), \
+            mock.patch.object(M.OffloadManager, "_upload_into", lambda self, ts: 0):
+        model = _Holder()
+        custom = model.layers[1].forward = lambda x: "instance forward"
+        mgr = M.get_offload_manager("rebind")
+        mgr.offload(model, OffloadConfig(include_patterns=["layers.*"]))
+    mgr.phase, mgr.loader = M.OffloadPhase.INFERENCE, _Loader()
+    twin = copy.deepcopy(model)
+    assert model.layers[0](1) == id(model.layers[0]) and twin.layers[0](1) == id(twin.layers[0])
+    assert model.layers[1](1) == "instance forward"
+    assert mgr.loader.calls[:2] == [("enter", "layers.0"), ("exit", "layers.0")]
+    mgr.phase, mgr.device = M.OffloadPhase.INFERENCE, torch.device("cpu")
+    with mock.patch.object(M.torch.cuda, "synchronize", lambda *a: None):
+        mgr.release()
+    assert "forward" not in model.layers[0].__dict__  # the class forward again
+    assert model.layers[1].forward is custom  # the caller's own forward is put back
