@@ -134,7 +134,6 @@ class AllocationBlock:
         self.shm_block_name = shm_block_name if self.device.type == "cpu" else None
         self.load_from_shm = load_from_shm
         self.shm_segment: Any = None
-        self._shm_pinned_ptr = 0
         self.memory_alignment = _check_alignment(memory_alignment)
         self.release_tensor_memory = release_tensor_memory
         self.tensors: list[torch.Tensor] = []
@@ -192,7 +191,6 @@ class AllocationBlock:
         block = torch.frombuffer(seg.buf, dtype=torch.uint8, count=size)
         if self.pinned_memory and self.host_pinner.enabled and self.host_pinner.mode == "host_register":
             self.host_pinner.pin_in_place(block)
-            self._shm_pinned_ptr = block.data_ptr()
         return block
 
     def allocate(self) -> list[torch.Tensor]:
@@ -238,13 +236,11 @@ class AllocationBlock:
         self.tensors = []
         seg, self.shm_segment = self.shm_segment, None
         if seg is not None:
-            if self._shm_pinned_ptr:
-                # a registered mapping must be unregistered before it can be unmapped
-                self.host_pinner.release(self._shm_pinned_ptr)
-                self._shm_pinned_ptr = 0
             # The creator removes the name; other processes' mappings stay valid. The
             # mapping itself is not closed here: tensors (restored parameters, user
             # references) may still view it, and it is unmapped with the last of them.
+            # An in-place pin of the mapping ends with the pinner's release_all(), like
+            # every other pin (pins are released at manager shutdown, not with blocks).
             seg.unlink()
 
 

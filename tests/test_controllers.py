@@ -234,3 +234,19 @@ def test_release_hands_back_block_views_and_ends_the_pins(recorded_pins):
     for p, w in zip(params, want):
         assert torch.equal(p, w) and p.untyped_storage().data_ptr() == host_block.data_ptr()
     assert len(recorded_pins["unregister"]) == 1 and pinner.pinned_bytes == 0
+
+
+def test_shared_memory_block_release_keeps_its_pin(recorded_pins):
+    """loaders_pin_fallback / allocation_block tests of the reference: only release_all ends pins,
+    also for a block living in a shared-memory segment."""
+    import uuid
+
+    pinner = HostPinner("host_register")
+    block = AllocationBlock(device="cpu", host_pinner=pinner, shm_block_name=f"ftx_t_{uuid.uuid4().hex[:10]}")
+    block.add(torch.arange(100, dtype=torch.int32))
+    views = block.allocate()
+    assert len(recorded_pins["register"]) == 1
+    block.release()
+    assert recorded_pins["unregister"] == [] and torch.equal(views[0], torch.arange(100, dtype=torch.int32))
+    pinner.release_all()
+    assert len(recorded_pins["unregister"]) == 1
