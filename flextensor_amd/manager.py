@@ -74,6 +74,7 @@ from .timing import OffloadTimingCollector, OffloadTimingReport
 
 LOGGER = logging.getLogger(__name__)
 DEFAULT_MANAGER_NAME = "default"
+MIN_GPU_BUDGET_BYTES = 256 * 1024**2  # below this much available memory a budget cannot be met
 
 
 class OffloadPhase(Enum):
@@ -1194,12 +1195,31 @@ class OffloadManager:
             self._to_inference()
 
     def _budget(self) -> int | None:
-        if self.config.max_gpu_mem_bytes is not None:
-            return self.config.max_gpu_mem_bytes
-        if self.config.max_gpu_mem_fraction is not None:
-            total = torch.cuda.get_device_properties(self.device).total_memory
-            return int(total * self.config.max_gpu_mem_fraction)
-        return None
+        """The plan's GPU byte budget (gpu_budget.py:66-113): ``max_gpu_mem_bytes``, else the fraction of
+        the device's total memory, capped by what is available now.
+
+        Available is the free memory plus the allocator's reusable cache, plus
+        the tensors this manager already placed (the plan counts them, yet
+        they no longer show as free). Less than 256 MiB available raises
+        ``RuntimeError``.
+        """
+        cfg = self.config
+        if cfg.max_gpu_mem_bytes is None and cfg.max_gpu_mem_fraction is None:
+            return None
+        free, total = torch.cuda.mem_get_info(self.device)
+        cache = max(0, torch.cuda.memory_reserved(self.device) - torch.cuda.memory_allocated(self.device))
+        if free + cache < MIN_GPU_BUDGET_BYTES:
+            raise RuntimeError(f"Insufficient free GPU memory: {(free + cache) / 2**30:.2f} GiB available (free="
+                               f"{free / 2**30:.2f}, reusable cache={cache / 2**30:.2f}), minimum required: "
+                               f"{MIN_GPU_BUDGET_BYTES / 2**30:.2f} GiB")
+        budget = cfg.max_gpu_mem_bytes if cfg.max_gpu_mem_bytes is not None else int(total * cfg.max_gpu_mem_fraction)
+        available = free + cache + self._resident_bytes
+        if budget > available:
+            LOGGER.warning("offload %r: capping the GPU memory budget from %.2f GiB to %.2f GiB (%.2f GiB free, "
+                           "%.2f GiB allocator cache, %.2f GiB already placed)", self.name, budget / 2**30,
+                           available / 2**30, free / 2**30, cache / 2**30, self._resident_bytes / 2**30)
+            budget = available
+        return budget
 
     def _plan_from_state(self, state: TensorManagerState) -> StreamPlan:
         for st in state.stats:

@@ -246,3 +246,35 @@ def test_patched_forward_runs_on_a_copy_of_the_module(names):
         mgr.release()
     assert "forward" not in model.layers[0].__dict__  # the class forward again
     assert model.layers[1].forward is custom  # the caller's own forward is put back
+
+
+def test_budget_is_capped_by_available_memory(caplog):
+    """gpu_budget.py:66-113: the fractional budget never exceeds free memory plus the allocator cache
+    (plus what the manager already placed); below 256 MiB available it refuses."""
+    GiB = 2**30
+    mgr = M.OffloadManager("budget")
+    mgr.device = torch.device("cuda", 0)
+    mgr._resident_bytes = 1 * GiB
+
+    def state(free, total, reserved, allocated):
+        return (mock.patch.object(M.torch.cuda, "mem_get_info", lambda d: (free, total)),
+                mock.patch.object(M.torch.cuda, "memory_reserved", lambda d: reserved),
+                mock.patch.object(M.torch.cuda, "memory_allocated", lambda d: allocated))
+
+    mgr.config = OffloadConfig(max_gpu_mem_fraction=0.5)
+    a, b, c = state(200 * GiB, 288 * GiB, 10 * GiB, 6 * GiB)
+    with a, b, c:
+        assert mgr._budget() == 144 * GiB  # fits: uncapped
+    a, b, c = state(100 * GiB, 288 * GiB, 10 * GiB, 6 * GiB)
+    with a, b, c, caplog.at_level("WARNING"):
+        assert mgr._budget() == (100 + 4 + 1) * GiB
+    assert "capping the GPU memory budget" in caplog.text
+    mgr.config = OffloadConfig(max_gpu_mem_bytes=8 * GiB)
+    with a, b, c:
+        assert mgr._budget() == 8 * GiB
+    mgr.config = OffloadConfig()
+    assert mgr._budget() is None
+    mgr.config = OffloadConfig(max_gpu_mem_fraction=0.9)
+    a, b, c = state(100 * 2**20, 288 * GiB, 0, 0)
+    with a, b, c, pytest.raises(RuntimeError, match="Insufficient free GPU memory"):
+        mgr._budget()
