@@ -98,6 +98,8 @@ class OffloadConfig(BaseModel):
             raise ValueError(f"transfer_mode must be one of {TRANSFER_MODES}, got {self.transfer_mode!r}")
         if self.shm_enabled and (self.shm_namespace is None or not self.shm_namespace.strip()):
             raise ValueError("shm_namespace must be non-empty when shm_enabled=True")
+        if self.num_blocks < self.min_blocks:
+            raise ValueError(f"num_blocks ({self.num_blocks}) must be >= min_blocks ({self.min_blocks})")
         if self.profile_mode == "torch_function":
             raise ValueError("profile_mode='torch_function' is only valid with transfer_mode='strategy', which this "
                              f"build does not provide; use 'view' or 'getter' with {self.transfer_mode!r}")

@@ -169,8 +169,16 @@ class _Unit:
 
 
 def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | None, base_bytes: int,
-                   num_blocks: int) -> StreamPlan:
-    """Choose streamed units and the slot plan under a GPU byte budget."""
+                   num_blocks: int, min_blocks: int | None = None) -> StreamPlan:
+    """Choose streamed units and the slot plan under a GPU byte budget.
+
+    The fewest units stream that fit, spread evenly over the pass. For that
+    choice the slot count is the largest in ``[min_blocks, num_blocks]`` whose
+    slots fit the budget (the deepest prefetch the memory allows; the
+    reference searches the same range, config.py:207-225). Slots beyond
+    ``num_blocks`` are added only while the reference's slot-reuse check
+    reports a hazard.
+    """
     by_label = {u.label: u for u in units}
     labels = list(order)
     sizes = [by_label[x].nbytes for x in labels]
@@ -179,6 +187,8 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
         return StreamPlan([], labels, None, {}, False, budget, total)
     n = len(labels)
     stats = [by_label[x].stats() for x in labels]
+    hi = max(num_blocks, 2)
+    lo = max(2, min(hi, min_blocks if min_blocks is not None else hi))
     for k in range(1, n + 1):
         pick = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
         if len(pick) < k:
@@ -186,23 +196,28 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
         streamed = [labels[i] for i in pick]
         if budget is None and k < n:
             continue
-        blocks = num_blocks
-        while True:
-            strategy = {}
-            for i in pick:
-                consumer = labels[i]
-                producer = labels[i - 1]  # i == 0 wraps to the last label: a cyclic preload
-                strategy[producer] = list(stats[i].tensors)
-            bd = prepare_block_strategy(strategy, stats, blocks)
-            if check_overlap_constraint(bd.transfer_to_compute_map, stats, bd.label_to_block_id):
-                break
-            blocks += 1
-            if blocks > n + 2:
-                raise RuntimeError("no hazard-free slot plan found")
+        # i == 0 wraps to the last label: a cyclic preload
+        strategy = {labels[i - 1]: list(stats[i].tensors) for i in pick}
         resident = [x for x in labels if x not in streamed]
-        gpu = base_bytes + sum(by_label[x].nbytes for x in resident) + sum(bd.block_sizes.values())
-        if budget is not None and gpu > budget:
+        placed = base_bytes + sum(by_label[x].nbytes for x in resident)
+        chosen = None
+        hazard_free = False
+        for blocks in [*range(hi, lo - 1, -1), *range(hi + 1, n + 3)]:
+            bd = prepare_block_strategy(strategy, stats, blocks)
+            if not check_overlap_constraint(bd.transfer_to_compute_map, stats, bd.label_to_block_id):
+                continue
+            hazard_free = True
+            gpu = placed + sum(bd.block_sizes.values())
+            if budget is None or gpu <= budget:
+                chosen = (bd, gpu)
+                break
+            if blocks > hi:
+                break  # extra slots only grow the footprint
+        if not hazard_free:
+            raise RuntimeError("no hazard-free slot plan found")
+        if chosen is None:
             continue
+        bd, gpu = chosen
         reordered = bool(resident)
         if reordered:
             t2c, l2b, remapped = rearrange_transfers(bd.transfer_to_compute_map, bd.label_to_block_id, stats)
@@ -1236,7 +1251,8 @@ class OffloadManager:
         if state is not None:
             self.plan = self._plan_from_state(state)
         else:
-            self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks)
+            self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks,
+                                       cfg.min_blocks)
         plan = self.plan
         resident_params = [p for x in plan.resident for p in self._unit(x).params]
         with _oom_context(resident_params, f"the {len(plan.resident)} offload units kept resident",

@@ -78,7 +78,7 @@ def test_file_then_env_then_kwargs(monkeypatch, tmp_path):
 
 @pytest.mark.parametrize("suffix", [".json", ".yaml"])
 def test_json_and_yaml_files(tmp_path, suffix):
-    data = {"enabled": "true", "num_blocks": 3, "include_patterns": ["blocks.*"], "not_a_field": 1,
+    data = {"enabled": "true", "num_blocks": 3, "min_blocks": 2, "include_patterns": ["blocks.*"], "not_a_field": 1,
             "max_gpu_mem_bytes": "1024"}
     path = tmp_path / f"ft{suffix}"
     if suffix == ".json":
@@ -88,7 +88,7 @@ def test_json_and_yaml_files(tmp_path, suffix):
 
         path.write_text(yaml.safe_dump(data))
     c = load_config_from_file(path)
-    assert c.enabled is True and c.num_blocks == 3 and c.include_patterns == ["blocks.*"]
+    assert c.enabled is True and c.num_blocks == 3 and c.min_blocks == 2 and c.include_patterns == ["blocks.*"]
     assert c.max_gpu_mem_bytes == 1024
 
 
@@ -141,8 +141,8 @@ def test_profiling_suspension_is_reference_counted():
 
 
 def test_init_and_set_config_before_offload():
-    ft.init(OffloadConfig(num_blocks=3), name="init-test")
-    assert ft.get_offload_manager("init-test").config.num_blocks == 3
+    ft.init(OffloadConfig(num_blocks=6), name="init-test")
+    assert ft.get_offload_manager("init-test").config.num_blocks == 6
     ft.set_config(OffloadConfig(num_blocks=5), name="init-test")
     assert ft.get_offload_manager("init-test").config.num_blocks == 5
     assert ft.offload_units("init-test") == () and ft.resident_units("init-test") == ()

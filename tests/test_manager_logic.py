@@ -101,3 +101,33 @@ def test_copy_policy_from_measured_curves():
     assert kmax == 1 << 20  # 2 MiB is only 2% faster on the kernel: not worth its cost to kernels beside it
     assert split_min == 2**63 - 1 and n_streams == 1  # splitting never helps
     assert choose_copy_policy(curves["sdma"], curves["kernel"], min_kernel_gain=1.0)[0] == 64 << 20
+
+
+def test_block_range_is_validated():
+    """config.py:468-472: num_blocks below min_blocks is refused."""
+    with pytest.raises(ValueError, match="must be >= min_blocks"):
+        OffloadConfig(num_blocks=2)  # min_blocks defaults to 4
+    assert OffloadConfig(num_blocks=2, min_blocks=2).num_blocks == 2
+
+
+def test_slot_count_is_the_largest_in_range_that_fits():
+    """Fewest streamed units first; then the deepest ring in [min_blocks, num_blocks] within the budget."""
+    units = _mk([1000] * 12)
+    order = [u.label for u in units]
+    roomy = plan_streaming(units, order, budget=10_500, base_bytes=0, num_blocks=4, min_blocks=2)
+    tight = plan_streaming(units, order, budget=10_500, base_bytes=0, num_blocks=2, min_blocks=2)
+    assert len(roomy.streamed) == len(tight.streamed)  # the slot count never costs a resident unit
+    assert len(roomy.block_data.block_sizes) >= len(tight.block_data.block_sizes)
+    assert roomy.planned_gpu_bytes <= 10_500 and tight.planned_gpu_bytes <= 10_500
+    fixed = plan_streaming(units, order, budget=10_500, base_bytes=0, num_blocks=4)  # min_blocks = num_blocks
+    # 8 resident units + 2 slots fit 10_500; with the range pinned at 4 slots only 6 units stay resident
+    assert (len(roomy.streamed), len(roomy.block_data.block_sizes)) == (4, 2)
+    assert (len(fixed.streamed), len(fixed.block_data.block_sizes)) == (6, 4)
+    # with equal units a slot costs what keeping one more unit resident costs, so slack keeps units resident
+    cheaper = plan_streaming(units, order, budget=11_000, base_bytes=0, num_blocks=4, min_blocks=2)
+    assert (len(cheaper.streamed), len(cheaper.block_data.block_sizes)) == (3, 2)
+    deeper = plan_streaming(units, order, budget=None, base_bytes=0, num_blocks=4, min_blocks=2)
+    assert len(deeper.streamed) == 12 and len(deeper.block_data.block_sizes) == 4  # no budget: the deepest ring
+    for p in (roomy, tight, fixed, cheaper, deeper):
+        stats = [LayerStatistics(x) for x in order]
+        assert check_overlap_constraint(p.block_data.transfer_to_compute_map, stats, p.block_data.label_to_block_id)
