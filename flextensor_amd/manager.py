@@ -351,6 +351,7 @@ class OffloadManager:
         self._load_from_shm = False
         self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
         self._from_state = False
+        self._reload_pending = False
         self._pinner: HostPinner | None = None
         self.memory_transfer_stats: dict[int, float] = {}
         self.skip_discovery_honored: bool | None = None  # None until offload() decides
@@ -496,6 +497,7 @@ class OffloadManager:
         self._forwards = 0
         self._resident_bytes = 0
         self._from_state = False
+        self._reload_pending = False
         self.skip_discovery_honored = None
         self.compile_fn = None
         self._load_from_shm = False
@@ -856,6 +858,7 @@ class OffloadManager:
         self._reset_manual()
         self._release_pins()
         self._from_state = False
+        self._reload_pending = False
         self.skip_discovery_honored = None
         self.loader = self.controller = self.plan = None
         self._pass_done = []
@@ -1118,6 +1121,8 @@ class OffloadManager:
 
     def _enter(self, label: str) -> None:
         if self.phase == OffloadPhase.INFERENCE:
+            if self._reload_pending and self.order and label == self.order[0]:
+                self._reload_if_pending()  # a load on a submodule, which the root's load hook did not see
             self.loader.enter(label)
             return
         if hip.is_capturing():
@@ -1278,6 +1283,7 @@ class OffloadManager:
                     "page-locked host memory.") from exc
             for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
                 tensors_map[tid].data = view
+            self._install_state_dict_hooks(tensors_map)
             reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"
             cls = PreallocatedBatchTransferTensorLoaderReordered if reordered else PreallocatedBatchTransferTensorLoader
             self.timing = OffloadTimingCollector(order, enabled=cfg.offload_timing != "off",
@@ -1298,6 +1304,69 @@ class OffloadManager:
                     len(plan.resident), self.build_seconds)
         if cfg.enable_diagnostics:
             LOGGER.info("offload %r plan:\n%s", self.name, self.plan_table())
+
+    def _install_state_dict_hooks(self, streamed: dict[int, torch.Tensor]) -> None:
+        """Serialize streamed parameters from their host blocks, and load into them.
+
+        While streaming, a streamed parameter views a ring slot that holds
+        whichever unit was loaded last, so ``state_dict()`` takes such a
+        parameter's bytes from its host block (the authoritative copy, viewed
+        without a copy, as a state dict views parameters). ``load_state_dict()``
+        writes them there too: for the load the parameter points at its host
+        block, so no slot is written (a slot write would also race the
+        transfers filling the ring). ``assign=True`` would replace the aliased
+        parameters and is refused; ``keep_vars=True`` keeps the live parameters.
+        """
+        assert self.model is not None and self.controller is not None
+        host: dict[int, torch.Tensor] = {}
+        for label in self.controller.block_map_cpu:
+            for tid, view in zip(self.controller.label_to_cpu_tensor_id_map[label], self._cpu_views(label)):
+                host[tid] = view
+        owners: dict[int, tuple[nn.Module, dict[str, nn.Parameter]]] = {}
+        for mod in self.model.modules():
+            for key, p in mod._parameters.items():
+                if p is not None and id(p) in host and id(p) in streamed:
+                    owners.setdefault(id(mod), (mod, {}))[1][key] = p
+        name, device, mgr = self.name, self.device, self
+        streamed_view = {tid: t.data for tid, t in streamed.items()}
+
+        for mod, local in owners.values():
+            def save_hook(module: nn.Module, state_dict: dict, prefix: str, _meta: Any,
+                          local: dict[str, nn.Parameter] = local) -> None:
+                for key, p in local.items():
+                    k = prefix + key
+                    if k in state_dict and not isinstance(state_dict[k], nn.Parameter):
+                        state_dict[k] = host[id(p)]
+
+            def before_load(module: nn.Module, *_args: Any, local: dict[str, nn.Parameter] = local,
+                            **_kwargs: Any) -> None:
+                torch.cuda.synchronize(device)  # no transfer may still be reading a host block
+                for p in local.values():
+                    p.data = host[id(p)]
+
+            def after_load(module: nn.Module, _incompatible: Any, local: dict[str, nn.Parameter] = local) -> None:
+                mgr._reload_pending = True
+                for key, p in local.items():
+                    p.data = streamed_view[id(p)]
+                    if module._parameters.get(key) is not p:
+                        raise RuntimeError(f"offload manager {name!r}: load_state_dict(assign=True) replaced the "
+                                           f"streamed parameter {key!r}; release() the model before assigning")
+
+            self._hooks.append(mod.register_state_dict_post_hook(save_hook))
+            self._hooks.append(mod._register_load_state_dict_pre_hook(before_load, with_module=True))
+            self._hooks.append(mod.register_load_state_dict_post_hook(after_load))
+        # The root's load hook runs after every submodule's: reload the next pass's first slots, which the
+        # previous pass already filled from the old bytes.
+        self._hooks.append(self.model.register_load_state_dict_post_hook(lambda *_: mgr._reload_if_pending()))
+
+    def _reload_if_pending(self) -> None:
+        """After new streamed bytes were loaded, refill the slots the previous pass preloaded."""
+        if not self._reload_pending or self.phase != OffloadPhase.INFERENCE or hip.is_capturing():
+            return
+        self._reload_pending = False
+        preload = getattr(self.loader, "preload", None)
+        if preload is not None:
+            preload()
 
     def _build_controller(self, cfg: OffloadConfig, plan: StreamPlan, bd: Any, tensors_map: dict[int, torch.Tensor],
                           pinner: HostPinner, mode: int, state: TensorManagerState | None) -> None:

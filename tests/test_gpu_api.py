@@ -161,3 +161,50 @@ def test_a_failing_unit_leaves_every_phase_usable(gpu):
         for _ in range(2):
             assert torch.equal(model(x), want)
     ft.release(name)
+
+
+def test_state_dict_and_load_state_dict_while_streaming(gpu):
+    """A streamed parameter views a ring slot that holds whichever unit came last; its state dict entry
+    comes from the host block, and loaded weights land there (and so in every later pass)."""
+    model = W.build_mlp_stack(6, 256, 704, seed=95)
+    original = {k: v.clone() for k, v in model.state_dict().items()}
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, max_gpu_mem_bytes=4 * layer)
+    name = "state-dict"
+    ft.offload(model, cfg, name=name)
+    mgr = ft.get_offload_manager(name)
+    x = W.mlp_input(8, 256, seed=95).to(gpu)
+    with torch.no_grad():
+        for _ in range(3):
+            model(x)
+    assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.streamed
+    streamed = {f"{u}.{n}" for u in mgr.plan.streamed for n in ("fc1.weight", "fc1.bias", "fc2.weight", "fc2.bias")}
+    sd = model.state_dict()
+    assert set(sd) == set(original)
+    for k, v in original.items():
+        assert torch.equal(sd[k].cpu(), v), k
+        assert (sd[k].device.type == "cpu") == (k in streamed), k  # streamed entries come from the host blocks
+    assert isinstance(model.state_dict(keep_vars=True)[next(iter(streamed))], torch.nn.Parameter)
+
+    other = W.build_mlp_stack(6, 256, 704, seed=96)
+    with torch.no_grad():
+        want = copy.deepcopy(other).to(gpu)(x)
+        model.load_state_dict(other.state_dict())
+        for _ in range(3):
+            assert torch.equal(model(x), want)  # every pass streams the loaded weights
+    for k, v in other.state_dict().items():
+        assert torch.equal(model.state_dict()[k].cpu(), v), k
+    # a load into one streamed unit alone: the next pass streams it too
+    unit = mgr.plan.streamed[0]
+    third = W.build_mlp_stack(6, 256, 704, seed=97)
+    mixed = copy.deepcopy(other)
+    mixed.get_submodule(unit).load_state_dict(third.get_submodule(unit).state_dict())
+    with torch.no_grad():
+        want = copy.deepcopy(mixed).to(gpu)(x)
+        model.get_submodule(unit).load_state_dict(third.get_submodule(unit).state_dict())
+        for _ in range(3):
+            assert torch.equal(model(x), want)
+    with pytest.raises(RuntimeError, match="assign=True"):
+        model.load_state_dict(other.state_dict(), assign=True)
+    ft.release(name)
