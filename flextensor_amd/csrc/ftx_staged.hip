@@ -2,16 +2,20 @@
 //
 // A pageable source (an ordinary allocation, or a POSIX shared-memory mapping
 // that cannot be page-locked in place) cannot be read by the SDMA engines
-// directly. The staged engine copies it in pieces through two page-locked
+// directly. The staged engine copies it in pieces through three page-locked
 // staging buffers per device:
 //
-//   for piece j:  wait until buffer j%2's previous DMA has finished (host wait
+//   for piece j:  wait until buffer j%3's previous DMA has finished (host wait
 //                 on its event), copy the piece into it with the host thread
 //                 pool, enqueue hipMemcpyAsync(buffer -> device) on the caller's
 //                 stream and record the buffer's event after it.
 //
-// The host copy of piece j+1 runs while the SDMA engine moves piece j, so a
-// copy runs at about the slower of the two rates. The call returns once the
+// The host copy of piece j+1 runs while the SDMA engine moves the pieces
+// before it; with three buffers two DMAs stay queued while the host fills the
+// third, so jitter in the host copy (which shares host memory bandwidth with
+// the DMA) does not idle the link. Pieces ramp from a sixteenth of the policy
+// size up to the full size so the first DMA starts early. A copy runs at
+// about the slower of the two rates. The call returns once the
 // last piece is enqueued; the DMA itself stays stream-ordered. The host work
 // happens at call time, so a staged copy cannot be captured into a graph
 // (the entry point rejects capturing streams).
@@ -123,14 +127,16 @@ class HostCopyPool {
   bool stop_ = false;
 };
 
+constexpr int kStagingBuffers = 3;  // two DMAs stay queued while the host fills the third
+
 struct StagingState {
-  void *buf[2] = {nullptr, nullptr};
-  hipEvent_t done[2] = {nullptr, nullptr};
+  void *buf[kStagingBuffers] = {};
+  hipEvent_t done[kStagingBuffers] = {};
   size_t bytes = 0;  // per buffer
 };
 
 std::mutex g_stage_mutex;  // guards the policy and the staging buffers
-size_t g_piece_bytes = size_t(32) << 20;
+size_t g_piece_bytes = size_t(64) << 20;
 int g_threads = 0;  // 0: chosen from the host's core count
 StagingState g_stage[kMaxDevices];
 
@@ -151,13 +157,13 @@ int staging(size_t bytes, StagingState **out) {
   if (dev < 0 || dev >= kMaxDevices) return fail(FTX_ERR_UNSUPPORTED, "device index out of range");
   StagingState &st = g_stage[dev];
   if (st.bytes != bytes) {
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < kStagingBuffers; ++b) {
       if (st.done[b]) FTX_HIP(hipEventSynchronize(st.done[b]));
       if (st.buf[b]) FTX_HIP(hipHostFree(st.buf[b]));
       st.buf[b] = nullptr;
     }
     st.bytes = 0;
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < kStagingBuffers; ++b) {
       hipError_t err = hipHostMalloc(&st.buf[b], bytes, hipHostMallocDefault);
       if (err != hipSuccess) {
         (void)hipGetLastError();
@@ -212,15 +218,20 @@ int staged_copy_h2d(void *dst, const void *src, size_t nbytes, hipStream_t strea
   if (rc != FTX_OK) return rc;
   uint8_t *d = static_cast<uint8_t *>(dst);
   const uint8_t *s = static_cast<const uint8_t *>(src);
+  // The first piece's host copy has no DMA to overlap with, so pieces start
+  // small (a sixteenth of the policy's piece, at least 1 MiB) and double up to
+  // the full piece: the link starts early and the pipeline fills at once.
+  size_t piece = std::min(st->bytes, std::max(kMinPartBytes, st->bytes / 16));
   size_t off = 0;
   for (int j = 0; off < nbytes; ++j) {
-    const int b = j & 1;
-    const size_t len = std::min(st->bytes, nbytes - off);
+    const int b = j % kStagingBuffers;
+    const size_t len = std::min(piece, nbytes - off);
     FTX_HIP(hipEventSynchronize(st->done[b]));  // the buffer's previous DMA has read it
     pool().copy(st->buf[b], s + off, len, threads);
     FTX_HIP(hipMemcpyAsync(d + off, st->buf[b], len, hipMemcpyHostToDevice, stream));
     FTX_HIP(hipEventRecord(st->done[b], stream));
     off += len;
+    piece = std::min(st->bytes, piece * 2);
   }
   return FTX_OK;
 }

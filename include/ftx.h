@@ -145,9 +145,9 @@ int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *
  * not page-locked (pinned_memory=False blocks, allocation_block.py:104-106 with
  * an unpinned source; FlexibleSharedMemory blocks without in-place
  * registration, shm/flexible_shm.py:832-848): FTX_COPY_STAGED copies the
- * source in pieces of `piece_bytes` into two page-locked staging buffers per
- * device with `n_threads` host threads, each piece then crossing the link by
- * SDMA while the next one is copied. The call returns once the last piece is
+ * source in pieces (ramping up to `piece_bytes`, 64 MiB by default) into
+ * three page-locked staging buffers per device with `n_threads` host threads,
+ * each piece then crossing the link by SDMA while the next one is copied. The call returns once the last piece is
  * enqueued; the source may be reused then. Staged copies are refused on a
  * capturing stream. ftx_host_memcpy is the same thread pool's parallel host
  * copy (no overlap allowed). n_threads 0 = half the host's cores, at most 8. */
