@@ -100,3 +100,68 @@ def test_compiling_before_inference_is_refused():
     with pytest.raises(Exception, match="profiling"):
         torch.compile(model, backend="eager", fullgraph=True)(W.mlp_input(2, 16, seed=3))
     custom_ops.unregister_manager(id(mgr))
+
+
+class _Recorder:
+    def __init__(self) -> None:
+        self.calls: list[tuple[str, str]] = []
+
+    def _enter(self, label: str) -> None:
+        self.calls.append(("enter", label))
+
+    def _exit(self, label: str) -> None:
+        self.calls.append(("exit", label))
+
+
+def test_opcheck_accepts_the_compute_boundary_ops():
+    """tests/unit/test_custom_ops.py:214-230: schema, autograd, fake and AOT dispatch checks."""
+    for op in (torch.ops.flextensor.pre_compute.default, torch.ops.flextensor.post_compute.default):
+        result = torch.library.opcheck(op, (torch.zeros(3), "unit", 987654321))
+        assert set(result.values()) == {"SUCCESS"}, result
+
+
+def test_fake_tensors_never_reach_the_manager():
+    """tests/unit/test_custom_ops.py:54-96: tracing with fake tensors must not enter or exit units."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from flextensor_amd import custom_ops as C
+
+    rec = _Recorder()
+    C.register_manager(4242, rec)
+    try:
+        with FakeTensorMode() as mode:
+            fake = mode.from_tensor(torch.zeros(2))
+            torch.ops.flextensor.pre_compute(fake, "u", 4242)
+            torch.ops.flextensor.post_compute(fake, "u", 4242)
+        assert rec.calls == []
+        carrier = torch.arange(4.0)
+        torch.ops.flextensor.pre_compute(carrier, "u", 4242)
+        torch.ops.flextensor.post_compute(carrier, "u", 4242)
+        assert rec.calls == [("enter", "u"), ("exit", "u")]
+        assert torch.equal(carrier, torch.arange(4.0))  # declared mutated, never written
+    finally:
+        C.unregister_manager(4242)
+
+
+def test_managers_dispatch_independently():
+    """tests/unit/test_custom_ops.py:151-200: each manager id reaches its own manager; releasing one leaves
+    the other working."""
+    from flextensor_amd import custom_ops as C
+
+    a, b = _Recorder(), _Recorder()
+    C.register_manager(1001, a)
+    C.register_manager(1002, b)
+    try:
+        torch.ops.flextensor.pre_compute(torch.zeros(1), "x", 1001)
+        torch.ops.flextensor.pre_compute(torch.zeros(1), "y", 1002)
+        C.unregister_manager(1001)
+        torch.ops.flextensor.post_compute(torch.zeros(1), "y", 1002)
+        with pytest.raises(RuntimeError, match="released"):
+            torch.ops.flextensor.post_compute(torch.zeros(1), "x", 1001)
+        assert a.calls == [("enter", "x")] and b.calls == [("enter", "y"), ("exit", "y")]
+        C.register_manager(1001, b)  # a new registration under the id replaces the old one
+        torch.ops.flextensor.pre_compute(torch.zeros(1), "z", 1001)
+        assert b.calls[-1] == ("enter", "z")
+    finally:
+        C.unregister_manager(1001)
+        C.unregister_manager(1002)
