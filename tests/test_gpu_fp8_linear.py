@@ -87,7 +87,8 @@ def test_workspace_size_follows_the_split(gpu, default_config):
     hip.set_fp8_linear_config(0, 1024)
     assert hip.fp8_linear_workspace_bytes(8, 1000, 4096) == 4 * 8 * 1000 * 4
     hip.set_fp8_linear_config(0, 0)
-    assert hip.fp8_linear_workspace_bytes(8, 1000, 1024) == 0  # one slice of four iterations
+    assert hip.fp8_linear_workspace_bytes(8, 1000, 1024) == 2 * 8 * 1000 * 4  # narrow: slices of two iterations
+    assert hip.fp8_linear_workspace_bytes(8, 65536, 1024) == 0  # wide: one slice of four iterations
     hip.set_fp8_linear_config(0, 256)
     assert hip.fp8_linear_workspace_bytes(8, 1000, 512) == 2 * 8 * 1000 * 4
     # the activation slice and eight 16-row weight tiles share 64 KiB of LDS:
