@@ -83,13 +83,19 @@ class ShmCreatorFailedError(ShmCoordinatorError):
 
 
 class ShmCreatorDiedError(ShmCoordinatorError):
-    """Raised in followers when the initializing creator's heartbeat expired."""
+    """Raised in followers when the creator's heartbeat expired (while initializing, or after it was ready)."""
 
-    def __init__(self, namespace: str, creator_identity: int | None) -> None:
+    def __init__(self, namespace: str, creator_identity: int | None, *, after_ready: bool = False) -> None:
         self.namespace = namespace
         self.creator_identity = creator_identity
+        self.after_ready = after_ready
         detail = "unknown" if creator_identity is None else str(creator_identity)
-        super().__init__(f"Creator participant {detail} died while initializing shared namespace '{namespace}'")
+        if after_ready:
+            super().__init__(f"Creator participant {detail} of shared namespace '{namespace}' has exited; its "
+                             "segments are left from a finished run. Remove them with "
+                             "SharedOffloadSession.cleanup_namespace before reusing the namespace")
+        else:
+            super().__init__(f"Creator participant {detail} died while initializing shared namespace '{namespace}'")
 
 
 def control_segment_name(namespace: str) -> str:
@@ -191,24 +197,31 @@ class ShmCoordinator:
         return self._header()[0]
 
     def is_creator_alive(self) -> bool:
-        state, _, _, beat = self._header()
-        return state == READY or time.time() - beat <= self.keep_alive_seconds
+        """Whether the creator's heartbeat is fresh (it beats from creation until the creator closes)."""
+        return time.time() - self._header()[3] <= self.keep_alive_seconds
 
     def wait_for_ready(self, timeout: float | None = None, poll: float = 0.02) -> None:
-        """Return once the creator is ready; raise when it failed, died or ``timeout`` passed."""
+        """Return once the creator is ready; raise when it failed, died or ``timeout`` passed.
+
+        A ready namespace whose creator no longer beats is refused too: its
+        segments are what a finished (or killed) run left behind, and a new
+        run that joined them would read that run's weights
+        (the reference refuses a generation with no live participant,
+        shm/coordinator.py:75-360).
+        """
         deadline = None if not timeout else time.monotonic() + timeout
         stale = 0
         while True:
             state, msg_len, pid, beat = self._header()
-            if state == READY:
-                return
             if state == FAILED:
                 msg = bytes(self._control.buf[_MESSAGE_OFFSET:_MESSAGE_OFFSET + msg_len]).decode("utf-8", "replace")
                 raise ShmCreatorFailedError(self.namespace, msg)
             # a stale heartbeat must be seen on two polls in a row (a read racing a write is not proof)
             stale = stale + 1 if time.time() - beat > self.keep_alive_seconds else 0
+            if state == READY and stale == 0:
+                return
             if stale >= 2:
-                raise ShmCreatorDiedError(self.namespace, pid)
+                raise ShmCreatorDiedError(self.namespace, pid, after_ready=state == READY)
             if deadline is not None and time.monotonic() > deadline:
                 raise TimeoutError(f"timed out after {timeout} s waiting for the creator of namespace "
                                    f"'{self.namespace}'")

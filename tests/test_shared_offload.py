@@ -324,3 +324,63 @@ def test_cleanup_namespace_refuses_a_live_creator():
         SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=0.1)
     live.close()
     assert _leftovers(ns) == []
+
+
+def _creator_until_killed(ns, ready, started):
+    c = ShmCoordinator(ns, heartbeat_interval=0.05)
+    if ready:
+        c.notify_ready()
+    started.set()
+    time.sleep(600)  # the test kills this process long before
+
+
+@pytest.mark.parametrize("ready", [False, True])
+def test_killed_creator_is_detected_and_its_namespace_reclaimed(ready):
+    """A creator killed by SIGKILL (no rollback, names left behind) is detected by its expired heartbeat,
+    both while initializing and after it was ready; new joiners are refused until cleanup removes the
+    names, after which the next coordinator is a fresh creator (tests/unit/shm/test_coordinator.py:198-224,
+    tests/unit/shm/test_cleanup.py:231-256)."""
+    import signal
+
+    base = _ns()
+    ns = SharedOffloadSession(base).namespace_for("default")
+    ctx = mp.get_context("spawn")
+    started = ctx.Event()
+    proc = ctx.Process(target=_creator_until_killed, args=(ns, ready, started))
+    proc.start()
+    try:
+        assert started.wait(120), proc.exitcode
+        follower = ShmCoordinator(ns, keep_alive_seconds=0.3)
+        assert not follower.is_creator and follower.is_creator_alive()
+        if ready:
+            follower.wait_for_ready(timeout=5.0)  # live creator: ready at once
+        with pytest.raises(ShmCoordinatorError, match="live creator"):
+            SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=0.2,
+                                                   keep_alive_seconds=0.3)
+        proc.kill()
+        proc.join(30)
+        assert proc.exitcode == -signal.SIGKILL
+        time.sleep(0.4)  # past the keep-alive: within it a joiner cannot tell a dead creator from a live one
+        with pytest.raises(ShmCreatorDiedError) as err:
+            follower.wait_for_ready(timeout=10.0)
+        assert err.value.creator_identity == proc.pid and err.value.after_ready is ready
+        assert not follower.is_creator_alive()
+        follower.close()
+        assert _leftovers(ns)  # SIGKILL skips the creator's own removal
+        for _ in range(2):  # joiners are refused, and joining does not revive the namespace
+            joiner = ShmCoordinator(ns, keep_alive_seconds=0.3)
+            assert not joiner.is_creator
+            with pytest.raises(ShmCreatorDiedError):
+                joiner.wait_for_ready(timeout=10.0)
+            joiner.close()
+        SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=5.0, keep_alive_seconds=0.3)
+        assert _leftovers(ns) == []
+        fresh = ShmCoordinator(ns)
+        assert fresh.is_creator
+        fresh.close()
+        assert _leftovers(ns) == []
+    finally:
+        if proc.is_alive():
+            proc.kill()
+            proc.join(30)
+        SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=0.0, keep_alive_seconds=1e-3)
