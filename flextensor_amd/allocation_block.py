@@ -234,14 +234,16 @@ class AllocationBlock:
         self.views = []
         self.slots = []
         self.tensors = []
-        seg, self.shm_segment = self.shm_segment, None
+        seg = self.shm_segment
         if seg is not None:
             # The creator removes the name; other processes' mappings stay valid. The
             # mapping itself is not closed here: tensors (restored parameters, user
             # references) may still view it, and it is unmapped with the last of them.
             # An in-place pin of the mapping ends with the pinner's release_all(), like
             # every other pin (pins are released at manager shutdown, not with blocks).
+            # A failed unlink keeps the segment, so release() can be retried.
             seg.unlink()
+        self.shm_segment = None
 
 
 def _current(device: torch.device):

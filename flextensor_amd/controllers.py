@@ -32,6 +32,32 @@ from .planner import TensorStatistics
 LOGGER = logging.getLogger(__name__)
 
 
+CLEANUP_NOTE = ("construction cleanup is incomplete; call exception._flextensor_cleanup_controller.shutdown() "
+                "to retry it.")
+
+
+def _cleanup_keeping_error(controller: Any, primary: BaseException) -> None:
+    """Undo a failed build; a failing cleanup never replaces ``primary``.
+
+    The controller stays reachable from the primary error as
+    ``_flextensor_cleanup_controller`` (and the cleanup's own error as
+    ``_flextensor_cleanup_error``) so the caller can retry ``shutdown()``
+    (loaders.py:1269-1286).
+    """
+    try:
+        controller.shutdown()
+    except BaseException as cleanup_error:
+        LOGGER.warning("cleanup of a failed block build is incomplete", exc_info=True)
+        try:
+            primary.__dict__["_flextensor_cleanup_controller"] = controller
+            primary.__dict__["_flextensor_cleanup_error"] = cleanup_error
+            add_note = getattr(primary, "add_note", None)
+            if callable(add_note):
+                add_note(CLEANUP_NOTE)
+        except BaseException:
+            LOGGER.exception("could not attach the retryable cleanup handle to the primary error")
+
+
 class _Rollback:
     """Remembers packed-and-released sources so a failed build can restore them."""
 
@@ -131,10 +157,9 @@ class AllocationBlockController:
                 self.block_map_gpu[label_to_block_id[label]] = prefix
                 self.gpu_block_view_map[label] = prefix
             self.prepare_tensor_id_to_view_mapping()
-        except BaseException:
-            self._rollback.restore()
-            self._release_shm_blocks()  # segments this build created must not outlive it
-            self._clear()
+        except BaseException as primary:
+            # sources restored, segments this build created removed, maps cleared
+            _cleanup_keeping_error(self, primary)
             raise
 
     def prepare_tensor_id_to_view_mapping(self) -> None:
@@ -161,7 +186,10 @@ class AllocationBlockController:
         self._rollback.commit()
 
     def abort_construction(self, primary_error: BaseException | None = None) -> None:
-        self.shutdown()
+        if primary_error is None:
+            self.shutdown()
+        else:
+            _cleanup_keeping_error(self, primary_error)
 
     def _clear(self) -> None:
         for d in (self.block_map_cpu, self.label_to_cpu_tensor_id_map, self.label_to_gpu_block, self.block_map_gpu,
@@ -170,9 +198,16 @@ class AllocationBlockController:
         self._gpu_slots = []
 
     def _release_shm_blocks(self) -> None:
+        """Release every segment-backed block; raise the first failure after trying them all (retryable)."""
+        first: BaseException | None = None
         for block in self.block_map_cpu.values():
             if block.shm_segment is not None:
-                block.release()  # the creator removes the segment's name; the mapping goes with its last view
+                try:
+                    block.release()  # the creator removes the segment's name; the mapping goes with its last view
+                except BaseException as error:
+                    first = first or error
+        if first is not None:
+            raise first
 
     def shutdown(self) -> None:
         self._rollback.restore()
@@ -238,9 +273,8 @@ class RawBlockController:
                 if label in self.block_map_cpu
             }
             self.prepare_tensor_id_to_view_mapping()
-        except BaseException:
-            self._rollback.restore()
-            self.shutdown()
+        except BaseException as primary:
+            _cleanup_keeping_error(self, primary)
             raise
 
     def combine_tensors(self, tensors: Sequence[torch.Tensor], combined: torch.Tensor) -> list:
@@ -298,7 +332,10 @@ class RawBlockController:
         self._rollback.commit()
 
     def abort_construction(self, primary_error: BaseException | None = None) -> None:
-        self.shutdown()
+        if primary_error is None:
+            self.shutdown()
+        else:
+            _cleanup_keeping_error(self, primary_error)
 
     def shutdown(self) -> None:
         self._rollback.restore()

@@ -1276,11 +1276,15 @@ class OffloadManager:
             except (torch.cuda.OutOfMemoryError, nat.FtxOutOfMemoryError) as exc:
                 host = sum(bd.label_to_size_map.values())
                 slots = sum(bd.block_sizes.values())
-                raise torch.cuda.OutOfMemoryError(
+                oom = torch.cuda.OutOfMemoryError(
                     f"out of memory while building the streaming blocks: {len(bd.label_to_size_map)} page-locked "
                     f"host blocks ({host / 2**30:.2f} GiB) and {len(bd.block_sizes)} GPU ring slots "
                     f"({slots / 2**30:.2f} GiB). The slots take GPU memory within the budget; the blocks take "
-                    "page-locked host memory.") from exc
+                    "page-locked host memory.")
+                for key in ("_flextensor_cleanup_controller", "_flextensor_cleanup_error"):
+                    if key in exc.__dict__:  # a retryable cleanup handle stays on the error the caller sees
+                        oom.__dict__[key] = exc.__dict__[key]
+                raise oom from exc
             for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
                 tensors_map[tid].data = view
             self._install_state_dict_hooks(tensors_map)

@@ -250,3 +250,41 @@ def test_shared_memory_block_release_keeps_its_pin(recorded_pins):
     assert recorded_pins["unregister"] == [] and torch.equal(views[0], torch.arange(100, dtype=torch.int32))
     pinner.release_all()
     assert len(recorded_pins["unregister"]) == 1
+
+
+@pytest.mark.parametrize("raw", [False, True])
+def test_failed_cleanup_keeps_the_primary_error_and_a_retry_handle(monkeypatch, raw):
+    """loaders.py:1269-1286: a cleanup that fails never replaces the build's own error; the controller stays
+    reachable from it so shutdown() can be retried, and the retry restores the released sources."""
+    import flextensor_amd.controllers as C
+
+    tensors = {1: torch.arange(64, dtype=torch.uint8), 2: torch.arange(16, dtype=torch.float32)}
+    want = {k: v.clone() for k, v in tensors.items()}
+    calls = []
+    real_restore = C._Rollback.restore
+
+    def flaky_restore(self):
+        calls.append(1)
+        if len(calls) == 1:
+            raise RuntimeError("restore interrupted")
+        real_restore(self)
+
+    monkeypatch.setattr(C._Rollback, "restore", flaky_restore)
+    with pytest.raises(nat.FtxOutOfMemoryError) as caught:
+        if raw:
+            RawBlockController({"a": 64, "b": 64}, {0: 64}, torch.device("cpu"), tensors,
+                               {"a": _stats(1, 64), "b": _stats(2, 64)}, {"a": 0, "b": 0},
+                               host_pinner=_FailingPinner(fail_at=2))
+        else:
+            AllocationBlockController({0: ["a"], 1: ["b"]}, torch.device("cpu"), tensors,
+                                      {"a": _stats(1, 64), "b": _stats(2, 64)}, {"a": 0, "b": 1},
+                                      host_pinner=_FailingPinner(fail_at=2))
+    err = caught.value
+    assert "hipHostMalloc failed" in str(err)  # the primary error, not the cleanup's
+    ctrl = err.__dict__["_flextensor_cleanup_controller"]
+    assert str(err.__dict__["_flextensor_cleanup_error"]) == "restore interrupted"
+    assert tensors[1].numel() == 0  # "a" was packed and released before "b" failed; not yet restored
+    ctrl.shutdown()
+    for k in tensors:
+        assert torch.equal(tensors[k], want[k])
+    assert ctrl.block_map_cpu == {}
