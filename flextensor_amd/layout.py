@@ -90,6 +90,49 @@ def raw_storage_bytes(t: torch.Tensor) -> torch.Tensor:
     return raw
 
 
+def storage_byte_span(t: torch.Tensor) -> tuple[int, int]:
+    """``[lo, hi)``: the bytes of its storage that ``t`` can touch (any strides, including negative)."""
+    es = t.element_size()
+    lowest = t.storage_offset() + sum((k - 1) * s for k, s in zip(t.shape, t.stride()) if s < 0)
+    extent = 1 + sum((k - 1) * abs(s) for k, s in zip(t.shape, t.stride()))
+    return lowest * es, (lowest + extent) * es
+
+
+def overlapping_views(managed: Iterable[torch.Tensor], others: Iterable[torch.Tensor] = ()) -> list[list[int]]:
+    """Groups of distinct tensors (by ``id``) whose byte ranges overlap within one storage, each group
+    holding at least one ``managed`` tensor. Disjoint views of one storage are not reported."""
+    groups: dict[tuple[str, int], list[tuple[int, int, int, bool]]] = {}
+    seen: set[int] = set()
+    for flag, ts in ((True, managed), (False, others)):
+        for t in ts:
+            if id(t) in seen or t.is_meta or t.layout != torch.strided or t.numel() == 0:
+                continue
+            seen.add(id(t))
+            st = t.untyped_storage()
+            if st.nbytes() == 0:
+                continue
+            lo, hi = storage_byte_span(t)
+            groups.setdefault((str(t.device), st.data_ptr()), []).append((lo, hi, id(t), flag))
+    out: list[list[int]] = []
+
+    def flush(cluster: list[tuple[int, int, int, bool]]) -> None:
+        if len(cluster) > 1 and any(c[3] for c in cluster):
+            out.append(sorted(c[2] for c in cluster))
+
+    for spans in groups.values():
+        spans.sort()
+        cluster, end = [spans[0]], spans[0][1]
+        for span in spans[1:]:
+            if span[0] < end:  # starts inside the cluster's reach: overlaps one of its members
+                cluster.append(span)
+                end = max(end, span[1])
+            else:
+                flush(cluster)
+                cluster, end = [span], span[1]
+        flush(cluster)
+    return out
+
+
 @dataclass(frozen=True)
 class TensorSlot:
     """Placement of one tensor inside a packed block."""

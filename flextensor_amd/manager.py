@@ -55,6 +55,7 @@ from . import custom_ops, hip
 from .allocation_block import HostPinner
 from .config import OffloadConfig
 from .controllers import AllocationBlockController, RawBlockController
+from .layout import overlapping_views
 from .loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
 from .planner import (
     BlockStrategyData,
@@ -1259,6 +1260,7 @@ class OffloadManager:
             self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks,
                                        cfg.min_blocks)
         plan = self.plan
+        self._validate_source_storage(plan)
         resident_params = [p for x in plan.resident for p in self._unit(x).params]
         with _oom_context(resident_params, f"the {len(plan.resident)} offload units kept resident",
                           "Lower the budget (max_gpu_mem_fraction / max_gpu_mem_bytes) so that more units stream."):
@@ -1308,6 +1310,30 @@ class OffloadManager:
                     len(plan.resident), self.build_seconds)
         if cfg.enable_diagnostics:
             LOGGER.info("offload %r plan:\n%s", self.name, self.plan_table())
+
+    def _validate_source_storage(self, plan: StreamPlan) -> None:
+        """Refuse streamed tensors that overlap another distinct tensor's bytes, before anything moves.
+
+        Each tensor is packed into its block on its own, so two views of the
+        same bytes would stop aliasing once streamed (loaders.py:1217-1243).
+        Disjoint views of one storage (parameters that view a released host
+        block) are fine.
+        """
+        managed = [p for x in plan.streamed for p in self._unit(x).params]
+        if not managed or self.model is None:
+            return
+        others = [t for _, t in self.model.named_parameters(remove_duplicate=False)]
+        others += [t for _, t in self.model.named_buffers(remove_duplicate=False) if t is not None]
+        groups = overlapping_views(managed, others)
+        if groups:
+            names: dict[int, str] = {}
+            for n, t in list(self.model.named_parameters(remove_duplicate=False)) + list(
+                    self.model.named_buffers(remove_duplicate=False)):
+                names.setdefault(id(t), n)
+            shown = [sorted(names.get(i, f"tensor id {i}") for i in g) for g in groups]
+            raise ValueError("Block loaders cannot preserve distinct tensor views sharing storage with overlapping "
+                             f"byte regions ({shown}); give them separate storage (clone one) or keep their "
+                             "modules out of the offload units")
 
     def _install_state_dict_hooks(self, streamed: dict[int, torch.Tensor]) -> None:
         """Serialize streamed parameters from their host blocks, and load into them.

@@ -208,3 +208,29 @@ def test_state_dict_and_load_state_dict_while_streaming(gpu):
     with pytest.raises(RuntimeError, match="assign=True"):
         model.load_state_dict(other.state_dict(), assign=True)
     ft.release(name)
+
+
+def test_overlapping_parameter_views_are_refused_at_the_plan(gpu):
+    """loaders.py:1217-1243: a streamed parameter that overlaps another parameter's bytes is refused when
+    streaming would start, before any tensor moves; the model keeps its aliasing and can be released."""
+    model = W.build_mlp_stack(4, 256, 704, seed=97)
+    first_w = next(p for p in model.layers[0].parameters() if p.dim() == 2)
+    owner_name, bias = next((n, p) for n, p in model.layers[1].named_parameters() if p.dim() == 1)
+    owner = model.layers[1].get_submodule(owner_name.rpartition(".")[0]) if "." in owner_name else model.layers[1]
+    shared = torch.nn.Parameter(first_w.data.view(-1)[: bias.numel()])
+    setattr(owner, owner_name.rpartition(".")[2], shared)
+    want = [p.detach().clone() for p in model.parameters()]
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, max_gpu_mem_bytes=3 * layer)
+    name = "overlap-refused"
+    ft.offload(model, cfg, name=name)
+    x = W.mlp_input(16, 256, seed=97).to(gpu)
+    with torch.no_grad(), pytest.raises(ValueError, match="overlapping byte regions"):
+        for _ in range(4):
+            model(x)
+    assert ft.get_offload_manager(name).phase == OffloadPhase.PROFILING
+    ft.release(name)
+    for p, w in zip(model.parameters(), want):
+        assert p.device.type == "cpu" and torch.equal(p.detach(), w)
+    assert shared.untyped_storage().data_ptr() == first_w.untyped_storage().data_ptr()

@@ -278,3 +278,36 @@ def test_budget_is_capped_by_available_memory(caplog):
     a, b, c = state(100 * 2**20, 288 * GiB, 0, 0)
     with a, b, c, pytest.raises(RuntimeError, match="Insufficient free GPU memory"):
         mgr._budget()
+
+
+def test_overlapping_views_are_refused_before_anything_moves():
+    """loaders.py:1217-1243: distinct tensors viewing overlapping bytes of one storage cannot be packed
+    into blocks (they would stop aliasing); disjoint views of one storage are accepted."""
+    from flextensor_amd.layout import overlapping_views
+
+    model = torch.nn.Sequential(torch.nn.Linear(8, 8), torch.nn.Linear(8, 8), torch.nn.Linear(8, 8))
+    mgr = M.OffloadManager("overlap-check")
+    mgr.model = model
+
+    def units():
+        return [M._Unit(str(i), model[i], list(model[i].parameters()), [f"{i}.weight", f"{i}.bias"])
+                for i in range(3)]
+
+    plan = M.StreamPlan(["0", "1"], ["2"], None, {}, False, None, 0)
+    mgr.units = units()
+    mgr._validate_source_storage(plan)  # separate storages
+
+    backing = torch.zeros(8 * 8 + 8)
+    model[0].weight = torch.nn.Parameter(backing[:64].view(8, 8))
+    model[0].bias = torch.nn.Parameter(backing[64:])  # disjoint view of the same storage: fine
+    mgr.units = units()
+    mgr._validate_source_storage(plan)
+    assert overlapping_views([model[0].weight], [model[0].bias]) == []
+
+    model[2].bias = torch.nn.Parameter(backing[60:68])  # resident, but overlaps a streamed weight and bias
+    mgr.units = units()
+    with pytest.raises(ValueError, match=r"overlapping byte regions \(\[\['0.bias', '0.weight', '2.bias'\]\]\)"):
+        mgr._validate_source_storage(plan)
+    resident_only = M.StreamPlan(["1"], ["0", "2"], None, {}, False, None, 0)
+    mgr._validate_source_storage(resident_only)  # no streamed tensor is involved
+    M._MANAGERS.pop("overlap-check", None)
