@@ -231,7 +231,14 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
                 transfer_to_compute_map=t2c,
             )
         return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
-    raise ValueError(f"GPU budget of {budget} bytes cannot hold the ring slots plus {base_bytes} resident bytes")
+    # Even streaming every unit does not fit: the tensors placed outside the
+    # units leave too little for the ring (gpu_budget.py:200-225).
+    raise RuntimeError(
+        "Insufficient GPU budget after reserving the tensors kept on the GPU outside the offload units: "
+        f"budget={budget} bytes, reserved_outside_units={base_bytes} bytes, "
+        f"effective_budget={max(0, (budget or 0) - base_bytes)} bytes, "
+        f"minimum_ring={2 * max(sizes)} bytes (two slots of the largest unit). Raise max_gpu_mem_bytes / "
+        "max_gpu_mem_fraction or include the large outside tensors' modules in the offload units.")
 
 
 def state_from_plan(model: nn.Module, units: Sequence[_Unit], plan: StreamPlan, durations: dict[str, float],

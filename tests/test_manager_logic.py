@@ -80,7 +80,7 @@ def test_plan_everything_resident_when_it_fits():
 
 def test_plan_rejects_impossible_budget():
     units = _mk([1000] * 4)
-    with pytest.raises(ValueError, match="budget"):
+    with pytest.raises(RuntimeError, match="Insufficient GPU budget"):
         plan_streaming(units, [u.label for u in units], budget=1500, base_bytes=0, num_blocks=2)
 
 
@@ -131,3 +131,15 @@ def test_slot_count_is_the_largest_in_range_that_fits():
     for p in (roomy, tight, fixed, cheaper, deeper):
         stats = [LayerStatistics(x) for x in order]
         assert check_overlap_constraint(p.block_data.transfer_to_compute_map, stats, p.block_data.label_to_block_id)
+
+
+def test_plan_budget_exhausted_by_outside_tensors_names_the_reservation():
+    """gpu_budget.py:200-225: when the tensors kept on the GPU outside the units leave no room for the
+    ring, planning fails with a RuntimeError that states the budget, the reservation and the minimum."""
+    units = _mk([1000] * 6)
+    order = [u.label for u in units]
+    plan = plan_streaming(units, order, budget=2000 + 500, base_bytes=500, num_blocks=2)  # just fits
+    assert plan.streamed == order
+    with pytest.raises(RuntimeError, match=r"budget=2499 bytes, reserved_outside_units=500 bytes, "
+                                           r"effective_budget=1999 bytes, minimum_ring=2000 bytes"):
+        plan_streaming(units, order, budget=2499, base_bytes=500, num_blocks=2)
