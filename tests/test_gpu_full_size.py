@@ -2,11 +2,11 @@
 
 2000 bf16 tensors with byte sizes log-uniform in [4 KiB, 64 MiB] (seed 1),
 13.9 GB in all, are packed into 512 MiB pinned chunks, streamed into a
-two-slot device ring and placed by the scatter kernel. The oracle's
-checksum cannot be afforded as a byte-for-byte comparison at this size, so
-the test compares a size-independent property instead: the device checksum
-of every destination tensor against the oracle's checksum of its source,
-plus the shape and strides each destination keeps.
+two-slot device ring and placed by the scatter kernel. A byte-for-byte
+comparison would copy all 13.9 GB back to the host, so the test compares a
+size-independent property instead: the device checksum of every
+destination tensor against the oracle's checksum of its source, plus the
+shape and strides each destination keeps.
 """
 
 from __future__ import annotations
