@@ -42,3 +42,30 @@ def test_error_path_without_device_call():
     rc = lib.ftx_set_copy_policy(0, 0, 99, 0)
     assert rc == _native.FTX_ERR_INVALID
     assert b"n_copy_streams" in lib.ftx_last_error()
+
+
+def test_missing_library_fails_loudly():
+    """With no built library the product refuses to run: the first native call raises
+    FtxLibraryMissing (an ImportError); nothing falls back to a host path or to the oracle."""
+    import subprocess
+    import sys
+
+    code = (
+        "from pathlib import Path\n"
+        "import flextensor_amd._native as nat\n"
+        "nat.LIB_PATH = Path('/nonexistent/libftx_hip.so')\n"
+        "for attempt in (lambda: nat.load(), lambda: nat.checksum64(0, 0, 0),\n"
+        "                lambda: nat.call('ftx_scatter', None, None, 0, None)):\n"
+        "    try:\n"
+        "        attempt()\n"
+        "    except nat.FtxLibraryMissing as e:\n"
+        "        assert isinstance(e, ImportError) and 'libftx_hip.so is missing' in str(e)\n"
+        "    else:\n"
+        "        raise SystemExit('a native call ran without the library')\n"
+        "import sys\n"
+        "assert not any(m == 'oracle' or m.startswith('oracle.') for m in sys.modules), 'oracle imported'\n"
+        "print('refused')\n"
+    )
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                         cwd=str(Path(__file__).resolve().parents[1]))
+    assert out.returncode == 0 and out.stdout.strip().endswith("refused"), out.stdout + out.stderr
