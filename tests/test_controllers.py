@@ -288,3 +288,29 @@ def test_failed_cleanup_keeps_the_primary_error_and_a_retry_handle(monkeypatch, 
     for k in tensors:
         assert torch.equal(tensors[k], want[k])
     assert ctrl.block_map_cpu == {}
+
+
+def test_abort_construction_keeps_the_callers_error(monkeypatch):
+    """abort_construction(primary) after a later setup step failed: the cleanup's own failure is attached
+    to the caller's error, never raised in its place (loaders.py:1269-1286)."""
+    tensors = {1: torch.arange(64, dtype=torch.uint8)}
+    want = tensors[1].clone()
+    ctrl = RawBlockController({"a": 64}, {0: 64}, torch.device("cpu"), tensors, {"a": _stats(1, 64)}, {"a": 0},
+                              host_pinner=_FailingPinner(fail_at=0))
+    assert tensors[1].numel() == 0  # packed and released into the host block
+    primary = RuntimeError("loader construction failed")
+    real = type(ctrl).shutdown
+    failures = iter([RuntimeError("first cleanup attempt failed")])
+
+    def flaky(self):
+        err = next(failures, None)
+        if err is not None:
+            raise err
+        real(self)
+
+    monkeypatch.setattr(type(ctrl), "shutdown", flaky)
+    ctrl.abort_construction(primary)  # does not raise
+    assert primary.__dict__["_flextensor_cleanup_controller"] is ctrl
+    assert str(primary.__dict__["_flextensor_cleanup_error"]) == "first cleanup attempt failed"
+    ctrl.shutdown()  # the retry
+    assert torch.equal(tensors[1], want)
