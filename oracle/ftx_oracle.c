@@ -8,6 +8,10 @@
  *   oracle_pack           follows AllocationBlock._tensors_to_memory_block
  *                         (allocation_block.py:179-181): per-tensor byte copy of a
  *                         dense tensor's storage bytes into the block at its offset.
+ *                         Pinned by the reference's three-tensor block and its
+ *                         Fortran byte-order case (test_allocation_block.py:14-56,
+ *                         test_stride_preservation.py:38-70), written out byte
+ *                         by byte; a shifted offset fails that check.
  *   oracle_scatter        the semantics of one batched scatter: for every
  *                         descriptor dst[0:n) = chunk[off:off+n), as the
  *                         reference's per-tensor copies produce it

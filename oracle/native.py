@@ -53,6 +53,27 @@ def packed_layout(sizes, alignment: int = 128) -> tuple[list[int], int]:
     return [int(x) for x in offsets[: len(sizes)]], int(total)
 
 
+def pack(block: np.ndarray, offsets, sources) -> None:
+    """C restatement of the block pack (allocation_block.py:179-181): ``block[off_i : off_i + n_i]`` =
+    the storage bytes of source ``i`` (a contiguous uint8 numpy array of ``n_i`` bytes)."""
+    sources = [np.ascontiguousarray(s).view(np.uint8).reshape(-1) for s in sources]
+    offsets = list(offsets)
+    if len(offsets) != len(sources):
+        raise ValueError("one offset per source")
+    for off, src in zip(offsets, sources):
+        if off < 0 or off + src.nbytes > block.nbytes:
+            raise ValueError(f"source of {src.nbytes} bytes at offset {off} overruns a {block.nbytes}-byte block")
+    n = max(1, len(sources))
+    offs = np.zeros(n, dtype=np.uint64)
+    ptrs = np.zeros(n, dtype=np.uint64)
+    sizes = np.zeros(n, dtype=np.uint64)
+    for i, (off, src) in enumerate(zip(offsets, sources)):
+        offs[i], ptrs[i], sizes[i] = off, src.ctypes.data, src.nbytes
+    if not block.flags["C_CONTIGUOUS"]:
+        raise ValueError("the block must be contiguous")
+    lib().oracle_pack(block.ctypes.data, offs.ctypes.data, ptrs.ctypes.data, sizes.ctypes.data, len(sources))
+
+
 def checksum64(data) -> int:
     """Checksum of a bytes-like / numpy uint8 array / CPU uint8 tensor."""
     if hasattr(data, "numpy"):

@@ -6,6 +6,7 @@ from __future__ import annotations
 import json
 import math
 import random
+import struct
 from pathlib import Path
 
 import numpy as np
@@ -209,6 +210,63 @@ def test_dense_layout_cases():
     assert ol.is_dense((4, 2, 3), (1, 12, 4))  # permuted 3-D
     assert not ol.is_dense((3, 2, 5), (20, 10, 1))  # sliced 3-D
     assert not ol.is_dense((4,), (3,))
+
+
+# ---- block pack -----------------------------------------------------------------
+
+_NP = {"float32": np.float32, "int32": np.int32}
+
+
+def _pack_fixture():
+    c = GOLD["allocation_block_pack"]
+    return c, [np.full(t["numel"], t["fill"], dtype=_NP[t["dtype"]]) for t in c["tensors"]]
+
+
+def _expected_block(c) -> bytes:
+    """The fixture's block written out with ``struct``, independently of the oracle."""
+    out = bytearray(c["total"])
+    for t, off in zip(c["tensors"], c["offsets"]):
+        raw = struct.pack("<%d%s" % (t["numel"], "f" if t["dtype"] == "float32" else "i"), *([t["fill"]] * t["numel"]))
+        out[off: off + len(raw)] = raw
+    return bytes(out)
+
+
+def test_pack_known_answer():
+    c, srcs = _pack_fixture()
+    offs, total = ol.packed_layout([s.nbytes for s in srcs], c["alignment"])
+    assert (offs, total) == (c["offsets"], c["total"])
+    block = np.zeros(total, np.uint8)
+    onat.pack(block, offs, srcs)
+    assert block.tobytes() == _expected_block(c)
+    # 1.0f, 2.0f and int32 3 spelled out byte by byte, little-endian
+    assert block[0:4].tobytes() == b"\x00\x00\x80\x3f" and block[128:132].tobytes() == b"\x00\x00\x00\x40"
+    assert block[256:260].tobytes() == b"\x03\x00\x00\x00" and not block[308:].any() and not block[48:128].any()
+
+
+@pytest.mark.parametrize("wrong", [[0, 124, 256], [0, 128, 252], [4, 128, 256], [0, 256, 128]])
+def test_pack_known_answer_catches_a_wrong_offset(wrong):
+    c, srcs = _pack_fixture()
+    block = np.zeros(c["total"], np.uint8)
+    onat.pack(block, wrong, srcs)
+    assert block.tobytes() != _expected_block(c)
+
+
+def test_pack_keeps_fortran_memory_order():
+    import torch
+
+    f = GOLD["allocation_block_pack"]["fortran"]
+    t = torch.arange(12, dtype=torch.float32).reshape(*f["base_shape"]).t()
+    assert tuple(t.shape) == tuple(f["shape"]) and t.stride() == tuple(f["stride"])
+    raw = np.frombuffer(bytes(t.untyped_storage()), dtype=np.uint8)
+    block = np.zeros(128, np.uint8)
+    onat.pack(block, [0], [raw])
+    assert block[:48].tobytes() == struct.pack("<12f", *f["memory_order_values"])
+    assert t.contiguous().numpy().tobytes() != block[:48].tobytes()  # a pack in C order would fail the check
+
+
+def test_pack_rejects_overruns():
+    with pytest.raises(ValueError, match="overruns"):
+        onat.pack(np.zeros(64, np.uint8), [32], [np.zeros(40, np.uint8)])
 
 
 # ---- interpolator --------------------------------------------------------------
