@@ -206,8 +206,20 @@ def arena_free(ptr: int) -> None:
     call("ftx_arena_free", ptr)
 
 
+HOST_REGISTER_REFUSED = (
+    "in-place page-locking (pinned_memory_mode='host_register', hipHostRegister of existing memory) is refused "
+    "in this build: the MI355X hosts it targets reject hipHostRegister, and the failed call's error can surface "
+    "in the next GPU call. Use pinned_memory_mode='torch' (blocks are allocated directly in page-locked arenas); "
+    "shared-memory blocks then stream through the staged copy engine.")
+
+
 def arena_register(ptr: int, nbytes: int, flags: int = 0) -> None:
-    call("ftx_arena_register", ptr, nbytes, flags)
+    """Page-lock existing host memory in place: refused in this build (``HOST_REGISTER_REFUSED``).
+
+    ``ftx_arena_register`` stays in the C ABI for hosts that allow it; the
+    Python path never reaches it.
+    """
+    raise FtxError(FTX_ERR_UNSUPPORTED, HOST_REGISTER_REFUSED)
 
 
 def arena_unregister(ptr: int) -> None:

@@ -236,13 +236,13 @@ class AllocationBlock:
         self.tensors = []
         seg = self.shm_segment
         if seg is not None:
-            # The creator removes the name; other processes' mappings stay valid. The
-            # mapping itself is not closed here: tensors (restored parameters, user
-            # references) may still view it, and it is unmapped with the last of them.
+            # The creator removes the name; other processes' mappings stay valid. Closing
+            # drops the block's hold on the mapping: tensors that still view it (restored
+            # parameters, user references) keep it mapped until the last of them goes.
             # An in-place pin of the mapping ends with the pinner's release_all(), like
             # every other pin (pins are released at manager shutdown, not with blocks).
             # A failed unlink keeps the segment, so release() can be retried.
-            seg.unlink()
+            seg.close()
         self.shm_segment = None
 
 

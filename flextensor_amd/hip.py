@@ -173,16 +173,21 @@ def new_stream(device: torch.device | int | None = None, name: str = "transfer")
 
 _TRANSFER_STREAMS: dict[int, HipStream] = {}
 _REJECTED_STREAMS: list[Any] = []  # kept alive so later streams are not handed the same queue again
+_STREAM_PROBES: dict[int, dict[str, Any]] = {}
 
 
-def _runs_concurrently(candidate: HipStream, compute: HipStream, device: torch.device) -> bool:
-    """Whether work on ``candidate`` proceeds while ``compute`` is busy.
+class TransferStreamError(RuntimeError):
+    """No new stream ran beside the compute stream: transfers would queue behind every forward kernel."""
+
+
+def _probe_concurrency(candidate: HipStream, compute: HipStream, device: torch.device) -> tuple[float, float]:
+    """``(busy_ms, candidate_ms)``: how long the compute stream's queued work took, and when a tiny fill
+    queued on ``candidate`` at the same time finished.
 
     Streams share the device's hardware queues; a stream on the compute
-    stream's queue waits behind every compute packet. The check queues about
+    stream's queue waits behind every compute packet. The probe queues about
     two milliseconds of matrix products on ``compute`` (enqueued in a tenth of
-    that) and a one-kilobyte fill on ``candidate``, and compares when each
-    finishes.
+    that) and a one-kilobyte fill on ``candidate``.
     """
     a = torch.ones(4096, 4096, dtype=torch.bfloat16, device=device)
     small = torch.empty(1024, dtype=torch.uint8, device=device)
@@ -197,13 +202,13 @@ def _runs_concurrently(candidate: HipStream, compute: HipStream, device: torch.d
         small.fill_(1)
     candidate.record_event(s_end)
     torch.cuda.synchronize(device)
-    busy = start.elapsed_time(c_end)
-    return start.elapsed_time(s_end) < 0.5 * busy
+    return start.elapsed_time(c_end), start.elapsed_time(s_end)
 
 
-@contextmanager
-def _nullctx() -> Iterator[None]:
-    yield
+def _runs_concurrently(candidate: HipStream, compute: HipStream, device: torch.device) -> bool:
+    """Whether work on ``candidate`` finishes while ``compute`` is still busy (in the first half)."""
+    busy, cand = _probe_concurrency(candidate, compute, device)
+    return cand < 0.5 * busy
 
 
 def transfer_stream(device: torch.device | int | None = None, attempts: int = 8) -> HipStream:
@@ -211,8 +216,10 @@ def transfer_stream(device: torch.device | int | None = None, attempts: int = 8)
 
     Chosen once per device among new default-priority streams: the first one
     whose work runs concurrently with torch's current stream (see
-    :func:`_runs_concurrently`). If none of ``attempts`` candidates does, the
-    last one is used and a warning is logged.
+    :func:`_probe_concurrency`). Rejected candidates stay allocated, so the
+    pool does not hand their queue out again. If none of ``attempts``
+    candidates runs beside the compute stream, :class:`TransferStreamError`
+    names the measurements. :func:`transfer_stream_probe` reports the outcome.
     """
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
     if dev.index is None:
@@ -221,20 +228,30 @@ def transfer_stream(device: torch.device | int | None = None, attempts: int = 8)
     if cached is not None:
         return cached
     compute = current_stream(dev)
-    chosen = None
-    for _ in range(attempts):
+    tried: list[tuple[float, float]] = []
+    for i in range(attempts):
         cand = new_stream(dev, name="transfer")
-        if _runs_concurrently(cand, compute, dev):
-            chosen = cand
-            break
+        busy, done = _probe_concurrency(cand, compute, dev)
+        tried.append((round(busy, 3), round(done, 3)))
+        if done < 0.5 * busy:
+            _STREAM_PROBES[dev.index] = {"chosen_candidate": i, "rejected": i, "attempts": attempts,
+                                         "compute_busy_ms": tried[-1][0], "transfer_fill_done_ms": tried[-1][1]}
+            _TRANSFER_STREAMS[dev.index] = cand
+            return cand
         _REJECTED_STREAMS.append(cand)
-    if chosen is None:
-        import logging
+    raise TransferStreamError(
+        f"no transfer stream on cuda:{dev.index} runs beside the compute stream: each of {attempts} new "
+        f"default-priority streams finished a 1 KB fill only after the compute stream's queued matrix products "
+        f"(compute busy ms, fill done ms per candidate: {tried}). Every candidate shares the compute stream's "
+        "hardware queue, so transfers would wait behind each forward kernel; check GPU_MAX_HW_QUEUES and other "
+        "work on this device")
 
-        logging.getLogger(__name__).warning("no transfer stream found that runs beside the compute stream")
-        chosen = _REJECTED_STREAMS.pop()
-    _TRANSFER_STREAMS[dev.index] = chosen
-    return chosen
+
+def transfer_stream_probe(device: torch.device | int | None = None) -> dict[str, Any] | None:
+    """How the transfer stream of ``device`` was chosen: candidate index, rejected count and the timings
+    of the accepted probe; None before :func:`transfer_stream` ran there."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    return _STREAM_PROBES.get(dev.index if dev.index is not None else torch.cuda.current_device())
 
 
 @contextmanager

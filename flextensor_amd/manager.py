@@ -399,6 +399,8 @@ class OffloadManager:
         self.config = config or OffloadConfig()
         if load_from_shm and (state is None or not self.config.shm_enabled or not state.shm_block_name_map):
             raise ValueError("load_from_shm needs shm_enabled and a saved state that names its shared blocks")
+        if self.config.enabled and self.config.pinned_memory and self.config.pinned_memory_mode == "host_register":
+            raise ValueError(nat.HOST_REGISTER_REFUSED)
         self.compile_fn = compile_fn
         self._load_from_shm = load_from_shm
         if not self.config.enabled:
@@ -1138,11 +1140,21 @@ class OffloadManager:
                                "profiling passes eagerly before capturing a graph")
         if label in self._seen_this_pass:
             raise NotImplementedError(f"offload unit {label!r} ran twice in one forward")
-        self._seen_this_pass.append(label)
         u = self._unit(label)
-        for p in u.params:
-            self._cpu_data[id(p)] = p.data
-            p.data = p.data.to(self.device, non_blocking=False)
+        moved: list[nn.Parameter] = []
+        try:
+            for p in u.params:
+                host = p.data
+                p.data = host.to(self.device, non_blocking=False)
+                self._cpu_data[id(p)] = host
+                moved.append(p)
+        except BaseException:
+            # a move that failed part way (out of memory) puts back the ones already moved, so the host
+            # originals are never overwritten by device copies on the next pass
+            for p in moved:
+                p.data = self._cpu_data.pop(id(p))
+            raise
+        self._seen_this_pass.append(label)
         if self.phase == OffloadPhase.PROFILING:
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
@@ -1294,17 +1306,25 @@ class OffloadManager:
                     if key in exc.__dict__:  # a retryable cleanup handle stays on the error the caller sees
                         oom.__dict__[key] = exc.__dict__[key]
                 raise oom from exc
-            for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
-                tensors_map[tid].data = view
-            self._install_state_dict_hooks(tensors_map)
-            reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"
-            cls = PreallocatedBatchTransferTensorLoaderReordered if reordered else PreallocatedBatchTransferTensorLoader
-            self.timing = OffloadTimingCollector(order, enabled=cfg.offload_timing != "off",
-                                                 graph_replay=cfg.offload_timing == "cuda_graph")
-            policy = PiecewisePrefetchPolicy(enabled=cfg.piecewise_prefetch != "off",
-                                             strict=cfg.piecewise_prefetch == "error")
-            self.loader = cls(layer_stats, self.device, bd.label_to_block_id, bd.transfer_to_compute_map,
-                              self.controller, self.timing, policy)
+            bound = {tid: t.data for tid, t in tensors_map.items()}
+            n_hooks = len(self._hooks)
+            try:
+                for tid, view in self.controller.get_tensor_id_to_view_mapping().items():
+                    tensors_map[tid].data = view
+                self._install_state_dict_hooks(tensors_map)
+                reordered = plan.reordered if cfg.loader_order == "auto" else cfg.loader_order == "reordered"
+                cls = (PreallocatedBatchTransferTensorLoaderReordered if reordered
+                       else PreallocatedBatchTransferTensorLoader)
+                self.timing = OffloadTimingCollector(order, enabled=cfg.offload_timing != "off",
+                                                     graph_replay=cfg.offload_timing == "cuda_graph")
+                policy = PiecewisePrefetchPolicy(enabled=cfg.piecewise_prefetch != "off",
+                                                 strict=cfg.piecewise_prefetch == "error")
+                # the loader's constructor preloads the first slots: the first copies run here
+                self.loader = cls(layer_stats, self.device, bd.label_to_block_id, bd.transfer_to_compute_map,
+                                  self.controller, self.timing, policy)
+            except BaseException as primary:
+                self._abort_build(primary, tensors_map, bound, n_hooks)
+                raise
             self.controller.commit_construction()
         self.phase = OffloadPhase.INFERENCE
         if self.compile_fn is not None:
@@ -1317,6 +1337,34 @@ class OffloadManager:
                     len(plan.resident), self.build_seconds)
         if cfg.enable_diagnostics:
             LOGGER.info("offload %r plan:\n%s", self.name, self.plan_table())
+
+    def _abort_build(self, primary: BaseException, tensors_map: dict[int, torch.Tensor],
+                     bound: dict[int, torch.Tensor], n_hooks: int) -> None:
+        """Undo a streaming build that failed after its controller was made (tensor_manager.py:1585-1596).
+
+        Parameters go back to what they held before they were bound to slot
+        views, the state-dict hooks of the build go, and the controller's
+        ``abort_construction`` restores the released sources and frees the
+        host blocks, the GPU slots and any shared-memory segments. A cleanup
+        that fails never replaces ``primary``: the controller stays reachable
+        from it (``_flextensor_cleanup_controller``) so ``shutdown()`` can be
+        retried. Copies the loader already queued are waited for first, since
+        they read the host blocks about to be freed.
+        """
+        try:
+            torch.cuda.synchronize(self.device)
+        except Exception:  # noqa: BLE001 - the device may be what failed; the primary error is the one to report
+            LOGGER.warning("offload %r: synchronize before undoing the build failed", self.name, exc_info=True)
+        for h in self._hooks[n_hooks:]:
+            h.remove()
+        del self._hooks[n_hooks:]
+        for tid, t in tensors_map.items():
+            t.data = bound[tid]
+        self.loader = self.timing = None
+        controller, self.controller = self.controller, None
+        if controller is not None:
+            controller.abort_construction(primary)
+        self._release_pins()
 
     def _validate_source_storage(self, plan: StreamPlan) -> None:
         """Refuse streamed tensors that overlap another distinct tensor's bytes, before anything moves.
@@ -1444,6 +1492,10 @@ class OffloadManager:
             else:
                 where = "resident"
             rows.append(f"{label:<32} {u.nbytes / 2**20:>10.2f} {self._duration(label):>9.3f}  {where}")
+        probe = hip.transfer_stream_probe(self.device) if self.device is not None else None
+        if probe is not None:
+            rows.append(f"transfer stream: candidate {probe['chosen_candidate']} of {probe['attempts']} "
+                        f"({probe['rejected']} rejected for queueing behind the compute stream)")
         return "\n".join(rows)
 
 

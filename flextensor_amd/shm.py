@@ -99,11 +99,9 @@ class SharedSegment:
             os.ftruncate(fd, size)
             self._map(fd, size)
             if initializer is not None:
-                view = self._buf[:]
-                try:
-                    initializer(view)
-                finally:
-                    view.release()
+                # a slice of its own, dropped (not released) afterwards: tensors the initializer made
+                # from it keep the mapping alive by reference
+                initializer(self._buf[:])
             os.link(tmp, self.path)  # atomic publish; FileExistsError when the name is taken
         except BaseException:
             self._unmap()
@@ -133,12 +131,17 @@ class SharedSegment:
         return len(self.buf)
 
     def _unmap(self) -> None:
-        if self._buf is not None:
-            self._buf.release()
-            self._buf = None
-        if self._mmap is not None:
-            self._mmap.close()  # unmaps: callers make sure no tensor views the mapping any more
-            self._mmap = None
+        """Drop this object's references to the mapping (never a forced unmap).
+
+        ``torch.frombuffer(segment.buf)`` keeps the memoryview object alive but
+        holds no buffer export, so an explicit ``mmap.close()`` would succeed
+        and unmap memory that live tensors still point at. Instead the memory
+        is unmapped when the last reference goes: the memoryview holds the
+        mapping, and tensors hold the memoryview. With no tensor left the
+        mapping goes at once (reference counting).
+        """
+        self._buf = None
+        self._mmap = None
 
     def unlink(self) -> None:
         """The creator removes the name (other processes' mappings stay valid). Idempotent."""
@@ -150,13 +153,10 @@ class SharedSegment:
                 pass
 
     def close(self) -> None:
-        """The creator removes the name, then the mapping is closed. Idempotent.
+        """The creator removes the name, and this object lets go of the mapping. Idempotent.
 
-        Only for segments no tensor views any more: ``torch.frombuffer`` keeps
-        the buffer object alive but not its export, so closing would unmap
-        memory that live tensors still point at. Owners of tensor views call
-        :meth:`unlink` and drop the segment instead; the mapping then goes
-        away with the last tensor that references it.
+        Safe with live tensor views: the mapping stays until the last tensor
+        made from :attr:`buf` is gone, then it is unmapped.
         """
         if self._mmap is None:
             return

@@ -137,12 +137,20 @@ class Fp8Linear(nn.Module):
                                    requires_grad=False)
         self.scale = nn.Parameter(torch.ones(out_features, dtype=torch.bfloat16), requires_grad=False)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def kernel_eligible(self, x: torch.Tensor) -> bool:
+        """Whether the library kernel takes this call: a bf16 GPU input of 1..64 rows, K a multiple of
+        16, and a contiguous, 16-byte aligned weight (``raw_block_transfer`` packs weights back to back
+        without alignment; such a weight takes the dequantize path)."""
         k = x.shape[-1]
         m = x.numel() // k if k else 0
-        if (x.is_cuda and x.dtype == torch.bfloat16 and 0 < m <= hip.FP8_LINEAR_MAX_ROWS and k % 16 == 0
-                and self.weight.is_contiguous()):
-            y = hip.fp8_linear(x.reshape(m, k), self.weight, self.scale)
+        w = self.weight
+        return (x.is_cuda and x.dtype == torch.bfloat16 and 0 < m <= hip.FP8_LINEAR_MAX_ROWS and k % 16 == 0
+                and w.is_contiguous() and w.data_ptr() % 16 == 0)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.kernel_eligible(x):
+            k = x.shape[-1]
+            y = hip.fp8_linear(x.reshape(x.numel() // k, k), self.weight, self.scale)
             return y.view(*x.shape[:-1], y.shape[-1])
         w = self.weight.to(torch.bfloat16)
         return F.linear(x, w) * self.scale

@@ -193,6 +193,12 @@ def test_transfer_stream_runs_beside_compute(gpu):
     torch.cuda.synchronize()
     assert start.elapsed_time(copy_end) < 0.5 * start.elapsed_time(gemm_end)
     assert transfer_stream(gpu) is s  # one per device
+    from flextensor_amd.hip import transfer_stream_probe
+
+    probe = transfer_stream_probe(gpu)
+    print(f"transfer stream probe: {probe}", flush=True)
+    assert probe["chosen_candidate"] == probe["rejected"] < probe["attempts"]
+    assert probe["transfer_fill_done_ms"] < 0.5 * probe["compute_busy_ms"]
 
 
 def test_arena_freed_by_refcount_when_last_view_dies(gpu):

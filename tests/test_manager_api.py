@@ -311,3 +311,87 @@ def test_overlapping_views_are_refused_before_anything_moves():
     resident_only = M.StreamPlan(["1"], ["0", "2"], None, {}, False, None, 0)
     mgr._validate_source_storage(resident_only)  # no streamed tensor is involved
     M._MANAGERS.pop("overlap-check", None)
+
+
+# ---- a streaming build that fails after its controller exists (tensor_manager.py:1585-1596) ----------------
+
+
+class _PreloadFails:
+    """Stands in for a loader whose constructor's preload raises (a refused copy, an exhausted device)."""
+
+    def __init__(self, *args, **kwargs) -> None:
+        raise RuntimeError("preload copy refused")
+
+
+@pytest.mark.parametrize("shm", [False, True])
+def test_failed_loader_build_restores_sources_and_aborts_the_controller(host_offload, shm):
+    import os
+    import uuid
+
+    ns = f"ftx_abort_{uuid.uuid4().hex[:8]}"
+    extra = {"shm_enabled": True, "shm_namespace": ns} if shm else {}
+    mgr = host_offload(f"abort-{shm}", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1,
+                       pinned_memory=False, **extra)
+    params = [p for u in mgr.units for p in u.params]
+    want = [p.detach().clone() for p in params]
+    hooks_before = len(mgr._hooks)
+    mgr.device = torch.device("cpu")  # the ring slots live on the CPU, as in the controller tests
+    mgr.order = [u.label for u in mgr.units]
+    with mock.patch.object(M, "PreallocatedBatchTransferTensorLoader", _PreloadFails), \
+            mock.patch.object(M, "PreallocatedBatchTransferTensorLoaderReordered", _PreloadFails), \
+            mock.patch.object(M.torch.cuda, "synchronize", lambda *a: None):
+        with pytest.raises(RuntimeError, match="preload copy refused"):
+            mgr._to_inference()
+    assert mgr.controller is None and mgr.loader is None and len(mgr._hooks) == hooks_before
+    for p, w in zip(params, want):  # packed, released, bound to slot views, then put back
+        assert p.device.type == "cpu" and torch.equal(p, w)
+    if shm:
+        assert not [f for f in os.listdir("/dev/shm") if f.startswith(ns)]  # no segment outlives the build
+    assert mgr.phase != M.OffloadPhase.INFERENCE
+
+
+def test_a_failed_move_in_discovery_puts_back_the_moved_parameters(host_offload):
+    """A unit whose upload runs out of memory part way leaves every parameter on the host, and the next
+    pass still finds the host originals."""
+    mgr = host_offload("enter-oom", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
+    u = mgr.units[0]
+    want = [p.detach().clone() for p in u.params]
+    originals = [p.data_ptr() for p in u.params]
+    real_to = torch.Tensor.to
+    calls = {"n": 0}
+
+    def flaky_to(self, *args, **kwargs):
+        calls["n"] += 1
+        if calls["n"] == 2:
+            raise torch.cuda.OutOfMemoryError("HIP out of memory")
+        return real_to(self, "cpu").clone()  # a distinct tensor stands in for the device copy
+
+    mgr.device = torch.device("cpu")
+    with mock.patch.object(torch.Tensor, "to", flaky_to):
+        with pytest.raises(torch.cuda.OutOfMemoryError):
+            mgr._enter(u.label)
+    assert [p.data_ptr() for p in u.params] == originals and not mgr._cpu_data
+    assert u.label not in mgr._seen_this_pass
+    mgr._enter(u.label)  # the retry moves every parameter and keeps the host originals
+    assert [mgr._cpu_data[id(p)].data_ptr() for p in u.params] == originals
+    mgr._exit(u.label)
+    assert all(torch.equal(p, w) for p, w in zip(u.params, want))
+
+
+def test_host_register_mode_is_refused_before_anything_moves(names):
+    """In-place page-locking is refused in this build: offload() says so before touching the model, and
+    the native wrapper never reaches hipHostRegister."""
+    from flextensor_amd import _native as nat
+
+    names.append("host-reg")
+    model = _Stack()
+    want = [p.detach().clone() for p in model.parameters()]
+    with pytest.raises(ValueError, match="host_register"):
+        M.get_offload_manager("host-reg").offload(model, OffloadConfig(pinned_memory_mode="host_register"))
+    assert all(torch.equal(p, w) and p.device.type == "cpu" for p, w in zip(model.parameters(), want))
+    assert M.get_offload_manager("host-reg").model is None
+    with pytest.raises(nat.FtxError, match="refused in this build") as info:
+        nat.arena_register(0, 4096)
+    assert info.value.code == nat.FTX_ERR_UNSUPPORTED
+    # without pinning the mode has nothing to pin and is accepted
+    assert OffloadConfig(pinned_memory=False, pinned_memory_mode="host_register").pinned_memory_mode == "host_register"

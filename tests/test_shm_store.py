@@ -421,3 +421,92 @@ def test_follower_in_another_process(ns):
         assert got == (src.weight.detach().tolist(), src.counter.tolist(), 7.5)
     finally:
         creator.close()
+
+
+# ---- a closed segment never unmaps memory that tensors still view -----------------------
+
+
+def _mapped(addr: int) -> bool:
+    """Whether a shared-memory mapping of this process covers ``addr``."""
+    with open("/proc/self/maps") as fh:
+        for line in fh:
+            lo, hi = (int(x, 16) for x in line.split()[0].split("-"))
+            if lo <= addr < hi and "/dev/shm/" in line:
+                return True
+    return False
+
+
+def test_close_keeps_live_views_readable_and_unmaps_with_the_last(ns):
+    """The cause of a segfault in the shared-memory streaming release: a segment closed while
+    ``torch.frombuffer`` views were alive unmapped their memory. Now the views stay readable, the name is
+    gone at once, and the mapping goes with the last view."""
+    import gc
+
+    seg = SharedSegment(f"{ns}_v", 1 << 20, create=True)
+    path = seg.path
+    t = torch.frombuffer(seg.buf, dtype=torch.uint8)
+    t.copy_(torch.arange(1 << 20, dtype=torch.int64).remainder(251).to(torch.uint8))
+    view = t[4096:8192].view(torch.int32)
+    addr = t.data_ptr()
+    seg.close()
+    seg.close()  # idempotent
+    assert not os.path.exists(path)  # the creator removed the name
+    with pytest.raises(RuntimeError, match="closed"):
+        seg.buf
+    want = torch.arange(1 << 20, dtype=torch.int64).remainder(251).to(torch.uint8)
+    assert torch.equal(t, want) and torch.equal(view.view(torch.uint8), want[4096:8192])  # still mapped
+    assert _mapped(addr)
+    del t, view
+    gc.collect()
+    assert not _mapped(addr)  # unmapped once the last view went
+
+
+def test_close_without_views_unmaps_at_once(ns):
+    seg = SharedSegment(f"{ns}_n", 1 << 16, create=True)
+    seg.buf[0] = 1
+    addr = torch.frombuffer(seg.buf, dtype=torch.uint8).data_ptr()  # the temporary view is gone at once
+    assert _mapped(addr)
+    seg.close()
+    assert not _mapped(addr)
+
+
+def test_release_after_shared_memory_streaming_leaves_parameters_readable(ns):
+    """tensor_manager.py:2320-2354: release(preserve_model=True) copies shared-memory blocks out into the
+    parameters; the block segments go, and the parameters stay readable and equal to the originals."""
+    from unittest import mock
+
+    import flextensor_amd.manager as M
+    from flextensor_amd.allocation_block import HostPinner
+    from flextensor_amd.controllers import AllocationBlockController
+    from flextensor_amd.planner import TensorStatistics
+
+    model = nn.Sequential(nn.Linear(64, 32), nn.Linear(32, 64))
+    params = list(model.parameters())
+    want = [p.detach().clone() for p in params]
+    units = {"0": list(model[0].parameters()), "1": list(model[1].parameters())}
+    tensors = {id(p): p for p in params}
+    strategy = {x: [TensorStatistics(id(p), f"{x}.{i}", p.numel() * p.element_size(), 0.0)
+                    for i, p in enumerate(ps)] for x, ps in units.items()}
+    names = {x: f"{ns}_b{x}" for x in units}
+    ctrl = AllocationBlockController({0: ["0"], 1: ["1"]}, torch.device("cpu"), tensors, strategy, {"0": 0, "1": 1},
+                                     host_pinner=HostPinner("torch", enabled=False), shm_block_name_map=names)
+    ctrl.commit_construction()
+    for tid, view in ctrl.get_tensor_id_to_view_mapping().items():
+        tensors[tid].data = view  # the parameters alias their slots, as when streaming
+    for x in units:
+        ctrl.schedule_transfer(x)
+    mgr = M.OffloadManager(f"shm-release-{ns}")
+    mgr.model, mgr.controller, mgr.device = model, ctrl, torch.device("cpu")
+    # as in a streaming run, the loader's shutdown releases the controller's blocks (and their segments)
+    # after release() took the views it restores from, and before it copies them out
+    mgr.loader = type("_Loader", (), {"shutdown": staticmethod(ctrl.shutdown)})()
+    mgr.units = [M._Unit(x, model[int(x)], ps, [f"{x}.w", f"{x}.b"]) for x, ps in units.items()]
+    with mock.patch.object(M.torch.cuda, "synchronize", lambda *a: None):
+        mgr.release()
+    del ctrl
+    import gc
+
+    gc.collect()
+    for p, w in zip(params, want):
+        assert torch.equal(p, w)  # readable after the blocks' segments were released
+    assert not [f for f in os.listdir("/dev/shm") if f.startswith(f"{ns}_b")]

@@ -174,3 +174,29 @@ def test_fp8_llama_matches_dequantized_float32():
     want = twin(tokens, 0)
     assert float((got - want).norm() / want.norm()) < 1e-2
     assert W.LLAMA_70B_FP8.layer_bytes() == 855_838_720
+
+
+class _FakeGpuInput:
+    """Only what ``Fp8Linear.kernel_eligible`` reads of an input on the GPU."""
+
+    def __init__(self, m: int, k: int) -> None:
+        self.shape = (m, k)
+        self.is_cuda = True
+        self.dtype = torch.bfloat16
+
+    def numel(self) -> int:
+        return self.shape[0] * self.shape[1]
+
+
+def test_fp8_kernel_needs_an_aligned_weight():
+    """A weight packed without alignment (raw_block_transfer) takes the dequantize path instead of raising."""
+    lin = W.Fp8Linear(64, 32)
+    x = _FakeGpuInput(8, 64)
+    assert lin.kernel_eligible(x)
+    raw = torch.empty(32 * 64 + 16, dtype=torch.uint8)
+    for shift in (1, 8):
+        lin.weight.data = raw[shift: shift + 32 * 64].view(torch.float8_e4m3fn).view(32, 64)
+        assert lin.weight.data_ptr() % 16 and not lin.kernel_eligible(x)
+    lin.weight.data = raw[16: 16 + 32 * 64].view(torch.float8_e4m3fn).view(32, 64)
+    assert lin.kernel_eligible(x)
+    assert not lin.kernel_eligible(_FakeGpuInput(65, 64)) and not lin.kernel_eligible(_FakeGpuInput(8, 24))
