@@ -10,6 +10,12 @@
 
 #include "ftx_internal.h"
 
+// Split-K partial sums of ftx_fp8_linear_static, for callers that cannot
+// allocate: one array per GPU, held until the process ends. On the host this
+// name is a stand-in, not a device address: host code only ever uses the
+// address hipGetSymbolAddress returns for the current device (static_scratch).
+static __device__ __align__(256) uint8_t scratch[FTX_FP8_STATIC_SCRATCH_BYTES];
+
 namespace ftx {
 
 namespace {
@@ -34,6 +40,7 @@ struct DeviceState {
   hipStream_t copy_streams[kMaxCopyStreams] = {};
   hipEvent_t fork_event = nullptr;
   hipEvent_t join_events[kMaxCopyStreams] = {};
+  void *static_scratch = nullptr;  // this device's address of `scratch`, resolved on first use
 };
 
 struct ArenaRecord {
@@ -87,6 +94,23 @@ int device_state(DeviceState **out) {
     st.ready = true;
   }
   *out = &st;
+  return FTX_OK;
+}
+
+// This device's copy of the static scratch array: its address is looked up
+// once per device, with the device current, and kept.
+int static_scratch(void **out) {
+  DeviceState *st = nullptr;
+  int rc = device_state(&st);
+  if (rc != FTX_OK) return rc;
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  if (st->static_scratch == nullptr) {
+    void *ptr = nullptr;
+    FTX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (ptr == nullptr) return fail(FTX_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
+    st->static_scratch = ptr;
+  }
+  *out = st->static_scratch;
   return FTX_OK;
 }
 
@@ -685,16 +709,17 @@ int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes) {
   return FTX_OK;
 }
 
-int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
-                   void *workspace, size_t workspace_bytes, void *stream) {
-  ftx::Fp8LinearLaunch p;
-  int rc = plan_fp8(m, n, k, &p);
-  if (rc != FTX_OK) return rc;
-  if (m == 0 || n == 0) return FTX_OK;
+namespace {
+
+// Checks the operands of one planned fp8 linear call and launches it. The
+// workspace is checked against its allocation unless it is the static scratch.
+int run_fp8(ftx::Fp8LinearLaunch &p, const void *x, const void *w, const void *scale, void *y, void *workspace,
+            size_t workspace_bytes, bool static_workspace, void *stream) {
+  const int64_t m = p.m, n = p.n, k = p.k;
   if (!y || !scale) return ftx::fail(FTX_ERR_INVALID, "null pointer");
   if (reinterpret_cast<uintptr_t>(y) % 2 != 0 || reinterpret_cast<uintptr_t>(scale) % 2 != 0)
     return ftx::fail(FTX_ERR_INVALID, "y and scale need 2-byte alignment");
-  rc = ftx::check_device_range(y, static_cast<size_t>(m * n * 2), "fp8 linear output");
+  int rc = ftx::check_device_range(y, static_cast<size_t>(m * n * 2), "fp8 linear output");
   if (rc == FTX_OK) rc = ftx::check_device_range(scale, static_cast<size_t>(n * 2), "fp8 linear scale");
   if (rc != FTX_OK) return rc;
   if (k > 0) {
@@ -705,7 +730,7 @@ int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int
     if (rc == FTX_OK) rc = ftx::check_device_range(w, static_cast<size_t>(n * k), "fp8 linear weight");
     if (rc != FTX_OK) return rc;
   }
-  if (p.workspace_bytes > 0) {
+  if (p.workspace_bytes > 0 && !static_workspace) {
     if (!workspace || workspace_bytes < p.workspace_bytes)
       return ftx::fail(FTX_ERR_INVALID, "fp8 linear needs a workspace of " + std::to_string(p.workspace_bytes) +
                                             " bytes (ftx_fp8_linear_workspace)");
@@ -721,6 +746,37 @@ int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int
   p.workspace = workspace;
   FTX_HIP(ftx::launch_fp8_linear(p, static_cast<hipStream_t>(stream)));
   return FTX_OK;
+}
+
+}  // namespace
+
+int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  ftx::Fp8LinearLaunch p;
+  int rc = plan_fp8(m, n, k, &p);
+  if (rc != FTX_OK) return rc;
+  if (m == 0 || n == 0) return FTX_OK;
+  return run_fp8(p, x, w, scale, y, workspace, workspace_bytes, false, stream);
+}
+
+int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
+                          void *stream) {
+  ftx::Fp8LinearLaunch p;
+  int rc = plan_fp8(m, n, k, &p);
+  if (rc != FTX_OK) return rc;
+  if (m == 0 || n == 0) return FTX_OK;
+  if (p.workspace_bytes > FTX_FP8_STATIC_SCRATCH_BYTES)
+    return ftx::fail(FTX_ERR_UNSUPPORTED,
+                     "fp8 linear of " + std::to_string(m) + " x " + std::to_string(n) + " x " + std::to_string(k) +
+                         " needs " + std::to_string(p.workspace_bytes) + " bytes of split-K partial sums, more than "
+                         "the static scratch's " + std::to_string(FTX_FP8_STATIC_SCRATCH_BYTES) +
+                         " bytes; call ftx_fp8_linear with a workspace instead");
+  void *ws = nullptr;
+  if (p.workspace_bytes > 0) {
+    rc = ftx::static_scratch(&ws);
+    if (rc != FTX_OK) return rc;
+  }
+  return run_fp8(p, x, w, scale, y, ws, p.workspace_bytes, true, stream);
 }
 
 int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes, ftx_scatter_plan **plan) {

@@ -373,6 +373,23 @@ def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> to
     return y
 
 
+def fp8_linear_static(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """``fp8_linear`` into ``out`` (bf16 ``[m, n]``) with no allocation at all, for graph capture and serving
+    loops: the split-K partial sums live in the library's static per-GPU scratch array
+    (``ftx_fp8_linear_static``). Operands must already be contiguous and 16-byte aligned. Calls that may
+    overlap on one GPU share that scratch and must be ordered (one stream)."""
+    m, k = x.shape
+    n = weight.shape[0]
+    if out.shape != (m, n) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bf16 [{m}, {n}] tensor")
+    for name, t in (("x", x), ("weight", weight)):
+        if not t.is_contiguous() or t.data_ptr() % 16:
+            raise ValueError(f"fp8_linear_static needs a contiguous, 16-byte aligned {name}")
+    nat.call("ftx_fp8_linear_static", x.data_ptr(), weight.data_ptr(), scale.data_ptr(), out.data_ptr(), m, n, k,
+             torch.cuda.current_stream(x.device).cuda_stream)
+    return out
+
+
 def set_fp8_linear_config(waves: int = 0, slice_k: int = 0) -> None:
     """Fix the fp8 linear launch shape: wavefronts per workgroup and K values
     per workgroup (0 = chosen per call from the shape)."""

@@ -191,6 +191,23 @@ int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int
                    void *workspace, size_t workspace_bytes, void *stream);
 int ftx_set_fp8_linear_config(int waves, int slice_k);
 
+/* Bytes of the static scratch array behind ftx_fp8_linear_static (64 MiB per GPU). */
+#define FTX_FP8_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ftx_fp8_linear with its split-K partial sums in a static
+ * device array of FTX_FP8_STATIC_SCRATCH_BYTES that each GPU the library runs
+ * on holds until the process ends. Same operands, results and launch shape as
+ * ftx_fp8_linear; allocates nothing (no hipMalloc, hipFree or allocating
+ * library call). Returns FTX_ERR_UNSUPPORTED, before touching any operand,
+ * when the call's partial sums (ftx_fp8_linear_workspace) exceed the array.
+ * Every call on one GPU shares that GPU's array: calls that may overlap on one
+ * GPU (unordered streams, other host threads) race and must be ordered, e.g.
+ * on one stream. Every partial sum a call reads is written by that call
+ * first, so nothing needs clearing between calls. */
+int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
+                          void *stream);
+
 /* ---- checksums (size-independent parity checks on device data) ----------- */
 /* Order-sensitive 64-bit checksum of nbytes at dev (FNV-1a over 8-byte lanes,
  * folded per 4 KiB block); result written to *out after stream sync. */
