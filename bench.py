@@ -421,17 +421,20 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
     return out
 
 
-def bench_fp8_linear(batch: int = 8, reps: int = 40) -> dict:
-    """HBM roofline of the fp8-weight MFMA linear on the 70B-shape decode projections.
+def bench_fp8_linear(batch: int = 8, reps: int = 20) -> dict:
+    """HBM roofline of the fp8-weight MFMA linear on one 70B-shape decoder layer's projections.
 
-    One call per projection of a decoder layer (q, k, v, o, gate, up, down) at
-    ``batch`` activation rows. Algorithmic bytes per call = fp8 weights (n*k) +
-    bf16 activations (m*k*2) + bf16 outputs (m*n*2) + bf16 scales (n*2). The
-    time is GPU time per call: ``reps`` calls are captured in one HIP graph
-    and one replay is timed with HIP events on the replay stream, so host
-    overhead is excluded; a call is the main kernel plus, when K is split, the
-    reduce kernel. The dequantize-then-bf16-GEMM forward it replaces is timed
-    beside it (eager, same events).
+    Every projection has its own weights (858 MB per layer, more than the
+    256 MB Infinity Cache, so no call finds the previous call's weights
+    cached). The layer runs as the decoder runs it: grouped calls for q/k/v
+    and for gate/up, single calls for o and down, each the main kernel plus,
+    when K is split, one reduce launch. Algorithmic bytes per call = fp8
+    weights (n*k) + bf16 activations (m*k*2) + bf16 outputs (m*n*2) + bf16
+    scales (n*2). GPU time: ``reps`` layers captured in one HIP graph (two
+    layers' weights alternated), one replay timed with HIP events on the
+    replay stream, so host overhead is excluded. Each call is also timed the
+    same way on its own. One call per projection (no grouping) and the
+    dequantize-then-GEMM forward are timed beside them.
     """
     import torch
     import torch.nn.functional as F
@@ -445,68 +448,94 @@ def bench_fp8_linear(batch: int = 8, reps: int = 40) -> dict:
                    ("down", h, it)]
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(3)
+    n_layers = 2  # two layers' weights, alternated, so consecutive layers never share a weight byte
+    layers = []
+    for _ in range(n_layers):
+        layer = {}
+        for name, n, k in projections:
+            w = (torch.randn(n, k, device=dev, generator=gen) * 64).clamp(-448, 448).to(torch.float8_e4m3fn)
+            sc = (torch.rand(n, device=dev, generator=gen) / 448).to(torch.bfloat16)
+            layer[name] = (w, sc)
+        layers.append(layer)
+    xs = {k: torch.randn(batch, k, device=dev, generator=gen).to(torch.bfloat16) for k in (h, it)}
+    calls = [("qkv", ("wq", "wk", "wv"), h), ("o", ("wo",), q), ("gate+up", ("gate", "up"), h), ("down", ("down",), it)]
 
-    def timed_eager(fn, n):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(n):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / n
+    def run_call(layer, names, k):
+        if len(names) == 1:
+            w, sc = layer[names[0]]
+            return [hip.fp8_linear(xs[k], w, sc)]
+        return hip.fp8_linear_group(xs[k], [layer[nm][0] for nm in names], [layer[nm][1] for nm in names])
 
-    def timed_graph(fn, n):
+    def graph_ms(fn, n):
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            fn()
+            fn(0)
             torch.cuda.synchronize()
             with torch.cuda.graph(graph, stream=side):
-                for _ in range(n):
-                    fn()
+                for i in range(n):
+                    fn(i)
         torch.cuda.current_stream().wait_stream(side)
         graph.replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        graph.replay()
-        b.record()
+        with torch.cuda.stream(side):
+            a.record(side)
+            graph.replay()
+            b.record(side)
         torch.cuda.synchronize()
+        del graph
         return a.elapsed_time(b) / n
 
-    rows, cache = [], {}
-    total_bytes = total_ms = total_dq_ms = 0.0
-    for name, n, k in projections:
-        if (n, k) not in cache:
-            x = torch.randn(batch, k, device=dev, generator=gen).to(torch.bfloat16)
-            w = (torch.randn(n, k, device=dev, generator=gen) * 64).clamp(-448, 448).to(torch.float8_e4m3fn)
-            sc = (torch.rand(n, device=dev, generator=gen) / 448).to(torch.bfloat16)
-            ms = timed_graph(lambda: hip.fp8_linear(x, w, sc), reps)
-            eager_ms = timed_eager(lambda: hip.fp8_linear(x, w, sc), reps)
-            dq_ms = timed_eager(lambda: F.linear(x, w.to(torch.bfloat16)) * sc, max(5, reps // 5))
-            want = (x.float() @ w.float().t()) * sc.float()
-            err = float((hip.fp8_linear(x, w, sc).float() - want).norm() / want.norm())
-            splits = hip.fp8_linear_workspace_bytes(batch, n, k) // (4 * batch * n) or 1
-            cache[(n, k)] = (ms, eager_ms, dq_ms, err, splits)
-            del x, w, sc, want
-        ms, eager_ms, dq_ms, err, splits = cache[(n, k)]
-        nbytes = n * k + batch * k * 2 + batch * n * 2 + n * 2
-        total_bytes += nbytes
-        total_ms += ms
-        total_dq_ms += dq_ms
-        rows.append({"proj": name, "n": n, "k": k, "k_slices": splits, "us": round(ms * 1e3, 2),
-                     "GBps": round(nbytes / ms / 1e6, 1), "eager_call_us": round(eager_ms * 1e3, 2),
-                     "dequant_gemm_us": round(dq_ms * 1e3, 2), "rel_err_vs_fp32": round(err, 5)})
-    achieved = total_bytes / total_ms / 1e6
-    return {"batch": batch, "projections": rows, "layer_us": round(total_ms * 1e3, 2),
-            "layer_dequant_gemm_us": round(total_dq_ms * 1e3, 2), "timing": "HIP graph of calls, one replay",
-            "roofline": {"kernel": "fp8_linear_kernel + fp8_linear_reduce_kernel", "bound": "hbm",
-                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_layer": int(total_bytes)}}
+    rows = {name: n for name, n, _ in projections}
+
+    def nbytes(names, k):
+        return sum(rows[nm] * k + batch * rows[nm] * 2 + rows[nm] * 2 for nm in names) + batch * k * 2
+
+    layer_bytes = sum(nbytes(names, k) for _, names, k in calls)
+    layer_ms = graph_ms(lambda i: [run_call(layers[i % n_layers], names, k) for _, names, k in calls], reps)
+    per_call = []
+    for label, names, k in calls:
+        ms = graph_ms(lambda i, names=names, k=k: run_call(layers[i % n_layers], names, k), reps)
+        nb = nbytes(names, k)
+        ws = hip.fp8_linear_group_workspace_bytes(batch, [rows[nm] for nm in names], k)
+        per_call.append({"call": label, "matrices": list(names), "k": k, "us": round(ms * 1e3, 2),
+                         "GBps": round(nb / ms / 1e6, 1), "algorithmic_bytes": nb,
+                         "k_slices": ws // (4 * batch * sum(rows[nm] for nm in names)) or 1})
+    ungrouped_ms = graph_ms(lambda i: [hip.fp8_linear(xs[k], *layers[i % n_layers][nm]) for nm, _, k in projections], reps)
+    # accuracy of every output against float32, and the dequantize-then-GEMM forward it replaces
+    errs = {}
+    dq_ms = 0.0
+    for label, names, k in calls:
+        outs = run_call(layers[0], names, k)
+        for nm, y in zip(names, outs):
+            w, sc = layers[0][nm]
+            want = (xs[k].float() @ w.float().t()) * sc.float()
+            errs[nm] = round(float((y.float() - want).norm() / want.norm()), 5)
+            del want
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            F.linear(xs[k], w.to(torch.bfloat16)) * sc
+            a.record()
+            for _ in range(3):
+                F.linear(xs[k], w.to(torch.bfloat16)) * sc
+            b.record()
+            torch.cuda.synchronize()
+            dq_ms += a.elapsed_time(b) / 3
+    big = max(per_call, key=lambda c: c["algorithmic_bytes"])
+    achieved = layer_bytes / layer_ms / 1e6
+    del layers
+    torch.cuda.empty_cache()
+    return {"batch": batch, "calls": per_call, "layer_us": round(layer_ms * 1e3, 2),
+            "layer_ungrouped_us": round(ungrouped_ms * 1e3, 2), "layer_dequant_gemm_us": round(dq_ms * 1e3, 2),
+            "rel_err_vs_fp32": errs, "timing": f"HIP graph of {reps} layers (two layers' weights alternated), one replay",
+            "roofline": {"kernel": "fp8_linear_kernel + fp8_linear_reduce_kernel (grouped q/k/v and gate/up)",
+                         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "algorithmic_bytes_per_layer": int(layer_bytes),
+                         "per": "decoder layer (4 calls)"},
+            "roofline_largest_call": {"call": big["call"], "achieved": big["GBps"], "peak": HBM_PEAK_GBPS,
+                                      "unit": "GB/s", "frac": round(big["GBps"] / HBM_PEAK_GBPS, 4)}}
 
 
 def staged_sweep(repeats: int = 5) -> dict:

@@ -45,26 +45,32 @@ struct ScatterPlanDev {
 };
 
 // One launch of the fp8-weight linear kernel (ftx_gemm.hip), as planned by
-// plan_fp8_linear from the shape, the CU count and optional overrides.
+// plan_fp8_linear from the shapes, the CU count and optional overrides. A
+// launch covers `group` weight matrices (segments) that share the input x and
+// k: y_s = bf16(scale_s * x @ w_s^T) for each segment s.
+constexpr int kFp8MaxGroup = 4;
 struct Fp8LinearLaunch {
-  const void *x;      // bf16 [m, k]
-  const void *w;      // e4m3fn [n, k]
-  const void *scale;  // bf16 [n]
-  void *y;            // bf16 [m, n]
-  void *workspace;    // fp32 [splits, m, n] partial sums when splits > 1
-  int64_t m, n, k;
+  const void *x;                       // bf16 [m, k]
+  int group;                           // segments in this launch, 1..kFp8MaxGroup
+  const void *w[kFp8MaxGroup];         // e4m3fn [n_s, k]
+  const void *scale[kFp8MaxGroup];     // bf16 [n_s]
+  void *y[kFp8MaxGroup];               // bf16 [m, n_s]
+  int64_t n[kFp8MaxGroup];             // output rows of each segment
+  int64_t n_total;                     // sum of n
+  void *workspace;    // fp32 partial sums [splits, m, n_s] per segment, back to back, when splits > 1
+  int64_t m, k;
   int batch_blocks;   // 16-column batch blocks: 1, 2 or 4 (m <= 16 * batch_blocks)
   int waves;          // wavefronts per workgroup, 16 output rows each
   int splits;         // K slices, one workgroup each per row group
   int64_t kc;         // K values per slice (multiple of 256)
-  int64_t row_groups; // groups of 16 * waves output rows
+  int64_t row_groups; // groups of 16 * waves output rows, summed over segments
   int64_t grid;       // workgroups = row_groups * splits
   size_t lds_bytes;   // activation slice + one weight tile per wave
   size_t workspace_bytes;
 };
 constexpr int kFp8LinearMaxRows = 64;
 constexpr size_t kFp8LinearMaxLds = 64 * 1024;
-Fp8LinearLaunch plan_fp8_linear(int64_t m, int64_t n, int64_t k, int cus, int waves, int kc);
+Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int waves, int kc);
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream);
 
 // Staged copies from pageable host memory and the parallel host memcpy

@@ -671,15 +671,28 @@ int ftx_set_fp8_linear_config(int waves, int slice_k) {
 
 namespace {
 
-int plan_fp8(int64_t m, int64_t n, int64_t k, ftx::Fp8LinearLaunch *p) {
-  if (m < 0 || n < 0 || k < 0) return ftx::fail(FTX_ERR_INVALID, "negative dimension");
+int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLaunch *p) {
+  if (group < 1 || group > ftx::kFp8MaxGroup)
+    return ftx::fail(FTX_ERR_INVALID, "a grouped fp8 linear takes 1 to " + std::to_string(ftx::kFp8MaxGroup) +
+                                          " weight matrices");
+  if (!n) return ftx::fail(FTX_ERR_INVALID, "n is null");
+  int64_t n_total = 0;
+  for (int s = 0; s < group; ++s) {
+    if (n[s] < 0) return ftx::fail(FTX_ERR_INVALID, "negative dimension");
+    if (n[s] > (int64_t(1) << 30)) return ftx::fail(FTX_ERR_INVALID, "fp8 linear dimensions too large");
+    n_total += n[s];
+  }
+  if (m < 0 || k < 0) return ftx::fail(FTX_ERR_INVALID, "negative dimension");
   if (m > ftx::kFp8LinearMaxRows)
     return ftx::fail(FTX_ERR_UNSUPPORTED, "fp8 linear takes at most 64 activation rows");
   if (k % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "k must be a multiple of 16");
-  if (n > (int64_t(1) << 30) || k > (int64_t(1) << 30) || m * n > (int64_t(1) << 31))
+  if (n_total > (int64_t(1) << 30) || k > (int64_t(1) << 30) || m * n_total > (int64_t(1) << 31))
     return ftx::fail(FTX_ERR_INVALID, "fp8 linear dimensions too large");
-  if (m == 0 || n == 0) {
+  if (m == 0 || n_total == 0) {
     *p = ftx::Fp8LinearLaunch{};
+    p->group = group;
+    p->m = m;
+    p->k = k;
     return FTX_OK;
   }
   int waves, slice_k;
@@ -693,7 +706,7 @@ int plan_fp8(int64_t m, int64_t n, int64_t k, ftx::Fp8LinearLaunch *p) {
     ftx::DeviceState *st = nullptr;
     if (ftx::device_state(&st) == FTX_OK) cus = st->cu_count;
   }
-  *p = ftx::plan_fp8_linear(m, n, k, cus, waves, slice_k);
+  *p = ftx::plan_fp8_linear(m, n, group, k, cus, waves, slice_k);
   if (p->grid > (int64_t(1) << 31) - 1) return ftx::fail(FTX_ERR_INVALID, "fp8 linear grid too large");
   return FTX_OK;
 }
@@ -701,9 +714,13 @@ int plan_fp8(int64_t m, int64_t n, int64_t k, ftx::Fp8LinearLaunch *p) {
 }  // namespace
 
 int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes) {
+  return ftx_fp8_linear_group_workspace(m, &n, 1, k, bytes);
+}
+
+int ftx_fp8_linear_group_workspace(int64_t m, const int64_t *n, int group, int64_t k, size_t *bytes) {
   if (!bytes) return ftx::fail(FTX_ERR_INVALID, "bytes is null");
   ftx::Fp8LinearLaunch p;
-  int rc = plan_fp8(m, n, k, &p);
+  int rc = plan_fp8(m, n, group, k, &p);
   if (rc != FTX_OK) return rc;
   *bytes = p.workspace_bytes;
   return FTX_OK;
@@ -711,23 +728,36 @@ int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes) {
 
 namespace {
 
-// Checks the operands of one planned fp8 linear call and launches it. The
+// Checks the operands of one planned fp8 linear launch and launches it. The
 // workspace is checked against its allocation unless it is the static scratch.
-int run_fp8(ftx::Fp8LinearLaunch &p, const void *x, const void *w, const void *scale, void *y, void *workspace,
-            size_t workspace_bytes, bool static_workspace, void *stream) {
-  const int64_t m = p.m, n = p.n, k = p.k;
-  if (!y || !scale) return ftx::fail(FTX_ERR_INVALID, "null pointer");
-  if (reinterpret_cast<uintptr_t>(y) % 2 != 0 || reinterpret_cast<uintptr_t>(scale) % 2 != 0)
-    return ftx::fail(FTX_ERR_INVALID, "y and scale need 2-byte alignment");
-  int rc = ftx::check_device_range(y, static_cast<size_t>(m * n * 2), "fp8 linear output");
-  if (rc == FTX_OK) rc = ftx::check_device_range(scale, static_cast<size_t>(n * 2), "fp8 linear scale");
-  if (rc != FTX_OK) return rc;
+int run_fp8(ftx::Fp8LinearLaunch &p, const void *x, const void *const *w, const void *const *scale, void *const *y,
+            void *workspace, size_t workspace_bytes, bool static_workspace, void *stream) {
+  const int64_t m = p.m, k = p.k;
+  if (!w || !scale || !y) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  for (int s = 0; s < p.group; ++s) {
+    const int64_t n = p.n[s];
+    if (n == 0) continue;
+    if (!y[s] || !scale[s]) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+    if (reinterpret_cast<uintptr_t>(y[s]) % 2 != 0 || reinterpret_cast<uintptr_t>(scale[s]) % 2 != 0)
+      return ftx::fail(FTX_ERR_INVALID, "y and scale need 2-byte alignment");
+    int rc = ftx::check_device_range(y[s], static_cast<size_t>(m * n * 2), "fp8 linear output");
+    if (rc == FTX_OK) rc = ftx::check_device_range(scale[s], static_cast<size_t>(n * 2), "fp8 linear scale");
+    if (rc != FTX_OK) return rc;
+    if (k > 0) {
+      if (!w[s]) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+      if (reinterpret_cast<uintptr_t>(w[s]) % 16 != 0)
+        return ftx::fail(FTX_ERR_INVALID, "x and w need 16-byte alignment");
+      rc = ftx::check_device_range(w[s], static_cast<size_t>(n * k), "fp8 linear weight");
+      if (rc != FTX_OK) return rc;
+    }
+    p.w[s] = w[s];
+    p.scale[s] = scale[s];
+    p.y[s] = y[s];
+  }
   if (k > 0) {
-    if (!x || !w) return ftx::fail(FTX_ERR_INVALID, "null pointer");
-    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
-      return ftx::fail(FTX_ERR_INVALID, "x and w need 16-byte alignment");
-    rc = ftx::check_device_range(x, static_cast<size_t>(m * k * 2), "fp8 linear input");
-    if (rc == FTX_OK) rc = ftx::check_device_range(w, static_cast<size_t>(n * k), "fp8 linear weight");
+    if (!x) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "x and w need 16-byte alignment");
+    int rc = ftx::check_device_range(x, static_cast<size_t>(m * k * 2), "fp8 linear input");
     if (rc != FTX_OK) return rc;
   }
   if (p.workspace_bytes > 0 && !static_workspace) {
@@ -736,13 +766,10 @@ int run_fp8(ftx::Fp8LinearLaunch &p, const void *x, const void *w, const void *s
                                             " bytes (ftx_fp8_linear_workspace)");
     if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
       return ftx::fail(FTX_ERR_INVALID, "workspace needs 16-byte alignment");
-    rc = ftx::check_device_range(workspace, p.workspace_bytes, "fp8 linear workspace");
+    int rc = ftx::check_device_range(workspace, p.workspace_bytes, "fp8 linear workspace");
     if (rc != FTX_OK) return rc;
   }
   p.x = x;
-  p.w = w;
-  p.scale = scale;
-  p.y = y;
   p.workspace = workspace;
   FTX_HIP(ftx::launch_fp8_linear(p, static_cast<hipStream_t>(stream)));
   return FTX_OK;
@@ -752,17 +779,23 @@ int run_fp8(ftx::Fp8LinearLaunch &p, const void *x, const void *w, const void *s
 
 int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
                    void *workspace, size_t workspace_bytes, void *stream) {
+  return ftx_fp8_linear_group(x, 1, &w, &scale, &y, &n, m, k, workspace, workspace_bytes, stream);
+}
+
+int ftx_fp8_linear_group(const void *x, int group, const void *const *w, const void *const *scale, void *const *y,
+                         const int64_t *n, int64_t m, int64_t k, void *workspace, size_t workspace_bytes,
+                         void *stream) {
   ftx::Fp8LinearLaunch p;
-  int rc = plan_fp8(m, n, k, &p);
+  int rc = plan_fp8(m, n, group, k, &p);
   if (rc != FTX_OK) return rc;
-  if (m == 0 || n == 0) return FTX_OK;
+  if (m == 0 || p.n_total == 0) return FTX_OK;
   return run_fp8(p, x, w, scale, y, workspace, workspace_bytes, false, stream);
 }
 
 int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
                           void *stream) {
   ftx::Fp8LinearLaunch p;
-  int rc = plan_fp8(m, n, k, &p);
+  int rc = plan_fp8(m, &n, 1, k, &p);
   if (rc != FTX_OK) return rc;
   if (m == 0 || n == 0) return FTX_OK;
   if (p.workspace_bytes > FTX_FP8_STATIC_SCRATCH_BYTES)
@@ -776,7 +809,7 @@ int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void 
     rc = ftx::static_scratch(&ws);
     if (rc != FTX_OK) return rc;
   }
-  return run_fp8(p, x, w, scale, y, ws, p.workspace_bytes, true, stream);
+  return run_fp8(p, x, &w, &scale, &y, ws, p.workspace_bytes, true, stream);
 }
 
 int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes, ftx_scatter_plan **plan) {

@@ -325,7 +325,7 @@ def checksum(t: torch.Tensor, stream: HipStream | None = None) -> int:
 
 
 FP8_LINEAR_MAX_ROWS = 64
-_FP8_WORKSPACE: dict[tuple[int, int, int], int] = {}
+_FP8_WORKSPACE: dict[tuple, int] = {}
 
 
 def fp8_linear_workspace_bytes(m: int, n: int, k: int) -> int:
@@ -371,6 +371,52 @@ def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> to
     nat.call("ftx_fp8_linear", x.data_ptr(), weight.data_ptr(), scale.data_ptr(), y.data_ptr(), m, n, k,
              ws.data_ptr() if ws is not None else None, ws_bytes, torch.cuda.current_stream(x.device).cuda_stream)
     return y
+
+
+def fp8_linear_group_workspace_bytes(m: int, ns: list[int], k: int) -> int:
+    """Bytes of device workspace one ``fp8_linear_group`` call of these shapes needs (cached per shape)."""
+    key = ("group", m, k) + tuple(ns)  # distinct from the (m, n, k) keys of single calls
+    got = _FP8_WORKSPACE.get(key)
+    if got is None:
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        b = ctypes.c_size_t(0)
+        nat.call("ftx_fp8_linear_group_workspace", m, ctypes.cast(arr, ctypes.c_void_p), len(ns), k, ctypes.byref(b))
+        got = _FP8_WORKSPACE[key] = int(b.value)
+    return got
+
+
+def fp8_linear_group(x: torch.Tensor, weights: list[torch.Tensor], scales: list[torch.Tensor]) -> list[torch.Tensor]:
+    """``[fp8_linear(x, w, s) for w, s in zip(weights, scales)]`` in one launch (``ftx_fp8_linear_group``).
+
+    For up to four weight matrices that share ``x`` and ``k`` (a layer's q/k/v or gate/up projections): the
+    group pays one kernel launch, and one reduce launch when K is split, instead of one of each per matrix.
+    Each output equals the single call's to within fp32 rounding (the group may split K differently).
+    """
+    if not 1 <= len(weights) <= 4 or len(weights) != len(scales):
+        raise ValueError("fp8_linear_group takes 1 to 4 weights with one scale each")
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or not x.is_cuda:
+        raise ValueError("fp8_linear_group needs a bf16 GPU x [m, k]")
+    m, k = x.shape
+    for w, sc in zip(weights, scales):
+        if w.dtype != torch.float8_e4m3fn or w.dim() != 2 or w.shape[1] != k or w.device != x.device:
+            raise ValueError(f"every weight must be float8_e4m3fn [n, {k}] on {x.device}")
+        if not w.is_contiguous() or w.data_ptr() % 16:
+            raise ValueError("fp8_linear_group needs contiguous, 16-byte aligned weights")
+        if sc.dtype != torch.bfloat16 or sc.shape != (w.shape[0],) or sc.device != x.device:
+            raise ValueError("every scale must be bf16 [n] on the input's device")
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        x = x.clone(memory_format=torch.contiguous_format)
+    scales = [sc if sc.is_contiguous() else sc.contiguous() for sc in scales]
+    g = len(weights)
+    ns = (ctypes.c_int64 * g)(*[w.shape[0] for w in weights])
+    outs = [torch.empty((m, w.shape[0]), dtype=torch.bfloat16, device=x.device) for w in weights]
+    ws_bytes = fp8_linear_group_workspace_bytes(m, list(ns), k)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    ptrs = [(ctypes.c_void_p * g)(*[t.data_ptr() for t in ts]) for ts in (weights, scales, outs)]
+    nat.call("ftx_fp8_linear_group", x.data_ptr(), g, *(ctypes.cast(a, ctypes.c_void_p) for a in ptrs),
+             ctypes.cast(ns, ctypes.c_void_p), m, k, ws.data_ptr() if ws is not None else None, ws_bytes,
+             torch.cuda.current_stream(x.device).cuda_stream)
+    return outs
 
 
 def fp8_linear_static(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, out: torch.Tensor) -> torch.Tensor:

@@ -125,7 +125,8 @@ class Fp8Linear(nn.Module):
 
     On the GPU, decode-sized inputs (at most 64 rows, K a multiple of 16) run
     the library's fp8-weight MFMA kernel, which reads each fp8 weight once and
-    widens it to bf16 in registers. Larger inputs (prefill) and CPU inputs
+    widens it to bf16 in registers; the decoder groups its q/k/v and gate/up
+    projections into one launch each (:func:`fp8_group`). Larger inputs (prefill) and CPU inputs
     dequantise to bf16 and run a bf16 GEMM. Every e4m3 value is exactly
     representable in bf16, so both compute the same products; they differ in
     accumulation order and in rounding the product before the scale.
@@ -154,6 +155,17 @@ class Fp8Linear(nn.Module):
             return y.view(*x.shape[:-1], y.shape[-1])
         w = self.weight.to(torch.bfloat16)
         return F.linear(x, w) * self.scale
+
+
+def fp8_group(x: torch.Tensor, layers: list[nn.Module]) -> list[torch.Tensor] | None:
+    """The outputs of several ``Fp8Linear`` layers on one input in one grouped kernel launch, or None when
+    any of them would not take the kernel (the caller then runs them one by one)."""
+    if not all(isinstance(lin, Fp8Linear) and lin.kernel_eligible(x) for lin in layers):
+        return None
+    k = x.shape[-1]
+    ys = hip.fp8_linear_group(x.reshape(x.numel() // k, k), [lin.weight for lin in layers],
+                              [lin.scale for lin in layers])
+    return [y.view(*x.shape[:-1], y.shape[-1]) for y in ys]
 
 
 def _proj(s: LlamaShape, n_in: int, n_out: int, dtype: torch.dtype) -> nn.Module:
@@ -192,9 +204,11 @@ class Attention(nn.Module):
                 cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
         s = self.s
         b, t, _ = x.shape
-        q = self.wq(x).view(b, t, s.n_heads, s.head_dim)
-        k = self.wk(x).view(b, t, s.n_kv_heads, s.head_dim)
-        v = self.wv(x).view(b, t, s.n_kv_heads, s.head_dim)
+        qkv = fp8_group(x, [self.wq, self.wk, self.wv])
+        q, k, v = qkv if qkv is not None else (self.wq(x), self.wk(x), self.wv(x))
+        q = q.view(b, t, s.n_heads, s.head_dim)
+        k = k.view(b, t, s.n_kv_heads, s.head_dim)
+        v = v.view(b, t, s.n_kv_heads, s.head_dim)
         c = cos[pos: pos + t].view(1, t, 1, -1).to(q.dtype)
         sn = sin[pos: pos + t].view(1, t, 1, -1).to(q.dtype)
         q, k = _rotate(q, c, sn), _rotate(k, c, sn)
@@ -233,7 +247,9 @@ class DecoderLayer(nn.Module):
                 cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
         x = x + self.attn(self.attn_norm(x), pos, cos, sin, cache_k, cache_v)
         h = self.mlp_norm(x)
-        return x + self.down(F.silu(self.gate(h)) * self.up(h))
+        gu = fp8_group(h, [self.gate, self.up])
+        g, u = gu if gu is not None else (self.gate(h), self.up(h))
+        return x + self.down(F.silu(g) * u)
 
 
 class LlamaModel(nn.Module):

@@ -190,6 +190,17 @@ int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes);
 int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
                    void *workspace, size_t workspace_bytes, void *stream);
 int ftx_set_fp8_linear_config(int waves, int slice_k);
+/* Grouped form: `group` (1..4) weight matrices w[s] [n[s], k] with scales
+ * scale[s] and outputs y[s] [m, n[s]] that share the input x, in one launch
+ * (one reduce launch when K is split): a layer's q/k/v projections, or its
+ * gate/up projections. Each y[s] equals what ftx_fp8_linear computes for that
+ * matrix to within fp32 rounding (the K split may differ); results are
+ * deterministic for a given group. Workspace sizes from
+ * ftx_fp8_linear_group_workspace. */
+int ftx_fp8_linear_group_workspace(int64_t m, const int64_t *n, int group, int64_t k, size_t *bytes);
+int ftx_fp8_linear_group(const void *x, int group, const void *const *w, const void *const *scale, void *const *y,
+                         const int64_t *n, int64_t m, int64_t k, void *workspace, size_t workspace_bytes,
+                         void *stream);
 
 /* Bytes of the static scratch array behind ftx_fp8_linear_static (64 MiB per GPU). */
 #define FTX_FP8_STATIC_SCRATCH_BYTES ((size_t)64 << 20)

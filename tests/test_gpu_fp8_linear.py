@@ -315,3 +315,106 @@ def test_empty_shapes(gpu, default_config, m, n, k):
     torch.cuda.synchronize()
     assert y.shape == (m, n)
     assert bool((y == 0).all())
+
+
+# ---- grouped launches (ftx_fp8_linear_group) --------------------------------------------------------
+
+
+_GROUPS = [((96, 40, 1040), 2), ((8192, 1024, 1024), 8), ((640, 640), 8), ((300, 0, 17, 64), 5)]
+
+
+@pytest.mark.parametrize("waves,slice_k", [(0, 0), (4, 256), (8, 768)])
+@pytest.mark.parametrize("ns,m", _GROUPS)
+def test_group_exact_products_bit_exact(gpu, default_config, ns, m, waves, slice_k):
+    """Every matrix of a group matches the oracle bit for bit on exact-arithmetic data, for several launch
+    shapes (one slice, split K), with empty matrices and row counts that are not multiples of 16."""
+    from flextensor_amd import hip
+
+    k = 1024
+    hip.set_fp8_linear_config(waves, slice_k)
+    cases = [_exact_case(m, n, k, seed=n + i) for i, n in enumerate(ns)]
+    xt = _to_device(cases[0][0], cases[0][1], cases[0][2], gpu)[0]
+    dev = [_to_device(cases[0][0], w_raw, scale, gpu)[1:] for _, w_raw, scale in cases]
+    outs = hip.fp8_linear_group(xt, [d[0] for d in dev], [d[1] for d in dev])
+    torch.cuda.synchronize()
+    for (_, w_raw, scale), out, n in zip(cases, outs, ns):
+        assert out.shape == (m, n)
+        want = torch.from_numpy(ofp8.fp8_linear(cases[0][0], w_raw, scale)).to(torch.bfloat16)
+        assert _same_values(out, want)
+
+
+@pytest.mark.parametrize("ns", [(8192, 1024, 1024), (28672, 28672)])
+def test_group_70b_projections_match_float64_oracle(gpu, default_config, ns):
+    """The 70B layer's grouped q/k/v and gate/up calls at 8 rows, against the float64 oracle."""
+    from flextensor_amd import hip
+
+    m, k = 8, 8192
+    cases = [_random_case(m, n, k, seed=n + i) for i, n in enumerate(ns)]
+    xt = _to_device(*cases[0], gpu)[0]
+    dev = [_to_device(cases[0][0], w_raw, scale, gpu)[1:] for _, w_raw, scale in cases]
+    outs = hip.fp8_linear_group(xt, [d[0] for d in dev], [d[1] for d in dev])
+    again = hip.fp8_linear_group(xt, [d[0] for d in dev], [d[1] for d in dev])
+    singles = [hip.fp8_linear(xt, w, s) for w, s in dev]
+    xs = xt.float().cpu().numpy()
+    for (_, w_raw, _), (_, st), out, out2, one in zip(cases, dev, outs, again, singles):
+        assert torch.equal(out, out2)  # deterministic
+        want = torch.from_numpy(ofp8.fp8_linear(xs, w_raw, st.float().cpu().numpy()))
+        got = out.double().cpu()
+        assert float((got - want).norm() / want.norm()) < REL_TOL
+        bound = ELEM_TOL * torch.maximum(want.abs(), want.pow(2).mean().sqrt())
+        assert bool(((got - want).abs() <= bound).all())
+        # against the single call: the same products, possibly another K split (fp32 rounding only)
+        assert float((got - one.double().cpu()).norm() / want.norm()) < 1e-3
+
+
+def test_group_graph_replays_match_eager(gpu, default_config):
+    from flextensor_amd import hip
+
+    cases = [_random_case(8, n, 4096, seed=n) for n in (2048, 512, 512)]
+    xt = _to_device(*cases[0], gpu)[0]
+    dev = [_to_device(cases[0][0], w_raw, scale, gpu)[1:] for _, w_raw, scale in cases]
+    ws, ss = [d[0] for d in dev], [d[1] for d in dev]
+    eager = hip.fp8_linear_group(xt, ws, ss)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        hip.fp8_linear_group(xt, ws, ss)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            outs = hip.fp8_linear_group(xt, ws, ss)
+    torch.cuda.current_stream().wait_stream(stream)
+    for i in range(3):
+        for o in outs:
+            o.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, e) for o, e in zip(outs, eager)), f"replay {i}"
+        assert all(torch.equal(o, e) for o, e in zip(hip.fp8_linear_group(xt, ws, ss), eager))
+
+
+def test_group_rejects_bad_arguments(gpu, default_config):
+    import ctypes
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _exact_case(8, 32, 64, seed=1)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    with pytest.raises(ValueError):
+        hip.fp8_linear_group(xt, [wt] * 5, [st] * 5)
+    with pytest.raises(ValueError):
+        hip.fp8_linear_group(xt, [wt, wt[:, :48].contiguous()], [st, st])
+    b = ctypes.c_size_t(0)
+    ns = (ctypes.c_int64 * 5)(32, 32, 32, 32, 32)
+    for g in (0, 5):
+        with pytest.raises(nat.FtxError) as err:
+            nat.call("ftx_fp8_linear_group_workspace", 8, ctypes.cast(ns, ctypes.c_void_p), g, 64, ctypes.byref(b))
+        assert err.value.code == nat.FTX_ERR_INVALID
+    y = torch.empty(8, 32, dtype=torch.bfloat16, device=gpu)
+    ptrs = [(ctypes.c_void_p * 2)(t.data_ptr(), 0) for t in (wt, st, y)]  # second matrix: null pointers
+    with pytest.raises(nat.FtxError) as err:
+        nat.call("ftx_fp8_linear_group", xt.data_ptr(), 2, *(ctypes.cast(a, ctypes.c_void_p) for a in ptrs),
+                 ctypes.cast(ns, ctypes.c_void_p), 8, 64, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert err.value.code == nat.FTX_ERR_INVALID and "null" in str(err.value)
