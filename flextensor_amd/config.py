@@ -71,6 +71,10 @@ class OffloadConfig(BaseModel):
     exclude_patterns: list[str] = Field(default_factory=list)
     profile_storage_dir: str | None = None
     copy_engine: Literal["auto", "sdma", "kernel", "staged"] = "auto"
+    # With copy_engine="auto", time both copy engines on this device at the INFERENCE transition and
+    # choose the engine per chunk size from the measured curves (the role of the reference's live
+    # transfer benchmark, memory_transfer_benchmark.py:59-129). False keeps the library's default policy.
+    link_benchmark: bool = True
     loader_order: Literal["auto", "default", "reordered"] = "auto"
     # Before the host enqueues a streamed forward it waits until the forward
     # this many passes back has finished on the device (0: never waits). A host

@@ -11,6 +11,10 @@
   engine of this build (SDMA, SDMA split over copy streams, zero-copy
   kernel) and derive the per-chunk-size choice the library applies under
   ``FTX_COPY_AUTO``.
+* :func:`measure_link` is what the offload manager runs at the INFERENCE
+  transition: both engines over log-spaced sizes up to the largest streamed
+  unit, the policy they choose, and the SDMA curve in the reference's
+  ``{bytes: ms}`` form (its ``memory_transfer_stats``).
 """
 
 from __future__ import annotations
@@ -116,7 +120,7 @@ def time_h2d(nbytes: int, engine: str, repeats: int = 10, warmup: int = 2, devic
     """
     import torch
 
-    from .hip import HipEvent, HostArena, new_stream
+    from .hip import HostArena
 
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
     if device.type != "cuda":
@@ -124,6 +128,18 @@ def time_h2d(nbytes: int, engine: str, repeats: int = 10, warmup: int = 2, devic
     arena = HostArena(nbytes)
     arena.tensor[: min(nbytes, 1 << 20)].fill_(1)
     dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    try:
+        return _time_copies(dst, arena.ptr, nbytes, engine, repeats, warmup, device)
+    finally:
+        del dst
+
+
+def _time_copies(dst, src_ptr: int, nbytes: int, engine: str, repeats: int, warmup: int, device) -> list[float]:
+    """Milliseconds of ``repeats`` copies of ``nbytes`` from pinned ``src_ptr`` into device tensor ``dst``."""
+    from .hip import HipEvent, new_stream
+
+    if nbytes > dst.numel():
+        raise ValueError(f"copy of {nbytes} bytes into a {dst.numel()}-byte buffer")
     stream = new_stream(device, name="link-probe")
     old = nat.get_copy_policy()
     mode = nat.COPY_SDMA
@@ -141,7 +157,7 @@ def time_h2d(nbytes: int, engine: str, repeats: int = 10, warmup: int = 2, devic
         for i in range(warmup + repeats):
             e0, e1 = HipEvent(timing=True), HipEvent(timing=True)
             stream.record_event(e0)
-            nat.copy_h2d(dst.data_ptr(), arena.ptr, nbytes, mode, stream.handle)
+            nat.copy_h2d(dst.data_ptr(), src_ptr, nbytes, mode, stream.handle)
             stream.record_event(e1)
             e1.synchronize()
             if i >= warmup:
@@ -150,7 +166,6 @@ def time_h2d(nbytes: int, engine: str, repeats: int = 10, warmup: int = 2, devic
     finally:
         nat.set_copy_policy(*old)
         stream.synchronize()
-        del dst
 
 
 def measure_copy_curve(engine: str, sizes: list[int], repeats: int = 10, device=None) -> CopyCurve:
@@ -207,3 +222,87 @@ def benchmark_memory_transfers(max_label_bytes: int, device=None, max_depth: int
         times = sorted(time_h2d(n, engine, repeats=10, warmup=5, device=device))
         out[n] = times[len(times) // 2]
     return out
+
+
+LINK_PROBE_MIN_BYTES = 64 << 10
+LINK_PROBE_MAX_BYTES = 256 << 20  # the link's rate has settled well below this; keeps the probe's buffers small
+
+
+def link_probe_sizes(largest_unit_bytes: int) -> list[int]:
+    """Sizes the INFERENCE-transition probe times: 64 KiB, then x4 up to the largest streamed unit (at most
+    256 MiB), that size included. Multiples of 16 bytes, which every copy engine takes."""
+    top = max(LINK_PROBE_MIN_BYTES, min(int(largest_unit_bytes), LINK_PROBE_MAX_BYTES)) // 16 * 16
+    sizes, n = [], LINK_PROBE_MIN_BYTES
+    while n < top:
+        sizes.append(n)
+        n *= 4
+    return sizes + [top]
+
+
+@dataclass
+class LinkMeasurement:
+    """The live copy curves of one device and the ``FTX_COPY_AUTO`` policy chosen from them."""
+
+    sdma: CopyCurve
+    kernel: CopyCurve
+    kernel_max_bytes: int
+    split_min_bytes: int
+    n_copy_streams: int
+    source: str = "measured"  # "measured" at the transition, "profile" when restored from a saved plan
+
+    def memory_transfer_stats(self) -> dict[int, float]:
+        """The SDMA curve as ``{bytes: ms}``, the reference's ``memory_transfer_stats`` form."""
+        return dict(self.sdma.best_ms)
+
+    def policy(self) -> tuple[int, int, int]:
+        return self.kernel_max_bytes, self.split_min_bytes, self.n_copy_streams
+
+    def describe(self) -> str:
+        sd, kn = self.sdma.gbps(), self.kernel.gbps()
+        curve = ", ".join(f"{n >> 10} KiB {sd[n]:.1f}/{kn.get(n, float('nan')):.1f}" for n in sorted(sd))
+        where = (f"zero-copy kernel for chunks up to {self.kernel_max_bytes} bytes, SDMA above"
+                 if self.kernel_max_bytes else "SDMA for every chunk")
+        return f"copy policy ({self.source}): {where}; GB/s SDMA/kernel by size: {curve}"
+
+    def to_dict(self) -> dict:
+        return {"kernel_max_bytes": self.kernel_max_bytes, "split_min_bytes": min(self.split_min_bytes, 2**63 - 1),
+                "n_copy_streams": self.n_copy_streams,
+                "sdma_ms": {str(n): ms for n, ms in sorted(self.sdma.best_ms.items())},
+                "kernel_ms": {str(n): ms for n, ms in sorted(self.kernel.best_ms.items())}}
+
+    @classmethod
+    def from_dict(cls, data: dict, source: str = "profile") -> "LinkMeasurement":
+        try:
+            sdma = CopyCurve("sdma", {int(k): float(v) for k, v in data.get("sdma_ms", {}).items()})
+            kernel = CopyCurve("kernel", {int(k): float(v) for k, v in data.get("kernel_ms", {}).items()})
+            km, sm, ns = int(data["kernel_max_bytes"]), int(data["split_min_bytes"]), int(data["n_copy_streams"])
+        except (KeyError, TypeError, ValueError) as exc:
+            raise ValueError(f"invalid copy_policy in the saved state: {exc}") from exc
+        if km < 0 or sm < 0 or not 1 <= ns <= 8 or any(v <= 0 for v in sdma.best_ms.values()):
+            raise ValueError("invalid copy_policy in the saved state: out-of-range values")
+        return cls(sdma, kernel, km, sm, ns, source)
+
+
+def measure_link(sizes: list[int], device=None, repeats: int = 5, warmup: int = 1) -> LinkMeasurement:
+    """Best-of-``repeats`` host-to-device ms per size for SDMA and for the zero-copy kernel, from one pinned
+    arena into one device buffer of the largest size, and the policy :func:`choose_copy_policy` picks."""
+    import torch
+
+    from .hip import HostArena
+
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    top = max(sizes)
+    arena = HostArena(top)
+    arena.tensor[: min(top, 1 << 20)].fill_(1)
+    dst = torch.empty(top, dtype=torch.uint8, device=device)
+    try:
+        curves = {}
+        for engine in ("sdma", "kernel"):
+            curve = CopyCurve(engine)
+            for n in sizes:
+                curve.best_ms[n] = min(_time_copies(dst, arena.ptr, n, engine, repeats, warmup, device))
+            curves[engine] = curve
+    finally:
+        del dst
+    km, sm, ns = choose_copy_policy(curves["sdma"], curves["kernel"])
+    return LinkMeasurement(curves["sdma"], curves["kernel"], km, sm, ns)

@@ -35,6 +35,7 @@ the pass; slots are added while the slot-reuse check of the reference
 from __future__ import annotations
 
 import contextlib
+import dataclasses
 import logging
 import os
 import threading
@@ -56,6 +57,7 @@ from .allocation_block import HostPinner
 from .config import OffloadConfig
 from .controllers import AllocationBlockController, RawBlockController
 from .layout import overlapping_views
+from .link_model import LinkMeasurement, MemoryTransferInterpolator, link_probe_sizes, measure_link
 from .loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
 from .planner import (
     BlockStrategyData,
@@ -242,26 +244,43 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
 
 
 def state_from_plan(model: nn.Module, units: Sequence[_Unit], plan: StreamPlan, durations: dict[str, float],
-                    loader_type: str) -> TensorManagerState:
+                    loader_type: str, link: LinkMeasurement | None = None) -> TensorManagerState:
     """A plan as a saved state (state_handler.py:501-633): ids are this process's, names tie them to the model.
 
     ``units`` are the offload units in execution order; ``durations`` their
-    profiled seconds.
+    profiled seconds. With ``link`` (the measured host link), every tensor's
+    ``load_time_ms`` is its size on the measured SDMA curve, the reference's
+    per-tensor transfer benchmark (tensor_processors.py:1019-1062) from which a
+    loaded profile rebuilds the curve (collectors.py:33-66), and the chosen
+    copy policy is saved beside the plan.
     """
     id_to_name = {id(p): n for n, p in model.named_parameters()}
     params = {id(p): p for p in model.parameters()}
     bd = plan.block_data
-    streamed = [t for ts in plan.strategy_map.values() for t in ts]
+    interp = MemoryTransferInterpolator(link.memory_transfer_stats()) if link and link.sdma.best_ms else None
+
+    def timed(ts: Sequence[TensorStatistics]) -> list[TensorStatistics]:
+        if interp is None:
+            return list(ts)
+        return [dataclasses.replace(t, load_time_ms=interp.bytes_to_duration(t.size_bytes)) if t.size_bytes else t
+                for t in ts]
+
+    strategy = {k: timed(v) for k, v in plan.strategy_map.items()}
+    streamed = [t for ts in strategy.values() for t in ts]
+    stats = []
+    for u in units:
+        st = u.stats(durations.get(u.label, 0.0))
+        stats.append(dataclasses.replace(st, tensors=timed(st.tensors)))
     return TensorManagerState(
         loader_type=loader_type,
         tensor_id_to_name_map=id_to_name,
         allocation_ordered={b: list(v) for b, v in bd.allocation_ordered.items()} if bd else {},
         label_to_size_map=dict(bd.label_to_size_map) if bd else {},
         block_sizes=dict(bd.block_sizes) if bd else {},
-        load_strategy={k: list(v) for k, v in plan.strategy_map.items()},
+        load_strategy=strategy,
         release_strategy={},
         label_to_block_id=dict(bd.label_to_block_id) if bd else {},
-        stats=[u.stats(durations.get(u.label, 0.0)) for u in units],
+        stats=stats,
         transfer_to_compute_map=dict(bd.transfer_to_compute_map) if bd else {},
         view_tensors_ids=[t.tensor_id for t in streamed],
         view_tensors_names=[t.name for t in streamed],
@@ -269,6 +288,7 @@ def state_from_plan(model: nn.Module, units: Sequence[_Unit], plan: StreamPlan, 
         managed_tensor_dtypes={t.name: str(params[t.tensor_id].dtype).removeprefix("torch.") for t in streamed},
         managed_tensor_layouts={t.name: {"shape": list(params[t.tensor_id].shape),
                                          "stride": list(params[t.tensor_id].stride())} for t in streamed},
+        copy_policy=link.to_dict() if link is not None else None,
     )
 
 
@@ -362,6 +382,7 @@ class OffloadManager:
         self._reload_pending = False
         self._pinner: HostPinner | None = None
         self.memory_transfer_stats: dict[int, float] = {}
+        self.link: LinkMeasurement | None = None  # the measured host link and the copy policy it chose
         self.skip_discovery_honored: bool | None = None  # None until offload() decides
         self._discovery_passes = 0
         self._reset_manual()
@@ -500,6 +521,7 @@ class OffloadManager:
         self._reset_manual()
         self._release_pins()
         self.loader = self.controller = self.plan = self.timing = None
+        self.link = None
         self.model = None
         self.units, self._patched, self._hooks, self.order = [], [], [], []
         self._seen_this_pass, self._pass_done, self._events = [], [], {}
@@ -582,7 +604,7 @@ class OffloadManager:
         """The plan as a :class:`TensorManagerState` keyed by this process's tensor ids."""
         assert self.model is not None and self.plan is not None
         state = state_from_plan(self.model, [self._unit(x) for x in self.order], self.plan,
-                                {x: self._duration(x) for x in self.order}, self.config.transfer_mode)
+                                {x: self._duration(x) for x in self.order}, self.config.transfer_mode, self.link)
         names = getattr(self.controller, "shm_block_name_map", None)
         if names:
             state.shm_block_name_map = dict(names)
@@ -679,6 +701,11 @@ class OffloadManager:
     def eager_profiling_iters(self) -> int:
         """Profiling forwards before INFERENCE, at least 1 (offload_manager.py:731-740)."""
         return max(1, self.config.profiling_iters)
+
+    def get_memory_transfer_stats(self) -> dict[int, float] | None:
+        """The measured host-link curve ``{bytes: ms}`` (SDMA) of the current plan, None before INFERENCE
+        (tensor_manager.py:1632-1639)."""
+        return dict(self.memory_transfer_stats) if self.memory_transfer_stats else None
 
     def benchmark_transfers(self) -> dict[int, float]:
         """Measure host-to-device copy times at the largest unit's size and below
@@ -871,6 +898,7 @@ class OffloadManager:
         self._reload_pending = False
         self.skip_discovery_honored = None
         self.loader = self.controller = self.plan = None
+        self.link = None
         self._pass_done = []
         self.model = None
         self.units, self._patched, self._hooks = [], [], []
@@ -1289,6 +1317,7 @@ class OffloadManager:
             self.loader = _ResidentLoader()
         else:
             bd = plan.block_data
+            self._choose_copy_policy(plan, state)
             tensors_map = {id(p): p for x in plan.streamed for p in self._unit(x).params}
             pinner = self._pinner = HostPinner(cfg.pinned_memory_mode, enabled=cfg.pinned_memory)
             mode = nat.COPY_MODES[cfg.copy_engine]
@@ -1337,6 +1366,35 @@ class OffloadManager:
                     len(plan.resident), self.build_seconds)
         if cfg.enable_diagnostics:
             LOGGER.info("offload %r plan:\n%s", self.name, self.plan_table())
+
+    def _choose_copy_policy(self, plan: StreamPlan, state: TensorManagerState | None) -> None:
+        """Choose the copy engine per chunk size from the measured host link (``FTX_COPY_AUTO``).
+
+        At the INFERENCE transition the reference benchmarks the link live and
+        plans with the curve (tensor_manager.py:1618-1630,
+        memory_transfer_benchmark.py:59-129). Here both copy engines are timed
+        at sizes up to the largest streamed unit; the zero-copy kernel takes
+        the chunk sizes where it is at least 10% faster than SDMA
+        (:func:`~flextensor_amd.link_model.choose_copy_policy`), and the SDMA
+        curve becomes ``memory_transfer_stats``. A plan restored from a saved
+        state reapplies the saved policy without measuring, as the reference
+        rebuilds its curve from the saved statistics. Only ``copy_engine="auto"``
+        consults the policy; ``link_benchmark=False`` keeps the library default.
+        """
+        cfg = self.config
+        link = None
+        if state is not None and state.copy_policy:
+            link = LinkMeasurement.from_dict(state.copy_policy, source="profile")
+        elif cfg.link_benchmark and cfg.copy_engine == "auto" and plan.streamed:
+            largest = max(self._unit(x).nbytes for x in plan.streamed)
+            link = measure_link(link_probe_sizes(largest), self.device)
+        if link is None:
+            return
+        nat.set_copy_policy(link.kernel_max_bytes, link.split_min_bytes, link.n_copy_streams,
+                            nat.get_copy_policy()[3])
+        self.link = link
+        self.memory_transfer_stats = link.memory_transfer_stats()
+        LOGGER.info("offload %r: %s", self.name, link.describe())
 
     def _abort_build(self, primary: BaseException, tensors_map: dict[int, torch.Tensor],
                      bound: dict[int, torch.Tensor], n_hooks: int) -> None:
@@ -1492,6 +1550,8 @@ class OffloadManager:
             else:
                 where = "resident"
             rows.append(f"{label:<32} {u.nbytes / 2**20:>10.2f} {self._duration(label):>9.3f}  {where}")
+        if self.link is not None:
+            rows.append(self.link.describe())
         probe = hip.transfer_stream_probe(self.device) if self.device is not None else None
         if probe is not None:
             rows.append(f"transfer stream: candidate {probe['chosen_candidate']} of {probe['attempts']} "

@@ -63,6 +63,9 @@ class TensorManagerState:
     shm_block_name_map: dict[str, str] | None = None
     managed_tensor_dtypes: dict[str, str] = field(default_factory=dict)
     managed_tensor_layouts: dict[str, dict[str, list[int]]] = field(default_factory=dict)
+    # The copy-engine policy chosen from the measured link when the plan was made (this build's addition:
+    # readers that do not know the key ignore it, as the reference's reader does; None when absent).
+    copy_policy: dict[str, Any] | None = None
 
     # ---- consistency --------------------------------------------------------
 
@@ -168,6 +171,7 @@ class TensorManagerState:
             "shm_block_name_map": self.shm_block_name_map,
             "managed_tensor_dtypes": dict(self.managed_tensor_dtypes),
             "managed_tensor_layouts": {k: dict(v) for k, v in self.managed_tensor_layouts.items()},
+            **({"copy_policy": dict(self.copy_policy)} if self.copy_policy is not None else {}),
         }
 
     @classmethod
@@ -201,6 +205,7 @@ class TensorManagerState:
             shm_block_name_map=data.get("shm_block_name_map"),
             managed_tensor_dtypes=dict(data.get("managed_tensor_dtypes", {})),
             managed_tensor_layouts={k: dict(v) for k, v in data.get("managed_tensor_layouts", {}).items()},
+            copy_policy=dict(data["copy_policy"]) if isinstance(data.get("copy_policy"), dict) else None,
         )
         state.validate_internal()
         return state

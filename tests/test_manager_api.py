@@ -331,7 +331,7 @@ def test_failed_loader_build_restores_sources_and_aborts_the_controller(host_off
     ns = f"ftx_abort_{uuid.uuid4().hex[:8]}"
     extra = {"shm_enabled": True, "shm_namespace": ns} if shm else {}
     mgr = host_offload(f"abort-{shm}", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1,
-                       pinned_memory=False, **extra)
+                       pinned_memory=False, link_benchmark=False, **extra)
     params = [p for u in mgr.units for p in u.params]
     want = [p.detach().clone() for p in params]
     hooks_before = len(mgr._hooks)
@@ -395,3 +395,89 @@ def test_host_register_mode_is_refused_before_anything_moves(names):
     assert info.value.code == nat.FTX_ERR_UNSUPPORTED
     # without pinning the mode has nothing to pin and is accepted
     assert OffloadConfig(pinned_memory=False, pinned_memory_mode="host_register").pinned_memory_mode == "host_register"
+
+
+# ---- the copy policy follows the measured host link (memory_transfer_benchmark.py:59-129) ----------------
+
+
+def _fake_link(kernel_faster_up_to: int):
+    """Curves where the zero-copy kernel beats SDMA by 30% up to ``kernel_faster_up_to`` bytes, then trails."""
+    from flextensor_amd import link_model as L
+
+    sizes = L.link_probe_sizes(1 << 28)
+    sdma = L.CopyCurve("sdma", {n: 0.01 + n / 50e6 for n in sizes})
+    kernel = L.CopyCurve("kernel", {n: (sdma.best_ms[n] / 1.3 if n <= kernel_faster_up_to else sdma.best_ms[n] * 1.02)
+                                    for n in sizes})
+    km, sm, ns = L.choose_copy_policy(sdma, kernel)
+    return L.LinkMeasurement(sdma, kernel, km, sm, ns)
+
+
+@pytest.mark.parametrize("cut", [0, 1 << 18, 1 << 22])
+def test_copy_policy_follows_the_measured_curve(host_offload, cut):
+    from flextensor_amd import link_model as L
+
+    mgr = host_offload(f"link-{cut}", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
+    mgr.order = [u.label for u in mgr.units]
+    plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
+    link = _fake_link(cut)
+    assert link.kernel_max_bytes == cut  # the curve alone decides where the kernel stops paying
+    applied = []
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link) as _, \
+            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)), \
+            mock.patch.object(M.nat, "get_copy_policy", lambda: (1 << 20, 2**63 - 1, 1, 64)):
+        mgr._choose_copy_policy(plan, None)
+    assert applied == [(cut, link.split_min_bytes, 1, 64)]  # the measured policy, the kernel grid kept
+    assert mgr.get_memory_transfer_stats() == link.sdma.best_ms
+    mgr.plan = plan
+    table = mgr.plan_table()
+    assert "copy policy (measured)" in table
+    assert ("zero-copy kernel for chunks up to %d bytes" % cut in table) if cut else ("SDMA for every chunk" in table)
+    # the policy and the per-tensor transfer times travel with the saved plan
+    state = M.state_from_plan(mgr.model, mgr.units, plan, {}, "allocation_block_transfer", mgr.link)
+    assert state.copy_policy == link.to_dict()
+    interp = L.MemoryTransferInterpolator(link.sdma.best_ms)
+    t = state.load_strategy[next(iter(state.load_strategy))][0]
+    assert t.load_time_ms == pytest.approx(interp.bytes_to_duration(t.size_bytes))
+    from flextensor_amd.profile import TensorManagerState
+
+    back = TensorManagerState.from_dict(state.to_dict())
+    assert back.copy_policy == state.copy_policy
+    restored = L.LinkMeasurement.from_dict(back.copy_policy)
+    assert restored.policy() == link.policy() and restored.source == "profile"
+
+
+def test_saved_policy_is_reapplied_without_measuring(host_offload):
+    mgr = host_offload("link-saved", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
+    mgr.order = [u.label for u in mgr.units]
+    plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
+    saved = M.state_from_plan(mgr.model, mgr.units, plan, {}, "allocation_block_transfer", _fake_link(1 << 20))
+    applied = []
+
+    def no_measuring(*a):
+        raise AssertionError("a restored plan must not measure the link")
+
+    with mock.patch.object(M, "measure_link", no_measuring), \
+            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)), \
+            mock.patch.object(M.nat, "get_copy_policy", lambda: (0, 2**63 - 1, 1, 0)):
+        mgr._choose_copy_policy(plan, saved)
+    assert applied and applied[0][0] == 1 << 20 and mgr.link.source == "profile"
+
+
+def test_link_benchmark_off_or_explicit_engine_keeps_the_default(host_offload):
+    for name, cfg in (("link-off", {"link_benchmark": False}), ("link-sdma", {"copy_engine": "sdma"})):
+        mgr = host_offload(name, include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1, **cfg)
+        mgr.order = [u.label for u in mgr.units]
+        plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
+        with mock.patch.object(M, "measure_link", lambda *a: (_ for _ in ()).throw(AssertionError("measured"))), \
+                mock.patch.object(M.nat, "set_copy_policy", lambda *a: (_ for _ in ()).throw(AssertionError("set"))):
+            mgr._choose_copy_policy(plan, None)
+        assert mgr.link is None and mgr.get_memory_transfer_stats() is None
+
+
+def test_invalid_saved_policy_is_refused():
+    from flextensor_amd import link_model as L
+
+    with pytest.raises(ValueError, match="copy_policy"):
+        L.LinkMeasurement.from_dict({"kernel_max_bytes": 1})
+    with pytest.raises(ValueError, match="out-of-range"):
+        L.LinkMeasurement.from_dict({"kernel_max_bytes": 0, "split_min_bytes": 0, "n_copy_streams": 99})
