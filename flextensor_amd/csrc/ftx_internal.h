@@ -88,6 +88,7 @@ hipError_t launch_checksum(const void *dev, size_t nbytes, uint64_t *partials, i
                            hipStream_t stream);
 hipError_t launch_fill_u8(void *dev, uint8_t value, size_t nbytes, hipStream_t stream);
 hipError_t launch_timestamp(uint64_t *slot, hipStream_t stream);
+hipError_t launch_read_probe(const void *dev, size_t nbytes, uint32_t *sink, int grid, hipStream_t stream);
 
 // Host-side helpers shared with the oracle's definition of the checksum.
 inline uint64_t splitmix64(uint64_t x) {

@@ -15,6 +15,8 @@
 //                        capture in a graph).
 //  * timestamp_kernel  - writes the wall clock to device memory; the timing
 //                        points of captured graphs.
+//  * read_probe_kernel - a plain streaming read (measurement only): the HBM
+//                        read rate the HBM-bound kernels are compared with.
 //
 // None of these kernels has data reuse, so blockIdx is mapped linearly: the
 // round-robin dispatch over the 8 XCDs only spreads independent tiles.
@@ -228,6 +230,30 @@ __global__ __launch_bounds__(kThreads) void fill_kernel(uint8_t *__restrict__ p,
   for (uint64_t i = tid; i < n16; i += stride) d[i] = vv;
 }
 
+// Streams n16 16-byte vectors with eight non-temporal loads in flight per
+// lane (grid-stride), folds them into one word and stores it only when it
+// equals `never` (practically never): the loads cannot be optimised away and
+// nothing is written. Measures the plain read rate of HBM.
+constexpr int kReadProbeUnroll = 8;
+__global__ __launch_bounds__(kThreads) void read_probe_kernel(const u32x4 *__restrict__ p, uint64_t n16,
+                                                              uint32_t never, uint32_t *__restrict__ sink) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + (kReadProbeUnroll - 1) * stride < n16; i += kReadProbeUnroll * stride) {
+    u32x4 v[kReadProbeUnroll];
+#pragma unroll
+    for (int j = 0; j < kReadProbeUnroll; ++j) v[j] = __builtin_nontemporal_load(p + i + j * stride);
+#pragma unroll
+    for (int j = 0; j < kReadProbeUnroll; ++j) acc ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 v = __builtin_nontemporal_load(p + i);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (acc == never) sink[0] = acc;
+}
+
 // One lane writes the constant-rate wall clock (a vector store).
 __global__ __launch_bounds__(kWave) void timestamp_kernel(uint64_t *__restrict__ slot) {
   if (threadIdx.x == 0) *as_global<g_u64>(slot) = static_cast<uint64_t>(wall_clock64());
@@ -277,6 +303,12 @@ hipError_t launch_checksum(const void *dev, size_t nbytes, uint64_t *partials, i
   hipLaunchKernelGGL(checksum_kernel, dim3(groups), dim3(kThreads), 0, stream,
                      static_cast<const uint8_t *>(dev), static_cast<uint64_t>(nbytes), n_blocks,
                      partials);
+  return hipGetLastError();
+}
+
+hipError_t launch_read_probe(const void *dev, size_t nbytes, uint32_t *sink, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(read_probe_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream,
+                     static_cast<const u32x4 *>(dev), static_cast<uint64_t>(nbytes / 16), 0x9e3779b9u, sink);
   return hipGetLastError();
 }
 

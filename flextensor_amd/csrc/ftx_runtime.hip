@@ -884,6 +884,20 @@ int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stre
   return FTX_OK;
 }
 
+int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, void *stream) {
+  if (nbytes == 0) return FTX_OK;
+  if (!dev || !sink) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  if (reinterpret_cast<uintptr_t>(dev) % 16 != 0 || nbytes % 16 != 0)
+    return ftx::fail(FTX_ERR_INVALID, "the read probe needs a 16-byte aligned range of whole 16-byte vectors");
+  if (reinterpret_cast<uintptr_t>(sink) % 4 != 0) return ftx::fail(FTX_ERR_INVALID, "sink needs 4-byte alignment");
+  if (grid <= 0 || grid > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "grid must be in [1, 2^20]");
+  int rc = ftx::check_device_range(dev, nbytes, "read probe input");
+  if (rc == FTX_OK) rc = ftx::check_device_range(sink, 4, "read probe sink");
+  if (rc != FTX_OK) return rc;
+  FTX_HIP(ftx::launch_read_probe(dev, nbytes, static_cast<uint32_t *>(sink), grid, static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
 int ftx_checksum64(const void *dev, size_t nbytes, void *stream, uint64_t *out) {
   if (!out) return ftx::fail(FTX_ERR_INVALID, "out is null");
   if (nbytes == 0) {

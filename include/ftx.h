@@ -224,6 +224,14 @@ int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void 
  * folded per 4 KiB block); result written to *out after stream sync. */
 int ftx_checksum64(const void *dev, size_t nbytes, void *stream, uint64_t *out);
 
+/* ---- measurement ----------------------------------------------------------
+ * No reference counterpart. Reads nbytes at dev (16-byte aligned, a multiple
+ * of 16) with `grid` workgroups of 256 lanes, eight 16-byte non-temporal loads
+ * in flight per lane, and writes nothing (sink, 4 bytes of device memory, is
+ * written only if the folded data equals a fixed sentinel): the plain HBM
+ * read rate the HBM-bound kernels are measured against. */
+int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
