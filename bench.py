@@ -623,6 +623,98 @@ def bench_fp8_linear(batch: int = 8, reps: int = 20) -> dict:
                                       "unit": "GB/s", "frac": round(big["GBps"] / HBM_PEAK_GBPS, 4)}}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def bench_fp8_prefill(rows: int = 512, reps: int = 5) -> dict:
+    """The fp8 prefill kernel (tiled MFMA GEMM) on one 70B-shape layer's projections at ``rows`` activation rows
+    (batch 8 x 64 prompt tokens), as the decoder runs them (grouped q/k/v and gate/up, single o and down).
+
+    Compute-bound: 2 * rows * n * k flops per matrix, against the dense bf16 MFMA peak. GPU time from a HIP
+    graph of ``reps`` layers (two layers' weights alternated); the dequantize-then-bf16-GEMM forward it
+    replaces is timed beside it."""
+    import torch
+    import torch.nn.functional as F
+
+    from flextensor_amd import hip
+    from flextensor_amd import workloads as W
+
+    s = W.LLAMA_70B_FP8
+    h, q, kv, it = s.hidden, s.n_heads * s.head_dim, s.n_kv_heads * s.head_dim, s.inter
+    rows_of = {"wq": q, "wk": kv, "wv": kv, "wo": h, "gate": it, "up": it, "down": h}
+    calls = [("qkv", ("wq", "wk", "wv"), h), ("o", ("wo",), q), ("gate+up", ("gate", "up"), h), ("down", ("down",), it)]
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    layers = []
+    for _ in range(2):
+        layer = {}
+        for _, names, k in calls:
+            for nm in names:
+                w = (torch.randn(rows_of[nm], k, device=dev, generator=gen) * 64).clamp(-448, 448).to(torch.float8_e4m3fn)
+                layer[nm] = (w, (torch.rand(rows_of[nm], device=dev, generator=gen) / 448).to(torch.bfloat16))
+        layers.append(layer)
+    xs = {k: torch.randn(rows, k, device=dev, generator=gen).to(torch.bfloat16) for k in (h, it)}
+
+    def run(layer, names, k):
+        if len(names) == 1:
+            return [hip.fp8_linear(xs[k], *layer[names[0]])]
+        return hip.fp8_linear_group(xs[k], [layer[nm][0] for nm in names], [layer[nm][1] for nm in names])
+
+    def graph_ms(fn, n):
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn(0)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(n):
+                    fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(side):
+            a.record(side)
+            graph.replay()
+            b.record(side)
+        torch.cuda.synchronize()
+        del graph
+        return a.elapsed_time(b) / n
+
+    flops = {label: sum(2.0 * rows * rows_of[nm] * k for nm in names) for label, names, k in calls}
+    layer_ms = graph_ms(lambda i: [run(layers[i % 2], names, k) for _, names, k in calls], reps)
+    per_call = []
+    for label, names, k in calls:
+        ms = graph_ms(lambda i, names=names, k=k: run(layers[i % 2], names, k), reps)
+        per_call.append({"call": label, "us": round(ms * 1e3, 1), "TFLOPs": round(flops[label] / ms / 1e9, 1)})
+    errs, dq_ms = {}, 0.0
+    for label, names, k in calls:
+        for nm, y in zip(names, run(layers[0], names, k)):
+            w, sc = layers[0][nm]
+            want = (xs[k].float() @ w.float().t()) * sc.float()
+            errs[nm] = round(float((y.float() - want).norm() / want.norm()), 5)
+            del want
+            F.linear(xs[k], w.to(torch.bfloat16)) * sc
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(3):
+                F.linear(xs[k], w.to(torch.bfloat16)) * sc
+            b.record()
+            torch.cuda.synchronize()
+            dq_ms += a.elapsed_time(b) / 3
+    total = sum(flops.values())
+    achieved = total / layer_ms / 1e9
+    del layers
+    torch.cuda.empty_cache()
+    return {"rows": rows, "calls": per_call, "layer_us": round(layer_ms * 1e3, 1),
+            "layer_dequant_gemm_us": round(dq_ms * 1e3, 1), "rel_err_vs_fp32": errs,
+            "roofline": {"kernel": "fp8_prefill_kernel", "bound": "mfma", "achieved": round(achieved, 1),
+                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_layer": total}}
+
+
 def staged_sweep(repeats: int = 5) -> dict:
     """Host-to-device GB/s from pageable memory: the staged engine by threads and piece size.
 
@@ -920,7 +1012,7 @@ def main() -> int:
         print(json.dumps(engine_contention()), flush=True)
         return 0
     if args.fp8_linear_only:
-        print(json.dumps({"fp8_linear": bench_fp8_linear()}), flush=True)
+        print(json.dumps({"fp8_linear": bench_fp8_linear(), "fp8_prefill": bench_fp8_prefill()}), flush=True)
         return 0
     if args.staged_sweep:
         print(json.dumps({"staged_sweep": staged_sweep()}), flush=True)
@@ -1045,6 +1137,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["fp8_linear"] = bench_fp8_linear()
         _log(f"fp8 linear: {line['fp8_linear']}")
+        line["fp8_prefill"] = bench_fp8_prefill()
+        _log(f"fp8 prefill: {line['fp8_prefill']}")
         line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b)
         if not args.skip_cpu_baseline and "skipped" not in line["llama70b_fp8"]:
             line["llama70b_fp8"]["cpu_baseline"] = cpu_llama70b_decode_baseline()

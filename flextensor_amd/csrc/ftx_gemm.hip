@@ -3,7 +3,9 @@
 //   y[m, n] = bf16( scale[n] * sum_k x[m, k] * w[n, k] )
 //
 // x is bf16 [M, K], w is float8 e4m3fn [N, K] (row-major, K contiguous),
-// scale is one bf16 per output channel, y is bf16 [M, N]; M <= 64.
+// scale is one bf16 per output channel, y is bf16 [M, N]. Up to 64 rows
+// (decode) run fp8_linear_kernel below; more rows (prefill) run the tiled
+// fp8_prefill_kernel further down.
 //
 // Decode multiplies a few activation rows by a large weight matrix, so the
 // kernel is bound by reading the fp8 weights from HBM once (1 byte per
@@ -109,6 +111,10 @@ struct SegTable {
   int rb0[kFp8MaxGroup + 1];
   int count;
 };
+
+// Output tile of the prefill kernel (more than kFp8LinearMaxRows rows), below.
+constexpr int kPTileM = 128;  // activation rows
+constexpr int kPTileN = 128;  // output channels
 
 // MB: 16-column batch blocks (M <= 16*MB). Workgroup b owns rows
 // [rg*16*S, rg*16*S + 16*S) (S waves, 16 rows each), rg = b / splits, and
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(kReduceThreads) void fp8_linear_reduce_kernel(const
 SegTable seg_table(const Fp8LinearLaunch &p) {
   SegTable t{};
   t.count = p.group;
-  const int64_t rows = 16 * static_cast<int64_t>(p.waves);
+  const int64_t rows = p.prefill ? kPTileN : 16 * static_cast<int64_t>(p.waves);
   int rg = 0, rb = 0;
   int64_t off = 0;
   for (int s = 0; s < p.group; ++s) {
@@ -318,6 +324,153 @@ SegTable seg_table(const Fp8LinearLaunch &p) {
   return t;
 }
 
+// ---- prefill: inputs of more than kFp8LinearMaxRows rows -------------------
+//
+// Many activation rows make the layer a compute-bound GEMM, so this is a
+// tiled MFMA GEMM that still reads the weights as fp8 and widens them in
+// registers (no bf16 copy of the weights is ever written). Workgroup tile:
+// 128 activation rows x 128 output channels, K in steps of 64; four waves in a
+// 2 x 2 grid, each owning 64 x 64 outputs as 4 x 4 v_mfma_f32_16x16x32_bf16
+// tiles. Each step stages x[128][64] (bf16) and w[128][64] (fp8) in LDS,
+// double buffered: the next step's global loads sit in registers while the
+// current step multiplies. A operands (weights) are read from LDS as 8 fp8
+// bytes and widened with v_cvt_scalef32_pk_bf16_fp8, B operands (activations)
+// as 8 bf16; lane group g takes k = 8g..8g+7 of each 32-wide block for both.
+//
+// Block order: the hardware hands workgroup b to XCD b % xcds. The m-tiles of
+// one n-tile get consecutive slots on one XCD, so each weight tile comes from
+// HBM once and from that XCD's L2 for the other m-tiles.
+constexpr int kPTileK = 64;
+constexpr int kPThreads = 256;
+constexpr int kPXRow = kPTileK * 2 + 16;    // LDS bytes per staged activation row (+16: bank spread)
+constexpr int kPWRow = kPTileK + 16;        // LDS bytes per staged weight row
+constexpr int kPXBytes = kPTileM * kPXRow;  // 18 KiB
+constexpr int kPWBytes = kPTileN * kPWRow;  // 10 KiB
+constexpr int kPXVecs = kPTileM * kPTileK * 2 / 16 / kPThreads;  // 16-byte x vectors per thread per step (4)
+constexpr int kPWVecs = kPTileN * kPTileK / 16 / kPThreads;      // 16-byte w vectors per thread per step (2)
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(u32x2 w) {
+  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.0f, false);
+  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.0f, true);
+  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.0f, false);
+  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.0f, true);
+  return join8(p0, p1, p2, p3);
+}
+
+// seg.rg0 holds each matrix's first n-tile (tiles of kPTileN output channels).
+__global__ __launch_bounds__(kPThreads) void fp8_prefill_kernel(const uint8_t *__restrict__ x, SegTable seg, int M,
+                                                                int K, int m_tiles, int n_tiles, int xcds) {
+  __shared__ __align__(16) uint8_t lds[2 * (kPXBytes + kPWBytes)];
+  const int xcd = blockIdx.x % xcds;
+  const int slot = blockIdx.x / xcds;
+  const int nt = (slot / m_tiles) * xcds + xcd;
+  const int mt = slot % m_tiles;
+  if (nt >= n_tiles) return;  // the last round of n-tiles does not fill every XCD
+  int s = 0;
+  while (s + 1 < seg.count && nt >= seg.rg0[s + 1]) ++s;
+  const int N = seg.n[s];
+  const uint8_t *__restrict__ w = seg.w[s];
+  const int n_base = (nt - seg.rg0[s]) * kPTileN;
+  const int m_base = mt * kPTileM;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  u32x4 xv[kPXVecs], wv[kPWVecs];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < kPXVecs; ++q) {
+      const int v = threadIdx.x + q * kPThreads;
+      const int row = v >> 3, c = (v & 7) * 8;  // 8 bf16 per vector
+      const bool ok = m_base + row < M && k0 + c < K;
+      xv[q] = ok ? *reinterpret_cast<const u32x4 *>(x + (static_cast<size_t>(m_base + row) * K + k0 + c) * 2)
+                 : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < kPWVecs; ++q) {
+      const int v = threadIdx.x + q * kPThreads;
+      const int row = v >> 2, c = (v & 3) * 16;  // 16 fp8 per vector
+      const bool ok = n_base + row < N && k0 + c < K;
+      wv[q] = ok ? __builtin_nontemporal_load(
+                       reinterpret_cast<const u32x4 *>(w + static_cast<size_t>(n_base + row) * K + k0 + c))
+                 : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+    uint8_t *xs = lds + buf * (kPXBytes + kPWBytes);
+    uint8_t *ws = xs + kPXBytes;
+#pragma unroll
+    for (int q = 0; q < kPXVecs; ++q) {
+      const int v = threadIdx.x + q * kPThreads;
+      *reinterpret_cast<u32x4 *>(xs + (v >> 3) * kPXRow + (v & 7) * 16) = xv[q];
+    }
+#pragma unroll
+    for (int q = 0; q < kPWVecs; ++q) {
+      const int v = threadIdx.x + q * kPThreads;
+      *reinterpret_cast<u32x4 *>(ws + (v >> 2) * kPWRow + (v & 3) * 16) = wv[q];
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int steps = (K + kPTileK - 1) / kPTileK;
+  if (steps > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < steps; ++st) {
+    if (st + 1 < steps) load((st + 1) * kPTileK);
+    const uint8_t *xs = lds + (st & 1) * (kPXBytes + kPWBytes);
+    const uint8_t *ws = xs + kPXBytes;
+#pragma unroll
+    for (int kb = 0; kb < kPTileK / 32; ++kb) {
+      bf16x8 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[i] = fp8x8_to_bf16(*reinterpret_cast<const u32x2 *>(ws + (wn * 64 + i * 16 + r) * kPWRow + kb * 32 + g * 8));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[j] = as_bf16x8(*reinterpret_cast<const u32x4 *>(xs + (wm * 64 + j * 16 + r) * kPXRow + (kb * 32 + g * 8) * 2));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (st + 1 < steps) store((st + 1) & 1);
+    __syncthreads();
+  }
+
+  // lane holds D rows (output channels) 4g..4g+3 of column (activation row) r of every tile
+  const uint16_t *__restrict__ scale = seg.scale[s];
+  uint16_t *__restrict__ y = seg.y[s];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int nb = n_base + wn * 64 + i * 16 + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m_base + wm * 64 + j * 16 + r;
+      if (m >= M) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (nb + v < N) {
+          const float sc = __uint_as_float(static_cast<uint32_t>(scale[nb + v]) << 16);
+          y[static_cast<size_t>(m) * N + nb + v] = f32_to_bf16_bits(acc[i][j][v] * sc);
+        }
+    }
+  }
+}
+
 template <int MB>
 hipError_t launch_mb(const Fp8LinearLaunch &p, hipStream_t stream) {
   const SegTable seg = seg_table(p);
@@ -333,7 +486,7 @@ hipError_t launch_mb(const Fp8LinearLaunch &p, hipStream_t stream) {
 
 }  // namespace
 
-Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int waves,
+Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int xcds, int waves,
                                 int kc_override) {
   Fp8LinearLaunch p{};
   p.m = m;
@@ -342,6 +495,21 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
   for (int s = 0; s < group; ++s) {
     p.n[s] = n[s];
     p.n_total += n[s];
+  }
+  if (m > kFp8LinearMaxRows) {
+    // prefill: one workgroup per 128 x 128 output tile, whole K, no workspace
+    p.prefill = true;
+    p.splits = 1;
+    p.kc = k;
+    p.xcds = std::max(1, xcds);
+    const int64_t m_tiles = (m + kPTileM - 1) / kPTileM;
+    int64_t n_tiles = 0;
+    for (int s = 0; s < group; ++s) n_tiles += (n[s] + kPTileN - 1) / kPTileN;
+    p.m_tiles = m_tiles;
+    p.row_groups = n_tiles;
+    p.grid = p.xcds * m_tiles * ((n_tiles + p.xcds - 1) / p.xcds);
+    p.waves = kPThreads / kWave;
+    return p;
   }
   p.batch_blocks = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
   // LDS: m activation rows of (2*Kc + 16) bytes plus one weight tile per
@@ -386,6 +554,13 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
 }
 
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream) {
+  if (p.prefill) {
+    const SegTable seg = seg_table(p);
+    hipLaunchKernelGGL(fp8_prefill_kernel, dim3(static_cast<unsigned>(p.grid)), dim3(kPThreads), 0, stream,
+                       static_cast<const uint8_t *>(p.x), seg, static_cast<int>(p.m), static_cast<int>(p.k),
+                       static_cast<int>(p.m_tiles), static_cast<int>(p.row_groups), p.xcds);
+    return hipGetLastError();
+  }
   switch (p.batch_blocks) {
     case 1: return launch_mb<1>(p, stream);
     case 2: return launch_mb<2>(p, stream);

@@ -67,10 +67,14 @@ struct Fp8LinearLaunch {
   int64_t grid;       // workgroups = row_groups * splits
   size_t lds_bytes;   // activation slice + one weight tile per wave
   size_t workspace_bytes;
+  bool prefill;       // more than kFp8LinearMaxRows rows: the tiled prefill kernel (no split, no workspace)
+  int64_t m_tiles;    // prefill: tiles of 128 activation rows (row_groups then counts tiles of 128 channels)
+  int xcds;           // prefill: L2 domains the block order is arranged for
 };
 constexpr int kFp8LinearMaxRows = 64;
 constexpr size_t kFp8LinearMaxLds = 64 * 1024;
-Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int waves, int kc);
+Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int xcds, int waves,
+                                int kc);
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream);
 
 // Staged copies from pageable host memory and the parallel host memcpy

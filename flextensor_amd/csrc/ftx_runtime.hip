@@ -683,8 +683,6 @@ int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLa
     n_total += n[s];
   }
   if (m < 0 || k < 0) return ftx::fail(FTX_ERR_INVALID, "negative dimension");
-  if (m > ftx::kFp8LinearMaxRows)
-    return ftx::fail(FTX_ERR_UNSUPPORTED, "fp8 linear takes at most 64 activation rows");
   if (k % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "k must be a multiple of 16");
   if (n_total > (int64_t(1) << 30) || k > (int64_t(1) << 30) || m * n_total > (int64_t(1) << 31))
     return ftx::fail(FTX_ERR_INVALID, "fp8 linear dimensions too large");
@@ -701,12 +699,15 @@ int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLa
     waves = ftx::g_fp8_waves;
     slice_k = ftx::g_fp8_slice_k;
   }
-  int cus = 256;
+  int cus = 256, xcds = 8;
   {
     ftx::DeviceState *st = nullptr;
-    if (ftx::device_state(&st) == FTX_OK) cus = st->cu_count;
+    if (ftx::device_state(&st) == FTX_OK) {
+      cus = st->cu_count;
+      xcds = st->xcd_count;
+    }
   }
-  *p = ftx::plan_fp8_linear(m, n, group, k, cus, waves, slice_k);
+  *p = ftx::plan_fp8_linear(m, n, group, k, cus, xcds, waves, slice_k);
   if (p->grid > (int64_t(1) << 31) - 1) return ftx::fail(FTX_ERR_INVALID, "fp8 linear grid too large");
   return FTX_OK;
 }

@@ -324,7 +324,7 @@ def checksum(t: torch.Tensor, stream: HipStream | None = None) -> int:
     return nat.checksum64(t.data_ptr(), t.numel() * t.element_size(), s.handle)
 
 
-FP8_LINEAR_MAX_ROWS = 64
+FP8_DECODE_MAX_ROWS = 64  # more rows run the tiled prefill kernel
 _FP8_WORKSPACE: dict[tuple, int] = {}
 
 
@@ -342,10 +342,11 @@ def fp8_linear_workspace_bytes(m: int, n: int, k: int) -> int:
 def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """``bf16(scale * (x @ weight.T))`` by the library's fp8-weight MFMA kernel.
 
-    ``x``: bf16 ``[m, k]`` with ``m <= 64``; ``weight``: float8 e4m3fn ``[n, k]``;
-    ``scale``: bf16 ``[n]``; all on one device. The weights are widened to
-    bf16 in registers, so the products are those of dequantizing and running
-    a bf16 GEMM. Runs on torch's current stream; the split-K workspace comes
+    ``x``: bf16 ``[m, k]``; ``weight``: float8 e4m3fn ``[n, k]``; ``scale``:
+    bf16 ``[n]``; all on one device. The weights are widened to bf16 in
+    registers, so the products are those of dequantizing and running a bf16
+    GEMM. Up to 64 rows run the split-K decode kernel, more rows the tiled
+    prefill kernel. Runs on torch's current stream; a split-K workspace comes
     from torch's allocator on that stream.
     """
     if x.dim() != 2 or weight.dim() != 2 or scale.dim() != 1:

@@ -123,11 +123,12 @@ LLAMA_70B_FP8 = LlamaShape(n_layers=80, hidden=8192, n_heads=64, n_kv_heads=8, h
 class Fp8Linear(nn.Module):
     """y = x @ (W_fp8 * scale[:, None])^T with W in float8_e4m3fn and a bf16 scale per output channel.
 
-    On the GPU, decode-sized inputs (at most 64 rows, K a multiple of 16) run
-    the library's fp8-weight MFMA kernel, which reads each fp8 weight once and
-    widens it to bf16 in registers; the decoder groups its q/k/v and gate/up
-    projections into one launch each (:func:`fp8_group`). Larger inputs (prefill) and CPU inputs
-    dequantise to bf16 and run a bf16 GEMM. Every e4m3 value is exactly
+    On the GPU (K a multiple of 16) the library's fp8-weight MFMA kernels run:
+    up to 64 rows (decode) a split-K kernel that reads each fp8 weight once,
+    more rows (prefill) a tiled GEMM; both widen the weights to bf16 in
+    registers. The decoder groups its q/k/v and gate/up projections into one
+    launch each (:func:`fp8_group`). CPU inputs dequantise to bf16 and run a
+    bf16 GEMM. Every e4m3 value is exactly
     representable in bf16, so both compute the same products; they differ in
     accumulation order and in rounding the product before the scale.
     """
@@ -139,13 +140,13 @@ class Fp8Linear(nn.Module):
         self.scale = nn.Parameter(torch.ones(out_features, dtype=torch.bfloat16), requires_grad=False)
 
     def kernel_eligible(self, x: torch.Tensor) -> bool:
-        """Whether the library kernel takes this call: a bf16 GPU input of 1..64 rows, K a multiple of
+        """Whether the library kernels take this call: a non-empty bf16 GPU input with K a multiple of
         16, and a contiguous, 16-byte aligned weight (``raw_block_transfer`` packs weights back to back
         without alignment; such a weight takes the dequantize path)."""
         k = x.shape[-1]
         m = x.numel() // k if k else 0
         w = self.weight
-        return (x.is_cuda and x.dtype == torch.bfloat16 and 0 < m <= hip.FP8_LINEAR_MAX_ROWS and k % 16 == 0
+        return (x.is_cuda and x.dtype == torch.bfloat16 and m > 0 and k % 16 == 0 and m * w.shape[0] < 2**31
                 and w.is_contiguous() and w.data_ptr() % 16 == 0)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -169,23 +169,25 @@ int ftx_scatter_run(const ftx_scatter_plan *plan, const void *chunk, void *strea
 /* One-shot form: stream-ordered upload of the table, launch, stream-ordered free. */
 int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stream);
 
-/* ---- fp8-weight linear (the decode forward's GEMMs) ------------------------
+/* ---- fp8-weight linear (the decode and prefill forward's GEMMs) ------------
  * No reference counterpart: the reference streams weights for whatever
  * nn.Linear the user's model holds. This replaces the forward of an fp8 linear
- * layer, F.linear(x, w.to(bfloat16)) * scale, for decode-sized batches:
+ * layer, F.linear(x, w.to(bfloat16)) * scale:
  *   y[i, j] = bf16(scale[j] * sum_k x[i, k] * w[j, k])
  * x: bf16 [m, k] contiguous, 16-byte aligned; w: float8 e4m3fn [n, k]
- * contiguous, 16-byte aligned; scale: bf16 [n]; y: bf16 [m, n] contiguous.
- * m <= 64 (FTX_ERR_UNSUPPORTED above), k a multiple of 16. The weights are
- * widened to bf16 in registers and multiplied on the MFMA units in fp32.
- * K is split over workgroups; each slice's partial sums go to `workspace`
- * (device memory of at least ftx_fp8_linear_workspace bytes, 16-byte
- * aligned; it may be NULL when that size is 0) and a second kernel adds them
- * in slice order, so results are deterministic for a given launch shape.
+ * contiguous, 16-byte aligned; scale: bf16 [n]; y: bf16 [m, n] contiguous;
+ * k a multiple of 16. The weights are widened to bf16 in registers and
+ * multiplied on the MFMA units in fp32; no bf16 copy of them is written.
+ * Up to 64 rows (decode) K is split over workgroups; each slice's partial
+ * sums go to `workspace` (device memory of at least ftx_fp8_linear_workspace
+ * bytes, 16-byte aligned; it may be NULL when that size is 0) and a second
+ * kernel adds them in slice order, so results are deterministic for a given
+ * launch shape. More rows (prefill) run a tiled GEMM (128 x 128 output tiles,
+ * whole K per tile) that needs no workspace.
  * Calls that share a workspace must be ordered on one stream.
- * ftx_set_fp8_linear_config fixes the launch shape (0 = chosen per call):
- * waves (wavefronts per workgroup, 16 output rows each, 1..8) and slice_k (K
- * values per workgroup, a multiple of 256). */
+ * ftx_set_fp8_linear_config fixes the decode launch shape (0 = chosen per
+ * call): waves (wavefronts per workgroup, 16 output rows each, 1..8) and
+ * slice_k (K values per workgroup, a multiple of 256). */
 int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes);
 int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
                    void *workspace, size_t workspace_bytes, void *stream);

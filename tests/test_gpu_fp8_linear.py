@@ -1,4 +1,4 @@
-"""GPU parity of the fp8-weight MFMA linear kernel (``ftx_fp8_linear``).
+"""GPU parity of the fp8-weight MFMA linear kernels (``ftx_fp8_linear``): decode (up to 64 rows) and prefill.
 
 The oracle is ``oracle.fp8`` (e4m3fn decoded from the format definition, the
 layer in float64). Where every product and partial sum is exact in float32
@@ -223,9 +223,10 @@ def test_rejects_bad_arguments(gpu, default_config):
     xt, wt, st = _to_device(x, w_raw, scale, gpu)
     y = torch.empty(65 * 32, dtype=torch.bfloat16, device=gpu)
     s = torch.cuda.current_stream().cuda_stream
-    with pytest.raises(nat.FtxError) as err:  # more rows than the kernel takes
-        nat.call("ftx_fp8_linear", xt.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), 65, 32, 64, None, 0, s)
-    assert err.value.code == nat.FTX_ERR_UNSUPPORTED
+    with pytest.raises(nat.FtxError) as err:  # an output of more than 2^31 elements
+        nat.call("ftx_fp8_linear", xt.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), 1 << 12, 1 << 20, 64,
+                 None, 0, s)
+    assert err.value.code == nat.FTX_ERR_INVALID
     with pytest.raises(nat.FtxError) as err:  # k not a multiple of 16
         nat.call("ftx_fp8_linear", xt.data_ptr(), wt.data_ptr(), st.data_ptr(), y.data_ptr(), 8, 32, 24, None, 0, s)
     assert err.value.code == nat.FTX_ERR_INVALID
@@ -418,3 +419,55 @@ def test_group_rejects_bad_arguments(gpu, default_config):
         nat.call("ftx_fp8_linear_group", xt.data_ptr(), 2, *(ctypes.cast(a, ctypes.c_void_p) for a in ptrs),
                  ctypes.cast(ns, ctypes.c_void_p), 8, 64, None, 0, torch.cuda.current_stream().cuda_stream)
     assert err.value.code == nat.FTX_ERR_INVALID and "null" in str(err.value)
+
+
+# ---- prefill: more than 64 rows, the tiled kernel ---------------------------------------------------
+
+
+_PREFILL_SHAPES = [(65, 16, 16), (128, 128, 64), (200, 300, 528), (129, 17, 48), (512, 1024, 1024), (1000, 640, 256),
+                   (300, 4100, 80)]
+
+
+@pytest.mark.parametrize("m,n,k", _PREFILL_SHAPES)
+def test_prefill_exact_products_bit_exact(gpu, default_config, m, n, k):
+    """Tile edges in every dimension (rows, channels, K not a multiple of the 64-wide step) stay exact."""
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _exact_case(m, n, k, seed=m + 3 * n + k)
+    want = torch.from_numpy(ofp8.fp8_linear(x, w_raw, scale)).to(torch.bfloat16)
+    assert hip.fp8_linear_workspace_bytes(m, n, k) == 0  # the prefill kernel needs no workspace
+    got = hip.fp8_linear(*_to_device(x, w_raw, scale, gpu))
+    torch.cuda.synchronize()
+    assert got.shape == (m, n)
+    assert _same_values(got, want)
+
+
+@pytest.mark.parametrize("n,k", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)])
+def test_prefill_70b_shapes_match_float64_oracle(gpu, default_config, n, k):
+    """512 rows (batch 8 x 64 prompt tokens) at the 70B projection shapes, against the float64 oracle."""
+    from flextensor_amd import hip
+
+    m = 512
+    x, w_raw, scale = _random_case(m, n, k, seed=n + k)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    got = hip.fp8_linear(xt, wt, st)
+    again = hip.fp8_linear(xt, wt, st)
+    assert torch.equal(got, again)  # deterministic
+    want = torch.from_numpy(ofp8.fp8_linear(xt.float().cpu().numpy(), w_raw, st.float().cpu().numpy()))
+    g = got.double().cpu()
+    assert float((g - want).norm() / want.norm()) < REL_TOL
+    bound = ELEM_TOL * torch.maximum(want.abs(), want.pow(2).mean().sqrt())
+    assert bool(((g - want).abs() <= bound).all())
+
+
+def test_prefill_group_matches_single_calls(gpu, default_config):
+    """A grouped prefill call (q/k/v at 512 rows) computes each matrix exactly as its single call."""
+    from flextensor_amd import hip
+
+    m, k = 512, 2048
+    cases = [_random_case(m, n, k, seed=n) for n in (2048, 256, 256)]
+    xt = _to_device(*cases[0], gpu)[0]
+    dev = [_to_device(cases[0][0], w_raw, scale, gpu)[1:] for _, w_raw, scale in cases]
+    grouped = hip.fp8_linear_group(xt, [d[0] for d in dev], [d[1] for d in dev])
+    for (w, sc), y in zip(dev, grouped):
+        assert torch.equal(y, hip.fp8_linear(xt, w, sc))  # same tiles, same K order

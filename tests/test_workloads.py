@@ -199,4 +199,5 @@ def test_fp8_kernel_needs_an_aligned_weight():
         assert lin.weight.data_ptr() % 16 and not lin.kernel_eligible(x)
     lin.weight.data = raw[16: 16 + 32 * 64].view(torch.float8_e4m3fn).view(32, 64)
     assert lin.kernel_eligible(x)
-    assert not lin.kernel_eligible(_FakeGpuInput(65, 64)) and not lin.kernel_eligible(_FakeGpuInput(8, 24))
+    assert lin.kernel_eligible(_FakeGpuInput(512, 64))  # prefill rows take the tiled kernel
+    assert not lin.kernel_eligible(_FakeGpuInput(8, 24)) and not lin.kernel_eligible(_FakeGpuInput(0, 64))
