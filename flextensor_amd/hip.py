@@ -191,6 +191,8 @@ def _probe_concurrency(candidate: HipStream, compute: HipStream, device: torch.d
     """
     a = torch.ones(4096, 4096, dtype=torch.bfloat16, device=device)
     small = torch.empty(1024, dtype=torch.uint8, device=device)
+    with torch.cuda.stream(compute.torch_stream) if compute.torch_stream is not None else _nullctx():
+        torch.matmul(a, a)  # the first product at a shape selects its kernel on the host: keep that out of the window
     torch.cuda.synchronize(device)
     c_end, s_end, start = HipEvent(timing=True), HipEvent(timing=True), HipEvent(timing=True)
     compute.record_event(start)
@@ -205,10 +207,16 @@ def _probe_concurrency(candidate: HipStream, compute: HipStream, device: torch.d
     return start.elapsed_time(c_end), start.elapsed_time(s_end)
 
 
+# A candidate on the compute stream's hardware queue finishes its fill only after all of the queued
+# products (at about 100% of the busy time); one on another queue finishes within the first half, or
+# around 60% when a profiler's tracing slows every dispatch. 80% separates the two.
+_CONCURRENT_FRACTION = 0.8
+
+
 def _runs_concurrently(candidate: HipStream, compute: HipStream, device: torch.device) -> bool:
-    """Whether work on ``candidate`` finishes while ``compute`` is still busy (in the first half)."""
+    """Whether work on ``candidate`` finishes while ``compute`` is still busy."""
     busy, cand = _probe_concurrency(candidate, compute, device)
-    return cand < 0.5 * busy
+    return cand < _CONCURRENT_FRACTION * busy
 
 
 def transfer_stream(device: torch.device | int | None = None, attempts: int = 8) -> HipStream:
@@ -233,7 +241,7 @@ def transfer_stream(device: torch.device | int | None = None, attempts: int = 8)
         cand = new_stream(dev, name="transfer")
         busy, done = _probe_concurrency(cand, compute, dev)
         tried.append((round(busy, 3), round(done, 3)))
-        if done < 0.5 * busy:
+        if done < _CONCURRENT_FRACTION * busy:
             _STREAM_PROBES[dev.index] = {"chosen_candidate": i, "rejected": i, "attempts": attempts,
                                          "compute_busy_ms": tried[-1][0], "transfer_fill_done_ms": tried[-1][1]}
             _TRANSFER_STREAMS[dev.index] = cand

@@ -198,7 +198,7 @@ def test_transfer_stream_runs_beside_compute(gpu):
     probe = transfer_stream_probe(gpu)
     print(f"transfer stream probe: {probe}", flush=True)
     assert probe["chosen_candidate"] == probe["rejected"] < probe["attempts"]
-    assert probe["transfer_fill_done_ms"] < 0.5 * probe["compute_busy_ms"]
+    assert probe["transfer_fill_done_ms"] < 0.8 * probe["compute_busy_ms"]
 
 
 def test_arena_freed_by_refcount_when_last_view_dies(gpu):

@@ -58,3 +58,12 @@ def test_no_concurrent_candidate_is_an_error_naming_the_timings(fake_device):
             hip.transfer_stream(torch.device("cuda", 7), attempts=3)
     assert "(2.0, 2.1)" in str(info.value) and "GPU_MAX_HW_QUEUES" in str(info.value)
     assert 7 not in hip._TRANSFER_STREAMS and hip.transfer_stream_probe(torch.device("cuda", 7)) is None
+
+
+def test_slowed_dispatch_still_counts_as_concurrent(fake_device):
+    """Under a profiler every dispatch is slower and a concurrent fill lands near 60% of the compute time;
+    only a fill that waits for (nearly) all of it marks a shared queue."""
+    timings = iter([(1.5, 1.49), (1.5, 0.9)])
+    with mock.patch.object(hip, "_probe_concurrency", lambda c, comp, d: next(timings)):
+        s = hip.transfer_stream(torch.device("cuda", 7))
+    assert s is fake_device[1] and hip.transfer_stream_probe(torch.device("cuda", 7))["rejected"] == 1
