@@ -326,43 +326,87 @@ SegTable seg_table(const Fp8LinearLaunch &p) {
 
 // ---- prefill: inputs of more than kFp8LinearMaxRows rows -------------------
 //
-// Many activation rows make the layer a compute-bound GEMM, so this is a
-// tiled MFMA GEMM that still reads the weights as fp8 and widens them in
-// registers (no bf16 copy of the weights is ever written). Workgroup tile:
-// 128 activation rows x 128 output channels, K in steps of 64; four waves in a
-// 2 x 2 grid, each owning 64 x 64 outputs as 4 x 4 v_mfma_f32_16x16x32_bf16
-// tiles. Each step stages x[128][64] (bf16) and w[128][64] (fp8) in LDS,
-// double buffered: the next step's global loads sit in registers while the
-// current step multiplies. A operands (weights) are read from LDS as 8 fp8
-// bytes and widened with v_cvt_scalef32_pk_bf16_fp8, B operands (activations)
-// as 8 bf16; lane group g takes k = 8g..8g+7 of each 32-wide block for both.
+// Many activation rows make the layer a compute-bound GEMM. This is a tiled
+// MFMA GEMM that still reads the weights as fp8 and widens them in registers
+// (no bf16 copy of the weights is ever written).
+//
+// Workgroup tile: 128 output channels x 128 activation rows, K in steps of 64.
+// Each step's tiles go straight from global memory into an S-stage LDS ring
+// with global_load_lds_dwordx4 (no register staging): the activation tile as
+// 128 rows of 128 bytes, then the weight tile as 128 rows of 64 bytes. Each
+// load instruction writes 1 KB of LDS, lane l at +16 l, so the layout is
+// chosen by which global chunk each lane fetches:
+//   activation row R, 16-byte chunk c (k = 8c..8c+7) at slot c ^ (R & 7),
+//   weight row R,     16-byte chunk c (k = 16c..16c+15) at slot c ^ ((R >> 1) & 3),
+// which keeps the MFMA operand reads below free of bank conflicts.
+//
+// k permutation within a step (any one that both operands share gives the
+// same sum): lane group g feeds k = 16g + 8kb + (0..7) to the kb-th of the
+// step's two MFMAs, so one 16-byte weight read per lane covers both MFMAs.
+//
+// Two launch shapes, chosen by the planner (measured on the 70B projection
+// shapes at 512 rows):
+//   * more tiles than CUs: 4 waves (2 x 2, 64 x 64 each), 2 stages (48 KB
+//     LDS, three workgroups per CU);
+//   * at most one tile per CU: 8 waves (2 x 4, 64 x 32 each), 4 stages
+//     (96 KB, one workgroup per CU), so two waves share each SIMD; waves 0-3
+//     issue the loads (with all eight issuing them, the same kernel ran at
+//     half the load rate).
+// Both accumulate every output over the same MFMA sequence, so they give
+// identical results.
+//
+// Rows past M or N read the last valid row (their products land in outputs
+// that are never stored). A K that is not a multiple of 64 ends in a partial
+// step: its loads past K are clamped into the row and both operands are
+// zeroed for the lane groups past K.
 //
 // Block order: the hardware hands workgroup b to XCD b % xcds. The m-tiles of
 // one n-tile get consecutive slots on one XCD, so each weight tile comes from
 // HBM once and from that XCD's L2 for the other m-tiles.
 constexpr int kPTileK = 64;
-constexpr int kPThreads = 256;
-constexpr int kPXRow = kPTileK * 2 + 16;    // LDS bytes per staged activation row (+16: bank spread)
-constexpr int kPWRow = kPTileK + 16;        // LDS bytes per staged weight row
-constexpr int kPXBytes = kPTileM * kPXRow;  // 18 KiB
-constexpr int kPWBytes = kPTileN * kPWRow;  // 10 KiB
-constexpr int kPXVecs = kPTileM * kPTileK * 2 / 16 / kPThreads;  // 16-byte x vectors per thread per step (4)
-constexpr int kPWVecs = kPTileN * kPTileK / 16 / kPThreads;      // 16-byte w vectors per thread per step (2)
+constexpr int kPXStage = kPTileM * kPTileK * 2;      // 16 KiB activation tile
+constexpr int kPWStage = kPTileN * kPTileK;          // 8 KiB weight tile
+constexpr int kPStage = kPXStage + kPWStage;
+constexpr int kPLoadsPerWave = 6;                    // load instructions per loading wave and step
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ bf16x8 fp8x8_to_bf16(u32x2 w) {
-  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.0f, false);
-  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.0f, true);
-  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.0f, false);
-  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.0f, true);
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
   return join8(p0, p1, p2, p3);
 }
 
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt left free); n is a constant at every call.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0f76); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0f7c); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+  }
+}
+
+// Workgroup barrier that also keeps the compiler from moving memory accesses
+// across it; the LDS ring's ordering is carried by vmcnt waits and this.
+__device__ __forceinline__ void ring_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS reads are done
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // seg.rg0 holds each matrix's first n-tile (tiles of kPTileN output channels).
-__global__ __launch_bounds__(kPThreads) void fp8_prefill_kernel(const uint8_t *__restrict__ x, SegTable seg, int M,
-                                                                int K, int m_tiles, int n_tiles, int xcds) {
-  __shared__ __align__(16) uint8_t lds[2 * (kPXBytes + kPWBytes)];
+template <int WAVES, int S>
+__global__ __launch_bounds__(WAVES * 64) void fp8_prefill_kernel(const uint8_t *__restrict__ x, SegTable seg, int M,
+                                                                 int K, int m_tiles, int n_tiles, int xcds) {
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  constexpr int JT = 16 / WAVES;             // 16-row activation tiles per wave
+  constexpr int WROWS = 16 * JT;             // activation rows per wave
+  __shared__ __align__(1024) uint8_t lds[S * kPStage];
   const int xcd = blockIdx.x % xcds;
   const int slot = blockIdx.x / xcds;
   const int nt = (slot / m_tiles) * xcds + xcd;
@@ -379,94 +423,138 @@ __global__ __launch_bounds__(kPThreads) void fp8_prefill_kernel(const uint8_t *_
   const int wave = threadIdx.x / kWave;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int wm = wave >> 1;
   const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const bool loads = WAVES == 4 || wave < 4;
+  const int lw = wave & 3;
 
-  u32x4 xv[kPXVecs], wv[kPWVecs];
-  auto load = [&](int k0) {
+  // This lane's load sources: activation rows (lw*4 + t)*8 + lane/8, weight
+  // rows (lw*2 + t)*16 + lane/4, at the chunk the swizzle assigns.
+  const int xc = ((lane & 7) ^ (lane >> 3)) * 8;            // k offset (elements) within a step
+  const int wc = ((lane & 3) ^ ((lane >> 3) & 3)) * 16;     // k offset (bytes) within a step
+  const uint8_t *xrow[4];
+  const uint8_t *wrow[2];
 #pragma unroll
-    for (int q = 0; q < kPXVecs; ++q) {
-      const int v = threadIdx.x + q * kPThreads;
-      const int row = v >> 3, c = (v & 7) * 8;  // 8 bf16 per vector
-      const bool ok = m_base + row < M && k0 + c < K;
-      xv[q] = ok ? *reinterpret_cast<const u32x4 *>(x + (static_cast<size_t>(m_base + row) * K + k0 + c) * 2)
-                 : u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int t = 0; t < 4; ++t) {
+    const int gm = min(m_base + (lw * 4 + t) * 8 + (lane >> 3), M - 1);
+    xrow[t] = x + static_cast<size_t>(gm) * K * 2;
+  }
 #pragma unroll
-    for (int q = 0; q < kPWVecs; ++q) {
-      const int v = threadIdx.x + q * kPThreads;
-      const int row = v >> 2, c = (v & 3) * 16;  // 16 fp8 per vector
-      const bool ok = n_base + row < N && k0 + c < K;
-      wv[q] = ok ? __builtin_nontemporal_load(
-                       reinterpret_cast<const u32x4 *>(w + static_cast<size_t>(n_base + row) * K + k0 + c))
-                 : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&](int buf) {
-    uint8_t *xs = lds + buf * (kPXBytes + kPWBytes);
-    uint8_t *ws = xs + kPXBytes;
+  for (int t = 0; t < 2; ++t) {
+    const int gn = min(n_base + (lw * 2 + t) * 16 + (lane >> 2), N - 1);
+    wrow[t] = w + static_cast<size_t>(gn) * K;
+  }
+  const int full = K / kPTileK;                 // whole steps
+  const int tail = K % kPTileK;                 // k values of a final partial step, a multiple of 16
+  const int steps = full + (tail ? 1 : 0);
+  auto issue = [&](int st) {
+    uint8_t *base = lds + (st % S) * kPStage;
+    // the clamps only bind in a partial step (a whole step ends at K - 8 and K - 16)
+    const int kx = min(st * kPTileK + xc, K - 8);
+    const int kw = min(st * kPTileK + wc, K - 16);
 #pragma unroll
-    for (int q = 0; q < kPXVecs; ++q) {
-      const int v = threadIdx.x + q * kPThreads;
-      *reinterpret_cast<u32x4 *>(xs + (v >> 3) * kPXRow + (v & 7) * 16) = xv[q];
-    }
+    for (int t = 0; t < 4; ++t)
+      __builtin_amdgcn_global_load_lds(xrow[t] + static_cast<size_t>(kx) * 2,
+                                       (lds_void *)(base + (lw * 4 + t) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int q = 0; q < kPWVecs; ++q) {
-      const int v = threadIdx.x + q * kPThreads;
-      *reinterpret_cast<u32x4 *>(ws + (v >> 2) * kPWRow + (v & 3) * 16) = wv[q];
-    }
+    for (int t = 0; t < 2; ++t)
+      __builtin_amdgcn_global_load_lds(wrow[t] + kw, (lds_void *)(base + kPXStage + (lw * 2 + t) * 1024), 16, 0,
+                                       0);
   };
 
-  f32x4 acc[4][4];
+  int aoff[4], boff0[JT], boff1[JT];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int R = wn * 64 + i * 16 + r;
+    aoff[i] = kPXStage + R * kPTileK + ((g ^ ((R >> 1) & 3)) << 4);
+  }
+#pragma unroll
+  for (int j = 0; j < JT; ++j) {
+    const int R = wm * WROWS + j * 16 + r;
+    boff0[j] = R * 128 + (((2 * g) ^ (R & 7)) << 4);
+    boff1[j] = R * 128 + (((2 * g + 1) ^ (R & 7)) << 4);
+  }
+
+  f32x4 acc[4][JT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < JT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int steps = (K + kPTileK - 1) / kPTileK;
-  if (steps > 0) {
-    load(0);
-    store(0);
+  if (loads) {
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st)
+      if (st < steps) issue(st);
   }
-  __syncthreads();
-  for (int st = 0; st < steps; ++st) {
-    if (st + 1 < steps) load((st + 1) * kPTileK);
-    const uint8_t *xs = lds + (st & 1) * (kPXBytes + kPWBytes);
-    const uint8_t *ws = xs + kPXBytes;
-#pragma unroll
-    for (int kb = 0; kb < kPTileK / 32; ++kb) {
-      bf16x8 a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = fp8x8_to_bf16(*reinterpret_cast<const u32x2 *>(ws + (wn * 64 + i * 16 + r) * kPWRow + kb * 32 + g * 8));
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = as_bf16x8(*reinterpret_cast<const u32x4 *>(xs + (wm * 64 + j * 16 + r) * kPXRow + (kb * 32 + g * 8) * 2));
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  // One step: this wave's loads of step st are in LDS once at most the later
+  // steps' loads are outstanding; the barrier then covers every loading wave,
+  // and every wave has finished reading the buffer the next loads overwrite.
+  // `partial` (the final step of a K that is not a multiple of 64) zeroes both
+  // operands of the lane groups past K.
+  auto step = [&](int st, bool partial) {
+    if (loads) {
+      if (st + S - 2 < steps)
+        wait_vmcnt((S - 2) * kPLoadsPerWave);
+      else
+        wait_vmcnt(0);
     }
-    if (st + 1 < steps) store((st + 1) & 1);
-    __syncthreads();
-  }
+    ring_barrier();
+    if (loads && st + S - 1 < steps) issue(st + S - 1);
+    const uint8_t *sb = lds + (st % S) * kPStage;
+    u32x4 A[4], B0[JT], B1[JT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) A[i] = *reinterpret_cast<const u32x4 *>(sb + aoff[i]);
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+      B0[j] = *reinterpret_cast<const u32x4 *>(sb + boff0[j]);
+      B1[j] = *reinterpret_cast<const u32x4 *>(sb + boff1[j]);
+    }
+    if (partial && 16 * g >= tail) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) A[i] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < JT; ++j) B0[j] = B1[j] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16x8 a0 = fp8x8_to_bf16(A[i][0], A[i][1]);
+      const bf16x8 a1 = fp8x8_to_bf16(A[i][2], A[i][3]);
+#pragma unroll
+      for (int j = 0; j < JT; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, as_bf16x8(B0[j]), acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, as_bf16x8(B1[j]), acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+  for (int st = 0; st < full; ++st) step(st, false);
+  if (tail) step(full, true);
 
   // lane holds D rows (output channels) 4g..4g+3 of column (activation row) r of every tile
   const uint16_t *__restrict__ scale = seg.scale[s];
   uint16_t *__restrict__ y = seg.y[s];
+  const bool vec = (N & 3) == 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int nb = n_base + wn * 64 + i * 16 + 4 * g;
+    float sc[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m_base + wm * 64 + j * 16 + r;
+    for (int v = 0; v < 4; ++v) sc[v] = nb + v < N ? __uint_as_float(static_cast<uint32_t>(scale[nb + v]) << 16) : 0.f;
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+      const int m = m_base + wm * WROWS + j * 16 + r;
       if (m >= M) continue;
+      uint16_t *dst = y + static_cast<size_t>(m) * N + nb;
+      if (vec && nb + 3 < N) {
+        const uint32_t lo = f32_to_bf16_bits(acc[i][j][0] * sc[0]) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(acc[i][j][1] * sc[1])) << 16);
+        const uint32_t hi = f32_to_bf16_bits(acc[i][j][2] * sc[2]) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(acc[i][j][3] * sc[3])) << 16);
+        *reinterpret_cast<u32x2 *>(dst) = u32x2{lo, hi};
+      } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (nb + v < N) {
-          const float sc = __uint_as_float(static_cast<uint32_t>(scale[nb + v]) << 16);
-          y[static_cast<size_t>(m) * N + nb + v] = f32_to_bf16_bits(acc[i][j][v] * sc);
-        }
+        for (int v = 0; v < 4; ++v)
+          if (nb + v < N) dst[v] = f32_to_bf16_bits(acc[i][j][v] * sc[v]);
+      }
     }
   }
 }
@@ -508,7 +596,9 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
     p.m_tiles = m_tiles;
     p.row_groups = n_tiles;
     p.grid = p.xcds * m_tiles * ((n_tiles + p.xcds - 1) / p.xcds);
-    p.waves = kPThreads / kWave;
+    // at most one tile per CU: 8 waves (two per SIMD) and 4 LDS stages in one
+    // workgroup; more tiles: 4 waves and 2 stages, three workgroups per CU
+    p.waves = (waves == 4 || waves == 8) ? waves : (m_tiles * n_tiles <= cus ? 8 : 4);
     return p;
   }
   p.batch_blocks = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
@@ -556,9 +646,14 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream) {
   if (p.prefill) {
     const SegTable seg = seg_table(p);
-    hipLaunchKernelGGL(fp8_prefill_kernel, dim3(static_cast<unsigned>(p.grid)), dim3(kPThreads), 0, stream,
-                       static_cast<const uint8_t *>(p.x), seg, static_cast<int>(p.m), static_cast<int>(p.k),
-                       static_cast<int>(p.m_tiles), static_cast<int>(p.row_groups), p.xcds);
+    if (p.waves == 8)
+      hipLaunchKernelGGL((fp8_prefill_kernel<8, 4>), dim3(static_cast<unsigned>(p.grid)), dim3(8 * kWave), 0, stream,
+                         static_cast<const uint8_t *>(p.x), seg, static_cast<int>(p.m), static_cast<int>(p.k),
+                         static_cast<int>(p.m_tiles), static_cast<int>(p.row_groups), p.xcds);
+    else
+      hipLaunchKernelGGL((fp8_prefill_kernel<4, 2>), dim3(static_cast<unsigned>(p.grid)), dim3(4 * kWave), 0, stream,
+                         static_cast<const uint8_t *>(p.x), seg, static_cast<int>(p.m), static_cast<int>(p.k),
+                         static_cast<int>(p.m_tiles), static_cast<int>(p.row_groups), p.xcds);
     return hipGetLastError();
   }
   switch (p.batch_blocks) {

@@ -187,7 +187,10 @@ int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stre
  * Calls that share a workspace must be ordered on one stream.
  * ftx_set_fp8_linear_config fixes the decode launch shape (0 = chosen per
  * call): waves (wavefronts per workgroup, 16 output rows each, 1..8) and
- * slice_k (K values per workgroup, a multiple of 256). */
+ * slice_k (K values per workgroup, a multiple of 256). For more than 64 rows
+ * waves 4 or 8 fixes the prefill launch shape (4: two LDS stages; 8: four);
+ * any other value lets the tile count choose. Every launch shape gives the
+ * same results. */
 int ftx_fp8_linear_workspace(int64_t m, int64_t n, int64_t k, size_t *bytes);
 int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
                    void *workspace, size_t workspace_bytes, void *stream);

@@ -442,6 +442,36 @@ def test_prefill_exact_products_bit_exact(gpu, default_config, m, n, k):
     assert _same_values(got, want)
 
 
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("m,n,k", _PREFILL_SHAPES)
+def test_prefill_each_launch_shape_bit_exact(gpu, default_config, waves, m, n, k):
+    """Both prefill launch shapes (4 waves / 2 LDS stages, 8 waves / 4 stages), forced, on the tile-edge cases."""
+    from flextensor_amd import hip
+
+    hip.set_fp8_linear_config(waves, 0)
+    x, w_raw, scale = _exact_case(m, n, k, seed=7 * m + n + k + waves)
+    want = torch.from_numpy(ofp8.fp8_linear(x, w_raw, scale)).to(torch.bfloat16)
+    got = hip.fp8_linear(*_to_device(x, w_raw, scale, gpu))
+    torch.cuda.synchronize()
+    assert _same_values(got, want)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 1024, 2048), (300, 700, 1040), (1024, 2304, 8192)])
+def test_prefill_launch_shapes_agree_bitwise(gpu, default_config, m, n, k):
+    """Random data: the two launch shapes accumulate every output over the same MFMA sequence."""
+    from flextensor_amd import hip
+
+    xt, wt, st = _to_device(*_random_case(m, n, k, seed=m + n), gpu)
+    hip.set_fp8_linear_config(4, 0)
+    y4 = hip.fp8_linear(xt, wt, st)
+    hip.set_fp8_linear_config(8, 0)
+    y8 = hip.fp8_linear(xt, wt, st)
+    hip.set_fp8_linear_config(0, 0)
+    y_auto = hip.fp8_linear(xt, wt, st)
+    assert torch.equal(y4, y8)
+    assert torch.equal(y4, y_auto)
+
+
 @pytest.mark.parametrize("n,k", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)])
 def test_prefill_70b_shapes_match_float64_oracle(gpu, default_config, n, k):
     """512 rows (batch 8 x 64 prompt tokens) at the 70B projection shapes, against the float64 oracle."""
