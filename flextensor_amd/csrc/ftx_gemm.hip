@@ -559,6 +559,54 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_prefill_kernel(const uint8_t *
   }
 }
 
+// ---- measurement: the sustained MFMA rate -------------------------------
+//
+// Each wave keeps 16 independent accumulators and cycles through 8 operand
+// pairs of random bf16 values (finite, magnitude 0.5 to 4, from a hash of the
+// lane), so the operands change from one MFMA to the next as in a GEMM; the
+// MFMA pipe runs at a lower clock on changing data than on constant data.
+// Writes nothing: sink is written only if the sum equals a fixed sentinel.
+__device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+__global__ __launch_bounds__(256) void mfma_probe_kernel(float *sink, int iters) {
+  const uint32_t id = blockIdx.x * 256u + threadIdx.x;
+  u32x4 av[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t h = probe_hash(id * 64u + e * 8u + q);
+      const uint32_t h2 = probe_hash(h);
+      // two bf16 per dword: sign, exponent 126..129, 7 mantissa bits
+      auto bf = [](uint32_t r) { return ((r & 1u) << 15) | ((126u + ((r >> 1) & 3u)) << 7) | ((r >> 3) & 0x7fu); };
+      av[e][q] = bf(h) | (bf(h >> 10) << 16);
+      bv[e][q] = bf(h2) | (bf(h2 >> 10) << 16);
+    }
+  }
+  f32x4 acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[(i + h) & 7]), as_bf16x8(bv[(3 * i + h) & 7]),
+                                                         acc[i], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sum += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+  if (sum == 1234.5f) sink[0] = sum;
+}
+
 template <int MB>
 hipError_t launch_mb(const Fp8LinearLaunch &p, hipStream_t stream) {
   const SegTable seg = seg_table(p);
@@ -641,6 +689,11 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
   p.lds_bytes = static_cast<size_t>(m) * (2 * p.kc + 16) + static_cast<size_t>(tiles);
   p.workspace_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * m * p.n_total * sizeof(float) : 0;
   return p;
+}
+
+hipError_t launch_mfma_probe(int workgroups, int iters, float *sink, hipStream_t stream) {
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256), 0, stream, sink, iters);
+  return hipGetLastError();
 }
 
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream) {

@@ -236,6 +236,12 @@ int ftx_checksum64(const void *dev, size_t nbytes, void *stream, uint64_t *out);
  * written only if the folded data equals a fixed sentinel): the plain HBM
  * read rate the HBM-bound kernels are measured against. */
 int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, void *stream);
+/* No reference counterpart. Runs `workgroups` workgroups of 4 waves, each
+ * wave iters x 32 independent v_mfma_f32_16x16x32_bf16 (16384 flops each) on
+ * random bf16 operands that change from one MFMA to the next, and writes
+ * nothing (sink, 4 bytes of device memory, only on a fixed sentinel): the
+ * sustained MFMA rate the compute-bound kernels are measured against. */
+int ftx_mfma_probe(int workgroups, int iters, void *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -255,3 +255,26 @@ def test_timestamp_rejects_host_slot(gpu):
     host = torch.zeros(2, dtype=torch.int64)
     with pytest.raises(nat.FtxError):
         nat.call("ftx_timestamp", host.data_ptr(), current_stream(gpu).handle)
+
+
+def test_probes_write_nothing_and_check_arguments(gpu):
+    """The HBM read probe and the MFMA probe leave their sink alone and refuse bad arguments."""
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import current_stream
+
+    s = current_stream(gpu).handle
+    sink = torch.full((1,), -7, dtype=torch.int32, device=gpu)
+    buf = torch.randint(0, 256, (1 << 20,), dtype=torch.uint8, device=gpu)
+    nat.call("ftx_hbm_read_probe", buf.data_ptr(), buf.numel(), sink.data_ptr(), 64, s)
+    nat.call("ftx_mfma_probe", 8, 16, sink.data_ptr(), s)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == -7
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_hbm_read_probe", buf.data_ptr() + 1, 64, sink.data_ptr(), 64, s)
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_mfma_probe", 0, 16, sink.data_ptr(), s)
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_mfma_probe", 8, 0, sink.data_ptr(), s)
+    host = torch.zeros(1, dtype=torch.int32)
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_mfma_probe", 8, 16, host.data_ptr(), s)
