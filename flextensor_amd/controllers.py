@@ -19,14 +19,16 @@ loaders.py:1194-1207) before the error propagates.
 from __future__ import annotations
 
 import logging
+import math
 from collections.abc import Mapping, Sequence
 from typing import Any
 
 import torch
+from torch.multiprocessing.reductions import StorageWeakRef
 
 from . import _native as nat
 from .allocation_block import AllocationBlock, AllocationManager, HostPinner
-from .layout import contiguous_strides, is_dense_layout, raw_storage_bytes, view_from_block
+from .layout import contiguous_strides, is_dense_layout, overlapping_views, raw_storage_bytes, view_from_block
 from .planner import TensorStatistics
 
 LOGGER = logging.getLogger(__name__)
@@ -58,23 +60,83 @@ def _cleanup_keeping_error(controller: Any, primary: BaseException) -> None:
             LOGGER.exception("could not attach the retryable cleanup handle to the primary error")
 
 
+class _Released:
+    """One packed-and-released source: the tensor object, its layout, a weak
+    reference to the storage it viewed, and the host view holding its bytes."""
+
+    __slots__ = ("source", "view", "size", "stride", "offset", "dtype", "device", "storage", "storage_nbytes")
+
+    def __init__(self, source: torch.Tensor, view: torch.Tensor) -> None:
+        storage = source.untyped_storage()
+        self.source, self.view = source, view
+        self.size, self.stride, self.offset = tuple(source.shape), source.stride(), source.storage_offset()
+        self.dtype, self.device = source.dtype, source.device
+        self.storage = StorageWeakRef(storage)  # weak: a released source must not keep its bytes alive
+        self.storage_nbytes = storage.nbytes()
+
+
 class _Rollback:
-    """Remembers packed-and-released sources so a failed build can restore them."""
+    """Puts packed-and-released sources back as they were when a build fails.
+
+    A source whose original storage is still alive (another tensor, a parameter
+    or a view's base aliases it) views that storage again at its own offset and
+    strides; the bytes there were never touched. Sources whose storage died
+    with the release get one new storage per original storage, of the original
+    size, and their bytes are copied back from the host block at their own
+    offsets and strides, so disjoint views of one storage share one storage
+    again. The tensor objects are the same throughout (``.data`` is re-pointed).
+    """
 
     def __init__(self) -> None:
-        self._entries: list[tuple[torch.Tensor, torch.Tensor]] = []  # (source, host view holding its bytes)
+        self._entries: list[_Released] = []
 
     def record(self, source: torch.Tensor, view: torch.Tensor) -> None:
-        self._entries.append((source, view))
+        """Call before ``source`` is released."""
+        self._entries.append(_Released(source, view))
 
     def restore(self) -> None:
-        for source, view in reversed(self._entries):
-            if source.numel() == 0 and view.numel() != 0:
-                source.data = view.detach().clone()
+        replacements: dict[StorageWeakRef, torch.UntypedStorage] = {}
+        for e in self._entries:
+            if e.source.numel() != 0 or math.prod(e.size) == 0:
+                continue  # not released, or nothing to restore
+            if not e.storage.expired():
+                storage = torch.UntypedStorage._new_with_weak_ptr(e.storage.cdata)  # the surviving original
+                fill = False
+            else:
+                storage = replacements.get(e.storage)
+                if storage is None:
+                    storage = torch.empty(e.storage_nbytes, dtype=torch.uint8, device=e.device).untyped_storage()
+                    replacements[e.storage] = storage
+                fill = True
+            restored = torch.empty(0, dtype=e.dtype, device=e.device)
+            restored.set_(storage, e.offset, e.size, e.stride)
+            if fill:
+                dst, src = restored, e.view
+                for d, st in enumerate(e.stride):  # an expanded source: write each element once
+                    if st == 0 and e.size[d] > 1:
+                        dst, src = dst.narrow(d, 0, 1), src.narrow(d, 0, 1)
+                dst.copy_(src)
+            e.source.data = restored
         self._entries.clear()
 
     def commit(self) -> None:
         self._entries.clear()
+
+
+def _refuse_overlapping_sources(tensors_map: Mapping[int, torch.Tensor],
+                                strategy_map: Mapping[str, Sequence[TensorStatistics]]) -> None:
+    """Each source is packed on its own, so distinct tensors with overlapping bytes would stop aliasing:
+    refuse them before any source is released (loaders.py:1217-1243). The check covers every tensor of
+    ``tensors_map``, planned or not; disjoint views of one storage and repeated references to one tensor
+    are fine."""
+    managed = [tensors_map[i.tensor_id] for infos in strategy_map.values() for i in infos
+               if i.tensor_id in tensors_map]
+    groups = overlapping_views(managed, tensors_map.values())
+    if groups:
+        ids = {id(t): k for k, t in tensors_map.items()}
+        shown = [sorted(ids.get(i, i) for i in g) for g in groups]
+        raise ValueError("Block loaders cannot preserve distinct tensor views sharing storage with overlapping "
+                         f"byte regions (tensor ids {shown}); give them separate storage (clone one)")
 
 
 def _unique_tensors(strategy: Sequence[TensorStatistics], tensors_map: Mapping[int, torch.Tensor]):
@@ -125,6 +187,7 @@ class AllocationBlockController:
         self.tensor_id_to_view_map: dict[int, torch.Tensor] = {}
         self._gpu_slots: list[AllocationBlock] = []
         self._rollback = _Rollback()
+        _refuse_overlapping_sources(tensors_map, strategy_map)
         try:
             for _slot_id, labels in allocation_ordered.items():
                 manager = AllocationManager(host_pinner=host_pinner, memory_alignment=memory_alignment,
@@ -253,6 +316,7 @@ class RawBlockController:
         self.label_to_tensor_views_map: dict[str, list[torch.Tensor]] = {}
         self.tensor_id_to_view_map: dict[int, torch.Tensor] = {}
         self._rollback = _Rollback()
+        _refuse_overlapping_sources(tensors_map, strategy_map)
         try:
             # device slots first: a failed allocation then leaves every source untouched
             self.block_map_gpu = {

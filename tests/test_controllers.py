@@ -314,3 +314,150 @@ def test_abort_construction_keeps_the_callers_error(monkeypatch):
     assert str(primary.__dict__["_flextensor_cleanup_error"]) == "first cleanup attempt failed"
     ctrl.shutdown()  # the retry
     assert torch.equal(tensors[1], want)
+
+
+# ---- construction rollback: the reference's cases (test_allocation_block_controller.py:32-489) -----------
+
+
+@pytest.mark.parametrize("commit", [False, True])
+def test_sources_are_released_in_the_build_and_restored_unless_committed(commit):
+    """test_allocation_block_controller.py:37-64: the build releases each source once its bytes are in the
+    host block; shutdown() before commit_construction() gives them back, after it they stay released."""
+    t = torch.arange(6, dtype=torch.float32)
+    want = t.clone()
+    ctrl = AllocationBlockController({0: ["layer.0"]}, torch.device("cpu"), {1: t}, {"layer.0": _stats(1, 24)},
+                                     {"layer.0": 0}, host_pinner=NO_PIN)
+    assert t.numel() == 0 and t.untyped_storage().nbytes() == 0
+    ctrl.schedule_transfer("layer.0", non_blocking=False)
+    assert torch.equal(ctrl.get_tensor_id_to_view_mapping()[1], want)
+    if commit:
+        ctrl.commit_construction()
+    ctrl.shutdown()
+    if commit:
+        assert t.numel() == 0
+    else:
+        assert torch.equal(t, want)
+
+
+def _fail_slot_creation(monkeypatch, check):
+    def fail(self, device):
+        check()
+        raise RuntimeError("gpu block creation failed")
+
+    monkeypatch.setattr(AllocationManager, "create_max_block", fail)
+
+
+@pytest.mark.parametrize("kind", ["private_slice", "external_parameter", "external_view", "expanded_view"])
+def test_failed_build_restores_layout_and_surviving_storage(monkeypatch, kind):
+    """test_allocation_block_controller.py:442-486: the same tensor object comes back with its offset,
+    strides and values; a storage another tensor still holds is viewed again (writes reach the alias), and
+    a private storage is not kept alive by the rollback while the build runs."""
+    from torch.multiprocessing.reductions import StorageWeakRef
+
+    backing = torch.arange(16.0)
+    w = backing[2:5].expand(4, 3) if kind == "expanded_view" else backing[2:14].view(3, 4).t()
+    if kind in ("private_slice", "external_parameter"):
+        w = torch.nn.Parameter(w, requires_grad=False)
+    external = torch.nn.Parameter(backing, requires_grad=False) if kind == "external_parameter" else None
+    del backing
+    ref = StorageWeakRef(w.untyped_storage())
+    want, want_stride, obj = w.clone(), w.stride(), id(w)
+
+    def during_build():
+        assert w.numel() == 0
+        assert ref.expired() == (kind == "private_slice")
+
+    _fail_slot_creation(monkeypatch, during_build)
+    with pytest.raises(RuntimeError, match="gpu block creation failed"):
+        AllocationBlockController({0: ["w"]}, torch.device("cpu"), {obj: w, -1: w},  # one tensor, two ids
+                                  {"w": _stats(obj, w.numel() * w.element_size())}, {"w": 0}, host_pinner=NO_PIN)
+    assert id(w) == obj
+    assert w.storage_offset() == 2 and w.stride() == want_stride and torch.equal(w, want)
+    if kind != "private_slice":
+        assert not ref.expired() and w.untyped_storage().data_ptr() == torch.UntypedStorage._new_with_weak_ptr(
+            ref.cdata).data_ptr()
+        with torch.no_grad():
+            w[0, 0] = 99
+        alias = external if external is not None else w._base
+        assert alias[2].item() == 99
+
+
+@pytest.mark.parametrize("keep_backing", [False, True])
+def test_failed_build_restores_disjoint_views_of_one_storage_then_retries(monkeypatch, keep_backing):
+    """test_allocation_block_controller.py:388-439: two parameters viewing disjoint parts of one storage
+    share one storage again after a failed build (the original one while it lives), and a retry builds."""
+    from torch.multiprocessing.reductions import StorageWeakRef
+
+    backing = torch.arange(16.0)
+    first = torch.nn.Parameter(backing[2:8].reshape(2, 3).t(), requires_grad=False)
+    second = torch.nn.Parameter(backing[8:12].view(torch.uint8), requires_grad=False)
+    tensors = {1: first, 2: second}
+    want = {k: t.clone() for k, t in tensors.items()}
+    layout = {k: (t.storage_offset(), t.stride()) for k, t in tensors.items()}
+    ref = StorageWeakRef(first.untyped_storage())
+    if not keep_backing:
+        del backing
+    args = ({0: ["left"], 1: ["right"]}, torch.device("cpu"), tensors,
+            {"left": _stats(1, 24), "right": _stats(2, 16)}, {"left": 0, "right": 1})
+    real = AllocationBlock.project_views
+
+    def fail(self, slot):
+        assert first.numel() == second.numel() == 0
+        assert ref.expired() is not keep_backing
+        raise RuntimeError("view projection failed")
+
+    monkeypatch.setattr(AllocationBlock, "project_views", fail)
+    with pytest.raises(RuntimeError, match="view projection failed"):
+        AllocationBlockController(*args, host_pinner=NO_PIN)
+    assert first.untyped_storage().data_ptr() == second.untyped_storage().data_ptr()
+    if keep_backing:
+        assert first.untyped_storage().data_ptr() == backing.untyped_storage().data_ptr()
+    for k, t in tensors.items():
+        assert torch.equal(t, want[k]) and (t.storage_offset(), t.stride()) == layout[k]
+    monkeypatch.setattr(AllocationBlock, "project_views", real)
+    retry = AllocationBlockController(*args, host_pinner=NO_PIN)
+    retry.commit_construction()
+    for label in ("left", "right"):
+        retry.schedule_transfer(label, non_blocking=False)
+    for k, view in retry.get_tensor_id_to_view_mapping().items():
+        assert torch.equal(view, want[k])
+    retry.shutdown()
+
+
+@pytest.mark.parametrize("placement", ["same_label", "other_slot", "not_planned"])
+@pytest.mark.parametrize("raw", [False, True])
+def test_overlapping_sources_are_refused_before_any_is_released(placement, raw):
+    """test_allocation_block_controller.py:347-385: distinct tensors with overlapping bytes are refused by the
+    controller itself, whether the second one is in the same label, in another slot or in no label at all,
+    and every source is left as it was."""
+    backing = torch.arange(8.0)
+    first = torch.nn.Parameter(backing[:4], requires_grad=False)
+    second = torch.nn.Parameter(backing[2:6], requires_grad=False)
+    tensors = {1: torch.arange(3.0), 2: first, 3: second}
+    want = {k: t.clone() for k, t in tensors.items()}
+    ptrs = {k: t.untyped_storage().data_ptr() for k, t in tensors.items()}
+    strategy = {"independent": _stats(1, 12), "left": _stats(2, 16)}
+    slots, l2b = {0: ["independent", "left"]}, {"independent": 0, "left": 0}
+    if placement == "same_label":
+        strategy["left"] = strategy["left"] + _stats(3, 16)
+    elif placement == "other_slot":
+        strategy["right"], slots[1], l2b["right"] = _stats(3, 16), ["right"], 1
+    with pytest.raises(ValueError, match="distinct tensor views sharing storage"):
+        if raw:
+            sizes = {x: 64 for x in strategy}
+            RawBlockController(sizes, {b: 64 for b in set(l2b.values())}, torch.device("cpu"), tensors, strategy, l2b,
+                               host_pinner=NO_PIN)
+        else:
+            AllocationBlockController(slots, torch.device("cpu"), tensors, strategy, l2b, host_pinner=NO_PIN)
+    assert first.storage_offset() == 0 and second.storage_offset() == 2
+    for k, t in tensors.items():
+        assert torch.equal(t, want[k]) and t.untyped_storage().data_ptr() == ptrs[k]
+
+
+def test_one_tensor_under_two_ids_is_not_an_overlap():
+    t = torch.arange(8.0)
+    ctrl = AllocationBlockController({0: ["a"]}, torch.device("cpu"), {1: t, 2: t}, {"a": _stats(1, 32)}, {"a": 0},
+                                     host_pinner=NO_PIN)
+    ctrl.schedule_transfer("a", non_blocking=False)
+    assert torch.equal(ctrl.get_tensor_id_to_view_mapping()[1], torch.arange(8.0))
+    ctrl.shutdown()
