@@ -312,3 +312,18 @@ def test_reordered_wait_precedes_compute_start():
         w = next(i for i, (n, a) in enumerate(calls) if n == "record_wait_start" and a[0] == label)
         c = next(i for i, (n, a) in enumerate(calls) if n == "record_compute_start" and a[0] == label)
         assert w < c, calls
+
+
+@BOTH
+def test_shutdown_synchronizes_before_the_blocks_go(kind):
+    """test_loaders_pin_fallback.py:287-299: the transfer stream is synchronized before the controller
+    releases the blocks its copies read."""
+    from tests.fakes import Entry
+
+    labels, t2c, l2b = SHORT
+    loader, rec = _loader(kind, labels, t2c, l2b)
+    loader.allocation_controller.shutdown = lambda: rec.log.append(Entry("shutdown", "host", "controller"))
+    _run(loader, rec, labels)
+    rec.log.clear()
+    loader.shutdown()
+    assert [(e.op, e.stream) for e in rec.log][-2:] == [("synchronize", "transfer"), ("shutdown", "host")], rec.dump()
