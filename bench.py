@@ -107,6 +107,31 @@ def bench_scatter(steps: int, warmup: int, chunk_mib: int, n_tensors: int, copy_
     return res
 
 
+def device_copy_probe(nbytes: int, reps: int = 10) -> dict:
+    """The runtime's own device-to-device copy (``Tensor.copy_`` -> ``hipMemcpyAsync``) of ``nbytes``: the plain
+    copy rate the scatter kernel (which reads and writes the same bytes) is compared with. Best of ``reps``,
+    HIP events on torch's stream; GB/s count bytes read plus bytes written."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        b.synchronize()
+        best = min(best, a.elapsed_time(b))
+    ok = bool(torch.equal(dst, src))
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "GBps": round(2 * nbytes / best / 1e6, 1), "ms": round(best, 4), "bit_exact": ok}
+
+
 def cpu_baseline_scatter(chunks, sample_chunks: int = 4, reps: int = 3, threads: int = 16) -> dict:
     """The oracle's byte scatter (memcpy per descriptor) over the first chunks of the same workload, on
     ``threads`` host threads: each thread scatters a contiguous share of each chunk's descriptors (the
@@ -1140,6 +1165,9 @@ def main() -> int:
                             "avg_launch_ms": round(res["scatter_avg_ms"], 4),
                             "algorithmic_bytes_per_launch": int(res["scatter_bytes_per_launch"]),
                             "workload": "scatter microbenchmark (the placement of every tensor outside the ring)"}
+        copy = device_copy_probe(args.chunk_mib * MiB)
+        line["roofline"]["device_copy_GBps"] = copy["GBps"]
+        line["roofline"]["frac_of_device_copy"] = round(res["scatter_hbm_GBps"] / copy["GBps"], 4)
         line["scatter"] = {
             "workload": "2000 bf16 tensors, log-uniform 4 KiB-64 MiB, seed 1, "
                         f"{args.chunk_mib} MiB pinned chunks, 2-slot ring, one scatter launch per chunk",
