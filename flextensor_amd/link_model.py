@@ -93,6 +93,30 @@ class MemoryTransferInterpolator:
         )
 
 
+def _human_bytes(n: int) -> str:
+    for unit, scale in (("GiB", 1 << 30), ("MiB", 1 << 20), ("KiB", 1 << 10)):
+        if n >= scale:
+            return f"{n / scale:.1f} {unit}"
+    return f"{n} B"
+
+
+def format_memory_transfer_table(memory_stats: dict[int, float]) -> str:
+    """The measured link curve ``{bytes: ms}`` as the diagnostic table of the reference
+    (memory_transfer_benchmark.py:26-56): a rule of ``=``, the title, the rule, column
+    headings, a rule of ``-``, one row per size in ascending order (bytes, the size in
+    binary units, milliseconds, GB/s) and a closing ``=`` rule."""
+    if not memory_stats:
+        return "No memory transfer statistics available."
+    rule = "=" * 110
+    out = [rule, "Memory Transfer Statistics", rule,
+           f"{'Size (bytes)':>14} {'Size':>10} {'Transfer (ms)':>14} {'Bandwidth (GB/s)':>17}", "-" * 110]
+    for n, ms in sorted(memory_stats.items()):
+        gbps = n / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        out.append(f"{n:>14} {_human_bytes(n):>10} {ms:>14.3f} {gbps:>17.3f}")
+    out.append(rule)
+    return "\n".join(out)
+
+
 def create_interpolator_from_benchmarks(memory_transfers: dict[int, float]) -> MemoryTransferInterpolator:
     return MemoryTransferInterpolator(memory_transfers)
 

@@ -57,7 +57,8 @@ from .allocation_block import HostPinner
 from .config import OffloadConfig
 from .controllers import AllocationBlockController, RawBlockController
 from .layout import overlapping_views
-from .link_model import LinkMeasurement, MemoryTransferInterpolator, link_probe_sizes, measure_link
+from .link_model import (LinkMeasurement, MemoryTransferInterpolator, format_memory_transfer_table, link_probe_sizes,
+                         measure_link)
 from .loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
 from .planner import (
     BlockStrategyData,
@@ -1552,6 +1553,7 @@ class OffloadManager:
             rows.append(f"{label:<32} {u.nbytes / 2**20:>10.2f} {self._duration(label):>9.3f}  {where}")
         if self.link is not None:
             rows.append(self.link.describe())
+            rows.append(format_memory_transfer_table(self.link.memory_transfer_stats()))
         probe = hip.transfer_stream_probe(self.device) if self.device is not None else None
         if probe is not None:
             rows.append(f"transfer stream: candidate {probe['chosen_candidate']} of {probe['attempts']} "
