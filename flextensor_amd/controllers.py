@@ -75,6 +75,16 @@ class _Released:
         self.storage_nbytes = storage.nbytes()
 
 
+def _surviving(ref: StorageWeakRef) -> torch.UntypedStorage | None:
+    """The storage behind ``ref`` if something else still holds it. Re-attaching
+    through a weak reference is private torch API (``_new_with_weak_ptr``); where
+    it is missing the source is restored into a new storage instead."""
+    if ref.expired():
+        return None
+    attach = getattr(torch.UntypedStorage, "_new_with_weak_ptr", None)
+    return attach(ref.cdata) if attach is not None else None
+
+
 class _Rollback:
     """Puts packed-and-released sources back as they were when a build fails.
 
@@ -99,9 +109,9 @@ class _Rollback:
         for e in self._entries:
             if e.source.numel() != 0 or math.prod(e.size) == 0:
                 continue  # not released, or nothing to restore
-            if not e.storage.expired():
-                storage = torch.UntypedStorage._new_with_weak_ptr(e.storage.cdata)  # the surviving original
-                fill = False
+            storage = _surviving(e.storage)
+            if storage is not None:
+                fill = False  # the original storage, whose bytes were never touched
             else:
                 storage = replacements.get(e.storage)
                 if storage is None:

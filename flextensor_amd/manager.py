@@ -1388,7 +1388,12 @@ class OffloadManager:
             link = LinkMeasurement.from_dict(state.copy_policy, source="profile")
         elif cfg.link_benchmark and cfg.copy_engine == "auto" and plan.streamed:
             largest = max(self._unit(x).nbytes for x in plan.streamed)
-            link = measure_link(link_probe_sizes(largest), self.device)
+            try:
+                link = measure_link(link_probe_sizes(largest), self.device)
+            except (nat.FtxError, RuntimeError) as exc:  # an optimisation only: stream with the default policy
+                LOGGER.warning("offload %r: measuring the host link failed (%s); keeping the default copy policy",
+                               self.name, exc)
+                torch.cuda.empty_cache()
         if link is None:
             return
         nat.set_copy_policy(link.kernel_max_bytes, link.split_min_bytes, link.n_copy_streams,

@@ -8,6 +8,7 @@ winner; the error names both threads) and tests/unit/test_gpu_memory_usage.py
 
 from __future__ import annotations
 
+import logging
 import threading
 from unittest import mock
 
@@ -481,3 +482,23 @@ def test_invalid_saved_policy_is_refused():
         L.LinkMeasurement.from_dict({"kernel_max_bytes": 1})
     with pytest.raises(ValueError, match="out-of-range"):
         L.LinkMeasurement.from_dict({"kernel_max_bytes": 0, "split_min_bytes": 0, "n_copy_streams": 99})
+
+
+def test_a_failed_link_measurement_keeps_the_default_policy(host_offload, caplog):
+    """Measuring the link is an optimisation: if it fails, streaming goes on with the library's policy."""
+    from flextensor_amd import _native as nat
+
+    mgr = host_offload("link-fails", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
+    mgr.order = [u.label for u in mgr.units]
+    plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
+
+    def fails(*a):
+        raise nat.FtxOutOfMemoryError(nat.FTX_ERR_OOM, "hipHostMalloc failed")
+
+    with mock.patch.object(M, "measure_link", fails), \
+            mock.patch.object(M.nat, "set_copy_policy", lambda *a: (_ for _ in ()).throw(AssertionError("set"))), \
+            mock.patch.object(M.torch.cuda, "empty_cache", lambda: None), \
+            caplog.at_level(logging.WARNING, logger="flextensor_amd.manager"):
+        mgr._choose_copy_policy(plan, None)
+    assert mgr.link is None and mgr.get_memory_transfer_stats() is None
+    assert "measuring the host link failed" in caplog.text
