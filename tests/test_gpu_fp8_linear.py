@@ -501,3 +501,29 @@ def test_prefill_group_matches_single_calls(gpu, default_config):
     grouped = hip.fp8_linear_group(xt, [d[0] for d in dev], [d[1] for d in dev])
     for (w, sc), y in zip(dev, grouped):
         assert torch.equal(y, hip.fp8_linear(xt, w, sc))  # same tiles, same K order
+
+
+def test_prefill_weight_over_2gib_takes_the_wide_address_path(gpu, default_config):
+    """A weight matrix over 2 GiB (65552 x 32768 fp8) runs the prefill kernel's 64-bit address form (the scalar-
+    base form needs 31-bit offsets); sampled outputs equal exact sums of the small-integer operands."""
+    from flextensor_amd import hip
+
+    m, n, k = 80, 65552, 32768
+    assert n * k >= 1 << 31
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    mag = torch.randint(0, 3, (n, k), dtype=torch.uint8, device=gpu, generator=gen)  # |w| in {0, 1, 2}
+    sign = torch.randint(0, 2, (n, k), dtype=torch.uint8, device=gpu, generator=gen)
+    w_raw = torch.where(mag == 0, torch.zeros_like(mag), (0x30 + 8 * mag) | (sign << 7))  # e4m3fn 1.0 = 0x38, 2.0 = 0x40
+    del sign
+    x = torch.randint(-3, 4, (m, k), device=gpu, generator=gen).to(torch.bfloat16)
+    scale = torch.ones(n, dtype=torch.bfloat16, device=gpu)
+    y = hip.fp8_linear(x, w_raw.view(torch.float8_e4m3fn), scale)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(4)
+    xs = x.float().cpu().numpy()
+    for i, j in zip(rng.integers(0, m, 24), np.concatenate([rng.integers(0, n, 20), [0, n - 1, n - 17, 40000]])):
+        wv = ofp8.decode_e4m3fn(w_raw[j].cpu().numpy())
+        exact = float(np.dot(xs[i].astype(np.float64), wv))
+        assert float(y[i, j].float()) == float(torch.tensor(exact).to(torch.bfloat16).float()), (i, j)
+    del w_raw, mag
+    torch.cuda.empty_cache()
