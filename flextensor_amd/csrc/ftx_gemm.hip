@@ -350,8 +350,8 @@ SegTable seg_table(const Fp8LinearLaunch &p) {
 //     LDS, three workgroups per CU);
 //   * at most one tile per CU: 8 waves (2 x 4, 64 x 32 each), 4 stages
 //     (96 KB, one workgroup per CU), so two waves share each SIMD; waves 0-3
-//     issue the loads (with all eight issuing them, the same kernel ran at
-//     half the load rate).
+//     issue the loads (all eight issuing them measured slower, by 5% to 50%
+//     over runs).
 // Both accumulate every output over the same MFMA sequence, so they give
 // identical results.
 //
