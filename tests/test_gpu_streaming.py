@@ -11,7 +11,6 @@ from __future__ import annotations
 
 import copy
 
-import numpy as np
 import pytest
 import torch
 

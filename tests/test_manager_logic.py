@@ -11,7 +11,7 @@ from torch import nn
 from flextensor_amd.config import OffloadConfig, load_config_from_env
 from flextensor_amd.manager import _Unit, plan_streaming, select_offload_units
 from flextensor_amd.planner import LayerStatistics, check_overlap_constraint, check_transfer_constraint
-from flextensor_amd.workloads import LlamaModel, LlamaShape, MLPStack
+from flextensor_amd.workloads import LlamaModel, LlamaShape
 
 
 def test_select_units_llama():

@@ -17,7 +17,7 @@ import pytest
 import torch
 from torch import nn
 
-from flextensor_amd.shm import HEADER, MAGIC, SharedSegment, SharedTensorStore, store_segment_name
+from flextensor_amd.shm import HEADER, SharedSegment, SharedTensorStore, store_segment_name
 
 
 class _Mixed(nn.Module):
