@@ -61,7 +61,8 @@ def test_staged_copy_is_refused_while_capturing(gpu):
     dst = torch.zeros(1 << 20, dtype=torch.uint8, device=gpu)
     side = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
-    with pytest.raises(nat.FtxError) as err:
+    # the refused copy leaves the capture empty, which torch reports as it closes the capture
+    with pytest.warns(UserWarning, match="empty"), pytest.raises(nat.FtxError) as err:
         with torch.cuda.graph(graph, stream=side):
             nat.copy_h2d(dst.data_ptr(), src.data_ptr(), src.numel(), nat.COPY_STAGED, side.cuda_stream)
     assert err.value.code == nat.FTX_ERR_UNSUPPORTED and "captured" in str(err.value)
