@@ -637,7 +637,25 @@ def bench_fp8_linear(batch: int = 8, reps: int = 20) -> dict:
     achieved = layer_bytes / layer_ms / 1e6
     del layers
     torch.cuda.empty_cache()
+    # the same four launches as plain streaming reads of each call's bytes (ftx_hbm_read_probe), two sets of
+    # buffers alternated as the layers are: what HBM gives this launch structure with no compute at all
+    from flextensor_amd import _native as nat
+
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    sizes = [(nbytes(names, k) + 15) // 16 * 16 for _, names, k in calls]
+    bufs = [[torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 256) for n in sizes] for _ in range(n_layers)]
+
+    def read_layer(i):
+        stream = torch.cuda.current_stream().cuda_stream
+        for buf in bufs[i % n_layers]:
+            nat.call("ftx_hbm_read_probe", buf.data_ptr(), buf.numel(), sink.data_ptr(), 2048, stream)
+
+    read_ms = graph_ms(read_layer, reps)
+    del bufs
+    torch.cuda.empty_cache()
     return {"batch": batch, "calls": per_call, "layer_us": round(layer_ms * 1e3, 2),
+            "plain_read_layer_us": round(read_ms * 1e3, 2),
+            "frac_of_plain_read": round(read_ms / layer_ms, 4),
             "layer_ungrouped_us": round(ungrouped_ms * 1e3, 2), "layer_dequant_gemm_us": round(dq_ms * 1e3, 2),
             "rel_err_vs_fp32": errs, "timing": f"HIP graph of {reps} layers (two layers' weights alternated), one replay",
             "roofline": {"kernel": "fp8_linear_kernel + fp8_linear_reduce_kernel (grouped q/k/v and gate/up)",
