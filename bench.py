@@ -356,7 +356,7 @@ def cpu_llama_decode_baseline(layers: int = 2, tokens: int = 4, context: int = 5
                       "scaled linearly to 32 layers"}
 
 
-def bench_dit(budget_gb: float, tokens: int, text: int, steps: int) -> dict:
+def bench_dit(budget_gb: float, tokens: int, text: int, steps: int, copy_engine: str = "auto") -> dict:
     """One Wan-style DiT denoising step, all 40 blocks resident, then streamed under ``budget_gb``.
 
     The resident step is measured with the whole model on the GPU (28 GB of
@@ -393,7 +393,7 @@ def bench_dit(budget_gb: float, tokens: int, text: int, steps: int) -> dict:
     mgr = OffloadManager("bench-dit")
     mgr.offload(model, OffloadConfig(include_patterns=["blocks.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
                                      profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9),
-                                     offload_timing="eager"))
+                                     offload_timing="eager", copy_engine=copy_engine))
     with torch.no_grad():
         xs = x[:, :2048].contiguous()
         model(xs, e, ctx)
@@ -422,6 +422,7 @@ def bench_dit(budget_gb: float, tokens: int, text: int, steps: int) -> dict:
         "wait_ms_per_step": rep.total_wait_sum / rep.num_passes,
         "link_GBps_during_transfer": streamed / (rep.total_transfer_sum / rep.num_passes * 1e-3) / 1e9,
         "streamed_bytes_per_step": streamed,
+        "timed_steps": steps, "streamed_block_bytes": sorted({mgr._unit(b).nbytes for b in plan.streamed}),
         "tflops_per_step": S.block_flops(tokens, text) * S.n_blocks / 1e12,
         "achieved_tflops": S.block_flops(tokens, text) * S.n_blocks / step / 1e12,
         "gpu_weight_bytes": mgr.get_gpu_memory_usage().total_bytes, "budget_bytes": int(budget_gb * 1e9),
@@ -1070,6 +1071,7 @@ def main() -> int:
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
     ap.add_argument("--staged-sweep", action="store_true",
                     help="only print host-to-device GB/s of the staged engine from pageable and shared memory")
+    ap.add_argument("--dit-only", action="store_true", help="print only the DiT leg (for profiling it alone)")
     ap.add_argument("--fp8-linear-only", action="store_true",
                     help="only print the fp8 linear roofline on the 70B-shape decode projections")
     ap.add_argument("--layers-70b", type=int, default=80)
@@ -1100,6 +1102,9 @@ def main() -> int:
         return 0
     if args.fp8_linear_only:
         print(json.dumps({"fp8_linear": bench_fp8_linear(), "fp8_prefill": bench_fp8_prefill()}), flush=True)
+        return 0
+    if args.dit_only:
+        print(json.dumps({"dit": bench_dit(12.0, args.dit_tokens, 512, args.dit_steps, args.copy_engine)}), flush=True)
         return 0
     if args.staged_sweep:
         print(json.dumps({"staged_sweep": staged_sweep()}), flush=True)
