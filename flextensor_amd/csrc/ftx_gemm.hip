@@ -336,9 +336,13 @@ SegTable seg_table(const Fp8LinearLaunch &p) {
 // 128 rows of 128 bytes, then the weight tile as 128 rows of 64 bytes. Each
 // load instruction writes 1 KB of LDS, lane l at +16 l, so the layout is
 // chosen by which global chunk each lane fetches:
-//   activation row R, 16-byte chunk c (k = 8c..8c+7) at slot c ^ (R & 7),
-//   weight row R,     16-byte chunk c (k = 16c..16c+15) at slot c ^ ((R >> 1) & 3),
-// which keeps the MFMA operand reads below free of bank conflicts.
+//   activation row R, 16-byte chunk c (k = 8c..8c+7) at slot c ^ rot3(R & 7),
+//     rot3(v) = (v & 3) << 1 | v >> 2 (a rotation of the row's low three bits),
+//   weight row R,     16-byte chunk c (k = 16c..16c+15) at slot c ^ ((R >> 1) & 3).
+// Both keep the MFMA operand reads below (ds_read_b128, 1 KB per wave) free
+// of bank conflicts on gfx950: 6 LDS cycles per read, measured with the
+// SQ_LDS_BANK_CONFLICT counter. The plain c ^ (R & 7) for the activations
+// costs 8, two of them bank-conflict cycles.
 //
 // k permutation within a step (any one that both operands share gives the
 // same sum): lane group g feeds k = 16g + 8kb + (0..7) to the kb-th of the
@@ -379,6 +383,9 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
   const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
   return join8(p0, p1, p2, p3);
 }
+
+// Activation-tile swizzle: rotate a row's low three bits (see the layout above).
+__device__ __forceinline__ int rot3(int v) { return ((v & 3) << 1) | ((v >> 2) & 1); }
 
 // s_waitcnt vmcnt(n) (expcnt and lgkmcnt left free); n is a constant at every call.
 __device__ __forceinline__ void wait_vmcnt(int n) {
@@ -434,7 +441,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_prefill_kernel(const uint8_t *
 
   // This lane's load sources: activation rows (lw*4 + t)*8 + lane/8, weight
   // rows (lw*2 + t)*16 + lane/4, at the chunk the swizzle assigns.
-  const int xc = ((lane & 7) ^ (lane >> 3)) * 8;            // k offset (elements) within a step
+  const int xc = ((lane & 7) ^ rot3(lane >> 3)) * 8;        // k offset (elements) within a step
   const int wc = ((lane & 3) ^ ((lane >> 3) & 3)) * 16;     // k offset (bytes) within a step
   const uint8_t *xrow[4];
   const uint8_t *wrow[2];
@@ -501,8 +508,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_prefill_kernel(const uint8_t *
 #pragma unroll
   for (int j = 0; j < JT; ++j) {
     const int R = wm * WROWS + j * 16 + r;
-    boff0[j] = R * 128 + (((2 * g) ^ (R & 7)) << 4);
-    boff1[j] = R * 128 + (((2 * g + 1) ^ (R & 7)) << 4);
+    boff0[j] = R * 128 + (((2 * g) ^ rot3(R & 7)) << 4);
+    boff1[j] = R * 128 + (((2 * g + 1) ^ rot3(R & 7)) << 4);
   }
 
   f32x4 acc[4][JT];
