@@ -61,8 +61,10 @@ class HostPinner:
         return block
 
     def pin_in_place(self, block: torch.Tensor) -> torch.Tensor:
-        ptr = block.data_ptr()
-        nbytes = block.untyped_storage().nbytes()
+        """Page-lock the whole storage behind ``block`` once; views of a storage
+        already registered register nothing (host_pinning.py:96-122)."""
+        storage = block.untyped_storage()
+        ptr, nbytes = storage.data_ptr(), storage.nbytes()
         with self._lock:
             if ptr in self._registered:
                 return block
@@ -70,18 +72,44 @@ class HostPinner:
             self._registered[ptr] = (nbytes, block)
         return block
 
+    @staticmethod
+    def _should_skip_pin(tensor: torch.Tensor) -> bool:
+        """Non-CPU, meta and empty tensors cannot be pinned and already pinned ones
+        need not be (host_pinning.py:57-65)."""
+        if tensor.device.type != "cpu" or tensor.is_meta or tensor.numel() == 0:
+            return True
+        return bool(tensor.is_pinned())
+
     def pin(self, tensor: torch.Tensor) -> torch.Tensor:
-        """A pinned tensor with the same contents (``torch`` mode copies, ``host_register`` pins in place)."""
-        if not self.enabled:
+        """A pinned tensor with the same contents: ``torch`` mode returns a pinned
+        copy, ``host_register`` pins the storage in place and returns ``tensor``.
+        Tensors that cannot or need not be pinned come back unchanged, and a
+        failure to pin raises (host_pinning.py:28-54)."""
+        if not self.enabled or self._should_skip_pin(tensor):
             return tensor
         if self.mode == "host_register":
-            if not tensor.is_contiguous():
-                raise ValueError("host_register pinning needs a contiguous tensor")
             return self.pin_in_place(tensor)
         block = self.new_block(tensor.numel() * tensor.element_size())
         out = view_from_block(block, tensor.dtype, tuple(tensor.shape), 0, None)
         out.copy_(tensor)
         return out
+
+    def is_pinned(self, tensor: torch.Tensor) -> bool:
+        """``tensor.is_pinned()``, or in ``host_register`` mode whether this pinner
+        registered the tensor's storage (registration does not set torch's flag).
+        A tensor whose storage yields no pointer reads as not pinned
+        (host_pinning.py:67-88)."""
+        if tensor.is_pinned():
+            return True
+        if self.mode != "host_register":
+            return False
+        try:
+            ptr = tensor.untyped_storage().data_ptr()
+        except Exception:  # noqa: BLE001 - lazy or fake tensors without a storage pointer
+            LOGGER.debug("HostPinner.is_pinned: the tensor's storage has no data pointer; treating it as not pinned")
+            return False
+        with self._lock:
+            return ptr in self._registered
 
     def release(self, ptr: int) -> None:
         with self._lock:
