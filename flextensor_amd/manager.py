@@ -330,6 +330,51 @@ def plan_from_state(state: TensorManagerState, units: Sequence[_Unit], base_byte
     return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
 
 
+# Attributes every nn.Module gets from its constructor (parameters, buffers,
+# children, hooks); anything else in a module's __dict__ belongs to the model.
+_MODULE_INTERNALS = frozenset(vars(nn.Module()))
+
+
+def plain_tensors(model: nn.Module) -> list[torch.Tensor]:
+    """Tensors the model reaches that are neither parameters nor buffers.
+
+    These are plain tensor attributes of its modules and tensors held in lists,
+    tuples, sets, dicts or plain objects under them. They go to the GPU like
+    the reference's unmapped tensors (tensor_processors.py:324-360,685-742).
+    The walk reads and never rebinds. Types, Python module objects and
+    nn.Modules are not entered; every module is visited through
+    ``model.modules()``. Each object is visited once, so cycles end. Returns
+    each tensor once, in first-seen order.
+    """
+    skip = (type, types.ModuleType, nn.Module, str, bytes, int, float, complex, bool, type(None))
+    registered = {id(t) for t in model.parameters()} | {id(t) for t in model.buffers()}
+    found: dict[int, torch.Tensor] = {}
+    seen: set[int] = set()
+    for module in model.modules():
+        stack = [v for k, v in reversed(list(vars(module).items())) if k not in _MODULE_INTERNALS]
+        while stack:
+            value = stack.pop()
+            if isinstance(value, torch.Tensor):
+                if id(value) not in registered:
+                    found.setdefault(id(value), value)
+                continue
+            if isinstance(value, skip) or id(value) in seen:
+                continue
+            seen.add(id(value))
+            if isinstance(value, dict):
+                stack.extend(reversed(list(value.values())))
+            elif isinstance(value, (list, tuple)):
+                stack.extend(reversed(value))
+            elif isinstance(value, (set, frozenset)):
+                stack.extend(value)
+            elif getattr(type(value), "__dictoffset__", 0) != 0:
+                try:
+                    stack.extend(reversed(list(vars(value).values())))
+                except TypeError:
+                    pass
+    return list(found.values())
+
+
 @contextlib.contextmanager
 def _oom_context(tensors: Sequence[torch.Tensor], what: str, advice: str) -> Iterator[None]:
     """Re-raise a device allocation failure naming what was being placed (tensor_manager.py:755-775)."""
@@ -371,6 +416,7 @@ class OffloadManager:
         self._hooks: list[Any] = []
         self._patched: list[tuple[nn.Module, Any]] = []
         self._resident_bytes = 0
+        self._plain: list[torch.Tensor] = []  # plain tensors moved to the GPU by offload(); release() returns them
         self._cpu_data: dict[int, torch.Tensor] = {}
         self._seen_this_pass: list[str] = []
         self._events: dict[str, tuple[Any, Any]] = {}
@@ -471,7 +517,9 @@ class OffloadManager:
             if self._manual:
                 # manual offload blocks: parameters wait on the host until discovery sees where they are used
                 self._pending = {id(p): p for p in model.parameters() if p.device.type == "cpu"}
-                self._resident_bytes += self._upload_into([b for b in model.buffers() if b.device.type == "cpu"])
+                self._plain = [t for t in plain_tensors(model) if t.device.type == "cpu"]
+                self._resident_bytes += self._upload_into([b for b in model.buffers() if b.device.type == "cpu"]
+                                                          + self._plain)
                 self._patch_root(model)
             else:
                 self._place_outside_units(unit_params)
@@ -529,6 +577,7 @@ class OffloadManager:
         self._cpu_data = {}
         self._forwards = 0
         self._resident_bytes = 0
+        self._plain = []
         self._from_state = False
         self._reload_pending = False
         self.skip_discovery_honored = None
@@ -890,6 +939,9 @@ class OffloadManager:
         if preserve_model:
             for b in self.model.buffers():
                 b.data = b.data.cpu()
+            for t in self._plain:
+                t.data = t.data.cpu()
+        self._plain = []
         if self._mode is not None:
             self._mode_depth = 1
             self._pop_mode()
@@ -922,14 +974,18 @@ class OffloadManager:
         return block.views
 
     def _place_outside_units(self, unit_params: set[int]) -> None:
-        """Tensors outside the offload units go to the GPU once (stream-and-scatter)."""
+        """Tensors outside the offload units go to the GPU once (stream-and-scatter): parameters and
+        buffers of no unit, and every plain tensor the model reaches (tensor_manager.py:2547-2565)."""
         assert self.model is not None
         rest = [p for p in self.model.parameters() if id(p) not in unit_params and p.device.type == "cpu"]
         bufs = [b for b in self.model.buffers() if b.device.type == "cpu"]
-        with _oom_context(rest + bufs, "tensors outside the offload units", "Tensors outside the offload units "
-                          "(not matching include_patterns, or matching exclude_patterns) stay on the GPU for good. "
-                          "Broaden include_patterns or narrow exclude_patterns."):
-            self._resident_bytes += self._upload_into(rest + bufs)
+        plain = [t for t in plain_tensors(self.model) if t.device.type == "cpu"]  # never streamed
+        self._plain = plain
+        with _oom_context(rest + bufs + plain, "tensors outside the offload units", "Tensors outside the offload "
+                          "units (not matching include_patterns, or matching exclude_patterns, and tensors that are "
+                          "not parameters or buffers) stay on the GPU for good. Broaden include_patterns or narrow "
+                          "exclude_patterns."):
+            self._resident_bytes += self._upload_into(rest + bufs + plain)
 
     def _upload_into(self, tensors: Sequence[torch.Tensor]) -> int:
         cpu = [t for t in tensors if t.device.type == "cpu" and t.numel()]

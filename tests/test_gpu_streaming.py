@@ -46,6 +46,49 @@ def _stream(model, device, **cfg):
     return mgr
 
 
+class _Shifted(torch.nn.Module):
+    """An MLP stack whose forward also reads tensors that are neither parameters nor buffers."""
+
+    def __init__(self, stack):
+        super().__init__()
+        self.stack = stack
+        hidden = stack.layers[0].fc1.in_features
+        self.gain = torch.linspace(0.5, 1.5, hidden).to(torch.bfloat16)  # a plain attribute
+        self.extra = {"shift": [torch.full((hidden,), 0.25, dtype=torch.bfloat16)]}  # inside containers
+
+    def forward(self, x):
+        return self.stack(x * self.gain + self.extra["shift"][0])
+
+
+def test_plain_tensor_attributes_go_to_the_gpu_and_back(gpu):
+    """Tensors the model reaches outside its parameters and buffers are placed on the GPU once, keep
+    their identity (every alias sees the device copy), count as unmapped bytes, and return to the host
+    on release (tensor_processors.py:685-742, tensor_manager.py:2547-2565)."""
+    model = _Shifted(_small_mlp())
+    gain, shift = model.gain, model.extra["shift"][0]
+    gain_host, shift_host = gain.clone(), shift.clone()
+    ref = copy.deepcopy(model).to(gpu)  # .to() moves parameters and buffers only
+    ref.gain = ref.gain.to(gpu)
+    ref.extra["shift"][0] = ref.extra["shift"][0].to(gpu)
+    x = W.mlp_input(16, 256, seed=5).to(gpu)
+    with torch.no_grad():
+        want = ref(x)
+    mgr = _stream(model, gpu, include_patterns=["stack.layers.*"])
+    assert model.gain is gain and model.extra["shift"][0] is shift
+    assert gain.device.type == "cuda" and shift.device.type == "cuda"
+    with torch.no_grad():
+        outs = [model(x) for _ in range(4)]
+    torch.cuda.synchronize()
+    assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.streamed
+    for out in outs:
+        assert torch.equal(out, want)
+    plain_bytes = gain.numel() * gain.element_size() + shift.numel() * shift.element_size()
+    assert mgr.get_gpu_memory_usage().unmapped_tensors_bytes >= plain_bytes
+    mgr.release()
+    assert gain.device.type == "cpu" and torch.equal(gain, gain_host)
+    assert shift.device.type == "cpu" and torch.equal(shift, shift_host)
+
+
 @pytest.mark.parametrize("copy_engine", ["auto", "sdma", "kernel"])
 @pytest.mark.parametrize("transfer_mode", ["allocation_block_transfer", "raw_block_transfer"])
 def test_mlp_streamed_equals_resident(gpu, copy_engine, transfer_mode):

@@ -9,7 +9,7 @@ import torch
 from torch import nn
 
 from flextensor_amd.config import OffloadConfig, load_config_from_env
-from flextensor_amd.manager import _Unit, plan_streaming, select_offload_units
+from flextensor_amd.manager import _Unit, plain_tensors, plan_streaming, select_offload_units
 from flextensor_amd.planner import LayerStatistics, check_overlap_constraint, check_transfer_constraint
 from flextensor_amd.workloads import LlamaModel, LlamaShape
 
@@ -143,3 +143,38 @@ def test_plan_budget_exhausted_by_outside_tensors_names_the_reservation():
     with pytest.raises(RuntimeError, match=r"budget=2499 bytes, reserved_outside_units=500 bytes, "
                                            r"effective_budget=1999 bytes, minimum_ring=2000 bytes"):
         plan_streaming(units, order, budget=2499, base_bytes=500, num_blocks=2)
+
+
+def test_plain_tensors_reaches_attributes_and_containers_once():
+    """The tensors outside parameters and buffers that go to the GPU with the rest of the model: plain
+    attributes, tensors in lists, tuples, dicts and plain objects, each once (the reference's unmapped
+    tensors, tensor_processors.py:324-360,685-742; its reachable-tensor cases in
+    tests/unit/test_tensor_processors.py:293-356,513-553)."""
+
+    class Holder:
+        pass
+
+    class M(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.lin = nn.Linear(4, 4)
+            self.register_buffer("b", torch.zeros(3))
+            self.plain = torch.ones(2)
+            self.alias = self.plain
+            self.lst = [torch.ones(5), (torch.ones(6), {"k": torch.ones(7)})]
+            self.lst.append(self.lst)  # a list that holds itself
+            h = Holder()
+            h.t, h.me = torch.ones(8), h
+            self.holder = h
+            self.tied = self.lin.weight  # a parameter: placed with the parameters
+            self.buf_ref = [self.b]  # a buffer: placed with the buffers
+            self.namespace = torch  # a Python module is not entered
+            self.child = nn.Sequential(nn.Linear(2, 2))
+
+    m = M()
+    m.child.extra = torch.ones(9)  # a plain attribute of a submodule
+    got = plain_tensors(m)
+    assert [tuple(t.shape) for t in got] == [(2,), (5,), (6,), (7,), (8,), (9,)]
+    assert got[0] is m.plain and got[4] is m.holder.t
+    registered = {id(t) for t in m.parameters()} | {id(t) for t in m.buffers()}
+    assert not any(id(t) in registered for t in got)
