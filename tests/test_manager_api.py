@@ -251,7 +251,8 @@ def test_patched_forward_runs_on_a_copy_of_the_module(names):
 
 def test_budget_is_capped_by_available_memory(caplog):
     """gpu_budget.py:66-113: the fractional budget never exceeds free memory plus the allocator cache
-    (plus what the manager already placed); below 256 MiB available it refuses."""
+    (plus what the manager already placed); a negative cache counts as none; below 256 MiB available it
+    refuses (the reference's tests/unit/test_resolve_gpu_budget.py:14-113 cases)."""
     GiB = 2**30
     mgr = M.OffloadManager("budget")
     mgr.device = torch.device("cuda", 0)
@@ -273,6 +274,10 @@ def test_budget_is_capped_by_available_memory(caplog):
     mgr.config = OffloadConfig(max_gpu_mem_bytes=8 * GiB)
     with a, b, c:
         assert mgr._budget() == 8 * GiB
+    mgr.config = OffloadConfig(max_gpu_mem_fraction=0.9)
+    a2, b2, c2 = state(200 * GiB, 288 * GiB, 2 * GiB, 7 * GiB)  # allocated above reserved: no reusable cache
+    with a2, b2, c2:
+        assert mgr._budget() == (200 + 0 + 1) * GiB
     mgr.config = OffloadConfig()
     assert mgr._budget() is None
     mgr.config = OffloadConfig(max_gpu_mem_fraction=0.9)
