@@ -52,6 +52,21 @@ def is_dense_layout(t: torch.Tensor) -> bool:
     return span == t.numel()
 
 
+def is_packed_layout(shape: Sequence[int], stride: Sequence[int]) -> bool:
+    """Whether a shape/stride pair with non-negative strides covers one gap-free,
+    non-overlapping span: taking the dimensions longer than 1 in increasing
+    stride order, each stride equals the element count of the dimensions before
+    it (utils.py:86-98). Empty shapes qualify."""
+    if any(int(n) == 0 for n in shape):
+        return True
+    span = 1
+    for n, s in sorted(((int(n), int(s)) for n, s in zip(shape, stride) if int(n) > 1), key=lambda d: d[1]):
+        if s != span:
+            return False
+        span *= n
+    return True
+
+
 def contiguous_strides(shape: Sequence[int]) -> tuple[int, ...]:
     strides = []
     acc = 1

@@ -29,6 +29,7 @@ from typing import Any, ClassVar
 
 import torch
 
+from .layout import is_packed_layout
 from .planner import BlockStrategyData, LayerStatistics, TensorStatistics
 
 PROFILE_FILE = "profile.json"
@@ -115,8 +116,16 @@ class TensorManagerState:
             if not isinstance(lay, dict) or set(lay) != {"shape", "stride"}:
                 raise bad(f"invalid layout metadata for {name!r}: expected shape and stride")
             shape, stride = lay["shape"], lay["stride"]
-            if len(shape) != len(stride) or any(type(x) is not int or x < 0 for x in [*shape, *stride]):
-                raise bad(f"invalid layout metadata for {name!r}")
+            if not isinstance(shape, list) or not isinstance(stride, list) or len(shape) != len(stride) or \
+                    any(type(x) is not int or x < 0 for x in [*shape, *stride]):
+                raise bad(f"invalid layout metadata for {name!r}: shape and stride must be equal-length lists of "
+                          "non-negative integers")
+            if not is_packed_layout(shape, stride):
+                raise bad(f"invalid layout metadata for {name!r}: tensor layout must be non-overlapping and dense")
+            try:  # sizes and strides torch can represent (utils.py:101-111, state_handler.py:271-276)
+                torch.empty_strided(shape, stride, device="meta")
+            except (RuntimeError, OverflowError, TypeError, ValueError) as exc:
+                raise bad(f"invalid layout metadata for {name!r}: {exc}") from exc
         if set(self.gpu_tensors_names) != known - managed:
             raise bad("gpu_tensors_names does not match computed final-GPU inventory: "
                       f"missing={sorted((known - managed) - set(self.gpu_tensors_names))}, "

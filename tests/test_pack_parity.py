@@ -59,3 +59,25 @@ def test_pack_into_matches_the_oracle(seed):
     for v, t in zip(views, tensors):
         assert torch.equal(v.view(torch.uint8) if v.dtype == torch.float8_e4m3fn else v,
                            t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t)
+
+
+def test_packed_layout_rule_matches_brute_force():
+    """layout.is_packed_layout (utils.py:86-98) against enumerating every element offset: a layout is
+    packed exactly when its offsets are 0..numel-1, each once. All ranks up to 3, sizes 0-3, strides 0-7."""
+    import itertools
+
+    from flextensor_amd.layout import is_packed_layout
+
+    checked = 0
+    for rank in range(4):
+        for shape in itertools.product(range(4), repeat=rank):
+            for stride in itertools.product(range(8), repeat=rank):
+                n = 1
+                for d in shape:
+                    n *= d
+                offsets = sorted(sum(i * s for i, s in zip(idx, stride))
+                                 for idx in itertools.product(*(range(d) for d in shape)))
+                want = n == 0 or offsets == list(range(n))
+                assert is_packed_layout(shape, stride) == want, (shape, stride)
+                checked += 1
+    assert checked > 30000

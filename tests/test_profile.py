@@ -9,6 +9,7 @@ same slot plan, streamed set and loader order as the planner produced.
 from __future__ import annotations
 
 import json
+import struct
 
 import pytest
 import torch
@@ -137,6 +138,112 @@ def test_non_object_json_rejected(tmp_path):
     (tmp_path / PROFILE_FILE).write_text("[1, 2]")
     with pytest.raises(ValueError, match="JSON object"):
         load_state(tmp_path)
+
+
+# ---- managed tensor metadata (tests/unit/test_state_handler_shm.py) ------------------------
+
+
+def _block_state() -> TensorManagerState:
+    """tests/unit/test_state_handler_shm.py:16-44: an allocation-block plan of two labels."""
+    ts = [TensorStatistics(0, "layer0.weight", 1024, 0.1), TensorStatistics(1, "layer1.weight", 2048, 0.2),
+          TensorStatistics(2, "layer2.weight", 512, 0.05)]
+    return TensorManagerState(
+        loader_type="allocation_block_transfer",
+        tensor_id_to_name_map={0: "layer0.weight", 1: "layer1.weight", 2: "layer2.weight"},
+        allocation_ordered={0: ["trap_0"], 1: ["trap_1"]},
+        label_to_size_map={"trap_0": 3072, "trap_1": 512},
+        block_sizes={0: 3072, 1: 512},
+        load_strategy={"trap_0": ts[:2], "trap_1": ts[2:]},
+        release_strategy={"trap_0": ts[:2], "trap_1": ts[2:]},
+        label_to_block_id={"trap_0": 0, "trap_1": 1},
+        stats=[LayerStatistics("trap_0", ts[:2], 1.0), LayerStatistics("trap_1", ts[2:], 0.5)],
+        transfer_to_compute_map={"trap_0": "trap_0", "trap_1": "trap_1"},
+        view_tensors_ids=[0, 1, 2],
+        view_tensors_names=["layer0.weight", "layer1.weight", "layer2.weight"],
+        gpu_tensors_names=[],
+        shm_block_name_map=None,
+    )
+
+
+def test_block_state_round_trips_and_legacy_metadata_loads():
+    data = _block_state().to_dict()
+    assert data["version"] == 3 and TensorManagerState.from_dict(data).to_dict() == data
+    data.pop("managed_tensor_dtypes")
+    data.pop("managed_tensor_layouts")
+    legacy = TensorManagerState.from_dict(data)
+    assert legacy.managed_tensor_dtypes == {} and legacy.managed_tensor_layouts == {}
+
+
+@pytest.mark.parametrize("first_layout", [{"shape": [16, 16], "stride": [1, 16]}, {"shape": [16, 16], "stride": [16, 1]},
+                                          {"shape": [1, 256], "stride": [0, 1]},
+                                          {"shape": [4, 4, 16], "stride": [4, 1, 16]}])
+def test_mixed_dtypes_and_packed_layouts_round_trip_through_bytes(first_layout):
+    st = _block_state()
+    st.managed_tensor_dtypes = {"layer0.weight": "float32", "layer1.weight": "bfloat16",
+                                "layer2.weight": "float8_e4m3fn"}
+    st.managed_tensor_layouts = {"layer0.weight": first_layout, "layer1.weight": {"shape": [32, 32], "stride": [32, 1]},
+                                 "layer2.weight": {"shape": [512], "stride": [1]}}
+    back = load_state_from_bytes(save_state_to_bytes(st))
+    assert back.managed_tensor_dtypes == st.managed_tensor_dtypes
+    assert back.managed_tensor_layouts == st.managed_tensor_layouts
+
+
+@pytest.mark.parametrize("table,entry", [("managed_tensor_layouts", {"shape": [256], "stride": [1]}),
+                                         ("managed_tensor_dtypes", "float32")])
+def test_metadata_must_cover_every_managed_tensor(table, entry):
+    data = _block_state().to_dict()
+    data[table] = {"layer0.weight": entry}
+    with pytest.raises(ValueError, match=table + r".*cover every managed tensor"):
+        TensorManagerState.from_dict(data)
+
+
+@pytest.mark.parametrize("layout", [{"shape": [256]}, {"shape": [16, 16], "stride": [1]}, {"shape": [-256], "stride": [1]},
+                                    {"shape": [256], "stride": [-1]}, {"shape": [256], "stride": [2]},
+                                    {"shape": [256], "stride": [0]}, {"shape": [True], "stride": [1]},
+                                    {"shape": [256], "stride": [True]}, {"shape": [3, 3], "stride": [2, 2]},
+                                    {"shape": [1, 256], "stride": [2**64, 1]}])
+def test_layouts_that_are_not_packed_are_rejected(layout):
+    """Gaps, overlaps, negative or boolean values, rank mismatches and strides past int64 (:105-127)."""
+    data = _block_state().to_dict()
+    data["managed_tensor_layouts"] = {"layer0.weight": layout, "layer1.weight": {"shape": [512], "stride": [1]},
+                                      "layer2.weight": {"shape": [128], "stride": [1]}}
+    with pytest.raises(ValueError, match="invalid layout metadata"):
+        TensorManagerState.from_dict(data)
+
+
+@pytest.mark.parametrize("dtype_name", ["not_a_torch_dtype", "Tensor", "", "float"])
+def test_dtype_names_must_be_canonical_torch_dtypes(dtype_name):
+    data = _block_state().to_dict()
+    data["managed_tensor_dtypes"] = {"layer0.weight": "float32", "layer1.weight": dtype_name,
+                                     "layer2.weight": "float32"}
+    with pytest.raises(ValueError, match=r"invalid dtype metadata for 'layer1.weight'"):
+        TensorManagerState.from_dict(data)
+
+
+def test_state_loads_from_a_shared_memory_buffer():
+    """:169-183: the bytes form read back out of a POSIX shared-memory segment."""
+    from multiprocessing.shared_memory import SharedMemory
+
+    st = _block_state()
+    blob = save_state_to_bytes(st)
+    shm = SharedMemory(create=True, size=len(blob) + 1024)
+    try:
+        shm.buf[:len(blob)] = blob
+        back = load_state_from_bytes(bytes(shm.buf[:len(blob)]))
+        assert back.allocation_ordered == st.allocation_ordered and back.label_to_block_id == st.label_to_block_id
+        assert [(t.name, t.size_bytes) for t in back.load_strategy["trap_0"]] == \
+            [(t.name, t.size_bytes) for t in st.load_strategy["trap_0"]]
+        assert [(x.label, x.duration) for x in back.stats] == [(x.label, x.duration) for x in st.stats]
+    finally:
+        shm.close()
+        shm.unlink()
+
+
+def test_short_buffers_name_what_is_missing():
+    with pytest.raises(ValueError, match=r"Buffer too short.*length prefix"):
+        load_state_from_bytes(b"")
+    with pytest.raises(ValueError, match=r"Buffer too short.*1000 bytes"):
+        load_state_from_bytes(struct.pack("!I", 1000) + b"x" * 10)
 
 
 # ---- bytes form -------------------------------------------------------------------
