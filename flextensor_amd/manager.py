@@ -75,6 +75,7 @@ from .profile import TensorManagerState, load_state, save_state
 from .scatter import upload_tensors
 from .selection import select_offload_units
 from .timing import OffloadTimingCollector, OffloadTimingReport
+from .transfer import TransferStreamSynchronizationError
 
 LOGGER = logging.getLogger(__name__)
 DEFAULT_MANAGER_NAME = "default"
@@ -901,7 +902,15 @@ class OffloadManager:
         return True
 
     def release(self, preserve_model: bool = True) -> None:
-        """Stop streaming and hand the model back (tensors on the CPU when preserved)."""
+        """Stop streaming and hand the model back (tensors on the CPU when preserved).
+
+        In the reference's order (tensor_manager.py:2377-2421): the tensors are
+        put back first, then the loader shuts down and the in-place pins end.
+        A loader that fails to shut down still has the pins released before its
+        error is raised again; a pin-release failure on top of it is only
+        logged. A transfer stream that cannot be synchronised keeps the pins,
+        since a copy may still read them. The manager is reset in every case.
+        """
         self._check_thread()
         if self.model is None:
             return
@@ -925,37 +934,55 @@ class OffloadManager:
                         shared.add(tid)
         params = {id(p): p for u in self.units for p in u.params}
         params.update({id(p): p for p in self.model.parameters()})
-        if self.loader is not None:
-            self.loader.shutdown()
-        for tid, p in params.items():
-            if not preserve_model:
-                p.data = torch.empty(0, dtype=p.dtype)
-            elif tid in restore:
-                # the host block's own view (tensor_manager.py:2320-2354): no second copy of the model;
-                # a shared-memory block is copied out so the parameter does not keep other processes' segment
-                p.data = restore[tid].clone() if tid in shared else restore[tid]
-            elif p.device.type != "cpu":
-                p.data = p.data.cpu()
-        if preserve_model:
-            for b in self.model.buffers():
-                b.data = b.data.cpu()
-            for t in self._plain:
-                t.data = t.data.cpu()
-        self._plain = []
-        if self._mode is not None:
-            self._mode_depth = 1
-            self._pop_mode()
-        self._reset_manual()
-        self._release_pins()
-        self._from_state = False
-        self._reload_pending = False
-        self.skip_discovery_honored = None
-        self.loader = self.controller = self.plan = None
-        self.link = None
-        self._pass_done = []
-        self.model = None
-        self.units, self._patched, self._hooks = [], [], []
-        self.phase = OffloadPhase.NOT_INITIALIZED
+        teardown_error: Exception | None = None
+        try:
+            for tid, p in params.items():
+                if not preserve_model:
+                    p.data = torch.empty(0, dtype=p.dtype)
+                elif tid in restore:
+                    # the host block's own view (tensor_manager.py:2320-2354): no second copy of the model;
+                    # a shared-memory block is copied out so the parameter does not keep other processes' segment
+                    p.data = restore[tid].clone() if tid in shared else restore[tid]
+                elif p.device.type != "cpu":
+                    p.data = p.data.cpu()
+            if preserve_model:
+                for b in self.model.buffers():
+                    b.data = b.data.cpu()
+                for t in self._plain:
+                    t.data = t.data.cpu()
+            try:
+                if self.loader is not None:
+                    self.loader.shutdown()
+            except TransferStreamSynchronizationError:
+                self._pinner = None  # a copy may still read the pinned blocks: their pins stay
+                raise
+            except Exception as exc:  # noqa: BLE001 - raised again once the pins are released
+                teardown_error = exc
+            try:
+                self._release_pins()
+            except Exception:
+                if teardown_error is None:
+                    raise
+                LOGGER.exception("offload %r: host pinner release_all() failed after the loader shutdown failed; "
+                                 "the remaining pins stay until the process exits", self.name)
+        finally:
+            self._plain = []
+            if self._mode is not None:
+                self._mode_depth = 1
+                self._pop_mode()
+            self._reset_manual()
+            self._pinner = None
+            self._from_state = False
+            self._reload_pending = False
+            self.skip_discovery_honored = None
+            self.loader = self.controller = self.plan = None
+            self.link = None
+            self._pass_done = []
+            self.model = None
+            self.units, self._patched, self._hooks = [], [], []
+            self.phase = OffloadPhase.NOT_INITIALIZED
+        if teardown_error is not None:
+            raise teardown_error
 
     # -- internals ------------------------------------------------------------
 

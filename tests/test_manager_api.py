@@ -507,3 +507,85 @@ def test_a_failed_link_measurement_keeps_the_default_policy(host_offload, caplog
         mgr._choose_copy_policy(plan, None)
     assert mgr.link is None and mgr.get_memory_transfer_stats() is None
     assert "measuring the host link failed" in caplog.text
+
+
+# ---- release() when teardown fails (tests/unit/test_tensor_manager_pinned_memory_mode.py:306-420) ----
+
+
+def _inference_manager(monkeypatch, name, loader, pinner):
+    """A manager that holds a small host model as if it were streaming it: no GPU needed."""
+    monkeypatch.setattr(M.torch.cuda, "synchronize", lambda *a, **k: None)
+    mgr = M.OffloadManager(name)
+    mgr.model = torch.nn.Sequential(torch.nn.Linear(4, 4))
+    mgr.device = torch.device("cuda", 0)
+    mgr.loader, mgr._pinner = loader, pinner
+    mgr.phase = M.OffloadPhase.INFERENCE
+    return mgr
+
+
+def _assert_reset(mgr):
+    assert mgr.model is None and mgr.loader is None and mgr._pinner is None
+    assert mgr.phase == M.OffloadPhase.NOT_INITIALIZED
+
+
+def test_release_ends_pins_and_reraises_when_the_loader_shutdown_fails(monkeypatch):
+    loader, pinner = mock.MagicMock(), mock.MagicMock()
+    loader.shutdown.side_effect = RuntimeError("simulated SHM teardown failure")
+    mgr = _inference_manager(monkeypatch, "rel-loader", loader, pinner)
+    with pytest.raises(RuntimeError, match="simulated SHM teardown failure"):
+        mgr.release()
+    loader.shutdown.assert_called_once()
+    pinner.release_all.assert_called_once()
+    _assert_reset(mgr)
+
+
+def test_release_raises_a_pin_release_failure_when_the_loader_shut_down(monkeypatch):
+    pinner = mock.MagicMock()
+    pinner.release_all.side_effect = RuntimeError("pin release failed")
+    mgr = _inference_manager(monkeypatch, "rel-pins", mock.MagicMock(), pinner)
+    with pytest.raises(RuntimeError, match="pin release failed"):
+        mgr.release()
+    _assert_reset(mgr)
+
+
+def test_release_keeps_the_loader_error_when_the_pins_fail_too(monkeypatch, caplog):
+    loader, pinner = mock.MagicMock(), mock.MagicMock()
+    loader.shutdown.side_effect = RuntimeError("ROOT CAUSE: SHM teardown failure")
+    pinner.release_all.side_effect = RuntimeError("CLEANUP NOISE")
+    mgr = _inference_manager(monkeypatch, "rel-both", loader, pinner)
+    with caplog.at_level(logging.ERROR, logger="flextensor_amd.manager"), pytest.raises(RuntimeError, match="ROOT CAUSE"):
+        mgr.release()
+    errors = [r for r in caplog.records if r.levelno == logging.ERROR]
+    assert errors and any("release_all" in r.getMessage() for r in errors)
+    assert any(r.exc_info is not None for r in errors)
+    _assert_reset(mgr)
+
+
+def test_release_keeps_the_pins_when_the_transfer_stream_cannot_be_synchronised(monkeypatch):
+    from flextensor_amd.transfer import TransferStreamSynchronizationError
+
+    loader, pinner = mock.MagicMock(), mock.MagicMock()
+    loader.shutdown.side_effect = TransferStreamSynchronizationError("transfer sync failed")
+    mgr = _inference_manager(monkeypatch, "rel-sync", loader, pinner)
+    with pytest.raises(RuntimeError, match="transfer sync failed"):
+        mgr.release()
+    pinner.release_all.assert_not_called()  # a copy may still read the pinned blocks
+    _assert_reset(mgr)
+
+
+def test_release_puts_the_tensors_back_before_the_loader_goes(monkeypatch):
+    """A parameter views its host block again before the loader shuts down (tensor_manager.py:2398-2401)."""
+    seen = []
+    loader = mock.MagicMock()
+    mgr = _inference_manager(monkeypatch, "rel-order", loader, None)
+    weight = mgr.model[0].weight
+    host_view = torch.full_like(weight, 7.0)  # the label's host block view of this parameter
+    controller = mock.MagicMock()
+    controller.block_map_cpu = {"0": mock.MagicMock(shm_segment=None)}
+    controller.label_to_cpu_tensor_id_map = {"0": [id(weight)]}
+    mgr.controller = controller
+    monkeypatch.setattr(mgr, "_cpu_views", lambda label: [host_view])
+    loader.shutdown.side_effect = lambda: seen.append(weight.data_ptr() == host_view.data_ptr())
+    mgr.release()
+    assert seen == [True] and torch.equal(weight, host_view)
+    _assert_reset(mgr)
