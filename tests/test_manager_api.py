@@ -589,3 +589,19 @@ def test_release_puts_the_tensors_back_before_the_loader_goes(monkeypatch):
     mgr.release()
     assert seen == [True] and torch.equal(weight, host_view)
     _assert_reset(mgr)
+
+
+def test_disabled_offload_hands_the_model_back_untouched():
+    """OffloadConfig(enabled=False) is the reference's no-op manager (tests/unit/test_offload_manager_phase.py:620-638):
+    the model comes back as it was, its forward runs as before, and nothing needs the GPU library."""
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(torch.nn.Linear(8, 8), torch.nn.ReLU(), torch.nn.Linear(8, 2))
+    before = {n: p.detach().clone() for n, p in model.named_parameters()}
+    x = torch.randn(3, 8)
+    want = model(x)
+    mgr = M.OffloadManager("disabled")
+    out = mgr.offload(model, OffloadConfig(enabled=False, include_patterns=["0"]))
+    assert out is model and mgr.phase == M.OffloadPhase.NOT_INITIALIZED
+    assert torch.equal(model(x), want)
+    assert all(torch.equal(p, before[n]) and p.device.type == "cpu" for n, p in model.named_parameters())
+    mgr.release()  # nothing to release
