@@ -376,6 +376,24 @@ def plain_tensors(model: nn.Module) -> list[torch.Tensor]:
     return list(found.values())
 
 
+def shared_unit_parameters(model: nn.Module, labels: Sequence[str]) -> dict[int, list[str]]:
+    """Parameters that the modules of two or more offload units hold (tied weights): id -> unit labels.
+
+    A streamed parameter lives in its unit's ring slot only while that unit
+    runs, so a parameter another unit also reads would be read from a slot the
+    ring has since refilled. The reference promotes such cross-layer tensors to
+    permanent GPU residence (tensor_manager.py:226-272); these do the same.
+    """
+    owners: dict[int, list[str]] = {}
+    for label in labels:
+        mod = _submodule(model, label)
+        if mod is None:
+            continue
+        for pid in {id(q) for q in mod.parameters()}:
+            owners.setdefault(pid, []).append(label)
+    return {pid: units for pid, units in owners.items() if len(units) > 1}
+
+
 @contextlib.contextmanager
 def _oom_context(tensors: Sequence[torch.Tensor], what: str, advice: str) -> Iterator[None]:
     """Re-raise a device allocation failure naming what was being placed (tensor_manager.py:755-775)."""
@@ -485,9 +503,16 @@ class OffloadManager:
         unit_params: set[int] = set()
         by_name = dict(model.named_parameters())
         saved = {st.label: [t.name for t in st.tensors] for st in state.stats} if state is not None else {}
+        shared = shared_unit_parameters(model, labels)
+        if shared:
+            mib = sum(by_name[name_of[pid]].numel() * by_name[name_of[pid]].element_size() for pid in shared) / 2**20
+            LOGGER.warning("offload %r: %d parameter(s) belong to more than one offload unit and stay on the GPU for "
+                           "good (offload coverage reduced by %.2f MiB): %s", self.name, len(shared), mib,
+                           ", ".join(f"{name_of[pid]} ({' + '.join(u)})" for pid, u in list(shared.items())[:8]))
         for label in labels:
             mod = _submodule(model, label)
-            params = [p for p in mod.parameters() if id(p) not in unit_params] if mod is not None else []
+            params = [p for p in mod.parameters() if id(p) not in unit_params and id(p) not in shared] \
+                if mod is not None else []
             names = [name_of[id(p)] for p in params]
             if state is not None and (mod is None or names != saved[label]):
                 # a manual offload block of the saved plan: its tensors by name

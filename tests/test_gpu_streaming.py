@@ -89,6 +89,33 @@ def test_plain_tensor_attributes_go_to_the_gpu_and_back(gpu):
     assert shift.device.type == "cpu" and torch.equal(shift, shift_host)
 
 
+def test_weights_tied_across_units_stay_resident(gpu, caplog):
+    """A parameter held by two streamed units would be read from a ring slot that another unit has since
+    refilled; it stays on the GPU for good instead, with a warning, as the reference promotes tensors read
+    outside their owning layer (tensor_manager.py:226-272). Outputs stay bitwise equal to resident."""
+    model = _small_mlp()
+    model.layers[4].fc1.weight = model.layers[1].fc1.weight  # tied: one Parameter in two units
+    tied = model.layers[1].fc1.weight
+    ref = _resident(model, gpu)  # deepcopy keeps the tie
+    assert ref.layers[4].fc1.weight is ref.layers[1].fc1.weight
+    x = W.mlp_input(16, 256, seed=9).to(gpu)
+    with torch.no_grad():
+        want = ref(x)
+    with caplog.at_level("WARNING", logger="flextensor_amd.manager"):
+        mgr = _stream(model, gpu)
+    assert "more than one offload unit" in caplog.text and "layers.1.fc1.weight" in caplog.text
+    assert tied.device.type == "cuda" and all(tied is not q for u in mgr.units for q in u.params)
+    with torch.no_grad():
+        outs = [model(x) for _ in range(5)]
+    torch.cuda.synchronize()
+    assert mgr.phase == OffloadPhase.INFERENCE and len(mgr.plan.streamed) == 6
+    for out in outs:
+        assert torch.equal(out, want)
+    assert mgr.get_gpu_memory_usage().unmapped_tensors_bytes >= tied.numel() * tied.element_size()
+    mgr.release()
+    assert tied.device.type == "cpu" and torch.equal(tied, ref.layers[1].fc1.weight.cpu())
+
+
 @pytest.mark.parametrize("copy_engine", ["auto", "sdma", "kernel"])
 @pytest.mark.parametrize("transfer_mode", ["allocation_block_transfer", "raw_block_transfer"])
 def test_mlp_streamed_equals_resident(gpu, copy_engine, transfer_mode):

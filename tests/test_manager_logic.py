@@ -7,7 +7,7 @@ import torch
 from torch import nn
 
 from flextensor_amd.config import OffloadConfig, load_config_from_env
-from flextensor_amd.manager import _Unit, plain_tensors, plan_streaming, select_offload_units
+from flextensor_amd.manager import _Unit, plain_tensors, plan_streaming, select_offload_units, shared_unit_parameters
 from flextensor_amd.planner import LayerStatistics, check_overlap_constraint, check_transfer_constraint
 from flextensor_amd.workloads import LlamaModel, LlamaShape
 
@@ -176,3 +176,20 @@ def test_plain_tensors_reaches_attributes_and_containers_once():
     assert got[0] is m.plain and got[4] is m.holder.t
     registered = {id(t) for t in m.parameters()} | {id(t) for t in m.buffers()}
     assert not any(id(t) in registered for t in got)
+
+
+def test_parameters_held_by_two_units_are_found():
+    """Tied weights (one Parameter registered in two units' modules) are reported with every unit holding
+    them; a module reused under one name is not a tie."""
+    m = nn.Module()
+    m.layers = nn.ModuleList(nn.Linear(4, 4) for _ in range(4))
+    m.layers[3].weight = m.layers[0].weight
+    m.layers[2].bias = m.layers[1].bias
+    labels = [f"layers.{i}" for i in range(4)]
+    got = shared_unit_parameters(m, labels)
+    assert got == {id(m.layers[0].weight): ["layers.0", "layers.3"], id(m.layers[1].bias): ["layers.1", "layers.2"]}
+    assert shared_unit_parameters(m, ["layers.0", "layers.1"]) == {}
+    n = nn.Module()
+    block = nn.Linear(4, 4)
+    n.a, n.b = block, nn.Linear(4, 4)
+    assert shared_unit_parameters(n, ["a", "b"]) == {}
