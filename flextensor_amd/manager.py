@@ -73,7 +73,7 @@ from .planner import (
 from .prefetch_policy import PiecewisePrefetchPolicy
 from .profile import TensorManagerState, load_state, save_state
 from .scatter import upload_tensors
-from .selection import select_offload_units
+from .selection import parameter_filter, select_offload_units
 from .timing import OffloadTimingCollector, OffloadTimingReport
 from .transfer import TransferStreamSynchronizationError
 
@@ -509,10 +509,16 @@ class OffloadManager:
             LOGGER.warning("offload %r: %d parameter(s) belong to more than one offload unit and stay on the GPU for "
                            "good (offload coverage reduced by %.2f MiB): %s", self.name, len(shared), mib,
                            ", ".join(f"{name_of[pid]} ({' + '.join(u)})" for pid, u in list(shared.items())[:8]))
+        streamed = parameter_filter(model, self.config.include_patterns, self.config.exclude_patterns)
         for label in labels:
             mod = _submodule(model, label)
-            params = [p for p in mod.parameters() if id(p) not in unit_params and id(p) not in shared] \
-                if mod is not None else []
+            params = []
+            if mod is not None:
+                kept = [(n, q) for n, q in mod.named_parameters() if id(q) not in unit_params and id(q) not in shared]
+                params = [q for n, q in kept if streamed(f"{label}.{n}")]
+                if kept and not params and state is None:
+                    LOGGER.warning("offload %r: include/exclude patterns leave unit %r no parameter to stream; its "
+                                   "parameters stay on the GPU", self.name, label)
             names = [name_of[id(p)] for p in params]
             if state is not None and (mod is None or names != saved[label]):
                 # a manual offload block of the saved plan: its tensors by name

@@ -29,7 +29,7 @@ from __future__ import annotations
 import functools
 import logging
 import re
-from collections.abc import Sequence
+from collections.abc import Callable, Sequence
 
 from torch import nn
 
@@ -117,6 +117,40 @@ def _pattern_matched(model: nn.Module, pattern: str, module_paths: Sequence[str]
         return any(class_matches(type(m), classes) for p, m in model.named_modules() if p)
     return (any(path_matches(m, names[0], recursive_star=recursive) for m in module_paths)
             or bool(_param_paths(model, names[0])))
+
+
+def prefix_matches(path: str, patterns: Sequence[str]) -> bool:
+    """Whether a prefix of the dotted ``path`` (the whole path included) matches one of the path
+    ``patterns``, a lone ``*`` spanning segments (tensor_discovery.py:288-307): a module pattern
+    covers every parameter below that module."""
+    parts = path.split(".")
+    return any(path_matches(".".join(parts[:i]), p, recursive_star=True)
+               for i in range(1, len(parts) + 1) for p in patterns)
+
+
+def parameter_filter(model: nn.Module, include: Sequence[str], exclude: Sequence[str]) -> Callable[[str], bool]:
+    """``path -> bool``: whether the parameter at ``path`` is streamed with its unit.
+
+    Included when a prefix of its path matches an include path pattern or an
+    ancestor module's class matches an include ``class:`` pattern; dropped
+    when an exclude pattern matches the same way (tensor_discovery.py:326-372,
+    647-700). Parameters a unit does not stream stay on the GPU.
+    """
+    inc_names, inc_classes = partition(list(include) or ["*"])
+    ex_names, ex_classes = partition(list(exclude))
+    inc_paths = {p for p, m in model.named_modules() if p and inc_classes and class_matches(type(m), inc_classes)}
+    ex_paths = {p for p, m in model.named_modules() if p and ex_classes and class_matches(type(m), ex_classes)}
+
+    def under(path: str, paths: set[str]) -> bool:
+        parts = path.split(".")
+        return bool(paths) and any(".".join(parts[:i]) in paths for i in range(1, len(parts) + 1))
+
+    def streamed(path: str) -> bool:
+        if not (prefix_matches(path, inc_names) or under(path, inc_paths)):
+            return False
+        return not ((ex_names and prefix_matches(path, ex_names)) or under(path, ex_paths))
+
+    return streamed
 
 
 def select_offload_units(model: nn.Module, include: Sequence[str], exclude: Sequence[str]) -> list[str]:

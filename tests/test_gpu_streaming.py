@@ -89,6 +89,31 @@ def test_plain_tensor_attributes_go_to_the_gpu_and_back(gpu):
     assert shift.device.type == "cpu" and torch.equal(shift, shift_host)
 
 
+@pytest.mark.parametrize("include,exclude,kept", [(["layers.*.weight"], [], {"fc1.weight", "fc2.weight"}),
+                                                   (["layers.*"], ["layers.*.fc2"], {"fc1.weight", "fc1.bias"})])
+def test_patterns_choose_the_parameters_a_unit_streams(gpu, include, exclude, kept):
+    """Only the parameters that the include patterns name and the exclude patterns leave stream with their
+    unit; the rest of the unit stays on the GPU (tensor_discovery.py:326-372,647-700)."""
+    model = _small_mlp()
+    ref = _resident(model, gpu)
+    x = W.mlp_input(16, 256, seed=11).to(gpu)
+    with torch.no_grad():
+        want = ref(x)
+    mgr = _stream(model, gpu, include_patterns=include, exclude_patterns=exclude)
+    assert [u.label for u in mgr.units] == [f"layers.{i}" for i in range(6)]
+    for u in mgr.units:
+        assert {n.removeprefix(u.label + ".") for n in u.names} == kept
+    streamed = {id(q) for u in mgr.units for q in u.params}
+    assert all(p.device.type == "cuda" for p in model.parameters() if id(p) not in streamed)
+    with torch.no_grad():
+        outs = [model(x) for _ in range(4)]
+    torch.cuda.synchronize()
+    assert mgr.phase == OffloadPhase.INFERENCE and len(mgr.plan.streamed) == 6
+    for out in outs:
+        assert torch.equal(out, want)
+    mgr.release()
+
+
 def test_weights_tied_across_units_stay_resident(gpu, caplog):
     """A parameter held by two streamed units would be read from a ring slot that another unit has since
     refilled; it stays on the GPU for good instead, with a warning, as the reference promotes tensors read

@@ -12,7 +12,8 @@ import pytest
 import torch
 from torch import nn
 
-from flextensor_amd.selection import module_patterns, partition, path_matches, select_offload_units
+from flextensor_amd.selection import (module_patterns, parameter_filter, partition, path_matches, prefix_matches,
+                                      select_offload_units)
 
 
 class SimpleLayer(nn.Module):
@@ -191,3 +192,98 @@ def test_unmatched_patterns_warn_and_empty_selections_log_errors(caplog):
     with caplog.at_level("WARNING", logger="flextensor_amd.selection"):
         assert select_offload_units(m, [], []) == []
     assert "empty list" in caplog.text and "No modules matched" not in caplog.text
+
+
+# ---- which parameters of a unit stream (tests/unit/test_tensor_discovery.py) ----------------------
+
+
+@pytest.mark.parametrize("path,patterns,want", [
+    ("layers.0.weight", ["*"], True), ("head.bias", ["*"], True),
+    ("layers.0.weight", ["layers.*"], True), ("layers.0.bias", ["layers.*"], True), ("head.weight", ["layers.*"], False),
+    ("layers.0.weight", ["*.weight"], True), ("layers.0.bias", ["*.weight"], False),
+    ("layers.0.attn.weight", ["layers.*.attn.weight"], True), ("layers.0.attn.bias", ["layers.*.attn.weight"], False),
+    ("layers.0.mlp.weight", ["layers.*.attn.weight"], False),
+    ("layers.0.attn.q_proj.weight", ["layers.*"], True), ("layers.0.mlp.gate.weight", ["layers.*"], True),
+    ("embed.weight", ["layers.*"], False),
+    ("layers.0.attn.q_proj.weight", ["*.weight"], True), ("layers.0.attn.q_proj.bias", ["*.weight"], False),
+    ("layers.0.attn.q_proj.weight", ["layers.*.attn"], True), ("layers.0.attn.k_proj.bias", ["layers.*.attn"], True),
+    ("layers.0.mlp.gate.weight", ["layers.*.attn"], False),
+    ("layer1.weight", ["*layer*"], True), ("my_layer.bias", ["*layer*"], True), ("layers.0.weight", ["*layer*"], True),
+    ("head.weight", ["*layer*"], False), ("embed.bias", ["*layer*"], False),
+])
+def test_prefix_matching(path, patterns, want):
+    """_any_prefix_matches cases, :1413-1470."""
+    assert prefix_matches(path, patterns) is want
+
+
+@pytest.mark.parametrize("path,include,exclude,want", [
+    ("layers.0.weight", ["*"], [], True),
+    ("layers.0.weight", ["*.bias"], [], False), ("layers.0.weight", ["*.bias"], ["*.weight"], False),
+    ("layers.0.weight", ["*"], ["*.weight"], False),
+    ("layers.0.bias", ["*.bias"], [], True),
+    ("layers.0.attn.q.weight", ["layers.*"], [], True), ("embed.weight", ["layers.*"], [], False),
+    ("layers.0.attn.q.weight", ["*"], ["layers.*"], False), ("embed.weight", ["*"], ["layers.*"], True),
+    ("layers.0.mlp.weight", ["layers.*"], ["layers.*.attn"], True),
+    ("layers.0.attn.q.weight", ["layers.*"], ["layers.*.attn"], False),
+    ("layers.0.weight", ["*.weight"], ["layers.0.*"], False),
+    ("my_layer.weight", ["*layer*"], [], True), ("my_layer.weight", ["*layer*"], ["*layer*"], False),
+    ("my_layer.weight", ["*layer*"], ["*weight*"], True),  # a leaf segment is not a prefix of its own
+])
+def test_parameter_included_and_not_excluded(path, include, exclude, want):
+    """_should_offload_param cases, :1475-1530."""
+    assert parameter_filter(nn.Module(), include, exclude)(path) is want
+
+
+class _Bar(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.linear = nn.Linear(10, 10)
+
+
+class _Inner(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.bar = _Bar()
+        self.norm = nn.LayerNorm(10)
+
+
+def _nested():
+    m = nn.Module()
+    m.foo = nn.ModuleDict({"layers": nn.ModuleList([_Inner(), _Inner()])})
+    return m
+
+
+@pytest.mark.parametrize("exclude", [["foo.layers.0.bar"], ["foo.layers.*.bar"]])
+def test_excluded_module_inside_a_unit_keeps_its_parameters_out(exclude):
+    """:1139-1193: excluding a submodule of a unit drops all of its parameters and keeps the rest."""
+    m = _nested()
+    keep = parameter_filter(m, ["*"], exclude)
+    names = [n for n, _ in m.foo["layers"][0].named_parameters()]
+    streamed = {n for n in names if keep(f"foo.layers.0.{n}")}
+    assert streamed == {"norm.weight", "norm.bias"}
+
+
+def test_class_patterns_cover_the_parameters_below_the_class():
+    m = _nested()
+    keep = parameter_filter(m, ["class:_Inner"], ["class:LayerNorm"])
+    assert keep("foo.layers.1.bar.linear.weight") and not keep("foo.layers.1.norm.bias")
+    assert not parameter_filter(m, ["class:LayerNorm"], [])("foo.layers.0.bar.linear.bias")
+
+
+def test_parameter_patterns_choose_units_and_their_parameters():
+    """:79-116 with the parameter filter: the owning modules become units, and only the named parameters
+    of them stream."""
+    class Model(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.encoder = nn.Sequential(nn.Linear(4, 4), nn.ReLU(), nn.Linear(4, 4))
+            self.head = nn.Linear(4, 2)
+
+    m = Model()
+    include, exclude = ["encoder.0.weight", "encoder.2.weight", "head"], ["encoder.2"]
+    assert set(select_offload_units(m, include, exclude)) == {"encoder.0", "head"}
+    keep = parameter_filter(m, include, exclude)
+    assert [n for n, _ in m.named_parameters() if keep(n)] == ["encoder.0.weight", "head.weight", "head.bias"]
+    assert set(select_offload_units(m, ["class:Linear"], ["head"])) == {"encoder.0", "encoder.2"}
+    assert set(select_offload_units(m, ["encoder", "encoder.*"], [])) == {"encoder"}
+    assert select_offload_units(m, ["encoder.9.weight"], []) == []
