@@ -444,6 +444,8 @@ class OffloadManager:
         self.compile_fn: Callable[[nn.Module], Any] | None = None
         self._load_from_shm = False
         self._suspend_count = 0  # profiling suspensions outstanding (reference-counted)
+        # what init()/offload() set up: None before either, "noop" for enabled=False, else "live"
+        self._control: str | None = None
         self._from_state = False
         self._reload_pending = False
         self._pinner: HostPinner | None = None
@@ -484,6 +486,7 @@ class OffloadManager:
         if compile_fn is not None and not callable(compile_fn):
             raise TypeError("compile_fn must be callable: module -> compiled module")
         self.config = config or OffloadConfig()
+        self._control = "live" if self.config.enabled else "noop"
         if load_from_shm and (state is None or not self.config.shm_enabled or not state.shm_block_name_map):
             raise ValueError("load_from_shm needs shm_enabled and a saved state that names its shared blocks")
         if self.config.enabled and self.config.pinned_memory and self.config.pinned_memory_mode == "host_register":
@@ -610,6 +613,7 @@ class OffloadManager:
         self._forwards = 0
         self._resident_bytes = 0
         self._plain = []
+        self._control, self._suspend_count = None, 0
         self._from_state = False
         self._reload_pending = False
         self.skip_discovery_honored = None
@@ -820,6 +824,7 @@ class OffloadManager:
     def init(self, config: OffloadConfig | None = None) -> None:
         """Set the configuration before ``offload`` (offload_manager.py:2853-2856)."""
         self.set_config(config or OffloadConfig())
+        self._control = "live" if self.config.enabled else "noop"
 
     def set_config(self, config: OffloadConfig) -> None:
         """Replace the configuration; refused once a model is managed (offload_manager.py:2887-2895)."""
@@ -893,9 +898,18 @@ class OffloadManager:
         visit("", self.model, True)
         return tuple(out)
 
+    def _profiling_control(self, what: str) -> bool:
+        """Whether profiling control acts: refused before ``init``/``offload``, inert for a disabled
+        offload, as the reference's no-op manager (offload_manager.py:2521-2620)."""
+        if self._control is None:
+            raise RuntimeError(f"{what}() called before flextensor.offload(...); call flextensor.offload(model, "
+                               "config=...) first.")
+        return self._control == "live"
+
     def clear_profiling_durations(self) -> None:
         """Drop every profiled duration; the unit order found by discovery stays (offload_manager.py:3131-3141)."""
-        self.durations.clear()
+        if self._profiling_control("clear_profiling_durations"):
+            self.durations.clear()
 
     def suspend_profiling(self) -> None:
         """Stop recording profiling passes until the matching :meth:`resume_profiling`.
@@ -903,16 +917,26 @@ class OffloadManager:
         Suspensions nest. A suspended profiling pass records no durations and
         does not count against ``profiling_iters`` (offload_manager.py:3144-3184).
         """
-        self._suspend_count += 1
+        if self._profiling_control("suspend_profiling"):
+            self._suspend_count += 1
 
     def resume_profiling(self) -> None:
+        if not self._profiling_control("resume_profiling"):
+            return
         if self._suspend_count == 0:
             raise RuntimeError("resume_profiling() without a matching suspend_profiling()")
         self._suspend_count -= 1
 
+    def is_profiling_suspended(self) -> bool:
+        """Whether a suspension is outstanding; always False for a disabled offload."""
+        return self._control == "live" and self._suspend_count > 0
+
     @contextlib.contextmanager
     def pause_profiling(self) -> Iterator[None]:
         """Context-manager form of suspend/resume (offload_manager.py:3199-3220)."""
+        if not self._profiling_control("pause_profiling"):
+            yield
+            return
         self.suspend_profiling()
         try:
             yield
@@ -944,6 +968,7 @@ class OffloadManager:
         """
         self._check_thread()
         if self.model is None:
+            self._control, self._suspend_count = None, 0
             return
         torch.cuda.synchronize(self.device)
         custom_ops.unregister_manager(id(self))
@@ -998,6 +1023,8 @@ class OffloadManager:
                                  "the remaining pins stay until the process exits", self.name)
         finally:
             self._plain = []
+            self._suspend_count = 0
+            self._control = None
             if self._mode is not None:
                 self._mode_depth = 1
                 self._pop_mode()

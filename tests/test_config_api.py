@@ -12,6 +12,7 @@ from __future__ import annotations
 import json
 
 import pytest
+import torch
 
 import flextensor_amd as ft
 from flextensor_amd.config import OffloadConfig, load_config, load_config_from_env, load_config_from_file
@@ -129,15 +130,44 @@ def test_timing_tables():
 
 
 def test_profiling_suspension_is_reference_counted():
+    """tests/unit/test_profiling_control.py:67-133,409-445: control needs init() or offload() first; then
+    suspensions nest, an unbalanced resume raises, and release() forgets them."""
     mgr = ft.OffloadManager("suspend-test")
-    with pytest.raises(RuntimeError):
+    for call in (mgr.suspend_profiling, mgr.resume_profiling, mgr.clear_profiling_durations):
+        with pytest.raises(RuntimeError, match=rf"{call.__name__}\(\) called before flextensor\.offload"):
+            call()
+    with pytest.raises(RuntimeError, match=r"pause_profiling\(\) called before flextensor\.offload"):
+        with mgr.pause_profiling():
+            pass
+    mgr.init(OffloadConfig())
+    with pytest.raises(RuntimeError, match="without a matching"):
         mgr.resume_profiling()
     mgr.suspend_profiling()
     with mgr.pause_profiling():
-        assert mgr._suspend_count == 2
+        assert mgr._suspend_count == 2 and mgr.is_profiling_suspended()
     assert mgr._suspend_count == 1
     mgr.resume_profiling()
-    assert mgr._suspend_count == 0
+    assert mgr._suspend_count == 0 and not mgr.is_profiling_suspended()
+    mgr.suspend_profiling()
+    mgr.release()
+    assert not mgr.is_profiling_suspended()
+    with pytest.raises(RuntimeError, match="called before flextensor.offload"):
+        mgr.suspend_profiling()
+
+
+def test_profiling_control_is_inert_when_offload_is_disabled():
+    """tests/unit/test_profiling_control.py:357-400: the disabled manager accepts every call and is never
+    suspended."""
+    mgr = ft.OffloadManager("suspend-noop")
+    model = torch.nn.Linear(2, 2)
+    assert mgr.offload(model, OffloadConfig(enabled=False)) is model
+    mgr.resume_profiling()  # no matching suspend needed
+    mgr.suspend_profiling()
+    assert not mgr.is_profiling_suspended()
+    with mgr.pause_profiling() as inside:
+        assert inside is None and not mgr.is_profiling_suspended()
+    mgr.clear_profiling_durations()
+    mgr.release()
 
 
 def test_init_and_set_config_before_offload():
