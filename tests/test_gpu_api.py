@@ -234,3 +234,40 @@ def test_overlapping_parameter_views_are_refused_at_the_plan(gpu):
     for p, w in zip(model.parameters(), want):
         assert p.device.type == "cpu" and torch.equal(p.detach(), w)
     assert shared.untyped_storage().data_ptr() == first_w.untyped_storage().data_ptr()
+
+
+class _WithHead(torch.nn.Module):
+    """An MLP stack (the offload units) followed by a head that no unit holds."""
+
+    def __init__(self, seed):
+        super().__init__()
+        self.stack = W.build_mlp_stack(4, 256, 704, seed=seed)
+        self.head = torch.nn.Linear(256, 8, dtype=torch.bfloat16)
+        with torch.no_grad():
+            self.head.weight.copy_(torch.randn(8, 256, generator=torch.Generator().manual_seed(seed)) * 0.05)
+
+    def forward(self, x):
+        return self.head(self.stack(x))
+
+
+def test_one_manager_offloads_a_second_model_after_release(gpu):
+    """Everything a cycle sets up, including placing the tensors outside the units on the GPU, is redone
+    for the next model the same manager offloads (tests/unit/test_tensor_manager_lifecycle_gaps.py:140-188)."""
+    mgr = ft.OffloadManager("reuse")
+    cfg = OffloadConfig(include_patterns=["stack.layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1)
+    for seed in (21, 22):
+        model = _WithHead(seed)
+        ref = copy.deepcopy(model).to(gpu)
+        x = W.mlp_input(8, 256, seed=seed).to(gpu)
+        with torch.no_grad():
+            want = ref(x)
+        mgr.offload(model, cfg)
+        assert model.head.weight.device.type == "cuda"  # outside every unit: placed for good
+        with torch.no_grad():
+            outs = [model(x) for _ in range(4)]
+        torch.cuda.synchronize()
+        assert mgr.phase == OffloadPhase.INFERENCE and len(mgr.plan.streamed) == 4
+        assert all(torch.equal(o, want) for o in outs)
+        mgr.release()
+        assert all(p.device.type == "cpu" for p in model.parameters())
