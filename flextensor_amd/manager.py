@@ -562,8 +562,10 @@ class OffloadManager:
             for u in self.units:
                 if u.module is not None:
                     self._patch(u)
-            self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward()))
-            self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward()))
+            # first in line (offload_manager.py:2214-2242): the manager opens each pass before any user
+            # pre-hook runs, and user forward hooks see the phase this pass moved to
+            self._hooks.append(model.register_forward_pre_hook(lambda *_: self._before_forward(), prepend=True))
+            self._hooks.append(model.register_forward_hook(lambda *_: self._after_forward(), prepend=True))
             self.phase = OffloadPhase.DISCOVERY if self._discovery_passes > 0 else OffloadPhase.PROFILING
             if state is not None:
                 self.order = labels

@@ -271,3 +271,24 @@ def test_one_manager_offloads_a_second_model_after_release(gpu):
         assert all(torch.equal(o, want) for o in outs)
         mgr.release()
         assert all(p.device.type == "cpu" for p in model.parameters())
+
+
+def test_user_forward_hooks_see_the_phase_the_pass_moved_to(gpu):
+    """The manager's own forward hook runs first, whenever the user registered theirs
+    (tests/unit/test_offload_manager_hooks.py:1440-1481): a user hook on the model sees PROFILING after the
+    discovery pass and INFERENCE after the profiling pass."""
+    model = W.build_mlp_stack(4, 256, 704, seed=31)
+    mgr = ft.OffloadManager("hook-order")
+    seen_before, seen_after = [], []
+    model.register_forward_hook(lambda *_: seen_before.append(mgr.phase))
+    mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                                     profiling_iters=1))
+    model.register_forward_hook(lambda *_: seen_after.append(mgr.phase))
+    x = W.mlp_input(8, 256, seed=31).to(gpu)
+    with torch.no_grad():
+        for _ in range(3):
+            model(x)
+    torch.cuda.synchronize()
+    want = [OffloadPhase.PROFILING, OffloadPhase.INFERENCE, OffloadPhase.INFERENCE]
+    assert seen_before == want and seen_after == want
+    mgr.release()
