@@ -523,6 +523,11 @@ class OffloadManager:
                     LOGGER.warning("offload %r: include/exclude patterns leave unit %r no parameter to stream; its "
                                    "parameters stay on the GPU", self.name, label)
             names = [name_of[id(p)] for p in params]
+            if state is not None and mod is not None and names != saved[label] and self.config.include_patterns:
+                # module units (not manual blocks): the profile was made with other patterns or another model
+                raise ValueError(f"profile unit {label!r} streams {saved[label]}, but with these include/exclude "
+                                 f"patterns the model's unit streams {names}; offload with the patterns the profile "
+                                 "was made with, or profile again")
             if state is not None and (mod is None or names != saved[label]):
                 # a manual offload block of the saved plan: its tensors by name
                 mod = None

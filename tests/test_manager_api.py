@@ -605,3 +605,29 @@ def test_disabled_offload_hands_the_model_back_untouched():
     assert torch.equal(model(x), want)
     assert all(torch.equal(p, before[n]) and p.device.type == "cpu" for n, p in model.named_parameters())
     mgr.release()  # nothing to release
+
+
+def test_a_profile_made_with_other_patterns_is_refused(host_offload, names):
+    """A saved unit whose tensors differ from what the current patterns stream is an error, not a manual
+    block that no forward would enter (the profile must match the model and patterns it was made with)."""
+    from flextensor_amd.planner import LayerStatistics, TensorStatistics
+    from flextensor_amd.profile import TensorManagerState
+
+    model = _Stack()
+    inventory = [n for n, _ in model.named_parameters()]
+    ids = {n: i for i, n in enumerate(inventory)}
+    only_weight = [TensorStatistics(ids["layers.0.weight"], "layers.0.weight", 64, 0.1)]
+    state = TensorManagerState(
+        loader_type="allocation_block_transfer", tensor_id_to_name_map={i: n for n, i in ids.items()},
+        allocation_ordered={0: ["layers.0"]}, label_to_size_map={"layers.0": 64}, block_sizes={0: 64},
+        load_strategy={"layers.0": only_weight}, release_strategy={"layers.0": only_weight},
+        label_to_block_id={"layers.0": 0}, stats=[LayerStatistics("layers.0", only_weight, 1.0)],
+        transfer_to_compute_map={"layers.0": "layers.0"}, view_tensors_ids=[ids["layers.0.weight"]],
+        view_tensors_names=["layers.0.weight"], gpu_tensors_names=[n for n in inventory if n != "layers.0.weight"])
+    state.validate_internal()
+    names.append("profile-patterns")
+    mgr = M.get_offload_manager("profile-patterns")
+    with mock.patch.object(M.nat, "load", lambda: None), mock.patch.object(M.torch.cuda, "set_device", lambda d: None):
+        with pytest.raises(ValueError, match=r"profile unit 'layers.0' streams \['layers.0.weight'\]"):
+            mgr.offload(model, OffloadConfig(include_patterns=["layers.*"]), state=state)
+    assert mgr.model is None
