@@ -486,13 +486,13 @@ class OffloadManager:
         if compile_fn is not None and not callable(compile_fn):
             raise TypeError("compile_fn must be callable: module -> compiled module")
         self.config = config or OffloadConfig()
-        self._control = "live" if self.config.enabled else "noop"
         if load_from_shm and (state is None or not self.config.shm_enabled or not state.shm_block_name_map):
             raise ValueError("load_from_shm needs shm_enabled and a saved state that names its shared blocks")
         if self.config.enabled and self.config.pinned_memory and self.config.pinned_memory_mode == "host_register":
             raise ValueError(nat.HOST_REGISTER_REFUSED)
         self.compile_fn = compile_fn
         self._load_from_shm = load_from_shm
+        self._control = "live" if self.config.enabled else "noop"
         if not self.config.enabled:
             return model
         nat.load()
