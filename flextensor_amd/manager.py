@@ -523,11 +523,19 @@ class OffloadManager:
                     LOGGER.warning("offload %r: include/exclude patterns leave unit %r no parameter to stream; its "
                                    "parameters stay on the GPU", self.name, label)
             names = [name_of[id(p)] for p in params]
-            if state is not None and mod is not None and names != saved[label] and self.config.include_patterns:
-                # module units (not manual blocks): the profile was made with other patterns or another model
-                raise ValueError(f"profile unit {label!r} streams {saved[label]}, but with these include/exclude "
-                                 f"patterns the model's unit streams {names}; offload with the patterns the profile "
-                                 "was made with, or profile again")
+            if state is not None and mod is not None and names != saved[label]:
+                own = {name_of[id(q)] for q in mod.parameters() if id(q) not in shared}
+                if set(saved[label]) <= own:
+                    # the saved profile decides what the unit streams, over the runtime patterns, as the
+                    # reference adopts a profile's strategy; the module's other parameters stay resident
+                    names = list(saved[label])
+                    params = [by_name[n] for n in names]
+                elif self.config.include_patterns:
+                    # a module unit would stream tensors outside its module, which other modules may read
+                    # while its slot holds another unit
+                    raise ValueError(f"profile unit {label!r} streams {saved[label]}, which are not all parameters "
+                                     f"of the module {label!r} (tied or elsewhere in the model); profile this model "
+                                     "again")
             if state is not None and (mod is None or names != saved[label]):
                 # a manual offload block of the saved plan: its tensors by name
                 mod = None

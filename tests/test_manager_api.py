@@ -607,27 +607,42 @@ def test_disabled_offload_hands_the_model_back_untouched():
     mgr.release()  # nothing to release
 
 
-def test_a_profile_made_with_other_patterns_is_refused(host_offload, names):
-    """A saved unit whose tensors differ from what the current patterns stream is an error, not a manual
-    block that no forward would enter (the profile must match the model and patterns it was made with)."""
+def _one_label_state(model, label, streamed):
     from flextensor_amd.planner import LayerStatistics, TensorStatistics
     from flextensor_amd.profile import TensorManagerState
 
-    model = _Stack()
     inventory = [n for n, _ in model.named_parameters()]
     ids = {n: i for i, n in enumerate(inventory)}
-    only_weight = [TensorStatistics(ids["layers.0.weight"], "layers.0.weight", 64, 0.1)]
+    ts = [TensorStatistics(ids[n], n, 64, 0.1) for n in streamed]
     state = TensorManagerState(
         loader_type="allocation_block_transfer", tensor_id_to_name_map={i: n for n, i in ids.items()},
-        allocation_ordered={0: ["layers.0"]}, label_to_size_map={"layers.0": 64}, block_sizes={0: 64},
-        load_strategy={"layers.0": only_weight}, release_strategy={"layers.0": only_weight},
-        label_to_block_id={"layers.0": 0}, stats=[LayerStatistics("layers.0", only_weight, 1.0)],
-        transfer_to_compute_map={"layers.0": "layers.0"}, view_tensors_ids=[ids["layers.0.weight"]],
-        view_tensors_names=["layers.0.weight"], gpu_tensors_names=[n for n in inventory if n != "layers.0.weight"])
+        allocation_ordered={0: [label]}, label_to_size_map={label: 64 * len(ts)}, block_sizes={0: 64 * len(ts)},
+        load_strategy={label: ts}, release_strategy={label: ts}, label_to_block_id={label: 0},
+        stats=[LayerStatistics(label, ts, 1.0)], transfer_to_compute_map={label: label},
+        view_tensors_ids=[ids[n] for n in streamed], view_tensors_names=list(streamed),
+        gpu_tensors_names=[n for n in inventory if n not in streamed])
     state.validate_internal()
-    names.append("profile-patterns")
-    mgr = M.get_offload_manager("profile-patterns")
-    with mock.patch.object(M.nat, "load", lambda: None), mock.patch.object(M.torch.cuda, "set_device", lambda d: None):
-        with pytest.raises(ValueError, match=r"profile unit 'layers.0' streams \['layers.0.weight'\]"):
-            mgr.offload(model, OffloadConfig(include_patterns=["layers.*"]), state=state)
-    assert mgr.model is None
+    return state
+
+
+def test_a_saved_profile_decides_what_a_unit_streams(names):
+    """A profile made with other patterns is authoritative, as the reference adopts a profile's strategy over
+    the runtime selection config (tests/unit/test_state_adoption.py:447-474): the unit streams the saved
+    tensors of its module and the module's other parameters stay resident. A unit that would stream tensors
+    outside its module is refused."""
+    names.extend(["profile-patterns", "profile-outside"])
+    with mock.patch.object(M.nat, "load", lambda: None), mock.patch.object(M.torch.cuda, "set_device", lambda d: None), \
+            mock.patch.object(M.OffloadManager, "_to_inference", lambda self, state=None: None), \
+            mock.patch.object(M.OffloadManager, "_upload_into", lambda self, ts: 0), \
+            mock.patch.object(M.custom_ops, "register_manager", lambda *a: None):
+        model = _Stack()
+        mgr = M.get_offload_manager("profile-patterns")
+        mgr.offload(model, OffloadConfig(include_patterns=["layers.*"]),
+                    state=_one_label_state(model, "layers.0", ["layers.0.weight"]))
+        assert [(u.label, u.names, u.module is model.layers[0]) for u in mgr.units] == \
+            [("layers.0", ["layers.0.weight"], True)]
+        other = _Stack()
+        with pytest.raises(ValueError, match=r"not all parameters of the module 'layers.0'"):
+            M.get_offload_manager("profile-outside").offload(
+                other, OffloadConfig(include_patterns=["layers.*"]),
+                state=_one_label_state(other, "layers.0", ["layers.1.weight"]))
