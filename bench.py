@@ -32,6 +32,8 @@ import time
 MiB = 1 << 20
 HBM_PEAK_GBPS = 8000.0
 PCIE_GEN5_X16_GBPS = 63.0  # 32 GT/s x 16 lanes x 128/130 / 8
+# Offload units one level below a decoder layer: attention, gate, up and down (the norms stay resident).
+FINER_UNITS = ("layers.*.attn", "layers.*.gate", "layers.*.up", "layers.*.down")
 
 
 def _log(msg: str) -> None:
@@ -179,9 +181,12 @@ def cpu_baseline_scatter(chunks, sample_chunks: int = 4, reps: int = 3, threads:
                       f"on {threads} threads, best of {reps}"}
 
 
-def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str) -> dict:
+def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
+                  include_patterns: tuple[str, ...] = ("layers.*",)) -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
-    streaming under ``budget_gb`` (a step is one decode token)."""
+    streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
+    units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
+    returned under ``_check`` so that runs with other units can be compared bitwise."""
     import torch
 
     from flextensor_amd import hip
@@ -194,7 +199,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     model = W.build_llama(W.LLAMA_7B, seed=0, init_device="cuda")
     _log(f"llama7b: built in {time.perf_counter() - t0:.1f} s")
     mgr = OffloadManager("bench-llama")
-    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+    cfg = OffloadConfig(include_patterns=list(include_patterns), num_blocks=2, min_blocks=2, discovery_iters=1,
                         profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9), copy_engine=copy_engine)
     mgr.offload(model, cfg)
     prompt = W.prompt_tokens(1, prefill, W.LLAMA_7B.vocab, seed=0).to(dev)
@@ -215,15 +220,19 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         logits = model(prompt, 0)
         torch.cuda.synchronize()
         t_prefill = time.perf_counter() - t0
+        last_logits = logits[:, -1].float().cpu()
         tok = logits.argmax(-1)
+        toks = [tok]
         pos = prefill
         for _ in range(warmup):
             tok = model(tok, pos).argmax(-1)
+            toks.append(tok)
             pos += 1
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
             tok = model(tok, pos).argmax(-1)
+            toks.append(tok)
             pos += 1
         torch.cuda.synchronize()
         t_decode = time.perf_counter() - t0
@@ -246,6 +255,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
                                                                        "n_copy_streams")},
         "copy_policy_source": None if mgr.link is None else mgr.link.source,
         "transfer_stream": hip.transfer_stream_probe(dev),
+        "_check": {"last_logits": last_logits, "tokens": torch.cat(toks, -1).cpu()},
     }
     mgr.release(preserve_model=False)
     return out
@@ -1068,6 +1078,8 @@ def main() -> int:
     ap.add_argument("--skip-scatter", action="store_true")
     ap.add_argument("--skip-dit", action="store_true")
     ap.add_argument("--skip-mlp", action="store_true")
+    ap.add_argument("--skip-finer-units", action="store_true",
+                    help="skip the 7B decode with attention and MLP projections as separate offload units")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
     ap.add_argument("--staged-sweep", action="store_true",
                     help="only print host-to-device GB/s of the staged engine from pageable and shared memory")
@@ -1136,6 +1148,7 @@ def main() -> int:
 
     # ---- headline: 7B-shape decoder, 8 GB budget, one decode token per step
     llama = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine)
+    check = llama.pop("_check")
     _log(f"llama7b: {llama}")
     line = {
         "metric": "effective streamed-weight GB/s (% of link peak); tok/s at 7B shape, 8 GB budget",
@@ -1171,6 +1184,31 @@ def main() -> int:
     }
     gc.collect()
     torch.cuda.empty_cache()
+
+    # ---- the same decode with each layer's attention and three MLP projections as separate units
+    if not args.skip_finer_units:
+        fine = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
+                             include_patterns=FINER_UNITS)
+        fine_check = fine.pop("_check")
+        same = (torch.equal(fine_check["last_logits"], check["last_logits"])
+                and torch.equal(fine_check["tokens"], check["tokens"]))
+        line["llama7b_finer_units"] = {
+            "include_patterns": list(FINER_UNITS),
+            "streamed_units": fine["streamed_layers"], "resident_units": fine["resident_layers"],
+            "streamed_bytes_per_token": fine["streamed_bytes_per_token"],
+            "tok_s": round(fine["decode_tok_s"], 3), "ms_per_token": round(fine["ms_per_token"], 3),
+            "decode_effective_GBps": round(fine["decode_effective_GBps"], 3),
+            "pct_of_measured_peak": round(100 * fine["decode_effective_GBps"] / measured_peak, 2),
+            "gpu_weight_bytes": fine["gpu_weight_bytes"],
+            "prefill_logits_and_tokens_bitwise_equal_to_layer_units": same,
+        }
+        _log(f"llama7b finer units: {line['llama7b_finer_units']}")
+        del fine, fine_check
+        gc.collect()
+        torch.cuda.empty_cache()
+        if not same:
+            print("bench: the finer-unit decode differs from the whole-layer decode", file=sys.stderr)
+            return 1
 
     # ---- the scatter microbenchmark and the scatter kernel's HBM roofline
     if not args.skip_scatter:
