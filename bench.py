@@ -252,7 +252,8 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         "gpu_weight_bytes": usage.total_bytes,
         "budget_bytes": int(budget_gb * 1e9),
         "copy_policy": None if link is None else {k: link[k] for k in ("kernel_max_bytes", "split_min_bytes",
-                                                                       "n_copy_streams")},
+                                                                       "n_copy_streams", "kernel_grid",
+                                                                       "link_bound")},
         "copy_policy_source": None if mgr.link is None else mgr.link.source,
         "transfer_stream": hip.transfer_stream_probe(dev),
         "_check": {"last_logits": last_logits, "tokens": torch.cat(toks, -1).cpu()},
@@ -1200,6 +1201,7 @@ def main() -> int:
             "decode_effective_GBps": round(fine["decode_effective_GBps"], 3),
             "pct_of_measured_peak": round(100 * fine["decode_effective_GBps"] / measured_peak, 2),
             "gpu_weight_bytes": fine["gpu_weight_bytes"],
+            "copy_policy": fine["copy_policy"],
             "prefill_logits_and_tokens_bitwise_equal_to_layer_units": same,
         }
         _log(f"llama7b finer units: {line['llama7b_finer_units']}")

@@ -15,6 +15,10 @@
   transition: both engines over log-spaced sizes up to the largest streamed
   unit, the policy they choose, and the SDMA curve in the reference's
   ``{bytes: ms}`` form (its ``memory_transfer_stats``).
+* :func:`is_link_bound` then compares the profiled compute of a pass with
+  the curve's time for its streamed units; a link-bound pass copies every
+  ring slot with the zero-copy kernel
+  (:meth:`LinkMeasurement.for_link_bound_pass`).
 """
 
 from __future__ import annotations
@@ -228,6 +232,32 @@ def choose_copy_policy(sdma: CopyCurve, kernel: CopyCurve, split: CopyCurve | No
     return kernel_max, split_min, (n_split if split_min < 2**63 - 1 else 1)
 
 
+# A pass whose profiled compute takes less than this share of the time its
+# streamed units need on the link is link-bound: the compute stream waits on
+# the link whatever runs beside it.
+LINK_BOUND_COMPUTE_SHARE = 0.5
+# Zero-copy kernel workgroups for the ring copies of a link-bound pass. Eight
+# hold the link at its peak (57.3 GB/s for 512 MiB, against 57.1 at 64) and
+# leave the compute kernels most of the chip.
+RING_KERNEL_GRID = 8
+
+
+def is_link_bound(compute_ms: float, transfer_ms: float, share: float = LINK_BOUND_COMPUTE_SHARE) -> bool:
+    """Whether a pass that computes for ``compute_ms`` and streams for ``transfer_ms`` waits on the link.
+
+    In such a pass the ring copies go to the zero-copy kernel. Between two
+    SDMA copies of a streamed decode the link idles for 50-250 us, until the
+    waiting compute kernel and the next copy start together; kernel copies
+    in the same pass ran without that gap (7B-shape decode with 56 streamed
+    units per token: 102.5 ms per token against 115.7). The kernel's cost,
+    host reads that slow the kernels sharing its CUs, stays hidden while the
+    compute stream waits on the link anyway. It is not hidden in a
+    compute-bound pass: a diffusion step with 25 of 40 blocks streamed took
+    4% longer with kernel copies, so such a pass keeps SDMA.
+    """
+    return transfer_ms > 0.0 and compute_ms < share * transfer_ms
+
+
 def benchmark_memory_transfers(max_label_bytes: int, device=None, max_depth: int = 4,
                                max_size_bytes: int = 4 * 1024**3, engine: str = "sdma") -> dict[int, float]:
     """Median ms per size for sizes ``base / 2**d``, d < max_depth (pinned source).
@@ -273,6 +303,8 @@ class LinkMeasurement:
     split_min_bytes: int
     n_copy_streams: int
     source: str = "measured"  # "measured" at the transition, "profile" when restored from a saved plan
+    kernel_grid: int = 0  # zero-copy kernel workgroups; 0 is the library's default (64)
+    link_bound: bool = False  # the ring copies of a link-bound pass all go to the kernel
 
     def memory_transfer_stats(self) -> dict[int, float]:
         """The SDMA curve as ``{bytes: ms}``, the reference's ``memory_transfer_stats`` form."""
@@ -281,16 +313,34 @@ class LinkMeasurement:
     def policy(self) -> tuple[int, int, int]:
         return self.kernel_max_bytes, self.split_min_bytes, self.n_copy_streams
 
+    def transfer_ms(self, sizes: list[int]) -> float:
+        """Predicted SDMA time of copies of ``sizes`` bytes, interpolated from the measured curve."""
+        if not self.sdma.best_ms:
+            return 0.0
+        interp = MemoryTransferInterpolator(self.sdma.best_ms)
+        return float(sum(interp.bytes_to_duration(n) for n in sizes))
+
+    def for_link_bound_pass(self, largest_unit_bytes: int) -> "LinkMeasurement":
+        """The policy for a link-bound pass: every ring copy (up to ``largest_unit_bytes``) on the zero-copy
+        kernel at :data:`RING_KERNEL_GRID` workgroups; the measured curves are kept."""
+        return LinkMeasurement(self.sdma, self.kernel, max(self.kernel_max_bytes, int(largest_unit_bytes)),
+                               self.split_min_bytes, self.n_copy_streams, self.source, RING_KERNEL_GRID, True)
+
     def describe(self) -> str:
         sd, kn = self.sdma.gbps(), self.kernel.gbps()
         curve = ", ".join(f"{n >> 10} KiB {sd[n]:.1f}/{kn.get(n, float('nan')):.1f}" for n in sorted(sd))
         where = (f"zero-copy kernel for chunks up to {self.kernel_max_bytes} bytes, SDMA above"
                  if self.kernel_max_bytes else "SDMA for every chunk")
+        if self.kernel_grid:
+            where += f" (kernel grid {self.kernel_grid})"
+        if self.link_bound:
+            where = "link-bound pass: " + where
         return f"copy policy ({self.source}): {where}; GB/s SDMA/kernel by size: {curve}"
 
     def to_dict(self) -> dict:
         return {"kernel_max_bytes": self.kernel_max_bytes, "split_min_bytes": min(self.split_min_bytes, 2**63 - 1),
-                "n_copy_streams": self.n_copy_streams,
+                "n_copy_streams": self.n_copy_streams, "kernel_grid": self.kernel_grid,
+                "link_bound": self.link_bound,
                 "sdma_ms": {str(n): ms for n, ms in sorted(self.sdma.best_ms.items())},
                 "kernel_ms": {str(n): ms for n, ms in sorted(self.kernel.best_ms.items())}}
 
@@ -300,11 +350,14 @@ class LinkMeasurement:
             sdma = CopyCurve("sdma", {int(k): float(v) for k, v in data.get("sdma_ms", {}).items()})
             kernel = CopyCurve("kernel", {int(k): float(v) for k, v in data.get("kernel_ms", {}).items()})
             km, sm, ns = int(data["kernel_max_bytes"]), int(data["split_min_bytes"]), int(data["n_copy_streams"])
+            kg = int(data.get("kernel_grid", 0))  # plans saved before the grid was recorded use the default
+            bound = data.get("link_bound", False)
         except (KeyError, TypeError, ValueError) as exc:
             raise ValueError(f"invalid copy_policy in the saved state: {exc}") from exc
-        if km < 0 or sm < 0 or not 1 <= ns <= 8 or any(v <= 0 for v in sdma.best_ms.values()):
+        if km < 0 or sm < 0 or not 1 <= ns <= 8 or not 0 <= kg <= 1 << 20 or not isinstance(bound, bool) \
+                or any(v <= 0 for v in sdma.best_ms.values()):
             raise ValueError("invalid copy_policy in the saved state: out-of-range values")
-        return cls(sdma, kernel, km, sm, ns, source)
+        return cls(sdma, kernel, km, sm, ns, source, kg, bound)
 
 
 def measure_link(sizes: list[int], device=None, repeats: int = 5, warmup: int = 1) -> LinkMeasurement:

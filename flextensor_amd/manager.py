@@ -57,8 +57,8 @@ from .allocation_block import HostPinner
 from .config import OffloadConfig
 from .controllers import AllocationBlockController, RawBlockController
 from .layout import overlapping_views
-from .link_model import (LinkMeasurement, MemoryTransferInterpolator, format_memory_transfer_table, link_probe_sizes,
-                         measure_link)
+from .link_model import (LinkMeasurement, MemoryTransferInterpolator, format_memory_transfer_table, is_link_bound,
+                         link_probe_sizes, measure_link)
 from .loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
 from .planner import (
     BlockStrategyData,
@@ -1537,6 +1537,13 @@ class OffloadManager:
         state reapplies the saved policy without measuring, as the reference
         rebuilds its curve from the saved statistics. Only ``copy_engine="auto"``
         consults the policy; ``link_benchmark=False`` keeps the library default.
+
+        A measured policy then looks at the pass: when the profiled compute of
+        its units is under half the curve's time for its streamed units
+        (:func:`~flextensor_amd.link_model.is_link_bound`), every ring copy
+        goes to the zero-copy kernel at a small grid, which removes the idle
+        gap between consecutive SDMA copies. A pass with no profiled durations
+        keeps the measured policy.
         """
         cfg = self.config
         link = None
@@ -1552,8 +1559,12 @@ class OffloadManager:
                 torch.cuda.empty_cache()
         if link is None:
             return
-        nat.set_copy_policy(link.kernel_max_bytes, link.split_min_bytes, link.n_copy_streams,
-                            nat.get_copy_policy()[3])
+        if link.source == "measured" and any(self.durations.get(x) for x in plan.streamed):
+            compute_ms = sum(self._duration(x) for x in [*plan.streamed, *plan.resident])
+            sizes = [self._unit(x).nbytes for x in plan.streamed]
+            if is_link_bound(compute_ms, link.transfer_ms(sizes)):
+                link = link.for_link_bound_pass(max(sizes))
+        nat.set_copy_policy(link.kernel_max_bytes, link.split_min_bytes, link.n_copy_streams, link.kernel_grid)
         self.link = link
         self.memory_transfer_stats = link.memory_transfer_stats()
         LOGGER.info("offload %r: %s", self.name, link.describe())

@@ -432,7 +432,8 @@ def test_copy_policy_follows_the_measured_curve(host_offload, cut):
             mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)), \
             mock.patch.object(M.nat, "get_copy_policy", lambda: (1 << 20, 2**63 - 1, 1, 64)):
         mgr._choose_copy_policy(plan, None)
-    assert applied == [(cut, link.split_min_bytes, 1, 64)]  # the measured policy, the kernel grid kept
+    # no profiled durations: the measured policy as it is, at the library's default kernel grid
+    assert applied == [(cut, link.split_min_bytes, 1, 0)]
     assert mgr.get_memory_transfer_stats() == link.sdma.best_ms
     mgr.plan = plan
     table = mgr.plan_table()
@@ -450,6 +451,66 @@ def test_copy_policy_follows_the_measured_curve(host_offload, cut):
     assert back.copy_policy == state.copy_policy
     restored = L.LinkMeasurement.from_dict(back.copy_policy)
     assert restored.policy() == link.policy() and restored.source == "profile"
+
+
+def _profiled(mgr, ms_per_unit):
+    mgr.order = [u.label for u in mgr.units]
+    mgr.durations = {x: [ms_per_unit] for x in mgr.order}
+    return M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
+
+
+def test_a_link_bound_pass_copies_every_slot_with_the_kernel(host_offload):
+    from flextensor_amd import link_model as L
+
+    mgr = host_offload("link-bound", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
+    link = _fake_link(1 << 20)
+    plan = _profiled(mgr, 1e-6)  # the units compute for far less than their copies take
+    sizes = [mgr._unit(x).nbytes for x in plan.streamed]
+    assert L.is_link_bound(1e-6 * len(mgr.order), link.transfer_ms(sizes))
+    applied = []
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), \
+            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)):
+        mgr._choose_copy_policy(plan, None)
+    assert applied == [(max(1 << 20, max(sizes)), link.split_min_bytes, 1, L.RING_KERNEL_GRID)]
+    assert mgr.link.link_bound and mgr.link.kernel_grid == L.RING_KERNEL_GRID
+    assert mgr.link.sdma is link.sdma  # the measured curve stays the transfer model
+    assert "link-bound pass" in mgr.link.describe()
+    back = L.LinkMeasurement.from_dict(mgr.link.to_dict())
+    assert (back.kernel_grid, back.link_bound, back.policy()) == (L.RING_KERNEL_GRID, True, mgr.link.policy())
+
+
+def test_a_compute_bound_pass_keeps_the_measured_policy(host_offload):
+    mgr = host_offload("compute-bound", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
+    link = _fake_link(1 << 20)
+    plan = _profiled(mgr, 1e6)
+    applied = []
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), \
+            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)):
+        mgr._choose_copy_policy(plan, None)
+    assert applied == [(1 << 20, link.split_min_bytes, 1, 0)] and not mgr.link.link_bound
+
+
+def test_link_bound_rule():
+    from flextensor_amd import link_model as L
+
+    assert L.is_link_bound(10.0, 100.0) and L.is_link_bound(49.9, 100.0)
+    assert not L.is_link_bound(50.0, 100.0) and not L.is_link_bound(500.0, 100.0)
+    assert not L.is_link_bound(0.0, 0.0)  # nothing streams: nothing to choose
+    curve = L.CopyCurve("sdma", {1 << 20: 0.02, 1 << 22: 0.08})
+    link = L.LinkMeasurement(curve, L.CopyCurve("kernel"), 0, 2**63 - 1, 1)
+    assert link.transfer_ms([1 << 20, 1 << 22]) == pytest.approx(0.10)
+    assert link.transfer_ms([1 << 21]) == pytest.approx(0.04)  # log-log between the points
+
+
+def test_saved_policies_without_a_kernel_grid_read_as_the_default():
+    from flextensor_amd import link_model as L
+
+    old = {"kernel_max_bytes": 1 << 20, "split_min_bytes": 2**63 - 1, "n_copy_streams": 1}
+    link = L.LinkMeasurement.from_dict(old)
+    assert (link.kernel_grid, link.link_bound) == (0, False)
+    for bad in ({"kernel_grid": -1}, {"kernel_grid": 1 << 21}, {"link_bound": "yes"}):
+        with pytest.raises(ValueError, match="out-of-range"):
+            L.LinkMeasurement.from_dict({**old, **bad})
 
 
 def test_saved_policy_is_reapplied_without_measuring(host_offload):
