@@ -406,9 +406,9 @@ def bench_dit(budget_gb: float, tokens: int, text: int, steps: int, copy_engine:
                                      profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9),
                                      offload_timing="eager", copy_engine=copy_engine))
     with torch.no_grad():
-        xs = x[:, :2048].contiguous()
-        model(xs, e, ctx)
-        model(xs, e, ctx)
+        # discovery and profiling on the full step: the copy engine is chosen from the profiled compute
+        model(x, e, ctx)
+        model(x, e, ctx)
         got = model(x, e, ctx)  # warm-up step
         mgr.reset_offload_timing()
         step_times = []
@@ -437,6 +437,8 @@ def bench_dit(budget_gb: float, tokens: int, text: int, steps: int, copy_engine:
         "tflops_per_step": S.block_flops(tokens, text) * S.n_blocks / 1e12,
         "achieved_tflops": S.block_flops(tokens, text) * S.n_blocks / step / 1e12,
         "gpu_weight_bytes": mgr.get_gpu_memory_usage().total_bytes, "budget_bytes": int(budget_gb * 1e9),
+        "copy_policy": None if mgr.link is None else {k: mgr.link.to_dict()[k] for k in (
+            "kernel_max_bytes", "n_copy_streams", "kernel_grid", "link_bound")},
     }
     mgr.release(preserve_model=False)
     del want, got
