@@ -253,7 +253,8 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         "budget_bytes": int(budget_gb * 1e9),
         "copy_policy": None if link is None else {k: link[k] for k in ("kernel_max_bytes", "split_min_bytes",
                                                                        "n_copy_streams", "kernel_grid",
-                                                                       "link_bound")},
+                                                                       "link_bound", "pass_compute_ms",
+                                                                       "pass_transfer_ms")},
         "copy_policy_source": None if mgr.link is None else mgr.link.source,
         "transfer_stream": hip.transfer_stream_probe(dev),
         "_check": {"last_logits": last_logits, "tokens": torch.cat(toks, -1).cpu()},
@@ -438,7 +439,8 @@ def bench_dit(budget_gb: float, tokens: int, text: int, steps: int, copy_engine:
         "achieved_tflops": S.block_flops(tokens, text) * S.n_blocks / step / 1e12,
         "gpu_weight_bytes": mgr.get_gpu_memory_usage().total_bytes, "budget_bytes": int(budget_gb * 1e9),
         "copy_policy": None if mgr.link is None else {k: mgr.link.to_dict()[k] for k in (
-            "kernel_max_bytes", "n_copy_streams", "kernel_grid", "link_bound")},
+            "kernel_max_bytes", "n_copy_streams", "kernel_grid", "link_bound", "pass_compute_ms",
+            "pass_transfer_ms")},
     }
     mgr.release(preserve_model=False)
     del want, got

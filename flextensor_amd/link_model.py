@@ -24,7 +24,7 @@
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 
@@ -306,6 +306,9 @@ class LinkMeasurement:
     source: str = "measured"  # "measured" at the transition, "profile" when restored from a saved plan
     kernel_grid: int = 0  # zero-copy kernel workgroups; 0 is the library's default (64)
     link_bound: bool = False  # the ring copies of a link-bound pass all go to the kernel
+    # what decided it: the pass's profiled compute and its streamed units' time on the curve
+    pass_compute_ms: float | None = None
+    pass_transfer_ms: float | None = None
 
     def memory_transfer_stats(self) -> dict[int, float]:
         """The SDMA curve as ``{bytes: ms}``, the reference's ``memory_transfer_stats`` form."""
@@ -324,8 +327,8 @@ class LinkMeasurement:
     def for_link_bound_pass(self, largest_unit_bytes: int) -> "LinkMeasurement":
         """The policy for a link-bound pass: every ring copy (up to ``largest_unit_bytes``) on the zero-copy
         kernel at :data:`RING_KERNEL_GRID` workgroups; the measured curves are kept."""
-        return LinkMeasurement(self.sdma, self.kernel, max(self.kernel_max_bytes, int(largest_unit_bytes)),
-                               self.split_min_bytes, self.n_copy_streams, self.source, RING_KERNEL_GRID, True)
+        return replace(self, kernel_max_bytes=max(self.kernel_max_bytes, int(largest_unit_bytes)),
+                       kernel_grid=RING_KERNEL_GRID, link_bound=True)
 
     def describe(self) -> str:
         sd, kn = self.sdma.gbps(), self.kernel.gbps()
@@ -336,12 +339,15 @@ class LinkMeasurement:
             where += f" (kernel grid {self.kernel_grid})"
         if self.link_bound:
             where = "link-bound pass: " + where
+        if self.pass_compute_ms is not None and self.pass_transfer_ms is not None:
+            where += f"; pass compute {self.pass_compute_ms:.1f} ms against {self.pass_transfer_ms:.1f} ms on the link"
         return f"copy policy ({self.source}): {where}; GB/s SDMA/kernel by size: {curve}"
 
     def to_dict(self) -> dict:
         return {"kernel_max_bytes": self.kernel_max_bytes, "split_min_bytes": min(self.split_min_bytes, 2**63 - 1),
                 "n_copy_streams": self.n_copy_streams, "kernel_grid": self.kernel_grid,
-                "link_bound": self.link_bound,
+                "link_bound": self.link_bound, "pass_compute_ms": self.pass_compute_ms,
+                "pass_transfer_ms": self.pass_transfer_ms,
                 "sdma_ms": {str(n): ms for n, ms in sorted(self.sdma.best_ms.items())},
                 "kernel_ms": {str(n): ms for n, ms in sorted(self.kernel.best_ms.items())}}
 
@@ -353,12 +359,13 @@ class LinkMeasurement:
             km, sm, ns = int(data["kernel_max_bytes"]), int(data["split_min_bytes"]), int(data["n_copy_streams"])
             kg = int(data.get("kernel_grid", 0))  # plans saved before the grid was recorded use the default
             bound = data.get("link_bound", False)
+            times = [None if data.get(k) is None else float(data[k]) for k in ("pass_compute_ms", "pass_transfer_ms")]
         except (KeyError, TypeError, ValueError) as exc:
             raise ValueError(f"invalid copy_policy in the saved state: {exc}") from exc
         if km < 0 or sm < 0 or not 1 <= ns <= 8 or not 0 <= kg <= 1 << 20 or not isinstance(bound, bool) \
-                or any(v <= 0 for v in sdma.best_ms.values()):
+                or any(v <= 0 for v in sdma.best_ms.values()) or any(t is not None and t < 0 for t in times):
             raise ValueError("invalid copy_policy in the saved state: out-of-range values")
-        return cls(sdma, kernel, km, sm, ns, source, kg, bound)
+        return cls(sdma, kernel, km, sm, ns, source, kg, bound, *times)
 
 
 def measure_link(sizes: list[int], device=None, repeats: int = 5, warmup: int = 1) -> LinkMeasurement:

@@ -1562,7 +1562,9 @@ class OffloadManager:
         if link.source == "measured" and any(self.durations.get(x) for x in plan.streamed):
             compute_ms = sum(self._duration(x) for x in [*plan.streamed, *plan.resident])
             sizes = [self._unit(x).nbytes for x in plan.streamed]
-            if is_link_bound(compute_ms, link.transfer_ms(sizes)):
+            transfer_ms = link.transfer_ms(sizes)
+            link = dataclasses.replace(link, pass_compute_ms=compute_ms, pass_transfer_ms=transfer_ms)
+            if is_link_bound(compute_ms, transfer_ms):
                 link = link.for_link_bound_pass(max(sizes))
         nat.set_copy_policy(link.kernel_max_bytes, link.split_min_bytes, link.n_copy_streams, link.kernel_grid)
         self.link = link

@@ -475,8 +475,11 @@ def test_a_link_bound_pass_copies_every_slot_with_the_kernel(host_offload):
     assert mgr.link.link_bound and mgr.link.kernel_grid == L.RING_KERNEL_GRID
     assert mgr.link.sdma is link.sdma  # the measured curve stays the transfer model
     assert "link-bound pass" in mgr.link.describe()
+    assert mgr.link.pass_compute_ms == pytest.approx(1e-6 * len(mgr.order))
+    assert mgr.link.pass_transfer_ms == pytest.approx(link.transfer_ms(sizes))
     back = L.LinkMeasurement.from_dict(mgr.link.to_dict())
     assert (back.kernel_grid, back.link_bound, back.policy()) == (L.RING_KERNEL_GRID, True, mgr.link.policy())
+    assert (back.pass_compute_ms, back.pass_transfer_ms) == (mgr.link.pass_compute_ms, mgr.link.pass_transfer_ms)
 
 
 def test_a_compute_bound_pass_keeps_the_measured_policy(host_offload):
@@ -488,6 +491,8 @@ def test_a_compute_bound_pass_keeps_the_measured_policy(host_offload):
             mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)):
         mgr._choose_copy_policy(plan, None)
     assert applied == [(1 << 20, link.split_min_bytes, 1, 0)] and not mgr.link.link_bound
+    assert mgr.link.pass_compute_ms == pytest.approx(1e6 * len(mgr.order))  # recorded either way
+    assert "pass compute" in mgr.link.describe()
 
 
 def test_link_bound_rule():
@@ -508,7 +513,8 @@ def test_saved_policies_without_a_kernel_grid_read_as_the_default():
     old = {"kernel_max_bytes": 1 << 20, "split_min_bytes": 2**63 - 1, "n_copy_streams": 1}
     link = L.LinkMeasurement.from_dict(old)
     assert (link.kernel_grid, link.link_bound) == (0, False)
-    for bad in ({"kernel_grid": -1}, {"kernel_grid": 1 << 21}, {"link_bound": "yes"}):
+    assert (link.pass_compute_ms, link.pass_transfer_ms) == (None, None)
+    for bad in ({"kernel_grid": -1}, {"kernel_grid": 1 << 21}, {"link_bound": "yes"}, {"pass_compute_ms": -1.0}):
         with pytest.raises(ValueError, match="out-of-range"):
             L.LinkMeasurement.from_dict({**old, **bad})
 
