@@ -1067,6 +1067,8 @@ def main() -> int:
     ap.add_argument("--tensors", type=int, default=2000)
     ap.add_argument("--scatter-steps", type=int, default=5)
     ap.add_argument("--copy-engine", default="auto", choices=["auto", "sdma", "kernel"])
+    ap.add_argument("--kernel-grid", type=int, default=0,
+                    help="zero-copy kernel workgroups for --copy-engine kernel (0: the library default)")
     ap.add_argument("--skip-cpu-baseline", action="store_true")
     ap.add_argument("--budget-gb", type=float, default=8.0)
     ap.add_argument("--prefill", type=int, default=512)
@@ -1140,6 +1142,12 @@ def main() -> int:
                                                                      "split_min_bytes": policy[1],
                                                                      "n_copy_streams": policy[2]}}), flush=True)
         return 0
+    if args.kernel_grid:
+        if args.copy_engine != "kernel":
+            print("bench: --kernel-grid needs --copy-engine kernel (auto chooses its own grid)", file=sys.stderr)
+            return 2
+        kmax, smin, nstreams, _ = nat.get_copy_policy()
+        nat.set_copy_policy(kmax, smin, nstreams, args.kernel_grid)
     if args.calibration_copy_mib:
         src = torch.ones(args.calibration_copy_mib * MiB, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
