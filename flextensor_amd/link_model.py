@@ -250,7 +250,7 @@ def is_link_bound(compute_ms: float, transfer_ms: float, share: float = LINK_BOU
     SDMA copies of a streamed decode the link idles for 50-250 us, until the
     waiting compute kernel and the next copy start together; kernel copies
     in the same pass ran without that gap (7B-shape decode with 56 streamed
-    units per token: 102.5 ms per token against 115.7). The kernel's cost,
+    units per token: 102.7 ms per token against 115.7). The kernel's cost,
     host reads that slow the kernels sharing its CUs, stays hidden while the
     compute stream waits on the link anyway. It is not hidden in a
     compute-bound pass: a diffusion step with 25 of 40 blocks streamed took
