@@ -1539,7 +1539,7 @@ class OffloadManager:
         consults the policy; ``link_benchmark=False`` keeps the library default.
 
         A measured policy then looks at the pass: when the profiled compute of
-        its units is under a quarter of the curve's time for its streamed units
+        its units is under 0.4 of the curve's time for its streamed units
         (:func:`~flextensor_amd.link_model.is_link_bound`), every ring copy
         goes to the zero-copy kernel at a small grid, which removes the idle
         gap between consecutive SDMA copies. A pass with no profiled durations

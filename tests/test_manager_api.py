@@ -498,8 +498,8 @@ def test_a_compute_bound_pass_keeps_the_measured_policy(host_offload):
 def test_link_bound_rule():
     from flextensor_amd import link_model as L
 
-    assert L.is_link_bound(10.0, 100.0) and L.is_link_bound(24.9, 100.0)
-    assert not L.is_link_bound(25.0, 100.0) and not L.is_link_bound(500.0, 100.0)
+    assert L.is_link_bound(10.0, 100.0) and L.is_link_bound(39.9, 100.0)
+    assert not L.is_link_bound(40.0, 100.0) and not L.is_link_bound(500.0, 100.0)
     assert not L.is_link_bound(0.0, 0.0)  # nothing streams: nothing to choose
     curve = L.CopyCurve("sdma", {1 << 20: 0.02, 1 << 22: 0.08})
     link = L.LinkMeasurement(curve, L.CopyCurve("kernel"), 0, 2**63 - 1, 1)
