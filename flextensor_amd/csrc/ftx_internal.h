@@ -28,6 +28,9 @@ constexpr size_t kScatterTileBytes = 8 * 1024;
 // Default zero-copy grid: 64 workgroups keep the link at its peak (more
 // workgroups only add outstanding PCIe reads).
 constexpr int kZeroCopyDefaultGrid = 64;
+// A zero-copy launch of at most this many workgroups takes each CU it runs on
+// whole (its workgroups reserve the CU's LDS).
+constexpr int kZeroCopyReserveMaxGrid = 16;
 // Wave tiles handled by one workgroup (one tile per wavefront).
 constexpr int kScatterWavesPerGroup = 4;
 // Checksum block: 64 lanes x 8 bytes x 8 steps.
@@ -87,8 +90,11 @@ int set_staging_policy(size_t piece_bytes, int threads);
 void get_staging_policy(size_t *piece_bytes, int *threads);
 
 // Kernel launchers (ftx_kernels.hip). Each returns hipSuccess or the launch error.
-hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid,
+// `reserve_lds` bytes of dynamic LDS per workgroup (0: none); see zero_copy_kernel.
+hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid, size_t reserve_lds,
                             hipStream_t stream);
+// Lets zero_copy_kernel take `bytes` of dynamic LDS on the current device.
+hipError_t allow_zero_copy_lds(size_t bytes);
 hipError_t launch_scatter(const ScatterPlanDev &plan, const void *chunk, hipStream_t stream);
 hipError_t launch_checksum(const void *dev, size_t nbytes, uint64_t *partials, int n_waves,
                            hipStream_t stream);

@@ -2,7 +2,14 @@
 //
 //  * zero_copy_kernel  - host-to-device copy executed by the CUs: every lane
 //                        issues 16-byte non-temporal loads from mapped pinned
-//                        host memory (PCIe reads) and stores into HBM.
+//                        host memory (PCIe reads) and stores into HBM. A small
+//                        grid is launched with the CU's whole LDS as dynamic
+//                        shared memory, which the kernel never touches: no
+//                        workgroup that uses LDS (a GEMM's) can then share a CU
+//                        with a copy workgroup. Sharing one slowed both: an
+//                        LDS-using HBM reader beside an 8-workgroup copy ran
+//                        1.63-1.79x its time alone and the copy 49 GB/s; with
+//                        the CUs reserved, 1.15-1.25x and 56.6-56.9 GB/s.
 //  * scatter_kernel    - places one streamed chunk into many destination
 //                        tensors in one launch. Work is split into fixed-size
 //                        byte tiles; each workgroup stages the (at most four)
@@ -266,7 +273,12 @@ hipError_t launch_timestamp(uint64_t *slot, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid,
+hipError_t allow_zero_copy_lds(size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(zero_copy_kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int grid, size_t reserve_lds,
                             hipStream_t stream) {
   if (nbytes == 0) return hipSuccess;
   const uint64_t sa = reinterpret_cast<uint64_t>(src_dev);
@@ -276,7 +288,7 @@ hipError_t launch_zero_copy(void *dst, const void *src_dev, size_t nbytes, int g
   uint64_t need = (n16 + per_block - 1) / per_block;
   if (need < 1) need = 1;
   const int g = static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(grid)));
-  hipLaunchKernelGGL(zero_copy_kernel, dim3(g), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL(zero_copy_kernel, dim3(g), dim3(kThreads), static_cast<unsigned>(reserve_lds), stream,
                      static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src_dev),
                      static_cast<uint64_t>(nbytes), head, n16);
   return hipGetLastError();

@@ -41,6 +41,7 @@ struct DeviceState {
   hipEvent_t fork_event = nullptr;
   hipEvent_t join_events[kMaxCopyStreams] = {};
   void *static_scratch = nullptr;  // this device's address of `scratch`, resolved on first use
+  size_t copy_reserve_lds = 0;     // LDS a small zero-copy grid reserves per CU (0: not available)
 };
 
 struct ArenaRecord {
@@ -88,6 +89,13 @@ int device_state(DeviceState **out) {
     FTX_HIP(hipMemGetInfo(&free_b, &total_b));
     // Copy streams are created on the first split copy (copy_streams_ready):
     // every extra stream changes how streams share the device's hardware queues.
+    // The whole LDS of a CU, for small zero-copy grids. Where the runtime will
+    // not grant it, copies share their CUs as before.
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && lds > 0 &&
+        allow_zero_copy_lds(static_cast<size_t>(lds)) == hipSuccess)
+      st.copy_reserve_lds = static_cast<size_t>(lds);
+    (void)hipGetLastError();
     st.cu_count = cus;
     st.xcd_count = xccs;
     st.total_mem = total_b;
@@ -229,7 +237,8 @@ int copy_kernel(void *dst, const void *src, size_t nbytes, hipStream_t stream, c
   rc = device_state(&st);
   if (rc != FTX_OK) return rc;
   const int grid = pol.kernel_grid > 0 ? pol.kernel_grid : kZeroCopyDefaultGrid;
-  FTX_HIP(launch_zero_copy(dst, src_dev, nbytes, grid, stream));
+  const size_t reserve = grid <= kZeroCopyReserveMaxGrid ? st->copy_reserve_lds : 0;
+  FTX_HIP(launch_zero_copy(dst, src_dev, nbytes, grid, reserve, stream));
   return FTX_OK;
 }
 
