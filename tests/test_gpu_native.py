@@ -47,6 +47,27 @@ def test_copy_h2d_bit_exact(gpu, mode, nbytes, offset):
     assert (out[:offset] == 0xA5).all() and (out[offset + nbytes :] == 0xA5).all()
 
 
+@pytest.mark.parametrize("grid", [4, 8, 16, 17, 64])  # up to 16 workgroups reserve their CUs' LDS
+@pytest.mark.parametrize("nbytes", [4095, (1 << 20) + 7, (64 << 20) + 5])
+def test_kernel_copy_bit_exact_at_each_grid(gpu, grid, nbytes):
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import current_stream
+
+    data = _rand_bytes(nbytes, seed=grid + nbytes)
+    arena = _arena_with(data, pad=3)
+    dst = torch.full((nbytes + 64,), 0xA5, dtype=torch.uint8, device=gpu)
+    old = nat.get_copy_policy()
+    try:
+        nat.set_copy_policy(old[0], old[1], old[2], grid)
+        nat.copy_h2d(dst.data_ptr() + 3, arena.ptr + 3, nbytes, nat.COPY_KERNEL, current_stream(gpu).handle)
+        torch.cuda.synchronize()
+    finally:
+        nat.set_copy_policy(*old)
+    out = dst.cpu().numpy()
+    assert np.array_equal(out[3 : 3 + nbytes], data)
+    assert (out[:3] == 0xA5).all() and (out[3 + nbytes :] == 0xA5).all()
+
+
 def test_kernel_copy_rejects_non_congruent_alignment(gpu):
     from flextensor_amd import _native as nat
     from flextensor_amd.hip import current_stream
