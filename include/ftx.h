@@ -134,7 +134,9 @@ int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stre
  *   kernel_max_bytes  chunks <= this go to the zero-copy kernel under AUTO;
  *   split_min_bytes   SDMA copies >= this are split over n_copy_streams;
  *   n_copy_streams    1..8 dedicated copy streams;
- *   kernel_grid       zero-copy kernel workgroups (0 = 64, enough to hold the link at its peak). */
+ *   kernel_grid       zero-copy kernel workgroups (0 = 64, enough to hold the link at its peak).
+ *                     A grid of at most 16 reserves each CU it runs on: its workgroups take
+ *                     the CU's whole LDS, so kernels that use LDS run on the other CUs. */
 int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams,
                         int kernel_grid);
 int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams,
