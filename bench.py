@@ -181,12 +181,50 @@ def cpu_baseline_scatter(chunks, sample_chunks: int = 4, reps: int = 3, threads:
                       f"on {threads} threads, best of {reps}"}
 
 
+def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
+    """Every ring copy of ``tokens`` more streamed passes, timed one by one.
+
+    The offload timing collector (HIP events on the transfer stream around
+    each copy, offload_timing.py:31-44) is switched on for these passes only,
+    after the timed ones, so its per-pass synchronize cannot slow them.
+    ``step()`` runs one pass. Returns launches, mean microseconds and GB/s per
+    copy size, and the size that moves the most bytes.
+    """
+    import torch
+
+    from flextensor_amd.timing import OffloadTimingCollector
+
+    if mgr.controller is None:  # everything resident: no ring copies
+        return None
+    collector = OffloadTimingCollector(list(mgr.order))
+    loader = mgr.loader
+    kept, loader.offload_timing_collector = loader.offload_timing_collector, collector
+    try:
+        for _ in range(tokens):
+            step()
+        torch.cuda.synchronize()
+        report = collector.report()
+    finally:
+        loader.offload_timing_collector = kept
+    by_size: dict[int, list[float]] = {}
+    for snap in report.passes:
+        for rec in snap.per_trap:
+            if rec.transfer_ms > 0:
+                by_size.setdefault(mgr.controller.transfer_bytes(rec.label), []).append(rec.transfer_ms)
+    sizes = {n: {"launches": len(ms), "mean_us": round(1e3 * sum(ms) / len(ms), 1),
+                 "GBps": round(n * len(ms) / sum(ms) / 1e6, 3)} for n, ms in sorted(by_size.items())}
+    top = max(by_size, key=lambda n: n * len(by_size[n]))
+    return {"passes": report.num_passes, "by_size": {str(n): v for n, v in sizes.items()}, "dominant_bytes": top,
+            "dominant": sizes[top]}
+
+
 def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
-                  include_patterns: tuple[str, ...] = ("layers.*",)) -> dict:
+                  include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4) -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
     streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
     units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
-    returned under ``_check`` so that runs with other units can be compared bitwise."""
+    returned under ``_check`` so that runs with other units can be compared bitwise. After the timed
+    tokens, ``ring_tokens`` more decode tokens time every ring copy on its own (:func:`ring_copy_stats`)."""
     import torch
 
     from flextensor_amd import hip
@@ -203,7 +241,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
                         profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9), copy_engine=copy_engine)
     mgr.offload(model, cfg)
     prompt = W.prompt_tokens(1, prefill, W.LLAMA_7B.vocab, seed=0).to(dev)
-    total = prefill + warmup + steps + 2
+    total = prefill + warmup + steps + ring_tokens + 2
     model.init_cache(1, total, dev)
     with torch.no_grad():
         model(prompt[:, :16], 0)  # discovery
@@ -236,6 +274,13 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
             pos += 1
         torch.cuda.synchronize()
         t_decode = time.perf_counter() - t0
+        state = {"tok": tok, "pos": pos}
+
+        def one_token():
+            state["tok"] = model(state["tok"], state["pos"]).argmax(-1)
+            state["pos"] += 1
+
+        ring = ring_copy_stats(mgr, one_token, ring_tokens) if ring_tokens else None
     usage = mgr.get_gpu_memory_usage()
     link = mgr.link.to_dict() if mgr.link is not None else None
     out = {
@@ -257,10 +302,45 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
                                                                        "pass_transfer_ms")},
         "copy_policy_source": None if mgr.link is None else mgr.link.source,
         "transfer_stream": hip.transfer_stream_probe(dev),
+        "ring_copies": ring,
+        "ring_copy_engine": _ring_engine(mgr),
         "_check": {"last_logits": last_logits, "tokens": torch.cat(toks, -1).cpu()},
     }
     mgr.release(preserve_model=False)
     return out
+
+
+def _ring_roofline(run: dict, measured_peak: float) -> dict | None:
+    """The host-link roofline of a decode's dominant kernel, its ring copy: bytes per launch over the mean
+    launch time, against PCIe Gen5 x16 and against the measured link peak (512 MiB, best of 20)."""
+    ring = run.get("ring_copies")
+    if not ring:
+        return None
+    d = ring["dominant"]
+    return {"kernel": run["ring_copy_engine"], "bound": "host link (PCIe Gen5 x16)", "achieved": d["GBps"],
+            "peak": PCIE_GEN5_X16_GBPS, "unit": "GB/s", "frac": round(d["GBps"] / PCIE_GEN5_X16_GBPS, 4),
+            "frac_of_measured_peak": round(d["GBps"] / measured_peak, 4), "traffic": None,
+            "bytes_per_launch": ring["dominant_bytes"], "avg_launch_us": d["mean_us"], "launches": d["launches"],
+            "timing": f"HIP events on the transfer stream around each ring copy, over {ring['passes']} decode "
+                      "tokens after the timed ones",
+            "by_size": ring["by_size"]}
+
+
+def _ring_engine(mgr) -> str:
+    """Which engine the manager's ring copies run on: its copy mode and the policy its controller carries."""
+    from flextensor_amd import _native as nat
+
+    ctl = mgr.controller
+    mode, policy = ctl.copy_mode, ctl.copy_policy
+    if mode == nat.COPY_AUTO:
+        if policy is None:
+            policy = nat.copy_policy(*nat.get_copy_policy())
+        biggest = max(ctl.transfer_bytes(x) for x in ctl.block_map_cpu)
+        mode = nat.COPY_KERNEL if biggest <= policy.kernel_max_bytes else nat.COPY_SDMA
+    if mode == nat.COPY_KERNEL:
+        grid = (policy.kernel_grid if policy is not None else nat.get_copy_policy()[3]) or 64
+        return f"zero_copy_kernel ({grid} workgroups)"
+    return "SDMA (hipMemcpyAsync)" if mode == nat.COPY_SDMA else "staged"
 
 
 def bench_mlp(steps: int, copy_engine: str) -> dict:
@@ -509,13 +589,19 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
     t_build = time.perf_counter() - t0
     mgr = OffloadManager("bench-70b")
     t0 = time.perf_counter()
-    # module order is the execution order of this decoder: plan at offload() time
+    # Module order is the execution order of this decoder, so no discovery pass. One profiled pass, a batch
+    # decode token like the timed ones, gives the measured pass rule the compute it weighs against the link.
     mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=0,
-                                     profiling_iters=0, max_gpu_mem_bytes=int(budget_gb * 1e9)))
-    t_setup = time.perf_counter() - t0
-    _log(f"70b: built {t_build:.1f} s, streaming set up {t_setup:.1f} s; "
-         f"{len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers")
+                                     profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9)))
     prompt = W.prompt_tokens(batch, prompt_len, s.vocab, seed=3).to(dev)
+    model.init_cache(batch, prompt_len + decode + 2, dev)
+    with torch.no_grad():
+        model(prompt[:, :1], 0)  # the profiling pass; the plan, the copy policy and the loader are built after it
+    torch.cuda.synchronize()
+    t_setup = time.perf_counter() - t0
+    _log(f"70b: built {t_build:.1f} s, profiled and streaming set up {t_setup:.1f} s; "
+         f"{len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers; "
+         f"{mgr.link.describe() if mgr.link is not None else 'default copy policy'}")
     model.init_cache(batch, prompt_len + decode + 2, dev)
     with torch.no_grad():
         torch.cuda.synchronize()
@@ -542,6 +628,10 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
         "step_s": t_step, "decode_tok_s": batch / t_step, "decode_effective_GBps": streamed / t_step / 1e9,
         "prefill_s": t_prefill, "gpu_weight_bytes": mgr.get_gpu_memory_usage().total_bytes,
         "budget_bytes": int(budget_gb * 1e9), "setup_s": t_setup,
+        "copy_policy": None if mgr.link is None else {k: mgr.link.to_dict()[k] for k in (
+            "kernel_max_bytes", "n_copy_streams", "kernel_grid", "link_bound", "pass_compute_ms",
+            "pass_transfer_ms")},
+        "ring_copy_engine": _ring_engine(mgr),
     }
     mgr.release(preserve_model=False)
     return out
@@ -996,7 +1086,9 @@ def engine_contention() -> dict:
     arena = HostArena(n)
     arena.tensor.random_(0, 256)
     dst = torch.empty(n, dtype=torch.uint8, device=dev)
-    saved = nat.get_copy_policy()
+
+    def grid_policy(grid):  # each copy carries its grid; the library default stays as it is
+        return nat.copy_policy(0, 2**63 - 1, 1, grid)
 
     def median_ms(fn, stream, reps):
         ts = []
@@ -1010,51 +1102,144 @@ def engine_contention() -> dict:
         return sorted(ts)[len(ts) // 2]
 
     out: dict = {"kernel_grid_GBps": {}, "scatter_alone_us": {}, "scatter_beside_copy_us": {}}
-    try:
-        for grid in (4, 8, 16, 32, 64, 128, 1024):
-            nat.set_copy_policy(saved[0], saved[1], saved[2], grid)
-            ms = median_ms(lambda: nat.copy_h2d(dst.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, comp.handle), comp, 5)
-            out["kernel_grid_GBps"][grid] = round(n / ms / 1e6, 2)
-        sizes = W.scatter_sizes()
-        chunk = max(plan_chunks(sizes, 512 * MiB)[:6], key=lambda c: len(c.pieces))
-        dests = {p.index: torch.empty(sizes[p.index], dtype=torch.uint8, device=dev) for p in chunk.pieces}
-        descs = [(p.chunk_off, _dst_base(dests[p.index]) + p.tensor_off, p.nbytes) for p in chunk.pieces if p.nbytes]
-        if any(off + k > chunk.nbytes for off, _, k in descs) or chunk.nbytes > n:
-            raise RuntimeError("scatter probe descriptors exceed the chunk")
-        payload = sum(k for _, _, k in descs)
-        src = torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev)
-        for tile in (8 << 10, 16 << 10, 32 << 10, 64 << 10):
-            plan = ScatterPlan(descs, tile)
-            out["scatter_alone_us"][tile] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
-            plan.close()
-        # the same bytes as one descriptor into one buffer, and torch's own device copy: the plain-copy rate
-        whole = torch.empty(n, dtype=torch.uint8, device=dev)
-        plan = ScatterPlan([(0, whole.data_ptr(), chunk.nbytes)])
-        out["scatter_one_descriptor_us"] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
+    for grid in (4, 8, 16, 32, 64, 128, 1024):
+        pol = grid_policy(grid)
+        ms = median_ms(lambda: nat.copy_h2d(dst.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, comp.handle, pol),
+                       comp, 5)
+        out["kernel_grid_GBps"][grid] = round(n / ms / 1e6, 2)
+    sizes = W.scatter_sizes()
+    chunk = max(plan_chunks(sizes, 512 * MiB)[:6], key=lambda c: len(c.pieces))
+    dests = {p.index: torch.empty(sizes[p.index], dtype=torch.uint8, device=dev) for p in chunk.pieces}
+    descs = [(p.chunk_off, _dst_base(dests[p.index]) + p.tensor_off, p.nbytes) for p in chunk.pieces if p.nbytes]
+    if any(off + k > chunk.nbytes for off, _, k in descs) or chunk.nbytes > n:
+        raise RuntimeError("scatter probe descriptors exceed the chunk")
+    payload = sum(k for _, _, k in descs)
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev)
+    for tile in (8 << 10, 16 << 10, 32 << 10, 64 << 10):
+        plan = ScatterPlan(descs, tile)
+        out["scatter_alone_us"][tile] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
         plan.close()
-        out["torch_copy_us"] = round(1e3 * median_ms(lambda: whole[:chunk.nbytes].copy_(src[:chunk.nbytes]), comp, 10), 1)
-        del whole
-        plan = ScatterPlan(descs)
-        for label, mode, grid in (("hipMemcpyAsync", nat.COPY_SDMA, 0), ("kernel_grid_1024", nat.COPY_KERNEL, 1024),
-                                  ("kernel_grid_64", nat.COPY_KERNEL, 64), ("kernel_grid_16", nat.COPY_KERNEL, 16),
-                                  ("kernel_grid_4", nat.COPY_KERNEL, 4)):
-            nat.set_copy_policy(saved[0], saved[1], saved[2], grid)
-            ts = []
-            for _ in range(8):
+    # the same bytes as one descriptor into one buffer, and torch's own device copy: the plain-copy rate
+    whole = torch.empty(n, dtype=torch.uint8, device=dev)
+    plan = ScatterPlan([(0, whole.data_ptr(), chunk.nbytes)])
+    out["scatter_one_descriptor_us"] = round(1e3 * median_ms(lambda: plan.run(src, comp), comp, 10), 1)
+    plan.close()
+    out["torch_copy_us"] = round(1e3 * median_ms(lambda: whole[:chunk.nbytes].copy_(src[:chunk.nbytes]), comp, 10), 1)
+    del whole
+    plan = ScatterPlan(descs)
+    for label, mode, grid in (("hipMemcpyAsync", nat.COPY_SDMA, 0), ("kernel_grid_1024", nat.COPY_KERNEL, 1024),
+                              ("kernel_grid_64", nat.COPY_KERNEL, 64), ("kernel_grid_16", nat.COPY_KERNEL, 16),
+                              ("kernel_grid_4", nat.COPY_KERNEL, 4)):
+        pol = grid_policy(grid)
+        ts = []
+        for _ in range(8):
+            torch.cuda.synchronize()
+            nat.copy_h2d(dst.data_ptr(), arena.ptr, n, mode, xs.handle, pol)
+            a, b = HipEvent(True), HipEvent(True)
+            comp.record_event(a)
+            plan.run(src, comp)
+            comp.record_event(b)
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        out["scatter_beside_copy_us"][label] = round(1e3 * sorted(ts)[len(ts) // 2], 1)
+    plan.close()
+    out["scatter_payload_bytes"] = payload
+    out["scatter_pieces"] = len(descs)
+    return out
+
+
+def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
+    """Idle link time between consecutive ring copies, by what each copy depends on.
+
+    ``copies`` host-to-device copies of B bytes from one pinned arena (two
+    halves) into two device slots (a 2-slot ring), on the device's transfer
+    stream, the whole chain enqueued at once, in four arrangements:
+
+    * ``back_to_back``: the copies alone, one after another on the transfer stream;
+    * ``slot_waits``: before each copy the transfer stream waits on an event the
+      compute stream recorded as that slot's release. The compute stream has
+      nothing queued, so every wait is already met when the copy is enqueued;
+    * ``ring``: the streamed pass (loaders.py:1534-1573): the compute stream
+      waits for each copy, reads its slot with a small kernel and records the
+      slot's release, which the copy two later waits on;
+    * ``ring_kernel``: ``ring`` with zero-copy kernel copies at 8 workgroups, the
+      link-bound policy.
+
+    Per arrangement and size, the median of ``reps`` chains: microseconds per
+    copy (HIP events on the transfer stream around the chain), GB/s, and the
+    idle link time per boundary, (chain time - copies x the best single copy)
+    / (copies - 1). The best single copy is the fastest of 5 lone copies with
+    the same engine.
+    """
+    import torch
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import link_model as L
+    from flextensor_amd.hip import HipEvent, HostArena, current_stream, transfer_stream
+
+    dev = torch.device("cuda", 0)
+    comp, xs = current_stream(dev), transfer_stream(dev)
+    kernel_policy = nat.copy_policy(0, 2**63 - 1, 1, L.RING_KERNEL_GRID)
+    acc = torch.zeros(1, dtype=torch.float32, device=dev)
+    out: dict = {"copies": copies, "sizes": {}}
+    for mib in sizes_mib:
+        nb = mib * MiB
+        arena = HostArena(2 * nb)
+        arena.tensor.random_(0, 256)
+        slots = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(2)]
+
+        def one(slot, mode, policy, stream):
+            nat.copy_h2d(slots[slot].data_ptr(), arena.ptr + slot * nb, nb, mode, stream.handle, policy)
+
+        def lone_ms(mode, policy):
+            best = float("inf")
+            for _ in range(5):
                 torch.cuda.synchronize()
-                nat.copy_h2d(dst.data_ptr(), arena.ptr, n, mode, xs.handle)
                 a, b = HipEvent(True), HipEvent(True)
-                comp.record_event(a)
-                plan.run(src, comp)
-                comp.record_event(b)
-                torch.cuda.synchronize()
-                ts.append(a.elapsed_time(b))
-            out["scatter_beside_copy_us"][label] = round(1e3 * sorted(ts)[len(ts) // 2], 1)
-        plan.close()
-        out["scatter_payload_bytes"] = payload
-        out["scatter_pieces"] = len(descs)
-    finally:
-        nat.set_copy_policy(*saved)
+                xs.record_event(a)
+                one(0, mode, policy, xs)
+                xs.record_event(b)
+                b.synchronize()
+                best = min(best, a.elapsed_time(b))
+            return best
+
+        def chain_ms(kind):
+            mode, policy = (nat.COPY_KERNEL, kernel_policy) if kind == "ring_kernel" else (nat.COPY_SDMA, None)
+            torch.cuda.synchronize()
+            released = [None, None]
+            start, end = HipEvent(True), HipEvent(True)
+            xs.wait_stream(comp)
+            xs.record_event(start)
+            for i in range(copies):
+                s = i % 2
+                if kind == "slot_waits":
+                    xs.wait_event(comp.record_event())
+                elif kind != "back_to_back" and released[s] is not None:
+                    xs.wait_event(released[s])
+                one(s, mode, policy, xs)
+                if kind in ("ring", "ring_kernel"):
+                    comp.wait_event(xs.record_event())
+                    acc.add_(slots[s][:4096].float().sum())
+                    released[s] = comp.record_event()
+            xs.record_event(end)
+            torch.cuda.synchronize()
+            return start.elapsed_time(end)
+
+        row: dict = {"bytes": nb}
+        lone = {"sdma": lone_ms(nat.COPY_SDMA, None), "kernel_g8": lone_ms(nat.COPY_KERNEL, kernel_policy)}
+        row["lone_copy_us"] = {k: round(v * 1e3, 1) for k, v in lone.items()}
+        for kind in ("back_to_back", "slot_waits", "ring", "ring_kernel"):
+            chain_ms(kind)  # warm-up
+            t = sorted(chain_ms(kind) for _ in range(reps))[reps // 2]
+            base = lone["kernel_g8" if kind == "ring_kernel" else "sdma"]
+            row[kind] = {"us_per_copy": round(t * 1e3 / copies, 1), "GBps": round(copies * nb / t / 1e6, 2),
+                         "idle_us_per_boundary": round((t - copies * base) * 1e3 / (copies - 1), 1)}
+            _log(f"copy chain {mib} MiB {kind}: {row[kind]}")
+        bad = [i for i in range(2) if not torch.equal(slots[i].cpu(), arena.tensor[i * nb:(i + 1) * nb])]
+        row["slots_bit_exact"] = not bad
+        out["sizes"][str(mib)] = row
+        del slots, arena
+        torch.cuda.empty_cache()
     return out
 
 
@@ -1080,6 +1265,8 @@ def main() -> int:
                     help="only print the host-to-device GB/s of each copy engine over chunk sizes 64 KiB-512 MiB")
     ap.add_argument("--engine-contention", action="store_true",
                     help="only print how each copy engine shares the GPU with the scatter kernel")
+    ap.add_argument("--copy-chain", action="store_true",
+                    help="only print the idle link time between chained ring copies, by what each copy waits on")
     ap.add_argument("--hbm-read-probe", action="store_true",
                     help="only print the plain HBM read rate (the ceiling the HBM-bound kernels are compared with)")
     ap.add_argument("--skip-scatter", action="store_true")
@@ -1118,6 +1305,9 @@ def main() -> int:
         return traffic_probe(args)
     if args.engine_contention:
         print(json.dumps(engine_contention()), flush=True)
+        return 0
+    if args.copy_chain:
+        print(json.dumps({"copy_chain": copy_chain()}), flush=True)
         return 0
     if args.fp8_linear_only:
         print(json.dumps({"fp8_linear": bench_fp8_linear(), "fp8_prefill": bench_fp8_prefill()}), flush=True)
@@ -1193,6 +1383,7 @@ def main() -> int:
                  "pct_of_theoretical": round(100 * llama["decode_effective_GBps"] / PCIE_GEN5_X16_GBPS, 2),
                  "peak_sdma_GBps": round(peak["sdma"], 3), "peak_kernel_GBps": round(peak["kernel"], 3)},
         "roofline": None,
+        "roofline_ring_copy": _ring_roofline(llama, measured_peak),
         "cpu_baseline": None if args.skip_cpu_baseline else cpu_llama_decode_baseline(),
     }
     gc.collect()
@@ -1214,6 +1405,7 @@ def main() -> int:
             "pct_of_measured_peak": round(100 * fine["decode_effective_GBps"] / measured_peak, 2),
             "gpu_weight_bytes": fine["gpu_weight_bytes"],
             "copy_policy": fine["copy_policy"],
+            "ring_copies": _ring_roofline(fine, measured_peak),
             "prefill_logits_and_tokens_bitwise_equal_to_layer_units": same,
         }
         _log(f"llama7b finer units: {line['llama7b_finer_units']}")
@@ -1294,6 +1486,27 @@ def main() -> int:
     return 0
 
 
+def _finish() -> None:
+    """Leave nothing in flight at exit: drop what the legs left for the collector (their managers are already
+    released), wait for the device, and let the library release its own threads, staging buffers, streams
+    and events (``ftx_shutdown``) while the runtime is still up."""
+    import gc
+
+    gc.collect()
+    if "torch" in sys.modules:
+        import torch
+
+        if torch.cuda.is_available() and torch.cuda.is_initialized():
+            torch.cuda.synchronize()
+    nat = sys.modules.get("flextensor_amd._native")
+    if nat is not None and nat.live():
+        nat.shutdown()
+
+
 if __name__ == "__main__":
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    sys.exit(main())
+    try:
+        code = main()
+    finally:
+        _finish()
+    sys.exit(code)

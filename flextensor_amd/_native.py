@@ -12,6 +12,7 @@ from __future__ import annotations
 import atexit
 import ctypes
 import os
+import sys
 import threading
 from pathlib import Path
 
@@ -63,6 +64,36 @@ class FtxDesc(ctypes.Structure):
     _fields_ = [("src_off", ctypes.c_uint64), ("dst", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
 
 
+class CopyPolicy(ctypes.Structure):
+    """Mirror of ``ftx_copy_policy``: a copy policy a caller owns and passes with each copy.
+
+    ``kernel_max_bytes``: chunks up to this go to the zero-copy kernel under
+    ``COPY_AUTO``; ``split_min_bytes``: SDMA copies from this size up are split
+    over ``n_copy_streams`` (1..8); ``kernel_grid``: zero-copy workgroups (0 is
+    the library's default, 64).
+    """
+
+    _fields_ = [("kernel_max_bytes", ctypes.c_uint64), ("split_min_bytes", ctypes.c_uint64),
+                ("n_copy_streams", ctypes.c_int32), ("kernel_grid", ctypes.c_int32)]
+
+    def astuple(self) -> tuple[int, int, int, int]:
+        return (int(self.kernel_max_bytes), int(self.split_min_bytes), int(self.n_copy_streams),
+                int(self.kernel_grid))
+
+    def __eq__(self, other: object) -> bool:
+        return isinstance(other, CopyPolicy) and self.astuple() == other.astuple()
+
+    def __repr__(self) -> str:
+        km, sm, ns, kg = self.astuple()
+        return f"CopyPolicy(kernel_max_bytes={km}, split_min_bytes={sm}, n_copy_streams={ns}, kernel_grid={kg})"
+
+
+def copy_policy(kernel_max_bytes: int, split_min_bytes: int, n_copy_streams: int, kernel_grid: int = 0) -> CopyPolicy:
+    """A :class:`CopyPolicy`; ``split_min_bytes`` above the 64-bit range means "never split"."""
+    return CopyPolicy(int(kernel_max_bytes), min(int(split_min_bytes), 2**64 - 1), int(n_copy_streams),
+                      int(kernel_grid))
+
+
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _int = ctypes.c_int
@@ -98,6 +129,8 @@ _SIGNATURES: dict[str, list] = {
     "ftx_event_synchronize": [_vp],
     "ftx_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(ctypes.c_float)],
     "ftx_copy_h2d": [_vp, _vp, _sz, _int, _vp],
+    "ftx_copy_h2d_policy": [_vp, _vp, _sz, _int, ctypes.POINTER(CopyPolicy), _vp],
+    "ftx_shutdown": [],
     "ftx_set_copy_policy": [_sz, _sz, _int, _int],
     "ftx_get_copy_policy": [ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_int), ctypes.POINTER(_int)],
     "ftx_scatter_plan_create": [ctypes.POINTER(FtxDesc), _int, _sz, ctypes.POINTER(_vp)],
@@ -127,11 +160,25 @@ _alive = True
 
 
 def _mark_exit() -> None:
+    """At interpreter exit: stop finalizers from releasing handles, then let the library release what it
+    holds (``ftx_shutdown``: wait for the devices, join its host threads, free its staging buffers, copy
+    streams and events) while the HIP runtime is still up. Registered after ``import torch``, so it runs
+    ahead of torch's own exit handlers."""
     global _alive
     _alive = False
+    if _lib is not None:
+        rc = _lib.ftx_shutdown()
+        if rc != FTX_OK:  # the process is ending either way; say what could not be released
+            msg = (_lib.ftx_last_error() or b"").decode(errors="replace")
+            print(f"flextensor_amd: ftx_shutdown at exit returned {rc}: {msg}", file=sys.stderr, flush=True)
 
 
 atexit.register(_mark_exit)
+
+
+def shutdown() -> None:
+    """``ftx_shutdown``: release the library's own resources now; later work is refused (idempotent)."""
+    call("ftx_shutdown")
 
 
 def live() -> bool:
@@ -219,12 +266,13 @@ HOST_REGISTER_REFUSED = (
 
 
 def arena_register(ptr: int, nbytes: int, flags: int = 0) -> None:
-    """Page-lock existing host memory in place: refused in this build (``HOST_REGISTER_REFUSED``).
+    """Page-lock existing host memory in place: refused in this build.
 
-    ``ftx_arena_register`` stays in the C ABI for hosts that allow it; the
-    Python path never reaches it.
+    ``ftx_arena_register`` returns ``FTX_ERR_UNSUPPORTED`` for every input
+    without calling the runtime; this raises that as :class:`FtxError`.
     """
-    raise FtxError(FTX_ERR_UNSUPPORTED, HOST_REGISTER_REFUSED)
+    call("ftx_arena_register", ptr, nbytes, flags)
+    raise AssertionError("ftx_arena_register accepted a registration it is built to refuse")
 
 
 def arena_unregister(ptr: int) -> None:
@@ -261,8 +309,12 @@ def event_query(event: int) -> bool:
     return bool(done.value)
 
 
-def copy_h2d(dst: int, src: int, nbytes: int, mode: int, stream: int) -> None:
-    call("ftx_copy_h2d", dst, src, nbytes, mode, stream)
+def copy_h2d(dst: int, src: int, nbytes: int, mode: int, stream: int, policy: CopyPolicy | None = None) -> None:
+    """Host-to-device copy; ``policy`` None copies under the library default (``set_copy_policy``)."""
+    if policy is None:
+        call("ftx_copy_h2d", dst, src, nbytes, mode, stream)
+    else:
+        call("ftx_copy_h2d_policy", dst, src, nbytes, mode, ctypes.byref(policy), stream)
 
 
 def set_copy_policy(kernel_max_bytes: int, split_min_bytes: int, n_copy_streams: int, kernel_grid: int = 0) -> None:

@@ -245,15 +245,16 @@ class AllocationBlock:
         return [s.view(slot) for s in self.slots], slot[: block.numel()]
 
     def copy_to(self, gpu_view: torch.Tensor, non_blocking: bool = True, stream: Any = None,
-                mode: int = nat.COPY_AUTO) -> None:
-        """Copy the whole block into ``gpu_view`` on ``stream`` (default: current stream)."""
+                mode: int = nat.COPY_AUTO, policy: nat.CopyPolicy | None = None) -> None:
+        """Copy the whole block into ``gpu_view`` on ``stream`` (default: current stream), under the copy
+        ``policy`` of the caller (None: the library default)."""
         from .hip import copy_h2d
 
         block = self._require_block()
         if gpu_view.device.type != "cuda":
             gpu_view.copy_(block)
             return
-        copy_h2d(gpu_view, block, mode, stream)
+        copy_h2d(gpu_view, block, mode, stream, policy=policy)
         if not non_blocking:
             (stream if stream is not None else _current(gpu_view.device)).synchronize()
 

@@ -7,6 +7,13 @@ GPU views at the same byte offsets (the model's parameters alias them), and
 ``schedule_transfer(label)`` = one host-to-device copy of the label's block
 into its slot on the current (transfer) stream.
 
+Each controller carries its own copy engine (``copy_mode``) and copy policy
+(``copy_policy``, a :class:`~flextensor_amd._native.CopyPolicy` passed with
+every copy; None copies under the library default), so managers that stream
+side by side in one process each copy as their own link measurement chose,
+as the reference's named managers copy independently
+(offload_manager.py:2817-2850).
+
 :class:`RawBlockController` follows ``RawBlockController`` (loaders.py:903-1101):
 back-to-back packing without alignment; dense tensors are copied as raw
 storage bytes, tensors with gaps as C-contiguous copies.
@@ -173,6 +180,7 @@ class AllocationBlockController:
         host_pinner: HostPinner,
         release_tensor_memory: bool = True,
         copy_mode: int = nat.COPY_AUTO,
+        copy_policy: nat.CopyPolicy | None = None,
         memory_alignment: int = 128,
         shm_block_name_map: Mapping[str, str] | None = None,
         load_from_shm: bool = False,
@@ -186,6 +194,7 @@ class AllocationBlockController:
         self.host_pinner = host_pinner
         self.release_tensor_memory = release_tensor_memory
         self.copy_mode = copy_mode
+        self.copy_policy = copy_policy
         self.shm_block_name_map = dict(shm_block_name_map or {})
         self.load_from_shm = load_from_shm
         self.block_map_cpu: dict[str, AllocationBlock] = {}
@@ -250,7 +259,7 @@ class AllocationBlockController:
     def schedule_transfer(self, label: str, non_blocking: bool = True) -> None:
         """One host-to-device copy of ``label``'s block into its slot, on the current stream."""
         self.block_map_cpu[label].copy_to(self.gpu_block_view_map[label], non_blocking=non_blocking,
-                                          mode=self.copy_mode)
+                                          mode=self.copy_mode, policy=self.copy_policy)
 
     def transfer_bytes(self, label: str) -> int:
         return self.block_map_cpu[label].nbytes
@@ -312,11 +321,13 @@ class RawBlockController:
         host_pinner: HostPinner,
         release_tensor_memory: bool = True,
         copy_mode: int = nat.COPY_AUTO,
+        copy_policy: nat.CopyPolicy | None = None,
     ) -> None:
         self.device_gpu = torch.device(device_gpu)
         self.host_pinner = host_pinner
         self.release_tensor_memory = release_tensor_memory
         self.copy_mode = copy_mode
+        self.copy_policy = copy_policy
         self.label_to_block_id = dict(label_to_block_id)
         self.block_map_cpu: dict[str, torch.Tensor] = {}
         self.block_meta_map: dict[str, list] = {}
@@ -395,7 +406,7 @@ class RawBlockController:
         from .hip import copy_h2d, current_stream
 
         dst = self.gpu_block_view_map[label]
-        copy_h2d(dst, self.block_map_cpu[label], self.copy_mode)
+        copy_h2d(dst, self.block_map_cpu[label], self.copy_mode, policy=self.copy_policy)
         if not non_blocking:
             current_stream(dst.device).synchronize()
 

@@ -21,6 +21,15 @@ int hip_fail(hipError_t err, const char *what);
     if (ftx_err_ != hipSuccess) return ::ftx::hip_fail(ftx_err_, #expr); \
   } while (0)
 
+// Set once by ftx_shutdown. Entry points that start work or allocate refuse
+// afterwards (FTX_REQUIRE_LIVE); releasing, waiting and querying still work.
+bool is_shut_down();
+#define FTX_REQUIRE_LIVE()                                                                        \
+  do {                                                                                            \
+    if (::ftx::is_shut_down())                                                                    \
+      return ::ftx::fail(FTX_ERR_UNSUPPORTED, "the library has been shut down (ftx_shutdown)"); \
+  } while (0)
+
 // Default bytes per wave tile of the scatter kernel: one round of 8 loads and
 // 8 non-temporal stores of 16 bytes per lane (fastest of 8/16/32 KiB on the
 // 2000-tensor set's 512 MiB chunks: 5.94 TB/s against 5.78 and 5.77).
@@ -88,6 +97,9 @@ int staged_copy_h2d(void *dst, const void *src, size_t nbytes, hipStream_t strea
 int host_memcpy(void *dst, const void *src, size_t nbytes);
 int set_staging_policy(size_t piece_bytes, int threads);
 void get_staging_policy(size_t *piece_bytes, int *threads);
+// Joins the host threads and frees every device's staging buffers and events
+// (each device made current in turn). Returns the first failure, after trying all.
+int staged_shutdown();
 
 // Kernel launchers (ftx_kernels.hip). Each returns hipSuccess or the launch error.
 // `reserve_lds` bytes of dynamic LDS per workgroup (0: none); see zero_copy_kernel.

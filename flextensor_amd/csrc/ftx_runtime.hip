@@ -2,6 +2,7 @@
 // streams/events, scatter plans and checksums. Declarations and the reference
 // constructs each entry point replaces are in include/ftx.h.
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -32,6 +33,9 @@ struct CopyPolicy {
   int kernel_grid = 0;                 // 0: kZeroCopyDefaultGrid
 };
 
+int check_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams, int kernel_grid,
+                 CopyPolicy *out);
+
 struct DeviceState {
   bool ready = false;
   int cu_count = 0;
@@ -46,10 +50,10 @@ struct DeviceState {
 
 struct ArenaRecord {
   size_t nbytes;
-  void *dev;
-  bool registered;  // true: page-locked in place (hipHostRegister); false: hipHostMalloc
+  void *dev;  // device-visible address of the arena (hipHostGetDevicePointer)
 };
 
+std::atomic<bool> g_shut_down{false};
 std::mutex g_mutex;      // guards g_policy and g_arenas
 std::mutex g_dev_mutex;  // guards first-use setup of g_devices
 CopyPolicy g_policy;
@@ -89,11 +93,16 @@ int device_state(DeviceState **out) {
     FTX_HIP(hipMemGetInfo(&free_b, &total_b));
     // Copy streams are created on the first split copy (copy_streams_ready):
     // every extra stream changes how streams share the device's hardware queues.
-    // The whole LDS of a CU, for small zero-copy grids. Where the runtime will
-    // not grant it, copies share their CUs as before.
-    int lds = 0;
-    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && lds > 0 &&
-        allow_zero_copy_lds(static_cast<size_t>(lds)) == hipSuccess)
+    // The whole LDS of a CU, for small zero-copy grids: the per-CU figure,
+    // capped at what one workgroup may ask for. Where the runtime will not
+    // grant it, copies share their CUs as before.
+    int lds_cu = 0, lds_block = 0;
+    if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess)
+      lds_cu = 0;
+    if (hipDeviceGetAttribute(&lds_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      lds_block = 0;
+    const int lds = lds_cu > 0 && lds_block > 0 ? std::min(lds_cu, lds_block) : std::max(lds_cu, lds_block);
+    if (lds > 0 && allow_zero_copy_lds(static_cast<size_t>(lds)) == hipSuccess)
       st.copy_reserve_lds = static_cast<size_t>(lds);
     (void)hipGetLastError();
     st.cu_count = cus;
@@ -242,7 +251,70 @@ int copy_kernel(void *dst, const void *src, size_t nbytes, hipStream_t stream, c
   return FTX_OK;
 }
 
+int check_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams, int kernel_grid,
+                 CopyPolicy *out) {
+  if (n_copy_streams < 1 || n_copy_streams > kMaxCopyStreams)
+    return fail(FTX_ERR_INVALID, "n_copy_streams must be in [1, 8]");
+  if (kernel_grid < 0 || kernel_grid > (1 << 20)) return fail(FTX_ERR_INVALID, "kernel_grid must be in [0, 2^20]");
+  out->kernel_max_bytes = kernel_max_bytes;
+  out->split_min_bytes = split_min_bytes;
+  out->n_copy_streams = n_copy_streams;
+  out->kernel_grid = kernel_grid;
+  return FTX_OK;
+}
+
+// Waits for every device, then destroys the split-copy streams and events of
+// each device the library set up. Every device is tried; the first failure
+// is returned.
+int release_devices() {
+  int first = FTX_OK;
+  auto keep = [&first](int rc) {
+    if (first == FTX_OK) first = rc;
+  };
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) {  // no device or no driver: nothing ran, nothing to release
+    (void)hipGetLastError();
+    count = 0;
+  }
+  int prev = -1;
+  if (count > 0 && hipGetDevice(&prev) != hipSuccess) {
+    (void)hipGetLastError();
+    prev = -1;
+  }
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  for (int d = 0; d < std::min(count, kMaxDevices); ++d) {
+    hipError_t err = hipSetDevice(d);
+    if (err == hipSuccess) err = hipDeviceSynchronize();
+    if (err != hipSuccess) {
+      keep(hip_fail(err, "hipDeviceSynchronize at shutdown"));
+      continue;
+    }
+    DeviceState &st = g_devices[d];
+    for (int i = 0; i < kMaxCopyStreams; ++i) {
+      if (st.copy_streams[i]) {
+        err = hipStreamDestroy(st.copy_streams[i]);
+        if (err != hipSuccess) keep(hip_fail(err, "hipStreamDestroy(copy stream)"));
+        st.copy_streams[i] = nullptr;
+      }
+      if (st.join_events[i]) {
+        err = hipEventDestroy(st.join_events[i]);
+        if (err != hipSuccess) keep(hip_fail(err, "hipEventDestroy(join event)"));
+        st.join_events[i] = nullptr;
+      }
+    }
+    if (st.fork_event) {
+      err = hipEventDestroy(st.fork_event);
+      if (err != hipSuccess) keep(hip_fail(err, "hipEventDestroy(fork event)"));
+      st.fork_event = nullptr;
+    }
+  }
+  if (prev >= 0 && hipSetDevice(prev) != hipSuccess) (void)hipGetLastError();
+  return first;
+}
+
 }  // namespace
+
+bool is_shut_down() { return g_shut_down.load(); }
 
 void set_error(const std::string &msg) { g_last_error = msg; }
 
@@ -356,6 +428,15 @@ const char *ftx_last_error(void) { return ftx::g_last_error.c_str(); }
 
 int ftx_version(void) { return 1; }
 
+int ftx_shutdown(void) {
+  if (ftx::g_shut_down.exchange(true)) return FTX_OK;  // already done
+  // Devices first: the staging buffers and events are only released once no
+  // queued copy can still read them.
+  const int rc_dev = ftx::release_devices();
+  const int rc_stage = ftx::staged_shutdown();
+  return rc_dev != FTX_OK ? rc_dev : rc_stage;
+}
+
 int ftx_device_count(int *count) {
   if (!count) return ftx::fail(FTX_ERR_INVALID, "count is null");
   FTX_HIP(hipGetDeviceCount(count));
@@ -389,6 +470,7 @@ int ftx_device_info(int *cu_count, int *xcd_count, size_t *total_mem) {
 }
 
 int ftx_arena_alloc(size_t nbytes, unsigned flags, void **host) {
+  FTX_REQUIRE_LIVE();
   if (!host) return ftx::fail(FTX_ERR_INVALID, "host is null");
   if (nbytes == 0) return ftx::fail(FTX_ERR_INVALID, "arena size must be > 0");
   if ((flags & FTX_ARENA_COHERENT) && (flags & FTX_ARENA_NONCOHERENT))
@@ -408,7 +490,7 @@ int ftx_arena_alloc(size_t nbytes, unsigned flags, void **host) {
   }
   {
     std::lock_guard<std::mutex> lock(ftx::g_mutex);
-    ftx::g_arenas[reinterpret_cast<uintptr_t>(p)] = ftx::ArenaRecord{nbytes, dev, false};
+    ftx::g_arenas[reinterpret_cast<uintptr_t>(p)] = ftx::ArenaRecord{nbytes, dev};
   }
   *host = p;
   return FTX_OK;
@@ -419,8 +501,7 @@ int ftx_arena_free(void *host) {
   {
     std::lock_guard<std::mutex> lock(ftx::g_mutex);
     auto it = ftx::g_arenas.find(reinterpret_cast<uintptr_t>(host));
-    if (it == ftx::g_arenas.end() || it->second.registered)
-      return ftx::fail(FTX_ERR_INVALID, "pointer is not an arena from ftx_arena_alloc");
+    if (it == ftx::g_arenas.end()) return ftx::fail(FTX_ERR_INVALID, "pointer is not an arena from ftx_arena_alloc");
     ftx::g_arenas.erase(it);
   }
   FTX_HIP(hipHostFree(host));
@@ -428,35 +509,18 @@ int ftx_arena_free(void *host) {
 }
 
 int ftx_arena_register(void *host, size_t nbytes, unsigned flags) {
+  (void)host;
+  (void)nbytes;
   (void)flags;
-  if (!host || nbytes == 0) return ftx::fail(FTX_ERR_INVALID, "host is null or size is 0");
-  {
-    std::lock_guard<std::mutex> lock(ftx::g_mutex);
-    if (ftx::g_arenas.count(reinterpret_cast<uintptr_t>(host)))
-      return ftx::fail(FTX_ERR_INVALID, "memory is already pinned by this library");
-  }
-  FTX_HIP(hipHostRegister(host, nbytes, hipHostRegisterPortable | hipHostRegisterMapped));
-  void *dev = nullptr;
-  hipError_t err = hipHostGetDevicePointer(&dev, host, 0);
-  if (err != hipSuccess) {
-    (void)hipHostUnregister(host);
-    return ftx::hip_fail(err, "hipHostGetDevicePointer");
-  }
-  std::lock_guard<std::mutex> lock(ftx::g_mutex);
-  ftx::g_arenas[reinterpret_cast<uintptr_t>(host)] = ftx::ArenaRecord{nbytes, dev, true};
-  return FTX_OK;
+  return ftx::fail(FTX_ERR_UNSUPPORTED,
+                   "in-place page-locking (hipHostRegister of existing memory) is refused in this build: the MI355X "
+                   "hosts it targets reject it, and the failed call's error can surface in the next GPU call; "
+                   "allocate the block with ftx_arena_alloc, or stream a pageable source with FTX_COPY_STAGED");
 }
 
 int ftx_arena_unregister(void *host) {
-  {
-    std::lock_guard<std::mutex> lock(ftx::g_mutex);
-    auto it = ftx::g_arenas.find(reinterpret_cast<uintptr_t>(host));
-    if (it == ftx::g_arenas.end() || !it->second.registered)
-      return ftx::fail(FTX_ERR_INVALID, "pointer was not registered with ftx_arena_register");
-    ftx::g_arenas.erase(it);
-  }
-  FTX_HIP(hipHostUnregister(host));
-  return FTX_OK;
+  (void)host;
+  return ftx::fail(FTX_ERR_INVALID, "nothing is registered in place: ftx_arena_register is refused in this build");
 }
 
 int ftx_host_device_ptr(void *host, void **dev) {
@@ -469,6 +533,7 @@ int ftx_host_device_ptr(void *host, void **dev) {
 }
 
 int ftx_device_alloc(size_t nbytes, void **dev) {
+  FTX_REQUIRE_LIVE();
   if (!dev || nbytes == 0) return ftx::fail(FTX_ERR_INVALID, "dev is null or size is 0");
   FTX_HIP(hipMalloc(dev, nbytes));
   return FTX_OK;
@@ -481,6 +546,7 @@ int ftx_device_free(void *dev) {
 }
 
 int ftx_memset_async(void *dev, int value, size_t nbytes, void *stream) {
+  FTX_REQUIRE_LIVE();
   if (nbytes == 0) return FTX_OK;
   if (!dev) return ftx::fail(FTX_ERR_INVALID, "dev is null");
   int rc = ftx::check_device_range(dev, nbytes, "memset destination");
@@ -490,6 +556,7 @@ int ftx_memset_async(void *dev, int value, size_t nbytes, void *stream) {
 }
 
 int ftx_copy_d2h(void *dst_host, const void *src_dev, size_t nbytes, void *stream) {
+  FTX_REQUIRE_LIVE();
   if ((!dst_host || !src_dev) && nbytes) return ftx::fail(FTX_ERR_INVALID, "null argument");
   if (nbytes == 0) return FTX_OK;
   int rc = ftx::check_device_range(src_dev, nbytes, "copy source");
@@ -499,6 +566,7 @@ int ftx_copy_d2h(void *dst_host, const void *src_dev, size_t nbytes, void *strea
 }
 
 int ftx_stream_create(void **stream) {
+  FTX_REQUIRE_LIVE();
   if (!stream) return ftx::fail(FTX_ERR_INVALID, "stream is null");
   hipStream_t s = nullptr;
   FTX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
@@ -531,6 +599,7 @@ int ftx_stream_query(void *stream, int *done) {
 }
 
 int ftx_event_create(unsigned flags, void **event) {
+  FTX_REQUIRE_LIVE();
   if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
   hipEvent_t e = nullptr;
   FTX_HIP(hipEventCreateWithFlags(&e, (flags & FTX_EVENT_TIMING) ? hipEventDefault : hipEventDisableTiming));
@@ -545,12 +614,14 @@ int ftx_event_destroy(void *event) {
 }
 
 int ftx_event_record(void *event, void *stream) {
+  FTX_REQUIRE_LIVE();
   if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
   FTX_HIP(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
   return FTX_OK;
 }
 
 int ftx_timestamp(void *dev_slot, void *stream) {
+  FTX_REQUIRE_LIVE();
   if (!dev_slot) return ftx::fail(FTX_ERR_INVALID, "timestamp slot is null");
   if (reinterpret_cast<uintptr_t>(dev_slot) % 8) return ftx::fail(FTX_ERR_INVALID, "timestamp slot is not 8-byte aligned");
   int rc = ftx::check_device_range(dev_slot, 8, "timestamp slot");
@@ -568,6 +639,7 @@ int ftx_wall_clock_khz(int *khz) {
 }
 
 int ftx_stream_wait_event(void *stream, void *event) {
+  FTX_REQUIRE_LIVE();
   if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
   FTX_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0));
   return FTX_OK;
@@ -599,13 +671,23 @@ int ftx_event_elapsed_ms(void *start, void *end, float *ms) {
 }
 
 int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stream) {
-  if (nbytes == 0) return FTX_OK;
-  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  return ftx_copy_h2d_policy(dst, src, nbytes, mode, nullptr, stream);
+}
+
+int ftx_copy_h2d_policy(void *dst, const void *src, size_t nbytes, int mode, const ftx_copy_policy *policy,
+                        void *stream) {
+  FTX_REQUIRE_LIVE();
   ftx::CopyPolicy pol;
-  {
+  if (policy != nullptr) {
+    int rc = ftx::check_policy(policy->kernel_max_bytes, policy->split_min_bytes, policy->n_copy_streams,
+                               policy->kernel_grid, &pol);
+    if (rc != FTX_OK) return rc;
+  } else {
     std::lock_guard<std::mutex> lock(ftx::g_mutex);
     pol = ftx::g_policy;
   }
+  if (nbytes == 0) return FTX_OK;
+  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (mode) {
     case FTX_COPY_SDMA:
@@ -640,6 +722,7 @@ int ftx_get_staging_policy(size_t *piece_bytes, int *n_threads) {
 }
 
 int ftx_host_memcpy(void *dst, const void *src, size_t nbytes) {
+  FTX_REQUIRE_LIVE();
   if (nbytes == 0) return FTX_OK;
   if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
   const uintptr_t d = reinterpret_cast<uintptr_t>(dst), sp = reinterpret_cast<uintptr_t>(src);
@@ -648,14 +731,11 @@ int ftx_host_memcpy(void *dst, const void *src, size_t nbytes) {
 }
 
 int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams, int kernel_grid) {
-  if (n_copy_streams < 1 || n_copy_streams > ftx::kMaxCopyStreams)
-    return ftx::fail(FTX_ERR_INVALID, "n_copy_streams must be in [1, 8]");
-  if (kernel_grid < 0 || kernel_grid > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "kernel_grid out of range");
+  ftx::CopyPolicy pol;
+  int rc = ftx::check_policy(kernel_max_bytes, split_min_bytes, n_copy_streams, kernel_grid, &pol);
+  if (rc != FTX_OK) return rc;
   std::lock_guard<std::mutex> lock(ftx::g_mutex);
-  ftx::g_policy.kernel_max_bytes = kernel_max_bytes;
-  ftx::g_policy.split_min_bytes = split_min_bytes;
-  ftx::g_policy.n_copy_streams = n_copy_streams;
-  ftx::g_policy.kernel_grid = kernel_grid;
+  ftx::g_policy = pol;
   return FTX_OK;
 }
 
@@ -795,6 +875,7 @@ int ftx_fp8_linear(const void *x, const void *w, const void *scale, void *y, int
 int ftx_fp8_linear_group(const void *x, int group, const void *const *w, const void *const *scale, void *const *y,
                          const int64_t *n, int64_t m, int64_t k, void *workspace, size_t workspace_bytes,
                          void *stream) {
+  FTX_REQUIRE_LIVE();
   ftx::Fp8LinearLaunch p;
   int rc = plan_fp8(m, n, group, k, &p);
   if (rc != FTX_OK) return rc;
@@ -804,6 +885,7 @@ int ftx_fp8_linear_group(const void *x, int group, const void *const *w, const v
 
 int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,
                           void *stream) {
+  FTX_REQUIRE_LIVE();
   ftx::Fp8LinearLaunch p;
   int rc = plan_fp8(m, &n, 1, k, &p);
   if (rc != FTX_OK) return rc;
@@ -823,6 +905,7 @@ int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void 
 }
 
 int ftx_scatter_plan_create(const ftx_desc *descs, int n_desc, size_t tile_bytes, ftx_scatter_plan **plan) {
+  FTX_REQUIRE_LIVE();
   if (!plan) return ftx::fail(FTX_ERR_INVALID, "plan is null");
   PlanTables t;
   int rc = build_plan_tables(descs, n_desc, tile_bytes, &t);
@@ -861,6 +944,7 @@ int ftx_scatter_plan_info(const ftx_scatter_plan *plan, int *n_desc, int64_t *n_
 }
 
 int ftx_scatter_run(const ftx_scatter_plan *plan, const void *chunk, void *stream) {
+  FTX_REQUIRE_LIVE();
   if (!plan) return ftx::fail(FTX_ERR_INVALID, "plan is null");
   if (plan->dev.n_tiles == 0) return FTX_OK;
   if (!chunk) return ftx::fail(FTX_ERR_INVALID, "chunk is null");
@@ -871,6 +955,7 @@ int ftx_scatter_run(const ftx_scatter_plan *plan, const void *chunk, void *strea
 }
 
 int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stream) {
+  FTX_REQUIRE_LIVE();
   PlanTables t;
   int rc = build_plan_tables(descs, n_desc, 0, &t);
   if (rc != FTX_OK) return rc;
@@ -895,6 +980,7 @@ int ftx_scatter(const void *chunk, const ftx_desc *descs, int n_desc, void *stre
 }
 
 int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, void *stream) {
+  FTX_REQUIRE_LIVE();
   if (nbytes == 0) return FTX_OK;
   if (!dev || !sink) return ftx::fail(FTX_ERR_INVALID, "null pointer");
   if (reinterpret_cast<uintptr_t>(dev) % 16 != 0 || nbytes % 16 != 0)
@@ -909,6 +995,7 @@ int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, voi
 }
 
 int ftx_mfma_probe(int workgroups, int iters, void *sink, void *stream) {
+  FTX_REQUIRE_LIVE();
   if (!sink) return ftx::fail(FTX_ERR_INVALID, "null pointer");
   if (reinterpret_cast<uintptr_t>(sink) % 4 != 0) return ftx::fail(FTX_ERR_INVALID, "sink needs 4-byte alignment");
   if (workgroups <= 0 || workgroups > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "workgroups must be in [1, 2^20]");
@@ -920,6 +1007,7 @@ int ftx_mfma_probe(int workgroups, int iters, void *sink, void *stream) {
 }
 
 int ftx_checksum64(const void *dev, size_t nbytes, void *stream, uint64_t *out) {
+  FTX_REQUIRE_LIVE();
   if (!out) return ftx::fail(FTX_ERR_INVALID, "out is null");
   if (nbytes == 0) {
     *out = ftx::splitmix64(0);

@@ -54,13 +54,18 @@ struct CopyJob {
 
 class HostCopyPool {
  public:
-  ~HostCopyPool() {
+  ~HostCopyPool() { shutdown(); }
+
+  // Stops and joins the worker threads. Later copies run on the caller alone.
+  void shutdown() {
+    std::vector<std::thread> workers;
     {
       std::lock_guard<std::mutex> lock(m_);
       stop_ = true;
+      workers.swap(workers_);
     }
     cv_.notify_all();
-    for (auto &t : workers_) t.join();
+    for (auto &t : workers) t.join();
   }
 
   // Copies n bytes with up to `threads` threads (the caller is one of them).
@@ -76,13 +81,17 @@ class HostCopyPool {
     job->n = n;
     job->part = part;
     job->parts = parts;
+    bool shared = false;
     if (parts > 1 && threads > 1) {
       std::lock_guard<std::mutex> lock(m_);
-      while (static_cast<int>(workers_.size()) < threads - 1) workers_.emplace_back([this] { loop(); });
-      job_ = job;
-      ++gen_;
+      if (!stop_) {
+        while (static_cast<int>(workers_.size()) < threads - 1) workers_.emplace_back([this] { loop(); });
+        job_ = job;
+        ++gen_;
+        shared = true;
+      }
     }
-    if (parts > 1 && threads > 1) cv_.notify_all();
+    if (shared) cv_.notify_all();
     run(*job);
     std::unique_lock<std::mutex> lock(m_);
     done_cv_.wait(lock, [&] { return job->done.load() == job->parts; });
@@ -179,6 +188,48 @@ int staging(size_t bytes, StagingState **out) {
 }
 
 }  // namespace
+
+int staged_shutdown() {
+  pool().shutdown();
+  int first = FTX_OK;
+  auto keep = [&first](hipError_t err, const char *what) {
+    if (err != hipSuccess && first == FTX_OK) first = hip_fail(err, what);
+    if (err != hipSuccess) (void)hipGetLastError();
+  };
+  std::lock_guard<std::mutex> lock(g_stage_mutex);
+  int prev = -1;
+  bool any = false;
+  for (int d = 0; d < kMaxDevices; ++d) {
+    StagingState &st = g_stage[d];
+    bool held = false;
+    for (int b = 0; b < kStagingBuffers; ++b) held = held || st.buf[b] || st.done[b];
+    if (!held) continue;
+    if (!any) {
+      any = true;
+      if (hipGetDevice(&prev) != hipSuccess) {
+        (void)hipGetLastError();
+        prev = -1;
+      }
+    }
+    hipError_t err = hipSetDevice(d);
+    keep(err, "hipSetDevice at shutdown");
+    if (err != hipSuccess) continue;
+    for (int b = 0; b < kStagingBuffers; ++b) {
+      if (st.done[b]) {
+        keep(hipEventSynchronize(st.done[b]), "hipEventSynchronize(staging buffer)");
+        keep(hipEventDestroy(st.done[b]), "hipEventDestroy(staging buffer)");
+        st.done[b] = nullptr;
+      }
+      if (st.buf[b]) {
+        keep(hipHostFree(st.buf[b]), "hipHostFree(staging buffer)");
+        st.buf[b] = nullptr;
+      }
+    }
+    st.bytes = 0;
+  }
+  if (prev >= 0 && hipSetDevice(prev) != hipSuccess) (void)hipGetLastError();
+  return first;
+}
 
 int set_staging_policy(size_t piece_bytes, int threads) {
   if (piece_bytes < (size_t(1) << 20) || piece_bytes > (size_t(1) << 30))

@@ -313,15 +313,16 @@ class HostArena:
 
 
 def copy_h2d(dst: torch.Tensor, src: torch.Tensor, mode: int, stream: HipStream | None = None,
-             nbytes: int | None = None) -> None:
-    """Stream-ordered copy of ``nbytes`` (default: all of ``src``) host -> device."""
+             nbytes: int | None = None, policy: nat.CopyPolicy | None = None) -> None:
+    """Stream-ordered copy of ``nbytes`` (default: all of ``src``) host -> device, under ``policy`` (None: the
+    library default)."""
     n = src.numel() * src.element_size() if nbytes is None else int(nbytes)
     if n > dst.numel() * dst.element_size():
         raise ValueError(f"copy of {n} bytes does not fit destination of {dst.numel() * dst.element_size()} bytes")
     if src.device.type != "cpu" or dst.device.type != "cuda":
         raise ValueError("copy_h2d needs a CPU source and a device destination")
     s = stream if stream is not None else current_stream(dst.device)
-    nat.copy_h2d(dst.data_ptr(), src.data_ptr(), n, mode, s.handle)
+    nat.copy_h2d(dst.data_ptr(), src.data_ptr(), n, mode, s.handle, policy)
 
 
 def checksum(t: torch.Tensor, stream: HipStream | None = None) -> int:
@@ -347,6 +348,22 @@ def fp8_linear_workspace_bytes(m: int, n: int, k: int) -> int:
     return got
 
 
+def _check_fp8_operands(what: str, x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> tuple[int, int, int]:
+    """Ranks, dtypes, shapes and devices of an fp8 linear's operands; returns (m, k, n)."""
+    if x.dim() != 2 or weight.dim() != 2 or scale.dim() != 1:
+        raise ValueError(f"{what} needs x [m, k], weight [n, k] and scale [n]")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.float8_e4m3fn or scale.dtype != torch.bfloat16:
+        raise TypeError(f"{what} needs bf16 x, float8_e4m3fn weight and bf16 scale; got "
+                        f"{x.dtype}, {weight.dtype}, {scale.dtype}")
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or scale.shape[0] != n:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, weight {tuple(weight.shape)}, scale {tuple(scale.shape)}")
+    if not (x.is_cuda and weight.device == x.device and scale.device == x.device):
+        raise ValueError(f"{what} needs x, weight and scale on one GPU")
+    return m, k, n
+
+
 def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """``bf16(scale * (x @ weight.T))`` by the library's fp8-weight MFMA kernel.
 
@@ -357,17 +374,7 @@ def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor) -> to
     prefill kernel. Runs on torch's current stream; a split-K workspace comes
     from torch's allocator on that stream.
     """
-    if x.dim() != 2 or weight.dim() != 2 or scale.dim() != 1:
-        raise ValueError("fp8_linear needs x [m, k], weight [n, k] and scale [n]")
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.float8_e4m3fn or scale.dtype != torch.bfloat16:
-        raise TypeError(f"fp8_linear needs bf16 x, float8_e4m3fn weight and bf16 scale; got "
-                        f"{x.dtype}, {weight.dtype}, {scale.dtype}")
-    m, k = x.shape
-    n = weight.shape[0]
-    if weight.shape[1] != k or scale.shape[0] != n:
-        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, weight {tuple(weight.shape)}, scale {tuple(scale.shape)}")
-    if not (x.is_cuda and weight.device == x.device and scale.device == x.device):
-        raise ValueError("fp8_linear needs x, weight and scale on one GPU")
+    m, k, n = _check_fp8_operands("fp8_linear", x, weight, scale)
     if not weight.is_contiguous() or weight.data_ptr() % 16:
         raise ValueError("fp8_linear needs a contiguous, 16-byte aligned weight")
     if not x.is_contiguous() or x.data_ptr() % 16:
@@ -432,14 +439,16 @@ def fp8_linear_static(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor
     """``fp8_linear`` into ``out`` (bf16 ``[m, n]``) with no allocation at all, for graph capture and serving
     loops: the split-K partial sums live in the library's static per-GPU scratch array
     (``ftx_fp8_linear_static``). Operands must already be contiguous and 16-byte aligned. Calls that may
-    overlap on one GPU share that scratch and must be ordered (one stream)."""
-    m, k = x.shape
-    n = weight.shape[0]
-    if out.shape != (m, n) or out.dtype != torch.bfloat16 or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous bf16 [{m}, {n}] tensor")
+    overlap on one GPU share that scratch and must be ordered (one stream). Every operand is checked as
+    ``fp8_linear`` checks it (dtypes, shapes, one device); nothing is copied to fix a layout."""
+    m, k, n = _check_fp8_operands("fp8_linear_static", x, weight, scale)
+    if out.shape != (m, n) or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != x.device:
+        raise ValueError(f"out must be a contiguous bf16 [{m}, {n}] tensor on {x.device}")
     for name, t in (("x", x), ("weight", weight)):
         if not t.is_contiguous() or t.data_ptr() % 16:
             raise ValueError(f"fp8_linear_static needs a contiguous, 16-byte aligned {name}")
+    if not scale.is_contiguous():
+        raise ValueError("fp8_linear_static needs a contiguous scale")
     nat.call("ftx_fp8_linear_static", x.data_ptr(), weight.data_ptr(), scale.data_ptr(), out.data_ptr(), m, n, k,
              torch.cuda.current_stream(x.device).cuda_stream)
     return out

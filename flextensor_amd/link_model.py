@@ -168,31 +168,29 @@ def _time_copies(dst, src_ptr: int, nbytes: int, engine: str, repeats: int, warm
 
     if nbytes > dst.numel():
         raise ValueError(f"copy of {nbytes} bytes into a {dst.numel()}-byte buffer")
+    # Each engine is timed under a policy of its own, passed with every copy: the library default and the
+    # policies of managers already streaming stay as they are.
+    mode, policy = nat.COPY_SDMA, nat.copy_policy(0, 2**63 - 1, 1, 0)
+    if engine.startswith("sdma_split"):
+        policy = nat.copy_policy(0, 1, int(engine[len("sdma_split"):]), 0)
+    elif engine.startswith("kernel"):
+        mode = nat.COPY_KERNEL
+        policy = nat.copy_policy(0, 2**63 - 1, 1, int(engine[len("kernel_g"):]) if engine.startswith("kernel_g") else 0)
+    elif engine != "sdma":
+        raise ValueError(f"unknown engine {engine!r}")
     stream = new_stream(device, name="link-probe")
-    old = nat.get_copy_policy()
-    mode = nat.COPY_SDMA
     try:
-        if engine.startswith("sdma_split"):
-            k = int(engine[len("sdma_split"):])
-            nat.set_copy_policy(old[0], 1, k, old[3])
-        elif engine.startswith("kernel"):
-            mode = nat.COPY_KERNEL
-            grid = int(engine[len("kernel_g"):]) if engine.startswith("kernel_g") else 0
-            nat.set_copy_policy(old[0], old[1], old[2], grid)
-        elif engine != "sdma":
-            raise ValueError(f"unknown engine {engine!r}")
         times = []
         for i in range(warmup + repeats):
             e0, e1 = HipEvent(timing=True), HipEvent(timing=True)
             stream.record_event(e0)
-            nat.copy_h2d(dst.data_ptr(), src_ptr, nbytes, mode, stream.handle)
+            nat.copy_h2d(dst.data_ptr(), src_ptr, nbytes, mode, stream.handle, policy)
             stream.record_event(e1)
             e1.synchronize()
             if i >= warmup:
                 times.append(e0.elapsed_time(e1))
         return times
     finally:
-        nat.set_copy_policy(*old)
         stream.synchronize()
 
 
@@ -316,6 +314,11 @@ class LinkMeasurement:
 
     def policy(self) -> tuple[int, int, int]:
         return self.kernel_max_bytes, self.split_min_bytes, self.n_copy_streams
+
+    def native_policy(self) -> "nat.CopyPolicy":
+        """This measurement's policy as the library's ``ftx_copy_policy``, for the controller that copies
+        under it (every copy carries it; the library default is left alone)."""
+        return nat.copy_policy(self.kernel_max_bytes, self.split_min_bytes, self.n_copy_streams, self.kernel_grid)
 
     def transfer_ms(self, sizes: list[int]) -> float:
         """Predicted SDMA time of copies of ``sizes`` bytes, interpolated from the measured curve."""

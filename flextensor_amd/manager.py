@@ -1538,6 +1538,12 @@ class OffloadManager:
         rebuilds its curve from the saved statistics. Only ``copy_engine="auto"``
         consults the policy; ``link_benchmark=False`` keeps the library default.
 
+        The policy belongs to this manager: its controller passes it with
+        every copy (``ftx_copy_h2d_policy``), and nothing in the library's
+        process-wide state changes, so named managers streaming side by side
+        each copy under their own measurement, as the reference's named
+        managers copy independently (offload_manager.py:2817-2850).
+
         A measured policy then looks at the pass: when the profiled compute of
         its units is under 0.4 of the curve's time for its streamed units
         (:func:`~flextensor_amd.link_model.is_link_bound`), every ring copy
@@ -1566,7 +1572,6 @@ class OffloadManager:
             link = dataclasses.replace(link, pass_compute_ms=compute_ms, pass_transfer_ms=transfer_ms)
             if is_link_bound(compute_ms, transfer_ms):
                 link = link.for_link_bound_pass(max(sizes))
-        nat.set_copy_policy(link.kernel_max_bytes, link.split_min_bytes, link.n_copy_streams, link.kernel_grid)
         self.link = link
         self.memory_transfer_stats = link.memory_transfer_stats()
         LOGGER.info("offload %r: %s", self.name, link.describe())
@@ -1688,11 +1693,13 @@ class OffloadManager:
 
     def _build_controller(self, cfg: OffloadConfig, plan: StreamPlan, bd: Any, tensors_map: dict[int, torch.Tensor],
                           pinner: HostPinner, mode: int, state: TensorManagerState | None) -> None:
-        """The block controller of the plan: packed host blocks and GPU ring slots."""
+        """The block controller of the plan: packed host blocks and GPU ring slots, copying under this
+        manager's copy policy (the library default when no link was measured or restored)."""
+        policy = self.link.native_policy() if self.link is not None else None
         if cfg.transfer_mode == "raw_block_transfer":
             self.controller = RawBlockController(bd.label_to_size_map, bd.block_sizes, self.device, tensors_map,
                                                  plan.strategy_map, bd.label_to_block_id, host_pinner=pinner,
-                                                 copy_mode=mode)
+                                                 copy_mode=mode, copy_policy=policy)
         else:
             shm_names: dict[str, str] | None = None
             if cfg.shm_enabled:
@@ -1705,7 +1712,7 @@ class OffloadManager:
                     shm_names = {x: f"{cfg.shm_namespace}_b{i}" for i, x in enumerate(labels)}
             self.controller = AllocationBlockController(bd.allocation_ordered, self.device, tensors_map,
                                                         plan.strategy_map, bd.label_to_block_id,
-                                                        host_pinner=pinner, copy_mode=mode,
+                                                        host_pinner=pinner, copy_mode=mode, copy_policy=policy,
                                                         shm_block_name_map=shm_names,
                                                         load_from_shm=self._load_from_shm)
 

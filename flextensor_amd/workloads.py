@@ -160,10 +160,13 @@ class Fp8Linear(nn.Module):
 
 def fp8_group(x: torch.Tensor, layers: list[nn.Module]) -> list[torch.Tensor] | None:
     """The outputs of several ``Fp8Linear`` layers on one input in one grouped kernel launch, or None when
-    any of them would not take the kernel (the caller then runs them one by one)."""
+    any of them would not take the kernel, or the group's outputs together would reach 2^31 elements, the
+    library's limit for one launch (the caller then runs them one by one)."""
     if not all(isinstance(lin, Fp8Linear) and lin.kernel_eligible(x) for lin in layers):
         return None
     k = x.shape[-1]
+    if (x.numel() // k) * sum(lin.weight.shape[0] for lin in layers) >= 2**31:
+        return None
     ys = hip.fp8_linear_group(x.reshape(x.numel() // k, k), [lin.weight for lin in layers],
                               [lin.scale for lin in layers])
     return [y.view(*x.shape[:-1], y.shape[-1]) for y in ys]

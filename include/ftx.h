@@ -70,6 +70,16 @@ typedef struct ftx_scatter_plan ftx_scatter_plan;
 /* ---- library / device -------------------------------------------------- */
 const char *ftx_last_error(void);
 int ftx_version(void);                 /* returns the ABI version number (not a status) */
+/* Releases what the library holds for the process, while the HIP runtime is
+ * still up: waits for every device, joins the staged engine's host threads,
+ * frees its page-locked staging buffers and events, and destroys the copy
+ * streams and events of split SDMA copies. Idempotent. Afterwards every call
+ * that would start work or allocate returns FTX_ERR_UNSUPPORTED; calls that
+ * release, wait on or query existing handles still work. Meant for process
+ * exit, ahead of the runtime's own teardown. Replaces
+ * CudaTransferRuntime.close (core/transfer.py:133-142): synchronize, then
+ * refuse further work. */
+int ftx_shutdown(void);
 int ftx_device_count(int *count);
 int ftx_set_device(int device);
 int ftx_get_device(int *device);
@@ -83,9 +93,15 @@ int ftx_device_info(int *cu_count, int *xcd_count, size_t *total_mem);
  * per packed block. */
 int ftx_arena_alloc(size_t nbytes, unsigned flags, void **host);
 int ftx_arena_free(void *host);
-/* Replace HostPinRegistry.pin_in_place (host_pinning.py:206-265, the
+/* Stand in for HostPinRegistry.pin_in_place (host_pinning.py:206-265, the
  * cudaHostRegister(ptr, n, Portable) call at :257) and SHM pinning
- * (shm/flexible_shm.py:832-848): page-lock existing memory in place. */
+ * (shm/flexible_shm.py:832-848): page-locking existing memory in place.
+ * Refused in this build: the MI355X hosts it targets reject hipHostRegister,
+ * and the failed call's error can surface in the next GPU call. So
+ * ftx_arena_register returns FTX_ERR_UNSUPPORTED for every input without
+ * calling the runtime, and ftx_arena_unregister (nothing is ever registered)
+ * returns FTX_ERR_INVALID. Allocate blocks with ftx_arena_alloc instead;
+ * pageable or shared-memory sources stream through FTX_COPY_STAGED. */
 int ftx_arena_register(void *host, size_t nbytes, unsigned flags);
 int ftx_arena_unregister(void *host);
 /* Device-visible address of pinned host memory (zero-copy kernel source). */
@@ -130,13 +146,30 @@ int ftx_event_elapsed_ms(void *start, void *end, float *ms);
  * Stream-ordered on `stream`: work split over internal copy streams is forked
  * from and joined back into `stream`. `src` must be pinned host memory. */
 int ftx_copy_h2d(void *dst, const void *src, size_t nbytes, int mode, void *stream);
-/* Policy used by FTX_COPY_AUTO and by FTX_COPY_SDMA splitting:
+/* A copy policy: how FTX_COPY_AUTO picks the engine per chunk and how the
+ * engines run.
  *   kernel_max_bytes  chunks <= this go to the zero-copy kernel under AUTO;
  *   split_min_bytes   SDMA copies >= this are split over n_copy_streams;
  *   n_copy_streams    1..8 dedicated copy streams;
- *   kernel_grid       zero-copy kernel workgroups (0 = 64, enough to hold the link at its peak).
- *                     A grid of at most 16 reserves each CU it runs on: its workgroups take
- *                     the CU's whole LDS, so kernels that use LDS run on the other CUs. */
+ *   kernel_grid       zero-copy kernel workgroups, 0..2^20 (0 = 64, enough to hold the link at
+ *                     its peak). A grid of at most 16 reserves each CU it runs on: its
+ *                     workgroups take the CU's whole LDS, so kernels that use LDS run on the
+ *                     other CUs. */
+typedef struct ftx_copy_policy {
+  uint64_t kernel_max_bytes;
+  uint64_t split_min_bytes;
+  int32_t n_copy_streams;
+  int32_t kernel_grid;
+} ftx_copy_policy;
+/* ftx_copy_h2d under a policy the caller owns. Each named offload manager
+ * copies independently in the reference (offload_manager.py:2817-2850; each
+ * controller's AllocationBlock.copy_to, allocation_block.py:104-106), so each
+ * carries its own measured policy into every copy instead of changing the
+ * process's. policy NULL is the library default below. */
+int ftx_copy_h2d_policy(void *dst, const void *src, size_t nbytes, int mode, const ftx_copy_policy *policy,
+                        void *stream);
+/* The library default, used by ftx_copy_h2d (process-wide; 1 MiB kernel cut,
+ * no SDMA split, grid 0 until set). */
 int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_copy_streams,
                         int kernel_grid);
 int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams,

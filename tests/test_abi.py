@@ -5,6 +5,8 @@ from __future__ import annotations
 import re
 from pathlib import Path
 
+import pytest
+
 ROOT = Path(__file__).resolve().parents[1]
 
 
@@ -69,3 +71,107 @@ def test_missing_library_fails_loudly():
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
                          cwd=str(Path(__file__).resolve().parents[1]))
     assert out.returncode == 0 and out.stdout.strip().endswith("refused"), out.stdout + out.stderr
+
+
+def test_arena_register_is_refused_in_c_without_the_runtime():
+    """In-place page-locking is refused by the C entry point itself, for any input, before any runtime call
+    (host_pinning.py:206-265 is the reference's pin_in_place it stands in for): a C caller that binds
+    ``pin_in_place`` to it gets FTX_ERR_UNSUPPORTED on a box with no GPU at all."""
+    import ctypes
+
+    from flextensor_amd import _native
+
+    lib = _native.load()
+    buf = ctypes.create_string_buffer(1 << 16)
+    for ptr, n in ((ctypes.addressof(buf), 1 << 16), (None, 0), (ctypes.addressof(buf), 1)):
+        assert lib.ftx_arena_register(ptr, n, 0) == _native.FTX_ERR_UNSUPPORTED
+        assert b"refused in this build" in lib.ftx_last_error()
+    assert lib.ftx_arena_unregister(ctypes.addressof(buf)) == _native.FTX_ERR_INVALID
+    with pytest.raises(_native.FtxError, match="refused in this build") as info:
+        _native.arena_register(ctypes.addressof(buf), 1 << 16)
+    assert info.value.code == _native.FTX_ERR_UNSUPPORTED
+
+
+def test_a_per_call_copy_policy_is_checked_before_any_device_call():
+    """``ftx_copy_h2d_policy`` validates the caller's policy first: out-of-range values are refused with no
+    device present, and the library default is not changed by a per-call policy."""
+    import ctypes
+
+    from flextensor_amd import _native
+
+    lib = _native.load()
+    before = _native.get_copy_policy()
+    for bad in (_native.copy_policy(0, 0, 0, 0), _native.copy_policy(0, 0, 9, 0), _native.copy_policy(0, 0, 1, -1),
+                _native.copy_policy(0, 0, 1, (1 << 20) + 1)):
+        assert lib.ftx_copy_h2d_policy(None, None, 0, _native.COPY_SDMA, ctypes.byref(bad), None) == \
+            _native.FTX_ERR_INVALID
+    with pytest.raises(_native.FtxError, match="n_copy_streams"):
+        _native.copy_h2d(0, 0, 0, _native.COPY_AUTO, 0, _native.copy_policy(0, 0, 0, 0))
+    # a valid policy and nothing to copy: done without touching a device
+    _native.copy_h2d(0, 0, 0, _native.COPY_AUTO, 0, _native.copy_policy(1 << 30, 1, 8, 8))
+    assert _native.get_copy_policy() == before
+    p = _native.copy_policy(5, 2**64, 2, 3)  # above the 64-bit range reads as "never split"
+    assert p.astuple() == (5, 2**64 - 1, 2, 3) and p == _native.copy_policy(5, 2**64 - 1, 2, 3)
+
+
+def _run_python(code: str) -> "subprocess.CompletedProcess":
+    import subprocess
+    import sys
+
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                          cwd=str(ROOT))
+
+
+def test_shutdown_is_idempotent_and_refuses_later_work():
+    """``ftx_shutdown`` (core/transfer.py:133-142: synchronize, then refuse further work) releases the
+    library's own resources once; a second call is a no-op; afterwards calls that would start work or
+    allocate fail with FTX_ERR_UNSUPPORTED and a message, and calls that release handles still succeed.
+    Run in a child process: a shut-down library stays shut down for the rest of its process."""
+    code = (
+        "import ctypes\n"
+        "import flextensor_amd._native as nat\n"
+        "lib = nat.load()\n"
+        "src, dst = ctypes.create_string_buffer(8 << 20), ctypes.create_string_buffer(8 << 20)\n"
+        "nat.host_memcpy(ctypes.addressof(dst), ctypes.addressof(src), 8 << 20)  # starts the host thread pool\n"
+        "assert lib.ftx_shutdown() == 0 and lib.ftx_shutdown() == 0\n"
+        "nat.shutdown()\n"
+        "refused = {\n"
+        "  'host_memcpy': lib.ftx_host_memcpy(ctypes.addressof(dst), ctypes.addressof(src), 64),\n"
+        "  'copy_h2d': lib.ftx_copy_h2d(None, None, 0, 0, None),\n"
+        "  'arena_alloc': lib.ftx_arena_alloc(4096, 0, ctypes.byref(ctypes.c_void_p())),\n"
+        "  'event_create': lib.ftx_event_create(0, ctypes.byref(ctypes.c_void_p())),\n"
+        "  'scatter': lib.ftx_scatter(None, None, 0, None),\n"
+        "  'fp8_linear': lib.ftx_fp8_linear(None, None, None, None, 0, 0, 0, None, 0, None),\n"
+        "}\n"
+        "assert all(rc == nat.FTX_ERR_UNSUPPORTED for rc in refused.values()), refused\n"
+        "assert b'shut down' in lib.ftx_last_error()\n"
+        "released = [lib.ftx_event_destroy(None), lib.ftx_stream_destroy(None), lib.ftx_arena_free(None),\n"
+        "            lib.ftx_device_free(None), lib.ftx_scatter_plan_destroy(None)]\n"
+        "assert released == [0] * 5, released\n"
+        "print('shut down')\n"
+    )
+    out = _run_python(code)
+    assert out.returncode == 0 and out.stdout.strip() == "shut down", out.stdout + out.stderr
+
+
+def test_exit_releases_the_library_quietly():
+    """At interpreter exit the binding calls ``ftx_shutdown`` ahead of torch's exit handlers: a process whose
+    host thread pool is running exits with status 0 and nothing on stderr. Exit handlers run last-registered
+    first, so a probe registered before the binding is imported runs after its shutdown (and is refused),
+    and one registered after it runs before (and still works)."""
+    code = (
+        "import atexit, ctypes\n"
+        "held = {}\n"
+        "def probe(when):\n"
+        "    rc = held['lib'].ftx_host_memcpy(ctypes.addressof(held['dst']), ctypes.addressof(held['src']), 64)\n"
+        "    print(when, 'refused' if rc == 4 else 'live', flush=True)\n"
+        "atexit.register(probe, 'after')\n"
+        "import flextensor_amd._native as nat\n"
+        "held['lib'] = nat.load()\n"
+        "held['src'], held['dst'] = ctypes.create_string_buffer(32 << 20), ctypes.create_string_buffer(32 << 20)\n"
+        "nat.host_memcpy(ctypes.addressof(held['dst']), ctypes.addressof(held['src']), 32 << 20)\n"
+        "atexit.register(probe, 'before')\n"
+    )
+    out = _run_python(code)
+    assert out.returncode == 0 and out.stderr == "", out.stderr
+    assert out.stdout.split() == ["before", "live", "after", "refused"], out.stdout

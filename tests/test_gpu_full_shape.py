@@ -270,14 +270,24 @@ def test_llama70b_fp8_full_shape_streamed_equals_resident(gpu):
     model.to("cpu")
     _free()
     mgr = OffloadManager("full-70b")
-    # module order is the execution order of this decoder: plan at offload() time, as the benchmark does
+    # module order is the execution order of this decoder (no discovery pass); one profiled decode-shaped pass
+    # then lets the measured pass rule choose the ring's copy engine, as the benchmark does
     mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=0,
-                                     profiling_iters=0, max_gpu_mem_bytes=24_000_000_000))
+                                     profiling_iters=1, max_gpu_mem_bytes=24_000_000_000))
     rec = _UnitRecorder({f"layers.{i}": layer for i, layer in enumerate(model.layers)}, ("attn", "down"))
     try:
+        _say("llama70b fp8: profiling pass (one batch-8 decode-shaped token)")
+        model.init_cache(batch, 4, gpu)
+        with torch.no_grad():
+            model(prompt[:, :1], 0)
         plan = mgr.plan
         assert plan.streamed and plan.resident and mgr.get_gpu_memory_usage().total_bytes <= 24_000_000_000
-        _say(f"llama70b fp8: {len(plan.streamed)} streamed / {len(plan.resident)} resident layers")
+        link = mgr.link
+        assert link is not None and link.source == "measured" and link.pass_compute_ms is not None
+        _say(f"llama70b fp8: {len(plan.streamed)} streamed / {len(plan.resident)} resident layers; "
+             f"{link.describe()}")
+        # the decode computes for far less than its streamed layers take on the link: kernel ring copies
+        assert link.link_bound and mgr.controller.copy_policy.kernel_grid == link.kernel_grid > 0
         with torch.no_grad():
             got, got_toks = _prefill_and_decode(model, prompt, steps, toks, rec=rec)
         rec.remove()

@@ -1,11 +1,16 @@
-"""The copy engine a measured pass chooses, on the GPU.
+"""The copy engine a measured pass chooses, per manager, on the GPU.
 
 A pass whose profiled compute is far below its transfer time (an 8-layer
 4096 -> 11008 -> 4096 MLP stack at 16 rows) is link-bound: its ring copies
 go to the zero-copy kernel at the ring grid. The same stack at 32768 rows
 computes for about three times its transfer time and keeps the measured
-per-size policy (SDMA for the 180 MB layers). Both stream outputs bitwise
-equal to the resident forward, so the kernel copies move the same bytes.
+per-size policy (SDMA for the 180 MB layers).
+
+Both managers live in one process and stream in alternation, as the
+reference's named managers do (offload_manager.py:2817-2850): each
+controller carries its own policy into every copy, the library's
+process-wide default is never changed, and both stream outputs bitwise equal
+to the resident forward.
 """
 
 from __future__ import annotations
@@ -22,45 +27,48 @@ from flextensor_amd.manager import OffloadManager
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
-def keep_policy():
+def test_link_bound_and_compute_bound_managers_stream_side_by_side(gpu):
     nat.load()
-    before = nat.get_copy_policy()
-    yield
-    nat.set_copy_policy(*before)
-
-
-def _streamed_vs_resident(rows: int, name: str):
-    dev = torch.device("cuda", 0)
-    model = W.build_mlp_stack(8, 4096, 11008, seed=0)
-    x = W.mlp_input(rows, 4096, seed=0).to(dev)
-    with torch.no_grad():
-        want = W.build_mlp_stack(8, 4096, 11008, seed=0).to(dev)(x)
-    mgr = OffloadManager(name)
-    mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2,
-                                     discovery_iters=1, profiling_iters=1))
-    try:
+    default = nat.get_copy_policy()
+    dev = gpu
+    rows = {"link-bound-gpu": 16, "compute-bound-gpu": 32768}
+    models, inputs, want, managers = {}, {}, {}, {}
+    for name, m in rows.items():
+        models[name] = W.build_mlp_stack(8, 4096, 11008, seed=0)
+        inputs[name] = W.mlp_input(m, 4096, seed=0).to(dev)
         with torch.no_grad():
-            for _ in range(4):  # discovery, profiling, then two streamed passes
-                got = model(x)
+            want[name] = W.build_mlp_stack(8, 4096, 11008, seed=0).to(dev)(inputs[name])
+    torch.cuda.empty_cache()
+    try:
+        for name in rows:
+            managers[name] = OffloadManager(name)
+            managers[name].offload(models[name], OffloadConfig(include_patterns=["layers.*"], num_blocks=2,
+                                                               min_blocks=2, discovery_iters=1, profiling_iters=1))
+        got = {}
+        with torch.no_grad():
+            for _ in range(4):  # discovery, profiling, then two streamed passes, alternating managers
+                for name in rows:
+                    got[name] = models[name](inputs[name])
         torch.cuda.synchronize()
-        unit_bytes = max(mgr._unit(u).nbytes for u in mgr.plan.streamed)
-        return mgr.link, nat.get_copy_policy(), unit_bytes, bool(torch.equal(got, want))
+        link_bound, compute_bound = managers["link-bound-gpu"], managers["compute-bound-gpu"]
+        unit_bytes = max(link_bound._unit(u).nbytes for u in link_bound.plan.streamed)
+        assert link_bound.link is not None and link_bound.link.source == "measured"
+        assert link_bound.link.link_bound and link_bound.link.kernel_grid == L.RING_KERNEL_GRID
+        pol = link_bound.controller.copy_policy
+        assert pol.kernel_max_bytes >= unit_bytes and pol.kernel_grid == L.RING_KERNEL_GRID
+        assert compute_bound.link is not None and not compute_bound.link.link_bound
+        pol = compute_bound.controller.copy_policy
+        assert pol.kernel_max_bytes < unit_bytes and pol.kernel_grid == 0
+        assert nat.get_copy_policy() == default  # neither manager touched the process-wide default
+        for name in rows:
+            assert torch.equal(got[name], want[name]), name
+        # one manager goes; the other keeps streaming bitwise under its own policy
+        managers.pop("link-bound-gpu").release(preserve_model=False)
+        with torch.no_grad():
+            again = models["compute-bound-gpu"](inputs["compute-bound-gpu"])
+        assert torch.equal(again, want["compute-bound-gpu"])
+        assert nat.get_copy_policy() == default
     finally:
-        mgr.release(preserve_model=False)
+        for mgr in managers.values():
+            mgr.release(preserve_model=False)
         torch.cuda.empty_cache()
-
-
-def test_a_link_bound_pass_copies_its_slots_with_the_kernel(keep_policy):
-    link, policy, unit_bytes, same = _streamed_vs_resident(16, "link-bound-gpu")
-    assert link is not None and link.source == "measured"
-    assert link.link_bound and link.kernel_grid == L.RING_KERNEL_GRID
-    assert policy[0] >= unit_bytes and policy[3] == L.RING_KERNEL_GRID
-    assert same
-
-
-def test_a_compute_bound_pass_keeps_sdma_for_its_slots(keep_policy):
-    link, policy, unit_bytes, same = _streamed_vs_resident(32768, "compute-bound-gpu")
-    assert link is not None and not link.link_bound and link.kernel_grid == 0
-    assert policy[0] < unit_bytes and policy[3] == 0
-    assert same

@@ -56,13 +56,11 @@ def test_kernel_copy_bit_exact_at_each_grid(gpu, grid, nbytes):
     data = _rand_bytes(nbytes, seed=grid + nbytes)
     arena = _arena_with(data, pad=3)
     dst = torch.full((nbytes + 64,), 0xA5, dtype=torch.uint8, device=gpu)
-    old = nat.get_copy_policy()
-    try:
-        nat.set_copy_policy(old[0], old[1], old[2], grid)
-        nat.copy_h2d(dst.data_ptr() + 3, arena.ptr + 3, nbytes, nat.COPY_KERNEL, current_stream(gpu).handle)
-        torch.cuda.synchronize()
-    finally:
-        nat.set_copy_policy(*old)
+    default = nat.get_copy_policy()
+    policy = nat.copy_policy(0, 2**63 - 1, 1, grid)  # the grid travels with the call (ftx_copy_h2d_policy)
+    nat.copy_h2d(dst.data_ptr() + 3, arena.ptr + 3, nbytes, nat.COPY_KERNEL, current_stream(gpu).handle, policy)
+    torch.cuda.synchronize()
+    assert nat.get_copy_policy() == default
     out = dst.cpu().numpy()
     assert np.array_equal(out[3 : 3 + nbytes], data)
     assert (out[:3] == 0xA5).all() and (out[3 + nbytes :] == 0xA5).all()
@@ -85,20 +83,26 @@ def test_kernel_copy_rejects_non_congruent_alignment(gpu):
     assert np.array_equal(dst.cpu().numpy()[1:4097], data)
 
 
-def test_split_sdma_over_copy_streams(gpu):
+@pytest.mark.parametrize("per_call", [True, False])
+def test_split_sdma_over_copy_streams(gpu, per_call):
+    """SDMA split over four copy streams, under a per-call policy and under the library default."""
     from flextensor_amd import _native as nat
     from flextensor_amd.hip import current_stream
 
     old = nat.get_copy_policy()
+    policy = nat.copy_policy(1 << 20, 1 << 20, 4, 0)
     try:
-        nat.set_copy_policy(1 << 20, 1 << 20, 4, 0)
+        if not per_call:
+            nat.set_copy_policy(*policy.astuple())
         n = (48 << 20) + 333
         data = _rand_bytes(n, seed=11)
         arena = _arena_with(data)
-        dst = torch.zeros(n, dtype=torch.uint8, device=gpu)
-        nat.copy_h2d(dst.data_ptr(), arena.ptr, n, nat.COPY_SDMA, current_stream(gpu).handle)
-        torch.cuda.synchronize()
-        assert np.array_equal(dst.cpu().numpy(), data)
+        for mode in (nat.COPY_SDMA, nat.COPY_AUTO):
+            dst = torch.zeros(n, dtype=torch.uint8, device=gpu)
+            nat.copy_h2d(dst.data_ptr(), arena.ptr, n, mode, current_stream(gpu).handle,
+                         policy if per_call else None)
+            torch.cuda.synchronize()
+            assert np.array_equal(dst.cpu().numpy(), data)
     finally:
         nat.set_copy_policy(*old)
 

@@ -406,6 +406,14 @@ def test_host_register_mode_is_refused_before_anything_moves(names):
 # ---- the copy policy follows the measured host link (memory_transfer_benchmark.py:59-129) ----------------
 
 
+def _untouched_default():
+    """The library's process-wide copy policy must never change: a manager's policy travels with its copies."""
+    def refuse(*a):
+        raise AssertionError("a manager changed the library's process-wide copy policy")
+
+    return mock.patch.object(M.nat, "set_copy_policy", refuse)
+
+
 def _fake_link(kernel_faster_up_to: int):
     """Curves where the zero-copy kernel beats SDMA by 30% up to ``kernel_faster_up_to`` bytes, then trails."""
     from flextensor_amd import link_model as L
@@ -427,13 +435,10 @@ def test_copy_policy_follows_the_measured_curve(host_offload, cut):
     plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
     link = _fake_link(cut)
     assert link.kernel_max_bytes == cut  # the curve alone decides where the kernel stops paying
-    applied = []
-    with mock.patch.object(M, "measure_link", lambda sizes, dev: link) as _, \
-            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)), \
-            mock.patch.object(M.nat, "get_copy_policy", lambda: (1 << 20, 2**63 - 1, 1, 64)):
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link) as _, _untouched_default():
         mgr._choose_copy_policy(plan, None)
     # no profiled durations: the measured policy as it is, at the library's default kernel grid
-    assert applied == [(cut, link.split_min_bytes, 1, 0)]
+    assert mgr.link.native_policy().astuple() == (cut, link.split_min_bytes, 1, 0)
     assert mgr.get_memory_transfer_stats() == link.sdma.best_ms
     mgr.plan = plan
     table = mgr.plan_table()
@@ -467,11 +472,10 @@ def test_a_link_bound_pass_copies_every_slot_with_the_kernel(host_offload):
     plan = _profiled(mgr, 1e-6)  # the units compute for far less than their copies take
     sizes = [mgr._unit(x).nbytes for x in plan.streamed]
     assert L.is_link_bound(1e-6 * len(mgr.order), link.transfer_ms(sizes))
-    applied = []
-    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), \
-            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)):
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), _untouched_default():
         mgr._choose_copy_policy(plan, None)
-    assert applied == [(max(1 << 20, max(sizes)), link.split_min_bytes, 1, L.RING_KERNEL_GRID)]
+    assert mgr.link.native_policy().astuple() == (max(1 << 20, max(sizes)), link.split_min_bytes, 1,
+                                                  L.RING_KERNEL_GRID)
     assert mgr.link.link_bound and mgr.link.kernel_grid == L.RING_KERNEL_GRID
     assert mgr.link.sdma is link.sdma  # the measured curve stays the transfer model
     assert "link-bound pass" in mgr.link.describe()
@@ -486,11 +490,9 @@ def test_a_compute_bound_pass_keeps_the_measured_policy(host_offload):
     mgr = host_offload("compute-bound", include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1)
     link = _fake_link(1 << 20)
     plan = _profiled(mgr, 1e6)
-    applied = []
-    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), \
-            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)):
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), _untouched_default():
         mgr._choose_copy_policy(plan, None)
-    assert applied == [(1 << 20, link.split_min_bytes, 1, 0)] and not mgr.link.link_bound
+    assert mgr.link.native_policy().astuple() == (1 << 20, link.split_min_bytes, 1, 0) and not mgr.link.link_bound
     assert mgr.link.pass_compute_ms == pytest.approx(1e6 * len(mgr.order))  # recorded either way
     assert "pass compute" in mgr.link.describe()
 
@@ -524,16 +526,13 @@ def test_saved_policy_is_reapplied_without_measuring(host_offload):
     mgr.order = [u.label for u in mgr.units]
     plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
     saved = M.state_from_plan(mgr.model, mgr.units, plan, {}, "allocation_block_transfer", _fake_link(1 << 20))
-    applied = []
 
     def no_measuring(*a):
         raise AssertionError("a restored plan must not measure the link")
 
-    with mock.patch.object(M, "measure_link", no_measuring), \
-            mock.patch.object(M.nat, "set_copy_policy", lambda *a: applied.append(a)), \
-            mock.patch.object(M.nat, "get_copy_policy", lambda: (0, 2**63 - 1, 1, 0)):
+    with mock.patch.object(M, "measure_link", no_measuring), _untouched_default():
         mgr._choose_copy_policy(plan, saved)
-    assert applied and applied[0][0] == 1 << 20 and mgr.link.source == "profile"
+    assert mgr.link.native_policy().kernel_max_bytes == 1 << 20 and mgr.link.source == "profile"
 
 
 def test_link_benchmark_off_or_explicit_engine_keeps_the_default(host_offload):
@@ -542,7 +541,7 @@ def test_link_benchmark_off_or_explicit_engine_keeps_the_default(host_offload):
         mgr.order = [u.label for u in mgr.units]
         plan = M.plan_streaming(mgr.units, mgr.order, None, 0, 2, 2)
         with mock.patch.object(M, "measure_link", lambda *a: (_ for _ in ()).throw(AssertionError("measured"))), \
-                mock.patch.object(M.nat, "set_copy_policy", lambda *a: (_ for _ in ()).throw(AssertionError("set"))):
+                _untouched_default():
             mgr._choose_copy_policy(plan, None)
         assert mgr.link is None and mgr.get_memory_transfer_stats() is None
 
@@ -567,13 +566,88 @@ def test_a_failed_link_measurement_keeps_the_default_policy(host_offload, caplog
     def fails(*a):
         raise nat.FtxOutOfMemoryError(nat.FTX_ERR_OOM, "hipHostMalloc failed")
 
-    with mock.patch.object(M, "measure_link", fails), \
-            mock.patch.object(M.nat, "set_copy_policy", lambda *a: (_ for _ in ()).throw(AssertionError("set"))), \
+    with mock.patch.object(M, "measure_link", fails), _untouched_default(), \
             mock.patch.object(M.torch.cuda, "empty_cache", lambda: None), \
             caplog.at_level(logging.WARNING, logger="flextensor_amd.manager"):
         mgr._choose_copy_policy(plan, None)
     assert mgr.link is None and mgr.get_memory_transfer_stats() is None
     assert "measuring the host link failed" in caplog.text
+
+
+def test_named_managers_each_copy_under_their_own_policy(host_offload):
+    """Named managers copy independently (offload_manager.py:2817-2850, allocation_block.py:104-106).
+
+    A link-bound manager, a compute-bound one and one with no link measurement
+    stream their passes in alternation in one process. Every copy of each
+    manager's controller carries that manager's engine and policy, the library's
+    process-wide policy is never written, and releasing one manager leaves the
+    others' copies as they were.
+    """
+    import functools
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import allocation_block as AB
+    from flextensor_amd import link_model as L
+    from tests.fakes import FakeBackend, Recorder
+
+    link = _fake_link(1 << 20)
+    cases = {  # name: (config, profiled ms per unit)
+        "pair-link": ({}, 1e-6),
+        "pair-compute": ({}, 1e6),
+        "pair-default": ({"link_benchmark": False, "copy_engine": "sdma"}, 1.0),
+    }
+    rec = Recorder()
+    loaders = {cls: functools.partial(getattr(M, cls), backend=FakeBackend(rec))
+               for cls in ("PreallocatedBatchTransferTensorLoader", "PreallocatedBatchTransferTensorLoaderReordered")}
+    managers = {}
+    with mock.patch.object(M, "measure_link", lambda sizes, dev: link), _untouched_default(), \
+            mock.patch.object(M.torch.cuda, "synchronize", lambda *a: None), \
+            mock.patch.multiple(M, **loaders):
+        for name, (cfg, ms) in cases.items():
+            mgr = host_offload(name, include_patterns=["layers.*"], discovery_iters=1, profiling_iters=1,
+                               pinned_memory=False, **cfg)
+            mgr.device = torch.device("cpu")  # the ring slots live on the CPU, as in the controller tests
+            _profiled(mgr, ms)
+            mgr._to_inference()
+            assert mgr.phase == M.OffloadPhase.INFERENCE and mgr.plan.streamed
+            managers[name] = mgr
+    want = {
+        "pair-link": (nat.COPY_AUTO, managers["pair-link"].link.native_policy().astuple()),
+        "pair-compute": (nat.COPY_AUTO, (1 << 20, link.split_min_bytes, 1, 0)),
+        "pair-default": (nat.COPY_SDMA, None),
+    }
+    assert managers["pair-link"].link.link_bound and want["pair-link"][1][3] == L.RING_KERNEL_GRID
+    assert not managers["pair-compute"].link.link_bound and managers["pair-default"].link is None
+    owner = {id(b): name for name, mgr in managers.items() for b in mgr.controller.block_map_cpu.values()}
+
+    copies: list[tuple[str, int, tuple | None]] = []
+    real_copy_to = AB.AllocationBlock.copy_to
+
+    def recording_copy_to(self, gpu_view, non_blocking=True, stream=None, mode=nat.COPY_AUTO, policy=None):
+        copies.append((owner[id(self)], mode, None if policy is None else policy.astuple()))
+        real_copy_to(self, gpu_view, non_blocking, stream, mode, policy)
+
+    with mock.patch.object(AB.AllocationBlock, "copy_to", recording_copy_to), _untouched_default():
+        for _ in range(2):  # alternate whole passes of the three managers
+            for mgr in managers.values():
+                for label in mgr.order:
+                    mgr.loader.enter(label)
+                    mgr.loader.exit(label)
+        assert {name for name, *_ in copies} == set(managers)
+        assert all((mode, pol) == want[name] for name, mode, pol in copies), copies
+        # the order of managers in the log alternates: no manager's copies ran under another's policy
+        runs = [copies[0][0]] + [b[0] for a, b in zip(copies, copies[1:]) if a[0] != b[0]]
+        assert len(runs) >= 2 * len(managers) - 1
+        # one manager goes; the others keep copying under their own policies
+        for mgr in (managers["pair-link"],):
+            mgr.loader.shutdown()
+            mgr.controller.shutdown()
+        copies.clear()
+        for name in ("pair-compute", "pair-default"):
+            for label in managers[name].order:
+                managers[name].loader.enter(label)
+                managers[name].loader.exit(label)
+        assert copies and all((mode, pol) == want[name] for name, mode, pol in copies)
 
 
 # ---- release() when teardown fails (tests/unit/test_tensor_manager_pinned_memory_mode.py:306-420) ----

@@ -202,3 +202,20 @@ def test_fp8_kernel_needs_an_aligned_weight():
     assert lin.kernel_eligible(x)
     assert lin.kernel_eligible(_FakeGpuInput(512, 64))  # prefill rows take the tiled kernel
     assert not lin.kernel_eligible(_FakeGpuInput(8, 24)) and not lin.kernel_eligible(_FakeGpuInput(0, 64))
+
+
+def test_fp8_group_falls_back_when_the_group_reaches_the_launch_limit(monkeypatch):
+    """One grouped launch takes at most 2^31 output elements in all (the library refuses m * sum(n) above it):
+    a long prefill through gate/up, each layer eligible alone, runs them one by one instead of raising."""
+    class _Input(_FakeGpuInput):
+        def reshape(self, *shape):
+            return self
+
+    calls = []
+    monkeypatch.setattr(W.hip, "fp8_linear_group", lambda x, ws, ss: calls.append(len(ws)) or
+                        [torch.empty(x.shape[0], w.shape[0], device="meta") for w in ws])
+    gate, up = W.Fp8Linear(16, 28672), W.Fp8Linear(16, 28672)
+    long_prefill = _Input(65536, 16)  # 65536 * 57344 >= 2^31, each layer alone is 65536 * 28672 < 2^31
+    assert gate.kernel_eligible(long_prefill) and up.kernel_eligible(long_prefill)
+    assert W.fp8_group(long_prefill, [gate, up]) is None and calls == []
+    assert W.fp8_group(_Input(32768, 16), [gate, up]) is not None and calls == [2]  # 32768 * 57344 < 2^31

@@ -64,3 +64,30 @@ def test_static_scratch_refuses_calls_beyond_its_size(gpu):
     with pytest.raises(nat.FtxError, match="static scratch") as info:
         nat.call("ftx_fp8_linear_static", None, None, None, None, m, n, k, torch.cuda.current_stream(gpu).cuda_stream)
     assert info.value.code == nat.FTX_ERR_UNSUPPORTED
+
+
+def test_python_wrapper_refuses_bad_operands_and_matches_the_entry_point(gpu):
+    """``hip.fp8_linear_static`` checks its operands as ``fp8_linear`` does (dtypes, shapes, one device,
+    contiguity) before the call, and otherwise returns what ``fp8_linear`` computes, bit for bit."""
+    from flextensor_amd import hip
+
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    m, n, k = 8, 1024, 4096
+    x, w, sc = _operands(gen, m, n, k, gpu)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    assert torch.equal(hip.fp8_linear_static(x, w, sc, out), hip.fp8_linear(x, w, sc))
+    bad = {
+        "float32 scale": (x, w, sc.float(), out),
+        "bf16 weight": (x, w.to(torch.bfloat16), sc, out),
+        "weight K mismatch": (x, w[:, : k // 2].contiguous(), sc, out),
+        "scale length": (x, w, sc[: n // 2], out),
+        "scale on the host": (x, w, sc.cpu(), out),
+        "strided scale": (x, w, torch.stack([sc, sc], 1)[:, 0], out),
+        "wrong out shape": (x, w, sc, out[:, : n // 2]),
+        "float32 out": (x, w, sc, out.float()),
+    }
+    for case, args in bad.items():
+        with pytest.raises((ValueError, TypeError)):
+            hip.fp8_linear_static(*args)
+        print(f"fp8_linear_static refused: {case}", flush=True)
+    torch.cuda.synchronize()
