@@ -1153,17 +1153,26 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
 
     ``copies`` host-to-device copies of B bytes from one pinned arena (two
     halves) into two device slots (a 2-slot ring), on the device's transfer
-    stream, the whole chain enqueued at once, in four arrangements:
+    stream, the whole chain enqueued at once, in these arrangements:
 
     * ``back_to_back``: the copies alone, one after another on the transfer stream;
     * ``slot_waits``: before each copy the transfer stream waits on an event the
       compute stream recorded as that slot's release. The compute stream has
       nothing queued, so every wait is already met when the copy is enqueued;
+    * ``marks``: an event recorded on the transfer stream after each copy (the
+      copy's ready event), which nothing waits on;
     * ``ring``: the streamed pass (loaders.py:1534-1573): the compute stream
-      waits for each copy, reads its slot with a small kernel and records the
-      slot's release, which the copy two later waits on;
+      waits for each copy's ready event, reads its slot with a small kernel and
+      records the slot's release, which the copy two later waits on;
+    * ``consume_only``: the compute stream waits for each ready event and reads
+      the slot, but no copy waits on a release (what the compute side costs);
+    * ``handshake_only``: the ring's events and waits with no compute kernels
+      (what the cross-stream waits cost);
     * ``ring_kernel``: ``ring`` with zero-copy kernel copies at 8 workgroups, the
-      link-bound policy.
+      link-bound policy;
+    * ``*_device_only``: the same with every ready and release event created
+      ``device_only`` (``FTX_EVENT_DEVICE_ONLY``: no system-scope fence when
+      recorded).
 
     Per arrangement and size, the median of ``reps`` chains: microseconds per
     copy (HIP events on the transfer stream around the chain), GB/s, and the
@@ -1181,6 +1190,8 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
     comp, xs = current_stream(dev), transfer_stream(dev)
     kernel_policy = nat.copy_policy(0, 2**63 - 1, 1, L.RING_KERNEL_GRID)
     acc = torch.zeros(1, dtype=torch.float32, device=dev)
+    kinds = ("back_to_back", "slot_waits", "marks", "marks_device_only", "consume_only", "handshake_only", "ring",
+             "ring_device_only", "ring_kernel", "ring_kernel_device_only")
     out: dict = {"copies": copies, "sizes": {}}
     for mib in sizes_mib:
         nb = mib * MiB
@@ -1204,7 +1215,11 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
             return best
 
         def chain_ms(kind):
-            mode, policy = (nat.COPY_KERNEL, kernel_policy) if kind == "ring_kernel" else (nat.COPY_SDMA, None)
+            kernel = kind.startswith("ring_kernel")
+            mode, policy = (nat.COPY_KERNEL, kernel_policy) if kernel else (nat.COPY_SDMA, None)
+            device_only = kind.endswith("_device_only")
+            ring = kind.startswith("ring") or kind == "handshake_only"
+            consume = kind.startswith("ring") or kind == "consume_only"
             torch.cuda.synchronize()
             released = [None, None]
             start, end = HipEvent(True), HipEvent(True)
@@ -1214,13 +1229,16 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
                 s = i % 2
                 if kind == "slot_waits":
                     xs.wait_event(comp.record_event())
-                elif kind != "back_to_back" and released[s] is not None:
+                elif ring and released[s] is not None:
                     xs.wait_event(released[s])
                 one(s, mode, policy, xs)
-                if kind in ("ring", "ring_kernel"):
-                    comp.wait_event(xs.record_event())
-                    acc.add_(slots[s][:4096].float().sum())
-                    released[s] = comp.record_event()
+                if kind.startswith("marks") or ring or consume:
+                    ready = xs.record_event(HipEvent(device_only=device_only))
+                    if ring or consume:
+                        comp.wait_event(ready)
+                        if consume:
+                            acc.add_(slots[s][:4096].float().sum())
+                        released[s] = comp.record_event(HipEvent(device_only=device_only))
             xs.record_event(end)
             torch.cuda.synchronize()
             return start.elapsed_time(end)
@@ -1228,10 +1246,10 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
         row: dict = {"bytes": nb}
         lone = {"sdma": lone_ms(nat.COPY_SDMA, None), "kernel_g8": lone_ms(nat.COPY_KERNEL, kernel_policy)}
         row["lone_copy_us"] = {k: round(v * 1e3, 1) for k, v in lone.items()}
-        for kind in ("back_to_back", "slot_waits", "ring", "ring_kernel"):
+        for kind in kinds:
             chain_ms(kind)  # warm-up
             t = sorted(chain_ms(kind) for _ in range(reps))[reps // 2]
-            base = lone["kernel_g8" if kind == "ring_kernel" else "sdma"]
+            base = lone["kernel_g8" if kind.startswith("ring_kernel") else "sdma"]
             row[kind] = {"us_per_copy": round(t * 1e3 / copies, 1), "GBps": round(copies * nb / t / 1e6, 2),
                          "idle_us_per_boundary": round((t - copies * base) * 1e3 / (copies - 1), 1)}
             _log(f"copy chain {mib} MiB {kind}: {row[kind]}")

@@ -40,6 +40,7 @@ ARENA_NUMA_USER = 8
 
 EVENT_DEFAULT = 0
 EVENT_TIMING = 1
+EVENT_DEVICE_ONLY = 2
 
 
 class FtxError(RuntimeError):

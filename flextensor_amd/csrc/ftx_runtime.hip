@@ -601,8 +601,11 @@ int ftx_stream_query(void *stream, int *done) {
 int ftx_event_create(unsigned flags, void **event) {
   FTX_REQUIRE_LIVE();
   if (!event) return ftx::fail(FTX_ERR_INVALID, "event is null");
+  if (flags & ~(FTX_EVENT_TIMING | FTX_EVENT_DEVICE_ONLY)) return ftx::fail(FTX_ERR_INVALID, "unknown event flags");
+  unsigned hflags = (flags & FTX_EVENT_TIMING) ? hipEventDefault : hipEventDisableTiming;
+  if (flags & FTX_EVENT_DEVICE_ONLY) hflags |= hipEventDisableSystemFence;
   hipEvent_t e = nullptr;
-  FTX_HIP(hipEventCreateWithFlags(&e, (flags & FTX_EVENT_TIMING) ? hipEventDefault : hipEventDisableTiming));
+  FTX_HIP(hipEventCreateWithFlags(&e, hflags));
   *event = e;
   return FTX_OK;
 }

@@ -20,7 +20,7 @@ import torch
 from . import _native as nat
 
 
-_FREE_EVENTS: dict[bool, list[int]] = {False: [], True: []}
+_FREE_EVENTS: dict[int, list[int]] = {}  # recycled handles by creation flags
 _MAX_FREE_EVENTS = 4096
 
 
@@ -34,12 +34,15 @@ class HipEvent:
     preceded it.
     """
 
-    __slots__ = ("handle", "timing", "__weakref__")
+    __slots__ = ("handle", "timing", "flags", "__weakref__")
 
-    def __init__(self, timing: bool = False) -> None:
+    def __init__(self, timing: bool = False, device_only: bool = False) -> None:
+        """``device_only``: only streams of this device wait on it, so recording it skips the system-scope
+        fence (``FTX_EVENT_DEVICE_ONLY``); host waits still see it complete."""
         self.timing = timing
-        free = _FREE_EVENTS[timing]
-        self.handle = free.pop() if free else nat.event_create(nat.EVENT_TIMING if timing else nat.EVENT_DEFAULT)
+        self.flags = (nat.EVENT_TIMING if timing else nat.EVENT_DEFAULT) | (nat.EVENT_DEVICE_ONLY if device_only else 0)
+        free = _FREE_EVENTS.setdefault(self.flags, [])
+        self.handle = free.pop() if free else nat.event_create(self.flags)
 
     def record(self, stream: "HipStream | None" = None) -> "HipEvent":
         s = stream if stream is not None else current_stream()
@@ -63,7 +66,7 @@ class HipEvent:
         try:
             if not nat.live():
                 return
-            free = _FREE_EVENTS[self.timing]
+            free = _FREE_EVENTS.setdefault(self.flags, [])
             if len(free) < _MAX_FREE_EVENTS:
                 free.append(h)
             else:

@@ -53,6 +53,12 @@ extern "C" {
 /* ---- events ------------------------------------------------------------ */
 #define FTX_EVENT_DEFAULT 0u /* no timing: cheapest record/wait */
 #define FTX_EVENT_TIMING 1u  /* timing enabled (ftx_event_elapsed_ms) */
+/* Only streams of this device wait on the event: recording it skips the
+ * system-scope fence (cache writeback and invalidation for the host's view,
+ * hipEventDisableSystemFence); device-scope ordering between the streams is
+ * kept. Host waits still see it complete, but device writes before it are not
+ * made visible to the host. For the ring's ready and slot-release events. */
+#define FTX_EVENT_DEVICE_ONLY 2u
 
 /* One scatter descriptor: dst[0:nbytes) = chunk[src_off : src_off+nbytes).
  * Replaces the per-tensor copies the reference makes when it places tensors
