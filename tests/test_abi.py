@@ -175,3 +175,18 @@ def test_exit_releases_the_library_quietly():
     out = _run_python(code)
     assert out.returncode == 0 and out.stderr == "", out.stderr
     assert out.stdout.split() == ["before", "live", "after", "refused"], out.stdout
+
+
+def test_event_flags_are_checked_before_the_runtime():
+    """``ftx_event_create`` takes FTX_EVENT_TIMING and FTX_EVENT_DEVICE_ONLY; any other bit is refused on the
+    host, with no device involved."""
+    import ctypes
+
+    from flextensor_amd import _native
+
+    lib = _native.load()
+    ev = ctypes.c_void_p()
+    for bad in (4, 8, 0x20000000, 0x80000003):
+        assert lib.ftx_event_create(bad, ctypes.byref(ev)) == _native.FTX_ERR_INVALID
+        assert b"unknown event flags" in lib.ftx_last_error()
+    assert (_native.EVENT_TIMING, _native.EVENT_DEVICE_ONLY) == (1, 2)

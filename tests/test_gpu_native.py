@@ -303,3 +303,26 @@ def test_probes_write_nothing_and_check_arguments(gpu):
     host = torch.zeros(1, dtype=torch.int32)
     with pytest.raises(nat.FtxError):
         nat.call("ftx_mfma_probe", 8, 16, host.data_ptr(), s)
+
+
+@pytest.mark.parametrize("mode", ["sdma", "kernel"])
+def test_device_only_event_orders_a_copy_before_its_consumer(gpu, mode):
+    """An ``FTX_EVENT_DEVICE_ONLY`` event recorded after a copy on one stream orders a kernel on another
+    stream after the copy: the consumer reads every copied byte."""
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import HipEvent, current_stream, new_stream
+
+    n = (32 << 20) + 48
+    data = _rand_bytes(n, seed=23)
+    arena = _arena_with(data)
+    dst = torch.zeros(n, dtype=torch.uint8, device=gpu)
+    comp, xs = current_stream(gpu), new_stream(gpu, name="device-only-event-test")
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.zero_()
+        xs.wait_stream(comp)
+        nat.copy_h2d(dst.data_ptr(), arena.ptr, n, nat.COPY_MODES[mode], xs.handle)
+        comp.wait_event(xs.record_event(HipEvent(device_only=True)))
+        got = dst.clone()  # on the compute stream, after the wait
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), data)
