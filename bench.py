@@ -711,6 +711,28 @@ def bench_fp8_linear(batch: int = 8, reps: int = 20) -> dict:
 
     layer_bytes = sum(nbytes(names, k) for _, names, k in calls)
     layer_ms = graph_ms(lambda i: [run_call(layers[i % n_layers], names, k) for _, names, k in calls], reps)
+    # The same projections with the operations that consume their outputs, as the decoder runs them: the
+    # residual add after o and after down, SiLU(gate) * up before down (whose input it is). Separately
+    # (torch's bf16 ops after each call), then with those ops folded into the calls' reduce kernels.
+    resid = torch.randn(batch, h, device=dev, generator=gen).to(torch.bfloat16)
+
+    def path_separate(i):
+        lay = layers[i % n_layers]
+        run_call(lay, ("wq", "wk", "wv"), h)
+        h1 = resid + hip.fp8_linear(xs[q], *lay["wo"])
+        g, u = run_call(lay, ("gate", "up"), h)
+        return h1 + hip.fp8_linear(F.silu(g) * u, *lay["down"])
+
+    def path_fused(i):
+        lay = layers[i % n_layers]
+        run_call(lay, ("wq", "wk", "wv"), h)
+        h1 = hip.fp8_linear_residual(xs[q], *lay["wo"], resid)
+        act = hip.fp8_linear_swiglu(xs[h], *lay["gate"], *lay["up"])
+        return hip.fp8_linear_residual(act, *lay["down"], h1)
+
+    separate_ms = graph_ms(path_separate, reps)
+    fused_ms = graph_ms(path_fused, reps)
+    path_err = float((path_fused(0).double() - path_separate(0).double()).norm() / path_separate(0).double().norm())
     per_call = []
     for label, names, k in calls:
         ms = graph_ms(lambda i, names=names, k=k: run_call(layers[i % n_layers], names, k), reps)
@@ -760,6 +782,13 @@ def bench_fp8_linear(batch: int = 8, reps: int = 20) -> dict:
     del bufs
     torch.cuda.empty_cache()
     return {"batch": batch, "calls": per_call, "layer_us": round(layer_ms * 1e3, 2),
+            "decoder_path": {
+                "what": "the four calls with their consumers: residual adds after o and down, SiLU(gate)*up "
+                        "feeding down",
+                "separate_us": round(separate_ms * 1e3, 2), "fused_us": round(fused_ms * 1e3, 2),
+                "frac_separate": round(layer_bytes / separate_ms / 1e6 / HBM_PEAK_GBPS, 4),
+                "frac_fused": round(layer_bytes / fused_ms / 1e6 / HBM_PEAK_GBPS, 4),
+                "fused_vs_separate_rel_err": round(path_err, 6)},
             "plain_read_layer_us": round(read_ms * 1e3, 2),
             "frac_of_plain_read": round(read_ms / layer_ms, 4),
             "layer_ungrouped_us": round(ungrouped_ms * 1e3, 2), "layer_dequant_gemm_us": round(dq_ms * 1e3, 2),

@@ -151,7 +151,15 @@ _SIGNATURES: dict[str, list] = {
     "ftx_fp8_linear_group_workspace": [ctypes.c_int64, _vp, ctypes.c_int, ctypes.c_int64, ctypes.POINTER(_sz)],
     "ftx_fp8_linear_group": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _sz, _vp],
     "ftx_set_fp8_linear_config": [_int, _int],
+    "ftx_fp8_linear_fused_workspace": [ctypes.c_int64, _vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
+                                       ctypes.POINTER(_sz)],
+    "ftx_fp8_linear_fused": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _vp,
+                             _vp, _sz, _vp],
 }
+
+FP8_EPILOGUE_NONE = 0
+FP8_EPILOGUE_SWIGLU = 1
+FP8_EPILOGUE_RESIDUAL = 2
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()

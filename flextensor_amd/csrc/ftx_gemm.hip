@@ -229,7 +229,7 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
 
   // Lane l holds rows n0 + 4*(l/16) + i, column b*16 + l%16.
   const int nb = n0 + 4 * g;
-  if (splits == 1) {
+  if (part == nullptr) {  // one slice and no epilogue: the kernel writes y itself
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
       const int m = b * 16 + r;
@@ -259,21 +259,24 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
 // summed in slice order. Blocks [rb0[s], rb0[s+1]) reduce matrix s; each
 // thread owns kReduceVec consecutive outputs and keeps up to kReduceBatch
 // independent loads in flight.
+//
+// Epilogues fold the operation that consumes the output into the reduce, with
+// the rounding of that operation run on its own in bf16 (each value rounded to
+// bf16 where the separate operation would round it):
+//   kFp8EpilogueSwiglu (two matrices of equal n, gate then up):
+//     y_0[i] = bf16(bf16(silu(g)) * u), g = bf16(gate), u = bf16(up);
+//   kFp8EpilogueResidual (one matrix): y_0[i] = bf16(residual[i] + bf16(...)).
 constexpr int kReduceVec = 4;
 constexpr int kReduceBatch = 8;
 constexpr int kReduceThreads = 256;
-__global__ __launch_bounds__(kReduceThreads) void fp8_linear_reduce_kernel(const float *__restrict__ part,
-                                                                           SegTable seg, int M, int splits) {
-  int s = 0;
-  while (s + 1 < seg.count && static_cast<int>(blockIdx.x) >= seg.rb0[s + 1]) ++s;
-  const int N = seg.n[s];
-  const int64_t MN = static_cast<int64_t>(M) * N;
-  const int64_t i0 = (static_cast<int64_t>(blockIdx.x - seg.rb0[s]) * blockDim.x + threadIdx.x) * kReduceVec;
-  if (i0 >= MN) return;
-  const float *__restrict__ p = part + seg.part0[s];
-  const uint16_t *__restrict__ scale = seg.scale[s];
-  uint16_t *__restrict__ y = seg.y[s];
-  float acc[kReduceVec] = {0.f, 0.f, 0.f, 0.f};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// Sum over slices of kReduceVec consecutive partials starting at i0 (fewer at the end of MN).
+__device__ __forceinline__ void sum_slices(const float *__restrict__ p, int64_t MN, int64_t i0, int splits,
+                                           float (&acc)[kReduceVec]) {
+#pragma unroll
+  for (int e = 0; e < kReduceVec; ++e) acc[e] = 0.f;
   if (MN % kReduceVec == 0) {
     for (int p0 = 0; p0 < splits; p0 += kReduceBatch) {
       f32x4 v[kReduceBatch];
@@ -291,12 +294,46 @@ __global__ __launch_bounds__(kReduceThreads) void fp8_linear_reduce_kernel(const
       for (int e = 0; e < kReduceVec; ++e)
         if (i0 + e < MN) acc[e] += p[q * MN + i0 + e];
   }
+}
+
+__global__ __launch_bounds__(kReduceThreads) void fp8_linear_reduce_kernel(const float *__restrict__ part,
+                                                                           SegTable seg, int M, int splits,
+                                                                           int epilogue,
+                                                                           const uint16_t *__restrict__ residual) {
+  int s = 0;
+  while (s + 1 < seg.count && static_cast<int>(blockIdx.x) >= seg.rb0[s + 1]) ++s;
+  const int N = seg.n[s];
+  const int64_t MN = static_cast<int64_t>(M) * N;
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x - seg.rb0[s]) * blockDim.x + threadIdx.x) * kReduceVec;
+  if (i0 >= MN) return;
+  const uint16_t *__restrict__ scale = seg.scale[s];
+  uint16_t *__restrict__ y = seg.y[s];
+  float acc[kReduceVec];
+  sum_slices(part + seg.part0[s], MN, i0, splits, acc);
+  if (epilogue == kFp8EpilogueSwiglu) {  // s is 0: the gate; the up matrix is segment 1, same shape
+    float up[kReduceVec];
+    sum_slices(part + seg.part0[1], MN, i0, splits, up);
+    const uint16_t *__restrict__ scale_up = seg.scale[1];
+#pragma unroll
+    for (int e = 0; e < kReduceVec; ++e) {
+      const int64_t i = i0 + e;
+      if (i < MN) {
+        const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[e] * bf16_bits_to_f32(scale[i % N])));
+        const float u = bf16_bits_to_f32(f32_to_bf16_bits(up[e] * bf16_bits_to_f32(scale_up[i % N])));
+        const float act = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.0f + expf(-g))));
+        y[i] = f32_to_bf16_bits(act * u);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < kReduceVec; ++e) {
     const int64_t i = i0 + e;
     if (i < MN) {
-      const float sc = __uint_as_float(static_cast<uint32_t>(scale[i % N]) << 16);
-      y[i] = f32_to_bf16_bits(acc[e] * sc);
+      const uint16_t out = f32_to_bf16_bits(acc[e] * bf16_bits_to_f32(scale[i % N]));
+      y[i] = epilogue == kFp8EpilogueResidual
+                 ? f32_to_bf16_bits(bf16_bits_to_f32(residual[i]) + bf16_bits_to_f32(out))
+                 : out;
     }
   }
 }
@@ -647,21 +684,27 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(float *sink, int iters)
 template <int MB>
 hipError_t launch_mb(const Fp8LinearLaunch &p, hipStream_t stream) {
   const SegTable seg = seg_table(p);
+  const bool reduce = p.workspace_bytes > 0;  // split K, or an epilogue: partials, then the reduce kernel
   hipLaunchKernelGGL((fp8_linear_kernel<MB>), dim3(static_cast<unsigned>(p.grid)), dim3(p.waves * kWave),
-                     p.lds_bytes, stream, static_cast<const uint8_t *>(p.x), seg, static_cast<float *>(p.workspace),
-                     static_cast<int>(p.m), static_cast<int>(p.k), static_cast<int>(p.kc), p.splits);
+                     p.lds_bytes, stream, static_cast<const uint8_t *>(p.x), seg,
+                     reduce ? static_cast<float *>(p.workspace) : nullptr, static_cast<int>(p.m), static_cast<int>(p.k),
+                     static_cast<int>(p.kc), p.splits);
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess || p.splits == 1) return err;
-  hipLaunchKernelGGL(fp8_linear_reduce_kernel, dim3(static_cast<unsigned>(seg.rb0[p.group])), dim3(kReduceThreads),
-                     0, stream, static_cast<const float *>(p.workspace), seg, static_cast<int>(p.m), p.splits);
+  if (err != hipSuccess || !reduce) return err;
+  // the SwiGLU epilogue writes one output per gate/up pair: the gate's blocks only
+  const int blocks = p.epilogue == kFp8EpilogueSwiglu ? seg.rb0[1] : seg.rb0[p.group];
+  hipLaunchKernelGGL(fp8_linear_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kReduceThreads), 0, stream,
+                     static_cast<const float *>(p.workspace), seg, static_cast<int>(p.m), p.splits, p.epilogue,
+                     static_cast<const uint16_t *>(p.residual));
   return hipGetLastError();
 }
 
 }  // namespace
 
 Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int xcds, int waves,
-                                int kc_override) {
+                                int kc_override, int epilogue) {
   Fp8LinearLaunch p{};
+  p.epilogue = epilogue;
   p.m = m;
   p.k = k;
   p.group = group;
@@ -724,7 +767,10 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
   p.grid = row_groups * p.splits;
   p.row_groups = row_groups;
   p.lds_bytes = static_cast<size_t>(m) * (2 * p.kc + 16) + static_cast<size_t>(tiles);
-  p.workspace_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * m * p.n_total * sizeof(float) : 0;
+  // partials when K is split, and always under an epilogue (the reduce kernel applies it)
+  p.workspace_bytes = p.splits > 1 || epilogue != kFp8EpilogueNone
+                          ? static_cast<size_t>(p.splits) * m * p.n_total * sizeof(float)
+                          : 0;
   return p;
 }
 

@@ -61,6 +61,10 @@ struct ScatterPlanDev {
 // launch covers `group` weight matrices (segments) that share the input x and
 // k: y_s = bf16(scale_s * x @ w_s^T) for each segment s.
 constexpr int kFp8MaxGroup = 4;
+// Epilogues the decode kernel's reduce can apply (FTX_FP8_EPILOGUE_* in ftx.h).
+constexpr int kFp8EpilogueNone = FTX_FP8_EPILOGUE_NONE;
+constexpr int kFp8EpilogueSwiglu = FTX_FP8_EPILOGUE_SWIGLU;
+constexpr int kFp8EpilogueResidual = FTX_FP8_EPILOGUE_RESIDUAL;
 struct Fp8LinearLaunch {
   const void *x;                       // bf16 [m, k]
   int group;                           // segments in this launch, 1..kFp8MaxGroup
@@ -79,6 +83,8 @@ struct Fp8LinearLaunch {
   int64_t grid;       // workgroups = row_groups * splits
   size_t lds_bytes;   // activation slice + one weight tile per wave
   size_t workspace_bytes;
+  int epilogue;         // kFp8Epilogue*: what the reduce kernel applies to the outputs
+  const void *residual; // bf16 [m, n[0]] for kFp8EpilogueResidual
   bool prefill;       // more than kFp8LinearMaxRows rows: the tiled prefill kernel (no split, no workspace)
   int64_t m_tiles;    // prefill: tiles of 128 activation rows (row_groups then counts tiles of 128 channels)
   int xcds;           // prefill: L2 domains the block order is arranged for
@@ -86,7 +92,7 @@ struct Fp8LinearLaunch {
 constexpr int kFp8LinearMaxRows = 64;
 constexpr size_t kFp8LinearMaxLds = 64 * 1024;
 Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t k, int cus, int xcds, int waves,
-                                int kc);
+                                int kc, int epilogue);
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream);
 // MFMA rate probe: `workgroups` x 4 waves, each iters x 32 v_mfma_f32_16x16x32_bf16.
 hipError_t launch_mfma_probe(int workgroups, int iters, float *sink, hipStream_t stream);

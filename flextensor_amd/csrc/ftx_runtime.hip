@@ -763,7 +763,8 @@ int ftx_set_fp8_linear_config(int waves, int slice_k) {
 
 namespace {
 
-int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLaunch *p) {
+int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLaunch *p,
+             int epilogue = ftx::kFp8EpilogueNone) {
   if (group < 1 || group > ftx::kFp8MaxGroup)
     return ftx::fail(FTX_ERR_INVALID, "a grouped fp8 linear takes 1 to " + std::to_string(ftx::kFp8MaxGroup) +
                                           " weight matrices");
@@ -778,11 +779,23 @@ int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLa
   if (k % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "k must be a multiple of 16");
   if (n_total > (int64_t(1) << 30) || k > (int64_t(1) << 30) || m * n_total > (int64_t(1) << 31))
     return ftx::fail(FTX_ERR_INVALID, "fp8 linear dimensions too large");
+  if (epilogue == ftx::kFp8EpilogueSwiglu) {
+    if (group != 2 || n[0] != n[1])
+      return ftx::fail(FTX_ERR_INVALID, "the SwiGLU epilogue takes two matrices (gate, up) with the same n");
+  } else if (epilogue == ftx::kFp8EpilogueResidual) {
+    if (group != 1) return ftx::fail(FTX_ERR_INVALID, "the residual epilogue takes one matrix");
+  } else if (epilogue != ftx::kFp8EpilogueNone) {
+    return ftx::fail(FTX_ERR_INVALID, "unknown fp8 linear epilogue");
+  }
+  if (epilogue != ftx::kFp8EpilogueNone && m > ftx::kFp8LinearMaxRows)
+    return ftx::fail(FTX_ERR_UNSUPPORTED, "fp8 linear epilogues run in the decode kernel only (at most " +
+                                              std::to_string(ftx::kFp8LinearMaxRows) + " rows)");
   if (m == 0 || n_total == 0) {
     *p = ftx::Fp8LinearLaunch{};
     p->group = group;
     p->m = m;
     p->k = k;
+    p->epilogue = epilogue;
     return FTX_OK;
   }
   int waves, slice_k;
@@ -799,7 +812,7 @@ int plan_fp8(int64_t m, const int64_t *n, int group, int64_t k, ftx::Fp8LinearLa
       xcds = st->xcd_count;
     }
   }
-  *p = ftx::plan_fp8_linear(m, n, group, k, cus, xcds, waves, slice_k);
+  *p = ftx::plan_fp8_linear(m, n, group, k, cus, xcds, waves, slice_k, epilogue);
   if (p->grid > (int64_t(1) << 31) - 1) return ftx::fail(FTX_ERR_INVALID, "fp8 linear grid too large");
   return FTX_OK;
 }
@@ -853,6 +866,13 @@ int run_fp8(ftx::Fp8LinearLaunch &p, const void *x, const void *const *w, const 
     int rc = ftx::check_device_range(x, static_cast<size_t>(m * k * 2), "fp8 linear input");
     if (rc != FTX_OK) return rc;
   }
+  if (p.epilogue == ftx::kFp8EpilogueResidual) {
+    if (!p.residual) return ftx::fail(FTX_ERR_INVALID, "the residual epilogue needs a residual");
+    if (reinterpret_cast<uintptr_t>(p.residual) % 2 != 0)
+      return ftx::fail(FTX_ERR_INVALID, "residual needs 2-byte alignment");
+    int rc = ftx::check_device_range(p.residual, static_cast<size_t>(m * p.n[0] * 2), "fp8 linear residual");
+    if (rc != FTX_OK) return rc;
+  }
   if (p.workspace_bytes > 0 && !static_workspace) {
     if (!workspace || workspace_bytes < p.workspace_bytes)
       return ftx::fail(FTX_ERR_INVALID, "fp8 linear needs a workspace of " + std::to_string(p.workspace_bytes) +
@@ -884,6 +904,31 @@ int ftx_fp8_linear_group(const void *x, int group, const void *const *w, const v
   if (rc != FTX_OK) return rc;
   if (m == 0 || p.n_total == 0) return FTX_OK;
   return run_fp8(p, x, w, scale, y, workspace, workspace_bytes, false, stream);
+}
+
+int ftx_fp8_linear_fused_workspace(int64_t m, const int64_t *n, int group, int64_t k, int epilogue, size_t *bytes) {
+  if (!bytes) return ftx::fail(FTX_ERR_INVALID, "bytes is null");
+  ftx::Fp8LinearLaunch p;
+  int rc = plan_fp8(m, n, group, k, &p, epilogue);
+  if (rc != FTX_OK) return rc;
+  *bytes = p.workspace_bytes;
+  return FTX_OK;
+}
+
+int ftx_fp8_linear_fused(const void *x, int group, const void *const *w, const void *const *scale, void *y,
+                         const int64_t *n, int64_t m, int64_t k, int epilogue, const void *residual, void *workspace,
+                         size_t workspace_bytes, void *stream) {
+  FTX_REQUIRE_LIVE();
+  ftx::Fp8LinearLaunch p;
+  int rc = plan_fp8(m, n, group, k, &p, epilogue);
+  if (rc != FTX_OK) return rc;
+  if (m == 0 || p.n_total == 0) return FTX_OK;
+  if (!y) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  // Each matrix's output slot is the one output: the SwiGLU reduce writes only the gate's, and the
+  // up matrix's slot (same shape) is checked and never written.
+  void *const ys[ftx::kFp8MaxGroup] = {y, y, y, y};
+  p.residual = residual;
+  return run_fp8(p, x, w, scale, ys, workspace, workspace_bytes, false, stream);
 }
 
 int ftx_fp8_linear_static(const void *x, const void *w, const void *scale, void *y, int64_t m, int64_t n, int64_t k,

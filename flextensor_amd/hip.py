@@ -438,6 +438,69 @@ def fp8_linear_group(x: torch.Tensor, weights: list[torch.Tensor], scales: list[
     return outs
 
 
+def fp8_linear_fused_workspace_bytes(m: int, ns: list[int], k: int, epilogue: int) -> int:
+    """Bytes of device workspace one ``ftx_fp8_linear_fused`` call of these shapes needs (cached per shape)."""
+    key = ("fused", epilogue, m, k) + tuple(ns)
+    got = _FP8_WORKSPACE.get(key)
+    if got is None:
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        b = ctypes.c_size_t(0)
+        nat.call("ftx_fp8_linear_fused_workspace", m, ctypes.cast(arr, ctypes.c_void_p), len(ns), k, epilogue,
+                 ctypes.byref(b))
+        got = _FP8_WORKSPACE[key] = int(b.value)
+    return got
+
+
+def _fp8_fused(x: torch.Tensor, weights: list[torch.Tensor], scales: list[torch.Tensor], epilogue: int,
+               residual: torch.Tensor | None, what: str) -> torch.Tensor:
+    ms = [_check_fp8_operands(what, x, w, sc) for w, sc in zip(weights, scales)]
+    m, k, n = ms[0]
+    if m > FP8_DECODE_MAX_ROWS:
+        raise ValueError(f"{what} runs in the decode kernel: at most {FP8_DECODE_MAX_ROWS} rows, got {m}")
+    for w in weights:
+        if not w.is_contiguous() or w.data_ptr() % 16:
+            raise ValueError(f"{what} needs contiguous, 16-byte aligned weights")
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        x = x.clone(memory_format=torch.contiguous_format)
+    scales = [sc if sc.is_contiguous() else sc.contiguous() for sc in scales]
+    if residual is not None:
+        if residual.shape != (m, n) or residual.dtype != torch.bfloat16 or residual.device != x.device:
+            raise ValueError(f"{what}: the residual must be bf16 [{m}, {n}] on {x.device}")
+        if not residual.is_contiguous():
+            residual = residual.contiguous()
+    g = len(weights)
+    ns = [w.shape[0] for w in weights]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    ws_bytes = fp8_linear_fused_workspace_bytes(m, ns, k, epilogue)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    arrays = [(ctypes.c_void_p * g)(*[t.data_ptr() for t in ts]) for ts in (weights, scales)]
+    n_arr = (ctypes.c_int64 * g)(*ns)
+    nat.call("ftx_fp8_linear_fused", x.data_ptr(), g, *(ctypes.cast(a, ctypes.c_void_p) for a in arrays),
+             y.data_ptr(), ctypes.cast(n_arr, ctypes.c_void_p), m, k, epilogue,
+             residual.data_ptr() if residual is not None else None, ws.data_ptr(), ws_bytes,
+             torch.cuda.current_stream(x.device).cuda_stream)
+    return y
+
+
+def fp8_linear_swiglu(x: torch.Tensor, w_gate: torch.Tensor, s_gate: torch.Tensor, w_up: torch.Tensor,
+                      s_up: torch.Tensor) -> torch.Tensor:
+    """``F.silu(g) * u`` for ``g, u = fp8_linear(x, w_gate, s_gate), fp8_linear(x, w_up, s_up)`` in one grouped
+    launch plus its reduce (``FTX_FP8_EPILOGUE_SWIGLU``): a SwiGLU MLP's gate and up projections and their
+    activation. Decode batches only (at most 64 rows); g and u are rounded to bf16 as the separate
+    projections round them, silu(g) is rounded to bf16, then the product."""
+    if w_gate.shape != w_up.shape:
+        raise ValueError(f"gate and up weights differ in shape: {tuple(w_gate.shape)} and {tuple(w_up.shape)}")
+    return _fp8_fused(x, [w_gate, w_up], [s_gate, s_up], nat.FP8_EPILOGUE_SWIGLU, None, "fp8_linear_swiglu")
+
+
+def fp8_linear_residual(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
+                        residual: torch.Tensor) -> torch.Tensor:
+    """``residual + fp8_linear(x, weight, scale)`` with the add folded into the reduce
+    (``FTX_FP8_EPILOGUE_RESIDUAL``): a decoder's output projection and its residual connection. Decode
+    batches only (at most 64 rows); the same bits as the separate linear and bf16 add."""
+    return _fp8_fused(x, [weight], [scale], nat.FP8_EPILOGUE_RESIDUAL, residual, "fp8_linear_residual")
+
+
 def fp8_linear_static(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     """``fp8_linear`` into ``out`` (bf16 ``[m, n]``) with no allocation at all, for graph capture and serving
     loops: the split-K partial sums live in the library's static per-GPU scratch array

@@ -158,11 +158,22 @@ class Fp8Linear(nn.Module):
         return F.linear(x, w) * self.scale
 
 
+def _plain_call(module: nn.Module) -> bool:
+    """Whether calling ``module`` would run its class's forward and nothing else: no forward set on the
+    instance (an offload manager's enter/exit trap is one) and no forward hooks. Only then may a caller
+    compute the module's output from its weights directly, in a grouped or fused launch."""
+    from torch.nn.modules import module as torch_module
+
+    return ("forward" not in module.__dict__ and not module._forward_hooks and not module._forward_pre_hooks
+            and not torch_module._global_forward_hooks and not torch_module._global_forward_pre_hooks)
+
+
 def fp8_group(x: torch.Tensor, layers: list[nn.Module]) -> list[torch.Tensor] | None:
     """The outputs of several ``Fp8Linear`` layers on one input in one grouped kernel launch, or None when
-    any of them would not take the kernel, or the group's outputs together would reach 2^31 elements, the
-    library's limit for one launch (the caller then runs them one by one)."""
-    if not all(isinstance(lin, Fp8Linear) and lin.kernel_eligible(x) for lin in layers):
+    any of them would not take the kernel, would run more than its own forward when called (an offload
+    unit's trap, a hook), or the group's outputs together would reach 2^31 elements, the library's limit
+    for one launch (the caller then runs them one by one)."""
+    if not all(isinstance(lin, Fp8Linear) and lin.kernel_eligible(x) and _plain_call(lin) for lin in layers):
         return None
     k = x.shape[-1]
     if (x.numel() // k) * sum(lin.weight.shape[0] for lin in layers) >= 2**31:
@@ -170,6 +181,35 @@ def fp8_group(x: torch.Tensor, layers: list[nn.Module]) -> list[torch.Tensor] | 
     ys = hip.fp8_linear_group(x.reshape(x.numel() // k, k), [lin.weight for lin in layers],
                               [lin.scale for lin in layers])
     return [y.view(*x.shape[:-1], y.shape[-1]) for y in ys]
+
+
+def _fusable(x: torch.Tensor, layers: list[nn.Module]) -> bool:
+    """Whether a decode-batch call of these ``Fp8Linear`` layers on ``x`` can take a fused epilogue."""
+    k = x.shape[-1]
+    return (all(isinstance(lin, Fp8Linear) and lin.kernel_eligible(x) and _plain_call(lin) for lin in layers)
+            and x.numel() // k <= hip.FP8_DECODE_MAX_ROWS)
+
+
+def fp8_swiglu(x: torch.Tensor, gate: nn.Module, up: nn.Module) -> torch.Tensor | None:
+    """``F.silu(gate(x)) * up(x)`` as one grouped launch whose reduce applies the activation, or None when
+    the fused form does not apply (the caller then runs the layers and the activation as usual)."""
+    if not _fusable(x, [gate, up]) or gate.weight.shape != up.weight.shape:
+        return None
+    k = x.shape[-1]
+    y = hip.fp8_linear_swiglu(x.reshape(x.numel() // k, k), gate.weight, gate.scale, up.weight, up.scale)
+    return y.view(*x.shape[:-1], y.shape[-1])
+
+
+def fp8_residual(x: torch.Tensor, lin: nn.Module, residual: torch.Tensor) -> torch.Tensor | None:
+    """``residual + lin(x)`` with the add folded into the linear's reduce, or None when the fused form
+    does not apply (the caller then adds as usual)."""
+    if not _fusable(x, [lin]) or residual.dtype != torch.bfloat16 or \
+            residual.shape != (*x.shape[:-1], lin.weight.shape[0]):
+        return None
+    k = x.shape[-1]
+    m = x.numel() // k
+    y = hip.fp8_linear_residual(x.reshape(m, k), lin.weight, lin.scale, residual.reshape(m, -1))
+    return y.view(residual.shape)
 
 
 def _proj(s: LlamaShape, n_in: int, n_out: int, dtype: torch.dtype) -> nn.Module:
@@ -205,7 +245,9 @@ class Attention(nn.Module):
         self.wo = _proj(s, s.n_heads * s.head_dim, s.hidden, dtype)
 
     def forward(self, x: torch.Tensor, pos: int, cos: torch.Tensor, sin: torch.Tensor,
-                cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
+                cache_k: torch.Tensor, cache_v: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        """The attention block's output, plus ``residual`` when given (folded into the output projection's
+        reduce for fp8 decode batches)."""
         s = self.s
         b, t, _ = x.shape
         qkv = fp8_group(x, [self.wq, self.wk, self.wv])
@@ -234,7 +276,10 @@ class Attention(nn.Module):
             scores = scores.masked_fill(mask, float("-inf"))
         p = torch.softmax(scores, dim=-1).to(vh.dtype)
         o = torch.matmul(p, vh).transpose(1, 2).reshape(b, t, s.n_heads * s.head_dim)
-        return self.wo(o)
+        if residual is None:
+            return self.wo(o)
+        fused = fp8_residual(o, self.wo, residual)
+        return fused if fused is not None else residual + self.wo(o)
 
 
 class DecoderLayer(nn.Module):
@@ -249,11 +294,15 @@ class DecoderLayer(nn.Module):
 
     def forward(self, x: torch.Tensor, pos: int, cos: torch.Tensor, sin: torch.Tensor,
                 cache_k: torch.Tensor, cache_v: torch.Tensor) -> torch.Tensor:
-        x = x + self.attn(self.attn_norm(x), pos, cos, sin, cache_k, cache_v)
+        x = self.attn(self.attn_norm(x), pos, cos, sin, cache_k, cache_v, residual=x)
         h = self.mlp_norm(x)
-        gu = fp8_group(h, [self.gate, self.up])
-        g, u = gu if gu is not None else (self.gate(h), self.up(h))
-        return x + self.down(F.silu(g) * u)
+        act = fp8_swiglu(h, self.gate, self.up)
+        if act is None:
+            gu = fp8_group(h, [self.gate, self.up])
+            g, u = gu if gu is not None else (self.gate(h), self.up(h))
+            act = F.silu(g) * u
+        out = fp8_residual(act, self.down, x)
+        return out if out is not None else x + self.down(act)
 
 
 class LlamaModel(nn.Module):

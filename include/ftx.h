@@ -248,6 +248,29 @@ int ftx_fp8_linear_group(const void *x, int group, const void *const *w, const v
                          const int64_t *n, int64_t m, int64_t k, void *workspace, size_t workspace_bytes,
                          void *stream);
 
+/* Fused forms for decode batches (m <= 64): the reduce kernel that sums the
+ * split-K partials also applies the operation that consumes the output, so it
+ * is not a launch of its own. No counterpart in the reference, whose models
+ * run these as separate PyTorch operations; each epilogue rounds to bf16
+ * where those operations do.
+ *   FTX_FP8_EPILOGUE_SWIGLU   group 2 (gate, up), n[0] == n[1]:
+ *                             y = bf16(bf16(silu(g)) * u), g and u the bf16
+ *                             outputs of the two matrices (F.silu(g) * u);
+ *   FTX_FP8_EPILOGUE_RESIDUAL group 1: y = bf16(residual + bf16(out))
+ *                             (residual + F.linear(...)); residual is bf16
+ *                             [m, n] and may be y itself.
+ * y is one bf16 [m, n[0]] output. Every call goes through the workspace
+ * (ftx_fp8_linear_fused_workspace, non-zero). More than 64 rows, or an
+ * epilogue of the wrong group shape, returns FTX_ERR_UNSUPPORTED or
+ * FTX_ERR_INVALID before any operand is touched. */
+#define FTX_FP8_EPILOGUE_NONE 0
+#define FTX_FP8_EPILOGUE_SWIGLU 1
+#define FTX_FP8_EPILOGUE_RESIDUAL 2
+int ftx_fp8_linear_fused_workspace(int64_t m, const int64_t *n, int group, int64_t k, int epilogue, size_t *bytes);
+int ftx_fp8_linear_fused(const void *x, int group, const void *const *w, const void *const *scale, void *y,
+                         const int64_t *n, int64_t m, int64_t k, int epilogue, const void *residual, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
 /* Bytes of the static scratch array behind ftx_fp8_linear_static (64 MiB per GPU). */
 #define FTX_FP8_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
 /* No counterpart in the reference. For callers that cannot allocate device

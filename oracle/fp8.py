@@ -41,3 +41,31 @@ def fp8_linear(x: np.ndarray, w_raw: np.ndarray, scale: np.ndarray) -> np.ndarra
     """float64 ``scale[j] * sum_k x[i, k] * w[j, k]``; x and scale as float64-convertible arrays."""
     w = decode_e4m3fn(w_raw)
     return (np.asarray(x, dtype=np.float64) @ w.T) * np.asarray(scale, dtype=np.float64)[None, :]
+
+
+def bf16_round(a) -> np.ndarray:
+    """float64 values rounded to the nearest bfloat16 (ties to even), the rounding of every bf16 tensor
+    operation: to float32 first (exact for float32 inputs), then the low 16 bits of the float32 pattern
+    rounded away. NaN stays NaN; values past the largest bf16 round to infinity."""
+    with np.errstate(over="ignore"):  # beyond float32's range is beyond bf16's: infinity either way
+        f = np.asarray(a, dtype=np.float64).astype(np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = rounded.astype(np.uint32).view(np.float32).astype(np.float64)
+    return np.where(np.isnan(f), np.nan, out)
+
+
+def fp8_linear_swiglu(x: np.ndarray, wg_raw: np.ndarray, sg: np.ndarray, wu_raw: np.ndarray,
+                      su: np.ndarray) -> np.ndarray:
+    """``F.silu(g) * u`` of two bf16 fp8 linears, each operation rounded to bf16 as the separate PyTorch
+    operations round it: g = bf16(gate), u = bf16(up), a = bf16(g / (1 + exp(-g))), then bf16(a * u).
+    The arithmetic between roundings is exact float64."""
+    g = bf16_round(fp8_linear(x, wg_raw, sg))
+    u = bf16_round(fp8_linear(x, wu_raw, su))
+    act = bf16_round(g / (1.0 + np.exp(-g)))
+    return bf16_round(act * u)
+
+
+def fp8_linear_residual(x: np.ndarray, w_raw: np.ndarray, scale: np.ndarray, residual: np.ndarray) -> np.ndarray:
+    """``residual + F.linear(...)`` in bf16: bf16(residual + bf16(linear)), the add exact in float64."""
+    return bf16_round(np.asarray(residual, dtype=np.float64) + bf16_round(fp8_linear(x, w_raw, scale)))

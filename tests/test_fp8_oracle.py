@@ -49,3 +49,42 @@ def test_fp8_linear_matches_brute_force():
         for j in range(5):
             s = sum(x[i, k] * fp8.e4m3fn_value(int(w_raw[j, k])) for k in range(7))
             assert math.isclose(got[i, j], s * scale[j], rel_tol=1e-12, abs_tol=1e-12)
+
+
+def test_bf16_round_closed_forms_and_torch():
+    """Round to nearest bf16, ties to even: known answers a dropped tie rule or a truncation fails, and
+    agreement with torch's own float32 -> bfloat16 conversion on random and edge values."""
+    r = fp8.bf16_round
+    assert r(1.0) == 1.0 and r(-2.5) == -2.5
+    assert r(1.0 + 2.0 ** -8) == 1.0  # tie below an even mantissa: stays
+    assert r(1.0 + 3 * 2.0 ** -8) == 1.0 + 2.0 ** -6  # tie above an odd mantissa: up to even
+    assert r(1.0 + 2.0 ** -8 + 2.0 ** -20) == 1.0 + 2.0 ** -7  # past the tie: up
+    assert r(1.0 + 2.0 ** -9) == 1.0  # below the tie: truncates
+    assert math.isnan(float(r(float("nan")))) and r(3.5e38) == float("inf")
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([rng.standard_normal(20000) * 10.0 ** rng.integers(-30, 30, 20000),
+                           [0.0, -0.0, 1e-40, -1e-40, 3.3895e38]]).astype(np.float32)
+    want = torch.from_numpy(vals).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(r(vals), want)
+
+
+def test_swiglu_and_residual_restate_the_separate_operations():
+    """The epilogue oracles equal the separate bf16 operations as PyTorch runs them on the CPU (linear,
+    silu, product, add), up to the float32 rounding of silu (1 bf16 ulp at most, in a small share)."""
+    rng = np.random.default_rng(9)
+    m, n, k = 6, 40, 64
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    codes = rng.integers(0, 256, size=(2, n, k), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38
+    scales = torch.from_numpy(rng.random((2, n)).astype(np.float32) / 8 + 0.01).to(torch.bfloat16)
+    xs = x.double().numpy()
+    gate, up = (fp8.bf16_round(fp8.fp8_linear(xs, codes[i], scales[i].double().numpy())) for i in range(2))
+    g, u = torch.from_numpy(gate).to(torch.bfloat16), torch.from_numpy(up).to(torch.bfloat16)
+    want = (torch.nn.functional.silu(g) * u).double().numpy()
+    got = fp8.fp8_linear_swiglu(xs, codes[0], scales[0].double().numpy(), codes[1], scales[1].double().numpy())
+    ulp = np.abs(want) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(got - want) <= ulp) and np.mean(got == want) > 0.97
+    resid = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(torch.bfloat16)
+    want_r = (resid + g).double().numpy()
+    got_r = fp8.fp8_linear_residual(xs, codes[0], scales[0].double().numpy(), resid.double().numpy())
+    assert np.array_equal(got_r, want_r)

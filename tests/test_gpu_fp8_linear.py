@@ -527,3 +527,190 @@ def test_prefill_weight_over_2gib_takes_the_wide_address_path(gpu, default_confi
         assert float(y[i, j].float()) == float(torch.tensor(exact).to(torch.bfloat16).float()), (i, j)
     del w_raw, mag
     torch.cuda.empty_cache()
+
+
+# ---- fused epilogues: SwiGLU after gate/up, the residual add after o and down ---------------------------
+
+_FUSED_SHAPES = [(1, 16, 16), (8, 1024, 8192), (5, 100, 48), (3, 300, 256), (17, 96, 1040), (64, 512, 256),
+                 (8, 8192, 28672)]
+
+
+def _fused_call(nat, x, ws, ss, epilogue, residual=None, out=None):
+    """ftx_fp8_linear_fused through the C ABI; returns the output."""
+    import ctypes
+
+    m, k = x.shape
+    ns = [w.shape[0] for w in ws]
+    g = len(ws)
+    n_arr = (ctypes.c_int64 * g)(*ns)
+    b = ctypes.c_size_t(0)
+    nat.call("ftx_fp8_linear_fused_workspace", m, ctypes.cast(n_arr, ctypes.c_void_p), g, k, epilogue,
+             ctypes.byref(b))
+    ws_buf = torch.empty(b.value, dtype=torch.uint8, device=x.device)
+    y = out if out is not None else torch.empty(m, ns[0], dtype=torch.bfloat16, device=x.device)
+    arrays = [(ctypes.c_void_p * g)(*[t.data_ptr() for t in ts]) for ts in (ws, ss)]
+    nat.call("ftx_fp8_linear_fused", x.data_ptr(), g, *(ctypes.cast(a, ctypes.c_void_p) for a in arrays),
+             y.data_ptr(), ctypes.cast(n_arr, ctypes.c_void_p), m, k, epilogue,
+             residual.data_ptr() if residual is not None else None, ws_buf.data_ptr(), b.value,
+             torch.cuda.current_stream(x.device).cuda_stream)
+    return y, b.value
+
+
+@pytest.mark.parametrize("m,n,k", _FUSED_SHAPES)
+def test_residual_epilogue_is_the_linear_then_the_bf16_add(gpu, default_config, m, n, k):
+    """bf16(residual + bf16(linear)): bit for bit the separate linear and torch's bf16 add, also in place
+    (the residual is the output), and equal to the oracle on exact products."""
+    from flextensor_amd import _native as nat
+    from flextensor_amd import hip
+
+    print(f"residual epilogue m={m} n={n} k={k}", flush=True)
+    x, w_raw, scale = _random_case(m, n, k, seed=3 * m + n + k)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    resid = torch.randn(m, n, device=gpu).to(torch.bfloat16)
+    want = resid + hip.fp8_linear(xt, wt, st)
+    assert torch.equal(hip.fp8_linear_residual(xt, wt, st, resid), want)
+    in_place = resid.clone()
+    got, ws = _fused_call(nat, xt, [wt], [st], nat.FP8_EPILOGUE_RESIDUAL, residual=in_place, out=in_place)
+    torch.cuda.synchronize()
+    assert ws > 0 and torch.equal(got, want)
+    xe, we, se = _exact_case(m, n, k, seed=m + n)
+    re = np.random.default_rng(m).integers(-8, 9, size=(m, n)).astype(np.float32)
+    oracle = ofp8.fp8_linear_residual(xe, we, se, re)
+    got = hip.fp8_linear_residual(*_to_device(xe, we, se, gpu), torch.from_numpy(re).to(torch.bfloat16).to(gpu))
+    assert _same_values(got, torch.from_numpy(oracle).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("m,n,k", _FUSED_SHAPES)
+def test_swiglu_epilogue_matches_the_oracle_and_the_separate_operations(gpu, default_config, m, n, k):
+    """bf16(bf16(silu(g)) * u) against the stepwise-rounded float64 oracle on exact products, and against
+    torch's F.silu(g) * u on the grouped outputs for random weights: within one bf16 ulp everywhere, equal
+    almost everywhere (only silu's float32 rounding may differ)."""
+    from flextensor_amd import hip
+
+    print(f"swiglu epilogue m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m * 11 + n + k)
+    for exact in (True, False):
+        if exact:
+            xg, wg, sg = _exact_case(m, n, k, seed=m + 2 * n + k)
+            _, wu, su = _exact_case(m, n, k, seed=m + 3 * n + k)
+            want = torch.from_numpy(ofp8.fp8_linear_swiglu(xg, wg, sg, wu, su))
+        else:
+            xg, wg, sg = _random_case(m, n, k, seed=int(rng.integers(1 << 30)))
+            _, wu, su = _random_case(m, n, k, seed=int(rng.integers(1 << 30)))
+        xt, wgt, sgt = _to_device(xg, wg, sg, gpu)
+        _, wut, sut = _to_device(xg, wu, su, gpu)
+        got = hip.fp8_linear_swiglu(xt, wgt, sgt, wut, sut).double().cpu()
+        if not exact:
+            g, u = hip.fp8_linear_group(xt, [wgt, wut], [sgt, sut])
+            want = (torch.nn.functional.silu(g) * u).double().cpu()
+        ulp = want.abs() * 2.0 ** -7 + 1e-30
+        assert bool(((got - want).abs() <= ulp).all()), f"exact={exact}"
+        assert float((got == want).double().mean()) > 0.99, f"exact={exact}"
+
+
+def test_fused_epilogues_with_one_k_slice_and_in_graphs(gpu, default_config):
+    """A call with one K slice still goes through the partials (the reduce applies the epilogue), and a
+    captured graph of fused calls replays to the eager results."""
+    from flextensor_amd import hip
+
+    x, wg, sg = _random_case(4, 64, 256, seed=1)
+    _, wu, su = _random_case(4, 64, 256, seed=2)
+    xt, wgt, sgt = _to_device(x, wg, sg, gpu)
+    _, wut, sut = _to_device(x, wu, su, gpu)
+    resid = torch.randn(4, 64, device=gpu).to(torch.bfloat16)
+    assert hip.fp8_linear_fused_workspace_bytes(4, [64], 256, 2) > 0
+    assert torch.equal(hip.fp8_linear_residual(xt, wgt, sgt, resid), resid + hip.fp8_linear(xt, wgt, sgt))
+    eager = (hip.fp8_linear_swiglu(xt, wgt, sgt, wut, sut), hip.fp8_linear_residual(xt, wgt, sgt, resid))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        hip.fp8_linear_swiglu(xt, wgt, sgt, wut, sut)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            static = (hip.fp8_linear_swiglu(xt, wgt, sgt, wut, sut), hip.fp8_linear_residual(xt, wgt, sgt, resid))
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static[0], eager[0]) and torch.equal(static[1], eager[1])
+    del graph
+
+
+def test_fused_rejects_bad_arguments(gpu, default_config):
+    import ctypes
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import hip
+
+    x, w_raw, scale = _random_case(8, 64, 256, seed=4)
+    xt, wt, st = _to_device(x, w_raw, scale, gpu)
+    resid = torch.zeros(8, 64, dtype=torch.bfloat16, device=gpu)
+    n2 = (ctypes.c_int64 * 2)(64, 64)
+    b = ctypes.c_size_t(0)
+    cases = {
+        "SwiGLU with one matrix": (8, [64], nat.FP8_EPILOGUE_SWIGLU, nat.FTX_ERR_INVALID),
+        "SwiGLU with unequal n": (8, [64, 32], nat.FP8_EPILOGUE_SWIGLU, nat.FTX_ERR_INVALID),
+        "residual with two matrices": (8, [64, 64], nat.FP8_EPILOGUE_RESIDUAL, nat.FTX_ERR_INVALID),
+        "unknown epilogue": (8, [64], 7, nat.FTX_ERR_INVALID),
+        "prefill rows": (65, [64], nat.FP8_EPILOGUE_RESIDUAL, nat.FTX_ERR_UNSUPPORTED),
+    }
+    for case, (m, ns, epi, code) in cases.items():
+        arr = (ctypes.c_int64 * len(ns))(*ns)
+        rc = nat.lib().ftx_fp8_linear_fused_workspace(m, ctypes.cast(arr, ctypes.c_void_p), len(ns), 256, epi,
+                                                      ctypes.byref(b))
+        assert rc == code, case
+    del n2
+    with pytest.raises(nat.FtxError, match="needs a residual"):
+        _fused_call(nat, xt, [wt], [st], nat.FP8_EPILOGUE_RESIDUAL, residual=None)
+    with pytest.raises(nat.FtxError, match="not device memory"):
+        _fused_call(nat, xt, [wt], [st], nat.FP8_EPILOGUE_RESIDUAL, residual=resid.cpu())
+    with pytest.raises(ValueError, match="residual must be"):
+        hip.fp8_linear_residual(xt, wt, st, resid[:, :32])
+    with pytest.raises(ValueError, match="decode kernel"):
+        hip.fp8_linear_residual(torch.zeros(65, 256, dtype=torch.bfloat16, device=gpu), wt, st,
+                                torch.zeros(65, 64, dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError, match="differ in shape"):
+        hip.fp8_linear_swiglu(xt, wt, st, wt[:32].contiguous(), st[:32].contiguous())
+    torch.cuda.synchronize()
+
+
+def test_decoder_layer_fused_path_against_the_separate_operations(gpu, default_config, monkeypatch):
+    """A 70B-shaped fp8 decoder layer at batch 8, one decode token: with the fused SwiGLU and residual
+    epilogues, and with each fold switched off. Folding only the residual adds changes no bit; folding
+    SwiGLU changes at most the float32 rounding of silu, so the layer stays within 1e-2 of the separate
+    operations. Hooks on a projection (as the unit checks use) make the layer call that module instead."""
+    from flextensor_amd import workloads as W
+
+    s = W.LlamaShape(**{**W.LLAMA_70B_FP8.__dict__, "n_layers": 1, "vocab": 64, "max_seq": 16})
+    model = W.build_llama(s, seed=3, init_device="cuda").to(gpu)
+    model.init_cache(8, 8, gpu)
+    layer = model.layers[0]
+    x = (torch.randn(8, 1, s.hidden, device=gpu) * 0.5).to(torch.bfloat16)
+
+    def run():
+        with torch.no_grad():
+            return layer(x, 3, model.rope_cos, model.rope_sin, model.cache_k[0], model.cache_v[0])
+
+    calls = {"swiglu": 0, "residual": 0}
+    real_sw, real_res = W.fp8_swiglu, W.fp8_residual
+    monkeypatch.setattr(W, "fp8_swiglu", lambda *a: calls.__setitem__("swiglu", calls["swiglu"] + 1) or real_sw(*a))
+    monkeypatch.setattr(W, "fp8_residual",
+                        lambda *a: calls.__setitem__("residual", calls["residual"] + 1) or real_res(*a))
+    fused = run()
+    assert calls == {"swiglu": 1, "residual": 2}
+    monkeypatch.setattr(W, "fp8_residual", lambda *a: None)
+    no_residual = run()
+    monkeypatch.setattr(W, "fp8_swiglu", lambda *a: None)
+    separate = run()
+    monkeypatch.setattr(W, "fp8_swiglu", real_sw)
+    monkeypatch.setattr(W, "fp8_residual", real_res)
+    assert torch.equal(no_residual, fused)  # the residual folds change no bit
+    assert float((fused.double() - separate.double()).norm() / separate.double().norm()) < 1e-2
+    seen = []
+    handle = layer.down.register_forward_hook(lambda mod, args, out: seen.append(out))
+    hooked = run()
+    handle.remove()
+    assert len(seen) == 1 and torch.equal(hooked, fused)
+    del model
+    torch.cuda.empty_cache()

@@ -219,3 +219,62 @@ def test_fp8_group_falls_back_when_the_group_reaches_the_launch_limit(monkeypatc
     assert gate.kernel_eligible(long_prefill) and up.kernel_eligible(long_prefill)
     assert W.fp8_group(long_prefill, [gate, up]) is None and calls == []
     assert W.fp8_group(_Input(32768, 16), [gate, up]) is not None and calls == [2]  # 32768 * 57344 < 2^31
+
+
+def test_grouped_and_fused_calls_only_for_modules_that_run_nothing_else(monkeypatch):
+    """The decoder computes a projection from its weights directly (grouped q/k/v and gate/up, the fused
+    SwiGLU and residual epilogues) only when calling the module would run its class's forward and nothing
+    else. An offload unit's trap (a forward set on the instance) or a hook sends the call through the module,
+    so a streamed projection is loaded before it is read and hooks see their calls."""
+    class _Input(_FakeGpuInput):
+        def reshape(self, *shape):
+            return self
+
+        def numel(self) -> int:
+            return self.shape[0] * self.shape[1]
+
+    calls = []
+    monkeypatch.setattr(W.hip, "fp8_linear_group", lambda x, ws, ss: calls.append("group") or
+                        [torch.empty(x.shape[0], w.shape[0], device="meta") for w in ws])
+    monkeypatch.setattr(W.hip, "fp8_linear_swiglu", lambda x, wg, sg, wu, su: calls.append("swiglu") or
+                        torch.empty(x.shape[0], wg.shape[0], device="meta"))
+    gate, up, down = W.Fp8Linear(16, 32), W.Fp8Linear(16, 32), W.Fp8Linear(32, 16)
+    x = _Input(8, 16)
+    assert W.fp8_group(x, [gate, up]) is not None and W.fp8_swiglu(x, gate, up) is not None
+    assert calls == ["group", "swiglu"]
+    calls.clear()
+    up.forward = lambda t: t  # what an offload manager's trap looks like: a forward on the instance
+    assert W.fp8_group(x, [gate, up]) is None and W.fp8_swiglu(x, gate, up) is None
+    del up.forward
+    handle = gate.register_forward_pre_hook(lambda mod, args: None)
+    assert W.fp8_group(x, [gate, up]) is None and W.fp8_swiglu(x, gate, up) is None
+    handle.remove()
+    handle = torch.nn.modules.module.register_module_forward_hook(lambda mod, args, out: None)
+    assert W.fp8_group(x, [gate, up]) is None
+    handle.remove()
+    assert calls == []
+    # prefill rows take no fused epilogue (the decode kernel's reduce applies them), and unequal gate/up
+    # shapes take no SwiGLU epilogue
+    assert W.fp8_swiglu(_Input(65, 16), gate, up) is None
+    assert W.fp8_swiglu(x, gate, W.Fp8Linear(16, 48)) is None
+    resid = torch.empty(8, 16, dtype=torch.bfloat16, device="meta")
+    assert W.fp8_residual(_Input(65, 32), down, torch.empty(65, 16, dtype=torch.bfloat16, device="meta")) is None
+    assert W.fp8_residual(_Input(8, 32), down, resid.float()) is None
+    assert calls == []
+
+
+def test_decoder_layer_keeps_its_numerics_on_the_cpu():
+    """Moving the residual adds into the attention call and the MLP step changes no bit on the host path:
+    x + o and residual + o are the same bf16 add."""
+    s = W.LlamaShape(n_layers=1, hidden=64, n_heads=4, n_kv_heads=2, head_dim=16, inter=96, vocab=32, max_seq=8)
+    model = W.build_llama(s, seed=0)
+    model.init_cache(2, 8, torch.device("cpu"))
+    layer = model.layers[0]
+    x = torch.randn(2, 3, 64).to(torch.bfloat16)
+    with torch.no_grad():
+        got = layer(x, 0, model.rope_cos, model.rope_sin, model.cache_k[0], model.cache_v[0])
+        model.init_cache(2, 8, torch.device("cpu"))
+        h = x + layer.attn(layer.attn_norm(x), 0, model.rope_cos, model.rope_sin, model.cache_k[0], model.cache_v[0])
+        n2 = layer.mlp_norm(h)
+        want = h + layer.down(torch.nn.functional.silu(layer.gate(n2)) * layer.up(n2))
+    assert torch.equal(got, want)
