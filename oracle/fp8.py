@@ -43,6 +43,9 @@ def fp8_linear(x: np.ndarray, w_raw: np.ndarray, scale: np.ndarray) -> np.ndarra
     return (np.asarray(x, dtype=np.float64) @ w.T) * np.asarray(scale, dtype=np.float64)[None, :]
 
 
+FLOAT32_MAX = float(np.finfo(np.float32).max)
+
+
 def bf16_round(a) -> np.ndarray:
     """float64 values rounded to the nearest bfloat16 (ties to even), the rounding of every bf16 tensor
     operation: to float32 first (exact for float32 inputs), then the low 16 bits of the float32 pattern
@@ -59,10 +62,15 @@ def fp8_linear_swiglu(x: np.ndarray, wg_raw: np.ndarray, sg: np.ndarray, wu_raw:
                       su: np.ndarray) -> np.ndarray:
     """``F.silu(g) * u`` of two bf16 fp8 linears, each operation rounded to bf16 as the separate PyTorch
     operations round it: g = bf16(gate), u = bf16(up), a = bf16(g / (1 + exp(-g))), then bf16(a * u).
-    The arithmetic between roundings is exact float64."""
+    The arithmetic between roundings is float64, with one float32 trait kept: PyTorch evaluates a bf16
+    silu in float32, where exp(-g) overflows to infinity once it passes float32's largest value (g below
+    about -88.72), and the quotient is then a zero of g's sign."""
     g = bf16_round(fp8_linear(x, wg_raw, sg))
     u = bf16_round(fp8_linear(x, wu_raw, su))
-    act = bf16_round(g / (1.0 + np.exp(-g)))
+    with np.errstate(over="ignore"):
+        e = np.exp(-g)
+    e = np.where(e > FLOAT32_MAX, np.inf, e)
+    act = bf16_round(g / (1.0 + e))
     return bf16_round(act * u)
 
 

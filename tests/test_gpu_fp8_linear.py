@@ -580,11 +580,21 @@ def test_residual_epilogue_is_the_linear_then_the_bf16_add(gpu, default_config, 
     assert _same_values(got, torch.from_numpy(oracle).to(torch.bfloat16))
 
 
+def _silu_near_a_bf16_midpoint(g: torch.Tensor) -> torch.Tensor:
+    """Where silu(g), in float64, lies within 2^-10 of a bf16 ulp from a rounding midpoint: the only places
+    where two float32 evaluations of silu (about 2^-14 of a bf16 ulp apart) may round to different bf16
+    values. ``g`` holds the bf16 gate outputs."""
+    a = (g.double() / (1.0 + torch.exp(-g.double()))).abs()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(a.clamp_min(1e-300))) - 7)
+    return ((a / ulp) % 1.0 - 0.5).abs() < 2.0 ** -10
+
+
 @pytest.mark.parametrize("m,n,k", _FUSED_SHAPES)
 def test_swiglu_epilogue_matches_the_oracle_and_the_separate_operations(gpu, default_config, m, n, k):
     """bf16(bf16(silu(g)) * u) against the stepwise-rounded float64 oracle on exact products, and against
-    torch's F.silu(g) * u on the grouped outputs for random weights: within one bf16 ulp everywhere, equal
-    almost everywhere (only silu's float32 rounding may differ)."""
+    torch's F.silu(g) * u on the grouped outputs for random weights. Every output is within one bf16 ulp,
+    and any that differs has its silu(g) next to a bf16 rounding midpoint, where float32 evaluations of
+    silu may round either way; everywhere else the bits are equal."""
     from flextensor_amd import hip
 
     print(f"swiglu epilogue m={m} n={n} k={k}", flush=True)
@@ -593,19 +603,27 @@ def test_swiglu_epilogue_matches_the_oracle_and_the_separate_operations(gpu, def
         if exact:
             xg, wg, sg = _exact_case(m, n, k, seed=m + 2 * n + k)
             _, wu, su = _exact_case(m, n, k, seed=m + 3 * n + k)
-            want = torch.from_numpy(ofp8.fp8_linear_swiglu(xg, wg, sg, wu, su))
         else:
             xg, wg, sg = _random_case(m, n, k, seed=int(rng.integers(1 << 30)))
             _, wu, su = _random_case(m, n, k, seed=int(rng.integers(1 << 30)))
         xt, wgt, sgt = _to_device(xg, wg, sg, gpu)
         _, wut, sut = _to_device(xg, wu, su, gpu)
         got = hip.fp8_linear_swiglu(xt, wgt, sgt, wut, sut).double().cpu()
-        if not exact:
-            g, u = hip.fp8_linear_group(xt, [wgt, wut], [sgt, sut])
+        g, u = hip.fp8_linear_group(xt, [wgt, wut], [sgt, sut])
+        if exact:
+            xf = xt.float().cpu().numpy()
+            want = torch.from_numpy(ofp8.fp8_linear_swiglu(xf, wg, sgt.float().cpu().numpy(), wu,
+                                                           sut.float().cpu().numpy()))
+            assert _same_values(g, torch.from_numpy(ofp8.fp8_linear(xf, wg, sgt.float().cpu().numpy())).to(
+                torch.bfloat16))  # the gate itself is exact
+        else:
             want = (torch.nn.functional.silu(g) * u).double().cpu()
         ulp = want.abs() * 2.0 ** -7 + 1e-30
         assert bool(((got - want).abs() <= ulp).all()), f"exact={exact}"
-        assert float((got == want).double().mean()) > 0.99, f"exact={exact}"
+        differ = got != want
+        near = _silu_near_a_bf16_midpoint(g.cpu())
+        assert not bool((differ & ~near).any()), f"exact={exact}: {int(differ.sum())} differ, " \
+                                                  f"{int((differ & ~near).sum())} away from a midpoint"
 
 
 def test_fused_epilogues_with_one_k_slice_and_in_graphs(gpu, default_config):
