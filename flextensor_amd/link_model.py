@@ -232,8 +232,9 @@ def choose_copy_policy(sdma: CopyCurve, kernel: CopyCurve, split: CopyCurve | No
 
 # A pass whose profiled compute takes less than this share of the time its
 # streamed units need on the link is link-bound: the compute stream waits on
-# the link whatever runs beside it. Beside the zero-copy kernel, the decode's
-# HBM-bound GEMVs ran 2.5 times longer; under 0.4 they stay hidden even then.
+# the link whatever runs beside it. The share leaves room for compute that
+# runs slower beside the zero-copy kernel: the decode's HBM-bound GEMVs once
+# ran 2.5 times longer there, before small copy grids reserved their CUs.
 LINK_BOUND_COMPUTE_SHARE = 0.4
 # Zero-copy kernel workgroups for the ring copies of a link-bound pass. Eight
 # hold the link at its peak (57.3 GB/s for 512 MiB, against 57.1 at 64) and
