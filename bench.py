@@ -1089,6 +1089,80 @@ def traffic_probe(args) -> int:
     return 0
 
 
+def copy_behind_fp8(reps: int = 5) -> dict:
+    """How long a reserved-CU ring copy waits when it is queued behind a running LDS-heavy fp8 grid.
+
+    A copy grid of at most 16 workgroups asks for each CU's whole LDS, so it
+    cannot start on a CU where a workgroup that uses LDS is resident. Here the
+    grouped gate/up projections of a 70B-shape layer run on the compute
+    stream, once at 512 rows (the prefill kernel) and once at 8 rows (the
+    decode kernel and its reduce). A 64 MiB zero-copy copy at 8 workgroups is
+    queued on the transfer stream as the GEMM starts. Device timestamps
+    (``ftx_timestamp``) bracket both; medians of ``reps``. The copy's start
+    delay is its bracketed time beside the GEMM minus its time alone.
+    """
+    import torch
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import hip
+    from flextensor_amd import link_model as L
+    from flextensor_amd import workloads as W
+
+    dev = torch.device("cuda", 0)
+    comp, xs = hip.current_stream(dev), hip.transfer_stream(dev)
+    s = W.LLAMA_70B_FP8
+    gen = torch.Generator(device=dev).manual_seed(5)
+    ws = [(torch.randn(s.inter, s.hidden, device=dev, generator=gen) * 64).clamp(-448, 448).to(torch.float8_e4m3fn)
+          for _ in range(2)]
+    scs = [(torch.rand(s.inter, device=dev, generator=gen) / 448).to(torch.bfloat16) for _ in range(2)]
+    n = 64 * MiB
+    arena = hip.HostArena(n)
+    arena.tensor.random_(0, 256)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    policy = nat.copy_policy(0, 2**63 - 1, 1, L.RING_KERNEL_GRID)
+
+    def copy(stream):
+        nat.copy_h2d(dst.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, stream.handle, policy)
+
+    out: dict = {"copy_bytes": n, "copy_workgroups": L.RING_KERNEL_GRID}
+    for label, rows in (("prefill_gate_up_512_rows", 512), ("decode_gate_up_8_rows", 8)):
+        x = torch.randn(rows, s.hidden, device=dev, generator=gen).to(torch.bfloat16)
+        hip.fp8_linear_group(x, ws, scs)  # warm-up, and the workspace shape is cached
+        copy(xs)
+        torch.cuda.synchronize()
+        rec: dict[str, list[float]] = {"gemm_alone_us": [], "copy_alone_us": [], "gemm_beside_copy_us": [],
+                                       "copy_behind_gemm_us": []}
+        for _ in range(reps):
+            clock = hip.DeviceClock(8, dev)
+            e = [clock.event() for _ in range(8)]
+            e[0].record(comp)
+            hip.fp8_linear_group(x, ws, scs)
+            e[1].record(comp)
+            torch.cuda.synchronize()
+            e[2].record(xs)
+            copy(xs)
+            e[3].record(xs)
+            torch.cuda.synchronize()
+            e[4].record(comp)
+            started = comp.record_event()  # reached once the GEMM is dispatched
+            hip.fp8_linear_group(x, ws, scs)
+            e[5].record(comp)
+            xs.wait_event(started)
+            e[6].record(xs)
+            copy(xs)
+            e[7].record(xs)
+            torch.cuda.synchronize()
+            clock.refresh()
+            for key, (a, b) in (("gemm_alone_us", (0, 1)), ("copy_alone_us", (2, 3)),
+                                ("gemm_beside_copy_us", (4, 5)), ("copy_behind_gemm_us", (6, 7))):
+                rec[key].append(1e3 * e[a].elapsed_time(e[b]))
+        row = {k: round(sorted(v)[len(v) // 2], 1) for k, v in rec.items()}
+        row["copy_start_delay_us"] = round(row["copy_behind_gemm_us"] - row["copy_alone_us"], 1)
+        out[label] = row
+        _log(f"copy behind fp8 {label}: {row}")
+    return out
+
+
 def engine_contention() -> dict:
     """How each copy engine shares the GPU with an HBM-bound kernel.
 
@@ -1174,6 +1248,9 @@ def engine_contention() -> dict:
     plan.close()
     out["scatter_payload_bytes"] = payload
     out["scatter_pieces"] = len(descs)
+    del dst, src, arena
+    torch.cuda.empty_cache()
+    out["copy_queued_behind_fp8"] = copy_behind_fp8()
     return out
 
 
