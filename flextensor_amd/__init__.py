@@ -38,6 +38,7 @@ from .manager import (  # noqa: E402
     offload_units,
     pause_profiling,
     release,
+    request_strategy_replan,
     reset_offload_timing,
     resident_units,
     resume_profiling,
@@ -48,6 +49,7 @@ from .manager import (  # noqa: E402
     update_state,
 )
 from .profile import TensorManagerState, load_state, save_state  # noqa: E402
+from .replan import StrategyReplanStatus  # noqa: E402
 from .shared_offload import (  # noqa: E402
     SharedOffloadSession,
     ShmCoordinatorError,
@@ -70,6 +72,7 @@ __all__ = [
     "ShmCoordinatorError",
     "ShmCreatorDiedError",
     "ShmCreatorFailedError",
+    "StrategyReplanStatus",
     "TensorManagerState",
     "clear_profiling_durations",
     "collect_offload_timing",
@@ -90,6 +93,7 @@ __all__ = [
     "offload_units",
     "pause_profiling",
     "release",
+    "request_strategy_replan",
     "reset_offload_timing",
     "resident_units",
     "resume_profiling",

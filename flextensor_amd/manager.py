@@ -72,6 +72,8 @@ from .planner import (
 )
 from .prefetch_policy import PiecewisePrefetchPolicy
 from .profile import TensorManagerState, load_state, save_state
+from .replan import (REPLAN_MEASURE_PASSES, REPLAN_WARMUP_PASSES, StrategyReplanState, StrategyReplanStatus,
+                     measured_compute, replanned_link)
 from .scatter import upload_tensors
 from .selection import parameter_filter, select_offload_units
 from .timing import OffloadTimingCollector, OffloadTimingReport
@@ -451,6 +453,7 @@ class OffloadManager:
         self._pinner: HostPinner | None = None
         self.memory_transfer_stats: dict[int, float] = {}
         self.link: LinkMeasurement | None = None  # the measured host link and the copy policy it chose
+        self._reset_replan()
         self.skip_discovery_honored: bool | None = None  # None until offload() decides
         self._discovery_passes = 0
         self._reset_manual()
@@ -621,6 +624,7 @@ class OffloadManager:
         self._release_pins()
         self.loader = self.controller = self.plan = self.timing = None
         self.link = None
+        self._reset_replan()
         self.model = None
         self.units, self._patched, self._hooks, self.order = [], [], [], []
         self._seen_this_pass, self._pass_done, self._events = [], [], {}
@@ -965,6 +969,130 @@ class OffloadManager:
         """
         self._after_forward()
 
+    # ---- re-measuring the plan in flight (offload_manager.py:667-720, 1294-1325) ----------------------------
+
+    def _reset_replan(self) -> None:
+        self._replan: dict[str, Any] | None = None  # the armed tail: passes left, its collector, its start
+        self._replan_state: StrategyReplanState = "idle"
+        self._replan_applied: bool | None = None
+
+    def _strategy_replan_unavailable_reason(self, manual: bool = False) -> str | None:
+        """Why a replan request cannot start now, or None when it can."""
+        if self.phase != OffloadPhase.INFERENCE:
+            return (f"the offload is in {self.phase.value}; run iters_before_inference forwards to reach "
+                    "inference first")
+        if self._replan is not None:
+            return "a replan is already in flight; run the passes the request returned"
+        if self._replan_state == "failed":
+            return "an earlier replan failed, so inference is already unsafe; release the model and offload it again"
+        if self.controller is None or self.loader is None:
+            return "nothing streams, so there is nothing to re-measure"
+        if hip.is_capturing():
+            return "a graph is being captured"
+        if manual and not (self.timing is not None and self.timing.enabled and self.timing.graph_replay):
+            return ("manual_update_state=True measures graph replays, which needs offload_timing='cuda_graph' "
+                    "when the graph is captured")
+        return None
+
+    @property
+    def strategy_replan_status(self) -> StrategyReplanStatus:
+        """Passive snapshot of the replan; reading it never starts or advances one."""
+        applied = self._replan_applied if self._replan_state in ("done", "failed") else None
+        return StrategyReplanStatus(self._replan_state, self._strategy_replan_unavailable_reason() is None, applied)
+
+    def _new_replan_collector(self) -> OffloadTimingCollector:
+        return OffloadTimingCollector(list(self.order), log_every=0)
+
+    def request_strategy_replan(self, *, manual_update_state: bool = False) -> int:
+        """Re-measure the units' compute under the current runtime and rebuild what depends on it.
+
+        What depends on it here is the ring's copy engine: a pass computing
+        far less than its streamed units take on the link copies every slot
+        with the zero-copy kernel, any other keeps the per-size policy. Call
+        it after the compute changed under a running offload (a compiled
+        forward, a captured graph, other batch shapes).
+
+        * ``manual_update_state=False``: run the returned number of forwards;
+          the post-forward hook advances the replan.
+        * ``manual_update_state=True``: for graph replays, which run no hooks.
+          Capture with ``offload_timing="cuda_graph"``, then call
+          ``graph.replay()`` and :meth:`update_state` the returned number of
+          times; recapture afterwards, since the captured copies keep the old
+          engine.
+
+        Returns the passes to run (a warm-up pass and the measured ones), or 0
+        with a warning when a replan cannot start now
+        (:attr:`strategy_replan_status`.can_request).
+        """
+        self._check_thread()
+        reason = self._strategy_replan_unavailable_reason(manual_update_state)
+        if reason is not None:
+            LOGGER.warning("offload %r: request_strategy_replan() ignored - %s", self.name, reason)
+            return 0
+        passes = REPLAN_WARMUP_PASSES + REPLAN_MEASURE_PASSES
+        if manual_update_state:
+            self._replan = {"left": passes, "manual": True, "start": len(self.timing.snapshots)}
+        else:
+            # a collector of its own on the loader for these passes: they are timed for the replan and are not
+            # reported by collect_offload_timing()
+            collector = self._new_replan_collector()
+            self._replan = {"left": passes, "manual": False, "collector": collector,
+                            "kept": self.loader.offload_timing_collector}
+            self.loader.offload_timing_collector = collector
+        self._replan_state, self._replan_applied = "in_progress", None
+        LOGGER.info("offload %r: replan armed; run %d passes", self.name, passes)
+        return passes
+
+    def _advance_replan(self) -> None:
+        tail = self._replan
+        if tail is None:
+            return
+        if tail["manual"]:
+            self.timing.flush()  # publishes the latest replay's times
+        tail["left"] -= 1
+        if tail["left"] > 0:
+            return
+        self._replan = None
+        try:
+            if tail["manual"]:
+                passes = list(self.timing.snapshots[tail["start"]:])
+            else:
+                try:
+                    passes = list(tail["collector"].report().passes)
+                finally:
+                    self.loader.offload_timing_collector = tail["kept"]
+            self._rebuild_from(passes[-REPLAN_MEASURE_PASSES:])
+        except Exception:
+            self._replan_state, self._replan_applied = "failed", False
+            LOGGER.exception("offload %r: the replan failed; inference is unsafe until the model is offloaded again",
+                             self.name)
+            raise
+
+    def _rebuild_from(self, passes: list) -> None:
+        """New unit durations from the measured passes, and the ring's copy policy re-decided from them."""
+        measured = measured_compute(passes, self.order)
+        self._replan_state = "done"
+        if not measured:
+            self._replan_applied = False
+            LOGGER.warning("offload %r: the replan measured no unit; the plan is kept", self.name)
+            return
+        for label, ms in measured.items():
+            self.durations[label] = [ms]
+        plan = self.plan
+        if self.link is None or self.controller is None or plan is None:
+            # no link measurement (link_benchmark=False or a pinned copy engine): nothing decided from the times
+            self._replan_applied = False
+            LOGGER.info("offload %r: replan measured %d units; the copy engine does not depend on them", self.name,
+                        len(measured))
+            return
+        compute_ms = sum(self._duration(x) for x in [*plan.streamed, *plan.resident])
+        link = replanned_link(self.link, compute_ms, [self._unit(x).nbytes for x in plan.streamed])
+        self.link = link
+        self.memory_transfer_stats = link.memory_transfer_stats()
+        self.controller.copy_policy = link.native_policy()
+        self._replan_applied = True
+        LOGGER.info("offload %r: replanned: %s", self.name, link.describe())
+
     def update_offload_timing(self) -> bool:
         """Store the current timing pass (offload_manager.py:3061-3072); True when stored or timing is off."""
         if self.timing is not None and self.timing.enabled:
@@ -1050,6 +1178,7 @@ class OffloadManager:
             self.skip_discovery_honored = None
             self.loader = self.controller = self.plan = None
             self.link = None
+            self._reset_replan()
             self._pass_done = []
             self.model = None
             self.units, self._patched, self._hooks = [], [], []
@@ -1395,6 +1524,7 @@ class OffloadManager:
 
                 self._pass_done.append(HipEvent().record(current_stream(self.device)))
                 del self._pass_done[: -self.config.max_inflight_passes]
+            self._advance_replan()
             return
         if self.phase == OffloadPhase.PROFILING and self._suspend_count:
             # a suspended profiling pass records no durations and does not use up profiling_iters
@@ -1850,6 +1980,11 @@ def resume_profiling(name: str = DEFAULT_MANAGER_NAME) -> None:
 def pause_profiling(name: str = DEFAULT_MANAGER_NAME) -> Iterator[None]:
     with get_offload_manager(name).pause_profiling():
         yield
+
+
+def request_strategy_replan(name: str = DEFAULT_MANAGER_NAME, *, manual_update_state: bool = False) -> int:
+    """:meth:`OffloadManager.request_strategy_replan` of the named manager (offload_manager.py:3091-3107)."""
+    return get_offload_manager(name).request_strategy_replan(manual_update_state=manual_update_state)
 
 
 def update_state(name: str = DEFAULT_MANAGER_NAME) -> None:

@@ -72,3 +72,51 @@ def test_link_bound_and_compute_bound_managers_stream_side_by_side(gpu):
         for mgr in managers.values():
             mgr.release(preserve_model=False)
         torch.cuda.empty_cache()
+
+
+def test_a_replan_follows_the_workload_when_the_batch_changes(gpu):
+    """``request_strategy_replan`` (offload_manager.py:1294-1325) on the GPU. A stack profiled at 16 rows
+    is link-bound and copies its ring with the zero-copy kernel. Fed 32768-row batches it computes for
+    longer than its transfers, and a replan measured on those passes moves the ring back to the measured
+    per-size policy (SDMA for the 180 MB layers). Back at 16 rows, a second replan returns to the kernel.
+    Every pass is bitwise equal to the resident forward."""
+    import flextensor_amd as ft
+
+    nat.load()
+    default = nat.get_copy_policy()
+    model = W.build_mlp_stack(8, 4096, 11008, seed=0)
+    resident = W.build_mlp_stack(8, 4096, 11008, seed=0).to(gpu)
+    small, large = (W.mlp_input(m, 4096, seed=0).to(gpu) for m in (16, 32768))
+    with torch.no_grad():
+        want = {16: resident(small), 32768: resident(large)}
+    del resident
+    torch.cuda.empty_cache()
+    mgr = OffloadManager("replan-gpu")
+    mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                                     profiling_iters=1))
+    try:
+        assert mgr.strategy_replan_status == ft.StrategyReplanStatus("idle", False, None)
+        with torch.no_grad():
+            for _ in range(3):  # discovery, profiling at 16 rows, one streamed pass
+                got = model(small)
+        assert torch.equal(got, want[16])
+        assert mgr.link.link_bound and mgr.controller.copy_policy.kernel_grid == L.RING_KERNEL_GRID
+        assert mgr.strategy_replan_status.can_request
+        for rows, x, link_bound in ((32768, large, False), (16, small, True)):
+            print(f"replan at {rows} rows", flush=True)
+            n = mgr.request_strategy_replan()
+            assert n > 0 and mgr.strategy_replan_status.state == "in_progress"
+            with torch.no_grad():
+                for _ in range(n):
+                    got = model(x)
+                    assert torch.equal(got, want[rows])
+            status = mgr.strategy_replan_status
+            assert status == ft.StrategyReplanStatus("done", True, True), status
+            assert mgr.link.link_bound == link_bound and mgr.link.source == "replan", mgr.link.describe()
+            assert mgr.controller.copy_policy == mgr.link.native_policy()
+            with torch.no_grad():
+                assert torch.equal(model(x), want[rows])  # streaming under the new policy
+        assert nat.get_copy_policy() == default
+    finally:
+        mgr.release(preserve_model=False)
+        torch.cuda.empty_cache()

@@ -326,3 +326,52 @@ def test_device_only_event_orders_a_copy_before_its_consumer(gpu, mode):
         got = dst.clone()  # on the compute stream, after the wait
         torch.cuda.synchronize()
         assert np.array_equal(got.cpu().numpy(), data)
+
+
+def test_shutdown_drains_queued_copies_and_refuses_more_work(gpu):
+    """``ftx_shutdown`` on a GPU, in a child process (a shut-down library stays refused for the rest of its
+    process): copies queued on every engine (SDMA, SDMA split over copy streams, the zero-copy kernel, the
+    staged engine with its host threads and staging buffers) have all landed when it returns, later work
+    is refused with FTX_ERR_UNSUPPORTED, torch keeps working, and the process exits cleanly."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    code = (
+        "import torch\n"
+        "import flextensor_amd._native as nat\n"
+        "from flextensor_amd.hip import HostArena, current_stream\n"
+        "torch.cuda.set_device(0)\n"
+        "nat.load()\n"
+        "dev = torch.device('cuda', 0)\n"
+        "s = current_stream(dev)\n"
+        "n = 96 << 20\n"
+        "arena = HostArena(n)\n"
+        "arena.tensor.random_(0, 256)\n"
+        "pageable = torch.randint(0, 256, (n,), dtype=torch.uint8)\n"
+        "split = nat.copy_policy(1 << 20, 1 << 20, 4, 0)\n"
+        "outs = [torch.zeros(n, dtype=torch.uint8, device=dev) for _ in range(4)]\n"
+        "torch.cuda.synchronize()\n"
+        "nat.copy_h2d(outs[0].data_ptr(), arena.ptr, n, nat.COPY_SDMA, s.handle)\n"
+        "nat.copy_h2d(outs[1].data_ptr(), arena.ptr, n, nat.COPY_SDMA, s.handle, split)\n"
+        "nat.copy_h2d(outs[2].data_ptr(), arena.ptr, n, nat.COPY_KERNEL, s.handle)\n"
+        "nat.copy_h2d(outs[3].data_ptr(), pageable.data_ptr(), n, nat.COPY_STAGED, s.handle)\n"
+        "nat.shutdown()\n"
+        "assert s.query(), 'work still queued after ftx_shutdown'\n"
+        "host = arena.tensor.clone()\n"
+        "assert all(torch.equal(o.cpu(), host) for o in outs[:3]) and torch.equal(outs[3].cpu(), pageable)\n"
+        "try:\n"
+        "    nat.copy_h2d(outs[0].data_ptr(), arena.ptr, n, nat.COPY_SDMA, s.handle)\n"
+        "except nat.FtxError as e:\n"
+        "    assert e.code == nat.FTX_ERR_UNSUPPORTED and 'shut down' in str(e)\n"
+        "else:\n"
+        "    raise SystemExit('a copy ran after ftx_shutdown')\n"
+        "nat.shutdown()\n"
+        "assert float(torch.ones(4, device=dev).sum()) == 4.0\n"
+        "print('drained', flush=True)\n"
+    )
+    print("shutdown on the GPU: child process", flush=True)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=240,
+                         cwd=str(Path(__file__).resolve().parents[1]))
+    assert out.returncode == 0 and out.stdout.strip().endswith("drained"), out.stdout + out.stderr
+    assert "ftx_shutdown at exit returned" not in out.stderr
