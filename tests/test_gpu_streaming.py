@@ -290,3 +290,32 @@ def test_chunked_upload_bit_exact(gpu, chunk_mib, staged, n_host):
         assert checksum(dst.view(-1).view(torch.uint8)) == onat.checksum64(src.contiguous().view(-1).view(torch.uint8))
     assert out[-2].stride() == (1, 4)
     assert out[-1].is_contiguous()
+
+
+def test_fp8_llama_with_projections_as_units_matches_resident(gpu):
+    """fp8 projections that are offload units of their own (attention, gate, up and down) stream through
+    their traps: the decoder groups or fuses only projections whose module call would run nothing else, so
+    here it calls each streamed module and its weights are loaded before they are read. Greedy tokens and
+    every step's logits equal the resident model's, which takes the grouped and fused launches."""
+    shape = W.LlamaShape(n_layers=4, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=704, vocab=1000,
+                         max_seq=128, fp8=True)
+    model = W.build_llama(shape, seed=5)
+    prompt = W.prompt_tokens(8, 16, shape.vocab, seed=5).to(gpu)
+    ref = _resident(model, gpu)
+    ref.init_cache(8, 40, gpu)
+    want_tokens, want_logits = W.generate(ref, prompt, 6)
+    units = ["layers.*.attn", "layers.*.gate", "layers.*.up", "layers.*.down"]
+    unit_bytes = sum(p.numel() * p.element_size() for p in model.layers[0].parameters()) // 4
+    other = sum(p.numel() * p.element_size() for p in model.parameters()) - 4 * 4 * unit_bytes
+    other += sum(b.numel() * b.element_size() for b in model.buffers())
+    mgr = _stream(model, gpu, include_patterns=units, max_gpu_mem_bytes=other + 8 * unit_bytes)
+    model.init_cache(8, 40, gpu)
+    W.generate(model, prompt, 6)  # discovery + profiling
+    model.init_cache(8, 40, gpu)
+    got_tokens, got_logits = W.generate(model, prompt, 6)
+    streamed = set(mgr.plan.streamed)
+    assert streamed and any(x.endswith((".gate", ".up", ".down")) for x in streamed), sorted(streamed)
+    assert torch.equal(got_tokens, want_tokens)
+    for i, (a, b) in enumerate(zip(got_logits, want_logits)):
+        assert torch.equal(a, b), f"step {i}: max |diff| {float((a - b).abs().max()):.3e}"
+    mgr.release()
