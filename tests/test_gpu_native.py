@@ -66,6 +66,28 @@ def test_kernel_copy_bit_exact_at_each_grid(gpu, grid, nbytes):
     assert (out[:3] == 0xA5).all() and (out[3 + nbytes :] == 0xA5).all()
 
 
+@pytest.mark.parametrize("nbytes", [4095, (1 << 20) + 7, (64 << 20) + 5])
+def test_auto_copy_under_a_per_call_policy_takes_the_kernel_up_to_its_cut(gpu, nbytes):
+    """``FTX_COPY_AUTO`` under a caller's policy: chunks up to its kernel cut go to the zero-copy kernel at its
+    grid (a link-bound ring's policy: cut at the largest unit, 8 workgroups), larger ones to SDMA; bit-exact
+    either way, and the library default is untouched."""
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import current_stream
+
+    data = _rand_bytes(nbytes, seed=nbytes ^ 0x5A)
+    arena = _arena_with(data, pad=16)
+    default = nat.get_copy_policy()
+    for cut in (nbytes, nbytes - 1):  # kernel, then SDMA
+        dst = torch.full((nbytes + 64,), 0xA5, dtype=torch.uint8, device=gpu)
+        policy = nat.copy_policy(cut, 2**63 - 1, 1, 8)
+        nat.copy_h2d(dst.data_ptr() + 16, arena.ptr + 16, nbytes, nat.COPY_AUTO, current_stream(gpu).handle, policy)
+        torch.cuda.synchronize()
+        out = dst.cpu().numpy()
+        assert np.array_equal(out[16: 16 + nbytes], data), cut
+        assert (out[:16] == 0xA5).all() and (out[16 + nbytes:] == 0xA5).all()
+    assert nat.get_copy_policy() == default
+
+
 def test_kernel_copy_rejects_non_congruent_alignment(gpu):
     from flextensor_amd import _native as nat
     from flextensor_amd.hip import current_stream
