@@ -219,12 +219,14 @@ def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
 
 
 def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
-                  include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4) -> dict:
+                  include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4,
+                  ring_waits: str = "auto") -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
     streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
     units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
     returned under ``_check`` so that runs with other units can be compared bitwise. After the timed
-    tokens, ``ring_tokens`` more decode tokens time every ring copy on its own (:func:`ring_copy_stats`)."""
+    tokens, ``ring_tokens`` more decode tokens time every ring copy on its own (:func:`ring_copy_stats`).
+    ``ring_waits`` "stream" or "host" overrides how the ring's copies are waited for (:func:`_set_ring_waits`)."""
     import torch
 
     from flextensor_amd import hip
@@ -247,6 +249,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         model(prompt[:, :16], 0)  # discovery
         model(prompt[:, :16], 0)  # profiling -> plan and loader are built here
     _log(f"llama7b: streaming set up ({mgr.build_seconds:.1f} s to pack, measure the link and build)")
+    _set_ring_waits(mgr, ring_waits)
     plan = mgr.plan
     streamed_bytes = sum(mgr._unit(x).nbytes for x in plan.streamed)
     with torch.no_grad():
@@ -304,6 +307,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         "transfer_stream": hip.transfer_stream_probe(dev),
         "ring_copies": ring,
         "ring_copy_engine": _ring_engine(mgr),
+        "ring_waits": _ring_waits(mgr),
         "_check": {"last_logits": last_logits, "tokens": torch.cat(toks, -1).cpu()},
     }
     mgr.release(preserve_model=False)
@@ -324,6 +328,18 @@ def _ring_roofline(run: dict, measured_peak: float) -> dict | None:
             "timing": f"HIP events on the transfer stream around each ring copy, over {ring['passes']} decode "
                       "tokens after the timed ones",
             "by_size": ring["by_size"]}
+
+
+def _set_ring_waits(mgr, how: str) -> None:
+    """Override the manager's choice of ring waits: "stream" (the compute stream waits on each copy's
+    ready event) or "host" (the host blocks on it); "auto" keeps the manager's choice (host waits for a
+    link-bound pass)."""
+    if how != "auto" and hasattr(mgr.loader, "host_waits"):
+        mgr.loader.host_waits = how == "host"
+
+
+def _ring_waits(mgr) -> str:
+    return "host" if getattr(mgr.loader, "host_waits", False) else "stream"
 
 
 def _ring_engine(mgr) -> str:
@@ -570,7 +586,8 @@ def _mem_available_bytes() -> int:
     return 0
 
 
-def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: int, layers: int) -> dict:
+def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: int, layers: int,
+                       ring_waits: str = "auto") -> dict:
     """Batch decode of the 70B-shape decoder with fp8 weights (per-channel bf16 scales) under a GPU budget."""
     import torch
 
@@ -602,6 +619,7 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
     _log(f"70b: built {t_build:.1f} s, profiled and streaming set up {t_setup:.1f} s; "
          f"{len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers; "
          f"{mgr.link.describe() if mgr.link is not None else 'default copy policy'}")
+    _set_ring_waits(mgr, ring_waits)
     model.init_cache(batch, prompt_len + decode + 2, dev)
     with torch.no_grad():
         torch.cuda.synchronize()
@@ -632,6 +650,7 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
             "kernel_max_bytes", "n_copy_streams", "kernel_grid", "link_bound", "pass_compute_ms",
             "pass_transfer_ms")},
         "ring_copy_engine": _ring_engine(mgr),
+        "ring_waits": _ring_waits(mgr),
     }
     mgr.release(preserve_model=False)
     return out
@@ -1278,7 +1297,13 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
       link-bound policy;
     * ``*_device_only``: the same with every ready and release event created
       ``device_only`` (``FTX_EVENT_DEVICE_ONLY``: no system-scope fence when
-      recorded).
+      recorded);
+    * ``ring_host_wait`` / ``ring_kernel_host_wait``: the ring with the compute
+      stream never waiting on a ready event. The host enqueues two copies ahead,
+      then per copy blocks on its ready event, enqueues the slot's read and
+      release on the compute stream and the copy two later (behind its release
+      wait) on the transfer stream. A copy then has no waiter on another queue
+      while it runs.
 
     Per arrangement and size, the median of ``reps`` chains: microseconds per
     copy (HIP events on the transfer stream around the chain), GB/s, and the
@@ -1297,7 +1322,7 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
     kernel_policy = nat.copy_policy(0, 2**63 - 1, 1, L.RING_KERNEL_GRID)
     acc = torch.zeros(1, dtype=torch.float32, device=dev)
     kinds = ("back_to_back", "slot_waits", "marks", "marks_device_only", "consume_only", "handshake_only", "ring",
-             "ring_device_only", "ring_kernel", "ring_kernel_device_only")
+             "ring_device_only", "ring_kernel", "ring_kernel_device_only", "ring_host_wait", "ring_kernel_host_wait")
     out: dict = {"copies": copies, "sizes": {}}
     for mib in sizes_mib:
         nb = mib * MiB
@@ -1320,9 +1345,37 @@ def copy_chain(sizes_mib=(90, 386), copies: int = 56, reps: int = 3) -> dict:
                 best = min(best, a.elapsed_time(b))
             return best
 
+        def host_waited_ms(mode, policy):
+            torch.cuda.synchronize()
+            ready, released = [None] * copies, [None, None]
+            start, end = HipEvent(True), HipEvent(True)
+            xs.wait_stream(comp)
+            xs.record_event(start)
+
+            def enqueue(i):
+                s = i % 2
+                if released[s] is not None:
+                    xs.wait_event(released[s])
+                one(s, mode, policy, xs)
+                ready[i] = xs.record_event(HipEvent())
+
+            for i in range(min(2, copies)):
+                enqueue(i)
+            for i in range(copies):
+                ready[i].synchronize()
+                acc.add_(slots[i % 2][:4096].float().sum())
+                released[i % 2] = comp.record_event(HipEvent())
+                if i + 2 < copies:
+                    enqueue(i + 2)
+            xs.record_event(end)
+            torch.cuda.synchronize()
+            return start.elapsed_time(end)
+
         def chain_ms(kind):
             kernel = kind.startswith("ring_kernel")
             mode, policy = (nat.COPY_KERNEL, kernel_policy) if kernel else (nat.COPY_SDMA, None)
+            if kind.endswith("_host_wait"):
+                return host_waited_ms(mode, policy)
             device_only = kind.endswith("_device_only")
             ring = kind.startswith("ring") or kind == "handshake_only"
             consume = kind.startswith("ring") or kind == "consume_only"
@@ -1376,6 +1429,8 @@ def main() -> int:
     ap.add_argument("--tensors", type=int, default=2000)
     ap.add_argument("--scatter-steps", type=int, default=5)
     ap.add_argument("--copy-engine", default="auto", choices=["auto", "sdma", "kernel"])
+    ap.add_argument("--ring-waits", default="auto", choices=["auto", "stream", "host"],
+                    help="how the decodes wait for ring copies (auto: on the host in link-bound passes)")
     ap.add_argument("--kernel-grid", type=int, default=0,
                     help="zero-copy kernel workgroups for --copy-engine kernel (0: the library default)")
     ap.add_argument("--skip-cpu-baseline", action="store_true")
@@ -1474,7 +1529,8 @@ def main() -> int:
     _log(f"measured H2D peak (512 MiB, best of 20): sdma {peak['sdma']:.2f} GB/s, kernel {peak['kernel']:.2f} GB/s")
 
     # ---- headline: 7B-shape decoder, 8 GB budget, one decode token per step
-    llama = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine)
+    llama = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
+                          ring_waits=args.ring_waits)
     check = llama.pop("_check")
     _log(f"llama7b: {llama}")
     line = {
@@ -1497,7 +1553,7 @@ def main() -> int:
                    "streamed_layers": llama["streamed_layers"], "resident_layers": llama["resident_layers"],
                    "streamed_bytes_per_token": llama["streamed_bytes_per_token"], "copy_engine": args.copy_engine,
                    "copy_policy": llama["copy_policy"], "copy_policy_source": llama["copy_policy_source"],
-                   "transfer_stream": llama["transfer_stream"]},
+                   "ring_waits": llama["ring_waits"], "transfer_stream": llama["transfer_stream"]},
         "tok_s": round(llama["decode_tok_s"], 3),
         "prefill_tok_s": round(llama["prefill_tok_s"], 1),
         "link": {"decode_effective_GBps": round(llama["decode_effective_GBps"], 3),
@@ -1516,7 +1572,7 @@ def main() -> int:
     # ---- the same decode with each layer's attention and three MLP projections as separate units
     if not args.skip_finer_units:
         fine = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
-                             include_patterns=FINER_UNITS)
+                             include_patterns=FINER_UNITS, ring_waits=args.ring_waits)
         fine_check = fine.pop("_check")
         same = (torch.equal(fine_check["last_logits"], check["last_logits"])
                 and torch.equal(fine_check["tokens"], check["tokens"]))
@@ -1529,6 +1585,7 @@ def main() -> int:
             "pct_of_measured_peak": round(100 * fine["decode_effective_GBps"] / measured_peak, 2),
             "gpu_weight_bytes": fine["gpu_weight_bytes"],
             "copy_policy": fine["copy_policy"],
+            "ring_waits": fine["ring_waits"],
             "ring_copies": _ring_roofline(fine, measured_peak),
             "prefill_logits_and_tokens_bitwise_equal_to_layer_units": same,
         }
@@ -1602,7 +1659,7 @@ def main() -> int:
         _log(f"fp8 linear: {line['fp8_linear']}")
         line["fp8_prefill"] = bench_fp8_prefill()
         _log(f"fp8 prefill: {line['fp8_prefill']}")
-        line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b)
+        line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b, ring_waits=args.ring_waits)
         if not args.skip_cpu_baseline and "skipped" not in line["llama70b_fp8"]:
             line["llama70b_fp8"]["cpu_baseline"] = cpu_llama70b_decode_baseline()
         _log(f"70b: {line['llama70b_fp8']}")

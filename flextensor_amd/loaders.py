@@ -107,6 +107,9 @@ class _PipelinedLoader(PreallocatedLoader):
         self.first_layer_label = layer_stats[0].label if layer_stats else None
         self.last_layer_label = layer_stats[-1].label if layer_stats else None
         self.preload_transfers = find_transfers_for_preload(self.transfer_to_compute_map, layer_stats)
+        # Wait for ring copies on the host rather than on the compute stream (the reordered loader only;
+        # see its enter). The manager sets it for link-bound passes.
+        self.host_waits = False
 
     def _trace(self, label: str) -> str:
         return f"schedule={label} consume={self.transfer_to_compute_map[label]}"
@@ -235,22 +238,43 @@ class PreallocatedBatchTransferTensorLoaderReordered(_PipelinedLoader):
         rt.join()
 
     def enter(self, label: str) -> None:
+        """Wait for the transfers ``label`` consumes, then submit the one scheduled at ``label``.
+
+        With ``host_waits`` (link-bound passes) the host blocks on each
+        transfer instead of the compute stream waiting on it, and the
+        transfer scheduled at ``label`` is submitted before that block, so
+        the transfer stream already holds the next copy while the host
+        waits and the link never waits on the host. The slot it fills is
+        never one ``label`` consumes (those stay busy until ``exit``), so
+        the two orders fill the same slots. Graph capture keeps the
+        reference's order and stream waits.
+        """
         tc, pp, rt = self.offload_timing_collector, self.piecewise_prefetch_policy, self._transfer_runtime
         self._start_pass_if_first(label)
         if not rt.is_active:
             rt.begin()
         if label in self._preloaded_compute_labels:
             pp.on_wait(label)
+        host = self.host_waits and not self.backend.is_capturing()
+        ahead = host and label in self.label_to_block_id and self.transfer_to_compute_map[label] != label
+        if ahead:
+            self._submit(label)
         tickets = self.scheduled_transfers.pop(label, None)
         if tickets:
             tc.record_wait_start(label)
             for ticket in tickets:
-                rt.wait_ready(ticket)
+                rt.wait_ready(ticket, host=host)
             pp.on_wait(label)
             tc.record_wait_end(label)
         if label not in self.label_to_block_id:
             tc.record_compute_start(label)
             return
+        if not ahead:
+            self._submit(label)
+        tc.record_compute_start(label)
+
+    def _submit(self, label: str) -> None:
+        tc, pp, rt = self.offload_timing_collector, self.piecewise_prefetch_policy, self._transfer_runtime
         compute = self.transfer_to_compute_map[label]
 
         def transfer() -> None:
@@ -261,7 +285,6 @@ class PreallocatedBatchTransferTensorLoaderReordered(_PipelinedLoader):
         tc.record_transfer_end(label, self.transfer_stream)
         self.scheduled_transfers.setdefault(compute, []).append(ticket)
         pp.on_schedule(schedule_label=label, compute_label=compute)
-        tc.record_compute_start(label)
 
     def exit(self, label: str) -> None:
         self.offload_timing_collector.record_compute_end(label)

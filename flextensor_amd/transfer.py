@@ -9,7 +9,9 @@ rebuilt on HIP streams and events through the C ABI:
   wait for the slot's last use (:90-92), runs ``fn`` with the transfer stream
   current and records a readiness event (:96-100);
 * ``wait_ready(ticket)`` makes the current stream wait for a live ticket and
-  rejects stale or foreign tickets (:102-109);
+  rejects stale or foreign tickets (:102-109). ``wait_ready(ticket, host=True)``
+  blocks the calling thread on the ticket instead, so that no wait on another
+  queue is pending while the transfer runs;
 * ``finish_use(slot)`` records the slot's last use on the current stream
   (:111-117);
 * ``join()`` joins the transfer stream back and invalidates tickets (:119-131);
@@ -46,6 +48,8 @@ class StreamBackend(Protocol):
 
     def use_stream(self, stream: Any) -> AbstractContextManager: ...
 
+    def is_capturing(self) -> bool: ...
+
 
 class HipBackend:
     """Streams and events of the HIP runtime torch uses, through the C ABI."""
@@ -68,6 +72,11 @@ class HipBackend:
         from .hip import use_stream
 
         return use_stream(stream)
+
+    def is_capturing(self) -> bool:
+        from .hip import is_capturing
+
+        return is_capturing()
 
 
 @dataclass(frozen=True, slots=True)
@@ -137,12 +146,27 @@ class HipTransferRuntime:
         self._busy.add(slot)
         return ticket
 
-    def wait_ready(self, ticket: TransferTicket) -> None:
+    def wait_ready(self, ticket: TransferTicket, *, host: bool = False) -> None:
+        """Order the current stream's next work after ``ticket``'s transfer.
+
+        By default the current stream waits on the transfer's event. With
+        ``host`` the calling thread blocks until the transfer has finished
+        and the stream waits on nothing. A stream wait stays pending on the
+        compute queue for as long as the transfer runs, and a host-to-device
+        copy with such a waiter moves about 0.5% fewer bytes per second on
+        the MI355X (35-40 us per 386 MiB copy); a blocked host costs the
+        link nothing. Work the caller enqueues afterwards starts after the
+        transfer, as after any host synchronisation. Under graph capture the
+        transfer has not run yet, so the stream waits as by default.
+        """
         self._require_open()
         if ticket._runtime_token is not self._token:
             raise ValueError(f"ticket belongs to a different {type(self).__name__}")
         if self._tickets.get(ticket.slot) is not ticket:
             raise ValueError(f"stale {ticket}")
+        if host and not self.backend.is_capturing():
+            ticket._event.synchronize()
+            return
         self.backend.current_stream().wait_event(ticket._event)
 
     def finish_use(self, slot: Hashable) -> None:

@@ -16,6 +16,13 @@ from dataclasses import dataclass, field
 class FakeEvent:
     name: str
     completed: bool = True
+    rec: "Recorder | None" = field(default=None, repr=False, compare=False)
+
+    def synchronize(self) -> None:
+        """A host wait: logged on the "host" stream, stalled when the event had not completed."""
+        if self.rec is not None:
+            self.rec.log.append(Entry("synchronize_event", "host", self.name, not self.completed))
+        self.completed = True
 
 
 @dataclass
@@ -33,7 +40,7 @@ class Recorder:
 
     def new_event(self, stream: str, completed: bool) -> FakeEvent:
         self.counter += 1
-        return FakeEvent(f"{stream}_ev_{self.counter}", completed)
+        return FakeEvent(f"{stream}_ev_{self.counter}", completed, self)
 
     def forward(self, label: str) -> None:
         self.log.append(Entry("forward", "compute", label))
@@ -90,6 +97,7 @@ class FakeBackend:
         self.transfer = FakeStream("transfer", rec, completes=not slow_transfer)
         self.current = self.compute
         self.created = 0
+        self.capturing = False
 
     def current_stream(self):
         return self.current
@@ -105,6 +113,9 @@ class FakeBackend:
             yield
         finally:
             self.current = prev
+
+    def is_capturing(self) -> bool:
+        return self.capturing
 
 
 class FakeController:

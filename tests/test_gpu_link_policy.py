@@ -6,6 +6,9 @@ go to the zero-copy kernel at the ring grid. The same stack at 32768 rows
 computes for about three times its transfer time and keeps the measured
 per-size policy (SDMA for the 180 MB layers).
 
+The link-bound manager also waits for its ring copies on the host rather
+than on the compute stream.
+
 Both managers live in one process and stream in alternation, as the
 reference's named managers do (offload_manager.py:2817-2850): each
 controller carries its own policy into every copy, the library's
@@ -60,6 +63,8 @@ def test_link_bound_and_compute_bound_managers_stream_side_by_side(gpu):
         pol = compute_bound.controller.copy_policy
         assert pol.kernel_max_bytes < unit_bytes and pol.kernel_grid == 0
         assert nat.get_copy_policy() == default  # neither manager touched the process-wide default
+        # the link-bound ring waits for its copies on the host, the compute-bound one on the compute stream
+        assert link_bound.loader.host_waits and not compute_bound.loader.host_waits
         for name in rows:
             assert torch.equal(got[name], want[name]), name
         # one manager goes; the other keeps streaming bitwise under its own policy

@@ -108,6 +108,28 @@ def test_foreign_and_stale_tickets(rt):
         runtime.wait_ready(cur)
 
 
+def test_host_wait_blocks_the_host_and_leaves_the_stream_unordered(rt):
+    runtime, rec, backend = rt
+    runtime.begin()
+    ticket = runtime.submit("slot-0", lambda: None)
+    rec.log.clear()
+    runtime.wait_ready(ticket, host=True)
+    assert rec.triples() == [("synchronize_event", "host", ticket._event.name)]
+    backend.capturing = True  # a captured transfer has not run: the stream waits
+    rec.log.clear()
+    runtime.wait_ready(ticket, host=True)
+    assert rec.triples() == [("wait_event", "compute", ticket._event.name)]
+    backend.capturing = False
+    runtime.finish_use("slot-0")
+    runtime.submit("slot-0", lambda: None)
+    with pytest.raises(ValueError, match="stale"):  # the ticket checks hold for host waits too
+        runtime.wait_ready(ticket, host=True)
+    foreign = HipTransferRuntime(None, backend=backend)
+    foreign.begin()
+    with pytest.raises(ValueError, match="different"):
+        runtime.wait_ready(foreign.submit("slot-0", lambda: None), host=True)
+
+
 def test_lifecycle_errors(rt):
     runtime, rec, _ = rt
     with pytest.raises(RuntimeError, match="begin"):
@@ -225,6 +247,69 @@ def test_traces_match_oracle(kind, seed):
     _run(loader, rec, labels, passes)
     want = osch.trace(kind, labels, t2c, l2b, osch.passes(labels, passes))
     assert rec.triples() == want
+
+
+def _ready_waits(rec, op, stream):
+    """(ordinal of the transfer, forwards run before the wait) for each wait ``op`` on ``stream`` on a ready event."""
+    ready, pending, count, forwards, waits = {}, None, 0, 0, []
+    for e in rec.log:
+        if e.op == "schedule_transfer":
+            pending, count = count, count + 1
+        elif (e.op, e.stream) == ("record_event", "transfer") and pending is not None:
+            ready[e.target], pending = pending, None  # the submit records its ready event right after the copy
+        elif e.op == "forward":
+            forwards += 1
+        elif (e.op, e.stream) == (op, stream) and e.target in ready:
+            waits.append((ready[e.target], forwards))
+    return waits
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_host_waited_reordered_loader_waits_the_same_copies_on_the_host(seed):
+    """With ``host_waits`` the reordered loader issues the same copies in the same order, waits for each
+    consumed copy on the host before the same forward as the stream-waited loader does on the compute
+    stream, never makes the compute stream wait on a copy, and queues each label's copy before it blocks."""
+    rng = random.Random(seed)
+    n = rng.randrange(2, 11)
+    labels = ["embed"] + [f"L{i}" for i in range(n - 1)]
+    gaps = set(rng.sample(labels[1:], rng.randrange(0, max(1, n // 3))))
+    t2c, l2b = _pipeline(labels, gaps, rng.choice([2, 3]), rng.random() < 0.5)
+    passes = rng.choice([1, 2, 3])
+    streamed, s_rec, _ = _make("reordered", labels, t2c, l2b, slow=True, gaps=gaps)
+    _run(streamed, s_rec, labels, passes)
+    hosted, h_rec, _ = _make("reordered", labels, t2c, l2b, slow=True, gaps=gaps)
+    hosted.host_waits = True
+    _run(hosted, h_rec, labels, passes)
+    copies = [e.target for e in h_rec.log if e.op == "schedule_transfer"]
+    assert copies == [e.target for e in s_rec.log if e.op == "schedule_transfer"]
+    waited = _ready_waits(s_rec, "wait_event", "compute")
+    assert _ready_waits(h_rec, "synchronize_event", "host") == waited
+    assert _ready_waits(h_rec, "wait_event", "compute") == []
+    # between two forwards, the copy scheduled there is queued before the host blocks
+    segment: list = []
+    for e in [*h_rec.log, None]:
+        if e is None or e.op == "forward":
+            ops = [x.op for x in segment]
+            if "schedule_transfer" in ops and "synchronize_event" in ops:
+                assert ops.index("schedule_transfer") < ops.index("synchronize_event"), h_rec.dump()
+            segment = []
+        else:
+            segment.append(e)
+    assert not hosted.scheduled_transfers and not hosted._transfer_runtime.is_active
+
+
+@pytest.mark.parametrize("kind", ["default", "reordered"])
+def test_host_waits_keep_the_reference_trace_under_capture_and_in_the_default_loader(kind):
+    """Under graph capture the reordered loader keeps the reference's order and stream waits; the default
+    loader, whose copy is waited in the same unit that issued it, always does."""
+    labels = ["embed"] + [f"L{i}" for i in range(6)]
+    t2c, l2b = _pipeline(labels, {"L2"}, 2, kind == "reordered")
+    loader, rec, _ = _make(kind, labels, t2c, l2b, gaps={"L2"})
+    loader.host_waits = True
+    loader.backend.capturing = kind == "reordered"
+    _run(loader, rec, labels, 2)
+    assert rec.triples() == osch.trace(kind, labels, t2c, l2b, osch.passes(labels, 2))
+    assert not rec.find("synchronize_event")
 
 
 @pytest.mark.parametrize("kind", ["default", "reordered"])
