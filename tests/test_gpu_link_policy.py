@@ -84,7 +84,9 @@ def test_a_replan_follows_the_workload_when_the_batch_changes(gpu):
     is link-bound and copies its ring with the zero-copy kernel. Fed 32768-row batches it computes for
     longer than its transfers, and a replan measured on those passes moves the ring back to the measured
     per-size policy (SDMA for the 180 MB layers). Back at 16 rows, a second replan returns to the kernel.
-    Every pass is bitwise equal to the resident forward."""
+    A 1 GB budget keeps some layers resident, so the reordered loader runs and its ring waits follow the
+    policy: on the host while link-bound, on the compute stream otherwise. Every pass is bitwise equal to
+    the resident forward."""
     import flextensor_amd as ft
 
     nat.load()
@@ -98,14 +100,16 @@ def test_a_replan_follows_the_workload_when_the_batch_changes(gpu):
     torch.cuda.empty_cache()
     mgr = OffloadManager("replan-gpu")
     mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
-                                     profiling_iters=1))
+                                     profiling_iters=1, max_gpu_mem_bytes=1_000_000_000))
     try:
         assert mgr.strategy_replan_status == ft.StrategyReplanStatus("idle", False, None)
         with torch.no_grad():
             for _ in range(3):  # discovery, profiling at 16 rows, one streamed pass
                 got = model(small)
         assert torch.equal(got, want[16])
+        assert mgr.plan.resident and mgr.plan.reordered
         assert mgr.link.link_bound and mgr.controller.copy_policy.kernel_grid == L.RING_KERNEL_GRID
+        assert mgr.loader.host_waits
         assert mgr.strategy_replan_status.can_request
         for rows, x, link_bound in ((32768, large, False), (16, small, True)):
             print(f"replan at {rows} rows", flush=True)
@@ -119,6 +123,7 @@ def test_a_replan_follows_the_workload_when_the_batch_changes(gpu):
             assert status == ft.StrategyReplanStatus("done", True, True), status
             assert mgr.link.link_bound == link_bound and mgr.link.source == "replan", mgr.link.describe()
             assert mgr.controller.copy_policy == mgr.link.native_policy()
+            assert mgr.loader.host_waits == link_bound
             with torch.no_grad():
                 assert torch.equal(model(x), want[rows])  # streaming under the new policy
         assert nat.get_copy_policy() == default
