@@ -179,8 +179,15 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
                    num_blocks: int, min_blocks: int | None = None) -> StreamPlan:
     """Choose streamed units and the slot plan under a GPU byte budget.
 
-    The fewest units stream that fit, spread evenly over the pass. For that
-    choice the slot count is the largest in ``[min_blocks, num_blocks]`` whose
+    The fewest units stream that fit, spread evenly over the pass: the
+    picks centred in k equal spans, rotated so the first unit streams (the
+    gaps between consecutive picks, the last to the first included, are the
+    centred ones). A streamed first unit is loaded by a cyclic transfer
+    issued at the previous pass's last units, so the ring keeps the link busy
+    across the pass boundary; a first transfer issued inside the pass would
+    wait for the fork at the pass start, behind the previous pass's tail
+    compute. For that choice the slot count is the largest in
+    ``[min_blocks, num_blocks]`` whose
     slots fit the budget (the deepest prefetch the memory allows; the
     reference searches the same range, config.py:207-225). Slots beyond
     ``num_blocks`` are added only while the reference's slot-reuse check
@@ -197,7 +204,8 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
     hi = max(num_blocks, 2)
     lo = max(2, min(hi, min_blocks if min_blocks is not None else hi))
     for k in range(1, n + 1):
-        pick = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
+        centred = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
+        pick = [i - centred[0] for i in centred]
         if len(pick) < k:
             continue
         streamed = [labels[i] for i in pick]

@@ -70,6 +70,36 @@ def test_plan_fits_budget_and_spreads_streamed_units():
     assert 500 + (10 - (k - 1)) * 1000 + 2 * 1000 > 7000
 
 
+@pytest.mark.parametrize("n", [4, 7, 10, 32])
+def test_streamed_units_start_at_the_first_unit_and_keep_the_centred_gaps(n):
+    """The streamed picks are the centred ones rotated to start at the first unit: the cyclic gaps are
+    unchanged, and the first unit's transfer is a cyclic preload issued in the previous pass."""
+    from flextensor_amd.loaders import find_transfers_for_preload
+
+    units = _mk([1000] * n)
+    order = [u.label for u in units]
+    seen = set()
+    for budget in range(2000 + 1000, 1000 * n + 1, 500):
+        plan = plan_streaming(units, order, budget=budget, base_bytes=0, num_blocks=2, min_blocks=2)
+        if plan.block_data is None or len(plan.streamed) in seen:
+            continue
+        k = len(plan.streamed)
+        seen.add(k)
+        idx = [order.index(x) for x in plan.streamed]
+        centred = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
+
+        def gaps(p):
+            return [b - a for a, b in zip(p, p[1:])] + [n - p[-1] + p[0]]
+
+        assert idx[0] == 0 and gaps(idx) == gaps(centred), (k, idx, centred)
+        if plan.resident:
+            bd = plan.block_data
+            stats = [LayerStatistics(x) for x in order]
+            pre = find_transfers_for_preload(bd.transfer_to_compute_map, stats)
+            assert order[0] in pre.values(), (k, bd.transfer_to_compute_map)
+    assert seen
+
+
 def test_plan_everything_resident_when_it_fits():
     units = _mk([100] * 4)
     plan = plan_streaming(units, [u.label for u in units], budget=10_000, base_bytes=0, num_blocks=2)
