@@ -342,6 +342,9 @@ def test_killed_creator_is_detected_and_its_namespace_reclaimed(ready):
     tests/unit/shm/test_cleanup.py:231-256)."""
     import signal
 
+    # The creator beats every 0.05 s. A keep-alive of 1.5 s lets a loaded host stall the creator's process
+    # for over a second before a live creator reads as dead.
+    KEEP_ALIVE = 1.5
     base = _ns()
     ns = SharedOffloadSession(base).namespace_for("default")
     ctx = mp.get_context("spawn")
@@ -350,17 +353,17 @@ def test_killed_creator_is_detected_and_its_namespace_reclaimed(ready):
     proc.start()
     try:
         assert started.wait(120), proc.exitcode
-        follower = ShmCoordinator(ns, keep_alive_seconds=0.3)
+        follower = ShmCoordinator(ns, keep_alive_seconds=KEEP_ALIVE)
         assert not follower.is_creator and follower.is_creator_alive()
         if ready:
             follower.wait_for_ready(timeout=5.0)  # live creator: ready at once
         with pytest.raises(ShmCoordinatorError, match="live creator"):
             SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=0.2,
-                                                   keep_alive_seconds=0.3)
+                                                   keep_alive_seconds=KEEP_ALIVE)
         proc.kill()
         proc.join(30)
         assert proc.exitcode == -signal.SIGKILL
-        time.sleep(0.4)  # past the keep-alive: within it a joiner cannot tell a dead creator from a live one
+        time.sleep(KEEP_ALIVE + 0.1)  # past the keep-alive: within it a joiner cannot tell a dead creator from a live one
         with pytest.raises(ShmCreatorDiedError) as err:
             follower.wait_for_ready(timeout=10.0)
         assert err.value.creator_identity == proc.pid and err.value.after_ready is ready
@@ -368,12 +371,12 @@ def test_killed_creator_is_detected_and_its_namespace_reclaimed(ready):
         follower.close()
         assert _leftovers(ns)  # SIGKILL skips the creator's own removal
         for _ in range(2):  # joiners are refused, and joining does not revive the namespace
-            joiner = ShmCoordinator(ns, keep_alive_seconds=0.3)
+            joiner = ShmCoordinator(ns, keep_alive_seconds=KEEP_ALIVE)
             assert not joiner.is_creator
             with pytest.raises(ShmCreatorDiedError):
                 joiner.wait_for_ready(timeout=10.0)
             joiner.close()
-        SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=5.0, keep_alive_seconds=0.3)
+        SharedOffloadSession.cleanup_namespace(base, manager_names=["default"], timeout=5.0, keep_alive_seconds=KEEP_ALIVE)
         assert _leftovers(ns) == []
         fresh = ShmCoordinator(ns)
         assert fresh.is_creator
