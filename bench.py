@@ -1044,21 +1044,31 @@ def cpu_llama70b_decode_baseline(batch: int = 8, context: int = 64, steps: int =
                       f"at context {context}, scaled linearly to 80 layers"}
 
 
+RING_COPY_PROBES = 3  # ring copies of one 7B-shape decoder layer in the traffic probe
+
+
 def measure_traffic(args) -> dict | None:
-    """HBM bytes per scatter launch from two ``rocprofv3 --pmc`` child runs.
+    """HBM bytes per scatter launch and per ring copy from two ``rocprofv3 --pmc`` child runs.
 
     Each child runs this script in ``--traffic-probe`` mode: one 1 GiB
     device-to-device copy (the runtime's copy kernel, whose traffic is known:
-    1 GiB read, 1 GiB written), then one step of the scatter workload. The
-    counter reading of the calibration copy gives the scale of each counter;
-    traffic = scaled FETCH_SIZE + scaled WRITE_SIZE, averaged over the scatter
-    launches. Returns None when rocprofv3 is not available or a pass fails.
+    1 GiB read, 1 GiB written), then one step of the scatter workload, then
+    ``RING_COPY_PROBES`` ring copies of one 7B-shape decoder layer (404,766,720
+    B from a page-locked arena) on the zero-copy kernel at the link-bound
+    grid, as the headline decode copies them. The counter reading of the
+    calibration copy gives the scale of each counter; traffic = scaled
+    FETCH_SIZE + scaled WRITE_SIZE, averaged over the scatter launches. For the
+    ring copy FETCH_SIZE counts the bytes read from host memory over the link
+    and WRITE_SIZE the bytes written to HBM (``ring_copy``). Returns None when
+    rocprofv3 is not available or a pass fails.
     """
     import csv
     import glob
     import shutil
     import subprocess
     import tempfile
+
+    from flextensor_amd import link_model as L
 
     exe = shutil.which("rocprofv3")
     if exe is None:
@@ -1084,16 +1094,24 @@ def measure_traffic(args) -> dict | None:
             rows = sorted(csv.DictReader(fh), key=lambda row: int(row["Dispatch_Id"]))
         copies = [row for row in rows if row["Kernel_Name"] == "__amd_rocclr_copyBuffer"]
         scat = [row for row in rows if "scatter_kernel" in row["Kernel_Name"]]
+        ring = [row for row in rows if "zero_copy_kernel" in row["Kernel_Name"]
+                and int(row.get("Grid_Size", L.RING_KERNEL_GRID * 256)) == L.RING_KERNEL_GRID * 256]
         if not copies or not scat:
             return None
         scale = calib / (float(copies[0]["Counter_Value"]) * 1024)
         out[ctr] = {"scale": round(scale, 4),
-                    "bytes_per_launch": sum(float(row["Counter_Value"]) for row in scat) * 1024 * scale / len(scat)}
+                    "bytes_per_launch": sum(float(row["Counter_Value"]) for row in scat) * 1024 * scale / len(scat),
+                    "ring_bytes_per_launch": (sum(float(row["Counter_Value"]) for row in ring) * 1024 * scale / len(ring)
+                                              if len(ring) == RING_COPY_PROBES else None)}
         shutil.rmtree(d, ignore_errors=True)
-    return {"traffic": out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"],
-            "fetch_bytes_per_launch": out["FETCH_SIZE"]["bytes_per_launch"],
-            "write_bytes_per_launch": out["WRITE_SIZE"]["bytes_per_launch"],
-            "fetch_scale": out["FETCH_SIZE"]["scale"], "write_scale": out["WRITE_SIZE"]["scale"]}
+    res = {"traffic": out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"],
+           "fetch_bytes_per_launch": out["FETCH_SIZE"]["bytes_per_launch"],
+           "write_bytes_per_launch": out["WRITE_SIZE"]["bytes_per_launch"],
+           "fetch_scale": out["FETCH_SIZE"]["scale"], "write_scale": out["WRITE_SIZE"]["scale"]}
+    if out["FETCH_SIZE"]["ring_bytes_per_launch"] is not None and out["WRITE_SIZE"]["ring_bytes_per_launch"] is not None:
+        res["ring_copy"] = {"host_read_bytes_per_launch": out["FETCH_SIZE"]["ring_bytes_per_launch"],
+                            "hbm_write_bytes_per_launch": out["WRITE_SIZE"]["ring_bytes_per_launch"]}
+    return res
 
 
 def traffic_probe(args) -> int:
@@ -1105,6 +1123,19 @@ def traffic_probe(args) -> int:
     torch.cuda.synchronize()
     del src, dst
     bench_scatter(1, 0, args.chunk_mib, args.tensors, args.copy_engine, verify=False)
+    from flextensor_amd import _native as nat
+    from flextensor_amd import link_model as L
+    from flextensor_amd import workloads as W
+    from flextensor_amd.hip import HostArena, transfer_stream
+
+    n = W.LLAMA_7B.layer_bytes()
+    arena = HostArena(n)
+    slot = torch.empty(n, dtype=torch.uint8, device="cuda")
+    xs = transfer_stream(torch.device("cuda", 0))
+    ring_policy = nat.copy_policy(n, 2**63 - 1, 1, L.RING_KERNEL_GRID)
+    for _ in range(RING_COPY_PROBES):
+        nat.copy_h2d(slot.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, xs.handle, ring_policy)
+    xs.synchronize()
     return 0
 
 
@@ -1633,9 +1664,15 @@ def main() -> int:
             if tr is not None:
                 line["roofline"]["traffic"] = int(tr["traffic"])
                 line["roofline"]["traffic_detail"] = {k: (int(v) if "bytes" in k else v) for k, v in tr.items()
-                                                      if k != "traffic"}
+                                                      if k not in ("traffic", "ring_copy")}
                 _log(f"traffic per scatter launch: {tr['traffic'] / 1e9:.3f} GB "
                      f"(algorithmic {line['roofline']['algorithmic_bytes_per_launch'] / 1e9:.3f} GB)")
+                ring_tr = tr.get("ring_copy")
+                if ring_tr is not None and line.get("roofline_ring_copy"):
+                    # HBM bytes: the writes; the reads come from host memory over the link
+                    line["roofline_ring_copy"]["traffic"] = int(ring_tr["hbm_write_bytes_per_launch"])
+                    line["roofline_ring_copy"]["traffic_detail"] = {k: int(v) for k, v in ring_tr.items()}
+                    _log(f"traffic per ring copy: {ring_tr}")
     if not args.skip_mlp:
         gc.collect()
         torch.cuda.empty_cache()
