@@ -148,6 +148,7 @@ _SIGNATURES: dict[str, list] = {
     "ftx_fp8_linear_static": [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp],
     "ftx_hbm_read_probe": [_vp, _sz, _vp, ctypes.c_int, _vp],
     "ftx_mfma_probe": [ctypes.c_int, ctypes.c_int, _vp, _vp],
+    "ftx_mfma_probe_shape": [ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp],
     "ftx_fp8_linear_group_workspace": [ctypes.c_int64, _vp, ctypes.c_int, ctypes.c_int64, ctypes.POINTER(_sz)],
     "ftx_fp8_linear_group": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _sz, _vp],
     "ftx_set_fp8_linear_config": [_int, _int],

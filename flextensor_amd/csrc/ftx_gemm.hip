@@ -418,6 +418,7 @@ constexpr int kPStage = kPXStage + kPWStage;
 constexpr int kPLoadsPerWave = 6;                    // load instructions per loading wave and step
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
@@ -688,6 +689,45 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(float *sink, int iters)
   if (sum == 1234.5f) sink[0] = sum;
 }
 
+// The same probe on v_mfma_f32_32x32x16_bf16 (32768 flops each): 8
+// independent accumulators per wave, 16 MFMAs per iteration, so an iteration
+// has the flops of the 16 x 16 probe's. It reads half the operand registers
+// per flop, and on changing data it sustains a higher rate.
+__global__ __launch_bounds__(256) void mfma_probe_32x32_kernel(float *sink, int iters) {
+  const uint32_t id = blockIdx.x * 256u + threadIdx.x;
+  u32x4 av[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t h = probe_hash(id * 64u + e * 8u + q);
+      const uint32_t h2 = probe_hash(h);
+      auto bf = [](uint32_t r) { return ((r & 1u) << 15) | ((126u + ((r >> 1) & 3u)) << 7) | ((r >> 3) & 0x7fu); };
+      av[e][q] = bf(h) | (bf(h >> 10) << 16);
+      bv[e][q] = bf(h2) | (bf(h2 >> 10) << 16);
+    }
+  }
+  f32x16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av[(i + h) & 7]), as_bf16x8(bv[(3 * i + h) & 7]),
+                                                         acc[i], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sum += acc[i][e];
+  if (sum == 1234.5f) sink[0] = sum;
+}
+
 template <int MB>
 hipError_t launch_mb(const Fp8LinearLaunch &p, hipStream_t stream) {
   const SegTable seg = seg_table(p);
@@ -781,8 +821,13 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
   return p;
 }
 
-hipError_t launch_mfma_probe(int workgroups, int iters, float *sink, hipStream_t stream) {
-  hipLaunchKernelGGL(mfma_probe_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256), 0, stream, sink, iters);
+hipError_t launch_mfma_probe(int shape, int workgroups, int iters, float *sink, hipStream_t stream) {
+  if (shape == kMfmaProbe32x32x16)
+    hipLaunchKernelGGL(mfma_probe_32x32_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256), 0, stream, sink,
+                       iters);
+  else
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256), 0, stream, sink,
+                       iters);
   return hipGetLastError();
 }
 

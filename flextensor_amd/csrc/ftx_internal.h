@@ -95,7 +95,9 @@ Fp8LinearLaunch plan_fp8_linear(int64_t m, const int64_t *n, int group, int64_t 
                                 int kc, int epilogue);
 hipError_t launch_fp8_linear(const Fp8LinearLaunch &p, hipStream_t stream);
 // MFMA rate probe: `workgroups` x 4 waves, each iters x 32 v_mfma_f32_16x16x32_bf16.
-hipError_t launch_mfma_probe(int workgroups, int iters, float *sink, hipStream_t stream);
+constexpr int kMfmaProbe16x16x32 = 0;  // v_mfma_f32_16x16x32_bf16, the prefill kernel's instruction
+constexpr int kMfmaProbe32x32x16 = 1;  // v_mfma_f32_32x32x16_bf16
+hipError_t launch_mfma_probe(int shape, int workgroups, int iters, float *sink, hipStream_t stream);
 
 // Staged copies from pageable host memory and the parallel host memcpy
 // (ftx_staged.hip).

@@ -1043,14 +1043,21 @@ int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, voi
 }
 
 int ftx_mfma_probe(int workgroups, int iters, void *sink, void *stream) {
+  return ftx_mfma_probe_shape(ftx::kMfmaProbe16x16x32, workgroups, iters, sink, stream);
+}
+
+int ftx_mfma_probe_shape(int shape, int workgroups, int iters, void *sink, void *stream) {
   FTX_REQUIRE_LIVE();
+  if (shape != ftx::kMfmaProbe16x16x32 && shape != ftx::kMfmaProbe32x32x16)
+    return ftx::fail(FTX_ERR_INVALID, "shape must be 0 (16x16x32) or 1 (32x32x16)");
   if (!sink) return ftx::fail(FTX_ERR_INVALID, "null pointer");
   if (reinterpret_cast<uintptr_t>(sink) % 4 != 0) return ftx::fail(FTX_ERR_INVALID, "sink needs 4-byte alignment");
   if (workgroups <= 0 || workgroups > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "workgroups must be in [1, 2^20]");
   if (iters <= 0 || iters > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "iters must be in [1, 2^20]");
   int rc = ftx::check_device_range(sink, 4, "mfma probe sink");
   if (rc != FTX_OK) return rc;
-  FTX_HIP(ftx::launch_mfma_probe(workgroups, iters, static_cast<float *>(sink), static_cast<hipStream_t>(stream)));
+  FTX_HIP(ftx::launch_mfma_probe(shape, workgroups, iters, static_cast<float *>(sink),
+                                 static_cast<hipStream_t>(stream)));
   return FTX_OK;
 }
 

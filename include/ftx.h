@@ -306,6 +306,13 @@ int ftx_hbm_read_probe(const void *dev, size_t nbytes, void *sink, int grid, voi
  * nothing (sink, 4 bytes of device memory, only on a fixed sentinel): the
  * sustained MFMA rate the compute-bound kernels are measured against. */
 int ftx_mfma_probe(int workgroups, int iters, void *sink, void *stream);
+/* No reference counterpart. ftx_mfma_probe on another MFMA shape:
+ * FTX_MFMA_PROBE_16X16X32 (as above) or FTX_MFMA_PROBE_32X32X16 (each wave
+ * iters x 16 independent v_mfma_f32_32x32x16_bf16 of 32768 flops, the same
+ * flops per iteration). The better of the two is the measured ceiling. */
+#define FTX_MFMA_PROBE_16X16X32 0
+#define FTX_MFMA_PROBE_32X32X16 1
+int ftx_mfma_probe_shape(int shape, int workgroups, int iters, void *sink, void *stream);
 
 #ifdef __cplusplus
 }

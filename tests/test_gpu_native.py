@@ -314,8 +314,11 @@ def test_probes_write_nothing_and_check_arguments(gpu):
     buf = torch.randint(0, 256, (1 << 20,), dtype=torch.uint8, device=gpu)
     nat.call("ftx_hbm_read_probe", buf.data_ptr(), buf.numel(), sink.data_ptr(), 64, s)
     nat.call("ftx_mfma_probe", 8, 16, sink.data_ptr(), s)
+    nat.call("ftx_mfma_probe_shape", 1, 8, 16, sink.data_ptr(), s)
     torch.cuda.synchronize()
     assert int(sink.item()) == -7
+    with pytest.raises(nat.FtxError, match="shape"):
+        nat.call("ftx_mfma_probe_shape", 2, 8, 16, sink.data_ptr(), s)
     with pytest.raises(nat.FtxError):
         nat.call("ftx_hbm_read_probe", buf.data_ptr() + 1, 64, sink.data_ptr(), 64, s)
     with pytest.raises(nat.FtxError):
