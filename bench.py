@@ -1517,6 +1517,12 @@ def main() -> int:
     nat.load()
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.kernel_grid:
+        if args.copy_engine != "kernel":
+            print("bench: --kernel-grid needs --copy-engine kernel (auto chooses its own grid)", file=sys.stderr)
+            return 2
+        kmax, smin, nstreams, _ = nat.get_copy_policy()
+        nat.set_copy_policy(kmax, smin, nstreams, args.kernel_grid)
     if args.engine_contention:
         print(json.dumps(engine_contention()), flush=True)
         return 0
@@ -1546,12 +1552,6 @@ def main() -> int:
                                                                      "split_min_bytes": policy[1],
                                                                      "n_copy_streams": policy[2]}}), flush=True)
         return 0
-    if args.kernel_grid:
-        if args.copy_engine != "kernel":
-            print("bench: --kernel-grid needs --copy-engine kernel (auto chooses its own grid)", file=sys.stderr)
-            return 2
-        kmax, smin, nstreams, _ = nat.get_copy_policy()
-        nat.set_copy_policy(kmax, smin, nstreams, args.kernel_grid)
     if args.calibration_copy_mib:
         src = torch.ones(args.calibration_copy_mib * MiB, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
