@@ -220,13 +220,14 @@ def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
 
 def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
                   include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4,
-                  ring_waits: str = "auto") -> dict:
+                  ring_order: str = "auto") -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
     streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
     units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
     returned under ``_check`` so that runs with other units can be compared bitwise. After the timed
     tokens, ``ring_tokens`` more decode tokens time every ring copy on its own (:func:`ring_copy_stats`).
-    ``ring_waits`` "stream" or "host" overrides how the ring's copies are waited for (:func:`_set_ring_waits`)."""
+    ``ring_order`` "reference" or "link-bound" overrides how the ring's copies are waited for
+    (:func:`_set_ring_order`)."""
     import torch
 
     from flextensor_amd import hip
@@ -249,7 +250,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         model(prompt[:, :16], 0)  # discovery
         model(prompt[:, :16], 0)  # profiling -> plan and loader are built here
     _log(f"llama7b: streaming set up ({mgr.build_seconds:.1f} s to pack, measure the link and build)")
-    _set_ring_waits(mgr, ring_waits)
+    _set_ring_order(mgr, ring_order)
     plan = mgr.plan
     streamed_bytes = sum(mgr._unit(x).nbytes for x in plan.streamed)
     with torch.no_grad():
@@ -307,7 +308,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         "transfer_stream": hip.transfer_stream_probe(dev),
         "ring_copies": ring,
         "ring_copy_engine": _ring_engine(mgr),
-        "ring_waits": _ring_waits(mgr),
+        "ring_order": _ring_order(mgr),
         "_check": {"last_logits": last_logits, "tokens": torch.cat(toks, -1).cpu()},
     }
     mgr.release(preserve_model=False)
@@ -330,16 +331,17 @@ def _ring_roofline(run: dict, measured_peak: float) -> dict | None:
             "by_size": ring["by_size"]}
 
 
-def _set_ring_waits(mgr, how: str) -> None:
-    """Override the manager's choice of ring waits: "stream" (the compute stream waits on each copy's
-    ready event) or "host" (the host blocks on it); "auto" keeps the manager's choice (host waits for a
-    link-bound pass)."""
-    if how != "auto" and hasattr(mgr.loader, "host_waits"):
-        mgr.loader.host_waits = how == "host"
+def _set_ring_order(mgr, how: str) -> None:
+    """Override the manager's choice of ring order: "reference" (the reference's order: the compute stream
+    waits on each copy's ready event) or "link-bound" (the reordered loader blocks the host on it with the
+    next copy queued; the default loader releases a unit's slots before its wait); "auto" keeps the
+    manager's choice (link-bound for a link-bound pass)."""
+    if how != "auto" and hasattr(mgr.loader, "link_bound"):
+        mgr.loader.link_bound = how == "link-bound"
 
 
-def _ring_waits(mgr) -> str:
-    return "host" if getattr(mgr.loader, "host_waits", False) else "stream"
+def _ring_order(mgr) -> str:
+    return "link-bound" if getattr(mgr.loader, "link_bound", False) else "reference"
 
 
 def _ring_engine(mgr) -> str:
@@ -359,7 +361,7 @@ def _ring_engine(mgr) -> str:
     return "SDMA (hipMemcpyAsync)" if mode == nat.COPY_SDMA else "staged"
 
 
-def bench_mlp(steps: int, copy_engine: str) -> dict:
+def bench_mlp(steps: int, copy_engine: str, ring_order: str = "auto") -> dict:
     """The 8-layer 4096->11008->4096 MLP stack, every layer streamed through a 2-slot ring.
 
     Times ``steps`` eager streamed forwards, then the same forward captured in
@@ -385,7 +387,11 @@ def bench_mlp(steps: int, copy_engine: str) -> dict:
     mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
                                      profiling_iters=1, copy_engine=copy_engine))
     with torch.no_grad():
-        for _ in range(4):  # discovery, profiling, two streamed warm-up passes
+        for _ in range(2):  # discovery, then profiling: the plan and the loader are built at its end
+            out = model(x)
+        _set_ring_order(mgr, ring_order)
+        order = _ring_order(mgr)
+        for _ in range(2):  # two streamed warm-up passes
             out = model(x)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -429,6 +435,7 @@ def bench_mlp(steps: int, copy_engine: str) -> dict:
         "eager_effective_GBps": streamed_bytes / t_eager / 1e9,
         "graph_ms_per_forward": 1e3 * t_graph,
         "graph_effective_GBps": streamed_bytes / t_graph / 1e9,
+        "ring_order": order,
         "bitwise_equal_to_resident": eager_ok and graph_ok,
         "cpu_baseline": {"value": 1e3 * t_cpu, "unit": "ms per forward", "cores": torch.get_num_threads(),
                          "kind": "port",
@@ -587,7 +594,7 @@ def _mem_available_bytes() -> int:
 
 
 def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: int, layers: int,
-                       ring_waits: str = "auto") -> dict:
+                       ring_order: str = "auto") -> dict:
     """Batch decode of the 70B-shape decoder with fp8 weights (per-channel bf16 scales) under a GPU budget."""
     import torch
 
@@ -619,7 +626,7 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
     _log(f"70b: built {t_build:.1f} s, profiled and streaming set up {t_setup:.1f} s; "
          f"{len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers; "
          f"{mgr.link.describe() if mgr.link is not None else 'default copy policy'}")
-    _set_ring_waits(mgr, ring_waits)
+    _set_ring_order(mgr, ring_order)
     model.init_cache(batch, prompt_len + decode + 2, dev)
     with torch.no_grad():
         torch.cuda.synchronize()
@@ -650,7 +657,7 @@ def bench_llama70b_fp8(budget_gb: float, batch: int, prompt_len: int, decode: in
             "kernel_max_bytes", "n_copy_streams", "kernel_grid", "link_bound", "pass_compute_ms",
             "pass_transfer_ms")},
         "ring_copy_engine": _ring_engine(mgr),
-        "ring_waits": _ring_waits(mgr),
+        "ring_order": _ring_order(mgr),
     }
     mgr.release(preserve_model=False)
     return out
@@ -1464,8 +1471,9 @@ def main() -> int:
     ap.add_argument("--tensors", type=int, default=2000)
     ap.add_argument("--scatter-steps", type=int, default=5)
     ap.add_argument("--copy-engine", default="auto", choices=["auto", "sdma", "kernel"])
-    ap.add_argument("--ring-waits", default="auto", choices=["auto", "stream", "host"],
-                    help="how the decodes wait for ring copies (auto: on the host in link-bound passes)")
+    ap.add_argument("--ring-order", default="auto", choices=["auto", "reference", "link-bound"],
+                    help="how the streamed legs order their ring waits (auto: link-bound order in link-bound "
+                         "passes)")
     ap.add_argument("--kernel-grid", type=int, default=0,
                     help="zero-copy kernel workgroups for --copy-engine kernel (0: the library default)")
     ap.add_argument("--skip-cpu-baseline", action="store_true")
@@ -1565,7 +1573,7 @@ def main() -> int:
 
     # ---- headline: 7B-shape decoder, 8 GB budget, one decode token per step
     llama = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
-                          ring_waits=args.ring_waits)
+                          ring_order=args.ring_order)
     check = llama.pop("_check")
     _log(f"llama7b: {llama}")
     line = {
@@ -1588,7 +1596,7 @@ def main() -> int:
                    "streamed_layers": llama["streamed_layers"], "resident_layers": llama["resident_layers"],
                    "streamed_bytes_per_token": llama["streamed_bytes_per_token"], "copy_engine": args.copy_engine,
                    "copy_policy": llama["copy_policy"], "copy_policy_source": llama["copy_policy_source"],
-                   "ring_waits": llama["ring_waits"], "transfer_stream": llama["transfer_stream"]},
+                   "ring_order": llama["ring_order"], "transfer_stream": llama["transfer_stream"]},
         "tok_s": round(llama["decode_tok_s"], 3),
         "prefill_tok_s": round(llama["prefill_tok_s"], 1),
         "link": {"decode_effective_GBps": round(llama["decode_effective_GBps"], 3),
@@ -1607,7 +1615,7 @@ def main() -> int:
     # ---- the same decode with each layer's attention and three MLP projections as separate units
     if not args.skip_finer_units:
         fine = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
-                             include_patterns=FINER_UNITS, ring_waits=args.ring_waits)
+                             include_patterns=FINER_UNITS, ring_order=args.ring_order)
         fine_check = fine.pop("_check")
         same = (torch.equal(fine_check["last_logits"], check["last_logits"])
                 and torch.equal(fine_check["tokens"], check["tokens"]))
@@ -1620,7 +1628,7 @@ def main() -> int:
             "pct_of_measured_peak": round(100 * fine["decode_effective_GBps"] / measured_peak, 2),
             "gpu_weight_bytes": fine["gpu_weight_bytes"],
             "copy_policy": fine["copy_policy"],
-            "ring_waits": fine["ring_waits"],
+            "ring_order": fine["ring_order"],
             "ring_copies": _ring_roofline(fine, measured_peak),
             "prefill_logits_and_tokens_bitwise_equal_to_layer_units": same,
         }
@@ -1680,7 +1688,7 @@ def main() -> int:
     if not args.skip_mlp:
         gc.collect()
         torch.cuda.empty_cache()
-        line["mlp8"] = bench_mlp(20, args.copy_engine)
+        line["mlp8"] = bench_mlp(20, args.copy_engine, ring_order=args.ring_order)
         _log(f"mlp8: {line['mlp8']}")
         if not line["mlp8"]["bitwise_equal_to_resident"]:
             print("bench: the streamed MLP forward differs from the resident forward", file=sys.stderr)
@@ -1700,7 +1708,7 @@ def main() -> int:
         _log(f"fp8 linear: {line['fp8_linear']}")
         line["fp8_prefill"] = bench_fp8_prefill()
         _log(f"fp8 prefill: {line['fp8_prefill']}")
-        line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b, ring_waits=args.ring_waits)
+        line["llama70b_fp8"] = bench_llama70b_fp8(24.0, 8, 64, 8, args.layers_70b, ring_order=args.ring_order)
         if not args.skip_cpu_baseline and "skipped" not in line["llama70b_fp8"]:
             line["llama70b_fp8"]["cpu_baseline"] = cpu_llama70b_decode_baseline()
         _log(f"70b: {line['llama70b_fp8']}")

@@ -107,9 +107,11 @@ class _PipelinedLoader(PreallocatedLoader):
         self.first_layer_label = layer_stats[0].label if layer_stats else None
         self.last_layer_label = layer_stats[-1].label if layer_stats else None
         self.preload_transfers = find_transfers_for_preload(self.transfer_to_compute_map, layer_stats)
-        # Wait for ring copies on the host rather than on the compute stream (the reordered loader only;
-        # see its enter). The manager sets it for link-bound passes.
-        self.host_waits = False
+        # The pass waits on the link (the manager sets it for link-bound passes). Each loader then orders
+        # its waits for that: the reordered loader waits for ring copies on the host, the default loader
+        # releases the slots a label read before it waits (see their enter and exit). Graph capture keeps
+        # the reference's order.
+        self.link_bound = False
 
     def _trace(self, label: str) -> str:
         return f"schedule={label} consume={self.transfer_to_compute_map[label]}"
@@ -209,13 +211,19 @@ class PreallocatedBatchTransferTensorLoader(_PipelinedLoader):
     def exit(self, label: str) -> None:
         tc, pp = self.offload_timing_collector, self.piecewise_prefetch_policy
         tc.record_compute_end(label)  # before the wait: compute_ms excludes stalls
+        # link-bound: the slots this label read are released before the wait for the next transfer, so
+        # the transfer after it (into one of those slots) can queue behind it instead of waiting for it
+        early = self.link_bound and not self.backend.is_capturing()
+        if early:
+            self._release_slots(label)
         ticket = self.scheduled_transfers.get(label)
         if ticket is not None:
             tc.record_wait_start(label)
             self._transfer_runtime.wait_ready(ticket)
             pp.on_wait(label)
             tc.record_wait_end(label)
-        self._release_slots(label)
+        if not early:
+            self._release_slots(label)
         self._end_pass_if_last(label)
 
 
@@ -240,7 +248,7 @@ class PreallocatedBatchTransferTensorLoaderReordered(_PipelinedLoader):
     def enter(self, label: str) -> None:
         """Wait for the transfers ``label`` consumes, then submit the one scheduled at ``label``.
 
-        With ``host_waits`` (link-bound passes) the host blocks on each
+        With ``link_bound`` (link-bound passes) the host blocks on each
         transfer instead of the compute stream waiting on it, and the
         transfer scheduled at ``label`` is submitted before that block, so
         the transfer stream already holds the next copy while the host
@@ -255,7 +263,7 @@ class PreallocatedBatchTransferTensorLoaderReordered(_PipelinedLoader):
             rt.begin()
         if label in self._preloaded_compute_labels:
             pp.on_wait(label)
-        host = self.host_waits and not self.backend.is_capturing()
+        host = self.link_bound and not self.backend.is_capturing()
         ahead = host and label in self.label_to_block_id and self.transfer_to_compute_map[label] != label
         if ahead:
             self._submit(label)

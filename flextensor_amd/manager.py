@@ -1098,7 +1098,7 @@ class OffloadManager:
         self.link = link
         self.memory_transfer_stats = link.memory_transfer_stats()
         self.controller.copy_policy = link.native_policy()
-        self._apply_ring_waits()
+        self._apply_link_bound_order()
         self._replan_applied = True
         LOGGER.info("offload %r: replanned: %s", self.name, link.describe())
 
@@ -1647,7 +1647,7 @@ class OffloadManager:
                 # the loader's constructor preloads the first slots: the first copies run here
                 self.loader = cls(layer_stats, self.device, bd.label_to_block_id, bd.transfer_to_compute_map,
                                   self.controller, self.timing, policy)
-                self._apply_ring_waits()
+                self._apply_link_bound_order()
             except BaseException as primary:
                 self._abort_build(primary, tensors_map, bound, n_hooks)
                 raise
@@ -1716,18 +1716,21 @@ class OffloadManager:
         self.memory_transfer_stats = link.memory_transfer_stats()
         LOGGER.info("offload %r: %s", self.name, link.describe())
 
-    def _apply_ring_waits(self) -> None:
-        """A link-bound pass waits for its ring copies on the host; any other pass on the compute stream.
+    def _apply_link_bound_order(self) -> None:
+        """A link-bound pass orders its ring waits for the link; any other pass keeps the reference's order.
 
         While the compute stream waits on a copy's ready event, that copy
         loses 35-40 us per 386 MiB on the MI355X (0.5% of its rate). In a
         link-bound pass the compute stream has nothing to run meanwhile, so
         the reordered loader blocks the host on the copy instead, with the
-        next copy already queued (``host_waits``). A compute-bound pass
-        keeps stream waits, which let the host run ahead of the GPU.
+        next copy already queued; the default loader (every unit streamed)
+        releases the slots a unit read before it waits for the next copy,
+        so the copy after that queues behind it (``link_bound``). A
+        compute-bound pass keeps the reference's order and stream waits,
+        which let the host run ahead.
         """
-        if hasattr(self.loader, "host_waits"):
-            self.loader.host_waits = bool(self.link is not None and self.link.link_bound)
+        if hasattr(self.loader, "link_bound"):
+            self.loader.link_bound = bool(self.link is not None and self.link.link_bound)
 
     def _abort_build(self, primary: BaseException, tensors_map: dict[int, torch.Tensor],
                      bound: dict[int, torch.Tensor], n_hooks: int) -> None:

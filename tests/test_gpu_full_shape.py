@@ -244,7 +244,7 @@ def test_llama7b_full_shape_streamed_equals_resident(gpu):
         assert mgr.plan.streamed and mgr.plan.resident
         assert mgr.get_gpu_memory_usage().total_bytes <= 8_000_000_000
         _say(f"llama7b: {len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers, ring copies "
-             f"waited on the {'host' if mgr.loader.host_waits else 'compute stream'}")
+             f"waited on the {'host' if mgr.loader.link_bound else 'compute stream'}")
         assert torch.equal(got_toks, toks)
         for i, (a, b) in enumerate(zip(got, want)):
             assert torch.equal(a, b), f"step {i}"
@@ -290,7 +290,7 @@ def test_llama70b_fp8_full_shape_streamed_equals_resident(gpu):
         # the decode computes for far less than its streamed layers take on the link: kernel ring copies,
         # waited for on the host by the reordered loader (the plan keeps layers resident)
         assert link.link_bound and mgr.controller.copy_policy.kernel_grid == link.kernel_grid > 0
-        assert plan.reordered and mgr.loader.host_waits
+        assert plan.reordered and mgr.loader.link_bound
         with torch.no_grad():
             got, got_toks = _prefill_and_decode(model, prompt, steps, toks, rec=rec)
         rec.remove()

@@ -64,7 +64,7 @@ def test_link_bound_and_compute_bound_managers_stream_side_by_side(gpu):
         assert pol.kernel_max_bytes < unit_bytes and pol.kernel_grid == 0
         assert nat.get_copy_policy() == default  # neither manager touched the process-wide default
         # the link-bound ring waits for its copies on the host, the compute-bound one on the compute stream
-        assert link_bound.loader.host_waits and not compute_bound.loader.host_waits
+        assert link_bound.loader.link_bound and not compute_bound.loader.link_bound
         for name in rows:
             assert torch.equal(got[name], want[name]), name
         # one manager goes; the other keeps streaming bitwise under its own policy
@@ -109,7 +109,7 @@ def test_a_replan_follows_the_workload_when_the_batch_changes(gpu):
         assert torch.equal(got, want[16])
         assert mgr.plan.resident and mgr.plan.reordered
         assert mgr.link.link_bound and mgr.controller.copy_policy.kernel_grid == L.RING_KERNEL_GRID
-        assert mgr.loader.host_waits
+        assert mgr.loader.link_bound
         assert mgr.strategy_replan_status.can_request
         for rows, x, link_bound in ((32768, large, False), (16, small, True)):
             print(f"replan at {rows} rows", flush=True)
@@ -123,7 +123,7 @@ def test_a_replan_follows_the_workload_when_the_batch_changes(gpu):
             assert status == ft.StrategyReplanStatus("done", True, True), status
             assert mgr.link.link_bound == link_bound and mgr.link.source == "replan", mgr.link.describe()
             assert mgr.controller.copy_policy == mgr.link.native_policy()
-            assert mgr.loader.host_waits == link_bound
+            assert mgr.loader.link_bound == link_bound
             with torch.no_grad():
                 assert torch.equal(model(x), want[rows])  # streaming under the new policy
         assert nat.get_copy_policy() == default

@@ -101,6 +101,7 @@ def _bare_loader(cls):
     loader.transfer_stream = MagicMock()
     loader.last_layer_label = "L_last"
     loader.offload_timing_collector = MagicMock()
+    loader.link_bound = False
     return loader
 
 

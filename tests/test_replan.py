@@ -132,7 +132,7 @@ def test_a_compute_bound_replan_moves_a_link_bound_ring_back_to_the_measured_pol
     run, one_pass = streaming
     mgr = run("replan-down", 1e-6)
     assert mgr.link.link_bound and mgr.controller.copy_policy.kernel_grid == L.RING_KERNEL_GRID
-    assert mgr.loader.host_waits  # a link-bound ring waits for its copies on the host
+    assert mgr.loader.link_bound  # a link-bound ring waits for its copies on the host
     assert mgr.strategy_replan_status == StrategyReplanStatus("idle", True, None)
     compute = [1e6]
     with mock.patch.object(mgr, "_new_replan_collector", lambda: _scripted_collector(mgr.order, compute)):
@@ -151,14 +151,14 @@ def test_a_compute_bound_replan_moves_a_link_bound_ring_back_to_the_measured_pol
     assert not mgr.link.link_bound and mgr.link.source == "replan"
     assert mgr.link.pass_compute_ms == pytest.approx(1e6 * len(mgr.order))
     assert mgr.controller.copy_policy == mgr.link.native_policy() and mgr.controller.copy_policy.kernel_grid == 0
-    assert not mgr.loader.host_waits  # a compute-bound one on the compute stream, so the host runs ahead
+    assert not mgr.loader.link_bound  # a compute-bound one on the compute stream, so the host runs ahead
     # and back: a link-bound replan gives the ring the kernel again
     compute[0] = 1e-6
     with mock.patch.object(mgr, "_new_replan_collector", lambda: _scripted_collector(mgr.order, compute)):
         for _ in range(mgr.request_strategy_replan()):
             one_pass(mgr)
     assert mgr.link.link_bound and mgr.controller.copy_policy.kernel_grid == L.RING_KERNEL_GRID
-    assert mgr.loader.host_waits
+    assert mgr.loader.link_bound
     assert mgr.strategy_replan_status == StrategyReplanStatus("done", True, True)
 
 
@@ -193,7 +193,7 @@ def test_without_a_link_measurement_the_replan_keeps_the_plan(streaming):
     stores the new durations and reports applied=False."""
     run, one_pass = streaming
     mgr = run("replan-keep", 1.0, copy_engine="sdma", link_benchmark=False)
-    assert mgr.link is None and not mgr.loader.host_waits
+    assert mgr.link is None and not mgr.loader.link_bound
     policy = mgr.controller.copy_policy
     with mock.patch.object(mgr, "_new_replan_collector", lambda: _scripted_collector(mgr.order, [7.0])):
         for _ in range(mgr.request_strategy_replan()):

@@ -266,7 +266,7 @@ def _ready_waits(rec, op, stream):
 
 @pytest.mark.parametrize("seed", range(30))
 def test_host_waited_reordered_loader_waits_the_same_copies_on_the_host(seed):
-    """With ``host_waits`` the reordered loader issues the same copies in the same order, waits for each
+    """With ``link_bound`` the reordered loader issues the same copies in the same order, waits for each
     consumed copy on the host before the same forward as the stream-waited loader does on the compute
     stream, never makes the compute stream wait on a copy, and queues each label's copy before it blocks."""
     rng = random.Random(seed)
@@ -278,7 +278,7 @@ def test_host_waited_reordered_loader_waits_the_same_copies_on_the_host(seed):
     streamed, s_rec, _ = _make("reordered", labels, t2c, l2b, slow=True, gaps=gaps)
     _run(streamed, s_rec, labels, passes)
     hosted, h_rec, _ = _make("reordered", labels, t2c, l2b, slow=True, gaps=gaps)
-    hosted.host_waits = True
+    hosted.link_bound = True
     _run(hosted, h_rec, labels, passes)
     copies = [e.target for e in h_rec.log if e.op == "schedule_transfer"]
     assert copies == [e.target for e in s_rec.log if e.op == "schedule_transfer"]
@@ -299,17 +299,60 @@ def test_host_waited_reordered_loader_waits_the_same_copies_on_the_host(seed):
 
 
 @pytest.mark.parametrize("kind", ["default", "reordered"])
-def test_host_waits_keep_the_reference_trace_under_capture_and_in_the_default_loader(kind):
-    """Under graph capture the reordered loader keeps the reference's order and stream waits; the default
-    loader, whose copy is waited in the same unit that issued it, always does."""
+def test_link_bound_keeps_the_reference_trace_under_capture(kind):
+    """Under graph capture a link-bound loader keeps the reference's order and stream waits."""
     labels = ["embed"] + [f"L{i}" for i in range(6)]
     t2c, l2b = _pipeline(labels, {"L2"}, 2, kind == "reordered")
     loader, rec, _ = _make(kind, labels, t2c, l2b, gaps={"L2"})
-    loader.host_waits = True
-    loader.backend.capturing = kind == "reordered"
+    loader.link_bound = True
+    loader.backend.capturing = True
     _run(loader, rec, labels, 2)
     assert rec.triples() == osch.trace(kind, labels, t2c, l2b, osch.passes(labels, 2))
     assert not rec.find("synchronize_event")
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_link_bound_default_loader_releases_before_its_wait(seed):
+    """A link-bound default loader issues the same copies in the same order and makes the compute stream
+    wait for each before the same forward as the reference's order, but records the release of the slots
+    a label read before that wait, so the copy into one of them can queue behind the awaited one."""
+    rng = random.Random(seed)
+    n = rng.randrange(2, 11)
+    labels = ["embed"] + [f"L{i}" for i in range(n - 1)]
+    gaps = set(rng.sample(labels[1:], rng.randrange(0, max(1, n // 3))))
+    t2c, l2b = _pipeline(labels, gaps, rng.choice([2, 3]), False)
+    passes = rng.choice([1, 2, 3])
+    ref, r_rec, _ = _make("default", labels, t2c, l2b, slow=True, gaps=gaps)
+    _run(ref, r_rec, labels, passes)
+    early, e_rec, _ = _make("default", labels, t2c, l2b, slow=True, gaps=gaps)
+    early.link_bound = True
+    _run(early, e_rec, labels, passes)
+    assert [e.target for e in e_rec.log if e.op == "schedule_transfer"] == \
+        [e.target for e in r_rec.log if e.op == "schedule_transfer"]
+    assert _ready_waits(e_rec, "wait_event", "compute") == _ready_waits(r_rec, "wait_event", "compute")
+    assert sorted(e_rec.ops()) == sorted(r_rec.ops())  # the same operations, reordered
+    # within each exit (between a forward and the next schedule or forward), the compute stream's release
+    # record precedes its wait on a transfer; in the reference's order it follows it
+    for rec, release_first in ((e_rec, True), (r_rec, False)):
+        ready, pending = set(), False
+        for e in rec.log:  # a submit records its ready event right after the copy
+            if e.op == "schedule_transfer":
+                pending = True
+            elif (e.op, e.stream) == ("record_event", "transfer") and pending:
+                ready.add(e.target)
+                pending = False
+        segment: list = []
+        for e in [*rec.log, None]:
+            if e is None or e.op in ("forward", "schedule_transfer"):
+                ops = [(x.op, x.stream, x.target in ready) for x in segment]
+                waits = [i for i, (op, st, is_ready) in enumerate(ops) if (op, st, is_ready) == ("wait_event", "compute", True)]
+                releases = [i for i, (op, st, _) in enumerate(ops) if (op, st) == ("record_event", "compute")]
+                if waits and releases:
+                    assert (releases[0] < waits[0]) == release_first, rec.dump()
+                segment = []
+            else:
+                segment.append(e)
+    assert not early.scheduled_transfers and not early._transfer_runtime.is_active
 
 
 @pytest.mark.parametrize("kind", ["default", "reordered"])
