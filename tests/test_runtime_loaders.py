@@ -285,6 +285,7 @@ def test_host_waited_reordered_loader_waits_the_same_copies_on_the_host(seed):
     waited = _ready_waits(s_rec, "wait_event", "compute")
     assert _ready_waits(h_rec, "synchronize_event", "host") == waited
     assert _ready_waits(h_rec, "wait_event", "compute") == []
+    assert _host_waited_before_use(h_rec, t2c), h_rec.dump()
     # between two forwards, the copy scheduled there is queued before the host blocks
     segment: list = []
     for e in [*h_rec.log, None]:
@@ -353,6 +354,46 @@ def test_link_bound_default_loader_releases_before_its_wait(seed):
             else:
                 segment.append(e)
     assert not early.scheduled_transfers and not early._transfer_runtime.is_active
+
+
+def _host_waited_before_use(rec, t2c) -> bool:
+    """Every copy a unit consumes is host-synchronized before the unit's forward, unless a join (the
+    compute stream waiting on the transfer stream's tail) ordered it first."""
+    pending: dict = {}  # consumer -> ready events not yet ordered before it
+    waited, last_schedule, ready = set(), None, set()
+    for e in rec.log:
+        if e.op == "schedule_transfer":
+            last_schedule = e.target
+        elif (e.op, e.stream) == ("record_event", "transfer") and last_schedule is not None:
+            pending.setdefault(t2c[last_schedule], []).append(e.target)
+            ready.add(e.target)
+            last_schedule = None
+        elif e.op == "synchronize_event":
+            waited.add(e.target)
+        elif (e.op, e.stream) == ("wait_event", "compute") and e.target not in ready:
+            pending.clear()  # a join: everything queued before it is ordered
+        elif e.op == "forward":
+            if any(ev not in waited for ev in pending.pop(e.target, [])):
+                return False
+    return True
+
+
+def test_link_bound_abort_recovery_reloads_and_waits_on_the_host():
+    """A link-bound reordered pass that stops early leaves copies in flight; the next pass joins, loads
+    its first slots again, and blocks the host on every copy a unit consumes before that unit runs."""
+    labels = ["L0", "L1", "L2", "L3"]
+    t2c = {"L0": "L1", "L1": "L2", "L2": "L3", "L3": "L0"}
+    l2b = {"L0": 0, "L1": 1, "L2": 0, "L3": 1}
+    loader, rec, _ = _make("reordered", labels, t2c, l2b, slow=True)
+    loader.link_bound = True
+    for op, x in [("enter", "L0"), ("forward", "L0"), ("exit", "L0"), ("enter", "L1")]:  # stops in L1
+        getattr(loader, op)(x) if op != "forward" else rec.forward(x)
+    rec.log.clear()
+    _run(loader, rec, labels, 2)
+    assert [e.target for e in rec.log if e.op == "schedule_transfer"][0] == "L3"  # L0's slot loaded again
+    assert _ready_waits(rec, "wait_event", "compute") == []
+    assert _host_waited_before_use(rec, t2c), rec.dump()
+    assert rec.find("synchronize_event")
 
 
 @pytest.mark.parametrize("kind", ["default", "reordered"])
