@@ -242,6 +242,8 @@ def test_llama7b_full_shape_streamed_equals_resident(gpu):
             got, got_toks = _prefill_and_decode(model, prompt, 4, rec=rec)
         rec.remove()
         assert mgr.plan.streamed and mgr.plan.resident
+        # the first unit streams: its copy is the cyclic preload issued in the previous pass
+        assert mgr.plan.streamed[0] == "layers.0" and mgr.plan.reordered
         assert mgr.get_gpu_memory_usage().total_bytes <= 8_000_000_000
         _say(f"llama7b: {len(mgr.plan.streamed)} streamed / {len(mgr.plan.resident)} resident layers, ring copies "
              f"waited on the {'host' if mgr.loader.link_bound else 'compute stream'}")
