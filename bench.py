@@ -1500,6 +1500,8 @@ def main() -> int:
     ap.add_argument("--staged-sweep", action="store_true",
                     help="only print host-to-device GB/s of the staged engine from pageable and shared memory")
     ap.add_argument("--dit-only", action="store_true", help="print only the DiT leg (for profiling it alone)")
+    ap.add_argument("--mlp-only", action="store_true",
+                    help="print only the 8-layer MLP stack leg (for profiling it alone)")
     ap.add_argument("--fp8-linear-only", action="store_true",
                     help="only print the fp8 linear roofline on the 70B-shape decode projections")
     ap.add_argument("--layers-70b", type=int, default=80)
@@ -1542,6 +1544,9 @@ def main() -> int:
         return 0
     if args.dit_only:
         print(json.dumps({"dit": bench_dit(12.0, args.dit_tokens, 512, args.dit_steps, args.copy_engine)}), flush=True)
+        return 0
+    if args.mlp_only:
+        print(json.dumps({"mlp8": bench_mlp(20, args.copy_engine, ring_order=args.ring_order)}), flush=True)
         return 0
     if args.staged_sweep:
         print(json.dumps({"staged_sweep": staged_sweep()}), flush=True)
