@@ -204,13 +204,15 @@ int copy_sdma(void *dst, const void *src, size_t nbytes, hipStream_t stream, con
   int rc = device_state(&st);
   if (rc != FTX_OK) return rc;
   const int k = std::min(pol.n_copy_streams, kMaxCopyStreams);
-  {
-    std::lock_guard<std::mutex> lock(g_dev_mutex);
-    if (!st->fork_event) FTX_HIP(hipEventCreateWithFlags(&st->fork_event, hipEventDisableTiming));
-    for (int i = 0; i < k; ++i) {
-      if (!st->copy_streams[i]) FTX_HIP(hipStreamCreateWithFlags(&st->copy_streams[i], hipStreamNonBlocking));
-      if (!st->join_events[i]) FTX_HIP(hipEventCreateWithFlags(&st->join_events[i], hipEventDisableTiming));
-    }
+  // Every split copy on this device shares the fork and join events, so one
+  // copy's record-and-wait sequence is enqueued whole: a copy made from another
+  // host thread in between would re-record the fork event, and this copy's
+  // pieces would then wait on the other caller's stream instead of this one.
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  if (!st->fork_event) FTX_HIP(hipEventCreateWithFlags(&st->fork_event, hipEventDisableTiming));
+  for (int i = 0; i < k; ++i) {
+    if (!st->copy_streams[i]) FTX_HIP(hipStreamCreateWithFlags(&st->copy_streams[i], hipStreamNonBlocking));
+    if (!st->join_events[i]) FTX_HIP(hipEventCreateWithFlags(&st->join_events[i], hipEventDisableTiming));
   }
   const size_t align = size_t(1) << 16;
   size_t piece = (nbytes + k - 1) / k;
