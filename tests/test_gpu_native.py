@@ -129,6 +129,45 @@ def test_split_sdma_over_copy_streams(gpu, per_call):
         nat.set_copy_policy(*old)
 
 
+def test_split_sdma_from_two_host_threads(gpu):
+    """Split copies made from two host threads at once, each on its own stream right after a fill of its
+    destination. The split copies of a device share their fork and join events, so each copy's pieces must
+    still start after its own stream's fill: every destination ends up holding its own source bytes."""
+    import threading
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd.hip import new_stream
+
+    policy = nat.copy_policy(0, 1 << 20, 4, 0)
+    n = (24 << 20) + 77
+    datas = [_rand_bytes(n, seed=40 + i) for i in range(2)]
+    arenas = [_arena_with(d) for d in datas]
+    dsts = [torch.empty(n, dtype=torch.uint8, device=gpu) for _ in range(2)]
+    streams = [new_stream(gpu) for _ in range(2)]
+    torch.cuda.synchronize()
+    start = threading.Barrier(2)
+    errors: list[BaseException] = []
+
+    def worker(i: int) -> None:
+        try:
+            start.wait()
+            for _ in range(20):
+                nat.call("ftx_memset_async", dsts[i].data_ptr(), 0x5A, n, streams[i].handle)
+                nat.copy_h2d(dsts[i].data_ptr(), arenas[i].ptr, n, nat.COPY_SDMA, streams[i].handle, policy)
+        except BaseException as exc:  # reported by the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for dst, data in zip(dsts, datas):
+        assert np.array_equal(dst.cpu().numpy(), data)
+
+
 def _scatter_case(seed: int, n_desc: int, max_bytes: int, align_dst: bool):
     rng = np.random.default_rng(seed)
     sizes = np.exp(rng.uniform(np.log(1), np.log(max_bytes), size=n_desc)).astype(np.int64)
