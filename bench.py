@@ -207,12 +207,20 @@ def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
     finally:
         loader.offload_timing_collector = kept
     by_size: dict[int, list[float]] = {}
+    link: dict[int, list[int]] = {}  # bytes each launch read over the link (less than n for an encoded block)
+    ctl = mgr.controller
     for snap in report.passes:
         for rec in snap.per_trap:
             if rec.transfer_ms > 0:
-                by_size.setdefault(mgr.controller.transfer_bytes(rec.label), []).append(rec.transfer_ms)
+                n = ctl.transfer_bytes(rec.label)
+                by_size.setdefault(n, []).append(rec.transfer_ms)
+                link.setdefault(n, []).append(ctl.link_bytes(rec.label) if hasattr(ctl, "link_bytes") else n)
     sizes = {n: {"launches": len(ms), "mean_us": round(1e3 * sum(ms) / len(ms), 1),
                  "GBps": round(n * len(ms) / sum(ms) / 1e6, 3)} for n, ms in sorted(by_size.items())}
+    for n, v in sizes.items():
+        if sum(link[n]) != n * len(link[n]):
+            v["link_bytes_mean"] = round(sum(link[n]) / len(link[n]))
+            v["link_GBps"] = round(sum(link[n]) / sum(by_size[n]) / 1e6, 3)
     top = max(by_size, key=lambda n: n * len(by_size[n]))
     return {"passes": report.num_passes, "by_size": {str(n): v for n, v in sizes.items()}, "dominant_bytes": top,
             "dominant": sizes[top]}
@@ -220,14 +228,15 @@ def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
 
 def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
                   include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4,
-                  ring_order: str = "auto") -> dict:
+                  ring_order: str = "auto", encode: bool = False) -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
     streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
     units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
     returned under ``_check`` so that runs with other units can be compared bitwise. After the timed
     tokens, ``ring_tokens`` more decode tokens time every ring copy on its own (:func:`ring_copy_stats`).
     ``ring_order`` "reference" or "link-bound" overrides how the ring's copies are waited for
-    (:func:`_set_ring_order`)."""
+    (:func:`_set_ring_order`). ``encode`` streams the blocks exponent-coded
+    (``OffloadConfig.encode_streamed_blocks``)."""
     import torch
 
     from flextensor_amd import hip
@@ -241,7 +250,8 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     _log(f"llama7b: built in {time.perf_counter() - t0:.1f} s")
     mgr = OffloadManager("bench-llama")
     cfg = OffloadConfig(include_patterns=list(include_patterns), num_blocks=2, min_blocks=2, discovery_iters=1,
-                        profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9), copy_engine=copy_engine)
+                        profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9), copy_engine=copy_engine,
+                        encode_streamed_blocks=encode)
     mgr.offload(model, cfg)
     prompt = W.prompt_tokens(1, prefill, W.LLAMA_7B.vocab, seed=0).to(dev)
     total = prefill + warmup + steps + ring_tokens + 2
@@ -253,6 +263,9 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     _set_ring_order(mgr, ring_order)
     plan = mgr.plan
     streamed_bytes = sum(mgr._unit(x).nbytes for x in plan.streamed)
+    ctl = mgr.controller
+    link_bytes = sum(ctl.link_bytes(x) for x in ctl.block_map_cpu) if ctl is not None else 0
+    encoded = len(getattr(ctl, "encoded", {}) or {})
     with torch.no_grad():
         model.init_cache(1, total, dev)
         W.generate(model, prompt, 2)  # warm-up pass
@@ -296,6 +309,9 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         "ms_per_token": 1e3 * t_decode / steps,
         "streamed_bytes_per_token": streamed_bytes,
         "decode_effective_GBps": streamed_bytes * steps / t_decode / 1e9,
+        "link_bytes_per_token": link_bytes,
+        "decode_link_GBps": link_bytes * steps / t_decode / 1e9,
+        "encoded_blocks": encoded,
         "streamed_layers": len(plan.streamed),
         "resident_layers": len(plan.resident),
         "gpu_weight_bytes": usage.total_bytes,
@@ -349,6 +365,8 @@ def _ring_engine(mgr) -> str:
     from flextensor_amd import _native as nat
 
     ctl = mgr.controller
+    if getattr(ctl, "encoded", None):
+        return "expcode_decode_kernel (16 workgroups)"
     mode, policy = ctl.copy_mode, ctl.copy_policy
     if mode == nat.COPY_AUTO:
         if policy is None:
@@ -1496,6 +1514,8 @@ def main() -> int:
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--skip-finer-units", action="store_true",
                     help="skip the 7B decode with attention and MLP projections as separate offload units")
+    ap.add_argument("--skip-encoded", action="store_true",
+                    help="skip the 7B decode with exponent-coded blocks (OffloadConfig.encode_streamed_blocks)")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
     ap.add_argument("--staged-sweep", action="store_true",
                     help="only print host-to-device GB/s of the staged engine from pageable and shared memory")
@@ -1643,6 +1663,35 @@ def main() -> int:
         torch.cuda.empty_cache()
         if not same:
             print("bench: the finer-unit decode differs from the whole-layer decode", file=sys.stderr)
+            return 1
+
+    if not args.skip_encoded:
+        enc = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
+                            ring_order=args.ring_order, encode=True)
+        enc_check = enc.pop("_check")
+        same = (torch.equal(enc_check["last_logits"], check["last_logits"])
+                and torch.equal(enc_check["tokens"], check["tokens"]))
+        line["llama7b_encoded_blocks"] = {
+            "encoded_blocks": enc["encoded_blocks"], "streamed_layers": enc["streamed_layers"],
+            "streamed_bytes_per_token": enc["streamed_bytes_per_token"],
+            "link_bytes_per_token": enc["link_bytes_per_token"],
+            "link_bytes_ratio": round(enc["link_bytes_per_token"] / enc["streamed_bytes_per_token"], 4),
+            "tok_s": round(enc["decode_tok_s"], 3), "ms_per_token": round(enc["ms_per_token"], 3),
+            "decode_effective_GBps": round(enc["decode_effective_GBps"], 3),
+            "decode_link_GBps": round(enc["decode_link_GBps"], 3),
+            "link_pct_of_measured_peak": round(100 * enc["decode_link_GBps"] / measured_peak, 2),
+            "speedup_vs_raw_blocks": round(enc["decode_tok_s"] / llama["decode_tok_s"], 4),
+            "prefill_tok_s": round(enc["prefill_tok_s"], 1),
+            "ring_order": enc["ring_order"],
+            "ring_copies": _ring_roofline(enc, measured_peak),
+            "prefill_logits_and_tokens_bitwise_equal_to_raw_blocks": same,
+        }
+        _log(f"llama7b encoded blocks: {line['llama7b_encoded_blocks']}")
+        del enc, enc_check
+        gc.collect()
+        torch.cuda.empty_cache()
+        if not same:
+            print("bench: the decode with encoded blocks differs from the decode with raw blocks", file=sys.stderr)
             return 1
 
     # ---- the scatter microbenchmark and the scatter kernel's HBM roofline

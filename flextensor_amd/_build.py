@@ -16,7 +16,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libftx_hip.so"
-SOURCES = ("ftx_runtime.hip", "ftx_kernels.hip", "ftx_gemm.hip", "ftx_staged.hip")
+SOURCES = ("ftx_runtime.hip", "ftx_kernels.hip", "ftx_gemm.hip", "ftx_staged.hip", "ftx_expcode.hip")
 OFFLOAD_ARCH = "gfx950"
 
 

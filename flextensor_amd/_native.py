@@ -154,6 +154,9 @@ _SIGNATURES: dict[str, list] = {
     "ftx_set_fp8_linear_config": [_int, _int],
     "ftx_fp8_linear_fused_workspace": [ctypes.c_int64, _vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
                                        ctypes.POINTER(_sz)],
+    "ftx_expcode_encode": [_vp, _sz, _vp, _sz, ctypes.POINTER(_sz)],
+    "ftx_expcode_raw_bytes": [_vp, _sz, ctypes.POINTER(_sz)],
+    "ftx_expcode_decode_h2d": [_vp, _vp, _sz, ctypes.POINTER(CopyPolicy), _vp],
     "ftx_fp8_linear_fused": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _vp,
                              _vp, _sz, _vp],
 }

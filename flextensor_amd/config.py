@@ -29,8 +29,9 @@ Accepted for compatibility, acting differently or not at all here:
 
 Added for this build: ``max_gpu_mem_bytes`` (a budget in bytes instead of a
 fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel`` / ``staged``),
-``loader_order`` (``auto`` / ``default`` / ``reordered``) and
-``max_inflight_passes`` (bounded host run-ahead).
+``loader_order`` (``auto`` / ``default`` / ``reordered``),
+``max_inflight_passes`` (bounded host run-ahead) and ``encode_streamed_blocks``
+(streamed blocks cross the link exponent-coded and are decoded on the GPU).
 """
 
 from __future__ import annotations
@@ -81,6 +82,10 @@ class OffloadConfig(BaseModel):
     # that runs further ahead fills the device command queue and then issues
     # each next transfer late, which idles the host link.
     max_inflight_passes: int = Field(default=1, ge=0)
+    # Carry each streamed block over the link exponent-coded (about 0.75 of its bytes for bf16 weights)
+    # and decode it into its ring slot with a zero-copy kernel; the slot receives the raw bytes exactly.
+    # A block is kept encoded only when that saves a tenth of its bytes. allocation_block_transfer only.
+    encode_streamed_blocks: bool = False
     # Cross-process sharing of the streamed blocks through POSIX shared memory
     # (config.py:97-125): blocks live in named segments under ``shm_namespace``.
     shm_enabled: bool = False
@@ -102,6 +107,8 @@ class OffloadConfig(BaseModel):
             raise ValueError(f"transfer_mode must be one of {TRANSFER_MODES}, got {self.transfer_mode!r}")
         if self.shm_enabled and (self.shm_namespace is None or not self.shm_namespace.strip()):
             raise ValueError("shm_namespace must be non-empty when shm_enabled=True")
+        if self.encode_streamed_blocks and self.transfer_mode != "allocation_block_transfer":
+            raise ValueError("encode_streamed_blocks needs transfer_mode='allocation_block_transfer'")
         if self.num_blocks < self.min_blocks:
             raise ValueError(f"num_blocks ({self.num_blocks}) must be >= min_blocks ({self.min_blocks})")
         if self.profile_mode == "torch_function":

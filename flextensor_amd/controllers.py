@@ -184,10 +184,14 @@ class AllocationBlockController:
         memory_alignment: int = 128,
         shm_block_name_map: Mapping[str, str] | None = None,
         load_from_shm: bool = False,
+        encode_blocks: bool = False,
     ) -> None:
         """``shm_block_name_map`` puts each label's host block in a named shared-memory
         segment (loaders.py:1150-1175); with ``load_from_shm`` the segments already exist
-        and are mapped instead of packed, and the tensors only supply their layouts."""
+        and are mapped instead of packed, and the tensors only supply their layouts.
+        ``encode_blocks`` keeps an exponent-coded copy of each label's block that saves at least a
+        tenth of its bytes (:mod:`~flextensor_amd.expcode`); such a label's transfer is one decode
+        launch that writes the raw block into its slot (no reference counterpart)."""
         if load_from_shm and not shm_block_name_map:
             raise ValueError("load_from_shm needs shm_block_name_map")
         self.device_gpu = torch.device(device_gpu)
@@ -205,6 +209,7 @@ class AllocationBlockController:
         self.label_to_tensor_views_map: dict[str, list[torch.Tensor]] = {}
         self.tensor_id_to_view_map: dict[int, torch.Tensor] = {}
         self._gpu_slots: list[AllocationBlock] = []
+        self.encoded: dict[str, Any] = {}  # label -> expcode.EncodedBlock
         self._rollback = _Rollback()
         _refuse_overlapping_sources(tensors_map, strategy_map)
         try:
@@ -238,6 +243,13 @@ class AllocationBlockController:
                 self.label_to_tensor_views_map[label] = views
                 self.block_map_gpu[label_to_block_id[label]] = prefix
                 self.gpu_block_view_map[label] = prefix
+            if encode_blocks:
+                from . import expcode
+
+                for label, block in self.block_map_cpu.items():
+                    enc = expcode.encode_if_smaller(block.block)
+                    if enc is not None:
+                        self.encoded[label] = enc
             self.prepare_tensor_id_to_view_mapping()
         except BaseException as primary:
             # sources restored, segments this build created removed, maps cleared
@@ -257,12 +269,36 @@ class AllocationBlockController:
         return self.block_map_cpu[label].views
 
     def schedule_transfer(self, label: str, non_blocking: bool = True) -> None:
-        """One host-to-device copy of ``label``'s block into its slot, on the current stream."""
-        self.block_map_cpu[label].copy_to(self.gpu_block_view_map[label], non_blocking=non_blocking,
-                                          mode=self.copy_mode, policy=self.copy_policy)
+        """One host-to-device copy of ``label``'s block into its slot, on the current stream: a decode
+        launch for an encoded block (its workgroups hold the link at its peak, so the copy policy's grid
+        does not apply), else a copy under this controller's copy policy."""
+        enc = self.encoded.get(label)
+        if enc is None:
+            self.block_map_cpu[label].copy_to(self.gpu_block_view_map[label], non_blocking=non_blocking,
+                                              mode=self.copy_mode, policy=self.copy_policy)
+            return
+        from .expcode import decode_h2d
+        from .hip import current_stream
+
+        dst = self.gpu_block_view_map[label]
+        decode_h2d(dst, enc)
+        if not non_blocking:
+            current_stream(dst.device).synchronize()
 
     def transfer_bytes(self, label: str) -> int:
+        """Bytes ``label``'s transfer writes into its slot (the raw block)."""
         return self.block_map_cpu[label].nbytes
+
+    def refresh_encoded(self) -> None:
+        """Re-encode every encoded block in place from its host block, after the host blocks were
+        rewritten (a state-dict load). No transfer may be in flight."""
+        for label, enc in self.encoded.items():
+            enc.reencode(self.block_map_cpu[label].block)
+
+    def link_bytes(self, label: str) -> int:
+        """Bytes ``label``'s transfer reads over the host link: the encoded block when there is one."""
+        enc = self.encoded.get(label)
+        return enc.nbytes if enc is not None else self.block_map_cpu[label].nbytes
 
     def commit_construction(self) -> None:
         self._rollback.commit()
@@ -274,6 +310,7 @@ class AllocationBlockController:
             _cleanup_keeping_error(self, primary_error)
 
     def _clear(self) -> None:
+        self.encoded.clear()
         for d in (self.block_map_cpu, self.label_to_cpu_tensor_id_map, self.label_to_gpu_block, self.block_map_gpu,
                   self.gpu_block_view_map, self.label_to_tensor_views_map, self.tensor_id_to_view_map):
             d.clear()

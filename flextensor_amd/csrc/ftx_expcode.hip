@@ -1,0 +1,343 @@
+// Exponent-coded blocks: a lossless encoding of streamed bf16 weight blocks
+// that carries about three quarters of the raw bytes over the host link, and
+// the zero-copy kernel that decodes one straight from mapped host memory into
+// its ring slot.
+//
+// bf16 weights drawn from one distribution use few exponents: the 7B-shape
+// layers (N(0, 0.02)) have about 2.5 bits of exponent entropy and 15
+// exponents cover all but 0.02% of their words. A block of N raw bytes is read
+// as W = N / 2 little-endian 16-bit words (sign bit 15, exponent 14..7,
+// mantissa 6..0) in groups of 1024 words; an odd last byte is kept verbatim:
+//
+//   header (64 bytes, zero padded to 256): "FTXE", u32 version 1, u64 N, u64 W,
+//       u64 G (groups), u64 E (escapes), table[16], u8 tail byte, 7 zero bytes
+//   plane A at 256:           G*1024 bytes, sign << 7 | mantissa of each word
+//   plane B at 256 + 1024 G:  G*512 bytes, a 4-bit code per word (low nibble
+//                             first): code c < 15 is exponent table[c], 15 an
+//                             escape
+//   S at 256 + 1536 G:        G + 1 u32, escapes before each group
+//   X at S + align16(4 (G+1)): E u32, (word % 1024) << 8 | exponent, one per
+//                             escaped word in word order
+//
+// The table holds the 15 most frequent exponents, most frequent first, ties to
+// the smaller exponent. The encoded size is 256 + 1536 G + align16(4 (G+1)) +
+// 4 E bytes. The decode kernel reads planes A and B with 16- and 8-byte loads
+// per lane (coalesced across the wave, as the zero-copy copy's 16-byte loads),
+// rebuilds 16 words per lane in registers and writes them with two 16-byte
+// non-temporal stores; a group's escapes, when it has any, are patched from X.
+// Each lane holds eight groups' loads in flight.
+#include <algorithm>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "ftx_internal.h"
+
+namespace ftx {
+
+namespace {
+
+struct ExpHeader {
+  char magic[4];
+  uint32_t version;
+  uint64_t n;
+  uint64_t n_words;
+  uint64_t groups;
+  uint64_t escapes;
+  uint8_t table[16];
+  uint8_t tail;
+  uint8_t pad[7];
+};
+static_assert(sizeof(ExpHeader) == 64, "header layout");
+
+constexpr uint32_t kExpVersion = 1;
+constexpr uint32_t kExpEscape = 15;
+
+void sections(uint64_t groups, uint64_t escapes, ExpcodeInfo *p) {
+  p->off_b = kExpcodeHeaderBytes + kExpcodeGroupWords * groups;
+  p->off_s = p->off_b + kExpcodeGroupWords / 2 * groups;
+  p->off_x = p->off_s + (4 * (groups + 1) + 15) / 16 * 16;
+  p->total = p->off_x + 4 * escapes;
+}
+
+inline uint32_t word_at(const uint8_t *raw, uint64_t w) {
+  return static_cast<uint32_t>(raw[2 * w]) | (static_cast<uint32_t>(raw[2 * w + 1]) << 8);
+}
+
+// Runs f(begin, end) over [0, n) on up to `threads` threads (the caller is one).
+template <class F>
+void parallel_for(uint64_t n, int threads, F f) {
+  if (threads <= 1 || n < 2) {
+    f(0, n);
+    return;
+  }
+  const uint64_t t = std::min<uint64_t>(static_cast<uint64_t>(threads), n);
+  const uint64_t chunk = (n + t - 1) / t;
+  std::vector<std::thread> pool;
+  for (uint64_t i = 1; i < t; ++i) {
+    const uint64_t b = i * chunk, e = std::min(n, b + chunk);
+    if (b < e) pool.emplace_back([=] { f(b, e); });
+  }
+  f(0, std::min(n, chunk));
+  for (auto &th : pool) th.join();
+}
+
+int encode_threads(uint64_t n_words) {
+  if (n_words < (uint64_t(1) << 20)) return 1;
+  const unsigned hw = std::thread::hardware_concurrency();
+  return static_cast<int>(std::clamp<unsigned>(hw / 2, 1u, 16u));
+}
+
+// Exponent histogram, table and sizes of a raw block.
+struct ExpPlan {
+  ExpcodeInfo info;
+  uint8_t code_of[256];
+};
+
+int plan(const uint8_t *raw, uint64_t n, ExpPlan *p) {
+  ExpcodeInfo &info = p->info;
+  info = ExpcodeInfo{};
+  info.n = n;
+  info.n_words = n / 2;
+  info.groups = (info.n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  if (info.groups >= (uint64_t(1) << 32)) return fail(FTX_ERR_INVALID, "block too large to encode");
+  const int threads = encode_threads(info.n_words);
+  std::vector<uint64_t> hists(static_cast<size_t>(std::max(threads, 1)) * 256, 0);
+  const uint64_t chunk = (info.n_words + threads - 1) / std::max(threads, 1);
+  parallel_for(info.n_words, threads, [&](uint64_t b, uint64_t e) {
+    uint64_t *h = hists.data() + (chunk ? b / chunk : 0) * 256;
+    for (uint64_t w = b; w < e; ++w) ++h[(word_at(raw, w) >> 7) & 0xff];
+  });
+  uint64_t hist[256] = {};
+  for (int t = 0; t < threads; ++t)
+    for (int x = 0; x < 256; ++x) hist[x] += hists[static_cast<size_t>(t) * 256 + x];
+  std::vector<int> ranked;
+  for (int x = 0; x < 256; ++x)
+    if (hist[x]) ranked.push_back(x);
+  std::stable_sort(ranked.begin(), ranked.end(), [&](int a, int b) { return hist[a] > hist[b]; });
+  std::memset(p->code_of, kExpEscape, sizeof(p->code_of));
+  uint64_t covered = 0;
+  for (size_t c = 0; c < ranked.size() && c < kExpEscape; ++c) {
+    info.table[c] = static_cast<uint8_t>(ranked[c]);
+    p->code_of[ranked[c]] = static_cast<uint8_t>(c);
+    covered += hist[ranked[c]];
+  }
+  info.escapes = info.n_words - covered;
+  if (info.escapes >= (uint64_t(1) << 32)) return fail(FTX_ERR_INVALID, "block has too many escaped words to encode");
+  info.tail = n % 2 ? raw[n - 1] : 0;
+  sections(info.groups, info.escapes, &info);
+  return FTX_OK;
+}
+
+}  // namespace
+
+int expcode_encode(const void *raw_v, size_t nbytes, void *out_v, size_t out_capacity, size_t *out_bytes) {
+  const auto *raw = static_cast<const uint8_t *>(raw_v);
+  ExpPlan p;
+  int rc = plan(raw, nbytes, &p);
+  if (rc != FTX_OK) return rc;
+  const ExpcodeInfo &info = p.info;
+  *out_bytes = static_cast<size_t>(info.total);
+  if (out_v == nullptr) return FTX_OK;
+  if (out_capacity < info.total)
+    return fail(FTX_ERR_INVALID, "output buffer of " + std::to_string(out_capacity) + " bytes is smaller than the " +
+                                     std::to_string(info.total) + " the encoded block needs");
+  auto *out = static_cast<uint8_t *>(out_v);
+  std::memset(out, 0, kExpcodeHeaderBytes);
+  ExpHeader h{};
+  std::memcpy(h.magic, "FTXE", 4);
+  h.version = kExpVersion;
+  h.n = info.n;
+  h.n_words = info.n_words;
+  h.groups = info.groups;
+  h.escapes = info.escapes;
+  std::memcpy(h.table, info.table, 16);
+  h.tail = info.tail;
+  std::memcpy(out, &h, sizeof(h));
+  const uint64_t G = info.groups, W = info.n_words;
+  std::vector<uint32_t> counts(static_cast<size_t>(G), 0);
+  const int threads = encode_threads(W);
+  uint8_t *A = out + kExpcodeHeaderBytes, *B = out + info.off_b;
+  parallel_for(G, threads, [&](uint64_t gb, uint64_t ge) {
+    for (uint64_t g = gb; g < ge; ++g) {
+      const uint64_t w0 = g * kExpcodeGroupWords;
+      const uint64_t wn = std::min<uint64_t>(kExpcodeGroupWords, W - w0);
+      uint32_t cnt = 0;
+      for (uint64_t j = 0; j < kExpcodeGroupWords; j += 2) {
+        uint32_t c[2] = {0, 0};
+        for (int k = 0; k < 2; ++k) {
+          uint8_t a = 0;
+          if (j + k < wn) {
+            const uint32_t word = word_at(raw, w0 + j + k);
+            a = static_cast<uint8_t>(((word >> 8) & 0x80) | (word & 0x7f));
+            c[k] = p.code_of[(word >> 7) & 0xff];
+            cnt += c[k] == kExpEscape;
+          }
+          A[w0 + j + k] = a;
+        }
+        B[(w0 + j) / 2] = static_cast<uint8_t>(c[0] | (c[1] << 4));
+      }
+      counts[static_cast<size_t>(g)] = cnt;
+    }
+  });
+  std::vector<uint32_t> S(static_cast<size_t>(G) + 1, 0);
+  for (uint64_t g = 0; g < G; ++g) S[static_cast<size_t>(g) + 1] = S[static_cast<size_t>(g)] + counts[static_cast<size_t>(g)];
+  if (S[static_cast<size_t>(G)] != info.escapes) return fail(FTX_ERR_INVALID, "escape count mismatch while encoding");
+  std::memset(out + info.off_s, 0, static_cast<size_t>(info.off_x - info.off_s));
+  std::memcpy(out + info.off_s, S.data(), S.size() * sizeof(uint32_t));
+  uint8_t *X = out + info.off_x;
+  parallel_for(G, threads, [&](uint64_t gb, uint64_t ge) {
+    for (uint64_t g = gb; g < ge; ++g) {
+      if (!counts[static_cast<size_t>(g)]) continue;
+      const uint64_t w0 = g * kExpcodeGroupWords;
+      const uint64_t wn = std::min<uint64_t>(kExpcodeGroupWords, W - w0);
+      uint64_t k = S[static_cast<size_t>(g)];
+      for (uint64_t j = 0; j < wn; ++j) {
+        const uint32_t e = (word_at(raw, w0 + j) >> 7) & 0xff;
+        if (p.code_of[e] != kExpEscape) continue;
+        const uint32_t x = static_cast<uint32_t>(j << 8) | e;
+        std::memcpy(X + 4 * k, &x, 4);
+        ++k;
+      }
+    }
+  });
+  return FTX_OK;
+}
+
+int expcode_parse(const void *src, size_t src_bytes, ExpcodeInfo *info) {
+  if (src_bytes < kExpcodeHeaderBytes) return fail(FTX_ERR_INVALID, "encoded block shorter than its header");
+  ExpHeader h;
+  std::memcpy(&h, src, sizeof(h));
+  if (std::memcmp(h.magic, "FTXE", 4) != 0 || h.version != kExpVersion)
+    return fail(FTX_ERR_INVALID, "not an exponent-coded block (magic or version)");
+  if (h.n_words != h.n / 2 || h.groups != (h.n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords ||
+      h.groups >= (uint64_t(1) << 32) || h.escapes > h.n_words || h.escapes >= (uint64_t(1) << 32))
+    return fail(FTX_ERR_INVALID, "inconsistent exponent-coded block header");
+  *info = ExpcodeInfo{};
+  info->n = h.n;
+  info->n_words = h.n_words;
+  info->groups = h.groups;
+  info->escapes = h.escapes;
+  std::memcpy(info->table, h.table, 16);
+  info->tail = h.tail;
+  sections(h.groups, h.escapes, info);
+  if (info->total > src_bytes) return fail(FTX_ERR_INVALID, "encoded block is truncated");
+  return FTX_OK;
+}
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kExpThreads = 256;
+constexpr int kExpWaves = kExpThreads / 64;
+constexpr int kExpInFlight = 8;  // groups whose loads each lane keeps in flight
+
+__device__ __forceinline__ uint32_t decode_word(uint32_t a, uint32_t code, uint64_t t01, uint64_t t23) {
+  const uint64_t t = code < 8 ? t01 : t23;
+  const uint32_t e = static_cast<uint32_t>(t >> ((code & 7) * 8)) & 0xff;
+  return ((a & 0x80) << 8) | (e << 7) | (a & 0x7f);
+}
+
+// Wave w decodes groups w*8 .. w*8+7, then steps by 8 x (waves in the grid).
+// Lane l of a group rebuilds words 16l .. 16l+15 from A bytes 16l.. and B
+// bytes 8l.. of the group. Loads of groups past the last read the last group
+// (in bounds) and are discarded. The sections follow from the raw size n; the
+// escape count, table and tail byte are read from the block's header when the
+// kernel runs, so a graph that captured the launch decodes the block's
+// current contents after it is re-encoded in place. A header of another raw
+// size writes nothing, and escape reads stay inside `capacity` bytes.
+__global__ __launch_bounds__(kExpThreads) void expcode_decode_kernel(uint8_t *__restrict__ dst,
+                                                                     const uint8_t *__restrict__ src,
+                                                                     uint64_t capacity, uint64_t n) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = static_cast<uint64_t>(blockIdx.x) * kExpWaves + threadIdx.x / 64;
+  const uint64_t waves = static_cast<uint64_t>(gridDim.x) * kExpWaves;
+  const uint64_t n_words = n / 2;
+  const uint64_t groups = (n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  const uint64_t off_b = kExpcodeHeaderBytes + kExpcodeGroupWords * groups;
+  const uint64_t off_s = off_b + kExpcodeGroupWords / 2 * groups;
+  const uint64_t off_x = off_s + (4 * (groups + 1) + 15) / 16 * 16;
+  if (*reinterpret_cast<const uint64_t *>(src + 8) != n) return;
+  uint64_t escapes = *reinterpret_cast<const uint64_t *>(src + 32);
+  escapes = off_x <= capacity ? min(escapes, (capacity - off_x) / 4) : 0;
+  const uint64_t t01 = *reinterpret_cast<const uint64_t *>(src + 40);
+  const uint64_t t23 = *reinterpret_cast<const uint64_t *>(src + 48);
+  if ((n & 1) && blockIdx.x == 0 && threadIdx.x == 0) dst[n - 1] = src[56];
+  const uint8_t *A = src + kExpcodeHeaderBytes;
+  const uint8_t *B = src + off_b;
+  const uint32_t *S = reinterpret_cast<const uint32_t *>(src + off_s);
+  const uint32_t *X = reinterpret_cast<const uint32_t *>(src + off_x);
+  for (uint64_t g0 = wave * kExpInFlight; g0 < groups; g0 += waves * kExpInFlight) {
+    u32x4 a[kExpInFlight];
+    u32x2 b[kExpInFlight];
+#pragma unroll
+    for (int i = 0; i < kExpInFlight; ++i) {
+      const uint64_t g = min(g0 + i, groups - 1);
+      a[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(A + g * kExpcodeGroupWords) + lane);
+      b[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(B + g * (kExpcodeGroupWords / 2)) + lane);
+    }
+    // S[g0 .. g0 + 8], one entry per lane (lanes past them repeat the last), clamped to S[G]
+    const uint32_t sv = S[min(g0 + min(lane, kExpInFlight), groups)];
+#pragma unroll
+    for (int i = 0; i < kExpInFlight; ++i) {
+      const uint64_t g = g0 + i;
+      if (g >= groups) break;
+      uint32_t word[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t codes = b[i][q >> 1] >> ((q & 1) * 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          word[4 * q + r] = decode_word((a[i][q] >> (8 * r)) & 0xff, (codes >> (4 * r)) & 0xf, t01, t23);
+      }
+      const uint32_t s0 = __shfl(sv, i, 64);
+      const uint32_t s1 = min(static_cast<uint64_t>(__shfl(sv, i + 1, 64)), escapes);
+      for (uint32_t k = s0; k < s1; ++k) {  // wave-uniform; escapes are rare
+        const uint32_t x = X[k];
+        const uint32_t pos = x >> 8;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (pos == static_cast<uint32_t>(16 * lane + j)) word[j] = (word[j] & 0x807fu) | ((x & 0xffu) << 7);
+      }
+      const uint64_t w0 = g * kExpcodeGroupWords + 16 * static_cast<uint64_t>(lane);
+      uint8_t *out = dst + 2 * w0;
+      if (w0 + 16 <= n_words) {
+        u32x4 lo, hi;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          lo[k] = word[2 * k] | (word[2 * k + 1] << 16);
+          hi[k] = word[8 + 2 * k] | (word[8 + 2 * k + 1] << 16);
+        }
+        __builtin_nontemporal_store(lo, reinterpret_cast<u32x4 *>(out));
+        __builtin_nontemporal_store(hi, reinterpret_cast<u32x4 *>(out) + 1);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (w0 + j < n_words) reinterpret_cast<uint16_t *>(out)[j] = static_cast<uint16_t>(word[j]);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t allow_expcode_lds(size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(expcode_decode_kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+hipError_t launch_expcode_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
+                                 size_t reserve_lds, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const uint64_t groups = (n / 2 + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  const uint64_t per_block = static_cast<uint64_t>(kExpWaves) * kExpInFlight;
+  const uint64_t need = std::max<uint64_t>(1, (groups + per_block - 1) / per_block);
+  const unsigned g = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, static_cast<uint64_t>(grid))));
+  hipLaunchKernelGGL(expcode_decode_kernel, dim3(g), dim3(kExpThreads), static_cast<unsigned>(reserve_lds), stream,
+                     static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src_dev), capacity, n);
+  return hipGetLastError();
+}
+
+}  // namespace ftx

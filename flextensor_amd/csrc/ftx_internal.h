@@ -122,6 +122,30 @@ hipError_t launch_fill_u8(void *dev, uint8_t value, size_t nbytes, hipStream_t s
 hipError_t launch_timestamp(uint64_t *slot, hipStream_t stream);
 hipError_t launch_read_probe(const void *dev, size_t nbytes, uint32_t *sink, int grid, hipStream_t stream);
 
+// Exponent-coded blocks (ftx_expcode.hip): the layout of one encoded block.
+constexpr uint64_t kExpcodeHeaderBytes = 256;
+constexpr uint64_t kExpcodeGroupWords = 1024;
+// Default decode grid: workgroups of 4 waves, each lane with four groups' loads in flight.
+constexpr int kExpcodeDefaultGrid = 16;
+struct ExpcodeInfo {
+  uint64_t n;        // raw bytes
+  uint64_t n_words;  // n / 2
+  uint64_t groups;   // groups of kExpcodeGroupWords words
+  uint64_t escapes;  // escaped words
+  uint64_t off_b, off_s, off_x, total;  // section offsets and encoded size (plane A starts at the header's end)
+  uint8_t table[16];                    // exponent of each code below 15
+  uint8_t tail;                         // the odd last raw byte
+};
+// out == nullptr: only *out_bytes (the encoded size) is computed.
+int expcode_encode(const void *raw, size_t nbytes, void *out, size_t out_capacity, size_t *out_bytes);
+// Reads and checks the header of an encoded block of src_bytes bytes in host memory.
+int expcode_parse(const void *src, size_t src_bytes, ExpcodeInfo *info);
+// Decodes the block of raw size n at src_dev (a device-visible address, `capacity` bytes readable) into
+// dst; the kernel reads the block's header when it runs. `reserve_lds` as for launch_zero_copy.
+hipError_t launch_expcode_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
+                                 size_t reserve_lds, hipStream_t stream);
+hipError_t allow_expcode_lds(size_t bytes);
+
 // Host-side helpers shared with the oracle's definition of the checksum.
 inline uint64_t splitmix64(uint64_t x) {
   x += 0x9e3779b97f4a7c15ull;

@@ -102,7 +102,8 @@ int device_state(DeviceState **out) {
     if (hipDeviceGetAttribute(&lds_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
       lds_block = 0;
     const int lds = lds_cu > 0 && lds_block > 0 ? std::min(lds_cu, lds_block) : std::max(lds_cu, lds_block);
-    if (lds > 0 && allow_zero_copy_lds(static_cast<size_t>(lds)) == hipSuccess)
+    if (lds > 0 && allow_zero_copy_lds(static_cast<size_t>(lds)) == hipSuccess &&
+        allow_expcode_lds(static_cast<size_t>(lds)) == hipSuccess)
       st.copy_reserve_lds = static_cast<size_t>(lds);
     (void)hipGetLastError();
     st.cu_count = cus;
@@ -717,6 +718,59 @@ int ftx_copy_h2d_policy(void *dst, const void *src, size_t nbytes, int mode, con
     default:
       return ftx::fail(FTX_ERR_INVALID, "unknown copy mode");
   }
+}
+
+int ftx_expcode_encode(const void *raw, size_t nbytes, void *out, size_t out_capacity, size_t *out_bytes) {
+  FTX_REQUIRE_LIVE();
+  if (!out_bytes) return ftx::fail(FTX_ERR_INVALID, "out_bytes is null");
+  if (nbytes > 0 && !raw) return ftx::fail(FTX_ERR_INVALID, "raw is null");
+  if (out != nullptr) {
+    const uintptr_t o = reinterpret_cast<uintptr_t>(out), r = reinterpret_cast<uintptr_t>(raw);
+    if (nbytes > 0 && o < r + nbytes && r < o + out_capacity)
+      return ftx::fail(FTX_ERR_INVALID, "raw and out ranges overlap");
+  }
+  return ftx::expcode_encode(raw, nbytes, out, out_capacity, out_bytes);
+}
+
+int ftx_expcode_raw_bytes(const void *src, size_t src_bytes, size_t *raw_bytes) {
+  if (!src || !raw_bytes) return ftx::fail(FTX_ERR_INVALID, "null argument");
+  ftx::ExpcodeInfo info;
+  int rc = ftx::expcode_parse(src, src_bytes, &info);
+  if (rc != FTX_OK) return rc;
+  *raw_bytes = static_cast<size_t>(info.n);
+  return FTX_OK;
+}
+
+int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const ftx_copy_policy *policy,
+                           void *stream) {
+  FTX_REQUIRE_LIVE();
+  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  ftx::ExpcodeInfo info;
+  int rc = ftx::expcode_parse(src, src_bytes, &info);  // the header is read on the host: src is host memory
+  if (rc != FTX_OK) return rc;
+  if (info.n == 0) return FTX_OK;
+  if (reinterpret_cast<uintptr_t>(dst) % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "decode destination needs 16-byte alignment");
+  rc = ftx::check_device_range(dst, static_cast<size_t>(info.n), "decode destination");
+  if (rc != FTX_OK) return rc;
+  const void *src_dev = nullptr;
+  rc = ftx::mapped_source(src, src_bytes, &src_dev);  // the kernel may read up to src_bytes (a re-encoded block)
+  if (rc != FTX_OK) return rc;
+  if (reinterpret_cast<uintptr_t>(src_dev) % 16 != 0)
+    return ftx::fail(FTX_ERR_INVALID, "encoded block needs 16-byte alignment");
+  int grid = ftx::kExpcodeDefaultGrid;
+  if (policy != nullptr) {
+    ftx::CopyPolicy pol;
+    rc = ftx::check_policy(policy->kernel_max_bytes, policy->split_min_bytes, policy->n_copy_streams,
+                           policy->kernel_grid, &pol);
+    if (rc != FTX_OK) return rc;
+    if (pol.kernel_grid > 0) grid = pol.kernel_grid;
+  }
+  ftx::DeviceState *st = nullptr;
+  rc = ftx::device_state(&st);
+  if (rc != FTX_OK) return rc;
+  const size_t reserve = grid <= ftx::kZeroCopyReserveMaxGrid ? st->copy_reserve_lds : 0;
+  FTX_HIP(ftx::launch_expcode_decode(dst, src_dev, src_bytes, info.n, grid, reserve, static_cast<hipStream_t>(stream)));
+  return FTX_OK;
 }
 
 int ftx_set_staging_policy(size_t piece_bytes, int n_threads) { return ftx::set_staging_policy(piece_bytes, n_threads); }

@@ -1843,6 +1843,9 @@ class OffloadManager:
         if not self._reload_pending or self.phase != OffloadPhase.INFERENCE or hip.is_capturing():
             return
         self._reload_pending = False
+        if getattr(self.controller, "encoded", None):  # the new host bytes reach the link only once re-encoded
+            torch.cuda.synchronize(self.device)
+            self.controller.refresh_encoded()
         preload = getattr(self.loader, "preload", None)
         if preload is not None:
             preload()
@@ -1870,7 +1873,8 @@ class OffloadManager:
                                                         plan.strategy_map, bd.label_to_block_id,
                                                         host_pinner=pinner, copy_mode=mode, copy_policy=policy,
                                                         shm_block_name_map=shm_names,
-                                                        load_from_shm=self._load_from_shm)
+                                                        load_from_shm=self._load_from_shm,
+                                                        encode_blocks=cfg.encode_streamed_blocks)
 
     def plan_table(self) -> str:
         """Per unit: bytes, profiled ms, and where it lives (its slot and transfer label when streamed)."""

@@ -181,6 +181,32 @@ int ftx_set_copy_policy(size_t kernel_max_bytes, size_t split_min_bytes, int n_c
 int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *n_copy_streams,
                         int *kernel_grid);
 
+/* ---- exponent-coded blocks -------------------------------------------------
+ * No reference counterpart: the reference copies each label's packed block as
+ * raw bytes (allocation_block.py:104-106). These entry points carry the same
+ * block over the link encoded, and the GPU rebuilds the raw bytes exactly.
+ * The block is read as little-endian 16-bit words (bf16 bit patterns):
+ * sign and mantissa travel as one byte per word, the exponent as a 4-bit code
+ * for the block's 15 most frequent exponents, and the others as escapes.
+ * Blocks of bf16 weights from one distribution encode to about 0.75 of their
+ * raw size; other contents may grow (compare sizes before using it).
+ * ftx_expcode_encode: host only, no GPU. out NULL stores only the encoded size
+ * in *out_bytes; otherwise the block is written to out (out_capacity bytes,
+ * not overlapping raw). The format is exponent-coded block v1 ("FTXE").
+ * ftx_expcode_raw_bytes: the raw size recorded in an encoded block's header.
+ * ftx_expcode_decode_h2d: the host-to-device copy of an encoded block: src is
+ * the encoded block in pinned, device-mapped host memory (src_bytes bytes,
+ * 16-byte aligned), dst a 16-byte aligned device range of the raw size. A
+ * zero-copy kernel reads src over the link and writes the raw bytes, ordered
+ * on `stream`; policy->kernel_grid sets its workgroups (NULL or 0: 16), and a
+ * grid of at most 16 reserves its CUs as the zero-copy copy does. The header
+ * is read on the host at call time; the block must not change until the copy
+ * has run. */
+int ftx_expcode_encode(const void *raw, size_t nbytes, void *out, size_t out_capacity, size_t *out_bytes);
+int ftx_expcode_raw_bytes(const void *src, size_t src_bytes, size_t *raw_bytes);
+int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const ftx_copy_policy *policy,
+                           void *stream);
+
 /* ---- staged copies from pageable host memory ------------------------------
  * Replace the reference's copy from pageable or shared-memory blocks that are
  * not page-locked (pinned_memory=False blocks, allocation_block.py:104-106 with

@@ -19,4 +19,6 @@ a pure-Python library) and cites the file:line it follows:
                    fp8-weight linear layer in float64
 * ``native``       ctypes access to ``liboracle.so`` (plain C: layout, pack,
                    scatter, checksum)
+* ``expcode``      the exponent-coded block format of encoded streamed
+                   blocks (this build's own format, no reference counterpart)
 """

@@ -1,0 +1,128 @@
+"""Streaming with exponent-coded blocks (``OffloadConfig(encode_streamed_blocks=True)``).
+
+Each streamed label's transfer is one decode launch that rebuilds the raw block in its ring slot, so
+every forward must stay bitwise equal to the resident model's: eager, under a captured graph, with the
+reordered loader of a partial budget, through a decoder's generation, and after ``load_state_dict``
+rewrote the host blocks (which re-encodes them in place, so a graph captured before the load decodes
+the new weights).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from flextensor_amd import workloads as W
+from flextensor_amd.config import OffloadConfig
+from flextensor_amd.manager import OffloadManager, OffloadPhase
+
+pytestmark = pytest.mark.gpu
+
+
+def _offload(model, name, **cfg):
+    base = dict(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1, profiling_iters=1,
+                encode_streamed_blocks=True)
+    base.update(cfg)
+    mgr = OffloadManager(name=name)
+    mgr.offload(model, OffloadConfig(**base))
+    return mgr
+
+
+def _capture(model, static_x):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.no_grad():
+        for _ in range(2):
+            model(static_x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s), torch.no_grad():
+        out = model(static_x)
+    return g, out
+
+
+@pytest.mark.parametrize("budget_layers", [None, 5])
+def test_encoded_mlp_streams_bitwise_eager_and_in_graphs(gpu, budget_layers):
+    model = W.build_mlp_stack(8, 256, 704, seed=41)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    mgr = _offload(model, f"enc-mlp-{budget_layers}",
+                   max_gpu_mem_bytes=None if budget_layers is None else budget_layers * layer)
+    x = W.mlp_input(16, 256, seed=41).to(gpu)
+    with torch.no_grad():
+        want = resident(x)
+        outs = [model(x) for _ in range(5)]
+    assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.streamed
+    if budget_layers is not None:
+        assert mgr.plan.resident and mgr.plan.reordered
+    ctl = mgr.controller
+    assert set(ctl.encoded) == set(ctl.block_map_cpu)  # every streamed block of N(0, 0.02) weights encodes
+    for label in ctl.encoded:
+        assert ctl.link_bytes(label) < 0.8 * ctl.transfer_bytes(label)
+    for out in outs:
+        assert torch.equal(out, want)
+
+    static_x = x.clone()
+    g, static_out = _capture(model, static_x)
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, want), f"replay {i}"
+        with torch.no_grad():
+            assert torch.equal(model(x), want)  # eager streamed work between replays
+        torch.cuda.synchronize()
+    del g
+    mgr.release()
+    for p, q in zip(model.parameters(), resident.parameters()):
+        assert p.device.type == "cpu" and torch.equal(p, q.cpu())
+
+
+def test_encoded_llama_generation_matches_resident(gpu):
+    shape = W.LlamaShape(n_layers=4, hidden=256, n_heads=4, n_kv_heads=4, head_dim=64, inter=688, vocab=1000,
+                         max_seq=128)
+    model = W.build_llama(shape, seed=43)
+    prompt = W.prompt_tokens(1, 24, shape.vocab, seed=43).to(gpu)
+    ref = copy.deepcopy(model).to(gpu)
+    ref.init_cache(1, 64, gpu)
+    want_tokens, want_logits = W.generate(ref, prompt, 8)
+    mgr = _offload(model, "enc-llama")
+    model.init_cache(1, 64, gpu)
+    W.generate(model, prompt, 8)  # discovery and profiling happen inside
+    model.init_cache(1, 64, gpu)
+    got_tokens, got_logits = W.generate(model, prompt, 8)
+    assert mgr.phase == OffloadPhase.INFERENCE and mgr.controller.encoded
+    assert torch.equal(got_tokens, want_tokens)
+    for a, b in zip(got_logits, want_logits):
+        assert torch.equal(a, b)
+    mgr.release()
+
+
+def test_load_state_dict_reencodes_and_captured_graphs_follow(gpu):
+    model = W.build_mlp_stack(6, 256, 704, seed=45)
+    mgr = _offload(model, "enc-load")
+    x = W.mlp_input(8, 256, seed=45).to(gpu)
+    with torch.no_grad():
+        for _ in range(3):
+            model(x)
+    assert mgr.phase == OffloadPhase.INFERENCE and mgr.controller.encoded
+    static_x = x.clone()
+    g, static_out = _capture(model, static_x)
+
+    # new weights of another scale: another exponent table for every block
+    other = W.build_mlp_stack(6, 256, 704, seed=46)
+    with torch.no_grad():
+        for p in other.parameters():
+            p.mul_(7.0)
+    want = copy.deepcopy(other).to(gpu)
+    with torch.no_grad():
+        model.load_state_dict(other.state_dict())
+        for _ in range(2):
+            assert torch.equal(model(x), want(x))
+    g.replay()
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        assert torch.equal(static_out, want(static_x))
+    del g
+    mgr.release()
