@@ -347,6 +347,25 @@ def _ring_roofline(run: dict, measured_peak: float) -> dict | None:
             "by_size": ring["by_size"]}
 
 
+def _encoded_summary(enc: dict, measured_peak: float, raw_tok_s: float | None) -> dict:
+    """The 7B decode with exponent-coded blocks: weight bytes per token against the bytes that crossed
+    the link, the effective weight rate and the link's own rate."""
+    return {
+        "encoded_blocks": enc["encoded_blocks"], "streamed_layers": enc["streamed_layers"],
+        "streamed_bytes_per_token": enc["streamed_bytes_per_token"],
+        "link_bytes_per_token": enc["link_bytes_per_token"],
+        "link_bytes_ratio": round(enc["link_bytes_per_token"] / enc["streamed_bytes_per_token"], 4),
+        "tok_s": round(enc["decode_tok_s"], 3), "ms_per_token": round(enc["ms_per_token"], 3),
+        "decode_effective_GBps": round(enc["decode_effective_GBps"], 3),
+        "decode_link_GBps": round(enc["decode_link_GBps"], 3),
+        "link_pct_of_measured_peak": round(100 * enc["decode_link_GBps"] / measured_peak, 2),
+        "speedup_vs_raw_blocks": None if raw_tok_s is None else round(enc["decode_tok_s"] / raw_tok_s, 4),
+        "prefill_tok_s": round(enc["prefill_tok_s"], 1),
+        "ring_order": enc["ring_order"],
+        "ring_copies": _ring_roofline(enc, measured_peak),
+    }
+
+
 def _set_ring_order(mgr, how: str) -> None:
     """Override the manager's choice of ring order: "reference" (the reference's order: the compute stream
     waits on each copy's ready event) or "link-bound" (the reordered loader blocks the host on it with the
@@ -379,13 +398,14 @@ def _ring_engine(mgr) -> str:
     return "SDMA (hipMemcpyAsync)" if mode == nat.COPY_SDMA else "staged"
 
 
-def bench_mlp(steps: int, copy_engine: str, ring_order: str = "auto") -> dict:
+def bench_mlp(steps: int, copy_engine: str, ring_order: str = "auto", encode: bool = False) -> dict:
     """The 8-layer 4096->11008->4096 MLP stack, every layer streamed through a 2-slot ring.
 
     Times ``steps`` eager streamed forwards, then the same forward captured in
     a HIP graph and replayed ``steps`` times; both outputs are checked bitwise
     against the all-resident forward. The CPU baseline is the same forward in
-    PyTorch on the host cores.
+    PyTorch on the host cores. ``encode`` streams the blocks exponent-coded
+    (``OffloadConfig.encode_streamed_blocks``; no CPU baseline then).
     """
     import torch
 
@@ -403,10 +423,13 @@ def bench_mlp(steps: int, copy_engine: str, ring_order: str = "auto") -> dict:
     streamed_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
     mgr = OffloadManager("bench-mlp")
     mgr.offload(model, OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
-                                     profiling_iters=1, copy_engine=copy_engine))
+                                     profiling_iters=1, copy_engine=copy_engine, encode_streamed_blocks=encode))
     with torch.no_grad():
         for _ in range(2):  # discovery, then profiling: the plan and the loader are built at its end
             out = model(x)
+        ctl = mgr.controller
+        link_bytes = sum(ctl.link_bytes(label) for label in ctl.block_map_cpu)
+        encoded = len(ctl.encoded)
         _set_ring_order(mgr, ring_order)
         order = _ring_order(mgr)
         for _ in range(2):  # two streamed warm-up passes
@@ -436,6 +459,21 @@ def bench_mlp(steps: int, copy_engine: str, ring_order: str = "auto") -> dict:
     graph_ok = bool(torch.equal(static_out, want))
     del g, static_out
     mgr.release(preserve_model=True)
+    out = {
+        "streamed_bytes_per_forward": streamed_bytes,
+        "link_bytes_per_forward": link_bytes,
+        "encoded_blocks": encoded,
+        "eager_ms_per_forward": 1e3 * t_eager,
+        "eager_effective_GBps": streamed_bytes / t_eager / 1e9,
+        "eager_link_GBps": link_bytes / t_eager / 1e9,
+        "graph_ms_per_forward": 1e3 * t_graph,
+        "graph_effective_GBps": streamed_bytes / t_graph / 1e9,
+        "graph_link_GBps": link_bytes / t_graph / 1e9,
+        "ring_order": order,
+        "bitwise_equal_to_resident": eager_ok and graph_ok,
+    }
+    if encode:
+        return out
     # CPU baseline: the same forward in PyTorch on the host cores
     xc = x.cpu()
     with torch.no_grad():
@@ -447,18 +485,9 @@ def bench_mlp(steps: int, copy_engine: str, ring_order: str = "auto") -> dict:
             model(xc)
             ts.append(time.perf_counter() - t0)
     t_cpu = sorted(ts)[len(ts) // 2]
-    return {
-        "streamed_bytes_per_forward": streamed_bytes,
-        "eager_ms_per_forward": 1e3 * t_eager,
-        "eager_effective_GBps": streamed_bytes / t_eager / 1e9,
-        "graph_ms_per_forward": 1e3 * t_graph,
-        "graph_effective_GBps": streamed_bytes / t_graph / 1e9,
-        "ring_order": order,
-        "bitwise_equal_to_resident": eager_ok and graph_ok,
-        "cpu_baseline": {"value": 1e3 * t_cpu, "unit": "ms per forward", "cores": torch.get_num_threads(),
-                         "kind": "port",
-                         "sample": "the full 8-layer bf16 forward on the host cores, median of 5"},
-    }
+    out["cpu_baseline"] = {"value": 1e3 * t_cpu, "unit": "ms per forward", "cores": torch.get_num_threads(),
+                           "kind": "port", "sample": "the full 8-layer bf16 forward on the host cores, median of 5"}
+    return out
 
 
 def cpu_llama_decode_baseline(layers: int = 2, tokens: int = 4, context: int = 512) -> dict:
@@ -1514,6 +1543,8 @@ def main() -> int:
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--skip-finer-units", action="store_true",
                     help="skip the 7B decode with attention and MLP projections as separate offload units")
+    ap.add_argument("--encoded-only", action="store_true",
+                    help="print only the 7B decode with exponent-coded blocks (for profiling it alone)")
     ap.add_argument("--skip-encoded", action="store_true",
                     help="skip the 7B decode with exponent-coded blocks (OffloadConfig.encode_streamed_blocks)")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
@@ -1565,8 +1596,19 @@ def main() -> int:
     if args.dit_only:
         print(json.dumps({"dit": bench_dit(12.0, args.dit_tokens, 512, args.dit_steps, args.copy_engine)}), flush=True)
         return 0
+    if args.encoded_only:
+        peak = measure_link_peak()
+        enc = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
+                            ring_order=args.ring_order, encode=True)
+        enc.pop("_check")
+        print(json.dumps({"llama7b_encoded_blocks": _encoded_summary(enc, max(peak["sdma"], peak["kernel"]), None),
+                          "measured_peak": peak}), flush=True)
+        return 0
     if args.mlp_only:
-        print(json.dumps({"mlp8": bench_mlp(20, args.copy_engine, ring_order=args.ring_order)}), flush=True)
+        res = {"mlp8": bench_mlp(20, args.copy_engine, ring_order=args.ring_order)}
+        if not args.skip_encoded:
+            res["mlp8_encoded_blocks"] = bench_mlp(20, args.copy_engine, ring_order=args.ring_order, encode=True)
+        print(json.dumps(res), flush=True)
         return 0
     if args.staged_sweep:
         print(json.dumps({"staged_sweep": staged_sweep()}), flush=True)
@@ -1671,21 +1713,8 @@ def main() -> int:
         enc_check = enc.pop("_check")
         same = (torch.equal(enc_check["last_logits"], check["last_logits"])
                 and torch.equal(enc_check["tokens"], check["tokens"]))
-        line["llama7b_encoded_blocks"] = {
-            "encoded_blocks": enc["encoded_blocks"], "streamed_layers": enc["streamed_layers"],
-            "streamed_bytes_per_token": enc["streamed_bytes_per_token"],
-            "link_bytes_per_token": enc["link_bytes_per_token"],
-            "link_bytes_ratio": round(enc["link_bytes_per_token"] / enc["streamed_bytes_per_token"], 4),
-            "tok_s": round(enc["decode_tok_s"], 3), "ms_per_token": round(enc["ms_per_token"], 3),
-            "decode_effective_GBps": round(enc["decode_effective_GBps"], 3),
-            "decode_link_GBps": round(enc["decode_link_GBps"], 3),
-            "link_pct_of_measured_peak": round(100 * enc["decode_link_GBps"] / measured_peak, 2),
-            "speedup_vs_raw_blocks": round(enc["decode_tok_s"] / llama["decode_tok_s"], 4),
-            "prefill_tok_s": round(enc["prefill_tok_s"], 1),
-            "ring_order": enc["ring_order"],
-            "ring_copies": _ring_roofline(enc, measured_peak),
-            "prefill_logits_and_tokens_bitwise_equal_to_raw_blocks": same,
-        }
+        line["llama7b_encoded_blocks"] = _encoded_summary(enc, measured_peak, llama["decode_tok_s"])
+        line["llama7b_encoded_blocks"]["prefill_logits_and_tokens_bitwise_equal_to_raw_blocks"] = same
         _log(f"llama7b encoded blocks: {line['llama7b_encoded_blocks']}")
         del enc, enc_check
         gc.collect()
@@ -1747,6 +1776,19 @@ def main() -> int:
         if not line["mlp8"]["bitwise_equal_to_resident"]:
             print("bench: the streamed MLP forward differs from the resident forward", file=sys.stderr)
             return 1
+        if not args.skip_encoded:
+            gc.collect()
+            torch.cuda.empty_cache()
+            enc = bench_mlp(20, args.copy_engine, ring_order=args.ring_order, encode=True)
+            enc["link_bytes_ratio"] = round(enc["link_bytes_per_forward"] / enc["streamed_bytes_per_forward"], 4)
+            enc["eager_speedup_vs_raw_blocks"] = round(line["mlp8"]["eager_ms_per_forward"]
+                                                       / enc["eager_ms_per_forward"], 4)
+            line["mlp8"]["encoded_blocks"] = enc
+            _log(f"mlp8 encoded blocks: {enc}")
+            if not enc["bitwise_equal_to_resident"]:
+                print("bench: the streamed MLP forward with encoded blocks differs from the resident forward",
+                      file=sys.stderr)
+                return 1
     if not args.skip_dit:
         gc.collect()
         torch.cuda.empty_cache()

@@ -125,7 +125,7 @@ hipError_t launch_read_probe(const void *dev, size_t nbytes, uint32_t *sink, int
 // Exponent-coded blocks (ftx_expcode.hip): the layout of one encoded block.
 constexpr uint64_t kExpcodeHeaderBytes = 256;
 constexpr uint64_t kExpcodeGroupWords = 1024;
-// Default decode grid: workgroups of 4 waves, each lane with four groups' loads in flight.
+// Default decode grid: workgroups of 8 waves, each lane with eight groups' loads in flight.
 constexpr int kExpcodeDefaultGrid = 16;
 struct ExpcodeInfo {
   uint64_t n;        // raw bytes
