@@ -1545,6 +1545,8 @@ def main() -> int:
                     help="skip the 7B decode with attention and MLP projections as separate offload units")
     ap.add_argument("--encoded-only", action="store_true",
                     help="print only the 7B decode with exponent-coded blocks (for profiling it alone)")
+    ap.add_argument("--encoded-finer-units", action="store_true",
+                    help="with --encoded-only: each layer's attention and MLP projections as separate units")
     ap.add_argument("--skip-encoded", action="store_true",
                     help="skip the 7B decode with exponent-coded blocks (OffloadConfig.encode_streamed_blocks)")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
@@ -1598,11 +1600,13 @@ def main() -> int:
         return 0
     if args.encoded_only:
         peak = measure_link_peak()
+        units = FINER_UNITS if args.encoded_finer_units else ("layers.*",)
         enc = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
-                            ring_order=args.ring_order, encode=True)
+                            include_patterns=units, ring_order=args.ring_order, encode=True)
         enc.pop("_check")
-        print(json.dumps({"llama7b_encoded_blocks": _encoded_summary(enc, max(peak["sdma"], peak["kernel"]), None),
-                          "measured_peak": peak}), flush=True)
+        res = _encoded_summary(enc, max(peak["sdma"], peak["kernel"]), None)
+        res["include_patterns"] = list(units)
+        print(json.dumps({"llama7b_encoded_blocks": res, "measured_peak": peak}), flush=True)
         return 0
     if args.mlp_only:
         res = {"mlp8": bench_mlp(20, args.copy_engine, ring_order=args.ring_order)}
