@@ -21,11 +21,13 @@
 //
 // The table holds the 15 most frequent exponents, most frequent first, ties to
 // the smaller exponent. The encoded size is 256 + 1536 G + align16(4 (G+1)) +
-// 4 E bytes. The decode kernel reads planes A and B with 16- and 8-byte loads
-// per lane (coalesced across the wave, as the zero-copy copy's 16-byte loads),
-// rebuilds 16 words per lane in registers and writes them with two 16-byte
-// non-temporal stores; a group's escapes, when it has any, are patched from X.
-// Each lane holds eight groups' loads in flight.
+// 4 E bytes. Lane l of a wave decodes words [8l, 8l + 8) and [512 + 8l,
+// 512 + 8l + 8) of a group: it reads 8 bytes of plane A and 4 of plane B for
+// each run (coalesced across the wave), rebuilds the 16 words in registers and
+// writes each run with one 16-byte non-temporal store, so every store
+// instruction of the wave covers one contiguous KiB and HBM is written once
+// per byte. A group's escapes, when it has any, are patched from X. Each lane
+// holds eight groups' loads in flight.
 #include <algorithm>
 #include <cstring>
 #include <thread>
@@ -241,9 +243,8 @@ __device__ __forceinline__ uint32_t decode_word(uint32_t a, uint32_t code, uint6
 }
 
 // Wave w decodes groups w*8 .. w*8+7, then steps by 8 x (waves in the grid).
-// Lane l of a group rebuilds words 16l .. 16l+15 from A bytes 16l.. and B
-// bytes 8l.. of the group. Loads of groups past the last read the last group
-// (in bounds) and are discarded. The sections follow from the raw size n; the
+// Loads of groups past the last read the last group (in bounds) and are
+// discarded. The sections follow from the raw size n; the
 // escape count, table and tail byte are read from the block's header when the
 // kernel runs, so a graph that captured the launch decodes the block's
 // current contents after it is re-encoded in place. A header of another raw
@@ -269,14 +270,21 @@ __global__ __launch_bounds__(kExpThreads) void expcode_decode_kernel(uint8_t *__
   const uint8_t *B = src + off_b;
   const uint32_t *S = reinterpret_cast<const uint32_t *>(src + off_s);
   const uint32_t *X = reinterpret_cast<const uint32_t *>(src + off_x);
+  // Lane l decodes two runs of 8 words, [8l, 8l + 8) and [512 + 8l, 512 + 8l + 8) of the group, so that each
+  // 16-byte store instruction of the wave writes one contiguous KiB.
   for (uint64_t g0 = wave * kExpInFlight; g0 < groups; g0 += waves * kExpInFlight) {
-    u32x4 a[kExpInFlight];
-    u32x2 b[kExpInFlight];
+    u32x2 a[kExpInFlight][2];
+    uint32_t b[kExpInFlight][2];
 #pragma unroll
     for (int i = 0; i < kExpInFlight; ++i) {
       const uint64_t g = min(g0 + i, groups - 1);
-      a[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(A + g * kExpcodeGroupWords) + lane);
-      b[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(B + g * (kExpcodeGroupWords / 2)) + lane);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        a[i][h] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2 *>(A + g * kExpcodeGroupWords + 512 * h) + lane);
+        b[i][h] = __builtin_nontemporal_load(
+            reinterpret_cast<const uint32_t *>(B + g * (kExpcodeGroupWords / 2) + 256 * h) + lane);
+      }
     }
     // S[g0 .. g0 + 8], one entry per lane (lanes past them repeat the last), clamped to S[G]
     const uint32_t sv = S[min(g0 + min(lane, kExpInFlight), groups)];
@@ -284,38 +292,38 @@ __global__ __launch_bounds__(kExpThreads) void expcode_decode_kernel(uint8_t *__
     for (int i = 0; i < kExpInFlight; ++i) {
       const uint64_t g = g0 + i;
       if (g >= groups) break;
-      uint32_t word[16];
+      uint32_t word[16];  // run h, word j at 8h + j
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t codes = b[i][q >> 1] >> ((q & 1) * 16);
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          word[4 * q + r] = decode_word((a[i][q] >> (8 * r)) & 0xff, (codes >> (4 * r)) & 0xf, t01, t23);
-      }
+        for (int j = 0; j < 8; ++j)
+          word[8 * h + j] = decode_word((a[i][h][j >> 2] >> (8 * (j & 3))) & 0xff, (b[i][h] >> (4 * j)) & 0xf, t01, t23);
       const uint32_t s0 = __shfl(sv, i, 64);
       const uint32_t s1 = min(static_cast<uint64_t>(__shfl(sv, i + 1, 64)), escapes);
       for (uint32_t k = s0; k < s1; ++k) {  // wave-uniform; escapes are rare
         const uint32_t x = X[k];
         const uint32_t pos = x >> 8;
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (pos == static_cast<uint32_t>(16 * lane + j)) word[j] = (word[j] & 0x807fu) | ((x & 0xffu) << 7);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (pos == static_cast<uint32_t>(512 * h + 8 * lane + j))
+              word[8 * h + j] = (word[8 * h + j] & 0x807fu) | ((x & 0xffu) << 7);
       }
-      const uint64_t w0 = g * kExpcodeGroupWords + 16 * static_cast<uint64_t>(lane);
-      uint8_t *out = dst + 2 * w0;
-      if (w0 + 16 <= n_words) {
-        u32x4 lo, hi;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          lo[k] = word[2 * k] | (word[2 * k + 1] << 16);
-          hi[k] = word[8 + 2 * k] | (word[8 + 2 * k + 1] << 16);
+      for (int h = 0; h < 2; ++h) {
+        const uint64_t w0 = g * kExpcodeGroupWords + 512 * h + 8 * static_cast<uint64_t>(lane);
+        uint8_t *out = dst + 2 * w0;
+        if (w0 + 8 <= n_words) {
+          u32x4 v;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = word[8 * h + 2 * k] | (word[8 * h + 2 * k + 1] << 16);
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (w0 + j < n_words) reinterpret_cast<uint16_t *>(out)[j] = static_cast<uint16_t>(word[8 * h + j]);
         }
-        __builtin_nontemporal_store(lo, reinterpret_cast<u32x4 *>(out));
-        __builtin_nontemporal_store(hi, reinterpret_cast<u32x4 *>(out) + 1);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (w0 + j < n_words) reinterpret_cast<uint16_t *>(out)[j] = static_cast<uint16_t>(word[j]);
       }
     }
   }
