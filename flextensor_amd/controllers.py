@@ -210,6 +210,7 @@ class AllocationBlockController:
         self.tensor_id_to_view_map: dict[int, torch.Tensor] = {}
         self._gpu_slots: list[AllocationBlock] = []
         self.encoded: dict[str, Any] = {}  # label -> expcode.EncodedBlock
+        self.use_encoded = True  # transfers of encoded labels decode (False: they copy the raw blocks)
         self._rollback = _Rollback()
         _refuse_overlapping_sources(tensors_map, strategy_map)
         try:
@@ -272,7 +273,7 @@ class AllocationBlockController:
         """One host-to-device copy of ``label``'s block into its slot, on the current stream: a decode
         launch for an encoded block (its workgroups hold the link at its peak, so the copy policy's grid
         does not apply), else a copy under this controller's copy policy."""
-        enc = self.encoded.get(label)
+        enc = self.encoded.get(label) if self.use_encoded else None
         if enc is None:
             self.block_map_cpu[label].copy_to(self.gpu_block_view_map[label], non_blocking=non_blocking,
                                               mode=self.copy_mode, policy=self.copy_policy)
@@ -297,7 +298,7 @@ class AllocationBlockController:
 
     def link_bytes(self, label: str) -> int:
         """Bytes ``label``'s transfer reads over the host link: the encoded block when there is one."""
-        enc = self.encoded.get(label)
+        enc = self.encoded.get(label) if self.use_encoded else None
         return enc.nbytes if enc is not None else self.block_map_cpu[label].nbytes
 
     def commit_construction(self) -> None:

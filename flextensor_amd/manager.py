@@ -1716,6 +1716,11 @@ class OffloadManager:
         self.memory_transfer_stats = link.memory_transfer_stats()
         LOGGER.info("offload %r: %s", self.name, link.describe())
 
+    def _measured_compute_bound(self) -> bool:
+        """The link measurement profiled this pass and found it compute-bound (the pass rule)."""
+        link = self.link
+        return link is not None and link.pass_compute_ms is not None and not link.link_bound
+
     def _apply_link_bound_order(self) -> None:
         """A link-bound pass orders its ring waits for the link; any other pass keeps the reference's order.
 
@@ -1731,6 +1736,10 @@ class OffloadManager:
         """
         if hasattr(self.loader, "link_bound"):
             self.loader.link_bound = bool(self.link is not None and self.link.link_bound)
+        # Encoded blocks (encode_streamed_blocks) carry fewer bytes, and their decode holds 16 CUs while it
+        # runs: worth it while the link bounds the pass, not once the pass is measured compute-bound.
+        if getattr(self.controller, "encoded", None):
+            self.controller.use_encoded = not self._measured_compute_bound()
 
     def _abort_build(self, primary: BaseException, tensors_map: dict[int, torch.Tensor],
                      bound: dict[int, torch.Tensor], n_hooks: int) -> None:
@@ -1874,7 +1883,12 @@ class OffloadManager:
                                                         host_pinner=pinner, copy_mode=mode, copy_policy=policy,
                                                         shm_block_name_map=shm_names,
                                                         load_from_shm=self._load_from_shm,
-                                                        encode_blocks=cfg.encode_streamed_blocks)
+                                                        encode_blocks=cfg.encode_streamed_blocks
+                                                        and not self._measured_compute_bound())
+            if cfg.encode_streamed_blocks and not self.controller.encoded:
+                LOGGER.info("offload %r: encode_streamed_blocks: %s; the blocks cross the link raw", self.name,
+                            "the pass is compute-bound" if self._measured_compute_bound()
+                            else "no streamed block shrinks by a tenth")
 
     def plan_table(self) -> str:
         """Per unit: bytes, profiled ms, and where it lives (its slot and transfer label when streamed)."""

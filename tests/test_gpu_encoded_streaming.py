@@ -4,7 +4,8 @@ Each streamed label's transfer is one decode launch that rebuilds the raw block 
 every forward must stay bitwise equal to the resident model's: eager, under a captured graph, with the
 reordered loader of a partial budget, through a decoder's generation, and after ``load_state_dict``
 rewrote the host blocks (which re-encodes them in place, so a graph captured before the load decodes
-the new weights).
+the new weights). A pass that the link measurement finds compute-bound streams its blocks raw, and a
+replan switches the encoded transfers off and on with the regime.
 """
 
 from __future__ import annotations
@@ -22,8 +23,10 @@ pytestmark = pytest.mark.gpu
 
 
 def _offload(model, name, **cfg):
+    # No link measurement by default: small models are launch-bound, and a pass measured compute-bound
+    # keeps its blocks raw (the last two tests); without a measurement every block that shrinks is encoded.
     base = dict(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1, profiling_iters=1,
-                encode_streamed_blocks=True)
+                encode_streamed_blocks=True, link_benchmark=False)
     base.update(cfg)
     mgr = OffloadManager(name=name)
     mgr.offload(model, OffloadConfig(**base))
@@ -126,3 +129,60 @@ def test_load_state_dict_reencodes_and_captured_graphs_follow(gpu):
         assert torch.equal(static_out, want(static_x))
     del g
     mgr.release()
+
+
+def _mlp_stack_4096(gpu):
+    model = W.build_mlp_stack(8, 4096, 11008, seed=0)
+    resident = W.build_mlp_stack(8, 4096, 11008, seed=0).to(gpu)
+    small, large = (W.mlp_input(m, 4096, seed=0).to(gpu) for m in (16, 32768))
+    with torch.no_grad():
+        want = {16: resident(small), 32768: resident(large)}
+    del resident
+    torch.cuda.empty_cache()
+    return model, {16: small, 32768: large}, want
+
+
+def test_a_pass_profiled_compute_bound_streams_its_blocks_raw(gpu):
+    """The 4096 -> 11008 -> 4096 stack at 32768 rows computes for longer than its transfers: the decode's
+    16 CUs would cost more than the bytes it saves, so no block is encoded."""
+    model, x, want = _mlp_stack_4096(gpu)
+    mgr = _offload(model, "enc-compute-bound", link_benchmark=True)
+    try:
+        with torch.no_grad():
+            for _ in range(3):
+                got = model(x[32768])
+        assert mgr.phase == OffloadPhase.INFERENCE and mgr.link is not None and not mgr.link.link_bound
+        assert not mgr.controller.encoded
+        assert torch.equal(got, want[32768])
+    finally:
+        mgr.release(preserve_model=False)
+        torch.cuda.empty_cache()
+
+
+def test_a_replan_switches_encoded_blocks_with_the_regime(gpu):
+    """Profiled at 16 rows the stack is link-bound and its blocks are encoded. A replan measured on
+    32768-row passes finds it compute-bound and its transfers copy the raw blocks; a replan back at 16
+    rows decodes again. Every pass is bitwise equal to the resident forward."""
+    model, x, want = _mlp_stack_4096(gpu)
+    mgr = _offload(model, "enc-replan", max_gpu_mem_bytes=1_000_000_000, link_benchmark=True)
+    try:
+        with torch.no_grad():
+            for _ in range(3):
+                got = model(x[16])
+        assert torch.equal(got, want[16])
+        ctl = mgr.controller
+        assert mgr.link.link_bound and ctl.encoded and ctl.use_encoded
+        label = next(iter(ctl.encoded))
+        assert ctl.link_bytes(label) < ctl.transfer_bytes(label)
+        for rows, encoded in ((32768, False), (16, True)):
+            n = mgr.request_strategy_replan()
+            with torch.no_grad():
+                for _ in range(n):
+                    assert torch.equal(model(x[rows]), want[rows])
+            assert mgr.link.link_bound == encoded and ctl.use_encoded == encoded
+            assert (ctl.link_bytes(label) < ctl.transfer_bytes(label)) == encoded
+            with torch.no_grad():
+                assert torch.equal(model(x[rows]), want[rows])
+    finally:
+        mgr.release(preserve_model=False)
+        torch.cuda.empty_cache()
