@@ -186,3 +186,32 @@ def test_a_replan_switches_encoded_blocks_with_the_regime(gpu):
     finally:
         mgr.release(preserve_model=False)
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("source", ["pageable", "shared_memory"])
+def test_encoded_blocks_from_pageable_and_shared_memory_sources(gpu, source):
+    """Host blocks that are not page-locked (pinned_memory=False) or live in named shared-memory segments:
+    the encoded copy is this process's own pinned arena, and the streamed forward stays bitwise equal."""
+    import os
+    import uuid
+
+    extra = ({"pinned_memory": False} if source == "pageable"
+             else {"shm_enabled": True, "shm_namespace": f"ftenc_{uuid.uuid4().hex[:10]}"})
+    model = W.build_mlp_stack(8, 256, 704, seed=47)
+    resident = copy.deepcopy(model).to(gpu)
+    layer = sum(p.numel() * p.element_size() for p in model.layers[0].parameters())
+    mgr = _offload(model, f"enc-{source}", max_gpu_mem_bytes=4 * layer, **extra)
+    x = W.mlp_input(16, 256, seed=47).to(gpu)
+    try:
+        with torch.no_grad():
+            want = resident(x)
+            for _ in range(5):
+                assert torch.equal(model(x), want)
+        ctl = mgr.controller
+        assert mgr.plan.streamed and set(ctl.encoded) == set(ctl.block_map_cpu)
+        if source == "pageable":
+            assert all(not b.block.is_pinned() for b in ctl.block_map_cpu.values())
+        else:
+            assert all(os.path.exists(os.path.join("/dev/shm", n)) for n in ctl.shm_block_name_map.values())
+    finally:
+        mgr.release()
