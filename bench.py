@@ -352,6 +352,58 @@ def _ring_roofline(run: dict, measured_peak: float) -> dict | None:
     return out
 
 
+def expcode_sweep(grids=(8, 16, 32, 64, 128), reps: int = 6) -> dict:
+    """One 7B layer's block (404,766,720 bytes of N(0, 0.02) bf16) encoded, then decoded into the device by
+    ``expcode_decode_kernel`` at each grid, against the raw block's zero-copy copy and SDMA copy. Best of
+    ``reps`` HIP-event timings per case; every decode is checked bit for bit."""
+    import torch
+
+    from flextensor_amd import _native as nat
+    from flextensor_amd import expcode
+    from flextensor_amd.hip import HostArena, copy_h2d
+
+    from flextensor_amd import workloads as W
+
+    n = W.LLAMA_7B.layer_bytes()
+    g = torch.Generator().manual_seed(0)
+    arena = HostArena(n)
+    arena.tensor[:n].copy_((torch.randn(n // 2, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8))
+    raw = arena.tensor[:n]
+    t0 = time.perf_counter()
+    block = expcode.encode(raw)
+    encode_s = time.perf_counter() - t0
+    dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+    ref = raw.to("cuda")
+
+    def best(fn) -> float:
+        ms = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            ms.append(a.elapsed_time(b))
+        return min(ms)
+
+    out = {"raw_bytes": n, "encoded_bytes": block.nbytes, "ratio": round(block.ratio, 4),
+           "encode_s": round(encode_s, 3), "decode": {}}
+    for grid in grids:
+        pol = nat.copy_policy(0, 2**63 - 1, 1, grid)
+        dst.zero_()
+        ms = best(lambda: expcode.decode_h2d(dst, block, policy=pol))
+        out["decode"][str(grid)] = {"ms": round(ms, 3), "raw_GBps": round(n / ms / 1e6, 2),
+                                    "link_GBps": round(block.nbytes / ms / 1e6, 2),
+                                    "bit_exact": bool(torch.equal(dst, ref))}
+    pol = nat.copy_policy(1 << 40, 2**63 - 1, 1, 8)
+    ms = best(lambda: copy_h2d(dst, raw, nat.COPY_KERNEL, policy=pol))
+    out["zero_copy_raw_8_workgroups"] = {"ms": round(ms, 3), "GBps": round(n / ms / 1e6, 2)}
+    ms = best(lambda: copy_h2d(dst, raw, nat.COPY_SDMA))
+    out["sdma_raw"] = {"ms": round(ms, 3), "GBps": round(n / ms / 1e6, 2)}
+    return out
+
+
 def _encoded_summary(enc: dict, measured_peak: float, raw_tok_s: float | None) -> dict:
     """The 7B decode with exponent-coded blocks: weight bytes per token against the bytes that crossed
     the link, the effective weight rate and the link's own rate."""
@@ -1550,6 +1602,8 @@ def main() -> int:
                     help="skip the 7B decode with attention and MLP projections as separate offload units")
     ap.add_argument("--encoded-only", action="store_true",
                     help="print only the 7B decode with exponent-coded blocks (for profiling it alone)")
+    ap.add_argument("--expcode-sweep", action="store_true",
+                    help="print the encoded-block decode of one 7B layer at several grids against raw copies")
     ap.add_argument("--encoded-finer-units", action="store_true",
                     help="with --encoded-only: each layer's attention and MLP projections as separate units")
     ap.add_argument("--skip-encoded", action="store_true",
@@ -1602,6 +1656,9 @@ def main() -> int:
         return 0
     if args.dit_only:
         print(json.dumps({"dit": bench_dit(12.0, args.dit_tokens, 512, args.dit_steps, args.copy_engine)}), flush=True)
+        return 0
+    if args.expcode_sweep:
+        print(json.dumps({"expcode_sweep": expcode_sweep()}), flush=True)
         return 0
     if args.encoded_only:
         peak = measure_link_peak()
