@@ -1163,7 +1163,8 @@ RING_COPY_PROBES = 3  # ring copies of one 7B-shape decoder layer in the traffic
 
 
 def measure_traffic(args) -> dict | None:
-    """HBM bytes per scatter launch and per ring copy from two ``rocprofv3 --pmc`` child runs.
+    """HBM bytes per scatter launch, per ring copy and per encoded-block decode from two ``rocprofv3 --pmc``
+    child runs.
 
     Each child runs this script in ``--traffic-probe`` mode: one 1 GiB
     device-to-device copy (the runtime's copy kernel, whose traffic is known:
@@ -1174,8 +1175,11 @@ def measure_traffic(args) -> dict | None:
     calibration copy gives the scale of each counter; traffic = scaled
     FETCH_SIZE + scaled WRITE_SIZE, averaged over the scatter launches. For the
     ring copy FETCH_SIZE counts the bytes read from host memory over the link
-    and WRITE_SIZE the bytes written to HBM (``ring_copy``). Returns None when
-    rocprofv3 is not available or a pass fails.
+    and WRITE_SIZE the bytes written to HBM (``ring_copy``). The child then
+    decodes the same layer's bytes, as N(0, 0.02) bf16 weights exponent-coded,
+    ``RING_COPY_PROBES`` times (``expcode_decode``: the encoded bytes read over
+    the link, the raw bytes written). Returns None when rocprofv3 is not
+    available or a pass fails.
     """
     import csv
     import glob
@@ -1211,13 +1215,22 @@ def measure_traffic(args) -> dict | None:
         scat = [row for row in rows if "scatter_kernel" in row["Kernel_Name"]]
         ring = [row for row in rows if "zero_copy_kernel" in row["Kernel_Name"]
                 and int(row.get("Grid_Size", L.RING_KERNEL_GRID * 256)) == L.RING_KERNEL_GRID * 256]
+        dec = [row for row in rows if "expcode_decode_kernel" in row["Kernel_Name"]]
         if not copies or not scat:
             return None
         scale = calib / (float(copies[0]["Counter_Value"]) * 1024)
-        out[ctr] = {"scale": round(scale, 4),
-                    "bytes_per_launch": sum(float(row["Counter_Value"]) for row in scat) * 1024 * scale / len(scat),
-                    "ring_bytes_per_launch": (sum(float(row["Counter_Value"]) for row in ring) * 1024 * scale / len(ring)
-                                              if len(ring) == RING_COPY_PROBES else None)}
+
+        def per_launch(sel: list, want: int | None = None) -> float | None:
+            if not sel or (want is not None and len(sel) != want):
+                return None
+            return sum(float(row["Counter_Value"]) for row in sel) * 1024 * scale / len(sel)
+
+        out[ctr] = {"scale": round(scale, 4), "bytes_per_launch": per_launch(scat),
+                    "ring_bytes_per_launch": per_launch(ring, RING_COPY_PROBES),
+                    "decode_bytes_per_launch": per_launch(dec, RING_COPY_PROBES)}
+        for line in r.stdout.splitlines():
+            if line.startswith("expcode_encoded_bytes "):
+                out["expcode_encoded_bytes"] = int(line.split()[1])
         shutil.rmtree(d, ignore_errors=True)
     res = {"traffic": out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"],
            "fetch_bytes_per_launch": out["FETCH_SIZE"]["bytes_per_launch"],
@@ -1226,6 +1239,11 @@ def measure_traffic(args) -> dict | None:
     if out["FETCH_SIZE"]["ring_bytes_per_launch"] is not None and out["WRITE_SIZE"]["ring_bytes_per_launch"] is not None:
         res["ring_copy"] = {"host_read_bytes_per_launch": out["FETCH_SIZE"]["ring_bytes_per_launch"],
                             "hbm_write_bytes_per_launch": out["WRITE_SIZE"]["ring_bytes_per_launch"]}
+    if (out["FETCH_SIZE"]["decode_bytes_per_launch"] is not None
+            and out["WRITE_SIZE"]["decode_bytes_per_launch"] is not None):
+        res["expcode_decode"] = {"host_read_bytes_per_launch": out["FETCH_SIZE"]["decode_bytes_per_launch"],
+                                 "hbm_write_bytes_per_launch": out["WRITE_SIZE"]["decode_bytes_per_launch"],
+                                 "encoded_bytes_per_launch": out.get("expcode_encoded_bytes")}
     return res
 
 
@@ -1251,6 +1269,16 @@ def traffic_probe(args) -> int:
     for _ in range(RING_COPY_PROBES):
         nat.copy_h2d(slot.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, xs.handle, ring_policy)
     xs.synchronize()
+    # the same layer's bytes as N(0, 0.02) bf16 weights, exponent-coded, decoded as the encoded ring does
+    from flextensor_amd import expcode
+
+    g = torch.Generator().manual_seed(0)
+    arena.tensor[:n].copy_((torch.randn(n // 2, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8))
+    block = expcode.encode(arena.tensor[:n])
+    for _ in range(RING_COPY_PROBES):
+        expcode.decode_h2d(slot, block, stream=xs)
+    xs.synchronize()
+    print(f"expcode_encoded_bytes {block.nbytes}", flush=True)
     return 0
 
 
@@ -1825,7 +1853,7 @@ def main() -> int:
             if tr is not None:
                 line["roofline"]["traffic"] = int(tr["traffic"])
                 line["roofline"]["traffic_detail"] = {k: (int(v) if "bytes" in k else v) for k, v in tr.items()
-                                                      if k not in ("traffic", "ring_copy")}
+                                                      if k not in ("traffic", "ring_copy", "expcode_decode")}
                 _log(f"traffic per scatter launch: {tr['traffic'] / 1e9:.3f} GB "
                      f"(algorithmic {line['roofline']['algorithmic_bytes_per_launch'] / 1e9:.3f} GB)")
                 ring_tr = tr.get("ring_copy")
@@ -1834,6 +1862,12 @@ def main() -> int:
                     line["roofline_ring_copy"]["traffic"] = int(ring_tr["hbm_write_bytes_per_launch"])
                     line["roofline_ring_copy"]["traffic_detail"] = {k: int(v) for k, v in ring_tr.items()}
                     _log(f"traffic per ring copy: {ring_tr}")
+                dec_tr = tr.get("expcode_decode")
+                enc_roof = (line.get("llama7b_encoded_blocks") or {}).get("ring_copies")
+                if dec_tr is not None and enc_roof:
+                    enc_roof["traffic"] = int(dec_tr["hbm_write_bytes_per_launch"])
+                    enc_roof["traffic_detail"] = {k: int(v) for k, v in dec_tr.items() if v is not None}
+                    _log(f"traffic per encoded-block decode: {dec_tr}")
     if not args.skip_mlp:
         gc.collect()
         torch.cuda.empty_cache()
