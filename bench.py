@@ -1757,7 +1757,8 @@ def main() -> int:
                    "streamed_layers": llama["streamed_layers"], "resident_layers": llama["resident_layers"],
                    "streamed_bytes_per_token": llama["streamed_bytes_per_token"], "copy_engine": args.copy_engine,
                    "copy_policy": llama["copy_policy"], "copy_policy_source": llama["copy_policy_source"],
-                   "ring_order": llama["ring_order"], "transfer_stream": llama["transfer_stream"]},
+                   "ring_order": llama["ring_order"], "transfer_stream": llama["transfer_stream"],
+                   "encode_streamed_blocks": False},
         "tok_s": round(llama["decode_tok_s"], 3),
         "prefill_tok_s": round(llama["prefill_tok_s"], 1),
         "link": {"decode_effective_GBps": round(llama["decode_effective_GBps"], 3),
