@@ -30,8 +30,10 @@ Accepted for compatibility, acting differently or not at all here:
 Added for this build: ``max_gpu_mem_bytes`` (a budget in bytes instead of a
 fraction), ``copy_engine`` (``auto`` / ``sdma`` / ``kernel`` / ``staged``),
 ``loader_order`` (``auto`` / ``default`` / ``reordered``),
-``max_inflight_passes`` (bounded host run-ahead) and ``encode_streamed_blocks``
-(streamed blocks cross the link exponent-coded and are decoded on the GPU).
+``max_inflight_passes`` (bounded host run-ahead), ``encode_streamed_blocks``
+(streamed blocks cross the link exponent-coded and are decoded on the GPU) and
+``encode_resident_blocks`` (resident units kept exponent-coded in HBM, so more
+of them fit the budget and fewer stream).
 """
 
 from __future__ import annotations
@@ -86,6 +88,11 @@ class OffloadConfig(BaseModel):
     # and decode it into its ring slot with a zero-copy kernel; the slot receives the raw bytes exactly.
     # A block is kept encoded only when that saves a tenth of its bytes. allocation_block_transfer only.
     encode_streamed_blocks: bool = False
+    # When the resident units do not fit the GPU budget raw, keep some exponent-coded in device memory
+    # (about 0.75 of their bytes) instead of streaming more units; each such unit is decoded from HBM into
+    # one shared slot on the compute stream as it runs. For link-bound passes: the fewer units stream, the
+    # fewer bytes cross the link. allocation_block_transfer only, without shm_enabled.
+    encode_resident_blocks: bool = False
     # Cross-process sharing of the streamed blocks through POSIX shared memory
     # (config.py:97-125): blocks live in named segments under ``shm_namespace``.
     shm_enabled: bool = False
@@ -109,6 +116,11 @@ class OffloadConfig(BaseModel):
             raise ValueError("shm_namespace must be non-empty when shm_enabled=True")
         if self.encode_streamed_blocks and self.transfer_mode != "allocation_block_transfer":
             raise ValueError("encode_streamed_blocks needs transfer_mode='allocation_block_transfer'")
+        if self.encode_resident_blocks and self.transfer_mode != "allocation_block_transfer":
+            raise ValueError("encode_resident_blocks needs transfer_mode='allocation_block_transfer'")
+        if self.encode_resident_blocks and self.shm_enabled:
+            raise ValueError("encode_resident_blocks keeps its host blocks private: it cannot be combined with "
+                             "shm_enabled")
         if self.num_blocks < self.min_blocks:
             raise ValueError(f"num_blocks ({self.num_blocks}) must be >= min_blocks ({self.min_blocks})")
         if self.profile_mode == "torch_function":

@@ -185,13 +185,18 @@ class AllocationBlockController:
         shm_block_name_map: Mapping[str, str] | None = None,
         load_from_shm: bool = False,
         encode_blocks: bool = False,
+        hbm_encoded: Mapping[str, int] | None = None,
     ) -> None:
         """``shm_block_name_map`` puts each label's host block in a named shared-memory
         segment (loaders.py:1150-1175); with ``load_from_shm`` the segments already exist
         and are mapped instead of packed, and the tensors only supply their layouts.
         ``encode_blocks`` keeps an exponent-coded copy of each label's block that saves at least a
         tenth of its bytes (:mod:`~flextensor_amd.expcode`); such a label's transfer is one decode
-        launch that writes the raw block into its slot (no reference counterpart)."""
+        launch that writes the raw block into its slot (no reference counterpart).
+        ``hbm_encoded`` maps block keys of units kept resident in encoded form to the device bytes
+        reserved for each encoded block: their slot group is packed into pageable host blocks (nothing
+        crosses the link), each block is encoded into device memory, and :meth:`decode_resident`
+        rebuilds it in its slot on the current stream (no reference counterpart)."""
         if load_from_shm and not shm_block_name_map:
             raise ValueError("load_from_shm needs shm_block_name_map")
         self.device_gpu = torch.device(device_gpu)
@@ -211,12 +216,15 @@ class AllocationBlockController:
         self._gpu_slots: list[AllocationBlock] = []
         self.encoded: dict[str, Any] = {}  # label -> expcode.EncodedBlock
         self.use_encoded = True  # transfers of encoded labels decode (False: they copy the raw blocks)
+        self.hbm_capacity = dict(hbm_encoded or {})
+        self.hbm_encoded: dict[str, Any] = {}  # block key -> expcode.DeviceEncodedBlock
         self._rollback = _Rollback()
         _refuse_overlapping_sources(tensors_map, strategy_map)
         try:
             for _slot_id, labels in allocation_ordered.items():
+                in_hbm = bool(labels) and all(x in self.hbm_capacity for x in labels)
                 manager = AllocationManager(host_pinner=host_pinner, memory_alignment=memory_alignment,
-                                            release_tensor_memory=False)
+                                            release_tensor_memory=False, pinned_memory=not in_hbm)
                 for label in labels:
                     strategy = strategy_map.get(label, ())
                     if not strategy:
@@ -244,10 +252,18 @@ class AllocationBlockController:
                 self.label_to_tensor_views_map[label] = views
                 self.block_map_gpu[label_to_block_id[label]] = prefix
                 self.gpu_block_view_map[label] = prefix
+            if self.hbm_capacity:
+                from . import expcode
+
+                for key, cap in self.hbm_capacity.items():
+                    self.hbm_encoded[key] = expcode.DeviceEncodedBlock.from_raw(self.block_map_cpu[key].block, cap,
+                                                                                self.device_gpu)
             if encode_blocks:
                 from . import expcode
 
                 for label, block in self.block_map_cpu.items():
+                    if label in self.hbm_capacity:
+                        continue
                     enc = expcode.encode_if_smaller(block.block)
                     if enc is not None:
                         self.encoded[label] = enc
@@ -286,15 +302,27 @@ class AllocationBlockController:
         if not non_blocking:
             current_stream(dst.device).synchronize()
 
+    def decode_resident(self, key: str) -> None:
+        """Rebuild the raw block of ``key`` (a unit kept encoded in HBM) in its slot, on the current
+        stream."""
+        self.hbm_encoded[key].decode(self.gpu_block_view_map[key])
+
     def transfer_bytes(self, label: str) -> int:
         """Bytes ``label``'s transfer writes into its slot (the raw block)."""
         return self.block_map_cpu[label].nbytes
 
     def refresh_encoded(self) -> None:
         """Re-encode every encoded block in place from its host block, after the host blocks were
-        rewritten (a state-dict load). No transfer may be in flight."""
+        rewritten (a state-dict load). No transfer or decode may be in flight. A block kept in HBM
+        whose new encoding outgrows its reservation raises ValueError naming it."""
         for label, enc in self.encoded.items():
             enc.reencode(self.block_map_cpu[label].block)
+        for key, dev in self.hbm_encoded.items():
+            try:
+                dev.reencode(self.block_map_cpu[key].block)
+            except ValueError as exc:
+                raise ValueError(f"unit block {key!r} kept encoded in HBM: {exc}; release() and offload the "
+                                 "model again to size the reservation for the new weights") from exc
 
     def link_bytes(self, label: str) -> int:
         """Bytes ``label``'s transfer reads over the host link: the encoded block when there is one."""
@@ -312,6 +340,7 @@ class AllocationBlockController:
 
     def _clear(self) -> None:
         self.encoded.clear()
+        self.hbm_encoded.clear()
         for d in (self.block_map_cpu, self.label_to_cpu_tensor_id_map, self.label_to_gpu_block, self.block_map_gpu,
                   self.gpu_block_view_map, self.label_to_tensor_views_map, self.tensor_id_to_view_map):
             d.clear()
@@ -341,9 +370,11 @@ class AllocationBlockController:
         self.label_to_tensor_views_map = {}
         self.tensor_id_to_view_map = {}
         self._gpu_slots = []
+        self.hbm_encoded = {}
 
     def get_gpu_memory_bytes(self) -> int:
-        return sum(s.nbytes for s in self._gpu_slots)
+        """Ring slots, the slot units kept in HBM decode into, and their encoded blocks."""
+        return sum(s.nbytes for s in self._gpu_slots) + sum(d.capacity for d in self.hbm_encoded.values())
 
 
 class RawBlockController:

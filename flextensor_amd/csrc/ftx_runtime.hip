@@ -773,6 +773,32 @@ int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const f
   return FTX_OK;
 }
 
+int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid,
+                           void *stream) {
+  FTX_REQUIRE_LIVE();
+  if (raw_bytes == 0) return FTX_OK;
+  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  if (grid < 0 || grid > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "grid must be in [0, 2^20]");
+  if (reinterpret_cast<uintptr_t>(dst) % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+    return ftx::fail(FTX_ERR_INVALID, "decode source and destination need 16-byte alignment");
+  // The header is in device memory: the caller states the raw size, and the kernel reads the rest of the
+  // header when it runs (a header of another raw size writes nothing; escape reads stay within src_bytes).
+  const uint64_t groups = (raw_bytes / 2 + ftx::kExpcodeGroupWords - 1) / ftx::kExpcodeGroupWords;
+  const uint64_t off_x = ftx::kExpcodeHeaderBytes + ftx::kExpcodeGroupWords * groups +
+                         ftx::kExpcodeGroupWords / 2 * groups + (4 * (groups + 1) + 15) / 16 * 16;
+  if (src_bytes < off_x) return ftx::fail(FTX_ERR_INVALID, "encoded block is shorter than its raw size needs");
+  int rc = ftx::check_device_range(dst, raw_bytes, "decode destination");
+  if (rc == FTX_OK) rc = ftx::check_device_range(src, src_bytes, "encoded block");
+  if (rc != FTX_OK) return rc;
+  ftx::DeviceState *st = nullptr;
+  rc = ftx::device_state(&st);
+  if (rc != FTX_OK) return rc;
+  const int g = grid > 0 ? grid : st->cu_count;  // HBM to HBM: one workgroup per CU by default
+  const size_t reserve = g <= ftx::kZeroCopyReserveMaxGrid ? st->copy_reserve_lds : 0;
+  FTX_HIP(ftx::launch_expcode_decode(dst, src, src_bytes, raw_bytes, g, reserve, static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
 int ftx_set_staging_policy(size_t piece_bytes, int n_threads) { return ftx::set_staging_policy(piece_bytes, n_threads); }
 
 int ftx_get_staging_policy(size_t *piece_bytes, int *n_threads) {

@@ -8,6 +8,10 @@ reads the encoded bytes over the link and writes the raw bytes into the ring slo
 format (``FTXE`` v1) codes each bf16 word's exponent in 4 bits for the block's 15 most frequent
 exponents, with the rest as escapes; the encoder is the library's host routine
 (``ftx_expcode_encode``).
+
+With ``OffloadConfig.encode_resident_blocks`` resident units are kept encoded in device memory instead
+(:class:`DeviceEncodedBlock`): more units fit the GPU budget, fewer stream, and each such unit is
+decoded from HBM (``ftx_expcode_decode_d2d``) into one shared slot on the compute stream as it runs.
 """
 
 from __future__ import annotations
@@ -111,3 +115,95 @@ def decode_h2d(dst: torch.Tensor, block: EncodedBlock, stream: HipStream | None 
     s = stream if stream is not None else current_stream(dst.device)
     pol = ctypes.byref(policy) if policy is not None else None
     nat.call("ftx_expcode_decode_h2d", dst.data_ptr(), block.arena.ptr, block.arena.nbytes, pol, s.handle)
+
+
+def packed_encoded_size(tensors: list[torch.Tensor], alignment: int, scratch: torch.Tensor | None = None) -> \
+        tuple[int, int]:
+    """(encoded bytes, raw bytes) of the block that packs ``tensors`` (CPU) at ``alignment``, as a block
+    controller packs them: gaps zeroed, so the size is exact. ``scratch`` (uint8, CPU), when large enough,
+    holds the packed bytes instead of a new buffer."""
+    from .layout import pack_into, plan_block
+
+    slots, total = plan_block(tensors, alignment)
+    if total == 0:
+        return 0, 0
+    buf = scratch[:total] if scratch is not None and scratch.numel() >= total else torch.empty(total,
+                                                                                                 dtype=torch.uint8)
+    pack_into(buf, slots, tensors)
+    return encoded_size(buf), total
+
+
+class DeviceEncodedBlock:
+    """An encoded block kept in device memory: ``dev`` (uint8, ``capacity`` bytes) holds ``nbytes`` of
+    encoded bytes for a raw block of ``raw_bytes``. Serves units kept resident in HBM in encoded form:
+    :meth:`decode` rebuilds the raw block on the device before the unit runs.
+
+    :meth:`reencode` rewrites the block in place (same device buffer, so decodes captured in a graph stay
+    valid and read the new header when they run) as long as the new encoding fits ``capacity``."""
+
+    __slots__ = ("dev", "nbytes", "raw_bytes")
+
+    def __init__(self, dev: torch.Tensor, nbytes: int, raw_bytes: int) -> None:
+        self.dev = dev
+        self.nbytes = int(nbytes)
+        self.raw_bytes = int(raw_bytes)
+
+    @staticmethod
+    def _encode_host(raw: torch.Tensor) -> torch.Tensor:
+        ptr, n = _raw_ptr(raw)
+        size = encoded_size(raw)
+        host = torch.empty(max(size, 1), dtype=torch.uint8)
+        out = ctypes.c_size_t(0)
+        nat.call("ftx_expcode_encode", ptr, n, host.data_ptr(), host.numel(), ctypes.byref(out))
+        return host[: out.value]
+
+    @classmethod
+    def from_raw(cls, raw: torch.Tensor, capacity: int, device: torch.device) -> "DeviceEncodedBlock":
+        """Encode ``raw`` (contiguous CPU) into a new device buffer of ``capacity`` bytes."""
+        host = cls._encode_host(raw)
+        if host.numel() > capacity:
+            raise ValueError(f"the encoding needs {host.numel()} bytes, more than its capacity of {capacity}")
+        dev = torch.empty(max(int(capacity), 16), dtype=torch.uint8, device=device)
+        dev[: host.numel()].copy_(host)
+        return cls(dev, host.numel(), raw.numel() * raw.element_size())
+
+    @property
+    def capacity(self) -> int:
+        return self.dev.numel()
+
+    @property
+    def ratio(self) -> float:
+        return self.nbytes / self.raw_bytes if self.raw_bytes else 1.0
+
+    def reencode(self, raw: torch.Tensor) -> None:
+        """Encode ``raw`` (the same raw size) into this block's device buffer; the copy completes before
+        this returns. No decode of this block may be in flight. Raises ValueError (and leaves the block
+        unchanged) when the new encoding does not fit the capacity."""
+        n = raw.numel() * raw.element_size()
+        if n != self.raw_bytes:
+            raise ValueError(f"raw block of {n} bytes, but this block encodes {self.raw_bytes}")
+        host = self._encode_host(raw)
+        if host.numel() > self.capacity:
+            raise ValueError(f"the new encoding needs {host.numel()} bytes, more than the {self.capacity} "
+                             "reserved on the device")
+        self.dev[: host.numel()].copy_(host)
+        torch.cuda.synchronize(self.dev.device)
+        self.nbytes = host.numel()
+
+    def decode(self, dst: torch.Tensor, stream: HipStream | None = None) -> None:
+        """Stream-ordered decode into the first ``raw_bytes`` bytes of ``dst`` (one workgroup per CU)."""
+        decode_d2d(dst, self.dev, self.raw_bytes, stream)
+
+
+def decode_d2d(dst: torch.Tensor, encoded: torch.Tensor, raw_bytes: int, stream: HipStream | None = None,
+               grid: int = 0) -> None:
+    """Stream-ordered decode of an encoded block held in device memory (``encoded``, a uint8 device tensor)
+    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs one workgroup per CU."""
+    if dst.device.type != "cuda" or encoded.device.type != "cuda":
+        raise ValueError("decode_d2d needs device tensors")
+    if raw_bytes > dst.numel() * dst.element_size():
+        raise ValueError(f"decoded block of {raw_bytes} bytes does not fit destination of "
+                         f"{dst.numel() * dst.element_size()} bytes")
+    s = stream if stream is not None else current_stream(dst.device)
+    nat.call("ftx_expcode_decode_d2d", dst.data_ptr(), encoded.data_ptr(), encoded.numel(), raw_bytes, int(grid),
+             s.handle)

@@ -180,8 +180,18 @@ def pack_into(block: torch.Tensor, slots: Sequence[TensorSlot], tensors: Sequenc
 
     A dense tensor is copied as raw storage bytes, so the block holds the
     bytes in the tensor's own memory order; a tensor with gaps is copied
-    element-wise into a C-contiguous slot.
+    element-wise into a C-contiguous slot. The alignment gaps between slots
+    and after the last are zeroed, so a block's bytes depend only on its
+    tensors.
     """
+    pos = 0
+    flat = block.view(torch.uint8).reshape(-1)
+    for slot in sorted(slots, key=lambda x: x.offset):
+        if slot.offset > pos:
+            flat[pos:slot.offset].zero_()
+        pos = max(pos, slot.offset + slot.nbytes)
+    if flat.numel() > pos:
+        flat[pos:].zero_()
     views = []
     for slot, t in zip(slots, tensors):
         view = slot.view(block)

@@ -41,7 +41,7 @@ import os
 import threading
 import time
 import types
-from collections.abc import Callable, Iterator, Sequence
+from collections.abc import Callable, Iterator, Mapping, Sequence
 from dataclasses import dataclass, field
 from enum import Enum
 from typing import Any
@@ -130,6 +130,8 @@ class StreamPlan:
     reordered: bool
     budget_bytes: int | None
     planned_gpu_bytes: int
+    # resident units kept encoded in HBM (encode_resident_blocks), and the device bytes each reserves
+    encoded_resident: dict[str, int] = field(default_factory=dict)
 
 
 class _CompiledCall(threading.local):
@@ -175,8 +177,35 @@ class _Unit:
                                             for p, n in zip(self.params, names)], duration)
 
 
+def encode_residents(resident: Sequence[str], raw_bytes: Mapping[str, int],
+                     encodable: Mapping[str, tuple[int, int]], room: int) -> tuple[dict[str, int], int] | None:
+    """The fewest resident units to keep encoded in HBM so that the residents fit ``room`` bytes.
+
+    ``encodable[label]`` is (device bytes reserved for its encoded block, bytes of its packed raw block).
+    The units kept encoded share one decode slot, as large as the largest of their packed raw blocks,
+    counted once. Units are taken by the bytes they save, largest first (ties: earlier in the pass).
+    Returns ({label: reserved bytes}, resident bytes including the decode slot), or None when even
+    encoding every candidate does not fit."""
+    placed = sum(raw_bytes[x] for x in resident)
+    if placed <= room:
+        return {}, placed
+    pos = {x: i for i, x in enumerate(resident)}
+    cands = sorted((x for x in resident if x in encodable and encodable[x][0] < raw_bytes[x]),
+                   key=lambda x: (encodable[x][0] - raw_bytes[x], pos[x]))
+    chosen: dict[str, int] = {}
+    slot = 0
+    for x in cands:
+        placed -= raw_bytes[x] - encodable[x][0]
+        slot = max(slot, encodable[x][1])
+        chosen[x] = encodable[x][0]
+        if placed + slot <= room:
+            return chosen, placed + slot
+    return None
+
+
 def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | None, base_bytes: int,
-                   num_blocks: int, min_blocks: int | None = None) -> StreamPlan:
+                   num_blocks: int, min_blocks: int | None = None,
+                   encodable: Mapping[str, tuple[int, int]] | None = None) -> StreamPlan:
     """Choose streamed units and the slot plan under a GPU byte budget.
 
     The fewest units stream that fit, spread evenly over the pass: the
@@ -192,6 +221,11 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
     reference searches the same range, config.py:207-225). Slots beyond
     ``num_blocks`` are added only while the reference's slot-reuse check
     reports a hazard.
+
+    With ``encodable`` (``encode_resident_blocks``: per unit, the device
+    bytes of its encoded block and the bytes of its packed raw block) a
+    resident set that does not fit raw may keep some units encoded in HBM
+    (:func:`encode_residents`), so fewer units stream for the same budget.
     """
     by_label = {u.label: u for u in units}
     labels = list(order)
@@ -222,9 +256,16 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
             if not check_overlap_constraint(bd.transfer_to_compute_map, stats, bd.label_to_block_id):
                 continue
             hazard_free = True
-            gpu = placed + sum(bd.block_sizes.values())
+            ring = sum(bd.block_sizes.values())
+            gpu = placed + ring
+            enc: dict[str, int] = {}
+            if budget is not None and encodable and gpu > budget:
+                got = encode_residents(resident, {x: by_label[x].nbytes for x in resident}, encodable,
+                                       budget - base_bytes - ring)
+                if got is not None:
+                    enc, gpu = got[0], base_bytes + got[1] + ring
             if budget is None or gpu <= budget:
-                chosen = (bd, gpu)
+                chosen = (bd, gpu, enc)
                 break
             if blocks > hi:
                 break  # extra slots only grow the footprint
@@ -232,7 +273,7 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
             raise RuntimeError("no hazard-free slot plan found")
         if chosen is None:
             continue
-        bd, gpu = chosen
+        bd, gpu, enc = chosen
         reordered = bool(resident)
         if reordered:
             t2c, l2b, remapped = rearrange_transfers(bd.transfer_to_compute_map, bd.label_to_block_id, stats)
@@ -244,7 +285,7 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
                 label_to_block_id=l2b,
                 transfer_to_compute_map=t2c,
             )
-        return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
+        return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu, enc)
     # Even streaming every unit does not fit: the tensors placed outside the
     # units leave too little for the ring (gpu_budget.py:200-225).
     raise RuntimeError(
@@ -305,12 +346,14 @@ def state_from_plan(model: nn.Module, units: Sequence[_Unit], plan: StreamPlan, 
 
 
 def plan_from_state(state: TensorManagerState, units: Sequence[_Unit], base_bytes: int,
-                    budget: int | None) -> StreamPlan:
+                    budget: int | None, encodable: Mapping[str, tuple[int, int]] | None = None) -> StreamPlan:
     """The saved plan re-keyed to the live tensors by name (the role of state_handler.py:673-745, 1072-1420).
 
     ``units`` are the live offload units in the saved execution order. A
     streamed tensor that is missing, or whose size, dtype or layout differs
-    from the saved metadata, raises ``ValueError``.
+    from the saved metadata, raises ``ValueError``. With ``encodable``, residents
+    that do not fit the budget raw are kept encoded in HBM as
+    :func:`plan_streaming` keeps them.
     """
     by_name = {n: p for u in units for n, p in zip(u.names, u.params)}
     strategy: dict[str, list[TensorStatistics]] = {}
@@ -337,8 +380,15 @@ def plan_from_state(state: TensorManagerState, units: Sequence[_Unit], base_byte
     nxt = {a: order[(i + 1) % len(order)] for i, a in enumerate(order)}
     reordered = any(nxt.get(t) != c for t, c in state.transfer_to_compute_map.items())
     by_label = {u.label: u for u in units}
-    gpu = base_bytes + sum(by_label[x].nbytes for x in resident) + (sum(bd.block_sizes.values()) if bd else 0)
-    return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu)
+    ring = sum(bd.block_sizes.values()) if bd else 0
+    gpu = base_bytes + sum(by_label[x].nbytes for x in resident) + ring
+    enc: dict[str, int] = {}
+    if budget is not None and encodable and bd is not None and gpu > budget:
+        got = encode_residents(resident, {x: by_label[x].nbytes for x in resident}, encodable,
+                               budget - base_bytes - ring)
+        if got is not None:
+            enc, gpu = got[0], base_bytes + got[1] + ring
+    return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu, enc)
 
 
 # Attributes every nn.Module gets from its constructor (parameters, buffers,
@@ -458,6 +508,8 @@ class OffloadManager:
         self._control: str | None = None
         self._from_state = False
         self._reload_pending = False
+        self._hbm_keys: dict[str, str] = {}  # unit label -> its block key, for units kept encoded in HBM
+        self._hbm_stale: str | None = None  # why those blocks no longer match the model's weights
         self._pinner: HostPinner | None = None
         self.memory_transfer_stats: dict[int, float] = {}
         self.link: LinkMeasurement | None = None  # the measured host link and the copy policy it chose
@@ -643,6 +695,7 @@ class OffloadManager:
         self._control, self._suspend_count = None, 0
         self._from_state = False
         self._reload_pending = False
+        self._hbm_keys, self._hbm_stale = {}, None
         self.skip_discovery_honored = None
         self.compile_fn = None
         self._load_from_shm = False
@@ -1184,6 +1237,7 @@ class OffloadManager:
             self._pinner = None
             self._from_state = False
             self._reload_pending = False
+            self._hbm_keys, self._hbm_stale = {}, None
             self.skip_discovery_honored = None
             self.loader = self.controller = self.plan = None
             self.link = None
@@ -1457,6 +1511,11 @@ class OffloadManager:
             if self._reload_pending and self.order and label == self.order[0]:
                 self._reload_if_pending()  # a load on a submodule, which the root's load hook did not see
             self.loader.enter(label)
+            key = self._hbm_keys.get(label)
+            if key is not None:
+                if self._hbm_stale is not None:
+                    raise RuntimeError(f"offload manager {self.name!r}: {self._hbm_stale}")
+                self.controller.decode_resident(key)  # on the compute stream, ahead of the unit's kernels
             return
         if hip.is_capturing():
             raise RuntimeError(f"offload manager {self.name!r} is in {self.phase.value}: run the discovery and "
@@ -1585,11 +1644,44 @@ class OffloadManager:
             budget = available
         return budget
 
-    def _plan_from_state(self, state: TensorManagerState) -> StreamPlan:
+    def _plan_from_state(self, state: TensorManagerState, budget: int | None = None,
+                         encodable: Mapping[str, tuple[int, int]] | None = None) -> StreamPlan:
         for st in state.stats:
             if st.duration:
                 self.durations.setdefault(st.label, []).append(st.duration)
-        return plan_from_state(state, [self._unit(x) for x in self.order], self._resident_bytes, self._budget())
+        return plan_from_state(state, [self._unit(x) for x in self.order], self._resident_bytes,
+                               self._budget() if budget is None else budget, encodable)
+
+    def _encodable(self, units: Sequence[_Unit], budget: int | None) -> dict[str, tuple[int, int]] | None:
+        """Per unit whose packed block encodes to under 0.9 of its bytes: (device bytes to reserve for the
+        encoded block, bytes of the packed raw block). None when there is no budget or everything fits
+        raw. The reservation adds max(64 KiB, 0.1% of the raw block) to the encoded size, room for a
+        later state-dict load to re-encode in place."""
+        if budget is None or self._resident_bytes + sum(u.nbytes for u in units) <= budget:
+            return None
+        from . import expcode
+        from .layout import DEFAULT_ALIGNMENT
+
+        t0 = time.perf_counter()
+        out: dict[str, tuple[int, int]] = {}
+        scratch: torch.Tensor | None = None
+        for u in units:
+            seen: set[int] = set()
+            tensors = [p for p in u.params if not (id(p) in seen or seen.add(id(p)))]
+            if not tensors or any(p.device.type != "cpu" for p in tensors):
+                continue
+            need = sum(p.numel() * p.element_size() for p in tensors) + DEFAULT_ALIGNMENT * len(tensors)
+            if scratch is None or scratch.numel() < need:
+                scratch = torch.empty(need, dtype=torch.uint8)
+            size, raw = expcode.packed_encoded_size(tensors, DEFAULT_ALIGNMENT, scratch)
+            if raw == 0 or size > expcode.DEFAULT_MAX_RATIO * raw:
+                continue
+            reserve = (size + max(1 << 16, raw // 1024) + 255) // 256 * 256
+            out[u.label] = (min(reserve, raw), raw)
+        LOGGER.info("offload %r: encode_resident_blocks: %d of %d units encode below %.2f of their bytes "
+                    "(sized in %.1f s)", self.name, len(out), len(units), expcode.DEFAULT_MAX_RATIO,
+                    time.perf_counter() - t0)
+        return out
 
     def _to_inference(self, state: TensorManagerState | None = None) -> None:
         t0 = time.perf_counter()
@@ -1597,15 +1689,18 @@ class OffloadManager:
         units_in_order = [self._unit(x) for x in self.order] if self.order else list(self.units)
         order = [u.label for u in units_in_order]
         blocks = max(cfg.num_blocks, 2)
+        budget = self._budget()
+        encodable = self._encodable(units_in_order, budget) if cfg.encode_resident_blocks else None
         if state is not None:
-            self.plan = self._plan_from_state(state)
+            self.plan = self._plan_from_state(state, budget, encodable)
         else:
-            self.plan = plan_streaming(units_in_order, order, self._budget(), self._resident_bytes, blocks,
-                                       cfg.min_blocks)
+            self.plan = plan_streaming(units_in_order, order, budget, self._resident_bytes, blocks,
+                                       cfg.min_blocks, encodable)
         plan = self.plan
         self._validate_source_storage(plan)
-        resident_params = [p for x in plan.resident for p in self._unit(x).params]
-        with _oom_context(resident_params, f"the {len(plan.resident)} offload units kept resident",
+        hbm = plan.encoded_resident
+        resident_params = [p for x in plan.resident if x not in hbm for p in self._unit(x).params]
+        with _oom_context(resident_params, f"the {len(plan.resident) - len(hbm)} offload units kept resident",
                           "Lower the budget (max_gpu_mem_fraction / max_gpu_mem_bytes) so that more units stream."):
             self._resident_bytes += self._upload_into(resident_params)
         layer_stats = [self._unit(x).stats(self._duration(x)) for x in order]
@@ -1614,7 +1709,7 @@ class OffloadManager:
         else:
             bd = plan.block_data
             self._choose_copy_policy(plan, state)
-            tensors_map = {id(p): p for x in plan.streamed for p in self._unit(x).params}
+            tensors_map = {id(p): p for x in [*plan.streamed, *hbm] for p in self._unit(x).params}
             pinner = self._pinner = HostPinner(cfg.pinned_memory_mode, enabled=cfg.pinned_memory)
             mode = nat.COPY_MODES[cfg.copy_engine]
             try:
@@ -1764,6 +1859,7 @@ class OffloadManager:
         for tid, t in tensors_map.items():
             t.data = bound[tid]
         self.loader = self.timing = None
+        self._hbm_keys, self._hbm_stale = {}, None
         controller, self.controller = self.controller, None
         if controller is not None:
             controller.abort_construction(primary)
@@ -1852,9 +1948,14 @@ class OffloadManager:
         if not self._reload_pending or self.phase != OffloadPhase.INFERENCE or hip.is_capturing():
             return
         self._reload_pending = False
-        if getattr(self.controller, "encoded", None):  # the new host bytes reach the link only once re-encoded
+        # the new host bytes reach the link, or the units kept encoded in HBM, only once re-encoded
+        if getattr(self.controller, "encoded", None) or getattr(self.controller, "hbm_encoded", None):
             torch.cuda.synchronize(self.device)
-            self.controller.refresh_encoded()
+            try:
+                self.controller.refresh_encoded()
+            except ValueError as exc:
+                self._hbm_stale = f"{exc} (the units kept encoded in HBM no longer hold the loaded weights)"
+                raise
         preload = getattr(self.loader, "preload", None)
         if preload is not None:
             preload()
@@ -1878,13 +1979,28 @@ class OffloadManager:
                     labels = [x for group in bd.allocation_ordered.values() for x in group
                               if plan.strategy_map.get(x)]
                     shm_names = {x: f"{cfg.shm_namespace}_b{i}" for i, x in enumerate(labels)}
-            self.controller = AllocationBlockController(bd.allocation_ordered, self.device, tensors_map,
-                                                        plan.strategy_map, bd.label_to_block_id,
+            # Units kept encoded in HBM: one more slot group, keyed apart from the ring's transfer labels
+            allocation_ordered, strategy_map, l2b = bd.allocation_ordered, plan.strategy_map, bd.label_to_block_id
+            keys = {x: f"hbm::{x}" for x in plan.encoded_resident}
+            if keys:
+                clash = set(keys.values()) & set(strategy_map)
+                if clash:
+                    raise ValueError(f"offload unit labels {sorted(clash)} clash with the keys of units kept "
+                                     "encoded in HBM; rename them or turn encode_resident_blocks off")
+                tier = min(allocation_ordered, default=0) - 1
+                allocation_ordered = {**allocation_ordered, tier: list(keys.values())}
+                strategy_map = {**strategy_map, **{k: list(self._unit(x).stats().tensors) for x, k in keys.items()}}
+                l2b = {**l2b, **{k: tier for k in keys.values()}}
+            self.controller = AllocationBlockController(allocation_ordered, self.device, tensors_map,
+                                                        strategy_map, l2b,
                                                         host_pinner=pinner, copy_mode=mode, copy_policy=policy,
                                                         shm_block_name_map=shm_names,
                                                         load_from_shm=self._load_from_shm,
                                                         encode_blocks=cfg.encode_streamed_blocks
-                                                        and not self._measured_compute_bound())
+                                                        and not self._measured_compute_bound(),
+                                                        hbm_encoded={keys[x]: n
+                                                                     for x, n in plan.encoded_resident.items()})
+            self._hbm_keys = keys
             if cfg.encode_streamed_blocks and not self.controller.encoded:
                 LOGGER.info("offload %r: encode_streamed_blocks: %s; the blocks cross the link raw", self.name,
                             "the pass is compute-bound" if self._measured_compute_bound()
@@ -1903,6 +2019,8 @@ class OffloadManager:
             if label in plan.streamed and bd is not None:
                 src = producer.get(label, "?")
                 where = f"slot {bd.label_to_block_id.get(src, '?')}, loaded during {src!r}"
+            elif label in plan.encoded_resident:
+                where = f"resident, exponent-coded in HBM ({plan.encoded_resident[label] / 2**20:.2f} MB)"
             else:
                 where = "resident"
             rows.append(f"{label:<32} {u.nbytes / 2**20:>10.2f} {self._duration(label):>9.3f}  {where}")

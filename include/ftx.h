@@ -206,6 +206,13 @@ int ftx_expcode_encode(const void *raw, size_t nbytes, void *out, size_t out_cap
 int ftx_expcode_raw_bytes(const void *src, size_t src_bytes, size_t *raw_bytes);
 int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const ftx_copy_policy *policy,
                            void *stream);
+/* The same decode from an encoded block kept in device memory (src_bytes
+ * bytes, 16-byte aligned) into dst (raw_bytes). The header stays on the
+ * device: the caller states the raw size, and the kernel reads the table and
+ * escape count when it runs (a block of another raw size writes nothing).
+ * grid 0 runs one workgroup per CU. Serves units kept encoded in HBM
+ * (OffloadConfig.encode_resident_blocks). */
+int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid, void *stream);
 
 /* ---- staged copies from pageable host memory ------------------------------
  * Replace the reference's copy from pageable or shared-memory blocks that are
