@@ -228,7 +228,7 @@ def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
 
 def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
                   include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4,
-                  ring_order: str = "auto", encode: bool = False) -> dict:
+                  ring_order: str = "auto", encode: bool = False, encode_resident: bool = False) -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
     streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
     units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
@@ -236,7 +236,8 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     tokens, ``ring_tokens`` more decode tokens time every ring copy on its own (:func:`ring_copy_stats`).
     ``ring_order`` "reference" or "link-bound" overrides how the ring's copies are waited for
     (:func:`_set_ring_order`). ``encode`` streams the blocks exponent-coded
-    (``OffloadConfig.encode_streamed_blocks``)."""
+    (``OffloadConfig.encode_streamed_blocks``); ``encode_resident`` keeps resident layers exponent-coded
+    in HBM when they do not fit raw (``OffloadConfig.encode_resident_blocks``), so fewer layers stream."""
     import torch
 
     from flextensor_amd import hip
@@ -251,7 +252,7 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     mgr = OffloadManager("bench-llama")
     cfg = OffloadConfig(include_patterns=list(include_patterns), num_blocks=2, min_blocks=2, discovery_iters=1,
                         profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9), copy_engine=copy_engine,
-                        encode_streamed_blocks=encode)
+                        encode_streamed_blocks=encode, encode_resident_blocks=encode_resident)
     mgr.offload(model, cfg)
     prompt = W.prompt_tokens(1, prefill, W.LLAMA_7B.vocab, seed=0).to(dev)
     total = prefill + warmup + steps + ring_tokens + 2
@@ -264,8 +265,10 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     plan = mgr.plan
     streamed_bytes = sum(mgr._unit(x).nbytes for x in plan.streamed)
     ctl = mgr.controller
-    link_bytes = sum(ctl.link_bytes(x) for x in ctl.block_map_cpu) if ctl is not None else 0
+    hbm = getattr(ctl, "hbm_encoded", {}) or {}
+    link_bytes = sum(ctl.link_bytes(x) for x in ctl.block_map_cpu if x not in hbm) if ctl is not None else 0
     encoded = len(getattr(ctl, "encoded", {}) or {})
+    hbm_bytes = sum(b.capacity for b in hbm.values())
     with torch.no_grad():
         model.init_cache(1, total, dev)
         W.generate(model, prompt, 2)  # warm-up pass
@@ -312,6 +315,9 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
         "link_bytes_per_token": link_bytes,
         "decode_link_GBps": link_bytes * steps / t_decode / 1e9,
         "encoded_blocks": encoded,
+        "hbm_encoded_layers": len(hbm),
+        "hbm_encoded_bytes": hbm_bytes,
+        "hbm_encoded_ratio": round(hbm_bytes / sum(b.raw_bytes for b in hbm.values()), 4) if hbm else None,
         "streamed_layers": len(plan.streamed),
         "resident_layers": len(plan.resident),
         "gpu_weight_bytes": usage.total_bytes,
@@ -409,6 +415,8 @@ def _encoded_summary(enc: dict, measured_peak: float, raw_tok_s: float | None) -
     the link, the effective weight rate and the link's own rate."""
     return {
         "encoded_blocks": enc["encoded_blocks"], "streamed_layers": enc["streamed_layers"],
+        "resident_layers": enc["resident_layers"], "hbm_encoded_layers": enc["hbm_encoded_layers"],
+        "hbm_encoded_ratio": enc["hbm_encoded_ratio"], "gpu_weight_bytes": enc["gpu_weight_bytes"],
         "streamed_bytes_per_token": enc["streamed_bytes_per_token"],
         "link_bytes_per_token": enc["link_bytes_per_token"],
         "link_bytes_ratio": round(enc["link_bytes_per_token"] / enc["streamed_bytes_per_token"], 4),
@@ -1634,6 +1642,8 @@ def main() -> int:
                     help="print the encoded-block decode of one 7B layer at several grids against raw copies")
     ap.add_argument("--encoded-finer-units", action="store_true",
                     help="with --encoded-only: each layer's attention and MLP projections as separate units")
+    ap.add_argument("--encoded-resident", action="store_true",
+                    help="with --encoded-only: also keep resident layers exponent-coded in HBM")
     ap.add_argument("--skip-encoded", action="store_true",
                     help="skip the 7B decode with exponent-coded blocks (OffloadConfig.encode_streamed_blocks)")
     ap.add_argument("--skip-70b", action="store_true", help="skip the 80-layer fp8 70B-shape batch-8 decode")
@@ -1692,11 +1702,13 @@ def main() -> int:
         peak = measure_link_peak()
         units = FINER_UNITS if args.encoded_finer_units else ("layers.*",)
         enc = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
-                            include_patterns=units, ring_order=args.ring_order, encode=True)
+                            include_patterns=units, ring_order=args.ring_order, encode=True,
+                            encode_resident=args.encoded_resident)
         enc.pop("_check")
         res = _encoded_summary(enc, max(peak["sdma"], peak["kernel"]), None)
         res["include_patterns"] = list(units)
-        print(json.dumps({"llama7b_encoded_blocks": res, "measured_peak": peak}), flush=True)
+        key = "llama7b_encoded_resident" if args.encoded_resident else "llama7b_encoded_blocks"
+        print(json.dumps({key: res, "measured_peak": peak}), flush=True)
         return 0
     if args.mlp_only:
         res = {"mlp8": bench_mlp(20, args.copy_engine, ring_order=args.ring_order)}
@@ -1816,6 +1828,25 @@ def main() -> int:
         torch.cuda.empty_cache()
         if not same:
             print("bench: the decode with encoded blocks differs from the decode with raw blocks", file=sys.stderr)
+            return 1
+        # resident units also kept exponent-coded in HBM: more fit the budget, fewer stream. Attention and
+        # MLP projections as separate units: smaller ring and decode slots leave more room for them.
+        enc = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
+                            include_patterns=FINER_UNITS, ring_order=args.ring_order, encode=True,
+                            encode_resident=True)
+        enc_check = enc.pop("_check")
+        same = (torch.equal(enc_check["last_logits"], check["last_logits"])
+                and torch.equal(enc_check["tokens"], check["tokens"]))
+        line["llama7b_encoded_resident"] = _encoded_summary(enc, measured_peak, llama["decode_tok_s"])
+        line["llama7b_encoded_resident"]["prefill_logits_and_tokens_bitwise_equal_to_raw_blocks"] = same
+        line["llama7b_encoded_resident"]["include_patterns"] = list(FINER_UNITS)
+        _log(f"llama7b encoded resident: {line['llama7b_encoded_resident']}")
+        del enc, enc_check
+        gc.collect()
+        torch.cuda.empty_cache()
+        if not same:
+            print("bench: the decode with layers encoded in HBM differs from the decode with raw blocks",
+                  file=sys.stderr)
             return 1
 
     # ---- the scatter microbenchmark and the scatter kernel's HBM roofline

@@ -226,6 +226,9 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
     bytes of its encoded block and the bytes of its packed raw block) a
     resident set that does not fit raw may keep some units encoded in HBM
     (:func:`encode_residents`), so fewer units stream for the same budget.
+    Such a plan is chosen for the fewest streamed bytes, not the fewest
+    streamed units: of unequal units the fewest may not be the smallest
+    (counts up to twice the first that fits are compared).
     """
     by_label = {u.label: u for u in units}
     labels = list(order)
@@ -237,14 +240,14 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
     stats = [by_label[x].stats() for x in labels]
     hi = max(num_blocks, 2)
     lo = max(2, min(hi, min_blocks if min_blocks is not None else hi))
-    for k in range(1, n + 1):
+    def attempt(k: int) -> StreamPlan | None:
         centred = sorted({min(n - 1, int((i + 0.5) * n / k)) for i in range(k)})
         pick = [i - centred[0] for i in centred]
         if len(pick) < k:
-            continue
+            return None
         streamed = [labels[i] for i in pick]
         if budget is None and k < n:
-            continue
+            return None
         # i == 0 wraps to the last label: a cyclic preload
         strategy = {labels[i - 1]: list(stats[i].tensors) for i in pick}
         resident = [x for x in labels if x not in streamed]
@@ -272,7 +275,7 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
         if not hazard_free:
             raise RuntimeError("no hazard-free slot plan found")
         if chosen is None:
-            continue
+            return None
         bd, gpu, enc = chosen
         reordered = bool(resident)
         if reordered:
@@ -286,6 +289,23 @@ def plan_streaming(units: Sequence[_Unit], order: Sequence[str], budget: int | N
                 transfer_to_compute_map=t2c,
             )
         return StreamPlan(streamed, resident, bd, strategy, reordered, budget, gpu, enc)
+
+    def streamed_bytes(p: StreamPlan) -> int:
+        return sum(by_label[x].nbytes for x in p.streamed)
+
+    for k in range(1, n + 1):
+        plan = attempt(k)
+        if plan is None:
+            continue
+        if not encodable or budget is None:
+            return plan
+        # Units kept encoded make room by bytes, not by count: among the counts up to twice the first
+        # that fits, the plan that streams the fewest bytes (ties: fewer units).
+        for more in range(k + 1, min(n, 2 * k) + 1):
+            other = attempt(more)
+            if other is not None and streamed_bytes(other) < streamed_bytes(plan):
+                plan = other
+        return plan
     # Even streaming every unit does not fit: the tensors placed outside the
     # units leave too little for the ring (gpu_budget.py:200-225).
     raise RuntimeError(

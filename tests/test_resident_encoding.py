@@ -105,3 +105,31 @@ def test_config_rules():
         OffloadConfig(encode_resident_blocks=True, transfer_mode="raw_block_transfer")
     with pytest.raises(ValueError, match="encode_resident_blocks"):
         OffloadConfig(encode_resident_blocks=True, shm_enabled=True, shm_namespace="x")
+
+
+def test_encoded_plan_streams_the_fewest_bytes_of_unequal_units():
+    """Attention units of 1342 bytes and MLP projections of 902 (the 7B-shape decoder's finer units,
+    scaled down 10^5): the fewest streamed units that fit (32, every attention unit) are not the fewest
+    streamed bytes (36 units, more of them small)."""
+    sizes = [1342, 902, 902, 902] * 32
+    units = _mk(sizes)
+    order = [u.label for u in units]
+    encodable = {u.label: (int(u.nbytes * 0.7523) + u.nbytes // 1024, u.nbytes) for u in units}
+    budget, base = 80_000, 5_243
+    plan = plan_streaming(units, order, budget, base, 2, 2, encodable)
+    by = {u.label: u.nbytes for u in units}
+    got = sum(by[x] for x in plan.streamed)
+    assert plan.planned_gpu_bytes <= budget
+    # every count from 1 up: the first that fits streams more bytes than the plan chosen
+    first = None
+    for k in range(1, len(units) + 1):
+        centred = sorted({min(len(units) - 1, int((i + 0.5) * len(units) / k)) for i in range(k)})
+        picked = [order[i - centred[0]] for i in centred]
+        resident = [x for x in order if x not in picked]
+        if encode_residents(resident, by, encodable, budget - base - 2 * 1342) is not None:
+            first = sum(by[x] for x in picked)
+            break
+    assert first is not None and got < first
+    assert len(plan.streamed) > 32
+    raw = plan_streaming(units, order, budget, base, 2, 2)  # without encoding: the reference's fewest units
+    assert not raw.encoded_resident
