@@ -358,10 +358,12 @@ def _ring_roofline(run: dict, measured_peak: float) -> dict | None:
     return out
 
 
-def expcode_sweep(grids=(8, 16, 32, 64, 128), reps: int = 6) -> dict:
+def expcode_sweep(grids=(8, 16, 32, 64, 128), reps: int = 6, hbm_grids=(0, 256, 512, 1024, 2048, 4096)) -> dict:
     """One 7B layer's block (404,766,720 bytes of N(0, 0.02) bf16) encoded, then decoded into the device by
-    ``expcode_decode_kernel`` at each grid, against the raw block's zero-copy copy and SDMA copy. Best of
-    ``reps`` HIP-event timings per case; every decode is checked bit for bit."""
+    ``expcode_decode_kernel`` at each grid, against the raw block's zero-copy copy and SDMA copy; then the
+    same decode from a device-memory copy of the encoded block at ``hbm_grids`` (0: the library's eight per CU)
+    against a device-to-device copy of the raw block. Best of ``reps`` HIP-event timings per case; every
+    decode is checked bit for bit."""
     import torch
 
     from flextensor_amd import _native as nat
@@ -407,6 +409,19 @@ def expcode_sweep(grids=(8, 16, 32, 64, 128), reps: int = 6) -> dict:
     out["zero_copy_raw_8_workgroups"] = {"ms": round(ms, 3), "GBps": round(n / ms / 1e6, 2)}
     ms = best(lambda: copy_h2d(dst, raw, nat.COPY_SDMA))
     out["sdma_raw"] = {"ms": round(ms, 3), "GBps": round(n / ms / 1e6, 2)}
+    # The same block kept in device memory (a unit resident in HBM in encoded form): the decode reads
+    # the encoded bytes and writes the raw ones, both in HBM. Grid 0 is the library's default.
+    src = block.tensor.to("cuda")
+    moved = block.nbytes + n
+    out["decode_from_hbm"] = {}
+    for grid in hbm_grids:
+        dst.zero_()
+        ms = best(lambda: expcode.decode_d2d(dst, src, n, grid=grid))
+        out["decode_from_hbm"][str(grid)] = {"us": round(1e3 * ms, 1), "hbm_GBps": round(moved / ms / 1e6, 1),
+                                             "frac_of_8TBps": round(moved / ms / 1e6 / 8000, 4),
+                                             "bit_exact": bool(torch.equal(dst, ref))}
+    ms = best(lambda: dst.copy_(ref))
+    out["device_copy_raw"] = {"us": round(1e3 * ms, 1), "hbm_GBps": round(2 * n / ms / 1e6, 1)}
     return out
 
 
@@ -427,6 +442,8 @@ def _encoded_summary(enc: dict, measured_peak: float, raw_tok_s: float | None) -
         "speedup_vs_raw_blocks": None if raw_tok_s is None else round(enc["decode_tok_s"] / raw_tok_s, 4),
         "prefill_tok_s": round(enc["prefill_tok_s"], 1),
         "ring_order": enc["ring_order"],
+        "regime": None if enc["copy_policy"] is None else {k: enc["copy_policy"][k] for k in
+                                                           ("link_bound", "pass_compute_ms", "pass_transfer_ms")},
         "ring_copies": _ring_roofline(enc, measured_peak),
     }
 

@@ -793,7 +793,9 @@ int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t 
   ftx::DeviceState *st = nullptr;
   rc = ftx::device_state(&st);
   if (rc != FTX_OK) return rc;
-  const int g = grid > 0 ? grid : st->cu_count;  // HBM to HBM: one workgroup per CU by default
+  // HBM to HBM: eight workgroups per CU by default (a 7B-shape layer decodes at 5.4 TB/s of encoded plus raw
+  // bytes, the rate of a device-to-device copy; one per CU reaches 4.6 TB/s)
+  const int g = grid > 0 ? grid : 8 * st->cu_count;
   const size_t reserve = g <= ftx::kZeroCopyReserveMaxGrid ? st->copy_reserve_lds : 0;
   FTX_HIP(ftx::launch_expcode_decode(dst, src, src_bytes, raw_bytes, g, reserve, static_cast<hipStream_t>(stream)));
   return FTX_OK;

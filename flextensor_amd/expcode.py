@@ -191,14 +191,14 @@ class DeviceEncodedBlock:
         self.nbytes = host.numel()
 
     def decode(self, dst: torch.Tensor, stream: HipStream | None = None) -> None:
-        """Stream-ordered decode into the first ``raw_bytes`` bytes of ``dst`` (one workgroup per CU)."""
+        """Stream-ordered decode into the first ``raw_bytes`` bytes of ``dst`` (eight workgroups per CU)."""
         decode_d2d(dst, self.dev, self.raw_bytes, stream)
 
 
 def decode_d2d(dst: torch.Tensor, encoded: torch.Tensor, raw_bytes: int, stream: HipStream | None = None,
                grid: int = 0) -> None:
     """Stream-ordered decode of an encoded block held in device memory (``encoded``, a uint8 device tensor)
-    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs one workgroup per CU."""
+    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs eight workgroups per CU."""
     if dst.device.type != "cuda" or encoded.device.type != "cuda":
         raise ValueError("decode_d2d needs device tensors")
     if raw_bytes > dst.numel() * dst.element_size():

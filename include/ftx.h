@@ -210,7 +210,7 @@ int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const f
  * bytes, 16-byte aligned) into dst (raw_bytes). The header stays on the
  * device: the caller states the raw size, and the kernel reads the table and
  * escape count when it runs (a block of another raw size writes nothing).
- * grid 0 runs one workgroup per CU. Serves units kept encoded in HBM
+ * grid 0 runs eight workgroups per CU. Serves units kept encoded in HBM
  * (OffloadConfig.encode_resident_blocks). */
 int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid, void *stream);
 
