@@ -228,7 +228,8 @@ def ring_copy_stats(mgr, step, tokens: int) -> dict | None:
 
 def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_engine: str,
                   include_patterns: tuple[str, ...] = ("layers.*",), ring_tokens: int = 4,
-                  ring_order: str = "auto", encode: bool = False, encode_resident: bool = False) -> dict:
+                  ring_order: str = "auto", encode: bool = False, encode_resident: bool = False,
+                  link_benchmark: bool = True) -> dict:
     """Prefill, then ``warmup`` untimed and ``steps`` timed greedy decode tokens of the 7B-shape decoder
     streaming under ``budget_gb`` (a step is one decode token). ``include_patterns`` choose the offload
     units: whole decoder layers by default. The prefill's last-position logits and every decoded token are
@@ -237,7 +238,11 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     ``ring_order`` "reference" or "link-bound" overrides how the ring's copies are waited for
     (:func:`_set_ring_order`). ``encode`` streams the blocks exponent-coded
     (``OffloadConfig.encode_streamed_blocks``); ``encode_resident`` keeps resident layers exponent-coded
-    in HBM when they do not fit raw (``OffloadConfig.encode_resident_blocks``), so fewer layers stream."""
+    in HBM when they do not fit raw (``OffloadConfig.encode_resident_blocks``), so fewer layers stream.
+    ``link_benchmark`` False skips the host-link measurement (``OffloadConfig.link_benchmark``): no pass
+    regime is measured, so every streamed block that shrinks is encoded. Under a kernel tracer the
+    profiled compute of the pass is inflated and the measured regime would differ from an untraced run;
+    with ``ring_order="link-bound"`` this reproduces the untraced link-bound configuration."""
     import torch
 
     from flextensor_amd import hip
@@ -252,7 +257,8 @@ def bench_llama7b(budget_gb: float, prefill: int, steps: int, warmup: int, copy_
     mgr = OffloadManager("bench-llama")
     cfg = OffloadConfig(include_patterns=list(include_patterns), num_blocks=2, min_blocks=2, discovery_iters=1,
                         profiling_iters=1, max_gpu_mem_bytes=int(budget_gb * 1e9), copy_engine=copy_engine,
-                        encode_streamed_blocks=encode, encode_resident_blocks=encode_resident)
+                        encode_streamed_blocks=encode, encode_resident_blocks=encode_resident,
+                        link_benchmark=link_benchmark)
     mgr.offload(model, cfg)
     prompt = W.prompt_tokens(1, prefill, W.LLAMA_7B.vocab, seed=0).to(dev)
     total = prefill + warmup + steps + ring_tokens + 2
@@ -1659,6 +1665,9 @@ def main() -> int:
                     help="print the encoded-block decode of one 7B layer at several grids against raw copies")
     ap.add_argument("--encoded-finer-units", action="store_true",
                     help="with --encoded-only: each layer's attention and MLP projections as separate units")
+    ap.add_argument("--no-link-benchmark", action="store_true",
+                    help="with --encoded-only: skip the host-link measurement, so the pass regime is not measured "
+                         "(for kernel traces, which inflate the profiled compute); pair with --ring-order link-bound")
     ap.add_argument("--encoded-resident", action="store_true",
                     help="with --encoded-only: also keep resident layers exponent-coded in HBM")
     ap.add_argument("--skip-encoded", action="store_true",
@@ -1720,7 +1729,7 @@ def main() -> int:
         units = FINER_UNITS if args.encoded_finer_units else ("layers.*",)
         enc = bench_llama7b(args.budget_gb, args.prefill, args.steps, args.warmup, args.copy_engine,
                             include_patterns=units, ring_order=args.ring_order, encode=True,
-                            encode_resident=args.encoded_resident)
+                            encode_resident=args.encoded_resident, link_benchmark=not args.no_link_benchmark)
         enc.pop("_check")
         res = _encoded_summary(enc, max(peak["sdma"], peak["kernel"]), None)
         res["include_patterns"] = list(units)
