@@ -258,6 +258,20 @@ def is_link_bound(compute_ms: float, transfer_ms: float, share: float = LINK_BOU
     return transfer_ms > 0.0 and compute_ms < share * transfer_ms
 
 
+# Exponent-coded transfers take about a quarter of the bytes off the link, and their decode holds 16 CUs while
+# a transfer runs. While a pass's profiled compute stays under this share of its raw transfer time, the link
+# still bounds the pass, or nearly, and fewer bytes shorten it; at or above it the transfers were hidden, and
+# the held CUs would slow the compute.
+ENCODE_COMPUTE_SHARE = 0.9
+
+
+def encoding_pays(compute_ms: float, transfer_ms: float, share: float = ENCODE_COMPUTE_SHARE) -> bool:
+    """Whether exponent-coded transfers shorten a pass that computes for ``compute_ms`` and streams raw
+    blocks for ``transfer_ms``. A wider rule than :func:`is_link_bound`: between the two shares the ring
+    keeps SDMA and the reference's waits, and its transfers are still encoded."""
+    return transfer_ms > 0.0 and compute_ms < share * transfer_ms
+
+
 def benchmark_memory_transfers(max_label_bytes: int, device=None, max_depth: int = 4,
                                max_size_bytes: int = 4 * 1024**3, engine: str = "sdma") -> dict[int, float]:
     """Median ms per size for sizes ``base / 2**d``, d < max_depth (pinned source).

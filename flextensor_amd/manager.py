@@ -57,8 +57,8 @@ from .allocation_block import HostPinner
 from .config import OffloadConfig
 from .controllers import AllocationBlockController, RawBlockController
 from .layout import overlapping_views
-from .link_model import (LinkMeasurement, MemoryTransferInterpolator, format_memory_transfer_table, is_link_bound,
-                         link_probe_sizes, measure_link)
+from .link_model import (LinkMeasurement, MemoryTransferInterpolator, encoding_pays, format_memory_transfer_table,
+                         is_link_bound, link_probe_sizes, measure_link)
 from .loaders import PreallocatedBatchTransferTensorLoader, PreallocatedBatchTransferTensorLoaderReordered
 from .planner import (
     BlockStrategyData,
@@ -1832,9 +1832,12 @@ class OffloadManager:
         LOGGER.info("offload %r: %s", self.name, link.describe())
 
     def _measured_compute_bound(self) -> bool:
-        """The link measurement profiled this pass and found it compute-bound (the pass rule)."""
+        """The link measurement profiled this pass and found its compute too long for encoded transfers
+        to pay: 0.9 of its raw transfer time or more (:func:`~flextensor_amd.link_model.encoding_pays`)."""
         link = self.link
-        return link is not None and link.pass_compute_ms is not None and not link.link_bound
+        if link is None or link.pass_compute_ms is None or link.pass_transfer_ms is None:
+            return False
+        return not encoding_pays(link.pass_compute_ms, link.pass_transfer_ms)
 
     def _apply_link_bound_order(self) -> None:
         """A link-bound pass orders its ring waits for the link; any other pass keeps the reference's order.
@@ -1852,7 +1855,7 @@ class OffloadManager:
         if hasattr(self.loader, "link_bound"):
             self.loader.link_bound = bool(self.link is not None and self.link.link_bound)
         # Encoded blocks (encode_streamed_blocks) carry fewer bytes, and their decode holds 16 CUs while it
-        # runs: worth it while the link bounds the pass, not once the pass is measured compute-bound.
+        # runs: worth it until the pass's compute reaches 0.9 of its raw transfer time.
         if getattr(self.controller, "encoded", None):
             self.controller.use_encoded = not self._measured_compute_bound()
 

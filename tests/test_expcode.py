@@ -167,3 +167,24 @@ def test_config_needs_the_allocation_block_controller():
     assert OffloadConfig(encode_streamed_blocks=True).encode_streamed_blocks
     with pytest.raises(ValueError, match="encode_streamed_blocks"):
         OffloadConfig(encode_streamed_blocks=True, transfer_mode="raw_block_transfer")
+
+
+def test_encoding_follows_its_own_pass_rule():
+    """Encoded transfers stay on while the profiled compute is under 0.9 of the raw transfer time, also
+    where the ring already keeps SDMA (compute at 0.4 of the transfers or more); at 0.9 and above they are
+    off. No link measurement, or none that profiled the pass, keeps them on."""
+    import types
+
+    from flextensor_amd.link_model import ENCODE_COMPUTE_SHARE, encoding_pays, is_link_bound
+    from flextensor_amd.manager import OffloadManager
+
+    assert ENCODE_COMPUTE_SHARE == 0.9
+    assert encoding_pays(35.0, 113.0) and is_link_bound(35.0, 113.0)
+    assert encoding_pays(68.0, 84.7) and not is_link_bound(68.0, 84.7)  # between the two rules
+    assert not encoding_pays(90.0, 100.0) and not encoding_pays(1.0, 0.0)
+    mgr = OffloadManager(name="encode-rule")
+    for link, off in ((None, False), (types.SimpleNamespace(pass_compute_ms=None, pass_transfer_ms=None), False),
+                      (types.SimpleNamespace(pass_compute_ms=68.0, pass_transfer_ms=84.7), False),
+                      (types.SimpleNamespace(pass_compute_ms=95.0, pass_transfer_ms=100.0), True)):
+        mgr.link = link
+        assert mgr._measured_compute_bound() == off
