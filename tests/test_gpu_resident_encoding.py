@@ -5,7 +5,8 @@ against the oracle's encoding, for every size class and escape-heavy data, at th
 workgroup per CU) and at a small one; it refuses short or misaligned blocks and writes nothing for a
 block of another raw size. A captured decode follows an in-place re-encode. Offloaded models whose
 residents do not fit the budget raw keep some encoded, stream fewer units, and stay bitwise equal to
-the resident model: eager, in captured graphs, through generation, after ``load_state_dict`` and
+the resident model: eager, in captured graphs, compiled, restored from a saved profile, through
+generation, after ``load_state_dict`` and
 beside encoded streamed blocks; ``release()`` hands the original weights back.
 """
 
@@ -259,3 +260,65 @@ def test_a_load_that_outgrows_the_reservation_fails_loudly(gpu):
             model(x)
     finally:
         mgr.release()
+
+
+def test_compiled_forward_decodes_inside_the_traps(gpu):
+    """torch.compile (aot_eager: no code generation) keeps the traps as custom ops; the decode of each unit
+    kept in HBM runs inside its trap, and the compiled forward is bitwise the resident one."""
+    torch._dynamo.reset()
+    model = W.build_mlp_stack(16, 512, 1408, seed=59)
+    resident = copy.deepcopy(model).to(gpu)
+    budget = _outside_bytes(model) + 14 * _layer_bytes(model)
+    mgr = _offload(model, "hbm-compile", budget)
+    x = W.mlp_input(8, 512, seed=59).to(gpu)
+    try:
+        with torch.no_grad():
+            for _ in range(3):
+                model(x)
+            assert mgr.phase == OffloadPhase.INFERENCE and mgr.plan.encoded_resident
+            compiled = torch.compile(model, backend="aot_eager", fullgraph=True)
+            want = resident(resident(x))
+            for _ in range(3):
+                assert torch.equal(compiled(compiled(x)), want)
+        torch.cuda.synchronize()
+    finally:
+        torch._dynamo.reset()
+        mgr.release()
+
+
+def test_a_saved_profile_restores_the_units_kept_in_hbm(gpu, tmp_path):
+    """A plan saved from a manager that kept units encoded in HBM, restored into a fresh model with the
+    option on: the same units stream and the same units are kept encoded, with no discovery or profiling
+    pass, and the outputs are bitwise the resident model's."""
+    from flextensor_amd.manager import get_offload_manager, offload_from_profile, release
+
+    model = W.build_mlp_stack(16, 512, 1408, seed=61)
+    x = W.mlp_input(8, 512, seed=61).to(gpu)
+    with torch.no_grad():
+        want = copy.deepcopy(model).to(gpu)(x)
+    budget = _outside_bytes(model) + 14 * _layer_bytes(model)
+    mgr = _offload(model, "hbm-profile-src", budget, profile_storage_dir=str(tmp_path))
+    with torch.no_grad():
+        for _ in range(3):
+            assert torch.equal(model(x), want)
+    src = mgr.plan
+    assert src.encoded_resident
+    mgr.save_profile()
+    mgr.release()
+
+    twin = W.build_mlp_stack(16, 512, 1408, seed=61)
+    cfg = OffloadConfig(include_patterns=["layers.*"], num_blocks=2, min_blocks=2, discovery_iters=1,
+                        profiling_iters=1, encode_resident_blocks=True, link_benchmark=False,
+                        max_gpu_mem_bytes=budget, profile_storage_dir=str(tmp_path))
+    offload_from_profile(twin, None, cfg, name="hbm-profile-dst")
+    dst = get_offload_manager("hbm-profile-dst")
+    try:
+        assert dst.phase == OffloadPhase.INFERENCE
+        assert dst.plan.streamed == src.streamed and dst.plan.encoded_resident == src.encoded_resident
+        with torch.no_grad():
+            for _ in range(3):
+                assert torch.equal(twin(x), want)
+    finally:
+        release("hbm-profile-dst")
+    for p, q in zip(twin.parameters(), W.build_mlp_stack(16, 512, 1408, seed=61).parameters()):
+        assert p.device.type == "cpu" and torch.equal(p, q)
