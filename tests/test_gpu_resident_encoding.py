@@ -1,13 +1,13 @@
 """Units kept exponent-coded in HBM (``OffloadConfig(encode_resident_blocks=True)``) on the GPU.
 
 The device-side decode (``ftx_expcode_decode_d2d``) rebuilds blocks from device memory bit for bit
-against the oracle's encoding, for every size class and escape-heavy data, at the default grid (one
-workgroup per CU) and at a small one; it refuses short or misaligned blocks and writes nothing for a
+against the oracle's encoding, for every size class and escape-heavy data, at the default grid (eight
+workgroups per CU) and at a small one; it refuses short or misaligned blocks and writes nothing for a
 block of another raw size. A captured decode follows an in-place re-encode. Offloaded models whose
 residents do not fit the budget raw keep some encoded, stream fewer units, and stay bitwise equal to
 the resident model: eager, in captured graphs, compiled, restored from a saved profile, through
-generation, after ``load_state_dict`` and
-beside encoded streamed blocks; ``release()`` hands the original weights back.
+generation, after ``load_state_dict`` and beside encoded streamed blocks; ``release()`` hands the
+original weights back.
 """
 
 from __future__ import annotations
