@@ -428,6 +428,19 @@ def expcode_sweep(grids=(8, 16, 32, 64, 128), reps: int = 6, hbm_grids=(0, 256, 
                                              "bit_exact": bool(torch.equal(dst, ref))}
     ms = best(lambda: dst.copy_(ref))
     out["device_copy_raw"] = {"us": round(1e3 * ms, 1), "hbm_GBps": round(2 * n / ms / 1e6, 1)}
+    # The dense format (version 2) that units kept in HBM use
+    t0 = time.perf_counter()
+    dense = expcode.DeviceEncodedBlock.from_raw(raw, expcode.encoded_size(raw, dense=True), "cuda", dense=True)
+    dense_s = time.perf_counter() - t0
+    moved = dense.nbytes + n
+    out["dense"] = {"encoded_bytes": dense.nbytes, "ratio": round(dense.ratio, 4),
+                    "encode_and_upload_s": round(dense_s, 3), "decode_from_hbm": {}}
+    for grid in hbm_grids:
+        dst.zero_()
+        ms = best(lambda: expcode.decode_d2d(dst, dense.dev, n, grid=grid, dense=True))
+        out["dense"]["decode_from_hbm"][str(grid)] = {
+            "us": round(1e3 * ms, 1), "hbm_GBps": round(moved / ms / 1e6, 1),
+            "frac_of_8TBps": round(moved / ms / 1e6 / 8000, 4), "bit_exact": bool(torch.equal(dst, ref))}
     return out
 
 

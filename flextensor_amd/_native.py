@@ -158,6 +158,8 @@ _SIGNATURES: dict[str, list] = {
     "ftx_expcode_raw_bytes": [_vp, _sz, ctypes.POINTER(_sz)],
     "ftx_expcode_decode_h2d": [_vp, _vp, _sz, ctypes.POINTER(CopyPolicy), _vp],
     "ftx_expcode_decode_d2d": [_vp, _vp, _sz, _sz, ctypes.c_int, _vp],
+    "ftx_expcode_encode_dense": [_vp, _sz, _vp, _sz, ctypes.POINTER(_sz)],
+    "ftx_expcode_decode_dense_d2d": [_vp, _vp, _sz, _sz, ctypes.c_int, _vp],
     "ftx_fp8_linear_fused": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _vp,
                              _vp, _sz, _vp],
 }

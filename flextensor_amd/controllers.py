@@ -195,7 +195,8 @@ class AllocationBlockController:
         launch that writes the raw block into its slot (no reference counterpart).
         ``hbm_encoded`` maps block keys of units kept resident in encoded form to the device bytes
         reserved for each encoded block: their slot group is packed into pageable host blocks (nothing
-        crosses the link), each block is encoded into device memory, and :meth:`decode_resident`
+        crosses the link), each block is encoded into device memory in the dense format (version 2, decoded
+        only from device memory), and :meth:`decode_resident`
         rebuilds it in its slot on the current stream (no reference counterpart)."""
         if load_from_shm and not shm_block_name_map:
             raise ValueError("load_from_shm needs shm_block_name_map")
@@ -257,7 +258,7 @@ class AllocationBlockController:
 
                 for key, cap in self.hbm_capacity.items():
                     self.hbm_encoded[key] = expcode.DeviceEncodedBlock.from_raw(self.block_map_cpu[key].block, cap,
-                                                                                self.device_gpu)
+                                                                                self.device_gpu, dense=True)
             if encode_blocks:
                 from . import expcode
 

@@ -96,6 +96,25 @@ struct ExpPlan {
   uint8_t code_of[256];
 };
 
+// Exponent histogram of the first n_words words of raw (threaded above a million words), and the exponents
+// that occur, most frequent first, ties to the smaller exponent.
+void exponent_ranks(const uint8_t *raw, uint64_t n_words, uint64_t hist[256], std::vector<int> *ranked) {
+  const int threads = encode_threads(n_words);
+  std::vector<uint64_t> hists(static_cast<size_t>(std::max(threads, 1)) * 256, 0);
+  const uint64_t chunk = (n_words + threads - 1) / std::max(threads, 1);
+  parallel_for(n_words, threads, [&](uint64_t b, uint64_t e) {
+    uint64_t *h = hists.data() + (chunk ? b / chunk : 0) * 256;
+    for (uint64_t w = b; w < e; ++w) ++h[(word_at(raw, w) >> 7) & 0xff];
+  });
+  for (int x = 0; x < 256; ++x) hist[x] = 0;
+  for (int t = 0; t < threads; ++t)
+    for (int x = 0; x < 256; ++x) hist[x] += hists[static_cast<size_t>(t) * 256 + x];
+  ranked->clear();
+  for (int x = 0; x < 256; ++x)
+    if (hist[x]) ranked->push_back(x);
+  std::stable_sort(ranked->begin(), ranked->end(), [&](int a, int b) { return hist[a] > hist[b]; });
+}
+
 int plan(const uint8_t *raw, uint64_t n, ExpPlan *p) {
   ExpcodeInfo &info = p->info;
   info = ExpcodeInfo{};
@@ -103,20 +122,9 @@ int plan(const uint8_t *raw, uint64_t n, ExpPlan *p) {
   info.n_words = n / 2;
   info.groups = (info.n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
   if (info.groups >= (uint64_t(1) << 32)) return fail(FTX_ERR_INVALID, "block too large to encode");
-  const int threads = encode_threads(info.n_words);
-  std::vector<uint64_t> hists(static_cast<size_t>(std::max(threads, 1)) * 256, 0);
-  const uint64_t chunk = (info.n_words + threads - 1) / std::max(threads, 1);
-  parallel_for(info.n_words, threads, [&](uint64_t b, uint64_t e) {
-    uint64_t *h = hists.data() + (chunk ? b / chunk : 0) * 256;
-    for (uint64_t w = b; w < e; ++w) ++h[(word_at(raw, w) >> 7) & 0xff];
-  });
-  uint64_t hist[256] = {};
-  for (int t = 0; t < threads; ++t)
-    for (int x = 0; x < 256; ++x) hist[x] += hists[static_cast<size_t>(t) * 256 + x];
+  uint64_t hist[256];
   std::vector<int> ranked;
-  for (int x = 0; x < 256; ++x)
-    if (hist[x]) ranked.push_back(x);
-  std::stable_sort(ranked.begin(), ranked.end(), [&](int a, int b) { return hist[a] > hist[b]; });
+  exponent_ranks(raw, info.n_words, hist, &ranked);
   std::memset(p->code_of, kExpEscape, sizeof(p->code_of));
   uint64_t covered = 0;
   for (size_t c = 0; c < ranked.size() && c < kExpEscape; ++c) {
@@ -216,6 +224,171 @@ int expcode_encode(const void *raw_v, size_t nbytes, void *out_v, size_t out_cap
         const uint32_t x = static_cast<uint32_t>(j << 8) | e;
         std::memcpy(X + 4 * k, &x, 4);
         ++k;
+      }
+    }
+  });
+  return FTX_OK;
+}
+
+namespace {
+
+struct DenseHeader {
+  char magic[4];
+  uint32_t version;
+  uint64_t n;
+  uint64_t n_words;
+  uint64_t groups;
+  uint64_t e1;  // primary escapes
+  uint64_t e2;  // secondary escapes
+  uint8_t t1[8];
+  uint8_t t2[16];
+  uint8_t tail;
+  uint8_t pad[7];
+};
+static_assert(sizeof(DenseHeader) == 80, "dense header layout");
+
+constexpr uint32_t kDenseVersion = 2;
+constexpr uint32_t kPrimaryEscape = 7;
+constexpr uint32_t kSecondaryEscape = 15;
+
+}  // namespace
+
+DenseLayout dense_layout(uint64_t n, uint64_t e1, uint64_t e2) {
+  DenseLayout d{};
+  d.n = n;
+  d.n_words = n / 2;
+  d.groups = (d.n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  d.e1 = e1;
+  d.e2 = e2;
+  const uint64_t s = (4 * (d.groups + 1) + 15) / 16 * 16;
+  d.off_p = kExpcodeHeaderBytes + kExpcodeGroupWords * d.groups;
+  d.off_s1 = d.off_p + kDensePlaneBytes * d.groups;
+  d.off_s2 = d.off_s1 + s;
+  d.off_y = d.off_s2 + s;
+  d.off_x = d.off_y + ((e1 + 1) / 2 + 15) / 16 * 16;
+  d.total = d.off_x + 4 * e2;
+  return d;
+}
+
+int expcode_encode_dense(const void *raw_v, size_t nbytes, void *out_v, size_t out_capacity, size_t *out_bytes) {
+  const auto *raw = static_cast<const uint8_t *>(raw_v);
+  const uint64_t W = nbytes / 2;
+  const uint64_t G = (W + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  if (G >= (uint64_t(1) << 32)) return fail(FTX_ERR_INVALID, "block too large to encode");
+  uint64_t hist[256];
+  std::vector<int> ranked;
+  exponent_ranks(raw, W, hist, &ranked);
+  uint8_t code1[256], code2[256];
+  std::memset(code1, kPrimaryEscape, sizeof(code1));
+  std::memset(code2, kSecondaryEscape, sizeof(code2));
+  DenseHeader h{};
+  std::memcpy(h.magic, "FTXE", 4);
+  h.version = kDenseVersion;
+  uint64_t covered1 = 0, covered2 = 0;
+  for (size_t c = 0; c < ranked.size() && c < kPrimaryEscape + kSecondaryEscape; ++c) {
+    const int e = ranked[c];
+    if (c < kPrimaryEscape) {
+      h.t1[c] = static_cast<uint8_t>(e);
+      code1[e] = static_cast<uint8_t>(c);
+      covered1 += hist[e];
+    } else {
+      h.t2[c - kPrimaryEscape] = static_cast<uint8_t>(e);
+      code2[e] = static_cast<uint8_t>(c - kPrimaryEscape);
+      covered2 += hist[e];
+    }
+  }
+  const uint64_t e1 = W - covered1, e2 = e1 - covered2;
+  if (e1 >= (uint64_t(1) << 32)) return fail(FTX_ERR_INVALID, "block has too many escaped words to encode");
+  const DenseLayout d = dense_layout(nbytes, e1, e2);
+  *out_bytes = static_cast<size_t>(d.total);
+  if (out_v == nullptr) return FTX_OK;
+  if (out_capacity < d.total)
+    return fail(FTX_ERR_INVALID, "output buffer of " + std::to_string(out_capacity) + " bytes is smaller than the " +
+                                     std::to_string(d.total) + " the encoded block needs");
+  auto *out = static_cast<uint8_t *>(out_v);
+  std::memset(out, 0, kExpcodeHeaderBytes);
+  h.n = nbytes;
+  h.n_words = W;
+  h.groups = G;
+  h.e1 = e1;
+  h.e2 = e2;
+  h.tail = nbytes % 2 ? raw[nbytes - 1] : 0;
+  std::memcpy(out, &h, sizeof(h));
+  std::vector<uint32_t> count1(static_cast<size_t>(G), 0), count2(static_cast<size_t>(G), 0);
+  const int threads = encode_threads(W);
+  uint8_t *A = out + kExpcodeHeaderBytes, *P = out + d.off_p;
+  // Plane A and the code bit planes, eight words (one byte of each plane) at a time.
+  parallel_for(G, threads, [&](uint64_t gb, uint64_t ge) {
+    for (uint64_t g = gb; g < ge; ++g) {
+      const uint64_t w0 = g * kExpcodeGroupWords;
+      const uint64_t wn = std::min<uint64_t>(kExpcodeGroupWords, W - w0);
+      uint32_t c1 = 0, c2 = 0;
+      uint8_t *planes = P + g * kDensePlaneBytes;
+      for (uint64_t i = 0; i < kExpcodeGroupWords / 8; ++i) {
+        uint32_t b0 = 0, b1 = 0, b2 = 0;
+        for (uint64_t k = 0; k < 8; ++k) {
+          const uint64_t j = 8 * i + k;
+          uint8_t a = 0;
+          if (j < wn) {
+            const uint32_t word = word_at(raw, w0 + j);
+            const uint32_t e = (word >> 7) & 0xff;
+            const uint32_t c = code1[e];
+            a = static_cast<uint8_t>(((word >> 8) & 0x80) | (word & 0x7f));
+            b0 |= (c & 1) << k;
+            b1 |= ((c >> 1) & 1) << k;
+            b2 |= ((c >> 2) & 1) << k;
+            if (c == kPrimaryEscape) {
+              ++c1;
+              c2 += code2[e] == kSecondaryEscape;
+            }
+          }
+          A[w0 + j] = a;
+        }
+        planes[i] = static_cast<uint8_t>(b0);
+        planes[128 + i] = static_cast<uint8_t>(b1);
+        planes[256 + i] = static_cast<uint8_t>(b2);
+      }
+      count1[static_cast<size_t>(g)] = c1;
+      count2[static_cast<size_t>(g)] = c2;
+    }
+  });
+  std::vector<uint32_t> S1(static_cast<size_t>(G) + 1, 0), S2(static_cast<size_t>(G) + 1, 0);
+  for (uint64_t g = 0; g < G; ++g) {
+    S1[static_cast<size_t>(g) + 1] = S1[static_cast<size_t>(g)] + count1[static_cast<size_t>(g)];
+    S2[static_cast<size_t>(g) + 1] = S2[static_cast<size_t>(g)] + count2[static_cast<size_t>(g)];
+  }
+  if (S1[static_cast<size_t>(G)] != e1 || S2[static_cast<size_t>(G)] != e2)
+    return fail(FTX_ERR_INVALID, "escape count mismatch while encoding");
+  std::memset(out + d.off_s1, 0, static_cast<size_t>(d.off_x - d.off_s1));
+  std::memcpy(out + d.off_s1, S1.data(), S1.size() * sizeof(uint32_t));
+  std::memcpy(out + d.off_s2, S2.data(), S2.size() * sizeof(uint32_t));
+  uint8_t *Y = out + d.off_y, *X = out + d.off_x;
+  // The secondary codes and the list. A byte of Y holds two nibbles; the bytes at the ends of a thread's
+  // range of nibbles may hold a neighbouring range's nibble too, and take their nibble by an atomic or.
+  parallel_for(G, threads, [&](uint64_t gb, uint64_t ge) {
+    const uint64_t lo = S1[static_cast<size_t>(gb)], hi = S1[static_cast<size_t>(ge)];
+    if (lo == hi) return;
+    const uint64_t edge_lo = lo / 2, edge_hi = (hi - 1) / 2;
+    for (uint64_t g = gb; g < ge; ++g) {
+      if (!count1[static_cast<size_t>(g)]) continue;
+      const uint64_t w0 = g * kExpcodeGroupWords;
+      const uint64_t wn = std::min<uint64_t>(kExpcodeGroupWords, W - w0);
+      uint64_t r = S1[static_cast<size_t>(g)], x = S2[static_cast<size_t>(g)];
+      for (uint64_t j = 0; j < wn; ++j) {
+        const uint32_t e = (word_at(raw, w0 + j) >> 7) & 0xff;
+        if (code1[e] != kPrimaryEscape) continue;
+        const uint32_t c = code2[e];
+        const uint8_t bits = static_cast<uint8_t>(c << (4 * (r & 1)));
+        if (r / 2 == edge_lo || r / 2 == edge_hi)
+          __atomic_fetch_or(Y + r / 2, bits, __ATOMIC_RELAXED);
+        else
+          Y[r / 2] |= bits;
+        ++r;
+        if (c == kSecondaryEscape) {
+          const uint32_t v = static_cast<uint32_t>(j << 8) | e;
+          std::memcpy(X + 4 * x, &v, 4);
+          ++x;
+        }
       }
     }
   });
@@ -345,6 +518,138 @@ __global__ __launch_bounds__(kExpThreads) void expcode_decode_kernel(uint8_t *__
   }
 }
 
+constexpr int kDenseInFlight = 4;  // groups whose loads each lane keeps in flight (the source is HBM)
+
+// Dense blocks (version 2) from device memory. The same group walk and store mapping as
+// expcode_decode_kernel: lane l decodes runs h = 0, 1 of words [512h + 8l, 512h + 8l + 8) of each group.
+// A run's primary codes are bit l of byte 64h + l of the group's three bit planes; the escape mask of a run
+// is the AND of its three bytes. A primary escape's secondary code is the nibble at its rank in word order:
+// S1 of its group, plus the escapes of earlier runs and lanes (one inclusive scan of the packed per-lane
+// counts across the wave), plus those before it in its own run. Ranks and list reads are clamped to
+// `capacity`; a header of another raw size writes nothing.
+__global__ __launch_bounds__(kExpThreads) void expcode_dense_decode_kernel(uint8_t *__restrict__ dst,
+                                                                           const uint8_t *__restrict__ src,
+                                                                           uint64_t capacity, uint64_t n) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = static_cast<uint64_t>(blockIdx.x) * kExpWaves + threadIdx.x / 64;
+  const uint64_t waves = static_cast<uint64_t>(gridDim.x) * kExpWaves;
+  const uint64_t n_words = n / 2;
+  const uint64_t groups = (n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  const uint64_t sect = (4 * (groups + 1) + 15) / 16 * 16;
+  const uint64_t off_p = kExpcodeHeaderBytes + kExpcodeGroupWords * groups;
+  const uint64_t off_s1 = off_p + kDensePlaneBytes * groups;
+  const uint64_t off_s2 = off_s1 + sect;
+  const uint64_t off_y = off_s2 + sect;
+  if (off_y > capacity || *reinterpret_cast<const uint64_t *>(src + 8) != n) return;
+  const uint64_t e1 = *reinterpret_cast<const uint64_t *>(src + 32);
+  const uint64_t off_x = off_y + ((min(e1, capacity) + 1) / 2 + 15) / 16 * 16;
+  uint64_t e2 = *reinterpret_cast<const uint64_t *>(src + 40);
+  e2 = off_x <= capacity ? min(e2, (capacity - off_x) / 4) : 0;
+  const uint64_t y_bytes = capacity - off_y;
+  const uint64_t t1 = *reinterpret_cast<const uint64_t *>(src + 48);
+  const uint64_t t2a = *reinterpret_cast<const uint64_t *>(src + 56);
+  const uint64_t t2b = *reinterpret_cast<const uint64_t *>(src + 64);
+  if ((n & 1) && blockIdx.x == 0 && threadIdx.x == 0) dst[n - 1] = src[72];
+  const uint8_t *A = src + kExpcodeHeaderBytes;
+  const uint8_t *P = src + off_p;
+  const uint32_t *S1 = reinterpret_cast<const uint32_t *>(src + off_s1);
+  const uint32_t *S2 = reinterpret_cast<const uint32_t *>(src + off_s2);
+  const uint8_t *Y = src + off_y;
+  const uint32_t *X = reinterpret_cast<const uint32_t *>(src + off_x);
+  for (uint64_t g0 = wave * kDenseInFlight; g0 < groups; g0 += waves * kDenseInFlight) {
+    u32x2 a[kDenseInFlight][2];
+    uint32_t pl[kDenseInFlight][2][3];
+#pragma unroll
+    for (int i = 0; i < kDenseInFlight; ++i) {
+      const uint64_t g = min(g0 + i, groups - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        a[i][h] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2 *>(A + g * kExpcodeGroupWords + 512 * h) + lane);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) pl[i][h][k] = P[g * kDensePlaneBytes + 128 * k + 64 * h + lane];
+      }
+    }
+    // S1 and S2 at g0 .. g0 + kDenseInFlight, one entry per lane, clamped to the last
+    const uint64_t si = min(g0 + min(lane, kDenseInFlight), groups);
+    const uint32_t s1v = S1[si], s2v = S2[si];
+#pragma unroll
+    for (int i = 0; i < kDenseInFlight; ++i) {
+      const uint64_t g = g0 + i;
+      if (g >= groups) break;
+      uint32_t e[16];  // run h, word j at 8h + j
+      uint32_t mask[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        mask[h] = pl[i][h][0] & pl[i][h][1] & pl[i][h][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t c = ((pl[i][h][0] >> j) & 1) | (((pl[i][h][1] >> j) & 1) << 1) | (((pl[i][h][2] >> j) & 1) << 2);
+          e[8 * h + j] = static_cast<uint32_t>(t1 >> (8 * c)) & 0xff;
+        }
+      }
+      const uint32_t s1a = __shfl(s1v, i, 64), s1b = __shfl(s1v, i + 1, 64);
+      if (s1b > s1a) {  // wave-uniform: the group has primary escapes
+        const uint32_t cnt = __popc(mask[0]) | (__popc(mask[1]) << 16);
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t y = __shfl_up(incl, d, 64);
+          if (lane >= d) incl += y;
+        }
+        const uint32_t excl = incl - cnt;
+        const uint32_t run0 = __shfl(incl, 63, 64) & 0xffff;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint64_t r = static_cast<uint64_t>(s1a) + (h ? run0 + (excl >> 16) : (excl & 0xffff));
+          uint32_t m = mask[h];
+          while (m) {
+            const int j = __builtin_ctz(m);
+            m &= m - 1;
+            const uint32_t yb = (r >> 1) < y_bytes ? Y[r >> 1] : 0u;
+            const uint32_t c2 = (yb >> (4 * (r & 1))) & 0xf;
+            const uint64_t t = c2 < 8 ? t2a : t2b;
+            e[8 * h + j] = static_cast<uint32_t>(t >> (8 * (c2 & 7))) & 0xff;  // a secondary escape: patched below
+            ++r;
+          }
+        }
+        const uint32_t s2a = __shfl(s2v, i, 64);
+        const uint32_t s2b = min(static_cast<uint64_t>(__shfl(s2v, i + 1, 64)), e2);
+        for (uint32_t k = s2a; k < s2b; ++k) {  // wave-uniform; secondary escapes are rarer still
+          const uint32_t x = X[k];
+          const uint32_t pos = x >> 8;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (pos == static_cast<uint32_t>(512 * h + 8 * lane + j)) e[8 * h + j] = x & 0xffu;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint64_t w0 = g * kExpcodeGroupWords + 512 * h + 8 * static_cast<uint64_t>(lane);
+        uint8_t *out = dst + 2 * w0;
+        uint32_t word[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t av = (a[i][h][j >> 2] >> (8 * (j & 3))) & 0xff;
+          word[j] = ((av & 0x80) << 8) | (e[8 * h + j] << 7) | (av & 0x7f);
+        }
+        if (w0 + 8 <= n_words) {
+          u32x4 v;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = word[2 * k] | (word[2 * k + 1] << 16);
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (w0 + j < n_words) reinterpret_cast<uint16_t *>(out)[j] = static_cast<uint16_t>(word[j]);
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t allow_expcode_lds(size_t bytes) {
@@ -361,6 +666,18 @@ hipError_t launch_expcode_decode(void *dst, const void *src_dev, uint64_t capaci
   const unsigned g = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, static_cast<uint64_t>(grid))));
   hipLaunchKernelGGL(expcode_decode_kernel, dim3(g), dim3(kExpThreads), static_cast<unsigned>(reserve_lds), stream,
                      static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src_dev), capacity, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_expcode_dense_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
+                                       size_t reserve_lds, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const uint64_t groups = (n / 2 + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  const uint64_t per_block = static_cast<uint64_t>(kExpWaves) * kDenseInFlight;
+  const uint64_t need = std::max<uint64_t>(1, (groups + per_block - 1) / per_block);
+  const unsigned g = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, static_cast<uint64_t>(grid))));
+  hipLaunchKernelGGL(expcode_dense_decode_kernel, dim3(g), dim3(kExpThreads), static_cast<unsigned>(reserve_lds),
+                     stream, static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src_dev), capacity, n);
   return hipGetLastError();
 }
 

@@ -146,6 +146,24 @@ hipError_t launch_expcode_decode(void *dst, const void *src_dev, uint64_t capaci
                                  size_t reserve_lds, hipStream_t stream);
 hipError_t allow_expcode_lds(size_t bytes);
 
+// Dense exponent-coded blocks (version 2): 3-bit primary codes for the 7 most frequent exponents in three
+// bit planes, a 4-bit secondary code per primary escape for the next 15, a list for the rest. Sections
+// after the 256-byte header: plane A (1024 bytes a group), plane P (384 a group), S1 and S2 (G + 1 u32
+// each, 16-byte aligned), Y (a nibble per primary escape, 16-byte aligned), X (a u32 per secondary escape).
+constexpr uint64_t kDensePlaneBytes = 384;
+struct DenseLayout {
+  uint64_t n, n_words, groups, e1, e2;
+  uint64_t off_p, off_s1, off_s2, off_y, off_x, total;
+};
+// The section offsets of a dense block of raw size n with e1 primary and e2 secondary escapes.
+DenseLayout dense_layout(uint64_t n, uint64_t e1, uint64_t e2);
+// out == nullptr: only *out_bytes (the encoded size) is computed.
+int expcode_encode_dense(const void *raw, size_t nbytes, void *out, size_t out_capacity, size_t *out_bytes);
+// Decodes the dense block of raw size n at src_dev (device memory, `capacity` bytes readable) into dst; the
+// kernel reads the block's header when it runs and writes nothing for a header of another raw size.
+hipError_t launch_expcode_dense_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
+                                       size_t reserve_lds, hipStream_t stream);
+
 // Host-side helpers shared with the oracle's definition of the checksum.
 inline uint64_t splitmix64(uint64_t x) {
   x += 0x9e3779b97f4a7c15ull;

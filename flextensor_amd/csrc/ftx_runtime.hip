@@ -805,6 +805,41 @@ int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t 
   return FTX_OK;
 }
 
+int ftx_expcode_encode_dense(const void *raw, size_t n, void *out, size_t capacity, size_t *out_bytes) {
+  FTX_REQUIRE_LIVE();
+  if (!out_bytes) return ftx::fail(FTX_ERR_INVALID, "out_bytes is null");
+  if (n > 0 && !raw) return ftx::fail(FTX_ERR_INVALID, "raw is null");
+  if (out && raw && n > 0) {
+    const auto r = reinterpret_cast<uintptr_t>(raw), o = reinterpret_cast<uintptr_t>(out);
+    if (o < r + n && r < o + capacity) return ftx::fail(FTX_ERR_INVALID, "output overlaps the raw block");
+  }
+  return ftx::expcode_encode_dense(raw, n, out, capacity, out_bytes);
+}
+
+int ftx_expcode_decode_dense_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid,
+                                 void *stream) {
+  FTX_REQUIRE_LIVE();
+  if (raw_bytes == 0) return FTX_OK;
+  if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
+  if (grid < 0 || grid > (1 << 20)) return ftx::fail(FTX_ERR_INVALID, "grid must be in [0, 2^20]");
+  if (reinterpret_cast<uintptr_t>(dst) % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+    return ftx::fail(FTX_ERR_INVALID, "decode source and destination need 16-byte alignment");
+  const ftx::DenseLayout d = ftx::dense_layout(raw_bytes, 0, 0);
+  if (src_bytes < d.off_y) return ftx::fail(FTX_ERR_INVALID, "encoded block is shorter than its raw size needs");
+  int rc = ftx::check_device_range(dst, raw_bytes, "decode destination");
+  if (rc == FTX_OK) rc = ftx::check_device_range(src, src_bytes, "encoded block");
+  if (rc != FTX_OK) return rc;
+  ftx::DeviceState *st = nullptr;
+  rc = ftx::device_state(&st);
+  if (rc != FTX_OK) return rc;
+  const int g = grid > 0 ? grid : 8 * st->cu_count;
+  const size_t reserve = g <= ftx::kZeroCopyReserveMaxGrid ? st->copy_reserve_lds
+                                                           : (st->copy_reserve_lds ? size_t{1024} : size_t{0});
+  FTX_HIP(ftx::launch_expcode_dense_decode(dst, src, src_bytes, raw_bytes, g, reserve,
+                                           static_cast<hipStream_t>(stream)));
+  return FTX_OK;
+}
+
 int ftx_set_staging_policy(size_t piece_bytes, int n_threads) { return ftx::set_staging_policy(piece_bytes, n_threads); }
 
 int ftx_get_staging_policy(size_t *piece_bytes, int *n_threads) {

@@ -33,11 +33,12 @@ def _raw_ptr(raw: torch.Tensor) -> tuple[int, int]:
     return raw.data_ptr(), raw.numel() * raw.element_size()
 
 
-def encoded_size(raw: torch.Tensor) -> int:
-    """Bytes of the encoded block for ``raw`` (a contiguous CPU tensor, read as bytes)."""
+def encoded_size(raw: torch.Tensor, dense: bool = False) -> int:
+    """Bytes of the encoded block for ``raw`` (a contiguous CPU tensor, read as bytes); ``dense``: of the
+    dense format (version 2) that units kept in device memory use."""
     ptr, n = _raw_ptr(raw)
     out = ctypes.c_size_t(0)
-    nat.call("ftx_expcode_encode", ptr, n, None, 0, ctypes.byref(out))
+    nat.call("ftx_expcode_encode_dense" if dense else "ftx_expcode_encode", ptr, n, None, 0, ctypes.byref(out))
     return int(out.value)
 
 
@@ -117,11 +118,11 @@ def decode_h2d(dst: torch.Tensor, block: EncodedBlock, stream: HipStream | None 
     nat.call("ftx_expcode_decode_h2d", dst.data_ptr(), block.arena.ptr, block.arena.nbytes, pol, s.handle)
 
 
-def packed_encoded_size(tensors: list[torch.Tensor], alignment: int, scratch: torch.Tensor | None = None) -> \
-        tuple[int, int]:
+def packed_encoded_size(tensors: list[torch.Tensor], alignment: int, scratch: torch.Tensor | None = None,
+                        dense: bool = False) -> tuple[int, int]:
     """(encoded bytes, raw bytes) of the block that packs ``tensors`` (CPU) at ``alignment``, as a block
     controller packs them: gaps zeroed, so the size is exact. ``scratch`` (uint8, CPU), when large enough,
-    holds the packed bytes instead of a new buffer."""
+    holds the packed bytes instead of a new buffer; ``dense`` sizes the dense format (version 2)."""
     from .layout import pack_into, plan_block
 
     slots, total = plan_block(tensors, alignment)
@@ -130,42 +131,46 @@ def packed_encoded_size(tensors: list[torch.Tensor], alignment: int, scratch: to
     buf = scratch[:total] if scratch is not None and scratch.numel() >= total else torch.empty(total,
                                                                                                  dtype=torch.uint8)
     pack_into(buf, slots, tensors)
-    return encoded_size(buf), total
+    return encoded_size(buf, dense), total
 
 
 class DeviceEncodedBlock:
     """An encoded block kept in device memory: ``dev`` (uint8, ``capacity`` bytes) holds ``nbytes`` of
-    encoded bytes for a raw block of ``raw_bytes``. Serves units kept resident in HBM in encoded form:
-    :meth:`decode` rebuilds the raw block on the device before the unit runs.
+    encoded bytes for a raw block of ``raw_bytes``, in the dense format (version 2) when ``dense``, else
+    in version 1. Serves units kept resident in HBM in encoded form: :meth:`decode` rebuilds the raw block
+    on the device before the unit runs.
 
     :meth:`reencode` rewrites the block in place (same device buffer, so decodes captured in a graph stay
     valid and read the new header when they run) as long as the new encoding fits ``capacity``."""
 
-    __slots__ = ("dev", "nbytes", "raw_bytes")
+    __slots__ = ("dev", "nbytes", "raw_bytes", "dense")
 
-    def __init__(self, dev: torch.Tensor, nbytes: int, raw_bytes: int) -> None:
+    def __init__(self, dev: torch.Tensor, nbytes: int, raw_bytes: int, dense: bool = False) -> None:
         self.dev = dev
         self.nbytes = int(nbytes)
         self.raw_bytes = int(raw_bytes)
+        self.dense = bool(dense)
 
     @staticmethod
-    def _encode_host(raw: torch.Tensor) -> torch.Tensor:
+    def _encode_host(raw: torch.Tensor, dense: bool) -> torch.Tensor:
         ptr, n = _raw_ptr(raw)
-        size = encoded_size(raw)
+        size = encoded_size(raw, dense)
         host = torch.empty(max(size, 1), dtype=torch.uint8)
         out = ctypes.c_size_t(0)
-        nat.call("ftx_expcode_encode", ptr, n, host.data_ptr(), host.numel(), ctypes.byref(out))
+        nat.call("ftx_expcode_encode_dense" if dense else "ftx_expcode_encode", ptr, n, host.data_ptr(),
+                 host.numel(), ctypes.byref(out))
         return host[: out.value]
 
     @classmethod
-    def from_raw(cls, raw: torch.Tensor, capacity: int, device: torch.device) -> "DeviceEncodedBlock":
+    def from_raw(cls, raw: torch.Tensor, capacity: int, device: torch.device,
+                 dense: bool = False) -> "DeviceEncodedBlock":
         """Encode ``raw`` (contiguous CPU) into a new device buffer of ``capacity`` bytes."""
-        host = cls._encode_host(raw)
+        host = cls._encode_host(raw, dense)
         if host.numel() > capacity:
             raise ValueError(f"the encoding needs {host.numel()} bytes, more than its capacity of {capacity}")
         dev = torch.empty(max(int(capacity), 16), dtype=torch.uint8, device=device)
         dev[: host.numel()].copy_(host)
-        return cls(dev, host.numel(), raw.numel() * raw.element_size())
+        return cls(dev, host.numel(), raw.numel() * raw.element_size(), dense)
 
     @property
     def capacity(self) -> int:
@@ -182,7 +187,7 @@ class DeviceEncodedBlock:
         n = raw.numel() * raw.element_size()
         if n != self.raw_bytes:
             raise ValueError(f"raw block of {n} bytes, but this block encodes {self.raw_bytes}")
-        host = self._encode_host(raw)
+        host = self._encode_host(raw, self.dense)
         if host.numel() > self.capacity:
             raise ValueError(f"the new encoding needs {host.numel()} bytes, more than the {self.capacity} "
                              "reserved on the device")
@@ -192,18 +197,19 @@ class DeviceEncodedBlock:
 
     def decode(self, dst: torch.Tensor, stream: HipStream | None = None) -> None:
         """Stream-ordered decode into the first ``raw_bytes`` bytes of ``dst`` (eight workgroups per CU)."""
-        decode_d2d(dst, self.dev, self.raw_bytes, stream)
+        decode_d2d(dst, self.dev, self.raw_bytes, stream, dense=self.dense)
 
 
 def decode_d2d(dst: torch.Tensor, encoded: torch.Tensor, raw_bytes: int, stream: HipStream | None = None,
-               grid: int = 0) -> None:
+               grid: int = 0, dense: bool = False) -> None:
     """Stream-ordered decode of an encoded block held in device memory (``encoded``, a uint8 device tensor)
-    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs eight workgroups per CU."""
+    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs eight workgroups per CU. ``dense``: the
+    block is in the dense format (version 2)."""
     if dst.device.type != "cuda" or encoded.device.type != "cuda":
         raise ValueError("decode_d2d needs device tensors")
     if raw_bytes > dst.numel() * dst.element_size():
         raise ValueError(f"decoded block of {raw_bytes} bytes does not fit destination of "
                          f"{dst.numel() * dst.element_size()} bytes")
     s = stream if stream is not None else current_stream(dst.device)
-    nat.call("ftx_expcode_decode_d2d", dst.data_ptr(), encoded.data_ptr(), encoded.numel(), raw_bytes, int(grid),
-             s.handle)
+    nat.call("ftx_expcode_decode_dense_d2d" if dense else "ftx_expcode_decode_d2d", dst.data_ptr(),
+             encoded.data_ptr(), encoded.numel(), raw_bytes, int(grid), s.handle)

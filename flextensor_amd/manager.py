@@ -1673,8 +1673,8 @@ class OffloadManager:
                                self._budget() if budget is None else budget, encodable)
 
     def _encodable(self, units: Sequence[_Unit], budget: int | None) -> dict[str, tuple[int, int]] | None:
-        """Per unit whose packed block encodes to under 0.9 of its bytes: (device bytes to reserve for the
-        encoded block, bytes of the packed raw block). None when there is no budget or everything fits
+        """Per unit whose packed block encodes to under 0.9 of its bytes in the dense format (the one units
+        kept in HBM use): (device bytes to reserve for the encoded block, bytes of the packed raw block). None when there is no budget or everything fits
         raw. The reservation adds max(64 KiB, 0.1% of the raw block) to the encoded size, room for a
         later state-dict load to re-encode in place."""
         if budget is None or self._resident_bytes + sum(u.nbytes for u in units) <= budget:
@@ -1693,7 +1693,7 @@ class OffloadManager:
             need = sum(p.numel() * p.element_size() for p in tensors) + DEFAULT_ALIGNMENT * len(tensors)
             if scratch is None or scratch.numel() < need:
                 scratch = torch.empty(need, dtype=torch.uint8)
-            size, raw = expcode.packed_encoded_size(tensors, DEFAULT_ALIGNMENT, scratch)
+            size, raw = expcode.packed_encoded_size(tensors, DEFAULT_ALIGNMENT, scratch, dense=True)
             if raw == 0 or size > expcode.DEFAULT_MAX_RATIO * raw:
                 continue
             reserve = (size + max(1 << 16, raw // 1024) + 255) // 256 * 256

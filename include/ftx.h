@@ -213,6 +213,17 @@ int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const f
  * grid 0 runs eight workgroups per CU. Serves units kept encoded in HBM
  * (OffloadConfig.encode_resident_blocks). */
 int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid, void *stream);
+/* Dense exponent-coded blocks (FTXE version 2), for units kept encoded in
+ * device memory: 3-bit codes for a block's 7 most frequent exponents in three
+ * bit planes, a 4-bit code for each other word's exponent among the next 15,
+ * and a list for the rest; about 0.70 of the raw size for bf16 weights, against
+ * 0.75 for version 1. A decoder ranks each escaped word among the group's
+ * escapes, which costs a dependent read: cheap from HBM, so version 2 is decoded
+ * only from device memory. Same contracts as ftx_expcode_encode and
+ * ftx_expcode_decode_d2d. No reference counterpart. */
+int ftx_expcode_encode_dense(const void *raw, size_t n, void *out, size_t capacity, size_t *out_bytes);
+int ftx_expcode_decode_dense_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid,
+                                 void *stream);
 
 /* ---- staged copies from pageable host memory ------------------------------
  * Replace the reference's copy from pageable or shared-memory blocks that are

@@ -21,4 +21,6 @@ a pure-Python library) and cites the file:line it follows:
                    scatter, checksum)
 * ``expcode``      the exponent-coded block format of encoded streamed
                    blocks (this build's own format, no reference counterpart)
+* ``expcode_dense`` the dense exponent-coded format (v2) of units kept
+                   encoded in HBM (this build's own, no reference counterpart)
 """

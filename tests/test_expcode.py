@@ -188,3 +188,99 @@ def test_encoding_follows_its_own_pass_rule():
                       (types.SimpleNamespace(pass_compute_ms=95.0, pass_transfer_ms=100.0), True)):
         mgr.link = link
         assert mgr._measured_compute_bound() == off
+
+
+# ---- the dense format (version 2) of units kept encoded in HBM ---------------------------------------
+
+from oracle import expcode_dense as D  # noqa: E402
+
+
+def test_dense_known_answer_with_both_escape_levels():
+    # exponents 1..24, exponent e written 25 - e times: 1..7 are primary, 8..22 secondary, 23 and 24 listed
+    ws = [e << 7 | (e & 0x7F) for e in range(1, 25) for _ in range(25 - e)]
+    raw = _words(*ws)
+    enc = D.encode(raw)
+    h = D.parse_header(enc)
+    assert h["t1"] == list(range(1, 8)) + [0] and h["t2"] == list(range(8, 23)) + [0]
+    n8 = sum(25 - e for e in range(1, 8))  # words before the first primary escape
+    assert h["e1"] == len(ws) - n8 and h["e2"] == 2 + 1 and h["groups"] == 1
+    assert enc.size == D.sections(1, h["e1"], 3)["total"]
+    codes = np.zeros(1024, np.uint8)
+    planes = enc[h["off_p"]: h["off_p"] + 384].reshape(3, 128)
+    for k in range(3):
+        codes |= ((np.unpackbits(planes[k], bitorder="little")) << k).astype(np.uint8)
+    assert list(codes[:3]) == [0] * 3 and codes[n8 - 1] == 6 and codes[n8] == 7 and not codes[len(ws):].any()
+    y = enc[h["off_y"]: h["off_y"] + 2]
+    assert y[0] == 0x00 and list(enc[h["off_s1"]: h["off_s1"] + 8].view("<u4")) == [0, h["e1"]]
+    p23 = ws.index(23 << 7 | 23)
+    assert list(enc[h["off_x"]: h["off_x"] + 12].view("<u4")) == [p23 << 8 | 23, (p23 + 1) << 8 | 23, (p23 + 2) << 8 | 24]
+    assert D.decode(enc) == raw.tobytes()
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 3, 2046, 2048, 2049, 6145, 1 << 16])
+def test_dense_round_trips(n):
+    rng = np.random.default_rng(n + 5)
+    for raw in (_bf16(n // 2 + 1, n)[:n], rng.integers(0, 256, n, dtype=np.uint8)):
+        enc = D.encode(raw)
+        assert enc.size == D.encoded_size(raw)
+        assert D.decode(enc) == raw.tobytes()
+
+
+def test_dense_every_bf16_pattern_and_density():
+    words = np.arange(1 << 16, dtype=np.uint32).astype("<u2").view(np.uint8)
+    assert D.decode(D.encode(words)) == words.tobytes()
+    raw = _bf16(1 << 20, 7)
+    assert 0.69 < D.encoded_size(raw) / raw.size < 0.70 < 0.75 < X.encoded_size(raw) / raw.size
+
+
+def test_dense_decoder_refuses_inconsistent_blocks():
+    raw = _words(*[e << 7 for e in range(1, 30) for _ in range(31 - e)])
+    enc = D.encode(raw)
+    h = D.parse_header(enc)
+    bad = enc.copy()
+    bad[h["off_s1"] + 4] += 1  # S1[G] no longer E1
+    with pytest.raises(ValueError):
+        D.decode(bad)
+    bad = enc.copy()
+    bad[h["off_x"] + 1] ^= 0x01  # a listed word moved
+    with pytest.raises(ValueError):
+        D.decode(bad)
+    bad = enc.copy()
+    for k in range(3):
+        bad[h["off_p"] + 128 * k] |= 0x01  # word 0's primary code made an escape: one more than S1 counts
+    with pytest.raises(ValueError):
+        D.decode(bad)
+    with pytest.raises(ValueError):
+        D.decode(enc[: h["total"] - 1])
+
+
+def _lib_encode_dense(raw: np.ndarray) -> np.ndarray:
+    from flextensor_amd import _native as nat
+
+    raw = np.ascontiguousarray(raw)
+    size = ctypes.c_size_t(0)
+    ptr = raw.ctypes.data if raw.size else None
+    nat.call("ftx_expcode_encode_dense", ptr, raw.size, None, 0, ctypes.byref(size))
+    out = np.full(size.value + 8, 0xEE, dtype=np.uint8)
+    got = ctypes.c_size_t(0)
+    nat.call("ftx_expcode_encode_dense", ptr, raw.size, out.ctypes.data, out.size, ctypes.byref(got))
+    assert got.value == size.value and np.all(out[size.value:] == 0xEE)
+    return out[: size.value]
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 5, 2047, 2048, 2050, 10001, (1 << 21) + 3])
+def test_library_dense_encoder_matches_the_oracle(n):
+    rng = np.random.default_rng(n + 2)
+    for raw in (_bf16(n // 2 + 1, n)[:n], rng.integers(0, 256, n, dtype=np.uint8)):
+        assert np.array_equal(_lib_encode_dense(raw), D.encode(raw))
+
+
+def test_library_dense_encoder_on_threaded_blocks_with_shared_nibble_bytes():
+    """Blocks large enough for the encoder's threads: with escapes in every group, the nibble bytes at the
+    edges of one thread's range hold a nibble of the next (an odd count of escapes before them)."""
+    for seed in range(3):
+        raw = _bf16(3 << 20, 20 + seed, std=0.02 * (1 + seed))
+        rng = np.random.default_rng(seed)
+        idx = rng.integers(0, raw.size // 2, 5000) * 2 + 1  # high bytes: exponents off the tables
+        raw[idx] = rng.integers(0, 256, idx.size, dtype=np.uint8)
+        assert np.array_equal(_lib_encode_dense(raw), D.encode(raw))

@@ -22,6 +22,7 @@ from flextensor_amd import workloads as W
 from flextensor_amd.config import OffloadConfig
 from flextensor_amd.manager import OffloadManager, OffloadPhase
 from oracle import expcode as oxc
+from oracle import expcode_dense as oxd
 
 pytestmark = pytest.mark.gpu
 
@@ -37,20 +38,31 @@ def _dev(a: np.ndarray, gpu, pad: int = 0, fill: int = 0) -> torch.Tensor:
     return t
 
 
+def _escape_heavy(n: int, seed: int) -> np.ndarray:
+    """bf16 words whose high bytes are random at one word in 40: exponents off every table, in every group."""
+    raw = _bf16_bytes(n, seed)
+    rng = np.random.default_rng(seed)
+    idx = np.arange(1, n, 80)
+    raw[idx] = rng.integers(0, 256, idx.size, dtype=np.uint8)
+    return raw
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 2047, 2048, 2049, 16383, (1 << 20) + 5, 64 << 20])
-@pytest.mark.parametrize("kind", ["bf16", "bytes"])
-def test_decode_d2d_is_bit_exact(gpu, n, kind):
+@pytest.mark.parametrize("kind", ["bf16", "bytes", "mixed"])
+@pytest.mark.parametrize("dense", [False, True])
+def test_decode_d2d_is_bit_exact(gpu, n, kind, dense):
     from flextensor_amd import expcode
 
-    if kind == "bytes" and n > (1 << 21):
+    if kind != "bf16" and n > (1 << 21):
         pytest.skip("escape-heavy data: the smaller sizes cover it")
-    print(f"decode_d2d n={n} kind={kind}", flush=True)
-    raw = _bf16_bytes(n, n) if kind == "bf16" else np.random.default_rng(n).integers(0, 256, n, dtype=np.uint8)
-    enc = oxc.encode(raw)
+    print(f"decode_d2d n={n} kind={kind} dense={dense}", flush=True)
+    raw = (_bf16_bytes(n, n) if kind == "bf16" else _escape_heavy(n, n) if kind == "mixed"
+           else np.random.default_rng(n).integers(0, 256, n, dtype=np.uint8))
+    enc = (oxd if dense else oxc).encode(raw)
     src = _dev(enc, gpu, pad=(-enc.size) % 16)
     for grid in (0, 16):
         dst = torch.full((n + 64,), 0xA5, dtype=torch.uint8, device=gpu)
-        expcode.decode_d2d(dst, src, n, grid=grid)
+        expcode.decode_d2d(dst, src, n, grid=grid, dense=dense)
         torch.cuda.synchronize()
         got = dst.cpu().numpy()
         assert np.array_equal(got[:n], raw), f"grid {grid}"
@@ -79,15 +91,41 @@ def test_decode_d2d_refusals_and_a_foreign_header(gpu):
     assert torch.all(dst == 0x11)
 
 
-def test_device_block_reencodes_in_place_and_captured_decodes_follow(gpu):
+def test_dense_decode_refusals_and_a_foreign_header(gpu):
+    from flextensor_amd import _native as nat
     from flextensor_amd import expcode
 
+    raw = _escape_heavy(1 << 16, 3)
+    enc = oxd.encode(raw)
+    src = _dev(enc, gpu, pad=64)
+    dst = torch.full((raw.size + 64,), 0x11, dtype=torch.uint8, device=gpu)
+    with pytest.raises(nat.FtxError):  # shorter than the sections before Y
+        nat.call("ftx_expcode_decode_dense_d2d", dst.data_ptr(), src.data_ptr(), 1000, raw.size, 0, None)
+    with pytest.raises(nat.FtxError):
+        nat.call("ftx_expcode_decode_dense_d2d", dst.data_ptr() + 2, src.data_ptr(), src.numel(), raw.size, 0, None)
+    expcode.decode_d2d(dst, src, raw.size - 2048, dense=True)  # another raw size than the header's
+    torch.cuda.synchronize()
+    assert torch.all(dst == 0x11)
+    # a block cut short inside Y and X: reads stay in the stated bytes, and what they cover decodes
+    h = oxd.parse_header(enc)
+    assert h["e1"] > 100 and h["e2"] > 10
+    short = _dev(enc[: h["off_y"] + 16], gpu)
+    expcode.decode_d2d(dst, short, raw.size, dense=True)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dense", [False, True])
+def test_device_block_reencodes_in_place_and_captured_decodes_follow(gpu, dense):
+    from flextensor_amd import expcode
+
+    fmt = oxd if dense else oxc
     n = (3 << 20) + 2
     a = torch.from_numpy(_bf16_bytes(n, 7))
     b = torch.from_numpy(_bf16_bytes(n, 8, std=3.0))  # another exponent table
-    block = expcode.DeviceEncodedBlock.from_raw(a, oxc.encoded_size(b.numpy()) + 4096, gpu)
-    assert block.nbytes == oxc.encoded_size(a.numpy()) and block.raw_bytes == n and block.ratio < 0.76
-    assert np.array_equal(block.dev[: block.nbytes].cpu().numpy(), oxc.encode(a.numpy()))
+    block = expcode.DeviceEncodedBlock.from_raw(a, fmt.encoded_size(b.numpy()) + 4096, gpu, dense=dense)
+    assert block.nbytes == fmt.encoded_size(a.numpy()) and block.raw_bytes == n
+    assert block.ratio < (0.70 if dense else 0.76)
+    assert np.array_equal(block.dev[: block.nbytes].cpu().numpy(), fmt.encode(a.numpy()))
     dst = torch.empty(n, dtype=torch.uint8, device=gpu)
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):

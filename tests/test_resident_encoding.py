@@ -97,6 +97,10 @@ def test_packed_encoded_size_is_exact():
     assert size == X.encoded_size(block.numpy()) == X.encode(block.numpy()).size
     scratch = torch.full((total + 100,), 0x33, dtype=torch.uint8)  # a larger, dirty scratch gives the same
     assert expcode.packed_encoded_size(ts, 128, scratch) == (size, raw)
+    from oracle import expcode_dense as D
+
+    dense, _ = expcode.packed_encoded_size(ts, 128, scratch, dense=True)  # the format units kept in HBM use
+    assert dense == D.encoded_size(block.numpy()) == D.encode(block.numpy()).size < size
 
 
 def test_config_rules():
