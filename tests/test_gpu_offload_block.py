@@ -167,3 +167,32 @@ def test_block_errors(gpu):
     with torch.no_grad(), om2.offload_block("layers.0"):  # a patched module unit: the block does nothing
         patched.layers[0](x)
     om2.release()
+
+
+def test_blocks_kept_encoded_in_hbm(gpu):
+    """Manual blocks as units kept exponent-coded in HBM (encode_resident_blocks): bf16 layers of 2 MiB
+    under a budget of 11 of 12 layers. Raw, 3 blocks would stream; with the option fewer do, the rest
+    decode from HBM as their block opens, and every pass equals the resident forward bit for bit."""
+    torch.manual_seed(4)
+    model = BlockModel(n=12, width=1024).to(torch.bfloat16)
+    torch.manual_seed(4)
+    ref = BlockModel(n=12, width=1024).to(torch.bfloat16).to(gpu)
+    tokens = torch.randint(0, 64, (2, 8), device=gpu)
+    with torch.no_grad():
+        want = ref(tokens)
+    budget = _bytes(model.embed) + model.shared.numel() * 2 + 11 * _bytes(model.layers[0])
+    om = get_offload_manager("manual-hbm")
+    model.manager = om.name
+    om.offload(model, _cfg(budget, encode_resident_blocks=True, link_benchmark=False))
+    try:
+        with torch.no_grad():
+            for _ in range(4):
+                assert torch.equal(model(tokens), want)
+        assert om.phase == OffloadPhase.INFERENCE and om.plan.encoded_resident
+        assert 0 < len(om.plan.streamed) < 3
+        assert all(u.module is None for u in om.units)
+        assert om.get_gpu_memory_usage().total_bytes <= budget
+    finally:
+        om.release()
+    for p, q in zip(model.parameters(), ref.parameters()):
+        assert p.device.type == "cpu" and torch.equal(p, q.cpu())
