@@ -344,9 +344,10 @@ int expcode_encode_dense(const void *raw_v, size_t nbytes, void *out_v, size_t o
           }
           A[w0 + j] = a;
         }
-        planes[i] = static_cast<uint8_t>(b0);
-        planes[128 + i] = static_cast<uint8_t>(b1);
-        planes[256 + i] = static_cast<uint8_t>(b2);
+        const uint64_t at = 2 * (i % 64) + i / 64;  // words 512 h + 8 l .. : byte 2 l + h of each plane
+        planes[at] = static_cast<uint8_t>(b0);
+        planes[128 + at] = static_cast<uint8_t>(b1);
+        planes[256 + at] = static_cast<uint8_t>(b2);
       }
       count1[static_cast<size_t>(g)] = c1;
       count2[static_cast<size_t>(g)] = c2;
@@ -523,8 +524,8 @@ constexpr int kDenseInFlight = 4;  // groups whose loads each lane keeps in flig
 // Dense blocks (version 2) from device memory. The same group walk and store mapping as
 // expcode_decode_kernel: lane l decodes runs h = 0, 1 of words [512h + 8l, 512h + 8l + 8) of each group,
 // four words to a register with byte permutes (a 7B layer: 172 us, against 209 word by word).
-// A run's primary codes are bit l of byte 64h + l of the group's three bit planes; the escape mask of a run
-// is the AND of its three bytes. A primary escape's secondary code is the nibble at its rank in word order:
+// A lane's primary codes are one 16-bit value per bit plane (byte h for run h); the escape mask of a run is
+// the AND of its three bytes. A primary escape's secondary code is the nibble at its rank in word order:
 // S1 of its group, plus the escapes of earlier runs and lanes (one inclusive scan of the packed per-lane
 // counts across the wave), plus those before it in its own run. Ranks and list reads are clamped to
 // `capacity`; a header of another raw size writes nothing.
@@ -562,17 +563,17 @@ __global__ __launch_bounds__(kExpThreads) void expcode_dense_decode_kernel(uint8
   const uint32_t *X = reinterpret_cast<const uint32_t *>(src + off_x);
   for (uint64_t g0 = wave * kDenseInFlight; g0 < groups; g0 += waves * kDenseInFlight) {
     u32x2 a[kDenseInFlight][2];
-    uint32_t pl[kDenseInFlight][2][3];
+    uint32_t pw[kDenseInFlight][3];  // plane k: run 0's code bits in the low byte, run 1's in the next
 #pragma unroll
     for (int i = 0; i < kDenseInFlight; ++i) {
       const uint64_t g = min(g0 + i, groups - 1);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < 2; ++h)
         a[i][h] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x2 *>(A + g * kExpcodeGroupWords + 512 * h) + lane);
 #pragma unroll
-        for (int k = 0; k < 3; ++k) pl[i][h][k] = P[g * kDensePlaneBytes + 128 * k + 64 * h + lane];
-      }
+      for (int k = 0; k < 3; ++k)
+        pw[i][k] = reinterpret_cast<const uint16_t *>(P + g * kDensePlaneBytes + 128 * k)[lane];
     }
     // S1 and S2 at g0 .. g0 + kDenseInFlight, one entry per lane, clamped to the last
     const uint64_t si = min(g0 + min(lane, kDenseInFlight), groups);
@@ -588,12 +589,12 @@ __global__ __launch_bounds__(kExpThreads) void expcode_dense_decode_kernel(uint8
       uint32_t mask[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        mask[h] = pl[i][h][0] & pl[i][h][1] & pl[i][h][2];
+        mask[h] = (pw[i][0] & pw[i][1] & pw[i][2]) >> (8 * h) & 0xff;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           uint32_t codes = 0;
 #pragma unroll
-          for (int k = 0; k < 3; ++k) codes |= ((((pl[i][h][k] >> (4 * q)) & 0xf) * 0x00204081u) & 0x01010101u) << k;
+          for (int k = 0; k < 3; ++k) codes |= ((((pw[i][k] >> (8 * h + 4 * q)) & 0xf) * 0x00204081u) & 0x01010101u) << k;
           ex[h][q] = __builtin_amdgcn_perm(t1_hi, t1_lo, codes);
         }
       }

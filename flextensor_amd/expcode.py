@@ -196,15 +196,15 @@ class DeviceEncodedBlock:
         self.nbytes = host.numel()
 
     def decode(self, dst: torch.Tensor, stream: HipStream | None = None) -> None:
-        """Stream-ordered decode into the first ``raw_bytes`` bytes of ``dst`` (eight workgroups per CU)."""
+        """Stream-ordered decode into the first ``raw_bytes`` bytes of ``dst`` (the library's default grid)."""
         decode_d2d(dst, self.dev, self.raw_bytes, stream, dense=self.dense)
 
 
 def decode_d2d(dst: torch.Tensor, encoded: torch.Tensor, raw_bytes: int, stream: HipStream | None = None,
                grid: int = 0, dense: bool = False) -> None:
     """Stream-ordered decode of an encoded block held in device memory (``encoded``, a uint8 device tensor)
-    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs eight workgroups per CU. ``dense``: the
-    block is in the dense format (version 2)."""
+    into the first ``raw_bytes`` bytes of ``dst``; ``grid`` 0 runs eight workgroups per CU for version 1 and
+    sixteen for the dense format (``dense``, version 2)."""
     if dst.device.type != "cuda" or encoded.device.type != "cuda":
         raise ValueError("decode_d2d needs device tensors")
     if raw_bytes > dst.numel() * dst.element_size():

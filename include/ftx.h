@@ -220,7 +220,8 @@ int ftx_expcode_decode_d2d(void *dst, const void *src, size_t src_bytes, size_t 
  * 0.75 for version 1. A decoder ranks each escaped word among the group's
  * escapes, which costs a dependent read: cheap from HBM, so version 2 is decoded
  * only from device memory. Same contracts as ftx_expcode_encode and
- * ftx_expcode_decode_d2d. No reference counterpart. */
+ * ftx_expcode_decode_d2d, except that grid 0 runs sixteen workgroups per CU.
+ * No reference counterpart. */
 int ftx_expcode_encode_dense(const void *raw, size_t n, void *out, size_t capacity, size_t *out_bytes);
 int ftx_expcode_decode_dense_d2d(void *dst, const void *src, size_t src_bytes, size_t raw_bytes, int grid,
                                  void *stream);

@@ -18,7 +18,9 @@ block is:
   zero), u8 tail byte (the odd last byte, else 0), 7 zero bytes;
 * plane A at 256, G * 1024 bytes: byte w = sign(w) << 7 | mantissa(w); zero past W;
 * plane P at 256 + 1024 G, 384 bytes per group: for group g, three bit planes of 128 bytes; bit k of
-  word 1024 g + 8 i + b's primary code is bit b of byte i of plane k; zero past W;
+  the primary code of word 1024 g + 512 h + 8 l + b (h < 2, l < 64, b < 8) is bit b of byte 2 l + h of
+  plane k, so the 16 words a decoder lane takes (two runs of 8) have their code bits in one 16-bit
+  value per plane; zero past W;
 * S1 at 256 + 1408 G: G + 1 u32, primary escapes in groups before g (S1[G] = E1);
 * S2 at S1 + align16(4 (G + 1)): G + 1 u32, secondary escapes in groups before g (S2[G] = E2);
 * Y at S2 + align16(4 (G + 1)): one nibble per primary escape in word order, the r-th in the low
@@ -120,10 +122,11 @@ def encode(raw) -> np.ndarray:
     out[sec["off_a"]: sec["off_a"] + n_words] = (((words >> 8) & 0x80) | (words & 0x7F)).astype(np.uint8)
     codes = np.zeros(g * GROUP_WORDS, dtype=np.uint8)
     codes[:n_words] = c1
-    bits = codes.reshape(g, GROUP_WORDS // 8, 8)  # [group, byte, bit]
+    bits = codes.reshape(g, GROUP_WORDS // 8, 8)  # [group, word // 8 = 64 h + l, bit]
     weights = (1 << np.arange(8)).astype(np.uint16)
     planes = np.stack([(((bits >> k) & 1).astype(np.uint16) * weights).sum(-1).astype(np.uint8) for k in range(3)],
-                      axis=1)  # [group, plane, 128]
+                      axis=1)  # [group, plane, 64 h + l]
+    planes = planes.reshape(g, 3, 2, 64).transpose(0, 1, 3, 2)  # [group, plane, l, h]: byte 2 l + h
     out[sec["off_p"]: sec["off_p"] + PLANE_BYTES * g] = planes.reshape(-1)
     for key, esc in (("off_s1", esc1), ("off_s2", esc2)):
         counts = np.bincount(esc // GROUP_WORDS, minlength=g) if g else np.zeros(0, dtype=np.int64)
@@ -156,7 +159,8 @@ def decode(buf: np.ndarray) -> bytes:
     h = parse_header(buf)
     n, n_words, g, e1, e2 = h["n"], h["n_words"], h["groups"], h["e1"], h["e2"]
     a = buf[h["off_a"]: h["off_a"] + n_words].astype(np.uint32)
-    planes = buf[h["off_p"]: h["off_p"] + PLANE_BYTES * g].reshape(g, 3, GROUP_WORDS // 8)
+    planes = buf[h["off_p"]: h["off_p"] + PLANE_BYTES * g].reshape(g, 3, 64, 2).transpose(0, 1, 3, 2)
+    planes = planes.reshape(g, 3, GROUP_WORDS // 8)  # back to [group, plane, word // 8]
     c1 = np.zeros((g, GROUP_WORDS // 8, 8), dtype=np.uint8)
     for k in range(3):
         c1 |= (((planes[:, k, :, None] >> np.arange(8)) & 1) << k).astype(np.uint8)

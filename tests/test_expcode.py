@@ -206,9 +206,9 @@ def test_dense_known_answer_with_both_escape_levels():
     assert h["e1"] == len(ws) - n8 and h["e2"] == 2 + 1 and h["groups"] == 1
     assert enc.size == D.sections(1, h["e1"], 3)["total"]
     codes = np.zeros(1024, np.uint8)
-    planes = enc[h["off_p"]: h["off_p"] + 384].reshape(3, 128)
+    planes = enc[h["off_p"]: h["off_p"] + 384].reshape(3, 64, 2)  # [plane, lane l, run h]: words 512 h + 8 l + b
     for k in range(3):
-        codes |= ((np.unpackbits(planes[k], bitorder="little")) << k).astype(np.uint8)
+        codes |= (np.unpackbits(planes[k].T.reshape(-1), bitorder="little") << k).astype(np.uint8)
     assert list(codes[:3]) == [0] * 3 and codes[n8 - 1] == 6 and codes[n8] == 7 and not codes[len(ws):].any()
     y = enc[h["off_y"]: h["off_y"] + 2]
     assert y[0] == 0x00 and list(enc[h["off_s1"]: h["off_s1"] + 8].view("<u4")) == [0, h["e1"]]
