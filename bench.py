@@ -410,6 +410,17 @@ def expcode_sweep(grids=(8, 16, 32, 64, 128), reps: int = 6, hbm_grids=(0, 256, 
         out["decode"][str(grid)] = {"ms": round(ms, 3), "raw_GBps": round(n / ms / 1e6, 2),
                                     "link_GBps": round(block.nbytes / ms / 1e6, 2),
                                     "bit_exact": bool(torch.equal(dst, ref))}
+    # the dense format (version 2) over the link
+    dense_link = expcode.encode(raw, dense=True)
+    out["dense_link"] = {"encoded_bytes": dense_link.nbytes, "ratio": round(dense_link.ratio, 4), "decode": {}}
+    for grid in grids:
+        pol = nat.copy_policy(0, 2**63 - 1, 1, grid)
+        dst.zero_()
+        ms = best(lambda: expcode.decode_h2d(dst, dense_link, policy=pol))
+        out["dense_link"]["decode"][str(grid)] = {"ms": round(ms, 3), "raw_GBps": round(n / ms / 1e6, 2),
+                                                  "link_GBps": round(dense_link.nbytes / ms / 1e6, 2),
+                                                  "bit_exact": bool(torch.equal(dst, ref))}
+    del dense_link
     pol = nat.copy_policy(1 << 40, 2**63 - 1, 1, 8)
     ms = best(lambda: copy_h2d(dst, raw, nat.COPY_KERNEL, policy=pol))
     out["zero_copy_raw_8_workgroups"] = {"ms": round(ms, 3), "GBps": round(n / ms / 1e6, 2)}

@@ -190,9 +190,10 @@ class AllocationBlockController:
         """``shm_block_name_map`` puts each label's host block in a named shared-memory
         segment (loaders.py:1150-1175); with ``load_from_shm`` the segments already exist
         and are mapped instead of packed, and the tensors only supply their layouts.
-        ``encode_blocks`` keeps an exponent-coded copy of each label's block that saves at least a
-        tenth of its bytes (:mod:`~flextensor_amd.expcode`); such a label's transfer is one decode
-        launch that writes the raw block into its slot (no reference counterpart).
+        ``encode_blocks`` keeps an exponent-coded copy of each label's block, in the dense format
+        (version 2), that saves at least a tenth of its bytes (:mod:`~flextensor_amd.expcode`); such a
+        label's transfer is one decode launch that writes the raw block into its slot (no reference
+        counterpart).
         ``hbm_encoded`` maps block keys of units kept resident in encoded form to the device bytes
         reserved for each encoded block: their slot group is packed into pageable host blocks (nothing
         crosses the link), each block is encoded into device memory in the dense format (version 2, decoded
@@ -265,7 +266,7 @@ class AllocationBlockController:
                 for label, block in self.block_map_cpu.items():
                     if label in self.hbm_capacity:
                         continue
-                    enc = expcode.encode_if_smaller(block.block)
+                    enc = expcode.encode_if_smaller(block.block, dense=True)
                     if enc is not None:
                         self.encoded[label] = enc
             self.prepare_tensor_id_to_view_mapping()

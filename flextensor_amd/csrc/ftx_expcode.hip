@@ -396,6 +396,20 @@ int expcode_encode_dense(const void *raw_v, size_t nbytes, void *out_v, size_t o
   return FTX_OK;
 }
 
+int expcode_parse_dense(const void *src, size_t src_bytes, DenseLayout *layout) {
+  if (src_bytes < kExpcodeHeaderBytes) return fail(FTX_ERR_INVALID, "encoded block shorter than its header");
+  DenseHeader h;
+  std::memcpy(&h, src, sizeof(h));
+  if (std::memcmp(h.magic, "FTXE", 4) != 0 || h.version != kDenseVersion)
+    return fail(FTX_ERR_INVALID, "not a dense exponent-coded block (magic or version)");
+  if (h.n_words != h.n / 2 || h.groups != (h.n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords ||
+      h.groups >= (uint64_t(1) << 32) || h.e1 > h.n_words || h.e1 >= (uint64_t(1) << 32) || h.e2 > h.e1)
+    return fail(FTX_ERR_INVALID, "inconsistent dense exponent-coded block header");
+  *layout = dense_layout(h.n, h.e1, h.e2);
+  if (layout->total > src_bytes) return fail(FTX_ERR_INVALID, "encoded block is truncated");
+  return FTX_OK;
+}
+
 int expcode_parse(const void *src, size_t src_bytes, ExpcodeInfo *info) {
   if (src_bytes < kExpcodeHeaderBytes) return fail(FTX_ERR_INVALID, "encoded block shorter than its header");
   ExpHeader h;
@@ -668,10 +682,178 @@ __global__ __launch_bounds__(kExpThreads) void expcode_dense_decode_kernel(uint8
   }
 }
 
+constexpr int kDenseLinkInFlight = 8;  // groups per lane per batch (16 made the compiler spill to scratch)
+
+// Dense blocks (version 2) over the link: the source is mapped host memory, so every read is a PCIe round
+// trip and a group's nibble reads cannot wait on its own rank scan one group at a time. Each batch of
+// kDenseLinkInFlight groups per lane goes in three phases: the plane, code and prefix-count loads of every
+// group; the rank scans, then one 8-byte nibble window per run with escapes, all issued together; then the
+// words, built four to a register as in expcode_dense_decode_kernel. A run whose escapes pass its window,
+// or a window past the block, reads its nibbles byte by byte. Reads are clamped to `capacity`.
+__global__ __launch_bounds__(kExpThreads) void expcode_dense_link_decode_kernel(uint8_t *__restrict__ dst,
+                                                                                const uint8_t *__restrict__ src,
+                                                                                uint64_t capacity, uint64_t n) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = static_cast<uint64_t>(blockIdx.x) * kExpWaves + threadIdx.x / 64;
+  const uint64_t waves = static_cast<uint64_t>(gridDim.x) * kExpWaves;
+  const uint64_t n_words = n / 2;
+  const uint64_t groups = (n_words + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  const uint64_t sect = (4 * (groups + 1) + 15) / 16 * 16;
+  const uint64_t off_p = kExpcodeHeaderBytes + kExpcodeGroupWords * groups;
+  const uint64_t off_s1 = off_p + kDensePlaneBytes * groups;
+  const uint64_t off_s2 = off_s1 + sect;
+  const uint64_t off_y = off_s2 + sect;
+  if (off_y > capacity || *reinterpret_cast<const uint64_t *>(src + 8) != n) return;
+  const uint64_t e1 = *reinterpret_cast<const uint64_t *>(src + 32);
+  const uint64_t off_x = off_y + ((min(e1, capacity) + 1) / 2 + 15) / 16 * 16;
+  uint64_t e2 = *reinterpret_cast<const uint64_t *>(src + 40);
+  e2 = off_x <= capacity ? min(e2, (capacity - off_x) / 4) : 0;
+  const uint64_t y_bytes = capacity - off_y;
+  const uint32_t t1_lo = *reinterpret_cast<const uint32_t *>(src + 48);
+  const uint32_t t1_hi = *reinterpret_cast<const uint32_t *>(src + 52);
+  const uint32_t t2a_lo = *reinterpret_cast<const uint32_t *>(src + 56);
+  const uint32_t t2a_hi = *reinterpret_cast<const uint32_t *>(src + 60);
+  const uint32_t t2b_lo = *reinterpret_cast<const uint32_t *>(src + 64);
+  const uint32_t t2b_hi = *reinterpret_cast<const uint32_t *>(src + 68);
+  if ((n & 1) && blockIdx.x == 0 && threadIdx.x == 0) dst[n - 1] = src[72];
+  const uint8_t *A = src + kExpcodeHeaderBytes;
+  const uint8_t *P = src + off_p;
+  const uint32_t *S1 = reinterpret_cast<const uint32_t *>(src + off_s1);
+  const uint32_t *S2 = reinterpret_cast<const uint32_t *>(src + off_s2);
+  const uint8_t *Y = src + off_y;
+  const uint32_t *X = reinterpret_cast<const uint32_t *>(src + off_x);
+  constexpr int F = kDenseLinkInFlight;
+  for (uint64_t g0 = wave * F; g0 < groups; g0 += waves * F) {
+    // phase 1: planes, codes and prefix counts of F groups
+    u32x2 a[F][2];
+    uint32_t pw[F][3];
+#pragma unroll
+    for (int i = 0; i < F; ++i) {
+      const uint64_t g = min(g0 + i, groups - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        a[i][h] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2 *>(A + g * kExpcodeGroupWords + 512 * h) + lane);
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        pw[i][k] = reinterpret_cast<const uint16_t *>(P + g * kDensePlaneBytes + 128 * k)[lane];
+    }
+    const uint64_t si = min(g0 + min(lane, F), groups);  // lanes 0 .. F: S1 and S2 at g0 .. g0 + F
+    const uint32_t s1v = S1[si], s2v = S2[si];
+    // phase 2: ranks, then every run's nibble window
+    uint32_t rank0[F][2];
+    uint64_t wbase[F][2];
+    u32x2 win[F][2];
+#pragma unroll
+    for (int i = 0; i < F; ++i) {
+      const uint32_t m0 = (pw[i][0] & pw[i][1] & pw[i][2]) & 0xff, m1 = (pw[i][0] & pw[i][1] & pw[i][2]) >> 8 & 0xff;
+      const uint32_t s1a = __shfl(s1v, i, 64), s1b = __shfl(s1v, i + 1, 64);
+      uint32_t excl = 0, run0 = 0;
+      if (g0 + i < groups && s1b > s1a) {  // wave-uniform
+        const uint32_t cnt = __popc(m0) | (__popc(m1) << 16);
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t y = __shfl_up(incl, d, 64);
+          if (lane >= d) incl += y;
+        }
+        excl = incl - cnt;
+        run0 = __shfl(incl, 63, 64) & 0xffff;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint64_t r = static_cast<uint64_t>(s1a) + (h ? run0 + (excl >> 16) : (excl & 0xffff));
+        const uint64_t wb = (r >> 1) & ~uint64_t{7};
+        wbase[i][h] = wb;
+        rank0[i][h] = static_cast<uint32_t>(r - 2 * wb);
+        win[i][h] = u32x2{0, 0};
+        if (g0 + i < groups && (h ? m1 : m0) && wb + 8 <= y_bytes)
+          win[i][h] = *reinterpret_cast<const u32x2 *>(Y + wb);
+      }
+    }
+    // phase 3: words
+#pragma unroll
+    for (int i = 0; i < F; ++i) {
+      const uint64_t g = g0 + i;
+      if (g >= groups) break;
+      uint32_t ex[2][2];
+      const uint32_t all3 = pw[i][0] & pw[i][1] & pw[i][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          uint32_t codes = 0;
+#pragma unroll
+          for (int k = 0; k < 3; ++k) codes |= ((((pw[i][k] >> (8 * h + 4 * q)) & 0xf) * 0x00204081u) & 0x01010101u) << k;
+          ex[h][q] = __builtin_amdgcn_perm(t1_hi, t1_lo, codes);
+        }
+        uint32_t m = (all3 >> (8 * h)) & 0xff;
+        uint32_t q = rank0[i][h];
+        while (m) {
+          const int j = __builtin_ctz(m);
+          m &= m - 1;
+          uint32_t yb;
+          if (q < 16 && wbase[i][h] + 8 <= y_bytes) {
+            yb = (q < 8 ? win[i][h].x : win[i][h].y) >> (4 * (q & 7));
+          } else {
+            const uint64_t byte = wbase[i][h] + (q >> 1);
+            yb = byte < y_bytes ? static_cast<uint32_t>(Y[byte]) >> (4 * (q & 1)) : 0u;
+          }
+          const uint32_t c2 = yb & 0xf;
+          const uint32_t e = __builtin_amdgcn_perm(c2 < 8 ? t2a_hi : t2b_hi, c2 < 8 ? t2a_lo : t2b_lo, c2 & 7) & 0xff;
+          const uint32_t sh = 8 * (j & 3);
+          if (j < 4)
+            ex[h][0] = (ex[h][0] & ~(0xffu << sh)) | (e << sh);
+          else
+            ex[h][1] = (ex[h][1] & ~(0xffu << sh)) | (e << sh);
+          ++q;
+        }
+      }
+      const uint32_t s2a = __shfl(s2v, i, 64);
+      const uint32_t s2b = min(static_cast<uint64_t>(__shfl(s2v, i + 1, 64)), e2);
+      for (uint32_t k = s2a; k < s2b; ++k) {  // wave-uniform; secondary escapes are rarer still
+        const uint32_t x = X[k];
+        const uint32_t pos = x >> 8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (pos == static_cast<uint32_t>(512 * h + 8 * lane + j))
+              ex[h][j >> 2] = (ex[h][j >> 2] & ~(0xffu << (8 * (j & 3)))) | ((x & 0xffu) << (8 * (j & 3)));
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint64_t w0 = g * kExpcodeGroupWords + 512 * h + 8 * static_cast<uint64_t>(lane);
+        uint8_t *out = dst + 2 * w0;
+        u32x4 v;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const uint32_t sel = half ? 0x0c030c02u : 0x0c010c00u;
+            const uint32_t av = __builtin_amdgcn_perm(0u, a[i][h][q], sel);
+            const uint32_t ev = __builtin_amdgcn_perm(0u, ex[h][q], sel);
+            v[2 * q + half] = ((av & 0x00800080u) << 8) | (ev << 7) | (av & 0x007f007fu);
+          }
+        if (w0 + 8 <= n_words) {
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (w0 + j < n_words) reinterpret_cast<uint16_t *>(out)[j] = static_cast<uint16_t>(v[j >> 1] >> (16 * (j & 1)));
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t allow_expcode_lds(size_t bytes) {
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(expcode_decode_kernel),
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(expcode_decode_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(expcode_dense_link_decode_kernel),
                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
 }
 
@@ -684,6 +866,18 @@ hipError_t launch_expcode_decode(void *dst, const void *src_dev, uint64_t capaci
   const unsigned g = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, static_cast<uint64_t>(grid))));
   hipLaunchKernelGGL(expcode_decode_kernel, dim3(g), dim3(kExpThreads), static_cast<unsigned>(reserve_lds), stream,
                      static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src_dev), capacity, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_expcode_dense_link_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
+                                            size_t reserve_lds, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const uint64_t groups = (n / 2 + kExpcodeGroupWords - 1) / kExpcodeGroupWords;
+  const uint64_t per_block = static_cast<uint64_t>(kExpWaves) * kDenseLinkInFlight;
+  const uint64_t need = std::max<uint64_t>(1, (groups + per_block - 1) / per_block);
+  const unsigned g = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, static_cast<uint64_t>(grid))));
+  hipLaunchKernelGGL(expcode_dense_link_decode_kernel, dim3(g), dim3(kExpThreads), static_cast<unsigned>(reserve_lds),
+                     stream, static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src_dev), capacity, n);
   return hipGetLastError();
 }
 

@@ -163,6 +163,11 @@ int expcode_encode_dense(const void *raw, size_t nbytes, void *out, size_t out_c
 // kernel reads the block's header when it runs and writes nothing for a header of another raw size.
 hipError_t launch_expcode_dense_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
                                        size_t reserve_lds, hipStream_t stream);
+// Reads and checks the header of a dense block of src_bytes bytes in host memory.
+int expcode_parse_dense(const void *src, size_t src_bytes, DenseLayout *layout);
+// The dense decode from mapped host memory (over the link): `reserve_lds` as for launch_zero_copy.
+hipError_t launch_expcode_dense_link_decode(void *dst, const void *src_dev, uint64_t capacity, uint64_t n, int grid,
+                                            size_t reserve_lds, hipStream_t stream);
 
 // Host-side helpers shared with the oracle's definition of the checksum.
 inline uint64_t splitmix64(uint64_t x) {

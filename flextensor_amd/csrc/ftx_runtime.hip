@@ -734,6 +734,15 @@ int ftx_expcode_encode(const void *raw, size_t nbytes, void *out, size_t out_cap
 
 int ftx_expcode_raw_bytes(const void *src, size_t src_bytes, size_t *raw_bytes) {
   if (!src || !raw_bytes) return ftx::fail(FTX_ERR_INVALID, "null argument");
+  uint32_t version = 0;
+  if (src_bytes >= 8) std::memcpy(&version, static_cast<const uint8_t *>(src) + 4, 4);
+  if (version == 2) {
+    ftx::DenseLayout d;
+    const int rc = ftx::expcode_parse_dense(src, src_bytes, &d);
+    if (rc != FTX_OK) return rc;
+    *raw_bytes = static_cast<size_t>(d.n);
+    return FTX_OK;
+  }
   ftx::ExpcodeInfo info;
   int rc = ftx::expcode_parse(src, src_bytes, &info);
   if (rc != FTX_OK) return rc;
@@ -745,12 +754,25 @@ int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const f
                            void *stream) {
   FTX_REQUIRE_LIVE();
   if (!dst || !src) return ftx::fail(FTX_ERR_INVALID, "null pointer");
-  ftx::ExpcodeInfo info;
-  int rc = ftx::expcode_parse(src, src_bytes, &info);  // the header is read on the host: src is host memory
+  // The header is read on the host (src is host memory): version 1, or the dense version 2
+  uint32_t version = 0;
+  if (src_bytes >= 8) std::memcpy(&version, static_cast<const uint8_t *>(src) + 4, 4);
+  const bool dense = version == 2;
+  uint64_t n = 0;
+  int rc;
+  if (dense) {
+    ftx::DenseLayout d;
+    rc = ftx::expcode_parse_dense(src, src_bytes, &d);
+    n = d.n;
+  } else {
+    ftx::ExpcodeInfo info;
+    rc = ftx::expcode_parse(src, src_bytes, &info);
+    n = info.n;
+  }
   if (rc != FTX_OK) return rc;
-  if (info.n == 0) return FTX_OK;
+  if (n == 0) return FTX_OK;
   if (reinterpret_cast<uintptr_t>(dst) % 16 != 0) return ftx::fail(FTX_ERR_INVALID, "decode destination needs 16-byte alignment");
-  rc = ftx::check_device_range(dst, static_cast<size_t>(info.n), "decode destination");
+  rc = ftx::check_device_range(dst, static_cast<size_t>(n), "decode destination");
   if (rc != FTX_OK) return rc;
   const void *src_dev = nullptr;
   rc = ftx::mapped_source(src, src_bytes, &src_dev);  // the kernel may read up to src_bytes (a re-encoded block)
@@ -769,7 +791,11 @@ int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const f
   rc = ftx::device_state(&st);
   if (rc != FTX_OK) return rc;
   const size_t reserve = grid <= ftx::kZeroCopyReserveMaxGrid ? st->copy_reserve_lds : 0;
-  FTX_HIP(ftx::launch_expcode_decode(dst, src_dev, src_bytes, info.n, grid, reserve, static_cast<hipStream_t>(stream)));
+  if (dense)
+    FTX_HIP(ftx::launch_expcode_dense_link_decode(dst, src_dev, src_bytes, n, grid, reserve,
+                                                  static_cast<hipStream_t>(stream)));
+  else
+    FTX_HIP(ftx::launch_expcode_decode(dst, src_dev, src_bytes, n, grid, reserve, static_cast<hipStream_t>(stream)));
   return FTX_OK;
 }
 

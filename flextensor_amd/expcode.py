@@ -49,12 +49,13 @@ class EncodedBlock:
     (same arena, so decode launches captured in a graph stay valid, and they read the new header when
     they run) as long as the new encoding fits."""
 
-    __slots__ = ("arena", "nbytes", "raw_bytes")
+    __slots__ = ("arena", "nbytes", "raw_bytes", "dense")
 
-    def __init__(self, arena: HostArena, nbytes: int, raw_bytes: int) -> None:
+    def __init__(self, arena: HostArena, nbytes: int, raw_bytes: int, dense: bool = False) -> None:
         self.arena = arena
         self.nbytes = int(nbytes)
         self.raw_bytes = int(raw_bytes)
+        self.dense = bool(dense)  # the dense format (version 2); the decode reads the version from the header
 
     def reencode(self, raw: torch.Tensor) -> None:
         """Encode ``raw`` (the same raw size) into this block's arena. No decode of this block may be in
@@ -62,11 +63,12 @@ class EncodedBlock:
         ptr, n = _raw_ptr(raw)
         if n != self.raw_bytes:
             raise ValueError(f"raw block of {n} bytes, but this block encodes {self.raw_bytes}")
-        size = encoded_size(raw)
+        size = encoded_size(raw, self.dense)
         if size > self.arena.nbytes:
             raise ValueError(f"the new encoding needs {size} bytes, more than the {self.arena.nbytes} of its arena")
         out = ctypes.c_size_t(0)
-        nat.call("ftx_expcode_encode", ptr, n, self.arena.ptr, self.arena.nbytes, ctypes.byref(out))
+        nat.call("ftx_expcode_encode_dense" if self.dense else "ftx_expcode_encode", ptr, n, self.arena.ptr,
+                 self.arena.nbytes, ctypes.byref(out))
         self.nbytes = int(out.value)
 
     @property
@@ -79,29 +81,32 @@ class EncodedBlock:
         return self.arena.tensor[: self.nbytes]
 
 
-def encode(raw: torch.Tensor, size: int | None = None, capacity: int = 0) -> EncodedBlock:
+def encode(raw: torch.Tensor, size: int | None = None, capacity: int = 0, dense: bool = False) -> EncodedBlock:
     """Encode ``raw`` into a new arena of at least ``capacity`` bytes (``size``: the encoded size, if
-    already known)."""
+    already known), in the dense format (version 2) when ``dense``."""
     ptr, n = _raw_ptr(raw)
-    size = encoded_size(raw) if size is None else int(size)
+    size = encoded_size(raw, dense) if size is None else int(size)
     arena = HostArena(max(size, int(capacity), 1))
     out = ctypes.c_size_t(0)
-    nat.call("ftx_expcode_encode", ptr, n, arena.ptr, arena.nbytes, ctypes.byref(out))
+    nat.call("ftx_expcode_encode_dense" if dense else "ftx_expcode_encode", ptr, n, arena.ptr, arena.nbytes,
+             ctypes.byref(out))
     if out.value != size:
         raise RuntimeError(f"encoded size {out.value} differs from the {size} bytes planned")
-    return EncodedBlock(arena, size, n)
+    return EncodedBlock(arena, size, n, dense)
 
 
-def encode_if_smaller(raw: torch.Tensor, max_ratio: float = DEFAULT_MAX_RATIO) -> EncodedBlock | None:
+def encode_if_smaller(raw: torch.Tensor, max_ratio: float = DEFAULT_MAX_RATIO,
+                      dense: bool = False) -> EncodedBlock | None:
     """The encoded block, or None when it would not be below ``max_ratio`` of the raw size. Its arena
-    holds the raw size, so any later contents that encode no larger than raw re-encode in place."""
+    holds the raw size plus the dense format's worst case over raw (the sections' fixed cost), so any
+    later contents that encode no larger than that re-encode in place."""
     _, n = _raw_ptr(raw)
     if n == 0:
         return None
-    size = encoded_size(raw)
+    size = encoded_size(raw, dense)
     if size > max_ratio * n:
         return None
-    return encode(raw, size, capacity=n)
+    return encode(raw, size, capacity=n, dense=dense)
 
 
 def decode_h2d(dst: torch.Tensor, block: EncodedBlock, stream: HipStream | None = None,

@@ -201,7 +201,9 @@ int ftx_get_copy_policy(size_t *kernel_max_bytes, size_t *split_min_bytes, int *
  * on `stream`; policy->kernel_grid sets its workgroups (NULL or 0: 16), and a
  * grid of at most 16 reserves its CUs as the zero-copy copy does. The header
  * is read on the host at call time; the block must not change until the copy
- * has run. */
+ * has run. A dense block (version 2, ftx_expcode_encode_dense) is decoded by
+ * the dense kernel's link variant, whose nibble reads follow each batch's rank
+ * scans; ftx_expcode_raw_bytes reads either version. */
 int ftx_expcode_encode(const void *raw, size_t nbytes, void *out, size_t out_capacity, size_t *out_bytes);
 int ftx_expcode_raw_bytes(const void *src, size_t src_bytes, size_t *raw_bytes);
 int ftx_expcode_decode_h2d(void *dst, const void *src, size_t src_bytes, const ftx_copy_policy *policy,
