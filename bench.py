@@ -497,7 +497,8 @@ def _ring_engine(mgr) -> str:
 
     ctl = mgr.controller
     if getattr(ctl, "encoded", None):
-        return "expcode_decode_kernel (16 workgroups)"
+        dense = any(getattr(b, "dense", False) for b in ctl.encoded.values())
+        return f"{'expcode_dense_link_decode_kernel' if dense else 'expcode_decode_kernel'} (16 workgroups)"
     mode, policy = ctl.copy_mode, ctl.copy_policy
     if mode == nat.COPY_AUTO:
         if policy is None:
@@ -1270,7 +1271,7 @@ def measure_traffic(args) -> dict | None:
         scat = [row for row in rows if "scatter_kernel" in row["Kernel_Name"]]
         ring = [row for row in rows if "zero_copy_kernel" in row["Kernel_Name"]
                 and int(row.get("Grid_Size", L.RING_KERNEL_GRID * 256)) == L.RING_KERNEL_GRID * 256]
-        dec = [row for row in rows if "expcode_decode_kernel" in row["Kernel_Name"]]
+        dec = [row for row in rows if "expcode_dense_link_decode_kernel" in row["Kernel_Name"]]
         if not copies or not scat:
             return None
         scale = calib / (float(copies[0]["Counter_Value"]) * 1024)
@@ -1324,12 +1325,12 @@ def traffic_probe(args) -> int:
     for _ in range(RING_COPY_PROBES):
         nat.copy_h2d(slot.data_ptr(), arena.ptr, n, nat.COPY_KERNEL, xs.handle, ring_policy)
     xs.synchronize()
-    # the same layer's bytes as N(0, 0.02) bf16 weights, exponent-coded, decoded as the encoded ring does
+    # the same layer's bytes as N(0, 0.02) bf16 weights, in the dense format, decoded as the encoded ring does
     from flextensor_amd import expcode
 
     g = torch.Generator().manual_seed(0)
     arena.tensor[:n].copy_((torch.randn(n // 2, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8))
-    block = expcode.encode(arena.tensor[:n])
+    block = expcode.encode(arena.tensor[:n], dense=True)
     for _ in range(RING_COPY_PROBES):
         expcode.decode_h2d(slot, block, stream=xs)
     xs.synchronize()
