@@ -315,10 +315,14 @@ class AllocationBlockController:
 
     def refresh_encoded(self) -> None:
         """Re-encode every encoded block in place from its host block, after the host blocks were
-        rewritten (a state-dict load). No transfer or decode may be in flight. A block kept in HBM
-        whose new encoding outgrows its reservation raises ValueError naming it."""
+        rewritten (a state-dict load). No transfer or decode may be in flight. A block whose new encoding
+        outgrows its arena or reservation raises ValueError naming it."""
         for label, enc in self.encoded.items():
-            enc.reencode(self.block_map_cpu[label].block)
+            try:
+                enc.reencode(self.block_map_cpu[label].block)
+            except ValueError as exc:
+                raise ValueError(f"streamed unit block {label!r}: {exc}; release() and offload the model again "
+                                 "(weights that do not shrink stream raw)") from exc
         for key, dev in self.hbm_encoded.items():
             try:
                 dev.reencode(self.block_map_cpu[key].block)

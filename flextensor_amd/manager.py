@@ -529,7 +529,7 @@ class OffloadManager:
         self._from_state = False
         self._reload_pending = False
         self._hbm_keys: dict[str, str] = {}  # unit label -> its block key, for units kept encoded in HBM
-        self._hbm_stale: str | None = None  # why those blocks no longer match the model's weights
+        self._stale_encoding: str | None = None  # why the encoded blocks no longer match the model's weights
         self._pinner: HostPinner | None = None
         self.memory_transfer_stats: dict[int, float] = {}
         self.link: LinkMeasurement | None = None  # the measured host link and the copy policy it chose
@@ -715,7 +715,7 @@ class OffloadManager:
         self._control, self._suspend_count = None, 0
         self._from_state = False
         self._reload_pending = False
-        self._hbm_keys, self._hbm_stale = {}, None
+        self._hbm_keys, self._stale_encoding = {}, None
         self.skip_discovery_honored = None
         self.compile_fn = None
         self._load_from_shm = False
@@ -1257,7 +1257,7 @@ class OffloadManager:
             self._pinner = None
             self._from_state = False
             self._reload_pending = False
-            self._hbm_keys, self._hbm_stale = {}, None
+            self._hbm_keys, self._stale_encoding = {}, None
             self.skip_discovery_honored = None
             self.loader = self.controller = self.plan = None
             self.link = None
@@ -1530,11 +1530,11 @@ class OffloadManager:
         if self.phase == OffloadPhase.INFERENCE:
             if self._reload_pending and self.order and label == self.order[0]:
                 self._reload_if_pending()  # a load on a submodule, which the root's load hook did not see
+            if self._stale_encoding is not None:
+                raise RuntimeError(f"offload manager {self.name!r}: {self._stale_encoding}")
             self.loader.enter(label)
             key = self._hbm_keys.get(label)
             if key is not None:
-                if self._hbm_stale is not None:
-                    raise RuntimeError(f"offload manager {self.name!r}: {self._hbm_stale}")
                 self.controller.decode_resident(key)  # on the compute stream, ahead of the unit's kernels
             return
         if hip.is_capturing():
@@ -1882,7 +1882,7 @@ class OffloadManager:
         for tid, t in tensors_map.items():
             t.data = bound[tid]
         self.loader = self.timing = None
-        self._hbm_keys, self._hbm_stale = {}, None
+        self._hbm_keys, self._stale_encoding = {}, None
         controller, self.controller = self.controller, None
         if controller is not None:
             controller.abort_construction(primary)
@@ -1977,7 +1977,9 @@ class OffloadManager:
             try:
                 self.controller.refresh_encoded()
             except ValueError as exc:
-                self._hbm_stale = f"{exc} (the units kept encoded in HBM no longer hold the loaded weights)"
+                # Every later forward raises: the encoded blocks would feed the old weights. A graph captured
+                # before the load must not be replayed either.
+                self._stale_encoding = f"{exc} (the encoded blocks no longer hold the loaded weights)"
                 raise
         preload = getattr(self.loader, "preload", None)
         if preload is not None:

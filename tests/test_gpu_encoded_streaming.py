@@ -215,3 +215,27 @@ def test_encoded_blocks_from_pageable_and_shared_memory_sources(gpu, source):
             assert all(os.path.exists(os.path.join("/dev/shm", n)) for n in ctl.shm_block_name_map.values())
     finally:
         mgr.release()
+
+
+def test_a_load_that_does_not_encode_fails_loudly(gpu):
+    """Weights of random bit patterns encode to more than their arena holds: the load raises, and every
+    later forward raises too instead of decoding the old encoded blocks."""
+    model = W.build_mlp_stack(6, 256, 704, seed=49)
+    mgr = _offload(model, "enc-outgrow")
+    x = W.mlp_input(8, 256, seed=49).to(gpu)
+    try:
+        with torch.no_grad():
+            for _ in range(3):
+                model(x)
+        assert mgr.phase == OffloadPhase.INFERENCE and mgr.controller.encoded
+        noisy = W.build_mlp_stack(6, 256, 704, seed=50)
+        g = torch.Generator().manual_seed(50)
+        with torch.no_grad():
+            for p in noisy.parameters():
+                p.view(torch.int16).copy_(torch.randint(-32768, 32767, p.shape, generator=g, dtype=torch.int16))
+        with pytest.raises(ValueError, match="streamed unit block"):
+            model.load_state_dict(noisy.state_dict())
+        with pytest.raises(RuntimeError, match="encoded blocks no longer hold"), torch.no_grad():
+            model(x)
+    finally:
+        mgr.release()
