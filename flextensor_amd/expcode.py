@@ -1,17 +1,23 @@
-"""Exponent-coded host blocks: a streamed block carried over the link in about 0.75 of its bytes.
+"""Exponent-coded blocks: a streamed block carried over the link in about 0.70 of its bytes, a resident
+one kept in HBM in as few.
 
 No reference counterpart: the reference copies each label's packed block as raw bytes
 (allocation_block.py:104-106). With ``OffloadConfig.encode_streamed_blocks`` the block controller keeps,
 beside each streamed label's pinned raw block, an encoded copy in a pinned, device-mapped arena, and
 its host-to-device transfer becomes one decode launch (``ftx_expcode_decode_h2d``): a zero-copy kernel
-reads the encoded bytes over the link and writes the raw bytes into the ring slot, bit for bit. The
-format (``FTXE`` v1) codes each bf16 word's exponent in 4 bits for the block's 15 most frequent
-exponents, with the rest as escapes; the encoder is the library's host routine
-(``ftx_expcode_encode``).
+reads the encoded bytes over the link and writes the raw bytes into the ring slot, bit for bit.
+
+Two formats. Version 1 (``FTXE`` v1, ``ftx_expcode_encode``) codes each bf16 word's exponent in 4 bits
+for the block's 15 most frequent exponents, with the rest as escapes: 0.752 of the bytes. The dense
+version 2 (``ftx_expcode_encode_dense``) codes the 7 most frequent in 3 bits and the next 15 in a 4-bit
+secondary code per escape: 0.697. Its decoders rank escapes across the wave before reading their
+codes; the controllers use it for every block, and ``ftx_expcode_decode_h2d`` reads a block's version
+from its header. The encoders are the library's host routines.
 
 With ``OffloadConfig.encode_resident_blocks`` resident units are kept encoded in device memory instead
 (:class:`DeviceEncodedBlock`): more units fit the GPU budget, fewer stream, and each such unit is
-decoded from HBM (``ftx_expcode_decode_d2d``) into one shared slot on the compute stream as it runs.
+decoded from HBM (``ftx_expcode_decode_dense_d2d``) into one shared slot on the compute stream as it
+runs.
 """
 
 from __future__ import annotations
@@ -98,8 +104,7 @@ def encode(raw: torch.Tensor, size: int | None = None, capacity: int = 0, dense:
 def encode_if_smaller(raw: torch.Tensor, max_ratio: float = DEFAULT_MAX_RATIO,
                       dense: bool = False) -> EncodedBlock | None:
     """The encoded block, or None when it would not be below ``max_ratio`` of the raw size. Its arena
-    holds the raw size plus the dense format's worst case over raw (the sections' fixed cost), so any
-    later contents that encode no larger than that re-encode in place."""
+    holds the raw size, so any later contents that encode no larger than raw re-encode in place."""
     _, n = _raw_ptr(raw)
     if n == 0:
         return None
